@@ -1,0 +1,296 @@
+"""Decode-attention benchmark of the relux KV-cache hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload gqa8k|gqa_cfg2|mla8k]
+
+A step is one layer's decode over the whole batch: append one new token per
+sequence into the paged cache, then attend every sequence's query over its
+cache (and roll the token back so the context length stays fixed).  Steps
+rotate over several layers whose pools together exceed the 256 MB Infinity
+Cache, so every step streams its layer's cache from HBM.  Inputs are
+synthetic (N(0,1) K/V/latents, N(0,0.02) absorbed weights) and resident in
+HBM before the timed region.
+
+Prints ONE JSON line: value = decode query tokens/s of the whole job;
+roofline = algorithmic bytes of the dominant kernel / its average duration
+(HIP events on the stream it runs on); cpu_baseline = the reference's Go
+decode step as restated in C (oracle/), single thread, on a bounded sample.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # BASELINE config 2' (headline, 8k context): GQA paged decode
+    "gqa8k": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=8192, layers=2),
+    # context lengths U[512, 4096]
+    "gqa_cfg2": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=None, layers=8),
+    # BASELINE config 3 (headline, 8k context): MLA latent decode
+    "mla8k": dict(kind="mla", B=32, H=16, D=128, P=64, T=8192, layers=4),
+}
+
+
+def _lens(cfg, rng):
+    if cfg["T"] is not None:
+        return [cfg["T"]] * cfg["B"]
+    return [int(x) for x in rng.integers(512, 4097, size=cfg["B"])]
+
+
+def _fill_interleaved(append_fn, lens, P, rng):
+    """Append every sequence's tokens one page at a time, sequences in a
+    fresh random order each round, so each sequence's pages are scattered
+    over the shared pool."""
+    left = list(lens)
+    while any(left):
+        order = [int(i) for i in rng.permutation(len(lens)) if left[i] > 0]
+        n = [min(P, left[i]) for i in order]
+        append_fn(order, n)
+        for i, ni in zip(order, n):
+            left[i] -= ni
+
+
+def setup_gqa(cfg, torch, dev, rng):
+    from relux_amd import KVCache
+    B, H, KVH, D, P, L = cfg["B"], cfg["H"], cfg["KVH"], cfg["D"], cfg["P"], cfg["layers"]
+    lens = _lens(cfg, rng)
+    pool = sum(-(-(T + 1) // P) for T in lens) + 8
+    c = KVCache(num_layers=L, max_len=max(lens) + P, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=B, pool_pages=pool, device=dev.index)
+    for layer in range(L):
+        def app(order, n, layer=layer):
+            k = torch.randn(sum(n), KVH, D, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(sum(n), KVH, D, device=dev, dtype=torch.bfloat16)
+            c.Append(layer, k, v, seq_ids=order, n_tok=n, layout="SHD")
+        _fill_interleaved(app, lens, P, rng)
+    seqs = list(range(B))
+    k1 = torch.randn(B, KVH, D, device=dev, dtype=torch.bfloat16)
+    v1 = torch.randn(B, KVH, D, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(B, H, D, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+    ones = [1] * B
+
+    def step(i):
+        layer = i % L
+        c.Append(layer, k1, v1, seq_ids=seqs, n_tok=ones, layout="SHD")
+        c.Attend(layer, q, H, seq_ids=seqs, out=out)
+        c.Rollback(seqs, ones)
+
+    Tatt = [T + 1 for T in lens]  # attention sees the appended token
+    kv_bytes = sum(Tatt) * KVH * D * 2 * 2
+    table_bytes = sum(-(-T // P) for T in Tatt) * 4
+    kernel_bytes = kv_bytes + B * H * D * 2 + table_bytes
+    step_bytes = kernel_bytes + B * H * D * 2 + 2 * (B * KVH * D * 2 * 2)
+    desc = {"workload": f"gqa_paged_decode B{B} H{H} KVH{KVH} D{D} P{P} "
+                        + (f"T{cfg['T']}" if cfg["T"] else "T~U[512,4096]"),
+            "batch": B, "query_heads": H, "kv_heads": KVH, "head_dim": D, "page_tokens": P,
+            "context_mean": sum(lens) / B, "layers_rotated": L, "pages": "randomly interleaved pool"}
+    return c, step, B, kernel_bytes, step_bytes, desc, "gqa_decode_kernel", lens
+
+
+def setup_mla(cfg, torch, dev, rng):
+    from relux_amd import MLACache
+    B, H, D, P, L = cfg["B"], cfg["H"], cfg["D"], cfg["P"], cfg["layers"]
+    lens = _lens(cfg, rng)
+    pool = sum(-(-(T + 1) // P) for T in lens) + 8
+    c = MLACache(num_layers=L, max_len=max(lens) + P, page_tokens=P, max_seqs=B,
+                 pool_pages=pool, device=dev.index)
+    for layer in range(L):
+        def app(order, n, layer=layer):
+            cc = torch.randn(sum(n), 512, device=dev, dtype=torch.bfloat16)
+            kr = torch.randn(sum(n), 64, device=dev, dtype=torch.bfloat16)
+            c.Append(layer, cc, kr, seq_ids=order, n_tok=n)
+        _fill_interleaved(app, lens, P, rng)
+    seqs = list(range(B))
+    c1 = torch.randn(B, 512, device=dev, dtype=torch.bfloat16)
+    kr1 = torch.randn(B, 64, device=dev, dtype=torch.bfloat16)
+    qn = torch.randn(B, H, D, device=dev, dtype=torch.bfloat16)
+    qr = torch.randn(B, H, 64, device=dev, dtype=torch.bfloat16)
+    w_uk = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    w_uv = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+    ones = [1] * B
+
+    def step(i):
+        layer = i % L
+        c.Append(layer, c1, kr1, seq_ids=seqs, n_tok=ones)
+        c.Attend(layer, qn, qr, w_uk, w_uv, H, D, seq_ids=seqs, out=out)
+        c.Rollback(seqs, ones)
+
+    Tatt = [T + 1 for T in lens]
+    lat_bytes = sum(Tatt) * 576 * 2
+    table_bytes = sum(-(-T // P) for T in Tatt) * 4
+    kernel_bytes = lat_bytes + B * H * 576 * 2 + table_bytes
+    step_bytes = (kernel_bytes + 2 * 512 * H * D * 2 + B * H * (D + 64) * 2 + B * H * D * 2
+                  + 2 * B * 576 * 2)
+    desc = {"workload": f"mla_latent_decode B{B} H{H} dC512 dR64 D{D} P{P} T{cfg['T']}",
+            "batch": B, "heads": H, "kv_lora_rank": 512, "rope_dim": 64, "head_dim": D,
+            "page_tokens": P, "context_mean": sum(lens) / B, "layers_rotated": L}
+    return c, step, B, kernel_bytes, step_bytes, desc, "mla_decode_kernel", lens
+
+
+def run_workload(name, steps, warmup, torch, dev):
+    import numpy as np
+    cfg = WORKLOADS[name]
+    rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3}[name])
+    setup = setup_gqa if cfg["kind"] == "gqa" else setup_mla
+    c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
+    torch.cuda.synchronize(dev)
+    for i in range(warmup):
+        step(i)
+    c.Sync()
+    torch.cuda.synchronize(dev)
+    c.Timing(True)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(warmup + i)
+    c.Sync()
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    kms, kn = c.KernelTime()
+    c.Timing(False)
+    kavg_s = kms / max(kn, 1) / 1e3
+    achieved = kbytes / kavg_s / 1e9
+    res = {
+        "tokens_per_s": B * steps / elapsed,
+        "ms_per_step": elapsed / steps * 1e3,
+        "step_hbm_gbs": sbytes * steps / elapsed / 1e9,
+        "kernel": kname,
+        "kernel_avg_us": kavg_s * 1e6,
+        "kernel_bytes": kbytes,
+        "kernel_gbs": achieved,
+        "desc": desc,
+        "lens": lens,
+        "cfg": cfg,
+    }
+    c.close()
+    return res
+
+
+def cpu_baseline_gqa(cfg, lens, budget_s=12.0):
+    """The reference's decode step (mha.go:283-348) restated in C, one thread:
+    append, widen the whole capacity buffer, GQA-expand by copy, score /
+    fastexp softmax / P.V loops -- per sequence (the reference runs batch 1)."""
+    import numpy as np
+    import oracle
+    H, KVH, D = cfg["H"], cfg["KVH"], cfg["D"]
+    rng = np.random.default_rng(7)
+    done = 0
+    t_total = 0.0
+    i = 0
+    while t_total < budget_s and i < 4 * len(lens):
+        T = lens[i % len(lens)]
+        cap = T + 1
+        kb = oracle.bf16_from_f32(rng.standard_normal((cap, KVH * D), dtype=np.float32))
+        vb = oracle.bf16_from_f32(rng.standard_normal((cap, KVH * D), dtype=np.float32))
+        kn = rng.standard_normal(KVH * D, dtype=np.float32)
+        vn = rng.standard_normal(KVH * D, dtype=np.float32)
+        q = rng.standard_normal((H, D), dtype=np.float32)
+        t0 = time.perf_counter()
+        oracle.ref_gqa_decode_step(kb, vb, cap, T, kn, vn, q, H, KVH, D)
+        t_total += time.perf_counter() - t0
+        done += 1
+        i += 1
+    return {"value": done / t_total, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{done} single-sequence decode steps at T={lens[0]}+1 (C restatement of "
+                      f"mha.go:283-348, -O2 -ffp-contract=off, 1 thread), {t_total:.1f} s"}
+
+
+def cpu_baseline_mla(cfg, lens, budget_s=12.0):
+    """The reference's MLA decode step (mla.go:309-377: decompress every cached
+    latent through W_UK and W_UV, then attend) restated in C, one thread.
+    Sampled on a subset of heads (cost is linear in heads) and scaled."""
+    import numpy as np
+    import oracle
+    H, D, T = cfg["H"], cfg["D"], lens[0] + 1
+    h_s = 1
+    rng = np.random.default_rng(8)
+    c = oracle.round_bf16(rng.standard_normal((T, 512), dtype=np.float32))
+    kr = oracle.round_bf16(rng.standard_normal((T, 64), dtype=np.float32))
+    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, h_s * D)))
+    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, h_s * D)))
+    qc = rng.standard_normal((h_s, 1, D), dtype=np.float32)
+    qr = rng.standard_normal((h_s, 1, 64), dtype=np.float32)
+    t0 = time.perf_counter()
+    oracle.mla_attend(qc, qr, c, kr, w_uk, w_uv, "ref")
+    dt = (time.perf_counter() - t0) * (H / h_s)
+    return {"value": 1.0 / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"1 sequence step at T={T}, {h_s} of {H} heads timed ({dt / (H / h_s):.1f} s) "
+                      f"and scaled x{H // h_s} (decompress-all C restatement of mla.go:309-377, 1 thread)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", default="gqa8k", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the secondary workloads reported beside the headline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on ONE GPU (no collectives, no sharding); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import relux_amd
+    relux_amd.load()
+    dev = torch.device("cuda", 0)
+    print(f"[bench] workload {args.workload} steps {args.steps} warmup {args.warmup}",
+          file=sys.stderr, flush=True)
+    r = run_workload(args.workload, args.steps, args.warmup, torch, dev)
+    print(f"[bench] {args.workload}: {r['tokens_per_s']:.0f} tok/s, kernel {r['kernel_avg_us']:.1f} us, "
+          f"{r['kernel_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    secondary = []
+    if not args.no_secondary:
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k") if w != args.workload]:
+            s = run_workload(name, max(50, args.steps // 2), args.warmup, torch, dev)
+            print(f"[bench] {name}: {s['tokens_per_s']:.0f} tok/s, kernel {s['kernel_avg_us']:.1f} us, "
+                  f"{s['kernel_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+            secondary.append({"workload": s["desc"]["workload"], "tokens_per_s": round(s["tokens_per_s"], 1),
+                              "ms_per_step": round(s["ms_per_step"], 4),
+                              "kernel": s["kernel"], "kernel_avg_us": round(s["kernel_avg_us"], 2),
+                              "kernel_gbs": round(s["kernel_gbs"], 1),
+                              "kernel_frac_of_8TBs": round(s["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                              "step_hbm_gbs": round(s["step_hbm_gbs"], 1)})
+    cpu = None
+    if not args.no_cpu:
+        cfg = WORKLOADS[args.workload]
+        cpu = (cpu_baseline_gqa if cfg["kind"] == "gqa" else cpu_baseline_mla)(cfg, r["lens"])
+    line = {
+        "metric": "decode attn tokens/s + achieved HBM GB/s (% of 8 TB/s) at 1 MI355X, 8k ctx",
+        "value": round(r["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": r["desc"],
+        "hbm_gbs": round(r["step_hbm_gbs"], 1),
+        "hbm_frac": round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": r["kernel"],
+                     "kernel_avg_us": round(r["kernel_avg_us"], 2),
+                     "algorithmic_bytes": r["kernel_bytes"]},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

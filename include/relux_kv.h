@@ -1,0 +1,211 @@
+/*
+ * relux_kv.h -- C ABI of the MI355X (gfx950) KV-cache hot path for relux.
+ *
+ * One shared library, librelux_kv.so, exports these entry points.  They
+ * replace the cache objects and the cached-attention loops of relux's
+ * internal/transformer package; a Go host binds them with purego (no CGO),
+ * see INTEGRATION.md.  Plain C types only: int32/int64/float, void* for
+ * opaque handles and device buffers, int32* for small host arrays.  No
+ * struct is passed by value.
+ *
+ * Conventions
+ *   - Every entry returns int32: RLX_OK (0) or a negative RLX_ERR_* code;
+ *     rlx_last_error() copies the message of the calling thread's last
+ *     failure.
+ *   - Bulk tensors (K/V/latent sources, queries, outputs, weights) are
+ *     DEVICE pointers (from rlx_dev_alloc or any HIP allocation).  Small
+ *     metadata (sequence ids, token counts, dumps) are HOST pointers.
+ *   - A cache handle owns one in-order HIP stream; calls on a handle are
+ *     asynchronous on that stream unless they return host data (lengths,
+ *     tables, free lists), which synchronise.  rlx_cache_sync() waits.
+ *     Calls on one handle must be serialised by the caller (the reference
+ *     modules are not goroutine-safe either, module.go:62-63).
+ *   - bf16 storage uses the reference's integer round-to-nearest-even
+ *     conversion (dtype_convert.go:15-24), bit for bit.
+ */
+#ifndef RELUX_KV_H
+#define RELUX_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define RLX_OK 0
+#define RLX_ERR_INVALID -1     /* bad argument / shape                     */
+#define RLX_ERR_OVERFLOW -2    /* capacity exceeded: the reference panics,
+                                  kvcache.go:282-285, mla_cache.go:164-167 */
+#define RLX_ERR_POOL -3        /* page pool exhausted                      */
+#define RLX_ERR_LAYER -4       /* layer index out of range: the reference
+                                  panics, kvcache.go:241-243               */
+#define RLX_ERR_HIP -5         /* HIP runtime failure                      */
+#define RLX_ERR_UNSUPPORTED -6 /* shape outside the compiled kernel set    */
+#define RLX_ERR_STATE -7       /* rollback/evict beyond what is stored     */
+
+/* ---- element types and layouts --------------------------------------- */
+#define RLX_F32 0
+#define RLX_BF16 1
+
+/* Row layout of multi-sequence K/V sources and of queries/outputs.  A call
+ * names n_seqs sequences; sequence i contributes n[i] rows, concatenated in
+ * call order.
+ *   RLX_LAYOUT_HSD: per sequence [heads][n][dim] -- the reference's
+ *                   post-rearrange tensors (rearrangeBSNH, mha.go:789-803).
+ *   RLX_LAYOUT_SHD: per sequence [n][heads][dim] -- projection output order. */
+#define RLX_LAYOUT_HSD 0
+#define RLX_LAYOUT_SHD 1
+
+/* Attention mask for a call with n_q query rows on a sequence holding T
+ * live tokens (the queries are the last n_q tokens appended).
+ *   RLX_MASK_CAUSAL: query i attends keys j <= T - n_q + i.
+ *   RLX_MASK_REF:    the reference's rule: mask j > i only when n_q == T,
+ *                    else attend everything (mha.go:337-342, mla.go:365-370).
+ *   RLX_MASK_NONE:   attend every live key. */
+#define RLX_MASK_CAUSAL 0
+#define RLX_MASK_REF 1
+#define RLX_MASK_NONE 2
+
+/* ---- runtime ---------------------------------------------------------- */
+/* Select the device for this thread; must be a gfx950 GPU.  Replaces the
+ * rnxa engine bring-up the ladder does (internal/compute/factory.go:32-85). */
+int32_t rlx_init(int32_t device);
+int32_t rlx_last_error(char *buf, int64_t len);
+/* Library version string into buf. */
+int32_t rlx_version(char *buf, int64_t len);
+
+/* Device buffers for a host without a HIP binding of its own.  Replaces
+ * the host-side staging the rnxa MatMulFloat32 path performs
+ * (internal/compute/rnxa.go:219-227). */
+int32_t rlx_dev_alloc(int64_t bytes, void **out);
+int32_t rlx_dev_free(void *ptr);
+int32_t rlx_h2d(void *dst, const void *src, int64_t bytes);
+int32_t rlx_d2h(void *dst, const void *src, int64_t bytes);
+int32_t rlx_device_sync(void);
+
+/* ---- instrumentation (no reference counterpart) ----------------------- */
+/* enable != 0: bracket the main attention kernel of every later attend call
+ * on this handle with HIP events (on the handle's stream); 0 disables.
+ * Either way the recorded intervals are discarded. */
+int32_t rlx_cache_timing(void *cache, int32_t enable);
+/* Synchronise, then report the summed duration (ms) and number of the
+ * attention-kernel launches recorded since the last call, and clear them. */
+int32_t rlx_cache_kernel_time(void *cache, float *total_ms, int32_t *count);
+
+/* ---- cache lifetime --------------------------------------------------- */
+/* Paged bf16 GQA K/V cache for `layers` layers.  Replaces
+ * NewKVCacheSized(numLayers, maxLen, numKVHeads, headDim, BFloat16)
+ * (kvcache.go:66-93): capacity per sequence is max_pages_per_seq *
+ * page_tokens tokens; pool_pages pages per layer are shared by up to
+ * max_seqs sequences.  head_dim in {64, 128}; page_tokens a multiple of 16. */
+int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t page_tokens,
+                      int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
+
+/* Paged bf16 MLA latent cache: per token the latent c^KV (d_c) and the
+ * post-RoPE k^R (d_r).  Replaces NewMLACache(numLayers, maxLen, dC, dHR)
+ * (mla_cache.go:38-59), whose f32 storage becomes bf16 here.
+ * d_c = 512, d_r = 64 (DeepSeek-V2/V3 attention shapes). */
+int32_t rlx_mla_create(int32_t layers, int32_t d_c, int32_t d_r, int32_t page_tokens,
+                       int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
+
+int32_t rlx_cache_destroy(void *cache);
+/* Drop every sequence and return all pages.  Replaces KVCache.Reset /
+ * MLACache.Reset (kvcache.go:174-202, mla_cache.go:118-133); stored bytes
+ * are not cleared (the length is what makes them invisible). */
+int32_t rlx_cache_reset(void *cache);
+int32_t rlx_cache_sync(void *cache);
+/* Use `stream` (a hipStream_t, default priority) for this handle's work
+ * instead of its own stream; NULL restores the handle's stream. */
+int32_t rlx_cache_set_stream(void *cache, void *stream);
+
+/* ---- append (scatter into pages) -------------------------------------- */
+/* Append n_tok[i] tokens to sequence seq_ids[i] of `layer`, converting to
+ * bf16 with BF16FromF32.  k_src/v_src hold the rows of all n_seqs
+ * sequences in `src_layout` ([kv_heads][n][head_dim] or [n][kv_heads][...]).
+ * Replaces KVCache.Append + copyInto (kvcache.go:240-316, 407-438) for a
+ * batch of sequences; pages are taken from the layer's LIFO free list as
+ * page boundaries are crossed.  Fails without changing state on overflow
+ * (RLX_ERR_OVERFLOW) or pool exhaustion (RLX_ERR_POOL). */
+int32_t rlx_kv_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                      const int32_t *n_tok, const void *k_src, const void *v_src,
+                      int32_t src_dtype, int32_t src_layout);
+
+/* MLA: c_src [sum n][d_c], kr_src [sum n][d_r] (post-RoPE).  Replaces
+ * MLACache.Append (mla_cache.go:152-182). */
+int32_t rlx_mla_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_tok, const void *c_src, const void *kr_src,
+                       int32_t src_dtype);
+
+/* ---- paged gather (View) ---------------------------------------------- */
+/* Copy the live tokens of each listed sequence through the page table into
+ * dense bf16 device buffers: k_out/v_out per sequence [kv_heads][T][head_dim]
+ * (the shape View returns, kvcache.go:363-380), concatenated in call order. */
+int32_t rlx_kv_gather(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                      void *k_out, void *v_out);
+/* MLA: c_out [T][d_c], kr_out [T][d_r] per sequence (mla_cache.go:222-233). */
+int32_t rlx_mla_gather(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       void *c_out, void *kr_out);
+
+/* ---- attention over the cache ----------------------------------------- */
+/* GQA flash-decoding / verify / chunked prefill over the paged cache for
+ * n_seqs sequences with n_q[i] query rows each.  q and out: [rows of all
+ * sequences] in qo_layout with num_heads heads of head_dim; head h reads
+ * KV head h / (num_heads / kv_heads).  scale <= 0 selects 1/sqrt(head_dim).
+ * Replaces mha.go:291-348 (View, widen, GQA expand, score/softmax/PV
+ * loops).  Exact exp softmax with f32 accumulation; the reference's
+ * fastexp32 weights are matched within tolerance, not bit for bit. */
+int32_t rlx_gqa_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                       int32_t out_dtype);
+
+/* MLA absorbed decode / chunked prefill.  q_nope [rows][num_heads][head_dim],
+ * q_rope [rows][num_heads][d_r] (post-RoPE), w_uk and w_uv bf16
+ * [d_c][num_heads*head_dim] exactly as MLA.W_UK/W_UV are stored (mla.go:42-43),
+ * out [rows][num_heads][head_dim].  Computes the same attention as
+ * mla.go:316-377 (decompress-all) by absorbing W_UK into the query and
+ * W_UV into the output.  scale <= 0 selects 1/sqrt(head_dim + d_r). */
+int32_t rlx_mla_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
+                       const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
+                       float scale, int32_t mask_mode, void *out, int32_t out_dtype);
+
+/* ---- speculative rollback, eviction, compaction (no reference) -------- */
+/* Remove the last n_tokens[i] tokens of sequence seq_ids[i], in list order
+ * (layer -1: every layer).  Pages left empty return to the free list, last
+ * page first, so that append(a||b); rollback(|b|) leaves exactly the state
+ * of append(a).  Validated in full before any change.  The reference never
+ * truncates its caches (speculative.go:146-156); this is the rejected-draft
+ * rollback its SpeculativeDecoder.Generate loop (speculative.go:131-156)
+ * needs after acceptPhase. */
+int32_t rlx_rollback(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                     const int32_t *n_tokens);
+/* Drop the oldest n_pages[i] full pages of sequence seq_ids[i] (layer -1:
+ * every layer); their tokens leave attention, the RoPE position of later
+ * tokens is kept (pos_offset grows by n_pages*page_tokens).  Freed pages are
+ * pushed oldest first.  No reference counterpart. */
+int32_t rlx_evict(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                  const int32_t *n_pages);
+/* Rewrite page-table rows so live pages start at entry 0, logical order
+ * kept; K/V bytes do not move (layer -1: every layer). */
+int32_t rlx_compact(void *cache, int32_t layer);
+/* Free every page of one sequence (layer -1: every layer). */
+int32_t rlx_seq_release(void *cache, int32_t layer, int32_t seq);
+
+/* ---- state queries (synchronising) ------------------------------------ */
+/* Live token count; replaces TotalLen (kvcache.go:383-388). */
+int32_t rlx_seq_len(void *cache, int32_t layer, int32_t seq, int32_t *len_out);
+/* {live_len, first_entry, pos_offset, pages_in_use}. */
+int32_t rlx_seq_state(void *cache, int32_t layer, int32_t seq, int32_t *state4_out);
+/* Copy the DEVICE page-table row (max_pages_per_seq int32, -1 = empty). */
+int32_t rlx_page_table(void *cache, int32_t layer, int32_t seq, int32_t *row_out);
+/* Copy the layer's free-page stack bottom..top; *n_out = its depth. */
+int32_t rlx_free_list(void *cache, int32_t layer, int32_t *out, int32_t cap, int32_t *n_out);
+/* Device address of a layer's page pools (for zero-copy inspection). */
+int32_t rlx_pool_ptr(void *cache, int32_t layer, void **k_pool, void **v_pool);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RELUX_KV_H */

@@ -1,0 +1,229 @@
+// Page-table patches, paged append (scatter) and paged gather (View).
+//
+// These kernels are byte movers: HBM-bound, one pass, 16-byte accesses
+// on the contiguous side of every copy.
+#include "rlx_common.h"
+
+namespace rlx {
+
+__global__ void patch_kernel(int32_t *__restrict__ table, const Patch *__restrict__ p, int n) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) table[p[i].idx] = p[i].val;
+}
+
+__global__ void fill_i32_kernel(int32_t *__restrict__ dst, int32_t val, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = val;
+}
+
+hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n) {
+    if (n <= 0) return hipSuccess;
+    patch_kernel<<<(n + 255) / 256, 256, 0, s>>>(table, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n) {
+    if (n <= 0) return hipSuccess;
+    fill_i32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dst, val, n);
+    return hipGetLastError();
+}
+
+// Load 8 consecutive source elements (f32 or bf16) and convert them to bf16
+// with the reference's integer RNE rule (dtype_convert.go:15-24).
+__device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src_bf16,
+                                           uint16_t (&o)[8]) {
+    if (src_bf16) {
+        u32x4 v = *(const u32x4 *)((const uint16_t *)src + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[2 * i] = (uint16_t)(v[i] & 0xFFFFu);
+            o[2 * i + 1] = (uint16_t)(v[i] >> 16);
+        }
+    } else {
+        const float4 *f = (const float4 *)((const float *)src + off);
+        float4 a = f[0], b = f[1];
+        o[0] = bf16_rne(a.x); o[1] = bf16_rne(a.y); o[2] = bf16_rne(a.z); o[3] = bf16_rne(a.w);
+        o[4] = bf16_rne(b.x); o[5] = bf16_rne(b.y); o[6] = bf16_rne(b.z); o[7] = bf16_rne(b.w);
+    }
+}
+
+// GQA append.  Thread = (token, kv head, 8-dim chunk).  K goes to a row page
+// with one 16-byte store; V goes to a dim-major page (8 strided 2-byte
+// stores).  The first n_patch threads also apply the table patches; the
+// scatter itself takes its destinations from the plan, not the table.
+__global__ void kv_append_kernel(uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool,
+                                 int32_t *__restrict__ table, const Patch *__restrict__ patches,
+                                 int n_patch, const AppendTok *__restrict__ toks, int n_tok,
+                                 const void *__restrict__ k_src, const void *__restrict__ v_src,
+                                 int src_bf16, int layout, int kvh, int hd, int P) {
+    int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid < n_patch) table[patches[gid].idx] = patches[gid].val;
+    const int chunks = hd >> 3;
+    const int64_t per_tok = (int64_t)kvh * chunks;
+    if (gid >= (int64_t)n_tok * per_tok) return;
+    const int t = (int)(gid / per_tok);
+    const int rem = (int)(gid - (int64_t)t * per_tok);
+    const int h = rem / chunks;
+    const int d0 = (rem - h * chunks) * 8;
+    const AppendTok tk = toks[t];
+    const int j = t - tk.seq_row0;  // row within its sequence
+    int64_t src_off;
+    if (layout == kLayoutSHD)
+        src_off = ((int64_t)t * kvh + h) * hd + d0;
+    else
+        src_off = (int64_t)tk.seq_row0 * kvh * hd + ((int64_t)h * tk.seq_n + j) * hd + d0;
+    uint16_t kv[8], vv[8];
+    load8_bf16(k_src, src_off, src_bf16, kv);
+    load8_bf16(v_src, src_off, src_bf16, vv);
+    uint16_t *kd = kpool + (((int64_t)tk.page * kvh + h) * P + tk.slot) * hd + d0;
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = (uint32_t)kv[2 * i] | ((uint32_t)kv[2 * i + 1] << 16);
+    *(u32x4 *)kd = pk;
+    uint16_t *vd = vpool + (((int64_t)tk.page * kvh + h) * hd + d0) * P + tk.slot;
+#pragma unroll
+    for (int i = 0; i < 8; i++) vd[(int64_t)i * P] = vv[i];
+}
+
+hipError_t launch_kv_append(hipStream_t s, uint16_t *kpool, uint16_t *vpool, int32_t *table,
+                            const Patch *patches, int n_patch, const AppendTok *toks, int n_tok,
+                            const void *k_src, const void *v_src, int src_bf16, int layout,
+                            int kvh, int hd, int P) {
+    int64_t work = (int64_t)n_tok * kvh * (hd / 8);
+    if (work < n_patch) work = n_patch;
+    if (work <= 0) return hipSuccess;
+    kv_append_kernel<<<(unsigned)((work + 255) / 256), 256, 0, s>>>(
+        kpool, vpool, table, patches, n_patch, toks, n_tok, k_src, v_src, src_bf16, layout, kvh,
+        hd, P);
+    return hipGetLastError();
+}
+
+// MLA append.  Thread = (token, 8-element chunk of the 576-element row);
+// chunks 0..63 come from c_src, 64..71 from kr_src.
+__global__ void mla_append_kernel(uint16_t *__restrict__ pool, int32_t *__restrict__ table,
+                                  const Patch *__restrict__ patches, int n_patch,
+                                  const AppendTok *__restrict__ toks, int n_tok,
+                                  const void *__restrict__ c_src, const void *__restrict__ kr_src,
+                                  int src_bf16, int P) {
+    int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid < n_patch) table[patches[gid].idx] = patches[gid].val;
+    constexpr int chunks = kMlaRow / 8;  // 72
+    if (gid >= (int64_t)n_tok * chunks) return;
+    const int t = (int)(gid / chunks);
+    const int ch = (int)(gid - (int64_t)t * chunks);
+    const AppendTok tk = toks[t];
+    uint16_t v[8];
+    if (ch < kMlaDc / 8)
+        load8_bf16(c_src, (int64_t)t * kMlaDc + ch * 8, src_bf16, v);
+    else
+        load8_bf16(kr_src, (int64_t)t * kMlaDr + (ch - kMlaDc / 8) * 8, src_bf16, v);
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+    *(u32x4 *)(pool + ((int64_t)tk.page * P + tk.slot) * kMlaRow + ch * 8) = pk;
+}
+
+hipError_t launch_mla_append(hipStream_t s, uint16_t *pool, int32_t *table, const Patch *patches,
+                             int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
+                             const void *kr_src, int src_bf16, int P) {
+    int64_t work = (int64_t)n_tok * (kMlaRow / 8);
+    if (work < n_patch) work = n_patch;
+    if (work <= 0) return hipSuccess;
+    mla_append_kernel<<<(unsigned)((work + 255) / 256), 256, 0, s>>>(
+        pool, table, patches, n_patch, toks, n_tok, c_src, kr_src, src_bf16, P);
+    return hipGetLastError();
+}
+
+// Paged gather of GQA K and V into dense [kvh][T][hd] per sequence.
+// grid.y = sequence of the call; x covers the sequence's work.  K: thread =
+// (token, head, 8-dim chunk), 16-byte read and write.  V: thread = (head, dim,
+// 8-token chunk), 16-byte read of a dim-major page row, 8 strided writes.
+__global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
+                                 const uint16_t *__restrict__ vpool,
+                                 const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
+                                 uint16_t *__restrict__ k_out, uint16_t *__restrict__ v_out,
+                                 int kvh, int hd, int P) {
+    const AttRow R = rows[blockIdx.y];
+    const int chunks = hd >> 3;
+    const int64_t nk = (int64_t)R.len * kvh * chunks;
+    const int64_t base = (int64_t)R.qrow * kvh * hd;  // qrow holds the output token offset
+    for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < nk;
+         gid += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(gid / ((int64_t)kvh * chunks));
+        const int rem = (int)(gid - (int64_t)t * kvh * chunks);
+        const int h = rem / chunks;
+        const int d0 = (rem - h * chunks) * 8;
+        const int page = table[R.tab + t / P];
+        const int slot = t % P;
+        u32x4 v = *(const u32x4 *)(kpool + (((int64_t)page * kvh + h) * P + slot) * hd + d0);
+        *(u32x4 *)(k_out + base + ((int64_t)h * R.len + t) * hd + d0) = v;
+    }
+    const int tchunks = (R.len + 7) >> 3;
+    const int64_t nv = (int64_t)kvh * hd * tchunks;
+    for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < nv;
+         gid += (int64_t)gridDim.x * blockDim.x) {
+        const int tc = (int)(gid % tchunks);
+        const int hd_i = (int)(gid / tchunks);
+        const int h = hd_i / hd;
+        const int d = hd_i - h * hd;
+        const int t0 = tc * 8;
+        const int page = table[R.tab + t0 / P];
+        const int slot = t0 % P;
+        u32x4 v = *(const u32x4 *)(vpool + (((int64_t)page * kvh + h) * hd + d) * P + slot);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (t0 + i < R.len) {
+                uint32_t w = v[i >> 1];
+                v_out[base + ((int64_t)h * R.len + t0 + i) * hd + d] =
+                    (uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFFu));
+            }
+        }
+    }
+}
+
+hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                            const int32_t *table, const AttRow *rows, int n_rows, int max_len,
+                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int P) {
+    if (n_rows <= 0 || max_len <= 0) return hipSuccess;
+    int64_t work = (int64_t)max_len * kvh * (hd / 8);
+    int blocks = (int)((work + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    kv_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(kpool, vpool, table, rows, k_out, v_out,
+                                                          kvh, hd, P);
+    return hipGetLastError();
+}
+
+// Paged gather of MLA rows into dense c [T][512] and kr [T][64].
+__global__ void mla_gather_kernel(const uint16_t *__restrict__ pool,
+                                  const int32_t *__restrict__ table,
+                                  const AttRow *__restrict__ rows, uint16_t *__restrict__ c_out,
+                                  uint16_t *__restrict__ kr_out, int P) {
+    const AttRow R = rows[blockIdx.y];
+    constexpr int chunks = kMlaRow / 8;
+    const int64_t n = (int64_t)R.len * chunks;
+    for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < n;
+         gid += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(gid / chunks);
+        const int ch = (int)(gid - (int64_t)t * chunks);
+        const int page = table[R.tab + t / P];
+        u32x4 v = *(const u32x4 *)(pool + ((int64_t)page * P + t % P) * kMlaRow + ch * 8);
+        const int64_t row = (int64_t)R.qrow + t;
+        if (ch < kMlaDc / 8)
+            *(u32x4 *)(c_out + row * kMlaDc + ch * 8) = v;
+        else
+            *(u32x4 *)(kr_out + row * kMlaDr + (ch - kMlaDc / 8) * 8) = v;
+    }
+}
+
+hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
+                             uint16_t *kr_out, int P) {
+    if (n_rows <= 0 || max_len <= 0) return hipSuccess;
+    int64_t work = (int64_t)max_len * (kMlaRow / 8);
+    int blocks = (int)((work + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    mla_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(pool, table, rows, c_out, kr_out, P);
+    return hipGetLastError();
+}
+
+}  // namespace rlx

@@ -1,0 +1,102 @@
+// Shared device types, plan records and launcher declarations of librelux_kv.
+//
+// HBM layout of the paged caches (bf16 = uint16 bit patterns):
+//   GQA K pool : [pool_pages][kv_heads][page_tokens][head_dim]   (row pages)
+//   GQA V pool : [pool_pages][kv_heads][head_dim][page_tokens]   (dim-major pages:
+//                the tokens of one dim are contiguous, which is the operand
+//                order the P.V matrix-core step consumes)
+//   MLA pool   : [pool_pages][page_tokens][d_c + d_r]            (latent | rope key)
+//   page table : int32 [layers][max_seqs][max_pages_per_seq], -1 = empty entry
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rlx {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) short sh4;
+typedef __attribute__((ext_vector_type(4))) float fl4;
+typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+// dtype_convert.go:15-24: integer round-to-nearest-even, no NaN special case.
+__host__ __device__ __forceinline__ uint16_t bf16_rne(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__host__ __device__ __forceinline__ float bf16_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+constexpr int kLayoutHSD = 0;
+constexpr int kLayoutSHD = 1;
+constexpr int kMaskCausal = 0;
+constexpr int kMaskRef = 1;
+constexpr int kMaskNone = 2;
+
+constexpr int kMlaDc = 512;
+constexpr int kMlaDr = 64;
+constexpr int kMlaRow = kMlaDc + kMlaDr;  // 576 bf16 = 1152 B per token
+
+// One table write: table[idx] = val.  Indices in one batch are unique.
+struct Patch {
+    int32_t idx;
+    int32_t val;
+};
+
+// One appended token: destination page/slot and where its rows sit in the
+// caller's source buffer (sequence's first call-row and its row count).
+struct AppendTok {
+    int32_t page;
+    int32_t slot;
+    int32_t seq_row0;
+    int32_t seq_n;
+};
+
+// One sequence of an attention / gather call.
+struct AttRow {
+    int32_t tab;     // flat index of the sequence's first live table entry
+    int32_t len;     // live tokens
+    int32_t nq;      // query rows (the last nq live tokens)
+    int32_t qrow;    // first call-row of this sequence's queries / outputs
+    int32_t nsplit;  // context splits
+    int32_t part;    // first partial slot of this sequence
+};
+
+// ---- launchers (stream-ordered, return hipError_t of the launch) ----------
+hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
+hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n);
+
+hipError_t launch_kv_append(hipStream_t s, uint16_t *kpool, uint16_t *vpool, int32_t *table,
+                            const Patch *patches, int n_patch, const AppendTok *toks, int n_tok,
+                            const void *k_src, const void *v_src, int src_bf16, int layout,
+                            int kvh, int hd, int P);
+hipError_t launch_mla_append(hipStream_t s, uint16_t *pool, int32_t *table, const Patch *patches,
+                             int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
+                             const void *kr_src, int src_bf16, int P);
+
+hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                            const int32_t *table, const AttRow *rows, int n_rows, int max_len,
+                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int P);
+hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
+                             uint16_t *kr_out, int P);
+
+hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                             const int32_t *table, const AttRow *rows, int n_rows,
+                             const int2 *work, int n_work, const void *q, int q_bf16,
+                             int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
+                             int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
+                             int out_bf16, hipEvent_t ev0, hipEvent_t ev1);
+
+hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, int n_rows, const int2 *work, int n_work,
+                             const void *q_nope, const void *q_rope, int q_bf16,
+                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
+                             int total_q, int max_nq, int P, int chunk, float qscale,
+                             int mask_mode, int nqt, uint16_t *qlat, float *part_o,
+                             float *part_ml, void *out, int out_bf16, hipEvent_t ev0,
+                             hipEvent_t ev1);
+
+}  // namespace rlx

@@ -1,0 +1,307 @@
+// GQA flash-decoding over the paged bf16 cache (decode, speculative verify).
+//
+// Work item = (sequence, context split) x kv head; one 256-thread work-group
+// (4 waves) per item.  Each wave walks 16-token blocks of the split:
+//
+//   S^T[16 tok][16 q-rows] = K_blk[16 x D] . Q^T          (D/32 MFMA 16x16x32 bf16)
+//   online softmax per q-row column (lane-local state, exp2 domain)
+//   O^T[D][16 q-rows]    += V_blk^T[D x 16 tok] . P^T     (D/16 MFMA 16x16x16 bf16)
+//
+// The K rows are the A operand straight from a row page (8 consecutive dims
+// per lane, 16-byte loads); the V^T tile is the A operand straight from a
+// dim-major page (4 consecutive tokens per lane, 8-byte loads); the MFMA
+// result layout of S^T is exactly the B-operand layout P^T needs, so no LDS
+// and no shuffles sit between the two products.  The query rows of a kv head
+// (H/KVH heads x n_q queries) fill the 16-wide N dimension; a second N tile
+// covers up to 32 rows.  The 4 waves merge through LDS and write one
+// unnormalised partial per split; gqa_combine merges splits (log-sum-exp).
+//
+// Reference restated: mha.go:291-348 (score = q.k * 1/sqrt(D), mask,
+// softmaxRows, P.V); exact exp2 replaces fastexp32 (mha.go:823-833), f32
+// accumulation throughout.
+#include "rlx_common.h"
+
+namespace rlx {
+
+__device__ __forceinline__ float wave_max16(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+__device__ __forceinline__ float wave_sum16(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// Last key (inclusive, live index) query qi of a sequence may attend.
+__device__ __forceinline__ int key_limit(int mask_mode, int len, int nq, int qi) {
+    if (mask_mode == kMaskCausal) return len - nq + qi;
+    if (mask_mode == kMaskRef) return (nq == len) ? qi : len - 1;
+    return len - 1;
+}
+
+template <int D, int NQT>
+__global__ __launch_bounds__(256) void gqa_decode_kernel(
+    const uint16_t *__restrict__ kpool, const uint16_t *__restrict__ vpool,
+    const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
+    const int2 *__restrict__ work, const void *__restrict__ q, int q_bf16, int layout, int H,
+    int KVH, int P, int chunk, float qscale, int mask_mode, float *__restrict__ part_o,
+    float *__restrict__ part_ml) {
+    constexpr int KS = D / 32;  // QK k-steps
+    constexpr int MT = D / 16;  // PV m-tiles
+    constexpr int QRP = 16 * NQT;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int2 wk = work[blockIdx.x];
+    const AttRow R = rows[wk.x];
+    const int kvh = blockIdx.y;
+    const int G = H / KVH;
+    const int QR = G * R.nq;
+    const int t_begin = wk.y * chunk;
+    const int t_end = min(R.len, t_begin + chunk);
+
+    // Q^T operand (B of the score product), pre-scaled by scale*log2(e).
+    bf16x8 qb[NQT][KS];
+    int klim[NQT];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const int qr = nt * 16 + col;
+        klim[nt] = R.len - 1;
+        if (qr < QR) {
+            const int qi = qr / G;
+            const int h = kvh * G + (qr - qi * G);
+            klim[nt] = key_limit(mask_mode, R.len, R.nq, qi);
+            const int64_t base = (layout == kLayoutSHD)
+                                     ? ((int64_t)(R.qrow + qi) * H + h) * D
+                                     : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const int64_t off = base + ks * 32 + grp * 8;
+                u32x4 w;
+                if (q_bf16) {
+                    u32x4 raw = *(const u32x4 *)((const uint16_t *)q + off);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        float a = bf16_f32((uint16_t)(raw[i] & 0xFFFFu)) * qscale;
+                        float b = bf16_f32((uint16_t)(raw[i] >> 16)) * qscale;
+                        w[i] = (uint32_t)bf16_rne(a) | ((uint32_t)bf16_rne(b) << 16);
+                    }
+                } else {
+                    const float4 *f = (const float4 *)((const float *)q + off);
+                    float4 a = f[0], b = f[1];
+                    w[0] = (uint32_t)bf16_rne(a.x * qscale) | ((uint32_t)bf16_rne(a.y * qscale) << 16);
+                    w[1] = (uint32_t)bf16_rne(a.z * qscale) | ((uint32_t)bf16_rne(a.w * qscale) << 16);
+                    w[2] = (uint32_t)bf16_rne(b.x * qscale) | ((uint32_t)bf16_rne(b.y * qscale) << 16);
+                    w[3] = (uint32_t)bf16_rne(b.z * qscale) | ((uint32_t)bf16_rne(b.w * qscale) << 16);
+                }
+                qb[nt][ks] = __builtin_bit_cast(bf16x8, w);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) qb[nt][ks] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
+        }
+    }
+
+    float m_run[NQT], l_part[NQT];
+    fl4 acc[NQT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        m_run[nt] = -INFINITY;
+        l_part[nt] = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int64_t kstride = (int64_t)P * D;  // one kv head of one page
+    for (int t0 = t_begin + 16 * wave; t0 < t_end; t0 += 64) {
+        const int page = table[R.tab + t0 / P];
+        const int slot0 = t0 % P;
+        const uint16_t *kp = kpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)(slot0 + col) * D + grp * 8;
+        const uint16_t *vp = vpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)col * P + slot0 + grp * 4;
+        u32x4 kr[KS];
+        u32x2 vr[MT];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) kr[ks] = *(const u32x4 *)(kp + ks * 32);
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) vr[mt] = *(const u32x2 *)(vp + (int64_t)mt * 16 * P);
+
+        // Tokens past the live length sit in the tail page's unused slots:
+        // their V must contribute exact zeros whatever bytes they hold.
+        if (t0 + 16 > R.len) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (t0 + grp * 4 + j >= R.len) {
+                    const uint32_t keep = (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) vr[mt][j >> 1] &= keep;
+                }
+            }
+        }
+
+        sh4 pb[NQT];
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++) {
+            fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ks]), qb[nt][ks], s, 0, 0, 0);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + grp * 4 + i;
+                s[i] = (t <= klim[nt]) ? s[i] : -INFINITY;
+                mx = fmaxf(mx, s[i]);
+            }
+            mx = wave_max16(mx);
+            const float m_new = fmaxf(m_run[nt], mx);
+            float c, p[4];
+            if (m_new == -INFINITY) {
+                c = 1.f;
+                p[0] = p[1] = p[2] = p[3] = 0.f;
+            } else {
+                c = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
+#pragma unroll
+                for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
+            }
+            l_part[nt] = l_part[nt] * c + ((p[0] + p[1]) + (p[2] + p[3]));
+            m_run[nt] = m_new;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[nt][mt] *= c;
+            u32x2 pw;
+            pw[0] = (uint32_t)bf16_rne(p[0]) | ((uint32_t)bf16_rne(p[1]) << 16);
+            pw[1] = (uint32_t)bf16_rne(p[2]) | ((uint32_t)bf16_rne(p[3]) << 16);
+            pb[nt] = __builtin_bit_cast(sh4, pw);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(sh4, vr[mt]), pb[nt], acc[nt][mt], 0, 0, 0);
+    }
+
+    // ---- merge the 4 waves of the work-group -------------------------------
+    __shared__ float sm[4][QRP], sl[4][QRP];
+    __shared__ fl4 so[3][NQT][MT][64];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const float lt = wave_sum16(l_part[nt]);
+        if (grp == 0) {
+            sm[wave][nt * 16 + col] = m_run[nt];
+            sl[wave][nt * 16 + col] = lt;
+        }
+        if (wave > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) so[wave - 1][nt][mt][lane] = acc[nt][mt];
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int pidx = R.part + wk.y;
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const int qr = nt * 16 + col;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm[w][qr]);
+        float f[4], L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            f[w] = (sm[w][qr] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sm[w][qr] - M);
+            L += f[w] * sl[w][qr];
+        }
+        float *po = part_o + (((int64_t)pidx * KVH + kvh) * QRP + qr) * D;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            fl4 o = acc[nt][mt] * f[0];
+#pragma unroll
+            for (int w = 1; w < 4; w++) o += so[w - 1][nt][mt][lane] * f[w];
+            *(fl4 *)(po + mt * 16 + grp * 4) = o;
+        }
+        if (grp == 0) {
+            float *pm = part_ml + (((int64_t)pidx * KVH + kvh) * QRP + qr) * 2;
+            pm[0] = M;
+            pm[1] = L;
+        }
+    }
+}
+
+// Merge the splits of each (sequence, kv head): O = sum_s 2^(m_s-M) o_s /
+// sum_s 2^(m_s-M) l_s, written in the caller's layout and dtype.
+__global__ __launch_bounds__(256) void gqa_combine_kernel(
+    const AttRow *__restrict__ rows, const float *__restrict__ part_o,
+    const float *__restrict__ part_ml, void *__restrict__ out, int out_bf16, int layout, int H,
+    int KVH, int D, int QRP) {
+    const AttRow R = rows[blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int G = H / KVH;
+    const int QR = G * R.nq;
+    for (int idx = threadIdx.x; idx < QR * D; idx += blockDim.x) {
+        const int qr = idx / D;
+        const int d = idx - qr * D;
+        float M = -INFINITY;
+        for (int s = 0; s < R.nsplit; s++)
+            M = fmaxf(M, part_ml[(((int64_t)(R.part + s) * KVH + kvh) * QRP + qr) * 2]);
+        float L = 0.f, O = 0.f;
+        for (int s = 0; s < R.nsplit; s++) {
+            const int64_t b = ((int64_t)(R.part + s) * KVH + kvh) * QRP + qr;
+            const float m = part_ml[b * 2];
+            const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+            L += f * part_ml[b * 2 + 1];
+            O += f * part_o[b * D + d];
+        }
+        const float v = (L > 0.f) ? O / L : 0.f;
+        const int qi = qr / G;
+        const int h = kvh * G + (qr - qi * G);
+        const int64_t o = (layout == kLayoutSHD)
+                              ? ((int64_t)(R.qrow + qi) * H + h) * D + d
+                              : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D + d;
+        if (out_bf16)
+            ((uint16_t *)out)[o] = bf16_rne(v);
+        else
+            ((float *)out)[o] = v;
+    }
+}
+
+template <int D, int NQT>
+static hipError_t launch_gqa_t(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                               const int32_t *table, const AttRow *rows, int n_rows,
+                               const int2 *work, int n_work, const void *q, int q_bf16,
+                               int layout, int H, int KVH, int P, int chunk, float qscale,
+                               int mask_mode, float *part_o, float *part_ml, void *out,
+                               int out_bf16, hipEvent_t ev0, hipEvent_t ev1) {
+    if (ev0) (void)hipEventRecord(ev0, s);
+    gqa_decode_kernel<D, NQT><<<dim3(n_work, KVH), 256, 0, s>>>(
+        kpool, vpool, table, rows, work, q, q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode,
+        part_o, part_ml);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev1) (void)hipEventRecord(ev1, s);
+    gqa_combine_kernel<<<dim3(n_rows, KVH), 256, 0, s>>>(rows, part_o, part_ml, out, out_bf16,
+                                                         layout, H, KVH, D, 16 * NQT);
+    return hipGetLastError();
+}
+
+hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                             const int32_t *table, const AttRow *rows, int n_rows,
+                             const int2 *work, int n_work, const void *q, int q_bf16,
+                             int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
+                             int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
+                             int out_bf16, hipEvent_t ev0, hipEvent_t ev1) {
+    if (n_work <= 0) return hipSuccess;
+#define RLX_GQA_CASE(DD, NN)                                                                    \
+    if (hd == DD && nqt == NN)                                                                  \
+        return launch_gqa_t<DD, NN>(s, kpool, vpool, table, rows, n_rows, work, n_work, q,      \
+                                    q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode, part_o, \
+                                    part_ml, out, out_bf16, ev0, ev1);
+    RLX_GQA_CASE(128, 1)
+    RLX_GQA_CASE(128, 2)
+    RLX_GQA_CASE(64, 1)
+    RLX_GQA_CASE(64, 2)
+#undef RLX_GQA_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace rlx

@@ -1,0 +1,337 @@
+// MLA absorbed decode over the paged bf16 latent cache.
+//
+// The reference decompresses every cached latent each step (mla.go:316-377):
+//   K^C = C.W_UK, V = C.W_UV, s = (q_c.k_c + q_r.k_r)/sqrt(D+dR), o = softmax(s).V.
+// Because K^C and V are linear in C the same numbers follow from
+//   q_lat[h] = W_UK[:,h] q_c[h]            (absorb, once per query)
+//   s[h,t]   = q_lat[h].c_t + q_r[h].k^R_t  (576-wide dot on the raw cache row)
+//   o_lat[h] = sum_t p[h,t] c_t             (512-wide)
+//   o[h]     = W_UV[:,h]^T o_lat[h]         (once per query)
+// which reads each cached row once instead of expanding it H*D*2 times.
+//
+// Work item = (sequence, context split); one 256-thread work-group (4 waves).
+// A 16-token tile of cache rows (16 x 1152 B) is staged in LDS (double
+// buffered from registers).  Scores: the 36 k-steps of S^T[16 tok][16 rows]
+// are split 9 per wave (MFMA 16x16x16, A = tile rows read from LDS) and the
+// four partial S^T are summed in LDS.  Every wave then runs the same online
+// softmax; wave w owns latent channels [128w, 128w+128) of
+// O^T[512][16 rows] += C^T . P^T (MFMA 16x16x16, A = tile columns read
+// transposed from LDS, B = P^T straight from the score registers).
+#include "rlx_common.h"
+
+namespace rlx {
+
+constexpr int kPitch = kMlaRow + 4;  // 580 bf16 = 1160 B: 8-byte aligned rows,
+                                     // and 4-row strides fall on distinct banks
+
+__device__ __forceinline__ float mla_max16(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+__device__ __forceinline__ float mla_sum16(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+__device__ __forceinline__ int mla_key_limit(int mask_mode, int len, int nq, int qi) {
+    if (mask_mode == kMaskCausal) return len - nq + qi;
+    if (mask_mode == kMaskRef) return (nq == len) ? qi : len - 1;
+    return len - 1;
+}
+
+// q_lat[row][h][0:512] = bf16(qscale * sum_d q_nope[row][h][d] * W_UK[c][h*D+d]),
+// q_lat[row][h][512:576] = bf16(qscale * q_rope[row][h][:]).
+__global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
+                                                         const void *__restrict__ q_rope,
+                                                         int q_bf16,
+                                                         const uint16_t *__restrict__ w_uk,
+                                                         int H, int D, float qscale,
+                                                         uint16_t *__restrict__ qlat) {
+    const int row = blockIdx.x, h = blockIdx.y;
+    __shared__ float qn[256];
+    const int64_t qoff = ((int64_t)row * H + h) * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x)
+        qn[d] = q_bf16 ? bf16_f32(((const uint16_t *)q_nope)[qoff + d]) : ((const float *)q_nope)[qoff + d];
+    __syncthreads();
+    uint16_t *dst = qlat + ((int64_t)row * H + h) * kMlaRow;
+    const int64_t wpitch = (int64_t)H * D;
+    for (int c = threadIdx.x; c < kMlaDc; c += blockDim.x) {
+        const uint16_t *w = w_uk + (int64_t)c * wpitch + (int64_t)h * D;
+        float acc = 0.f;
+        for (int d = 0; d < D; d += 8) {
+            u32x4 v = *(const u32x4 *)(w + d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                acc += qn[d + 2 * i] * bf16_f32((uint16_t)(v[i] & 0xFFFFu));
+                acc += qn[d + 2 * i + 1] * bf16_f32((uint16_t)(v[i] >> 16));
+            }
+        }
+        dst[c] = bf16_rne(acc * qscale);
+    }
+    const int64_t roff = ((int64_t)row * H + h) * kMlaDr;
+    for (int r = threadIdx.x; r < kMlaDr; r += blockDim.x) {
+        const float x = q_bf16 ? bf16_f32(((const uint16_t *)q_rope)[roff + r]) : ((const float *)q_rope)[roff + r];
+        dst[kMlaDc + r] = bf16_rne(x * qscale);
+    }
+}
+
+template <int NQT>
+__global__ __launch_bounds__(256) void mla_decode_kernel(
+    const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
+    const AttRow *__restrict__ rows, const int2 *__restrict__ work,
+    const uint16_t *__restrict__ qlat, int H, int P, int chunk, int mask_mode,
+    float *__restrict__ part_o, float *__restrict__ part_ml) {
+    constexpr int QRP = 16 * NQT;
+    constexpr int CHUNKS = 16 * kMlaRow / 8;  // 16-byte pieces per tile: 1152
+    __shared__ uint16_t tile[2][16 * kPitch];
+    __shared__ fl4 spart[4][NQT][64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int2 wk = work[blockIdx.x];
+    const AttRow R = rows[wk.x];
+    const int QR = H * R.nq;
+    const int t_begin = wk.y * chunk;
+    const int t_end = min(R.len, t_begin + chunk);
+
+    // B operand of the score product for this wave's 9 k-steps.
+    sh4 qb[NQT][9];
+    int klim[NQT];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const int qr = nt * 16 + col;
+        klim[nt] = R.len - 1;
+        if (qr < QR) {
+            const int qi = qr / H;
+            const int h = qr - qi * H;
+            klim[nt] = mla_key_limit(mask_mode, R.len, R.nq, qi);
+            const uint16_t *qp = qlat + ((int64_t)(R.qrow + qi) * H + h) * kMlaRow + grp * 4;
+#pragma unroll
+            for (int kk = 0; kk < 9; kk++)
+                qb[nt][kk] = __builtin_bit_cast(sh4, *(const u32x2 *)(qp + (wave * 9 + kk) * 16));
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 9; kk++) qb[nt][kk] = sh4{0, 0, 0, 0};
+        }
+    }
+
+    float m_run[NQT], l_part[NQT];
+    fl4 acc[NQT][8];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        m_run[nt] = -INFINITY;
+        l_part[nt] = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 8; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Rows past the live length are staged as zeros.
+    u32x4 pre[5];
+    auto load_tile = [&](int t0) {
+        const int page = table[R.tab + t0 / P];
+        const uint16_t *src = pool + ((int64_t)page * P + (t0 % P)) * kMlaRow;
+#pragma unroll
+        for (int k = 0; k < 5; k++) {
+            const int c = tid + 256 * k;
+            pre[k] = u32x4{0, 0, 0, 0};
+            if (c < CHUNKS && t0 + c / 72 < R.len) pre[k] = *(const u32x4 *)(src + (int64_t)c * 8);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < 5; k++) {
+            const int c = tid + 256 * k;
+            if (c < CHUNKS) {
+                const int r = c / 72, cc = c - r * 72;
+                uint16_t *d = &tile[buf][r * kPitch + cc * 8];
+                *(u32x2 *)d = u32x2{pre[k][0], pre[k][1]};
+                *(u32x2 *)(d + 4) = u32x2{pre[k][2], pre[k][3]};
+            }
+        }
+    };
+
+    int buf = 0;
+    if (t_begin < t_end) {
+        load_tile(t_begin);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
+        const bool has_next = t0 + 16 < t_end;
+        if (has_next) load_tile(t0 + 16);
+        const uint16_t *T = tile[buf];
+        // Partial scores over this wave's quarter of the 576 channels.
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++) {
+            fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < 9; kk++) {
+                const sh4 a = __builtin_bit_cast(sh4, *(const u32x2 *)(T + col * kPitch + (wave * 9 + kk) * 16 + grp * 4));
+                s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, qb[nt][kk], s, 0, 0, 0);
+            }
+            spart[wave][nt][lane] = s;
+        }
+        __syncthreads();
+        sh4 pb[NQT];
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++) {
+            fl4 s = spart[0][nt][lane];
+            s += spart[1][nt][lane];
+            s += spart[2][nt][lane];
+            s += spart[3][nt][lane];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = t0 + grp * 4 + i;
+                s[i] = (t <= klim[nt]) ? s[i] : -INFINITY;
+                mx = fmaxf(mx, s[i]);
+            }
+            mx = mla_max16(mx);
+            const float m_new = fmaxf(m_run[nt], mx);
+            float c, p[4];
+            if (m_new == -INFINITY) {
+                c = 1.f;
+                p[0] = p[1] = p[2] = p[3] = 0.f;
+            } else {
+                c = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
+#pragma unroll
+                for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
+            }
+            l_part[nt] = l_part[nt] * c + ((p[0] + p[1]) + (p[2] + p[3]));
+            m_run[nt] = m_new;
+#pragma unroll
+            for (int mt = 0; mt < 8; mt++) acc[nt][mt] *= c;
+            u32x2 pw;
+            pw[0] = (uint32_t)bf16_rne(p[0]) | ((uint32_t)bf16_rne(p[1]) << 16);
+            pw[1] = (uint32_t)bf16_rne(p[2]) | ((uint32_t)bf16_rne(p[3]) << 16);
+            pb[nt] = __builtin_bit_cast(sh4, pw);
+        }
+        // O^T += C^T . P^T over this wave's 128 latent channels.
+#pragma unroll
+        for (int mt = 0; mt < 8; mt++) {
+            const int ch = wave * 128 + mt * 16 + col;
+            const uint16_t *tc = T + (grp * 4) * kPitch + ch;
+            u32x2 w;
+            w[0] = (uint32_t)tc[0] | ((uint32_t)tc[kPitch] << 16);
+            w[1] = (uint32_t)tc[2 * kPitch] | ((uint32_t)tc[3 * kPitch] << 16);
+            const sh4 a = __builtin_bit_cast(sh4, w);
+#pragma unroll
+            for (int nt = 0; nt < NQT; nt++)
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[nt], acc[nt][mt], 0, 0, 0);
+        }
+        if (has_next) store_tile(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+    }
+
+    const int pidx = R.part + wk.y;
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const int qr = nt * 16 + col;
+        const float lt = mla_sum16(l_part[nt]);
+        float *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * 128;
+#pragma unroll
+        for (int mt = 0; mt < 8; mt++) *(fl4 *)(po + mt * 16 + grp * 4) = acc[nt][mt];
+        if (wave == 0 && grp == 0) {
+            float *pm = part_ml + ((int64_t)pidx * QRP + qr) * 2;
+            pm[0] = m_run[nt];
+            pm[1] = lt;
+        }
+    }
+}
+
+// Merge the splits of one (sequence, query, head) into o_lat (LDS) and apply
+// W_UV: out[row][h][d] = sum_c o_lat[c] * W_UV[c][h*D+d].
+__global__ __launch_bounds__(128) void mla_output_kernel(
+    const AttRow *__restrict__ rows, const float *__restrict__ part_o,
+    const float *__restrict__ part_ml, const uint16_t *__restrict__ w_uv, int H, int D,
+    int QRP, void *__restrict__ out, int out_bf16) {
+    const AttRow R = rows[blockIdx.x];
+    const int qi = blockIdx.y / H;
+    const int h = blockIdx.y - qi * H;
+    if (qi >= R.nq) return;
+    const int qr = qi * H + h;
+    __shared__ float olat[kMlaDc];
+    __shared__ float fac[64];
+    __shared__ float invL;
+    if (threadIdx.x == 0) {
+        float M = -INFINITY;
+        for (int s = 0; s < R.nsplit; s++)
+            M = fmaxf(M, part_ml[((int64_t)(R.part + s) * QRP + qr) * 2]);
+        float L = 0.f;
+        for (int s = 0; s < R.nsplit; s++) {
+            const float *pm = part_ml + ((int64_t)(R.part + s) * QRP + qr) * 2;
+            const float f = (pm[0] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
+            if (s < 64) fac[s] = f;
+            L += f * pm[1];
+        }
+        invL = (L > 0.f) ? 1.f / L : 0.f;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < kMlaDc; c += blockDim.x) {
+        float o = 0.f;
+        for (int s = 0; s < R.nsplit; s++) {
+            float f;
+            if (s < 64) {
+                f = fac[s];
+            } else {
+                // Rare: more splits than the factor cache holds.
+                float M = -INFINITY;
+                for (int u = 0; u < R.nsplit; u++)
+                    M = fmaxf(M, part_ml[((int64_t)(R.part + u) * QRP + qr) * 2]);
+                const float m = part_ml[((int64_t)(R.part + s) * QRP + qr) * 2];
+                f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+            }
+            o += f * part_o[((int64_t)(R.part + s) * QRP + qr) * kMlaDc + c];
+        }
+        olat[c] = o * invL;
+    }
+    __syncthreads();
+    const int64_t wpitch = (int64_t)H * D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.f;
+        const uint16_t *w = w_uv + (int64_t)h * D + d;
+        for (int c = 0; c < kMlaDc; c++) acc += olat[c] * bf16_f32(w[(int64_t)c * wpitch]);
+        const int64_t o = ((int64_t)(R.qrow + qi) * H + h) * D + d;
+        if (out_bf16)
+            ((uint16_t *)out)[o] = bf16_rne(acc);
+        else
+            ((float *)out)[o] = acc;
+    }
+}
+
+hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, int n_rows, const int2 *work, int n_work,
+                             const void *q_nope, const void *q_rope, int q_bf16,
+                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
+                             int total_q, int max_nq, int P, int chunk, float qscale,
+                             int mask_mode, int nqt, uint16_t *qlat, float *part_o,
+                             float *part_ml, void *out, int out_bf16, hipEvent_t ev0,
+                             hipEvent_t ev1) {
+    if (n_work <= 0) return hipSuccess;
+    mla_absorb_kernel<<<dim3(total_q, H), 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, hd,
+                                                       qscale, qlat);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev0) (void)hipEventRecord(ev0, s);
+    if (nqt == 1)
+        mla_decode_kernel<1><<<n_work, 256, 0, s>>>(pool, table, rows, work, qlat, H, P, chunk,
+                                                    mask_mode, part_o, part_ml);
+    else if (nqt == 2)
+        mla_decode_kernel<2><<<n_work, 256, 0, s>>>(pool, table, rows, work, qlat, H, P, chunk,
+                                                    mask_mode, part_o, part_ml);
+    else
+        return hipErrorInvalidValue;
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (ev1) (void)hipEventRecord(ev1, s);
+    mla_output_kernel<<<dim3(n_rows, max_nq * H), 128, 0, s>>>(rows, part_o, part_ml, w_uv, H,
+                                                               hd, 16 * nqt, out, out_bf16);
+    return hipGetLastError();
+}
+
+}  // namespace rlx

@@ -1,0 +1,948 @@
+// Host runtime and C ABI of librelux_kv: cache handles, page pools, the
+// page-table state machine (append / rollback / evict / compact), plan
+// staging, and dispatch to the kernels.
+//
+// State ownership: the host keeps the authoritative integer state of every
+// (layer, sequence) -- live length, first live table entry, RoPE position
+// offset, pages in use -- plus a mirror of the page table and the LIFO free
+// stack of each layer.  The device holds the page pools and the page table
+// the kernels read.  Table writes are batched as (index, value) patches,
+// coalesced by index, and applied on the stream before the next kernel that
+// reads the table (fused into append, or a patch kernel).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/relux_kv.h"
+#include "rlx_common.h"
+
+using namespace rlx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int32_t fail(int32_t code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                       \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail(RLX_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_));        \
+    } while (0)
+
+enum Kind { kGQA = 0, kMLA = 1 };
+
+struct SeqState {
+    int32_t len = 0;         // live tokens
+    int32_t first = 0;       // first live entry of the table row
+    int32_t pos_offset = 0;  // absolute position of the first live token
+    int32_t pages = 0;       // live pages
+};
+
+struct LayerState {
+    uint16_t *pool0 = nullptr;  // GQA K row pages / MLA latent rows
+    uint16_t *pool1 = nullptr;  // GQA V dim-major pages
+    std::vector<int32_t> table;       // [max_seqs * max_pages], -1 empty
+    std::vector<int32_t> free_stack;  // back() is the next page handed out
+    std::vector<SeqState> seqs;
+};
+
+struct Slot {
+    void *host = nullptr;
+    void *dev = nullptr;
+    size_t cap = 0;
+    hipEvent_t ev = nullptr;
+    bool pending = false;
+};
+
+constexpr int kSlots = 8;
+
+struct Cache {
+    int kind = kGQA;
+    int layers = 0, kvh = 0, hd = 0, P = 0, pool_pages = 0, max_seqs = 0, max_pages = 0;
+    int dc = 0, dr = 0;
+    int device = 0;
+    std::vector<LayerState> L;
+    int32_t *d_table = nullptr;
+    hipStream_t own = nullptr, stream = nullptr;
+    std::map<int64_t, int32_t> pending;  // flat table index -> value
+    Slot slots[kSlots];
+    int next_slot = 0;
+    void *ws = nullptr;
+    size_t ws_cap = 0;
+    // Attention-kernel timing: event pairs, reused across reports.
+    bool timing = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> tev;
+    size_t tev_used = 0;
+
+    int64_t row_base(int layer, int seq) const {
+        return ((int64_t)layer * max_seqs + seq) * max_pages;
+    }
+    void set_entry(int layer, int seq, int k, int32_t v) {
+        const int64_t idx = row_base(layer, seq) + k;
+        L[layer].table[idx - (int64_t)layer * max_seqs * max_pages] = v;
+        pending[idx] = v;
+    }
+    int32_t entry(int layer, int seq, int k) const {
+        return L[layer].table[(int64_t)seq * max_pages + k];
+    }
+};
+
+// Copy `bytes` of host data into the next staging slot and enqueue its
+// upload; returns the device address the kernels should read.
+int32_t stage(Cache *c, const void *data, size_t bytes, void **dev_out) {
+    Slot &s = c->slots[c->next_slot];
+    c->next_slot = (c->next_slot + 1) % kSlots;
+    if (s.pending) {
+        HIP_TRY(hipEventSynchronize(s.ev));
+        s.pending = false;
+    }
+    if (bytes > s.cap) {
+        size_t cap = std::max<size_t>(bytes, 64 * 1024);
+        cap = (cap + 4095) & ~(size_t)4095;
+        // The device copy of this slot may still be read by queued kernels.
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (s.host) HIP_TRY(hipHostFree(s.host));
+        if (s.dev) HIP_TRY(hipFree(s.dev));
+        s.host = nullptr;
+        s.dev = nullptr;
+        HIP_TRY(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+        HIP_TRY(hipMalloc(&s.dev, cap));
+        s.cap = cap;
+    }
+    if (bytes) {
+        memcpy(s.host, data, bytes);
+        HIP_TRY(hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hipEventRecord(s.ev, c->stream));
+        s.pending = true;
+    }
+    *dev_out = s.dev;
+    return RLX_OK;
+}
+
+// Serialise a list of PODs into one byte blob with 16-byte aligned parts.
+struct Blob {
+    std::vector<char> bytes;
+    template <class T>
+    size_t add(const std::vector<T> &v) {
+        size_t off = (bytes.size() + 15) & ~(size_t)15;
+        bytes.resize(off + v.size() * sizeof(T));
+        if (!v.empty()) memcpy(bytes.data() + off, v.data(), v.size() * sizeof(T));
+        return off;
+    }
+};
+
+std::vector<Patch> take_pending(Cache *c) {
+    std::vector<Patch> p;
+    p.reserve(c->pending.size());
+    for (auto &kv : c->pending) p.push_back(Patch{(int32_t)kv.first, kv.second});
+    c->pending.clear();
+    return p;
+}
+
+// Apply pending table patches now (before a kernel that reads the table).
+int32_t flush_patches(Cache *c) {
+    if (c->pending.empty()) return RLX_OK;
+    std::vector<Patch> p = take_pending(c);
+    Blob b;
+    b.add(p);
+    void *dev;
+    int32_t rc = stage(c, b.bytes.data(), b.bytes.size(), &dev);
+    if (rc) return rc;
+    HIP_TRY(launch_patch(c->stream, c->d_table, (const Patch *)dev, (int)p.size()));
+    return RLX_OK;
+}
+
+int32_t ensure_ws(Cache *c, size_t bytes) {
+    if (bytes <= c->ws_cap) return RLX_OK;
+    size_t cap = std::max(bytes, c->ws_cap * 2);
+    cap = (cap + 65535) & ~(size_t)65535;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (c->ws) HIP_TRY(hipFree(c->ws));
+    c->ws = nullptr;
+    c->ws_cap = 0;
+    HIP_TRY(hipMalloc(&c->ws, cap));
+    c->ws_cap = cap;
+    return RLX_OK;
+}
+
+Cache *as_cache(void *h) { return static_cast<Cache *>(h); }
+
+// Next event pair bracketing an attention kernel, or nulls when timing is off.
+int32_t timing_events(Cache *c, hipEvent_t *e0, hipEvent_t *e1) {
+    *e0 = *e1 = nullptr;
+    if (!c->timing) return RLX_OK;
+    if (c->tev_used == c->tev.size()) {
+        hipEvent_t a, b;
+        HIP_TRY(hipEventCreate(&a));
+        HIP_TRY(hipEventCreate(&b));
+        c->tev.emplace_back(a, b);
+    }
+    *e0 = c->tev[c->tev_used].first;
+    *e1 = c->tev[c->tev_used].second;
+    c->tev_used++;
+    return RLX_OK;
+}
+
+int32_t check_layer(Cache *c, int layer, bool allow_all) {
+    if (allow_all && layer == -1) return RLX_OK;
+    if (layer < 0 || layer >= c->layers)
+        return fail(RLX_ERR_LAYER, "layerIdx=%d out of range [0, %d)", layer, c->layers);
+    return RLX_OK;
+}
+
+int32_t check_seqs(Cache *c, int n_seqs, const int32_t *seq_ids) {
+    if (n_seqs < 0 || (n_seqs > 0 && !seq_ids)) return fail(RLX_ERR_INVALID, "bad sequence list");
+    std::vector<char> seen(c->max_seqs, 0);
+    for (int i = 0; i < n_seqs; i++) {
+        const int s = seq_ids[i];
+        if (s < 0 || s >= c->max_seqs)
+            return fail(RLX_ERR_INVALID, "seq id %d out of range [0, %d)", s, c->max_seqs);
+        if (seen[s]) return fail(RLX_ERR_INVALID, "seq id %d listed twice in one call", s);
+        seen[s] = 1;
+    }
+    return RLX_OK;
+}
+
+void reset_layer_state(Cache *c, LayerState &ls) {
+    ls.table.assign((size_t)c->max_seqs * c->max_pages, -1);
+    ls.free_stack.resize(c->pool_pages);
+    // Pages are handed out 0, 1, 2, ... from a fresh pool.
+    for (int i = 0; i < c->pool_pages; i++) ls.free_stack[i] = c->pool_pages - 1 - i;
+    ls.seqs.assign(c->max_seqs, SeqState{});
+}
+
+int32_t create_common(Cache *c) {
+    HIP_TRY(hipGetDevice(&c->device));
+    HIP_TRY(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking));
+    c->stream = c->own;
+    for (auto &s : c->slots) HIP_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
+    const int64_t tab_n = (int64_t)c->layers * c->max_seqs * c->max_pages;
+    HIP_TRY(hipMalloc(&c->d_table, tab_n * sizeof(int32_t)));
+    HIP_TRY(launch_fill_i32(c->stream, c->d_table, -1, tab_n));
+    c->L.resize(c->layers);
+    for (auto &ls : c->L) reset_layer_state(c, ls);
+    size_t page_bytes = (c->kind == kGQA) ? (size_t)c->kvh * c->P * c->hd * 2 : (size_t)c->P * kMlaRow * 2;
+    for (auto &ls : c->L) {
+        HIP_TRY(hipMalloc(&ls.pool0, page_bytes * c->pool_pages));
+        // Zeroed so that never-written slots hold finite values.
+        HIP_TRY(hipMemsetAsync(ls.pool0, 0, page_bytes * c->pool_pages, c->stream));
+        if (c->kind == kGQA) {
+            HIP_TRY(hipMalloc(&ls.pool1, page_bytes * c->pool_pages));
+            HIP_TRY(hipMemsetAsync(ls.pool1, 0, page_bytes * c->pool_pages, c->stream));
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
+void destroy_cache(Cache *c) {
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->own) (void)hipStreamSynchronize(c->own);
+    for (auto &ls : c->L) {
+        if (ls.pool0) (void)hipFree(ls.pool0);
+        if (ls.pool1) (void)hipFree(ls.pool1);
+    }
+    if (c->d_table) (void)hipFree(c->d_table);
+    if (c->ws) (void)hipFree(c->ws);
+    for (auto &p : c->tev) {
+        (void)hipEventDestroy(p.first);
+        (void)hipEventDestroy(p.second);
+    }
+    for (auto &s : c->slots) {
+        if (s.host) (void)hipHostFree(s.host);
+        if (s.dev) (void)hipFree(s.dev);
+        if (s.ev) (void)hipEventDestroy(s.ev);
+    }
+    if (c->own) (void)hipStreamDestroy(c->own);
+    delete c;
+}
+
+// Plan the page allocations of one append call on one layer.  Validates
+// everything first so that a failing call changes no state.
+int32_t plan_append(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_tok,
+                    std::vector<AppendTok> &toks) {
+    LayerState &ls = c->L[layer];
+    int64_t need_pages = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        if (!n_tok || n_tok[i] < 0) return fail(RLX_ERR_INVALID, "negative token count");
+        const SeqState &s = ls.seqs[seq_ids[i]];
+        const int64_t new_len = (int64_t)s.len + n_tok[i];
+        const int64_t pages_after = (new_len + c->P - 1) / c->P;
+        if (s.first + pages_after > c->max_pages)
+            return fail(RLX_ERR_OVERFLOW,
+                        "Append: layer %d overflow: total=%d + newLen=%d > capacity=%d", layer,
+                        s.len, n_tok[i], (c->max_pages - s.first) * c->P);
+        need_pages += pages_after - s.pages;
+    }
+    if (need_pages > (int64_t)ls.free_stack.size())
+        return fail(RLX_ERR_POOL, "page pool exhausted: layer %d needs %lld pages, %zu free", layer,
+                    (long long)need_pages, ls.free_stack.size());
+    int32_t row0 = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        const int seq = seq_ids[i];
+        SeqState &s = ls.seqs[seq];
+        for (int j = 0; j < n_tok[i]; j++) {
+            const int pos = s.len + j;
+            const int k = s.first + pos / c->P;
+            if (pos % c->P == 0) {
+                const int32_t page = ls.free_stack.back();
+                ls.free_stack.pop_back();
+                c->set_entry(layer, seq, k, page);
+                s.pages++;
+            }
+            toks.push_back(AppendTok{c->entry(layer, seq, k), pos % c->P, row0, n_tok[i]});
+        }
+        s.len += n_tok[i];
+        row0 += n_tok[i];
+    }
+    return RLX_OK;
+}
+
+// Choose the context split (multiple of 64 tokens) so that the launch has
+// enough work-groups for 256 CUs without drowning in partials.
+int choose_chunk(int64_t total_tokens, int units_per_token_group, int max_len) {
+    int64_t target_groups = 2048;
+    int64_t chunk = (total_tokens * units_per_token_group) / target_groups;
+    chunk = std::max<int64_t>(chunk, 256);
+    chunk = std::min<int64_t>(chunk, 4096);
+    chunk = (chunk + 63) / 64 * 64;
+    if (chunk > max_len) chunk = ((max_len + 63) / 64) * 64;
+    if (chunk < 64) chunk = 64;
+    return (int)chunk;
+}
+
+int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
+                   int chunk, std::vector<AttRow> &rows, std::vector<int2> &work,
+                   int *total_q, int *max_nq, int *total_parts) {
+    LayerState &ls = c->L[layer];
+    int qrow = 0, part = 0, mx = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        const SeqState &s = ls.seqs[seq_ids[i]];
+        const int nq = n_q ? n_q[i] : 1;
+        if (s.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
+        if (nq < 1 || nq > s.len)
+            return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, s.len);
+        AttRow r;
+        r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
+        r.len = s.len;
+        r.nq = nq;
+        r.qrow = qrow;
+        r.nsplit = chunk > 0 ? (s.len + chunk - 1) / chunk : 1;
+        r.part = part;
+        for (int sp = 0; sp < r.nsplit; sp++) work.push_back(int2{i, sp});
+        rows.push_back(r);
+        qrow += nq;
+        part += r.nsplit;
+        mx = std::max(mx, nq);
+    }
+    *total_q = qrow;
+    *max_nq = mx;
+    *total_parts = part;
+    return RLX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t rlx_init(int32_t device) {
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n));
+    if (device < 0 || device >= n) return fail(RLX_ERR_INVALID, "device %d of %d", device, n);
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "device %d is %s; librelux_kv is built for gfx950", device,
+                    prop.gcnArchName);
+    return RLX_OK;
+}
+
+int32_t rlx_last_error(char *buf, int64_t len) {
+    if (!buf || len <= 0) return RLX_ERR_INVALID;
+    snprintf(buf, (size_t)len, "%s", g_err.c_str());
+    return RLX_OK;
+}
+
+int32_t rlx_version(char *buf, int64_t len) {
+    if (!buf || len <= 0) return RLX_ERR_INVALID;
+    snprintf(buf, (size_t)len, "librelux_kv 0.1 gfx950");
+    return RLX_OK;
+}
+
+int32_t rlx_dev_alloc(int64_t bytes, void **out) {
+    if (!out || bytes < 0) return fail(RLX_ERR_INVALID, "bad alloc request");
+    *out = nullptr;
+    if (bytes == 0) return RLX_OK;
+    HIP_TRY(hipMalloc(out, (size_t)bytes));
+    return RLX_OK;
+}
+
+int32_t rlx_dev_free(void *ptr) {
+    if (ptr) HIP_TRY(hipFree(ptr));
+    return RLX_OK;
+}
+
+int32_t rlx_h2d(void *dst, const void *src, int64_t bytes) {
+    if (bytes > 0) HIP_TRY(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyHostToDevice));
+    return RLX_OK;
+}
+
+int32_t rlx_d2h(void *dst, const void *src, int64_t bytes) {
+    if (bytes > 0) HIP_TRY(hipMemcpy(dst, src, (size_t)bytes, hipMemcpyDeviceToHost));
+    return RLX_OK;
+}
+
+int32_t rlx_device_sync(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    return RLX_OK;
+}
+
+int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t page_tokens,
+                      int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq,
+                      void **out) {
+    if (!out) return fail(RLX_ERR_INVALID, "null out");
+    *out = nullptr;
+    if (layers <= 0) return fail(RLX_ERR_INVALID, "NewKVCacheSized: numLayers=%d, must be > 0", layers);
+    if (kv_heads <= 0 || pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
+        return fail(RLX_ERR_INVALID, "kv_heads, pool_pages, max_seqs, max_pages must be > 0");
+    if (head_dim != 64 && head_dim != 128)
+        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: 64, 128)", head_dim);
+    if (page_tokens <= 0 || page_tokens % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
+    Cache *c = new Cache;
+    c->kind = kGQA;
+    c->layers = layers;
+    c->kvh = kv_heads;
+    c->hd = head_dim;
+    c->P = page_tokens;
+    c->pool_pages = pool_pages;
+    c->max_seqs = max_seqs;
+    c->max_pages = max_pages_per_seq;
+    int32_t rc = create_common(c);
+    if (rc) {
+        destroy_cache(c);
+        return rc;
+    }
+    *out = c;
+    return RLX_OK;
+}
+
+int32_t rlx_mla_create(int32_t layers, int32_t d_c, int32_t d_r, int32_t page_tokens,
+                       int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq,
+                       void **out) {
+    if (!out) return fail(RLX_ERR_INVALID, "null out");
+    *out = nullptr;
+    if (layers <= 0) return fail(RLX_ERR_INVALID, "NewMLACache: numLayers=%d, must be > 0", layers);
+    if (pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
+        return fail(RLX_ERR_INVALID, "pool_pages, max_seqs, max_pages must be > 0");
+    if (d_c != kMlaDc || d_r != kMlaDr)
+        return fail(RLX_ERR_UNSUPPORTED, "MLA d_c=%d d_r=%d (supported: 512, 64)", d_c, d_r);
+    if (page_tokens <= 0 || page_tokens % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
+    Cache *c = new Cache;
+    c->kind = kMLA;
+    c->layers = layers;
+    c->dc = d_c;
+    c->dr = d_r;
+    c->P = page_tokens;
+    c->pool_pages = pool_pages;
+    c->max_seqs = max_seqs;
+    c->max_pages = max_pages_per_seq;
+    int32_t rc = create_common(c);
+    if (rc) {
+        destroy_cache(c);
+        return rc;
+    }
+    *out = c;
+    return RLX_OK;
+}
+
+int32_t rlx_cache_destroy(void *h) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    destroy_cache(as_cache(h));
+    return RLX_OK;
+}
+
+int32_t rlx_cache_reset(void *h) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    for (auto &ls : c->L) reset_layer_state(c, ls);
+    c->pending.clear();
+    HIP_TRY(launch_fill_i32(c->stream, c->d_table, -1, (int64_t)c->layers * c->max_seqs * c->max_pages));
+    return RLX_OK;
+}
+
+int32_t rlx_cache_sync(void *h) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    HIP_TRY(hipStreamSynchronize(as_cache(h)->stream));
+    return RLX_OK;
+}
+
+int32_t rlx_cache_set_stream(void *h, void *stream) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->stream = stream ? (hipStream_t)stream : c->own;
+    return RLX_OK;
+}
+
+int32_t rlx_cache_timing(void *h, int32_t enable) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    c->timing = enable != 0;
+    c->tev_used = 0;
+    return RLX_OK;
+}
+
+int32_t rlx_cache_kernel_time(void *h, float *total_ms, int32_t *count) {
+    if (!h || !total_ms || !count) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    double sum = 0.0;
+    for (size_t i = 0; i < c->tev_used; i++) {
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->tev[i].first, c->tev[i].second));
+        sum += ms;
+    }
+    *total_ms = (float)sum;
+    *count = (int32_t)c->tev_used;
+    c->tev_used = 0;
+    return RLX_OK;
+}
+
+int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                      const int32_t *n_tok, const void *k_src, const void *v_src,
+                      int32_t src_dtype, int32_t src_layout) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_kv_append on an MLA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
+    if (src_layout != RLX_LAYOUT_HSD && src_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "src_layout");
+    std::vector<AppendTok> toks;
+    if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
+    if (!toks.empty() && (!k_src || !v_src)) return fail(RLX_ERR_INVALID, "null K/V source");
+    std::vector<Patch> patches = take_pending(c);
+    Blob b;
+    size_t o_p = b.add(patches), o_t = b.add(toks);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    LayerState &ls = c->L[layer];
+    HIP_TRY(launch_kv_append(c->stream, ls.pool0, ls.pool1, c->d_table,
+                             (const Patch *)((char *)dev + o_p), (int)patches.size(),
+                             (const AppendTok *)((char *)dev + o_t), (int)toks.size(), k_src,
+                             v_src, src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->P));
+    return RLX_OK;
+}
+
+int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_tok, const void *c_src, const void *kr_src,
+                       int32_t src_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_append on a GQA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
+    std::vector<AppendTok> toks;
+    if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
+    if (!toks.empty() && (!c_src || !kr_src)) return fail(RLX_ERR_INVALID, "null latent source");
+    std::vector<Patch> patches = take_pending(c);
+    Blob b;
+    size_t o_p = b.add(patches), o_t = b.add(toks);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    HIP_TRY(launch_mla_append(c->stream, c->L[layer].pool0, c->d_table,
+                              (const Patch *)((char *)dev + o_p), (int)patches.size(),
+                              (const AppendTok *)((char *)dev + o_t), (int)toks.size(), c_src,
+                              kr_src, src_dtype == RLX_BF16, c->P));
+    return RLX_OK;
+}
+
+static int32_t gather_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids,
+                           std::vector<AttRow> &rows, int *max_len) {
+    LayerState &ls = c->L[layer];
+    int off = 0, mx = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        const SeqState &s = ls.seqs[seq_ids[i]];
+        AttRow r{};
+        r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
+        r.len = s.len;
+        r.qrow = off;  // token offset of this sequence in the dense output
+        rows.push_back(r);
+        off += s.len;
+        mx = std::max(mx, s.len);
+    }
+    *max_len = mx;
+    return RLX_OK;
+}
+
+int32_t rlx_kv_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                      void *k_out, void *v_out) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_kv_gather on an MLA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if ((rc = flush_patches(c))) return rc;
+    std::vector<AttRow> rows;
+    int max_len = 0;
+    gather_rows(c, layer, n_seqs, seq_ids, rows, &max_len);
+    if (max_len == 0) return RLX_OK;
+    if (!k_out || !v_out) return fail(RLX_ERR_INVALID, "null gather output");
+    Blob b;
+    size_t o_r = b.add(rows);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    LayerState &ls = c->L[layer];
+    HIP_TRY(launch_kv_gather(c->stream, ls.pool0, ls.pool1, c->d_table,
+                             (const AttRow *)((char *)dev + o_r), n_seqs, max_len,
+                             (uint16_t *)k_out, (uint16_t *)v_out, c->kvh, c->hd, c->P));
+    return RLX_OK;
+}
+
+int32_t rlx_mla_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       void *c_out, void *kr_out) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_gather on a GQA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if ((rc = flush_patches(c))) return rc;
+    std::vector<AttRow> rows;
+    int max_len = 0;
+    gather_rows(c, layer, n_seqs, seq_ids, rows, &max_len);
+    if (max_len == 0) return RLX_OK;
+    if (!c_out || !kr_out) return fail(RLX_ERR_INVALID, "null gather output");
+    Blob b;
+    size_t o_r = b.add(rows);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    HIP_TRY(launch_mla_gather(c->stream, c->L[layer].pool0, c->d_table,
+                              (const AttRow *)((char *)dev + o_r), n_seqs, max_len,
+                              (uint16_t *)c_out, (uint16_t *)kr_out, c->P));
+    return RLX_OK;
+}
+
+int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                       int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_attend on an MLA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (num_heads <= 0 || num_heads % c->kvh != 0)
+        return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
+    if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
+    if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
+    if (qo_layout != RLX_LAYOUT_HSD && qo_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "qo_layout");
+    if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    const int G = num_heads / c->kvh;
+    LayerState &ls = c->L[layer];
+    int64_t total_tok = 0;
+    int max_len = 0, max_nq = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        total_tok += ls.seqs[seq_ids[i]].len;
+        max_len = std::max(max_len, ls.seqs[seq_ids[i]].len);
+        max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    }
+    const int max_qr = G * max_nq;
+    if (max_qr > 32)
+        return fail(RLX_ERR_UNSUPPORTED, "%d query rows per kv head (decode kernel handles <= 32)", max_qr);
+    const int nqt = max_qr > 16 ? 2 : 1;
+    const int chunk = choose_chunk(total_tok, c->kvh, std::max(max_len, 1));
+    std::vector<AttRow> rows;
+    std::vector<int2> work;
+    int total_q = 0, mnq = 0, parts = 0;
+    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts)))
+        return rc;
+    if ((rc = flush_patches(c))) return rc;
+    const int QRP = 16 * nqt;
+    const size_t po_bytes = (size_t)parts * c->kvh * QRP * c->hd * sizeof(float);
+    const size_t pm_bytes = (size_t)parts * c->kvh * QRP * 2 * sizeof(float);
+    if ((rc = ensure_ws(c, po_bytes + pm_bytes))) return rc;
+    Blob b;
+    size_t o_r = b.add(rows), o_w = b.add(work);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+    const float qscale = scale * 1.4426950408889634f;
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1))) return rc;
+    HIP_TRY(launch_gqa_decode(c->stream, ls.pool0, ls.pool1, c->d_table,
+                              (const AttRow *)((char *)dev + o_r), n_seqs,
+                              (const int2 *)((char *)dev + o_w), (int)work.size(), q,
+                              q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
+                              chunk, qscale, mask_mode, nqt, (float *)c->ws,
+                              (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
+                              e0, e1));
+    return RLX_OK;
+}
+
+int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
+                       const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
+                       float scale, int32_t mask_mode, void *out, int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_attend on a GQA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
+        return fail(RLX_ERR_INVALID, "num_heads=%d head_dim=%d", num_heads, head_dim);
+    if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
+    if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
+    if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
+    if (n_seqs == 0) return RLX_OK;
+    if (!q_nope || !q_rope || !w_uk || !w_uv || !out) return fail(RLX_ERR_INVALID, "null operand");
+    LayerState &ls = c->L[layer];
+    int64_t total_tok = 0;
+    int max_len = 0, max_nq = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        total_tok += ls.seqs[seq_ids[i]].len;
+        max_len = std::max(max_len, ls.seqs[seq_ids[i]].len);
+        max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    }
+    const int max_qr = num_heads * max_nq;
+    if (max_qr > 32)
+        return fail(RLX_ERR_UNSUPPORTED, "%d query rows (heads x queries) per sequence (decode kernel handles <= 32)", max_qr);
+    const int nqt = max_qr > 16 ? 2 : 1;
+    // One work-group covers all heads, so weigh a token 16 heads' worth less.
+    const int chunk = choose_chunk(total_tok, 1, std::max(max_len, 1));
+    std::vector<AttRow> rows;
+    std::vector<int2> work;
+    int total_q = 0, mnq = 0, parts = 0;
+    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts)))
+        return rc;
+    if ((rc = flush_patches(c))) return rc;
+    const int QRP = 16 * nqt;
+    const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
+    const size_t po_bytes = (size_t)parts * QRP * kMlaDc * sizeof(float);
+    const size_t pm_bytes = (size_t)parts * QRP * 2 * sizeof(float);
+    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes))) return rc;
+    Blob b;
+    size_t o_r = b.add(rows), o_w = b.add(work);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
+    const float qscale = scale * 1.4426950408889634f;
+    char *ws = (char *)c->ws;
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1))) return rc;
+    HIP_TRY(launch_mla_decode(c->stream, ls.pool0, c->d_table, (const AttRow *)((char *)dev + o_r),
+                              n_seqs, (const int2 *)((char *)dev + o_w), (int)work.size(), q_nope,
+                              q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
+                              (const uint16_t *)w_uv, num_heads, head_dim, total_q, max_nq, c->P,
+                              chunk, qscale, mask_mode, nqt, (uint16_t *)ws,
+                              (float *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes), out,
+                              out_dtype == RLX_BF16, e0, e1));
+    return RLX_OK;
+}
+
+static int32_t layer_range(Cache *c, int layer, int *lo, int *hi) {
+    int32_t rc = check_layer(c, layer, true);
+    if (rc) return rc;
+    *lo = layer < 0 ? 0 : layer;
+    *hi = layer < 0 ? c->layers : layer + 1;
+    return RLX_OK;
+}
+
+int32_t rlx_rollback(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                     const int32_t *n_tokens) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (n_seqs > 0 && !n_tokens) return fail(RLX_ERR_INVALID, "null token counts");
+    for (int i = 0; i < n_seqs; i++) {
+        if (n_tokens[i] < 0) return fail(RLX_ERR_INVALID, "negative rollback");
+        for (int l = lo; l < hi; l++)
+            if (n_tokens[i] > c->L[l].seqs[seq_ids[i]].len)
+                return fail(RLX_ERR_STATE, "rollback of %d tokens of seq %d on layer %d holding %d",
+                            n_tokens[i], seq_ids[i], l, c->L[l].seqs[seq_ids[i]].len);
+    }
+    for (int i = 0; i < n_seqs; i++) {
+        const int seq = seq_ids[i];
+        for (int l = lo; l < hi; l++) {
+            LayerState &ls = c->L[l];
+            SeqState &s = ls.seqs[seq];
+            s.len -= n_tokens[i];
+            const int keep = (s.len + c->P - 1) / c->P;
+            for (int k = s.pages - 1; k >= keep; k--) {
+                ls.free_stack.push_back(c->entry(l, seq, s.first + k));
+                c->set_entry(l, seq, s.first + k, -1);
+            }
+            s.pages = keep;
+        }
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_evict(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                  const int32_t *n_pages) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (n_seqs > 0 && !n_pages) return fail(RLX_ERR_INVALID, "null page counts");
+    for (int i = 0; i < n_seqs; i++) {
+        if (n_pages[i] < 0) return fail(RLX_ERR_INVALID, "negative eviction");
+        for (int l = lo; l < hi; l++)
+            if (n_pages[i] > c->L[l].seqs[seq_ids[i]].len / c->P)
+                return fail(RLX_ERR_STATE, "evicting %d pages of seq %d on layer %d with %d full pages",
+                            n_pages[i], seq_ids[i], l, c->L[l].seqs[seq_ids[i]].len / c->P);
+    }
+    for (int i = 0; i < n_seqs; i++) {
+        const int seq = seq_ids[i];
+        for (int l = lo; l < hi; l++) {
+            LayerState &ls = c->L[l];
+            SeqState &s = ls.seqs[seq];
+            for (int k = 0; k < n_pages[i]; k++) {
+                ls.free_stack.push_back(c->entry(l, seq, s.first + k));
+                c->set_entry(l, seq, s.first + k, -1);
+            }
+            s.first += n_pages[i];
+            s.pages -= n_pages[i];
+            s.len -= n_pages[i] * c->P;
+            s.pos_offset += n_pages[i] * c->P;
+        }
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_compact(void *h, int32_t layer) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    for (int l = lo; l < hi; l++) {
+        LayerState &ls = c->L[l];
+        for (int seq = 0; seq < c->max_seqs; seq++) {
+            SeqState &s = ls.seqs[seq];
+            if (s.first == 0) continue;
+            for (int k = 0; k < s.pages; k++) c->set_entry(l, seq, k, c->entry(l, seq, s.first + k));
+            for (int k = s.pages; k < s.first + s.pages; k++) c->set_entry(l, seq, k, -1);
+            s.first = 0;
+        }
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_seq_release(void *h, int32_t layer, int32_t seq) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    if (seq < 0 || seq >= c->max_seqs) return fail(RLX_ERR_INVALID, "seq id %d", seq);
+    for (int l = lo; l < hi; l++) {
+        LayerState &ls = c->L[l];
+        SeqState &s = ls.seqs[seq];
+        for (int k = s.pages - 1; k >= 0; k--) {
+            ls.free_stack.push_back(c->entry(l, seq, s.first + k));
+            c->set_entry(l, seq, s.first + k, -1);
+        }
+        s = SeqState{};
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_seq_len(void *h, int32_t layer, int32_t seq, int32_t *len_out) {
+    if (!h || !len_out) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    // TotalLen returns 0 for an out-of-range layer (kvcache.go:383-388).
+    if (layer < 0 || layer >= c->layers || seq < 0 || seq >= c->max_seqs) {
+        *len_out = 0;
+        return RLX_OK;
+    }
+    *len_out = c->L[layer].seqs[seq].len;
+    return RLX_OK;
+}
+
+int32_t rlx_seq_state(void *h, int32_t layer, int32_t seq, int32_t *st) {
+    if (!h || !st) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if (seq < 0 || seq >= c->max_seqs) return fail(RLX_ERR_INVALID, "seq id %d", seq);
+    const SeqState &s = c->L[layer].seqs[seq];
+    st[0] = s.len;
+    st[1] = s.first;
+    st[2] = s.pos_offset;
+    st[3] = s.pages;
+    return RLX_OK;
+}
+
+int32_t rlx_page_table(void *h, int32_t layer, int32_t seq, int32_t *row_out) {
+    if (!h || !row_out) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if (seq < 0 || seq >= c->max_seqs) return fail(RLX_ERR_INVALID, "seq id %d", seq);
+    if ((rc = flush_patches(c))) return rc;
+    HIP_TRY(hipMemcpyAsync(row_out, c->d_table + c->row_base(layer, seq),
+                           (size_t)c->max_pages * sizeof(int32_t), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
+int32_t rlx_free_list(void *h, int32_t layer, int32_t *out, int32_t cap, int32_t *n_out) {
+    if (!h || !n_out) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    const auto &fs = c->L[layer].free_stack;
+    *n_out = (int32_t)fs.size();
+    if (out) {
+        const int n = std::min<int>(cap, (int)fs.size());
+        for (int i = 0; i < n; i++) out[i] = fs[i];
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_pool_ptr(void *h, int32_t layer, void **k_pool, void **v_pool) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if (k_pool) *k_pool = c->L[layer].pool0;
+    if (v_pool) *v_pool = c->L[layer].pool1;
+    return RLX_OK;
+}
+
+}  // extern "C"

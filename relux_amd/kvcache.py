@@ -1,0 +1,320 @@
+"""Host-side mirror of relux's cache interface over librelux_kv.
+
+`KVCache` and `MLACache` keep the method names, argument meaning and panic
+sites of the reference's Go types (internal/transformer/kvcache.go,
+mla_cache.go) and add the paged operations the reference lacks (Rollback,
+Evict, Compact, Release) plus the fused attention entry points that replace
+the loops of MHA.forwardCached / MLA.forwardCached.  Tensors are torch tensors
+on the GPU; the library runs on torch's current stream, so ordering against
+torch work is implicit.  Every call goes to the HIP library: there is no CPU
+path here.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import check, i32_array
+
+_MASKS = {"causal": _lib.RLX_MASK_CAUSAL, "ref": _lib.RLX_MASK_REF, "none": _lib.RLX_MASK_NONE}
+_LAYOUTS = {"HSD": _lib.RLX_LAYOUT_HSD, "SHD": _lib.RLX_LAYOUT_SHD}
+
+
+def _dtype_code(t):
+    if t.dtype == torch.float32:
+        return _lib.RLX_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.RLX_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}: use float32 or bfloat16")
+
+
+def _as_lists(seq, n):
+    if isinstance(seq, (list, tuple)):
+        seqs = [int(s) for s in seq]
+        ns = [int(v) for v in n] if isinstance(n, (list, tuple)) else [int(n)] * len(seqs)
+        return seqs, ns
+    return [int(seq)], [int(n)]
+
+
+def _dev(t, what):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{what} must be a GPU torch tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class _PagedCache:
+    def __init__(self, handle, num_layers, page_tokens, max_pages, max_seqs, device):
+        self._h = handle
+        self.num_layers = num_layers
+        self.page_tokens = page_tokens
+        self.max_pages = max_pages
+        self.max_seqs = max_seqs
+        self.device = torch.device("cuda", device)
+        self._lib = _lib.load()
+        self.use_stream(torch.cuda.current_stream(self.device))
+
+    # -- lifetime ---------------------------------------------------------
+    def close(self):
+        if getattr(self, "_h", None):
+            check(self._lib.rlx_cache_destroy(self._h))
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def use_stream(self, stream):
+        """Run this cache's work on `stream` (a torch.cuda.Stream)."""
+        check(self._lib.rlx_cache_set_stream(self._h, ctypes.c_void_p(stream.cuda_stream)))
+
+    def Sync(self):
+        check(self._lib.rlx_cache_sync(self._h))
+
+    def Timing(self, enable=True):
+        """Bracket every later attention kernel with HIP events."""
+        check(self._lib.rlx_cache_timing(self._h, 1 if enable else 0))
+
+    def KernelTime(self):
+        """(total ms, launches) of the attention kernels timed since the last
+        report; synchronises."""
+        ms = ctypes.c_float()
+        n = ctypes.c_int32()
+        check(self._lib.rlx_cache_kernel_time(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+    # -- reference method set ---------------------------------------------
+    def Reset(self):
+        """KVCache.Reset / MLACache.Reset (kvcache.go:174-202): drop every
+        sequence, return every page."""
+        check(self._lib.rlx_cache_reset(self._h))
+
+    def TotalLen(self, layer_idx, seq=0):
+        """Live tokens of `seq` on `layer_idx` (kvcache.go:383-388); 0 for an
+        out-of-range layer, as the reference returns."""
+        n = ctypes.c_int32()
+        check(self._lib.rlx_seq_len(self._h, layer_idx, seq, ctypes.byref(n)))
+        return n.value
+
+    def DType(self):
+        return "bf16"
+
+    # -- paged operations (no reference counterpart) ------------------------
+    def Rollback(self, seq, n_tokens, layer=-1):
+        """Drop the last n_tokens of `seq` (int) or, with lists, of every
+        listed sequence in one call."""
+        seqs, ns = _as_lists(seq, n_tokens)
+        check(self._lib.rlx_rollback(self._h, layer, len(seqs), i32_array(seqs), i32_array(ns)))
+
+    def Evict(self, seq, n_pages, layer=-1):
+        """Drop the oldest n_pages full pages of `seq` (int or list)."""
+        seqs, ns = _as_lists(seq, n_pages)
+        check(self._lib.rlx_evict(self._h, layer, len(seqs), i32_array(seqs), i32_array(ns)))
+
+    def Compact(self, layer=-1):
+        check(self._lib.rlx_compact(self._h, layer))
+
+    def Release(self, seq, layer=-1):
+        check(self._lib.rlx_seq_release(self._h, layer, seq))
+
+    # -- state dumps ---------------------------------------------------------
+    def SeqState(self, layer, seq):
+        st = (ctypes.c_int32 * 4)()
+        check(self._lib.rlx_seq_state(self._h, layer, seq, st))
+        return {"len": st[0], "first": st[1], "pos_offset": st[2], "pages": st[3]}
+
+    def PageTable(self, layer, seq):
+        row = (ctypes.c_int32 * self.max_pages)()
+        check(self._lib.rlx_page_table(self._h, layer, seq, row))
+        return list(row)
+
+    def FreeList(self, layer):
+        n = ctypes.c_int32()
+        check(self._lib.rlx_free_list(self._h, layer, None, 0, ctypes.byref(n)))
+        buf = (ctypes.c_int32 * max(1, n.value))()
+        check(self._lib.rlx_free_list(self._h, layer, buf, n.value, ctypes.byref(n)))
+        return list(buf)[: n.value]
+
+    def _lens(self, layer_idx, seq_ids):
+        return [self.TotalLen(layer_idx, s) for s in seq_ids]
+
+
+class KVCache(_PagedCache):
+    """Paged bf16 GQA K/V cache.
+
+    KVCache(num_layers, max_len, num_kv_heads, head_dim) mirrors
+    NewKVCacheSized(numLayers, maxLen, numKVHeads, headDim, BFloat16)
+    (kvcache.go:66-93): every sequence may hold max_len tokens.  Pages of
+    `page_tokens` tokens come from a per-layer pool of `pool_pages` pages
+    (default: enough for max_seqs full sequences).
+    """
+
+    def __init__(self, num_layers, max_len, num_kv_heads, head_dim, page_tokens=16, max_seqs=1,
+                 pool_pages=None, device=0):
+        _lib.init(device)
+        if num_layers <= 0:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID,
+                                  f"NewKVCacheSized: numLayers={num_layers}, must be > 0")
+        if max_len <= 0:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID,
+                                  f"NewKVCacheSized: maxLen={max_len}, must be > 0")
+        max_pages = -(-max_len // page_tokens)
+        if pool_pages is None:
+            pool_pages = max_pages * max_seqs
+        h = ctypes.c_void_p()
+        check(_lib.load().rlx_kv_create(num_layers, num_kv_heads, head_dim, page_tokens, pool_pages,
+                                        max_seqs, max_pages, ctypes.byref(h)))
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.pool_pages = pool_pages
+        super().__init__(h, num_layers, page_tokens, max_pages, max_seqs, device)
+
+    def Append(self, layer_idx, new_k, new_v, seq_ids=(0,), n_tok=None, layout="HSD"):
+        """Append K/V rows (kvcache.go:240-316).  With one sequence and the
+        reference's [1, KVH, n, D] tensors this is KVCache.Append; with
+        several, n_tok[i] rows per sequence in `layout` order."""
+        if new_k.shape != new_v.shape:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID,
+                                  f"KVCache.Append: K and V shape mismatch: {tuple(new_k.shape)} vs {tuple(new_v.shape)}")
+        if new_k.dtype != new_v.dtype:
+            raise TypeError("K and V dtypes differ")
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [new_k.shape[-2] if layout == "HSD" else new_k.shape[-3]]
+        total = sum(n_tok)
+        if new_k.numel() != total * self.num_kv_heads * self.head_dim:
+            raise ValueError(f"K holds {new_k.numel()} elements, expected "
+                             f"{total}x{self.num_kv_heads}x{self.head_dim}")
+        check(self._lib.rlx_kv_append(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                      i32_array(n_tok), _dev(new_k, "K"), _dev(new_v, "V"),
+                                      _dtype_code(new_k), _LAYOUTS[layout]))
+
+    def View(self, layer_idx, seq=0):
+        """Dense bf16 (K, V) of one sequence, each [1, KVH, T, D], gathered
+        through the page table (kvcache.go:363-380).  None, None when empty."""
+        T = self.TotalLen(layer_idx, seq)
+        if not 0 <= layer_idx < self.num_layers:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_LAYER, f"KVCache.View: layerIdx={layer_idx} out of range")
+        if T == 0:
+            return None, None
+        k = torch.empty((1, self.num_kv_heads, T, self.head_dim), dtype=torch.bfloat16, device=self.device)
+        v = torch.empty_like(k)
+        check(self._lib.rlx_kv_gather(self._h, layer_idx, 1, i32_array([seq]), _dev(k, "k"), _dev(v, "v")))
+        return k, v
+
+    def Gather(self, layer_idx, seq_ids, k_out, v_out):
+        """Gather several sequences into caller-owned dense buffers
+        ([KVH][T_i][D] per sequence, concatenated)."""
+        check(self._lib.rlx_kv_gather(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                      _dev(k_out, "k_out"), _dev(v_out, "v_out")))
+
+    def Attend(self, layer_idx, q, num_heads, seq_ids=(0,), n_q=None, layout="SHD", scale=None,
+               mask="causal", out=None, out_dtype=torch.float32):
+        """Attention of n_q[i] query rows per sequence over its cached tokens
+        (mha.go:291-348).  q: rows x num_heads x head_dim in `layout`."""
+        seq_ids = list(seq_ids)
+        if n_q is None:
+            n_q = [1] * len(seq_ids)
+        rows = sum(n_q)
+        if q.numel() != rows * num_heads * self.head_dim:
+            raise ValueError("q size does not match sum(n_q) x num_heads x head_dim")
+        if out is None:
+            out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+        check(self._lib.rlx_gqa_attend(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                       i32_array(n_q), num_heads, _dev(q, "q"), _dtype_code(q),
+                                       _LAYOUTS[layout], float(scale or 0.0), _MASKS[mask],
+                                       _dev(out, "out"), _dtype_code(out)))
+        return out
+
+
+class MLACache(_PagedCache):
+    """Paged bf16 MLA latent cache (c^KV | k^R per token).
+
+    MLACache(num_layers, max_len, d_c, d_r) mirrors NewMLACache(numLayers,
+    maxLen, dC, dHR) (mla_cache.go:38-59); storage is bf16 instead of f32.
+    """
+
+    def __init__(self, num_layers, max_len, d_c=512, d_r=64, page_tokens=64, max_seqs=1,
+                 pool_pages=None, device=0):
+        _lib.init(device)
+        if num_layers <= 0:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID, f"NewMLACache: numLayers={num_layers}, must be > 0")
+        if max_len <= 0:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID, f"NewMLACache: maxLen={max_len}, must be > 0")
+        max_pages = -(-max_len // page_tokens)
+        if pool_pages is None:
+            pool_pages = max_pages * max_seqs
+        h = ctypes.c_void_p()
+        check(_lib.load().rlx_mla_create(num_layers, d_c, d_r, page_tokens, pool_pages, max_seqs,
+                                         max_pages, ctypes.byref(h)))
+        self.d_c = d_c
+        self.d_r = d_r
+        self.pool_pages = pool_pages
+        super().__init__(h, num_layers, page_tokens, max_pages, max_seqs, device)
+
+    def Append(self, layer_idx, new_c, new_kr, seq_ids=(0,), n_tok=None):
+        """Append latent rows (mla_cache.go:152-182): new_c [.., n, d_c],
+        new_kr [.., n, d_r] (post-RoPE)."""
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [new_c.shape[-2]]
+        total = sum(n_tok)
+        if new_c.numel() != total * self.d_c or new_kr.numel() != total * self.d_r:
+            raise ValueError("latent / rope-key sizes do not match sum(n_tok)")
+        if new_c.dtype != new_kr.dtype:
+            raise TypeError("c and kr dtypes differ")
+        check(self._lib.rlx_mla_append(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                       i32_array(n_tok), _dev(new_c, "c"), _dev(new_kr, "kr"),
+                                       _dtype_code(new_c)))
+
+    def View(self, layer_idx, seq=0):
+        """Dense bf16 (c [1, T, d_c], kr [1, T, d_r]) (mla_cache.go:222-233)."""
+        if not 0 <= layer_idx < self.num_layers:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_LAYER, f"MLACache.View: layerIdx={layer_idx} out of range")
+        T = self.TotalLen(layer_idx, seq)
+        if T == 0:
+            return None, None
+        c = torch.empty((1, T, self.d_c), dtype=torch.bfloat16, device=self.device)
+        kr = torch.empty((1, T, self.d_r), dtype=torch.bfloat16, device=self.device)
+        check(self._lib.rlx_mla_gather(self._h, layer_idx, 1, i32_array([seq]), _dev(c, "c"), _dev(kr, "kr")))
+        return c, kr
+
+    def Attend(self, layer_idx, q_nope, q_rope, w_uk, w_uv, num_heads, head_dim, seq_ids=(0,),
+               n_q=None, scale=None, mask="causal", out=None, out_dtype=torch.float32):
+        """Absorbed MLA attention of n_q[i] query rows per sequence
+        (mla.go:316-377).  q_nope [rows, H, D], q_rope [rows, H, d_r],
+        w_uk / w_uv bf16 [d_c, H*D]; returns [rows, H, D]."""
+        seq_ids = list(seq_ids)
+        if n_q is None:
+            n_q = [1] * len(seq_ids)
+        rows = sum(n_q)
+        if q_nope.numel() != rows * num_heads * head_dim or q_rope.numel() != rows * num_heads * self.d_r:
+            raise ValueError("query sizes do not match sum(n_q) x heads")
+        if w_uk.dtype != torch.bfloat16 or w_uv.dtype != torch.bfloat16:
+            raise TypeError("W_UK / W_UV must be bf16 (optim.Param.Data is bf16)")
+        if w_uk.numel() != self.d_c * num_heads * head_dim or w_uv.numel() != w_uk.numel():
+            raise ValueError("W_UK / W_UV must be [d_c, num_heads*head_dim]")
+        if out is None:
+            out = torch.empty((rows, num_heads, head_dim), dtype=out_dtype, device=q_nope.device)
+        if q_nope.dtype != q_rope.dtype:
+            raise TypeError("q_nope and q_rope dtypes differ")
+        check(self._lib.rlx_mla_attend(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                       i32_array(n_q), num_heads, head_dim, _dev(q_nope, "q_nope"),
+                                       _dev(q_rope, "q_rope"), _dtype_code(q_nope),
+                                       _dev(w_uk, "w_uk"), _dev(w_uv, "w_uv"), float(scale or 0.0),
+                                       _MASKS[mask], _dev(out, "out"), _dtype_code(out)))
+        return out
+
+
+def default_scale(head_dim, d_r=0):
+    """f32(1/sqrt(f64(D + dR))) as the reference computes it (mha.go:319,
+    mla.go:339-340)."""
+    return float(torch.tensor(1.0 / math.sqrt(head_dim + d_r), dtype=torch.float32))

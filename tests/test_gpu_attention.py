@@ -1,0 +1,273 @@
+"""GPU parity of decode / verify attention over the paged cache.
+
+Two references per case:
+  * the oracle's restatement of the reference loops (fastexp32 softmax,
+    mha.go:291-348 / mla.go:316-377): max-abs 2e-2, mean-abs 2e-3 at the
+    context lengths of the benchmark configs;
+  * an exact-softmax f64 attention (numpy, independent): max-abs 1e-2,
+    mean-abs 1e-3, which bounds the kernel's own bf16 operand rounding.
+At the full benchmark shapes a torch f32 attention over the gathered cache
+is the reference (same exact-softmax tolerance).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+TOL_ORACLE = (2e-2, 2e-3)
+TOL_EXACT = (1e-2, 1e-3)
+
+
+def _check(got, want, tol, what):
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64))
+    assert err.max() <= tol[0] and err.mean() <= tol[1], (
+        f"{what}: max-abs {err.max():.3e} mean-abs {err.mean():.3e} (tol {tol})")
+
+
+def _limits(mask, nq, T):
+    if mask == "causal":
+        return [T - nq + i for i in range(nq)]
+    if mask == "ref":
+        return [i if nq == T else T - 1 for i in range(nq)]
+    return [T - 1] * nq
+
+
+def _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=2):
+    """Append lens[i] tokens to sequence i in `chunks` multi-sequence calls;
+    returns the logical bf16 K/V per sequence as floats [KVH, T, D]."""
+    S = len(lens)
+    ks = [[] for _ in range(S)]
+    vs = [[] for _ in range(S)]
+    done = [0] * S
+    for ci in range(chunks):
+        n = [(L * (ci + 1)) // chunks - done[i] for i, L in enumerate(lens)]
+        k = rng.standard_normal((sum(n), KVH, D), dtype=np.float32)
+        v = rng.standard_normal((sum(n), KVH, D), dtype=np.float32)
+        c.Append(0, torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu),
+                 seq_ids=list(range(S)), n_tok=n, layout="SHD")
+        off = 0
+        for i in range(S):
+            ks[i].append(k[off:off + n[i]])
+            vs[i].append(v[off:off + n[i]])
+            off += n[i]
+            done[i] += n[i]
+    K = [oracle.round_bf16(np.concatenate(x)).transpose(1, 0, 2) for x in ks]
+    V = [oracle.round_bf16(np.concatenate(x)).transpose(1, 0, 2) for x in vs]
+    return K, V
+
+
+@pytest.mark.parametrize("H,KVH,D,lens,nq,mask", [
+    (32, 8, 128, [1, 2, 15, 16, 17, 64, 65, 300], 1, "causal"),     # ragged, page edges
+    (32, 8, 128, [600, 1, 257], 4, "causal"),                        # verify, 4 drafts x 4 heads
+    (64, 8, 128, [700, 33, 96], 4, "causal"),                        # 32 query rows per kv head
+    (8, 8, 64, [5, 129, 1000], 2, "none"),
+    (16, 4, 64, [7, 7, 40], 7, "ref"),                               # reference mask rule
+    (16, 4, 128, [3, 12], 3, "ref"),
+])
+def test_gqa_attend_matches_oracle(gpu, H, KVH, D, lens, nq, mask):
+    from relux_amd import KVCache
+    rng = np.random.default_rng(hash((H, KVH, D, nq, mask, len(lens))) % 2**32)
+    P = 16
+    c = KVCache(num_layers=1, max_len=max(lens) + 32, num_kv_heads=KVH, head_dim=D,
+                page_tokens=P, max_seqs=len(lens), device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    nqs = [min(nq, L) for L in lens]
+    q = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    out = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=list(range(len(lens))), n_q=nqs,
+                   mask=mask).cpu().numpy()
+    off = 0
+    for i, L in enumerate(lens):
+        qs = q[off:off + nqs[i]].transpose(1, 0, 2)            # [H, nq, D]
+        got = out[off:off + nqs[i]].transpose(1, 0, 2)
+        g = H // KVH
+        exact = oracle.exact_attention_f64(qs, np.repeat(K[i], g, 0), np.repeat(V[i], g, 0),
+                                           _limits(mask, nqs[i], L))
+        _check(got, exact, TOL_EXACT, f"seq {i} len {L} vs exact")
+        if L >= 256:
+            ref = oracle.gqa_attend(qs, K[i], V[i], mask)
+            _check(got, ref, TOL_ORACLE, f"seq {i} len {L} vs oracle")
+        off += nqs[i]
+
+
+def test_gqa_layouts_dtypes_and_bf16_output(gpu):
+    from relux_amd import KVCache
+    rng = np.random.default_rng(21)
+    H, KVH, D, lens = 16, 4, 128, [100, 333]
+    c = KVCache(num_layers=1, max_len=400, num_kv_heads=KVH, head_dim=D, max_seqs=2,
+                device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    q = torch.from_numpy(rng.standard_normal((2, H, D), dtype=np.float32)).to(gpu)
+    base = c.Attend(0, q, H, seq_ids=[0, 1]).cpu()
+    # HSD layout = per sequence [H][nq][D] (identical when nq == 1)
+    hsd = c.Attend(0, q, H, seq_ids=[0, 1], layout="HSD").cpu()
+    assert torch.equal(base, hsd)
+    b16 = c.Attend(0, q.bfloat16(), H, seq_ids=[0, 1], out_dtype=torch.bfloat16).float().cpu()
+    _check(b16.numpy(), base.numpy(), (1.5e-2, 1.5e-3), "bf16 q/out")
+    # reordered sequence list gives the same per-sequence rows
+    rev = c.Attend(0, torch.flip(q, [0]).contiguous(), H, seq_ids=[1, 0]).cpu()
+    assert torch.equal(rev[0], base[1]) and torch.equal(rev[1], base[0])
+
+
+def test_gqa_attention_after_evict_equals_dense_survivors(gpu):
+    """Attention over an evicted+compacted cache == exact attention over the
+    surviving tokens (row A17 of the parity contract)."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(22)
+    H, KVH, D, P = 32, 8, 128, 16
+    lens = [500, 260]
+    c = KVCache(num_layers=1, max_len=1024, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=2, device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    ev = [(L // P) // 4 for L in lens]
+    for s, e in enumerate(ev):
+        c.Evict(s, e)
+    q = torch.from_numpy(rng.standard_normal((2, H, D), dtype=np.float32)).to(gpu)
+    before = c.Attend(0, q, H, seq_ids=[0, 1]).cpu().numpy()
+    c.Compact()
+    after = c.Attend(0, q, H, seq_ids=[0, 1]).cpu().numpy()
+    assert np.array_equal(before, after)
+    for s in range(2):
+        Ks, Vs = K[s][:, ev[s] * P:], V[s][:, ev[s] * P:]
+        T = Ks.shape[1]
+        exact = oracle.exact_attention_f64(q[s:s + 1].cpu().numpy().transpose(1, 0, 2),
+                                           np.repeat(Ks, H // KVH, 0), np.repeat(Vs, H // KVH, 0),
+                                           [T - 1])
+        _check(after[s:s + 1].transpose(1, 0, 2), exact, TOL_EXACT, f"seq {s} survivors")
+
+
+def _torch_gqa_ref(k_list, v_list, q, H, KVH):
+    """f32 exact attention in torch over dense K/V (full-size property check)."""
+    outs = []
+    g = H // KVH
+    for i, (k, v) in enumerate(zip(k_list, v_list)):
+        kf = k[0].float().repeat_interleave(g, 0)          # [H, T, D]
+        vf = v[0].float().repeat_interleave(g, 0)
+        s = torch.einsum("hd,htd->ht", q[i].float(), kf) / math.sqrt(kf.shape[-1])
+        w = torch.softmax(s, dim=-1)
+        outs.append(torch.einsum("ht,htd->hd", w, vf))
+    return torch.stack(outs)
+
+
+def test_gqa_config2_full_shape(gpu):
+    """B 16, H 32, KVH 8, D 128, T ~ U[512, 4096], 16-token
+    pages randomly permuted in a shared pool, one append then one query."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(2)
+    B, H, KVH, D, P = 16, 32, 8, 128, 16
+    lens = rng.integers(512, 4097, size=B).tolist()
+    c = KVCache(num_layers=1, max_len=4096 + 16, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=B, pool_pages=sum(-(-(L + 1) // P) for L in lens) + 64, device=gpu.index)
+    # permute the pool: interleave sequences page by page in random order
+    left = list(lens)
+    while any(left):
+        order = [i for i in rng.permutation(B) if left[i] > 0]
+        n = [min(P, left[i]) for i in order]
+        k = torch.randn(sum(n), KVH, D, device=gpu)
+        c.Append(0, k, torch.randn_like(k), seq_ids=order, n_tok=n, layout="SHD")
+        for i, ni in zip(order, n):
+            left[i] -= ni
+    k1 = torch.randn(B, KVH, D, device=gpu)
+    c.Append(0, k1, torch.randn_like(k1), seq_ids=list(range(B)), n_tok=[1] * B, layout="SHD")
+    q = torch.randn(B, H, D, device=gpu)
+    out = c.Attend(0, q, H, seq_ids=list(range(B)))
+    views = [c.View(0, i) for i in range(B)]
+    ref = _torch_gqa_ref([v[0] for v in views], [v[1] for v in views], q, H, KVH)
+    _check(out.cpu().numpy(), ref.cpu().numpy(), TOL_EXACT, "config 2 vs torch f32")
+    for i in (0, 7):  # the reference loops themselves on two sequences
+        kk = views[i][0][0].float().cpu().numpy()
+        vv = views[i][1][0].float().cpu().numpy()
+        ref_o = oracle.gqa_attend(q[i:i + 1].cpu().numpy().transpose(1, 0, 2), kk, vv, "causal")
+        _check(out[i:i + 1].cpu().numpy().transpose(1, 0, 2), ref_o, TOL_ORACLE, f"seq {i} vs oracle")
+
+
+# ---- MLA -------------------------------------------------------------------
+
+def _mla_exact(qc, qr, c, kr, w_uk, w_uv, limits):
+    """Absorbed MLA in f64 with exact softmax; qc [H,nq,D], qr [H,nq,dR]."""
+    H, nq, D = qc.shape
+    dC = c.shape[1]
+    Wk = oracle.f32_from_bf16(w_uk).astype(np.float64).reshape(dC, H, D)
+    Wv = oracle.f32_from_bf16(w_uv).astype(np.float64).reshape(dC, H, D)
+    qlat = np.einsum("chd,hid->hic", Wk, qc.astype(np.float64))
+    s = (np.einsum("hic,tc->hit", qlat, c.astype(np.float64)) +
+         np.einsum("hir,tr->hit", qr.astype(np.float64), kr.astype(np.float64))) / math.sqrt(D + qr.shape[2])
+    T = c.shape[0]
+    s = np.where(np.arange(T)[None, None, :] <= np.asarray(limits)[None, :, None], s, -np.inf)
+    w = np.exp(s - s.max(-1, keepdims=True))
+    w /= w.sum(-1, keepdims=True)
+    return np.einsum("hic,chd->hid", np.einsum("hit,tc->hic", w, c.astype(np.float64)), Wv)
+
+
+@pytest.mark.parametrize("H,lens,nq,mask", [
+    (16, [1, 15, 64, 65, 200, 300], 1, "causal"),
+    (16, [260, 7], 2, "causal"),
+    (8, [90, 3], 3, "ref"),
+    (16, [128], 1, "none"),
+])
+def test_mla_attend_matches_oracle(gpu, H, lens, nq, mask):
+    from relux_amd import MLACache
+    rng = np.random.default_rng(31 + H + nq)
+    D, P = 128, 64
+    c = MLACache(num_layers=1, max_len=max(lens) + 64, page_tokens=P, max_seqs=len(lens),
+                 device=gpu.index)
+    cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
+    kr = rng.standard_normal((sum(lens), 64), dtype=np.float32)
+    c.Append(0, torch.from_numpy(cc).to(gpu), torch.from_numpy(kr).to(gpu),
+             seq_ids=list(range(len(lens))), n_tok=lens)
+    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    nqs = [min(nq, L) for L in lens]
+    qn = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    qr = rng.standard_normal((sum(nqs), H, 64), dtype=np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    wuk = t(w_uk.view(np.int16)).view(torch.bfloat16)
+    wuv = t(w_uv.view(np.int16)).view(torch.bfloat16)
+    out = c.Attend(0, t(qn), t(qr), wuk, wuv, H, D, seq_ids=list(range(len(lens))), n_q=nqs,
+                   mask=mask).cpu().numpy()
+    off = 0
+    toff = 0
+    for i, L in enumerate(lens):
+        cs = oracle.round_bf16(cc[toff:toff + L])
+        ks = oracle.round_bf16(kr[toff:toff + L])
+        qci = qn[off:off + nqs[i]].transpose(1, 0, 2)
+        qri = qr[off:off + nqs[i]].transpose(1, 0, 2)
+        got = out[off:off + nqs[i]].transpose(1, 0, 2)
+        exact = _mla_exact(qci, qri, cs, ks, w_uk, w_uv, _limits(mask, nqs[i], L))
+        # outputs are ~0.02-scale (W_UV N(0,0.02)): judge relative to that scale
+        _check(got / 0.1, exact / 0.1, TOL_EXACT, f"seq {i} len {L} vs exact (x10)")
+        if L >= 200:
+            ref = oracle.mla_attend(qci, qri, cs, ks, w_uk, w_uv, mask)
+            _check(got, ref, TOL_ORACLE, f"seq {i} len {L} vs oracle")
+        off += nqs[i]
+        toff += L
+
+
+def test_mla_config3_full_shape(gpu):
+    """BASELINE config 3 (reduced batch for test time): H 16, d_c 512, d_r 64,
+    context 8192, 64-token pages; torch f32 absorbed reference."""
+    from relux_amd import MLACache
+    torch.manual_seed(3)
+    B, H, D, T, P = 4, 16, 128, 8192, 64
+    c = MLACache(num_layers=1, max_len=T + P, page_tokens=P, max_seqs=B, device=gpu.index)
+    for i in range(B):
+        c.Append(0, torch.randn(T, 512, device=gpu), torch.randn(T, 64, device=gpu), seq_ids=[i])
+    w_uk = (torch.randn(512, H * D, device=gpu) * 0.02).bfloat16()
+    w_uv = (torch.randn(512, H * D, device=gpu) * 0.02).bfloat16()
+    qn = torch.randn(B, H, D, device=gpu)
+    qr = torch.randn(B, H, 64, device=gpu)
+    out = c.Attend(0, qn, qr, w_uk, w_uv, H, D, seq_ids=list(range(B)))
+    Wk = w_uk.float().view(512, H, D)
+    Wv = w_uv.float().view(512, H, D)
+    for i in range(B):
+        cc, kk = c.View(0, i)
+        cc, kk = cc[0].float(), kk[0].float()
+        qlat = torch.einsum("chd,hd->hc", Wk, qn[i])
+        s = (qlat @ cc.T + qr[i] @ kk.T) / math.sqrt(D + 64)
+        w = torch.softmax(s, dim=-1)
+        ref = torch.einsum("hc,chd->hd", w @ cc, Wv)
+        _check(out[i].cpu().numpy() / 0.1, ref.cpu().numpy() / 0.1, TOL_EXACT, f"seq {i} (x10)")

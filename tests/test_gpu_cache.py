@@ -1,0 +1,210 @@
+"""GPU parity of the paged cache state machine and byte movement.
+
+Every check is bit-exact: cache contents (via the paged gather) against
+BF16FromF32 of the appended rows in logical order (the oracle), page tables
+and free lists against oracle/paged.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle.paged import PagedModel
+
+pytestmark = pytest.mark.gpu
+
+
+def _kv(gpu, **kw):
+    from relux_amd import KVCache
+    return KVCache(device=gpu.index, **kw)
+
+
+def _mla(gpu, **kw):
+    from relux_amd import MLACache
+    return MLACache(device=gpu.index, **kw)
+
+
+def test_reference_kvcache_known_answers(gpu):
+    """kvcache_test.go:16-106 through the drop-in API."""
+    c = _kv(gpu, num_layers=2, max_len=16, num_kv_heads=2, head_dim=64)
+    assert c.TotalLen(0) == 0
+    k = torch.arange(1, 2 * 64 + 1, dtype=torch.float32, device=gpu).reshape(1, 2, 1, 64)
+    c.Append(0, k, k + 1000)
+    assert c.TotalLen(0) == 1 and c.TotalLen(1) == 0 and c.TotalLen(7) == 0
+    ck, cv = c.View(0)
+    assert tuple(ck.shape) == (1, 2, 1, 64)
+    want = oracle.round_bf16(k.cpu().numpy())
+    assert np.array_equal(ck.float().cpu().numpy(), want)
+    assert np.array_equal(cv.float().cpu().numpy(), oracle.round_bf16((k + 1000).cpu().numpy()))
+    k2 = torch.arange(9, 9 + 2 * 2 * 64, dtype=torch.float32, device=gpu).reshape(1, 2, 2, 64)
+    c.Append(0, k2, k2)
+    assert c.TotalLen(0) == 3
+    ck, _ = c.View(0)
+    full = np.concatenate([k.cpu().numpy(), k2.cpu().numpy()], axis=2)
+    assert np.array_equal(ck.float().cpu().numpy(), oracle.round_bf16(full))
+    c.Reset()
+    assert c.TotalLen(0) == 0 and c.View(0) == (None, None)
+
+
+def test_errors_mirror_reference_panics(gpu):
+    from relux_amd import ReluxError, ReluxPanic
+    c = _kv(gpu, num_layers=1, max_len=32, num_kv_heads=1, head_dim=64, max_seqs=2, pool_pages=3)
+    x = torch.zeros(1, 1, 20, 64, device=gpu)
+    c.Append(0, x, x)
+    tab = c.PageTable(0, 0)
+    with pytest.raises(ReluxPanic):                 # kvcache.go:282-285
+        c.Append(0, torch.zeros(1, 1, 13, 64, device=gpu), torch.zeros(1, 1, 13, 64, device=gpu))
+    with pytest.raises(ReluxPanic):                 # kvcache.go:241-243
+        c.Append(3, x, x)
+    with pytest.raises(ReluxError):                 # pool of 3 pages exhausted
+        c.Append(0, torch.zeros(1, 1, 40, 64, device=gpu), torch.zeros(1, 1, 40, 64, device=gpu),
+                 seq_ids=[1])
+    assert c.TotalLen(0) == 20 and c.PageTable(0, 0) == tab and c.TotalLen(0, 1) == 0
+    with pytest.raises(ReluxPanic):                 # K/V shape mismatch
+        c.Append(0, x, torch.zeros(1, 1, 19, 64, device=gpu))
+
+
+@pytest.mark.parametrize("src_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["HSD", "SHD"])
+def test_multi_sequence_append_gather_bit_exact(gpu, src_dtype, layout):
+    rng = np.random.default_rng(11)
+    KVH, D, P, S = 4, 128, 16, 5
+    c = _kv(gpu, num_layers=2, max_len=512, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+            max_seqs=S, pool_pages=120)
+    model = PagedModel(2, P, 120, S, 32)
+    logical = {(l, s): [] for l in range(2) for s in range(S)}
+    for step in range(6):
+        for layer in range(2):
+            seqs = [int(s) for s in rng.permutation(S)[: rng.integers(1, S + 1)]]
+            n = [int(v) for v in rng.integers(0, 40, size=len(seqs))]
+            k_tok = [rng.normal(size=(ni, KVH, D)).astype(np.float32) * 3 for ni in n]
+            v_tok = [rng.normal(size=(ni, KVH, D)).astype(np.float32) for ni in n]
+            if layout == "SHD":
+                kk = np.concatenate(k_tok) if sum(n) else np.zeros((0, KVH, D), np.float32)
+                vv = np.concatenate(v_tok) if sum(n) else np.zeros((0, KVH, D), np.float32)
+            else:
+                kk = np.concatenate([t.transpose(1, 0, 2).reshape(-1) for t in k_tok])
+                vv = np.concatenate([t.transpose(1, 0, 2).reshape(-1) for t in v_tok])
+            kt = torch.from_numpy(np.ascontiguousarray(kk)).to(gpu).to(src_dtype)
+            vt = torch.from_numpy(np.ascontiguousarray(vv)).to(gpu).to(src_dtype)
+            c.Append(layer, kt, vt, seq_ids=seqs, n_tok=n, layout=layout)
+            model.append(layer, seqs, n)
+            for s, kt_, vt_ in zip(seqs, k_tok, v_tok):
+                src_k = kt_ if src_dtype == torch.float32 else oracle.round_bf16(kt_)
+                src_v = vt_ if src_dtype == torch.float32 else oracle.round_bf16(vt_)
+                logical[(layer, s)].append((oracle.bf16_from_f32(src_k), oracle.bf16_from_f32(src_v)))
+    for layer in range(2):
+        assert c.FreeList(layer) == model.free[layer]
+        for s in range(S):
+            assert c.TotalLen(layer, s) == model.len[layer, s]
+            assert c.PageTable(layer, s) == list(model.table[layer][s])
+            ck, cv = c.View(layer, s)
+            parts = logical[(layer, s)]
+            if not parts or sum(p[0].shape[0] for p in parts) == 0:
+                assert ck is None
+                continue
+            want_k = np.concatenate([p[0] for p in parts]).transpose(1, 0, 2)
+            want_v = np.concatenate([p[1] for p in parts]).transpose(1, 0, 2)
+            assert np.array_equal(ck.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_k)
+            assert np.array_equal(cv.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_v)
+
+
+def test_append_conversion_edge_bits(gpu):
+    """NaN / Inf / denormal / tie patterns convert exactly as BF16FromF32."""
+    special = np.array([0x7FFFFFFF, 0x7F800001, 0x7FC00000, 0x7F7FFFFF, 0x00000001, 0x00008000,
+                        0x00018000, 0x80000000, 0xFF800000, 0x3F800000, 0x3F808000, 0x3F818000,
+                        0x807FFFFF, 0x00800000, 0x477FE000, 0xC77FF000], np.uint32)
+    D = 64
+    vals = np.resize(special, D).view(np.float32)
+    c = _kv(gpu, num_layers=1, max_len=16, num_kv_heads=1, head_dim=D)
+    k = torch.from_numpy(vals.copy()).to(gpu).reshape(1, 1, 1, D)
+    c.Append(0, k, k)
+    ck, cv = c.View(0)
+    got = ck.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    assert np.array_equal(got, oracle.bf16_from_f32(vals))
+
+
+def test_rollback_evict_compact_state(gpu):
+    rng = np.random.default_rng(12)
+    KVH, D, P, S, POOL, MAXP = 2, 64, 16, 4, 64, 20
+    c = _kv(gpu, num_layers=2, max_len=MAXP * P, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+            max_seqs=S, pool_pages=POOL)
+    m = PagedModel(2, P, POOL, S, MAXP)
+    rows = {(l, s): [] for l in range(2) for s in range(S)}
+    for step in range(40):
+        seqs = list(range(S))
+        n = [int(v) for v in rng.integers(1, 6, size=S)]
+        for layer in range(2):
+            room = [min(ni, (MAXP - int(m.first[layer, s])) * P - int(m.len[layer, s])) for s, ni in zip(seqs, n)]
+            n = [max(0, r) for r in room]
+        if sum(n) and sum(-(-(int(m.len[0, s]) + ni) // P) - int(m.pages[0, s]) for s, ni in zip(seqs, n)) <= len(m.free[0]):
+            for layer in range(2):
+                kk = rng.normal(size=(sum(n), KVH, D)).astype(np.float32)
+                t = torch.from_numpy(kk).to(gpu)
+                c.Append(layer, t, t, seq_ids=seqs, n_tok=n, layout="SHD")
+                m.append(layer, seqs, n)
+                off = 0
+                for s, ni in zip(seqs, n):
+                    rows[(layer, s)].extend(oracle.bf16_from_f32(kk[off:off + ni]))
+                    off += ni
+        for s in range(S):
+            r = int(rng.integers(0, 5))
+            r = min(r, int(m.len[0, s]))
+            c.Rollback(s, r)
+            m.rollback(-1, s, r)
+            for layer in range(2):
+                if r:
+                    del rows[(layer, s)][len(rows[(layer, s)]) - r:]
+        if step % 10 == 9:
+            for s in range(S):
+                e = (int(m.len[0, s]) // P) // 4
+                c.Evict(s, e)
+                m.evict(-1, s, e)
+                for layer in range(2):
+                    del rows[(layer, s)][: e * P]
+            if step % 20 == 19:
+                c.Compact()
+                m.compact(-1)
+        for layer in range(2):
+            assert c.FreeList(layer) == m.free[layer]
+            for s in range(S):
+                assert c.SeqState(layer, s) == m.state(layer, s)
+                assert c.PageTable(layer, s) == list(m.table[layer][s])
+    for layer in range(2):
+        for s in range(S):
+            ck, cv = c.View(layer, s)
+            if not rows[(layer, s)]:
+                assert ck is None
+                continue
+            want = np.stack(rows[(layer, s)]).transpose(1, 0, 2)
+            assert np.array_equal(ck.view(torch.int16).cpu().numpy().view(np.uint16)[0], want)
+    c.Release(0)
+    m.release(-1, 0)
+    assert c.FreeList(0) == m.free[0] and c.PageTable(1, 0) == list(m.table[1][0])
+
+
+def test_mla_append_gather_bit_exact(gpu):
+    rng = np.random.default_rng(13)
+    P, S = 64, 3
+    c = _mla(gpu, num_layers=1, max_len=1024, page_tokens=P, max_seqs=S, pool_pages=40)
+    m = PagedModel(1, P, 40, S, 16)
+    rows = {s: [] for s in range(S)}
+    for step in range(5):
+        n = [int(v) for v in rng.integers(0, 130, size=S)]
+        cc = rng.normal(size=(sum(n), 512)).astype(np.float32)
+        kr = rng.normal(size=(sum(n), 64)).astype(np.float32)
+        c.Append(0, torch.from_numpy(cc).to(gpu), torch.from_numpy(kr).to(gpu),
+                 seq_ids=list(range(S)), n_tok=n)
+        m.append(0, list(range(S)), n)
+        off = 0
+        for s in range(S):
+            rows[s].append((cc[off:off + n[s]], kr[off:off + n[s]]))
+            off += n[s]
+    assert c.FreeList(0) == m.free[0]
+    for s in range(S):
+        assert c.PageTable(0, s) == list(m.table[0][s])
+        got_c, got_kr = c.View(0, s)
+        want_c = oracle.bf16_from_f32(np.concatenate([r[0] for r in rows[s]]))
+        want_kr = oracle.bf16_from_f32(np.concatenate([r[1] for r in rows[s]]))
+        assert np.array_equal(got_c.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_c)
+        assert np.array_equal(got_kr.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_kr)
