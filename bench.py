@@ -225,6 +225,26 @@ def cpu_baseline_mla(cfg, lens, budget_s=12.0):
                       f"and scaled x{H // h_s} (decompress-all C restatement of mla.go:309-377, 1 thread)"}
 
 
+def copy_probe(torch, dev, nbytes=1 << 30, reps=20):
+    """Plain device-to-device copy of `nbytes` (torch's copy kernel): the
+    achievable-bandwidth reference, and the known-size kernel that scales the
+    FETCH_SIZE / WRITE_SIZE counters (it reads and writes nbytes per launch)."""
+    src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).uniform_()
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    s = e0.elapsed_time(e1) / 1e3 / reps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us": s * 1e6,
+            "copy_gbs": 2 * nbytes / s / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +254,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the secondary workloads reported beside the headline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only time a 1 GiB device copy (bandwidth reference) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on ONE GPU (no collectives, no sharding); "
@@ -244,6 +266,9 @@ def main():
     import relux_amd
     relux_amd.load()
     dev = torch.device("cuda", 0)
+    if args.copy_probe:
+        print(json.dumps(copy_probe(torch, dev)), flush=True)
+        return
     print(f"[bench] workload {args.workload} steps {args.steps} warmup {args.warmup}",
           file=sys.stderr, flush=True)
     r = run_workload(args.workload, args.steps, args.warmup, torch, dev)

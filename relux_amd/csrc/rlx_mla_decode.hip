@@ -40,39 +40,65 @@ __device__ __forceinline__ int mla_key_limit(int mask_mode, int len, int nq, int
     return len - 1;
 }
 
-// q_lat[row][h][0:512] = bf16(qscale * sum_d q_nope[row][h][d] * W_UK[c][h*D+d]),
-// q_lat[row][h][512:576] = bf16(qscale * q_rope[row][h][:]).
+// q_lat[row][h][c] = bf16(qscale * sum_d q_nope[row][h][d] * W_UK[c][h*D+d])
+// for c < 512 and q_lat[row][h][512+r] = bf16(qscale * q_rope[row][h][r]).
+// Block = (head, 8 query rows, 64 latent channels).  Four adjacent lanes share
+// a channel and split its D weights (16-byte loads, 4 lanes cover the head's
+// whole W_UK row segment); their partial dots meet by two lane swaps.
 __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
                                                          const void *__restrict__ q_rope,
                                                          int q_bf16,
                                                          const uint16_t *__restrict__ w_uk,
-                                                         int H, int D, float qscale,
+                                                         int H, int D, int total_q, float qscale,
                                                          uint16_t *__restrict__ qlat) {
-    const int row = blockIdx.x, h = blockIdx.y;
-    __shared__ float qn[256];
-    const int64_t qoff = ((int64_t)row * H + h) * D;
-    for (int d = threadIdx.x; d < D; d += blockDim.x)
-        qn[d] = q_bf16 ? bf16_f32(((const uint16_t *)q_nope)[qoff + d]) : ((const float *)q_nope)[qoff + d];
-    __syncthreads();
-    uint16_t *dst = qlat + ((int64_t)row * H + h) * kMlaRow;
-    const int64_t wpitch = (int64_t)H * D;
-    for (int c = threadIdx.x; c < kMlaDc; c += blockDim.x) {
-        const uint16_t *w = w_uk + (int64_t)c * wpitch + (int64_t)h * D;
-        float acc = 0.f;
-        for (int d = 0; d < D; d += 8) {
-            u32x4 v = *(const u32x4 *)(w + d);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                acc += qn[d + 2 * i] * bf16_f32((uint16_t)(v[i] & 0xFFFFu));
-                acc += qn[d + 2 * i + 1] * bf16_f32((uint16_t)(v[i] >> 16));
-            }
-        }
-        dst[c] = bf16_rne(acc * qscale);
+    const int h = blockIdx.x, r0 = blockIdx.y * 8;
+    __shared__ float qn[8][256];
+    for (int i = threadIdx.x; i < 8 * D; i += blockDim.x) {
+        const int r = i / D, d = i - r * D;
+        const int64_t off = ((int64_t)(r0 + r) * H + h) * D + d;
+        float x = 0.f;
+        if (r0 + r < total_q)
+            x = q_bf16 ? bf16_f32(((const uint16_t *)q_nope)[off]) : ((const float *)q_nope)[off];
+        qn[r][d] = x;
     }
-    const int64_t roff = ((int64_t)row * H + h) * kMlaDr;
-    for (int r = threadIdx.x; r < kMlaDr; r += blockDim.x) {
-        const float x = q_bf16 ? bf16_f32(((const uint16_t *)q_rope)[roff + r]) : ((const float *)q_rope)[roff + r];
-        dst[kMlaDc + r] = bf16_rne(x * qscale);
+    __syncthreads();
+    const int c = blockIdx.z * 64 + (threadIdx.x >> 2);
+    const int g = threadIdx.x & 3;
+    const int dq = D / 4;  // dims per lane: 16..64, a multiple of 8
+    const uint16_t *w = w_uk + (int64_t)c * H * D + (int64_t)h * D + g * dq;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < dq; d += 8) {
+        const u32x4 v = *(const u32x4 *)(w + d);
+        float wv[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            wv[2 * i] = bf16_f32((uint16_t)(v[i] & 0xFFFFu));
+            wv[2 * i + 1] = bf16_f32((uint16_t)(v[i] >> 16));
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc[r] += qn[r][g * dq + d + j] * wv[j];
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        acc[r] += __shfl_xor(acc[r], 1);
+        acc[r] += __shfl_xor(acc[r], 2);
+    }
+    if (g == 0) {
+#pragma unroll
+        for (int r = 0; r < 8; r++)
+            if (r0 + r < total_q)
+                qlat[((int64_t)(r0 + r) * H + h) * kMlaRow + c] = bf16_rne(acc[r] * qscale);
+    }
+    if (blockIdx.z == 0) {
+        for (int i = threadIdx.x; i < 8 * kMlaDr; i += blockDim.x) {
+            const int r = i / kMlaDr, k = i - r * kMlaDr;
+            if (r0 + r >= total_q) continue;
+            const int64_t off = ((int64_t)(r0 + r) * H + h) * kMlaDr + k;
+            const float x = q_bf16 ? bf16_f32(((const uint16_t *)q_rope)[off]) : ((const float *)q_rope)[off];
+            qlat[((int64_t)(r0 + r) * H + h) * kMlaRow + kMlaDc + k] = bf16_rne(x * qscale);
+        }
     }
 }
 
@@ -138,7 +164,7 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
         for (int k = 0; k < 5; k++) {
             const int c = tid + 256 * k;
             pre[k] = u32x4{0, 0, 0, 0};
-            if (c < CHUNKS && t0 + c / 72 < R.len) pre[k] = *(const u32x4 *)(src + (int64_t)c * 8);
+            if (c < CHUNKS && t0 + c / 72 < R.len) pre[k] = __builtin_nontemporal_load((const u32x4 *)(src + (int64_t)c * 8));
         }
     };
     auto store_tile = [&](int buf) {
@@ -244,63 +270,76 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
     }
 }
 
-// Merge the splits of one (sequence, query, head) into o_lat (LDS) and apply
-// W_UV: out[row][h][d] = sum_c o_lat[c] * W_UV[c][h*D+d].
-__global__ __launch_bounds__(128) void mla_output_kernel(
+// Merge the splits of one (sequence, query, head) into the normalised latent
+// output o_lat[row][h][0:512] (f32 workspace).  One 256-thread block per
+// query row: wave 0 computes the merge weights in LDS, then every thread
+// streams two latent channels across the splits.
+__global__ __launch_bounds__(256) void mla_combine_kernel(
     const AttRow *__restrict__ rows, const float *__restrict__ part_o,
-    const float *__restrict__ part_ml, const uint16_t *__restrict__ w_uv, int H, int D,
-    int QRP, void *__restrict__ out, int out_bf16) {
+    const float *__restrict__ part_ml, int H, int QRP, float *__restrict__ olat) {
     const AttRow R = rows[blockIdx.x];
     const int qi = blockIdx.y / H;
     const int h = blockIdx.y - qi * H;
     if (qi >= R.nq) return;
     const int qr = qi * H + h;
-    __shared__ float olat[kMlaDc];
-    __shared__ float fac[64];
-    __shared__ float invL;
-    if (threadIdx.x == 0) {
-        float M = -INFINITY;
-        for (int s = 0; s < R.nsplit; s++)
-            M = fmaxf(M, part_ml[((int64_t)(R.part + s) * QRP + qr) * 2]);
-        float L = 0.f;
-        for (int s = 0; s < R.nsplit; s++) {
-            const float *pm = part_ml + ((int64_t)(R.part + s) * QRP + qr) * 2;
-            const float f = (pm[0] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(pm[0] - M);
-            if (s < 64) fac[s] = f;
-            L += f * pm[1];
-        }
-        invL = (L > 0.f) ? 1.f / L : 0.f;
-    }
+    __shared__ float fac[kMaxSplits];
+    __shared__ float inv_l;
+    const int64_t b0 = (int64_t)R.part * QRP + qr;
+    merge_weights(part_ml + b0 * 2, QRP, R.nsplit, fac, &inv_l);
     __syncthreads();
+    float *dst = olat + ((int64_t)(R.qrow + qi) * H + h) * kMlaDc;
     for (int c = threadIdx.x; c < kMlaDc; c += blockDim.x) {
         float o = 0.f;
-        for (int s = 0; s < R.nsplit; s++) {
-            float f;
-            if (s < 64) {
-                f = fac[s];
-            } else {
-                // Rare: more splits than the factor cache holds.
-                float M = -INFINITY;
-                for (int u = 0; u < R.nsplit; u++)
-                    M = fmaxf(M, part_ml[((int64_t)(R.part + u) * QRP + qr) * 2]);
-                const float m = part_ml[((int64_t)(R.part + s) * QRP + qr) * 2];
-                f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
-            }
-            o += f * part_o[((int64_t)(R.part + s) * QRP + qr) * kMlaDc + c];
-        }
-        olat[c] = o * invL;
+        for (int s = 0; s < R.nsplit; s++) o += fac[s] * part_o[(b0 + (int64_t)s * QRP) * kMlaDc + c];
+        dst[c] = o * inv_l;
+    }
+}
+
+// out[row][h][d] = sum_c o_lat[row][h][c] * W_UV[c][h*D + d].  Block = (head,
+// 8 query rows, 32 output dims); thread = (dim, group of 64 channels), so each
+// W_UV element is loaded once per 8 rows, coalesced over the 32 dims.  The 8
+// channel-group partials meet in LDS and are added in a fixed order.
+__global__ __launch_bounds__(256) void mla_proj_kernel(const float *__restrict__ olat,
+                                                       const uint16_t *__restrict__ w_uv,
+                                                       int H, int D, int total_q,
+                                                       void *__restrict__ out, int out_bf16) {
+    const int h = blockIdx.x;
+    const int r0 = blockIdx.y * 8;
+    const int d = blockIdx.z * 32 + (threadIdx.x & 31);
+    const int cg = threadIdx.x >> 5;  // channels [64cg, 64cg+64)
+    __shared__ float tile[8][kMlaDc];
+    __shared__ float red[8][8][32];
+    for (int i = threadIdx.x; i < 8 * kMlaDc; i += blockDim.x) {
+        const int r = i / kMlaDc, c = i - r * kMlaDc;
+        tile[r][c] = (r0 + r < total_q) ? olat[((int64_t)(r0 + r) * H + h) * kMlaDc + c] : 0.f;
     }
     __syncthreads();
     const int64_t wpitch = (int64_t)H * D;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float acc = 0.f;
-        const uint16_t *w = w_uv + (int64_t)h * D + d;
-        for (int c = 0; c < kMlaDc; c++) acc += olat[c] * bf16_f32(w[(int64_t)c * wpitch]);
-        const int64_t o = ((int64_t)(R.qrow + qi) * H + h) * D + d;
-        if (out_bf16)
-            ((uint16_t *)out)[o] = bf16_rne(acc);
-        else
-            ((float *)out)[o] = acc;
+    const uint16_t *w = w_uv + (int64_t)(cg * 64) * wpitch + (int64_t)h * D + d;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 16
+    for (int k = 0; k < 64; k++) {
+        const float wv = bf16_f32(w[(int64_t)k * wpitch]);
+#pragma unroll
+        for (int r = 0; r < 8; r++) acc[r] += tile[r][cg * 64 + k] * wv;
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) red[cg][r][threadIdx.x & 31] = acc[r];
+    __syncthreads();
+    if (threadIdx.x < 32 * 8) {
+        const int r = threadIdx.x >> 5;  // row handled in the final sum
+        const int dl = threadIdx.x & 31;
+        const int row = r0 + r;
+        if (row < total_q) {
+            float v = 0.f;
+#pragma unroll
+            for (int g = 0; g < 8; g++) v += red[g][r][dl];
+            const int64_t o = ((int64_t)row * H + h) * D + blockIdx.z * 32 + dl;
+            if (out_bf16)
+                ((uint16_t *)out)[o] = bf16_rne(v);
+            else
+                ((float *)out)[o] = v;
+        }
     }
 }
 
@@ -310,11 +349,12 @@ hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t 
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
                              int total_q, int max_nq, int P, int chunk, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, float *part_o,
-                             float *part_ml, void *out, int out_bf16, hipEvent_t ev0,
-                             hipEvent_t ev1) {
+                             float *part_ml, float *olat, void *out, int out_bf16,
+                             hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
-    mla_absorb_kernel<<<dim3(total_q, H), 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, hd,
-                                                       qscale, qlat);
+    if (hd > 256 || hd % 64 != 0) return hipErrorInvalidValue;
+    mla_absorb_kernel<<<dim3(H, (total_q + 7) / 8, kMlaDc / 64), 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H,
+                                                                  hd, total_q, qscale, qlat);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev0) (void)hipEventRecord(ev0, s);
@@ -329,9 +369,21 @@ hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t 
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
-    mla_output_kernel<<<dim3(n_rows, max_nq * H), 128, 0, s>>>(rows, part_o, part_ml, w_uv, H,
-                                                               hd, 16 * nqt, out, out_bf16);
+    mla_combine_kernel<<<dim3(n_rows, max_nq * H), 256, 0, s>>>(rows, part_o, part_ml, H,
+                                                                16 * nqt, olat);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    mla_proj_kernel<<<dim3(H, (total_q + 7) / 8, hd / 32), 256, 0, s>>>(olat, w_uv, H, hd,
+                                                                        total_q, out, out_bf16);
     return hipGetLastError();
+}
+
+int mla_decode_wgs_per_cu(int nqt) {
+    int n = 0;
+    hipError_t e = hipErrorInvalidValue;
+    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1>, 256, 0);
+    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2>, 256, 0);
+    return (e == hipSuccess && n > 0) ? n : 1;
 }
 
 }  // namespace rlx

@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -78,6 +79,7 @@ struct Cache {
     int layers = 0, kvh = 0, hd = 0, P = 0, pool_pages = 0, max_seqs = 0, max_pages = 0;
     int dc = 0, dr = 0;
     int device = 0;
+    int cus = 256;  // compute units of the device
     std::vector<LayerState> L;
     int32_t *d_table = nullptr;
     hipStream_t own = nullptr, stream = nullptr;
@@ -230,6 +232,7 @@ void reset_layer_state(Cache *c, LayerState &ls) {
 
 int32_t create_common(Cache *c) {
     HIP_TRY(hipGetDevice(&c->device));
+    HIP_TRY(hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, c->device));
     HIP_TRY(hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking));
     c->stream = c->own;
     for (auto &s : c->slots) HIP_TRY(hipEventCreateWithFlags(&s.ev, hipEventDisableTiming));
@@ -315,17 +318,43 @@ int32_t plan_append(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, con
     return RLX_OK;
 }
 
-// Choose the context split (multiple of 64 tokens) so that the launch has
-// enough work-groups for 256 CUs without drowning in partials.
-int choose_chunk(int64_t total_tokens, int units_per_token_group, int max_len) {
-    int64_t target_groups = 2048;
-    int64_t chunk = (total_tokens * units_per_token_group) / target_groups;
-    chunk = std::max<int64_t>(chunk, 256);
-    chunk = std::min<int64_t>(chunk, 4096);
-    chunk = (chunk + 63) / 64 * 64;
-    if (chunk > max_len) chunk = ((max_len + 63) / 64) * 64;
-    if (chunk < 64) chunk = 64;
-    return (int)chunk;
+// Context split (tokens per work-group, a multiple of 64).  A decode launch
+// is bandwidth-bound with few work-groups per CU, so the best split is the
+// smallest one whose work-groups all fit in ONE residency round of the GPU
+// (slots = CUs x resident work-groups per CU): every CU then streams until
+// the end and none idles behind a partial last round.  When even one split
+// per sequence overflows the slots, splits are sized for about four rounds
+// so that unequal sequence lengths still balance.  At most kMaxSplits splits
+// per sequence (the merge kernel's weight buffer).
+int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
+    static const int64_t slot_override = [] {
+        const char *e = getenv("RLX_DECODE_SLOTS");  // tuning override
+        return e ? (int64_t)atoll(e) : (int64_t)0;
+    }();
+    if (slot_override > 0) slots = slot_override;
+    int max_len = 1;
+    for (int L : lens) max_len = std::max(max_len, L);
+    auto r64 = [](int64_t x) { return (int)((x + 63) / 64 * 64); };
+    const int lo_chunk = std::max(64, r64(((int64_t)max_len + kMaxSplits - 1) / kMaxSplits));
+    const int hi_chunk = std::max(lo_chunk, r64(max_len));
+    auto count = [&](int ch) {
+        int64_t n = 0;
+        for (int L : lens) n += (L + ch - 1) / ch;
+        return n * units;
+    };
+    int64_t target = slots;
+    if (count(hi_chunk) > slots) target = 4 * slots;
+    if (count(lo_chunk) <= target) return lo_chunk;
+    if (count(hi_chunk) > target) return hi_chunk;
+    int lo = lo_chunk / 64, hi = hi_chunk / 64;  // count(lo) > target >= count(hi)
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (count(mid * 64) <= target)
+            hi = mid;
+        else
+            lo = mid;
+    }
+    return hi * 64;
 }
 
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
@@ -500,7 +529,8 @@ int32_t rlx_cache_set_stream(void *h, void *stream) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     HIP_TRY(hipStreamSynchronize(c->stream));
-    c->stream = stream ? (hipStream_t)stream : c->own;
+    // NULL is the device's null stream (torch's default stream reports 0).
+    c->stream = (hipStream_t)stream;
     return RLX_OK;
 }
 
@@ -668,18 +698,17 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
     const int G = num_heads / c->kvh;
     LayerState &ls = c->L[layer];
-    int64_t total_tok = 0;
-    int max_len = 0, max_nq = 0;
+    std::vector<int> lens(n_seqs);
+    int max_nq = 0;
     for (int i = 0; i < n_seqs; i++) {
-        total_tok += ls.seqs[seq_ids[i]].len;
-        max_len = std::max(max_len, ls.seqs[seq_ids[i]].len);
+        lens[i] = ls.seqs[seq_ids[i]].len;
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = G * max_nq;
     if (max_qr > 32)
         return fail(RLX_ERR_UNSUPPORTED, "%d query rows per kv head (decode kernel handles <= 32)", max_qr);
     const int nqt = max_qr > 16 ? 2 : 1;
-    const int chunk = choose_chunk(total_tok, c->kvh, std::max(max_len, 1));
+    const int chunk = choose_chunk(lens, c->kvh, (int64_t)c->cus * gqa_decode_wgs_per_cu(c->hd, nqt));
     std::vector<AttRow> rows;
     std::vector<int2> work;
     int total_q = 0, mnq = 0, parts = 0;
@@ -704,7 +733,7 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                               q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
                               chunk, qscale, mask_mode, nqt, (float *)c->ws,
                               (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
-                              e0, e1));
+                              max_qr, e0, e1));
     return RLX_OK;
 }
 
@@ -718,27 +747,27 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     int32_t rc = check_layer(c, layer, false);
     if (rc) return rc;
     if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
-    if (num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
-        return fail(RLX_ERR_INVALID, "num_heads=%d head_dim=%d", num_heads, head_dim);
+    if (num_heads <= 0 || head_dim <= 0 || head_dim % 64 != 0 || head_dim > 256)
+        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim in {64,128,192,256})",
+                    num_heads, head_dim);
     if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
     if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
     if (n_seqs == 0) return RLX_OK;
     if (!q_nope || !q_rope || !w_uk || !w_uv || !out) return fail(RLX_ERR_INVALID, "null operand");
     LayerState &ls = c->L[layer];
-    int64_t total_tok = 0;
-    int max_len = 0, max_nq = 0;
+    std::vector<int> lens(n_seqs);
+    int max_nq = 0;
     for (int i = 0; i < n_seqs; i++) {
-        total_tok += ls.seqs[seq_ids[i]].len;
-        max_len = std::max(max_len, ls.seqs[seq_ids[i]].len);
+        lens[i] = ls.seqs[seq_ids[i]].len;
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = num_heads * max_nq;
     if (max_qr > 32)
         return fail(RLX_ERR_UNSUPPORTED, "%d query rows (heads x queries) per sequence (decode kernel handles <= 32)", max_qr);
     const int nqt = max_qr > 16 ? 2 : 1;
-    // One work-group covers all heads, so weigh a token 16 heads' worth less.
-    const int chunk = choose_chunk(total_tok, 1, std::max(max_len, 1));
+    // One work-group covers every head of a sequence's split.
+    const int chunk = choose_chunk(lens, 1, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
     std::vector<AttRow> rows;
     std::vector<int2> work;
     int total_q = 0, mnq = 0, parts = 0;
@@ -748,8 +777,9 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const int QRP = 16 * nqt;
     const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
     const size_t po_bytes = (size_t)parts * QRP * kMlaDc * sizeof(float);
-    const size_t pm_bytes = (size_t)parts * QRP * 2 * sizeof(float);
-    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes))) return rc;
+    const size_t pm_bytes = ((size_t)parts * QRP * 2 * sizeof(float) + 255) & ~(size_t)255;
+    const size_t ol_bytes = (size_t)total_q * num_heads * kMlaDc * sizeof(float);
+    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes + ol_bytes))) return rc;
     Blob b;
     size_t o_r = b.add(rows), o_w = b.add(work);
     void *dev;
@@ -764,7 +794,8 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                               q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
                               (const uint16_t *)w_uv, num_heads, head_dim, total_q, max_nq, c->P,
                               chunk, qscale, mask_mode, nqt, (uint16_t *)ws,
-                              (float *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes), out,
+                              (float *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes),
+                              (float *)(ws + ql_bytes + po_bytes + pm_bytes), out,
                               out_dtype == RLX_BF16, e0, e1));
     return RLX_OK;
 }

@@ -21,6 +21,7 @@ pytestmark = pytest.mark.gpu
 
 TOL_ORACLE = (2e-2, 2e-3)
 TOL_EXACT = (1e-2, 1e-3)
+TOL_MLA_EXACT = (5e-3, 5e-4)
 
 
 def _check(got, want, tol, what):
@@ -238,8 +239,9 @@ def test_mla_attend_matches_oracle(gpu, H, lens, nq, mask):
         qri = qr[off:off + nqs[i]].transpose(1, 0, 2)
         got = out[off:off + nqs[i]].transpose(1, 0, 2)
         exact = _mla_exact(qci, qri, cs, ks, w_uk, w_uv, _limits(mask, nqs[i], L))
-        # outputs are ~0.02-scale (W_UV N(0,0.02)): judge relative to that scale
-        _check(got / 0.1, exact / 0.1, TOL_EXACT, f"seq {i} len {L} vs exact (x10)")
+        # Outputs are ~0.05-0.5 (W_UV N(0,0.02) over 512 channels); short
+        # contexts see the bf16 rounding of P and q_lat at ~2e-3 absolute.
+        _check(got, exact, TOL_MLA_EXACT, f"seq {i} len {L} vs exact")
         if L >= 200:
             ref = oracle.mla_attend(qci, qri, cs, ks, w_uk, w_uv, mask)
             _check(got, ref, TOL_ORACLE, f"seq {i} len {L} vs oracle")
@@ -270,4 +272,4 @@ def test_mla_config3_full_shape(gpu):
         s = (qlat @ cc.T + qr[i] @ kk.T) / math.sqrt(D + 64)
         w = torch.softmax(s, dim=-1)
         ref = torch.einsum("hc,chd->hd", w @ cc, Wv)
-        _check(out[i].cpu().numpy() / 0.1, ref.cpu().numpy() / 0.1, TOL_EXACT, f"seq {i} (x10)")
+        _check(out[i].cpu().numpy(), ref.cpu().numpy(), TOL_MLA_EXACT, f"seq {i}")
