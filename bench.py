@@ -286,6 +286,12 @@ def main():
                               "kernel_gbs": round(s["kernel_gbs"], 1),
                               "kernel_frac_of_8TBs": round(s["kernel_gbs"] / HBM_PEAK_GBS, 4),
                               "step_hbm_gbs": round(s["step_hbm_gbs"], 1)})
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        t = json.load(open(tpath)).get(args.workload)
+        if t and t.get("kernel") == r["kernel"]:
+            traffic = t["fetch_bytes"] + t["write_bytes"]
     cpu = None
     if not args.no_cpu:
         cfg = WORKLOADS[args.workload]
@@ -308,7 +314,7 @@ def main():
         "hbm_frac": round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": r["kernel"],
+                     "traffic": traffic, "kernel": r["kernel"],
                      "kernel_avg_us": round(r["kernel_avg_us"], 2),
                      "algorithmic_bytes": r["kernel_bytes"]},
         "cpu_baseline": cpu,
