@@ -34,7 +34,10 @@ WORKLOADS = {
     "gqa_cfg2": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=None, layers=8),
     # BASELINE config 3 (headline, 8k context): MLA latent decode
     "mla8k": dict(kind="mla", B=32, H=16, D=128, P=64, T=8192, layers=4),
+    # MLA chunked prefill, 2048 new tokens on 6144 cached
+    "mla_prefill": dict(kind="mla_prefill", B=4, H=128, D=128, P=64, T=6144, n_new=2048, layers=1),
 }
+MFMA_BF16_PEAK_TFS = 2500.0
 
 
 def _lens(cfg, rng):
@@ -135,11 +138,51 @@ def setup_mla(cfg, torch, dev, rng):
     return c, step, B, kernel_bytes, step_bytes, desc, "mla_decode_kernel", lens
 
 
+def setup_mla_prefill(cfg, torch, dev, rng):
+    """Config 4: each step appends a 2048-token chunk to every sequence's
+    6144-token latent cache, runs causal chunked-prefill attention for the
+    chunk (latents expanded per head, FA2 over 8192 keys) and rolls the chunk
+    back.  FLOPs are declared in the decompressed form the kernels execute."""
+    from relux_amd import MLACache
+    B, H, D, P, T0, n = cfg["B"], cfg["H"], cfg["D"], cfg["P"], cfg["T"], cfg["n_new"]
+    lens = [T0] * B
+    c = MLACache(num_layers=1, max_len=T0 + n + P, page_tokens=P, max_seqs=B,
+                 pool_pages=B * (-(-(T0 + n) // P)) + 8, device=dev.index)
+
+    def app(order, cnt):
+        c.Append(0, torch.randn(sum(cnt), 512, device=dev, dtype=torch.bfloat16),
+                 torch.randn(sum(cnt), 64, device=dev, dtype=torch.bfloat16), seq_ids=order, n_tok=cnt)
+    _fill_interleaved(app, lens, P, rng)
+    seqs = list(range(B))
+    cn = torch.randn(B * n, 512, device=dev, dtype=torch.bfloat16)
+    krn = torch.randn(B * n, 64, device=dev, dtype=torch.bfloat16)
+    qn = torch.randn(B * n, H, D, device=dev, dtype=torch.bfloat16)
+    qr = torch.randn(B * n, H, 64, device=dev, dtype=torch.bfloat16)
+    w_uk = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    w_uv = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    out = torch.empty(B * n, H, D, device=dev, dtype=torch.bfloat16)
+    nts = [n] * B
+
+    def step(i):
+        c.Append(0, cn, krn, seq_ids=seqs, n_tok=nts)
+        c.Attend(0, qn, qr, w_uk, w_uv, H, D, seq_ids=seqs, n_q=nts, out=out)
+        c.Rollback(seqs, nts)
+
+    pairs = B * sum(T0 + 1 + i for i in range(n))
+    attn_flops = pairs * H * (D + 64 + D) * 2
+    expand_flops = B * (T0 + n) * 2 * 512 * H * D * 2
+    desc = {"workload": f"mla_chunked_prefill B{B} H{H} dC512 dR64 D{D} P{P} T0{T0}+{n} causal",
+            "batch": B, "heads": H, "cached": T0, "chunk": n,
+            "flops_attention": attn_flops, "flops_expand": expand_flops,
+            "flops_declared": attn_flops + expand_flops, "form": "decompressed"}
+    return c, step, B * n, attn_flops, attn_flops + expand_flops, desc, "prefill_kernel<192,128,dense>", lens
+
+
 def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
-    rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3}[name])
-    setup = setup_gqa if cfg["kind"] == "gqa" else setup_mla
+    rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4}[name])
+    setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
@@ -157,7 +200,13 @@ def run_workload(name, steps, warmup, torch, dev):
     c.Timing(False)
     kavg_s = kms / max(kn, 1) / 1e3
     achieved = kbytes / kavg_s / 1e9
+    mfma = cfg["kind"] == "mla_prefill"  # compute-bound: kbytes holds FLOPs
     res = {
+        "bound": "mfma" if mfma else "hbm",
+        "kernel_rate": kbytes / kavg_s / (1e12 if mfma else 1e9),
+        "rate_unit": "TFLOP/s" if mfma else "GB/s",
+        "rate_frac": kbytes / kavg_s / (1e12 * MFMA_BF16_PEAK_TFS if mfma else 1e9 * HBM_PEAK_GBS),
+        "step_tflops": sbytes * steps / elapsed / 1e12 if mfma else None,
         "tokens_per_s": B * steps / elapsed,
         "ms_per_step": elapsed / steps * 1e3,
         "step_hbm_gbs": sbytes * steps / elapsed / 1e9,
@@ -273,19 +322,25 @@ def main():
           file=sys.stderr, flush=True)
     r = run_workload(args.workload, args.steps, args.warmup, torch, dev)
     print(f"[bench] {args.workload}: {r['tokens_per_s']:.0f} tok/s, kernel {r['kernel_avg_us']:.1f} us, "
-          f"{r['kernel_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+          f"{r['kernel_rate']:.0f} {r['rate_unit']}", file=sys.stderr, flush=True)
     secondary = []
     if not args.no_secondary:
-        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k") if w != args.workload]:
-            s = run_workload(name, max(50, args.steps // 2), args.warmup, torch, dev)
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill") if w != args.workload]:
+            n_steps = 8 if name == "mla_prefill" else max(50, args.steps // 2)
+            s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)
             print(f"[bench] {name}: {s['tokens_per_s']:.0f} tok/s, kernel {s['kernel_avg_us']:.1f} us, "
-                  f"{s['kernel_gbs']:.0f} GB/s", file=sys.stderr, flush=True)
-            secondary.append({"workload": s["desc"]["workload"], "tokens_per_s": round(s["tokens_per_s"], 1),
-                              "ms_per_step": round(s["ms_per_step"], 4),
-                              "kernel": s["kernel"], "kernel_avg_us": round(s["kernel_avg_us"], 2),
-                              "kernel_gbs": round(s["kernel_gbs"], 1),
-                              "kernel_frac_of_8TBs": round(s["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                              "step_hbm_gbs": round(s["step_hbm_gbs"], 1)})
+                  f"{s['kernel_rate']:.0f} {s['rate_unit']}", file=sys.stderr, flush=True)
+            entry = {"workload": s["desc"]["workload"], "tokens_per_s": round(s["tokens_per_s"], 1),
+                     "ms_per_step": round(s["ms_per_step"], 4), "steps": n_steps,
+                     "kernel": s["kernel"], "kernel_avg_us": round(s["kernel_avg_us"], 2),
+                     "bound": s["bound"], "kernel_rate": round(s["kernel_rate"], 1),
+                     "rate_unit": s["rate_unit"], "kernel_frac_of_peak": round(s["rate_frac"], 4)}
+            if s["bound"] == "hbm":
+                entry["step_hbm_gbs"] = round(s["step_hbm_gbs"], 1)
+            else:
+                entry["step_tflops_declared"] = round(s["step_tflops"], 1)
+                entry["flops_declared"] = s["desc"]["flops_declared"]
+            secondary.append(entry)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
@@ -295,7 +350,10 @@ def main():
     cpu = None
     if not args.no_cpu:
         cfg = WORKLOADS[args.workload]
-        cpu = (cpu_baseline_gqa if cfg["kind"] == "gqa" else cpu_baseline_mla)(cfg, r["lens"])
+        if cfg["kind"] == "gqa":
+            cpu = cpu_baseline_gqa(cfg, r["lens"])
+        elif cfg["kind"] == "mla":
+            cpu = cpu_baseline_mla(cfg, r["lens"])
     line = {
         "metric": "decode attn tokens/s + achieved HBM GB/s (% of 8 TB/s) at 1 MI355X, 8k ctx",
         "value": round(r["tokens_per_s"], 1),
@@ -312,8 +370,9 @@ def main():
         "config": r["desc"],
         "hbm_gbs": round(r["step_hbm_gbs"], 1),
         "hbm_frac": round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(r["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": r["bound"], "achieved": round(r["kernel_rate"], 1),
+                     "peak": HBM_PEAK_GBS if r["bound"] == "hbm" else MFMA_BF16_PEAK_TFS,
+                     "unit": r["rate_unit"], "frac": round(r["rate_frac"], 4),
                      "traffic": traffic, "kernel": r["kernel"],
                      "kernel_avg_us": round(r["kernel_avg_us"], 2),
                      "algorithmic_bytes": r["kernel_bytes"]},

@@ -123,6 +123,34 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
                              int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1);
 
+// Sources of the prefill kernel: the paged GQA cache, or (MLA) per-sequence
+// decompressed K_c / V^T plus rope keys from the paged latent rows.
+constexpr int kSrcPaged = 0;
+constexpr int kSrcDense = 1;
+
+struct PrefillArgs {
+    const uint16_t *kpool;  // paged: K row pages; dense: latent pool (rope keys)
+    const uint16_t *vpool;  // paged: V dim-major pages
+    const uint16_t *kc;     // dense: K_c [H][Tp][128], sequence s at + part*H*128
+    const uint16_t *vt;     // dense: V^T [H][128][Tp], same sequence offsets
+    const int32_t *table;
+    const AttRow *rows;     // dense: part = token offset of the sequence, nsplit = Tp
+    const int4 *work;       // (row, head group, query tile, unused)
+    const void *q;          // paged: [rows][H][D]; dense: q_nope [rows][H][128]
+    const void *q2;         // dense: q_rope [rows][H][64]
+    void *out;
+    int q_bf16, layout, out_bf16, mask_mode;
+    int H, KVH, P;
+    float qscale;
+};
+
+hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, int n_work,
+                          hipEvent_t ev0, hipEvent_t ev1);
+hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, const int2 *work, int n_work, const uint16_t *w_uk,
+                             const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
+                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt);
+
 // Work-groups of the decode kernels one CU holds at once (occupancy).
 int gqa_decode_wgs_per_cu(int hd, int nqt);
 int mla_decode_wgs_per_cu(int nqt);

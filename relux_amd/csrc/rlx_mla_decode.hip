@@ -227,6 +227,9 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
 #pragma unroll
                 for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
             }
+            // The P.V product consumes bf16 weights: normalise by the same ones.
+#pragma unroll
+            for (int i = 0; i < 4; i++) p[i] = bf16_f32(bf16_rne(p[i]));
             l_part[nt] = l_part[nt] * c + ((p[0] + p[1]) + (p[2] + p[3]));
             m_run[nt] = m_new;
 #pragma unroll

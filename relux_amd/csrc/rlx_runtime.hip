@@ -705,8 +705,49 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = G * max_nq;
-    if (max_qr > 32)
-        return fail(RLX_ERR_UNSUPPORTED, "%d query rows per kv head (decode kernel handles <= 32)", max_qr);
+    if (max_qr > 32) {
+        // Chunked prefill / long verify: FA2 tiles of 128 query rows.
+        if (128 % G != 0)
+            return fail(RLX_ERR_UNSUPPORTED, "prefill needs 128 %% (heads per kv head = %d) == 0", G);
+        std::vector<AttRow> rows;
+        std::vector<int2> unused;
+        int total_q = 0, mnq = 0, parts = 0;
+        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
+            return rc;
+        const int toks = 128 / G;
+        std::vector<int4> work;
+        for (int i = 0; i < n_seqs; i++) {
+            const int tiles = (rows[i].nq + toks - 1) / toks;
+            for (int kvh = 0; kvh < c->kvh; kvh++)
+                for (int qt = tiles - 1; qt >= 0; qt--) work.push_back(int4{i, kvh, qt, 0});
+        }
+        if ((rc = flush_patches(c))) return rc;
+        Blob b;
+        size_t o_r = b.add(rows), o_w = b.add(work);
+        void *dev;
+        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+        PrefillArgs a{};
+        a.kpool = ls.pool0;
+        a.vpool = ls.pool1;
+        a.table = c->d_table;
+        a.rows = (const AttRow *)((char *)dev + o_r);
+        a.work = (const int4 *)((char *)dev + o_w);
+        a.q = q;
+        a.out = out;
+        a.q_bf16 = q_dtype == RLX_BF16;
+        a.layout = qo_layout;
+        a.out_bf16 = out_dtype == RLX_BF16;
+        a.mask_mode = mask_mode;
+        a.H = num_heads;
+        a.KVH = c->kvh;
+        a.P = c->P;
+        a.qscale = scale * 1.4426950408889634f;
+        hipEvent_t e0, e1;
+        if ((rc = timing_events(c, &e0, &e1))) return rc;
+        HIP_TRY(launch_prefill(c->stream, kSrcPaged, c->hd, a, (int)work.size(), e0, e1));
+        return RLX_OK;
+    }
     const int nqt = max_qr > 16 ? 2 : 1;
     const int chunk = choose_chunk(lens, c->kvh, (int64_t)c->cus * gqa_decode_wgs_per_cu(c->hd, nqt));
     std::vector<AttRow> rows;
@@ -763,8 +804,71 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = num_heads * max_nq;
-    if (max_qr > 32)
-        return fail(RLX_ERR_UNSUPPORTED, "%d query rows (heads x queries) per sequence (decode kernel handles <= 32)", max_qr);
+    if (max_qr > 32) {
+        // Chunked prefill: expand the latents into per-head K_c / V^T, then
+        // FA2 tiles of 128 query tokens per head.
+        if (head_dim != 128)
+            return fail(RLX_ERR_UNSUPPORTED, "MLA prefill supports head_dim 128 (got %d)", head_dim);
+        std::vector<AttRow> rows;
+        std::vector<int2> unused;
+        int total_q = 0, mnq = 0, parts = 0;
+        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
+            return rc;
+        std::vector<int2> dwork;
+        std::vector<int4> pwork;
+        int64_t tok_off = 0;
+        for (int i = 0; i < n_seqs; i++) {
+            const int Tp = (rows[i].len + 127) / 128 * 128;
+            rows[i].part = (int32_t)tok_off;  // token offset in the expanded buffers
+            rows[i].nsplit = Tp;              // padded length (row pitch of V^T)
+            for (int t0 = 0; t0 < Tp; t0 += 128) dwork.push_back(int2{i, t0});
+            const int tiles = (rows[i].nq + 127) / 128;
+            for (int h = 0; h < num_heads; h++)
+                for (int qt = tiles - 1; qt >= 0; qt--) pwork.push_back(int4{i, h, qt, 0});
+            tok_off += Tp;
+        }
+        if (tok_off * num_heads * 128 > INT32_MAX)
+            return fail(RLX_ERR_UNSUPPORTED, "MLA prefill call too large (%lld expanded rows)", (long long)tok_off);
+        if ((rc = flush_patches(c))) return rc;
+        const size_t w_bytes = (size_t)num_heads * 128 * kMlaDc * 2;
+        const size_t e_bytes = (size_t)tok_off * num_heads * 128 * 2;
+        if ((rc = ensure_ws(c, 2 * w_bytes + 2 * e_bytes))) return rc;
+        Blob b;
+        size_t o_r = b.add(rows), o_d = b.add(dwork), o_p = b.add(pwork);
+        void *dev;
+        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+        char *ws = (char *)c->ws;
+        uint16_t *wt_k = (uint16_t *)ws, *wt_v = (uint16_t *)(ws + w_bytes);
+        uint16_t *kc = (uint16_t *)(ws + 2 * w_bytes), *vt = (uint16_t *)(ws + 2 * w_bytes + e_bytes);
+        const AttRow *drows = (const AttRow *)((char *)dev + o_r);
+        HIP_TRY(launch_mla_expand(c->stream, ls.pool0, c->d_table, drows,
+                                  (const int2 *)((char *)dev + o_d), (int)dwork.size(),
+                                  (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
+                                  c->P, wt_k, wt_v, kc, vt));
+        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
+        PrefillArgs a{};
+        a.kpool = ls.pool0;
+        a.kc = kc;
+        a.vt = vt;
+        a.table = c->d_table;
+        a.rows = drows;
+        a.work = (const int4 *)((char *)dev + o_p);
+        a.q = q_nope;
+        a.q2 = q_rope;
+        a.out = out;
+        a.q_bf16 = q_dtype == RLX_BF16;
+        a.layout = RLX_LAYOUT_SHD;
+        a.out_bf16 = out_dtype == RLX_BF16;
+        a.mask_mode = mask_mode;
+        a.H = num_heads;
+        a.KVH = num_heads;
+        a.P = c->P;
+        a.qscale = scale * 1.4426950408889634f;
+        hipEvent_t e0, e1;
+        if ((rc = timing_events(c, &e0, &e1))) return rc;
+        HIP_TRY(launch_prefill(c->stream, kSrcDense, head_dim, a, (int)pwork.size(), e0, e1));
+        return RLX_OK;
+    }
     const int nqt = max_qr > 16 ? 2 : 1;
     // One work-group covers every head of a sequence's split.
     const int chunk = choose_chunk(lens, 1, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
