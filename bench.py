@@ -36,6 +36,10 @@ WORKLOADS = {
     "mla8k": dict(kind="mla", B=32, H=16, D=128, P=64, T=8192, layers=4),
     # MLA chunked prefill, 2048 new tokens on 6144 cached
     "mla_prefill": dict(kind="mla_prefill", B=4, H=128, D=128, P=64, T=6144, n_new=2048, layers=1),
+    # speculative verify stress, 4 drafts, rollback U{0..4},
+    # evict oldest 25% of pages + compact every 256 steps
+    "spec_stress": dict(kind="spec", B=64, H=64, KVH=8, D=128, P=16, drafts=4, evict_every=256,
+                        layers=1),
 }
 MFMA_BF16_PEAK_TFS = 2500.0
 
@@ -178,17 +182,76 @@ def setup_mla_prefill(cfg, torch, dev, rng):
     return c, step, B * n, attn_flops, attn_flops + expand_flops, desc, "prefill_kernel<192,128,dense>", lens
 
 
+def setup_spec(cfg, torch, dev, rng, max_steps=4096):
+    """Config 5: every step appends `drafts` tokens to each of 64 sequences,
+    verifies them with causal multi-query decode attention (4 drafts x 8
+    query heads = 32 rows per kv head), rolls back a rejected suffix of
+    U{0..drafts} tokens, and every `evict_every` steps evicts the oldest 25%
+    of each sequence's full pages and compacts the page table."""
+    import numpy as np
+    from relux_amd import KVCache
+    B, H, KVH, D, P, nd = cfg["B"], cfg["H"], cfg["KVH"], cfg["D"], cfg["P"], cfg["drafts"]
+    lens = [int(x) for x in np.exp(rng.uniform(np.log(1024), np.log(32768), size=B))]
+    grow = nd * 400  # headroom for the longest timed run between evictions
+    c = KVCache(num_layers=1, max_len=max(lens) + grow + P, num_kv_heads=KVH, head_dim=D,
+                page_tokens=P, max_seqs=B,
+                pool_pages=sum(-(-(T + grow) // P) for T in lens) + 8, device=dev.index)
+
+    def app(order, n):
+        k = torch.randn(sum(n), KVH, D, device=dev, dtype=torch.bfloat16)
+        c.Append(0, k, torch.randn_like(k), seq_ids=order, n_tok=n, layout="SHD")
+    _fill_interleaved(app, lens, P, rng)
+    seqs = list(range(B))
+    kd = torch.randn(B * nd, KVH, D, device=dev, dtype=torch.bfloat16)
+    vd = torch.randn(B * nd, KVH, D, device=dev, dtype=torch.bfloat16)
+    q = torch.randn(B * nd, H, D, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(B * nd, H, D, device=dev, dtype=torch.bfloat16)
+    drafts = [nd] * B
+    rejects = rng.integers(0, nd + 1, size=(max_steps, B))
+    state = {"lens": np.array(lens, dtype=np.int64), "attended": 0, "steps": 0, "evictions": 0}
+
+    def step(i):
+        c.Append(0, kd, vd, seq_ids=seqs, n_tok=drafts, layout="SHD")
+        state["attended"] += int((state["lens"] + nd).sum())
+        state["steps"] += 1
+        c.Attend(0, q, H, seq_ids=seqs, n_q=drafts, out=out)
+        r = rejects[i % max_steps]
+        c.Rollback(seqs, [int(x) for x in r])
+        state["lens"] += nd - r
+        if (i + 1) % cfg["evict_every"] == 0:
+            ev = [int((L // P) // 4) for L in state["lens"]]
+            c.Evict(seqs, ev)
+            c.Compact()
+            state["lens"] -= np.array(ev) * P
+            state["evictions"] += 1
+
+    mean_ctx = float(np.mean(lens))
+    kv_bytes = sum(T + nd for T in lens) * KVH * D * 2 * 2
+    kernel_bytes = kv_bytes + B * nd * H * D * 2 + sum(-(-(T + nd) // P) for T in lens) * 4
+    desc = {"workload": f"spec_verify_stress B{B} H{H} KVH{KVH} D{D} P{P} T~logU[1k,32k] "
+                        f"drafts{nd} rollback~U{{0..{nd}}} evict25%/{cfg['evict_every']}",
+            "batch": B, "query_heads": H, "kv_heads": KVH, "drafts": nd,
+            "context_mean_start": mean_ctx, "state": state}
+    return c, step, B * nd, kernel_bytes, kernel_bytes, desc, "gqa_decode_kernel<128,2>", lens
+
+
 def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
-    rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4}[name])
-    setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill}[cfg["kind"]]
+    rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
+                                 "spec_stress": 5}[name])
+    setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
+             "spec": setup_spec}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
         step(i)
     c.Sync()
     torch.cuda.synchronize(dev)
+    st = desc.get("state")
+    if st is not None:  # context lengths drift: count what the timed steps attend
+        st["attended"] = 0
+        st["steps"] = 0
     c.Timing(True)
     t0 = time.perf_counter()
     for i in range(steps):
@@ -199,6 +262,13 @@ def run_workload(name, steps, warmup, torch, dev):
     kms, kn = c.KernelTime()
     c.Timing(False)
     kavg_s = kms / max(kn, 1) / 1e3
+    if st is not None and st["steps"]:
+        per_step_tokens = st["attended"] / st["steps"]
+        extra = kbytes - sum(T + cfg["drafts"] for T in lens) * cfg["KVH"] * cfg["D"] * 4
+        kbytes = sbytes = int(per_step_tokens * cfg["KVH"] * cfg["D"] * 4 + extra)
+        desc["context_mean_timed"] = per_step_tokens / cfg["B"] - cfg["drafts"]
+        desc["evictions_timed"] = st["evictions"]
+        desc = {k: v for k, v in desc.items() if k != "state"}
     achieved = kbytes / kavg_s / 1e9
     mfma = cfg["kind"] == "mla_prefill"  # compute-bound: kbytes holds FLOPs
     res = {
@@ -325,8 +395,10 @@ def main():
           f"{r['kernel_rate']:.0f} {r['rate_unit']}", file=sys.stderr, flush=True)
     secondary = []
     if not args.no_secondary:
-        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill") if w != args.workload]:
-            n_steps = 8 if name == "mla_prefill" else max(50, args.steps // 2)
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress")
+                     if w != args.workload]:
+            # spec_stress: 300 timed steps after the warm-up cross one evict + compact
+            n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
             s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)
             print(f"[bench] {name}: {s['tokens_per_s']:.0f} tok/s, kernel {s['kernel_avg_us']:.1f} us, "
                   f"{s['kernel_rate']:.0f} {s['rate_unit']}", file=sys.stderr, flush=True)

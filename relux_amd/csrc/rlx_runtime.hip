@@ -332,29 +332,55 @@ int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
         return e ? (int64_t)atoll(e) : (int64_t)0;
     }();
     if (slot_override > 0) slots = slot_override;
+    static const int chunk_override = [] {
+        const char *e = getenv("RLX_DECODE_CHUNK");  // tuning override
+        return e ? atoi(e) : 0;
+    }();
     int max_len = 1;
     for (int L : lens) max_len = std::max(max_len, L);
     auto r64 = [](int64_t x) { return (int)((x + 63) / 64 * 64); };
     const int lo_chunk = std::max(64, r64(((int64_t)max_len + kMaxSplits - 1) / kMaxSplits));
     const int hi_chunk = std::max(lo_chunk, r64(max_len));
+    if (chunk_override > 0) return std::min(hi_chunk, std::max(lo_chunk, r64(chunk_override)));
     auto count = [&](int ch) {
         int64_t n = 0;
         for (int L : lens) n += (L + ch - 1) / ch;
         return n * units;
     };
-    int64_t target = slots;
-    if (count(hi_chunk) > slots) target = 4 * slots;
-    if (count(lo_chunk) <= target) return lo_chunk;
-    if (count(hi_chunk) > target) return hi_chunk;
-    int lo = lo_chunk / 64, hi = hi_chunk / 64;  // count(lo) > target >= count(hi)
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) / 2;
-        if (count(mid * 64) <= target)
-            hi = mid;
-        else
-            lo = mid;
+    // Cost model in token units per slot: a work-group costs its tokens plus
+    // a fixed c0 (Q load, wave merge, partial write); one residency round
+    // lasts as long as its largest split; several rounds cost the average
+    // per-slot work plus one split of tail.
+    constexpr double c0 = 400.0;
+    double work = 0.0;
+    for (int L : lens) work += (double)L * units;
+    int best = hi_chunk;
+    double best_est = 1e300;
+    if (count(hi_chunk) <= slots) {
+        int lo = lo_chunk / 64, hi = hi_chunk / 64;
+        if (count(lo_chunk) <= slots) {
+            hi = lo;
+        } else {
+            while (hi - lo > 1) {  // smallest split that still fits one round
+                const int mid = (lo + hi) / 2;
+                if (count(mid * 64) <= slots)
+                    hi = mid;
+                else
+                    lo = mid;
+            }
+        }
+        best = hi * 64;
+        best_est = best + c0;
     }
-    return hi * 64;
+    for (int ch = 256; ch <= hi_chunk; ch *= 2) {
+        if (ch < lo_chunk) continue;
+        const double est = (work + c0 * (double)count(ch)) / (double)slots + ch + c0;
+        if (est < best_est) {
+            best_est = est;
+            best = ch;
+        }
+    }
+    return best;
 }
 
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
