@@ -67,6 +67,9 @@ def lib():
                                 _i, _i, _f32p], None),
             "orc_ref_gqa_decode_step": ([_u16p, _u16p, _i, _i, _f32p, _f32p, _f32p, _i, _i, _i,
                                          _f32p], _i),
+            "orc_rmsnorm": ([_f32p, _u16p, ctypes.c_float, _i, _i, _f32p], None),
+            "orc_gelu_n": ([_f32p, _f32p, _i64], None),
+            "orc_add_bias": ([_f32p, _u16p, _i, _i], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -155,6 +158,38 @@ def rope_apply(x, start_pos, tables, max_seq):
     if rc != 0:
         raise IndexError("RotaryEmbedding.Apply: position >= maxSeqLen")
     return out
+
+
+def matmul_bf16w(a, w_bf16):
+    """matmulBatched3D pure-Go branch (mha.go:774-784): a[M,K] @ widen(w[K,N])."""
+    a = _f32(a)
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    M, K = a.shape
+    N = w.shape[1]
+    out = np.empty((M, N), np.float32)
+    lib().orc_matmul_bf16w(out, a, w, M, K, N)
+    return out
+
+
+def rmsnorm(x, gamma_bf16, eps=1e-5):
+    x = _f32(x)
+    rows, d = x.shape
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(x, np.ascontiguousarray(gamma_bf16, np.uint16), eps, rows, d, out)
+    return out
+
+
+def gelu(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_gelu_n(x.reshape(-1), y.reshape(-1), x.size)
+    return y
+
+
+def add_bias(y, b_bf16):
+    y = _f32(y).copy()
+    lib().orc_add_bias(y, np.ascontiguousarray(b_bf16, np.uint16), y.shape[0], y.shape[1])
+    return y
 
 
 def kv_copy_into(dst, src, start_row, seq_len, row_size):

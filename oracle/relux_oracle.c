@@ -281,3 +281,34 @@ int orc_ref_gqa_decode_step(uint16_t *kbuf, uint16_t *vbuf, int cap, int len, co
     free(kw); free(vw); free(ke); free(ve);
     return T;
 }
+
+/* rmsnorm.go:69-116 -- per row: sumSq ascending in f32, meanSq = sumSq/f32(d),
+ * rstd = f32(1/sqrt(f64(meanSq + eps))), out = (x*rstd)*gamma. */
+void orc_rmsnorm(const float *x, const uint16_t *gamma, float eps, int rows, int d, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (int64_t)r * d;
+        float sum = 0.0f;
+        for (int j = 0; j < d; j++) sum += xr[j] * xr[j];
+        float mean = sum / (float)d;
+        float rstd = (float)(1.0 / sqrt((double)(mean + eps)));
+        for (int j = 0; j < d; j++) {
+            volatile float t = xr[j] * rstd;
+            out[(int64_t)r * d + j] = t * orc_f32_from_bf16(gamma[j]);
+        }
+    }
+}
+
+/* mlp.go:448-451 -- 0.5*x*(1 + f32(erf(f64(x)/sqrt2))), f32 products. */
+void orc_gelu_n(const float *x, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        float e = (float)erf((double)x[i] / 1.4142135623730951);
+        volatile float h = 0.5f * x[i];
+        y[i] = h * (1.0f + e);
+    }
+}
+
+/* linear.go:65-106 and the bias adds of mlp.go:103-140 -- y[i][j] += f32(bf16 b[j]). */
+void orc_add_bias(float *y, const uint16_t *b, int rows, int cols) {
+    for (int i = 0; i < rows; i++)
+        for (int j = 0; j < cols; j++) y[(int64_t)i * cols + j] += orc_f32_from_bf16(b[j]);
+}

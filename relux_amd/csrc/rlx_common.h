@@ -62,6 +62,8 @@ struct AttRow {
     int32_t qrow;    // first call-row of this sequence's queries / outputs
     int32_t nsplit;  // context splits
     int32_t part;    // first partial slot of this sequence
+    int32_t q0;      // GQA decode query tiling: first query of this row ...
+    int32_t qn;      // ... and its query count (q0 = 0, qn = nq untiled)
 };
 
 // Upper bound on context splits of one sequence (the runtime sizes splits so

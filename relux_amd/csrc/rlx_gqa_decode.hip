@@ -48,8 +48,12 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const int2 *__restrict__ work, const void *__restrict__ q, int q_bf16, int layout, int H,
     int KVH, int P, int chunk, float qscale, int mask_mode, float *__restrict__ part_o,
     float *__restrict__ part_ml) {
-    constexpr int KS = D / 32;  // QK k-steps
-    constexpr int MT = D / 16;  // PV m-tiles
+    // head_dim 16 holds only 4 dims per lane: its score step is one MFMA
+    // 16x16x16 (4 bf16 per lane); wider heads use 16x16x32 k-steps.
+    constexpr bool K16 = (D == 16);
+    constexpr int KS = K16 ? 1 : D / 32;  // QK k-steps
+    constexpr int KW = K16 ? 4 : 8;       // dims per lane per k-step
+    constexpr int MT = D / 16;            // PV m-tiles
     constexpr int QRP = 16 * NQT;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -59,49 +63,46 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const AttRow R = rows[wk.x];
     const int kvh = blockIdx.y;
     const int G = H / KVH;
-    const int QR = G * R.nq;
+    const int QR = G * R.qn;  // query rows of this (tile of a) sequence
     const int t_begin = wk.y * chunk;
     const int t_end = min(R.len, t_begin + chunk);
 
-    // Q^T operand (B of the score product), pre-scaled by scale*log2(e).
-    bf16x8 qb[NQT][KS];
+    // Q^T operand (B of the score product), pre-scaled by scale*log2(e);
+    // KW consecutive dims per lane (the upper half stays zero when KW = 4).
+    u32x4 qb[NQT][KS];
     int klim[NQT];
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++) {
         const int qr = nt * 16 + col;
         klim[nt] = R.len - 1;
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qb[nt][ks] = u32x4{0, 0, 0, 0};
         if (qr < QR) {
-            const int qi = qr / G;
-            const int h = kvh * G + (qr - qi * G);
+            const int ql = qr / G;
+            const int h = kvh * G + (qr - ql * G);
+            const int qi = R.q0 + ql;
             klim[nt] = key_limit(mask_mode, R.len, R.nq, qi);
             const int64_t base = (layout == kLayoutSHD)
                                      ? ((int64_t)(R.qrow + qi) * H + h) * D
                                      : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D;
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
-                const int64_t off = base + ks * 32 + grp * 8;
-                u32x4 w;
+                const int64_t off = base + ks * 32 + grp * KW;
+                float v[8];
                 if (q_bf16) {
-                    u32x4 raw = *(const u32x4 *)((const uint16_t *)q + off);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        float a = bf16_f32((uint16_t)(raw[i] & 0xFFFFu)) * qscale;
-                        float b = bf16_f32((uint16_t)(raw[i] >> 16)) * qscale;
-                        w[i] = (uint32_t)bf16_rne(a) | ((uint32_t)bf16_rne(b) << 16);
-                    }
+                    for (int i = 0; i < KW; i++) v[i] = bf16_f32(((const uint16_t *)q)[off + i]);
                 } else {
-                    const float4 *f = (const float4 *)((const float *)q + off);
-                    float4 a = f[0], b = f[1];
-                    w[0] = (uint32_t)bf16_rne(a.x * qscale) | ((uint32_t)bf16_rne(a.y * qscale) << 16);
-                    w[1] = (uint32_t)bf16_rne(a.z * qscale) | ((uint32_t)bf16_rne(a.w * qscale) << 16);
-                    w[2] = (uint32_t)bf16_rne(b.x * qscale) | ((uint32_t)bf16_rne(b.y * qscale) << 16);
-                    w[3] = (uint32_t)bf16_rne(b.z * qscale) | ((uint32_t)bf16_rne(b.w * qscale) << 16);
-                }
-                qb[nt][ks] = __builtin_bit_cast(bf16x8, w);
-            }
-        } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) qb[nt][ks] = __builtin_bit_cast(bf16x8, u32x4{0, 0, 0, 0});
+                    for (int i = 0; i < KW; i += 4) {
+                        const float4 f = *(const float4 *)((const float *)q + off + i);
+                        v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < KW / 2; i++)
+                    qb[nt][ks][i] = (uint32_t)bf16_rne(v[2 * i] * qscale) | ((uint32_t)bf16_rne(v[2 * i + 1] * qscale) << 16);
+            }
         }
     }
 
@@ -121,12 +122,17 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         // displacing reusable lines (measured ~12% more read bandwidth).
         const int page = table[R.tab + t0 / P];
         const int slot0 = t0 % P;
-        const uint16_t *kp = kpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)(slot0 + col) * D + grp * 8;
+        const uint16_t *kp = kpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)(slot0 + col) * D + grp * KW;
         const uint16_t *vp = vpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)col * P + slot0 + grp * 4;
         u32x4 kr[KS];
         u32x2 vr[MT];
+        if constexpr (K16) {
+            const u32x2 k2 = __builtin_nontemporal_load((const u32x2 *)kp);
+            kr[0] = u32x4{k2[0], k2[1], 0, 0};
+        } else {
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) kr[ks] = __builtin_nontemporal_load((const u32x4 *)(kp + ks * 32));
+            for (int ks = 0; ks < KS; ks++) kr[ks] = __builtin_nontemporal_load((const u32x4 *)(kp + ks * 32));
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) vr[mt] = __builtin_nontemporal_load((const u32x2 *)(vp + (int64_t)mt * 16 * P));
 
@@ -147,9 +153,16 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
             fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (K16) {
+                s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+                    __builtin_bit_cast(sh4, u32x2{kr[0][0], kr[0][1]}),
+                    __builtin_bit_cast(sh4, u32x2{qb[nt][0][0], qb[nt][0][1]}), s, 0, 0, 0);
+            } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ks]), qb[nt][ks], s, 0, 0, 0);
+                for (int ks = 0; ks < KS; ks++)
+                    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ks]),
+                                                                __builtin_bit_cast(bf16x8, qb[nt][ks]), s, 0, 0, 0);
+            }
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -245,15 +258,16 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
     const int kvh = blockIdx.y;
     const int qr = blockIdx.z;
     const int G = H / KVH;
-    if (qr >= G * R.nq) return;
+    if (qr >= G * R.qn) return;
     __shared__ float fac[kMaxSplits];
     __shared__ float inv_l;
     const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // split 0
     const int64_t sstride = (int64_t)KVH * QRP;                    // between splits
     merge_weights(part_ml + b0 * 2, sstride, R.nsplit, fac, &inv_l);
     __syncthreads();
-    const int qi = qr / G;
-    const int h = kvh * G + (qr - qi * G);
+    const int ql = qr / G;
+    const int h = kvh * G + (qr - ql * G);
+    const int qi = R.q0 + ql;
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float O = 0.f;
         for (int s = 0; s < R.nsplit; s++) O += fac[s] * part_o[(b0 + s * sstride) * D + d];
@@ -282,7 +296,7 @@ static hipError_t launch_gqa_t(hipStream_t s, const uint16_t *kpool, const uint1
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
-    gqa_combine_kernel<<<dim3(n_rows, KVH, max_qr), D, 0, s>>>(rows, part_o, part_ml, out,
+    gqa_combine_kernel<<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(rows, part_o, part_ml, out,
                                                                out_bf16, layout, H, KVH, D,
                                                                16 * NQT);
     return hipGetLastError();
@@ -304,6 +318,10 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
     RLX_GQA_CASE(128, 2)
     RLX_GQA_CASE(64, 1)
     RLX_GQA_CASE(64, 2)
+    RLX_GQA_CASE(32, 1)
+    RLX_GQA_CASE(32, 2)
+    RLX_GQA_CASE(16, 1)
+    RLX_GQA_CASE(16, 2)
 #undef RLX_GQA_CASE
     return hipErrorInvalidValue;
 }
@@ -315,6 +333,10 @@ int gqa_decode_wgs_per_cu(int hd, int nqt) {
     if (hd == 128 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 2>, 256, 0);
     if (hd == 64 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 1>, 256, 0);
     if (hd == 64 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 2>, 256, 0);
+    if (hd == 32 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 1>, 256, 0);
+    if (hd == 32 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 2>, 256, 0);
+    if (hd == 16 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 1>, 256, 0);
+    if (hd == 16 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 2>, 256, 0);
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 

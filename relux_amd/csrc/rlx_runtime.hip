@@ -383,9 +383,11 @@ int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
     return best;
 }
 
+// One AttRow per sequence, or -- with qtile > 0 (GQA decode kernel only) --
+// one per tile of at most qtile queries, each with its own context splits.
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
                    int chunk, std::vector<AttRow> &rows, std::vector<int2> &work,
-                   int *total_q, int *max_nq, int *total_parts) {
+                   int *total_q, int *max_nq, int *total_parts, int qtile = 0) {
     LayerState &ls = c->L[layer];
     int qrow = 0, part = 0, mx = 0;
     for (int i = 0; i < n_seqs; i++) {
@@ -394,17 +396,22 @@ int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, cons
         if (s.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
         if (nq < 1 || nq > s.len)
             return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, s.len);
-        AttRow r;
-        r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
-        r.len = s.len;
-        r.nq = nq;
-        r.qrow = qrow;
-        r.nsplit = chunk > 0 ? (s.len + chunk - 1) / chunk : 1;
-        r.part = part;
-        for (int sp = 0; sp < r.nsplit; sp++) work.push_back(int2{i, sp});
-        rows.push_back(r);
+        const int step = qtile > 0 ? qtile : nq;
+        for (int q0 = 0; q0 < nq; q0 += step) {
+            AttRow r;
+            r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
+            r.len = s.len;
+            r.nq = nq;
+            r.qrow = qrow;
+            r.nsplit = chunk > 0 ? (s.len + chunk - 1) / chunk : 1;
+            r.part = part;
+            r.q0 = q0;
+            r.qn = std::min(step, nq - q0);
+            for (int sp = 0; sp < r.nsplit; sp++) work.push_back(int2{(int)rows.size(), sp});
+            rows.push_back(r);
+            part += r.nsplit;
+        }
         qrow += nq;
-        part += r.nsplit;
         mx = std::max(mx, nq);
     }
     *total_q = qrow;
@@ -478,8 +485,8 @@ int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_
     if (layers <= 0) return fail(RLX_ERR_INVALID, "NewKVCacheSized: numLayers=%d, must be > 0", layers);
     if (kv_heads <= 0 || pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
         return fail(RLX_ERR_INVALID, "kv_heads, pool_pages, max_seqs, max_pages must be > 0");
-    if (head_dim != 64 && head_dim != 128)
-        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: 64, 128)", head_dim);
+    if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
+        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: 16, 32, 64, 128)", head_dim);
     if (page_tokens <= 0 || page_tokens % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
     Cache *c = new Cache;
@@ -731,10 +738,14 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = G * max_nq;
-    if (max_qr > 32) {
+    // The FA2 prefill kernel covers head_dim 64/128 with G dividing 128;
+    // other shapes tile their queries through the decode kernel, whose
+    // work-group holds at most 32 query rows of one kv head.
+    const bool fa2 = (c->hd == 64 || c->hd == 128) && 128 % G == 0;
+    if (max_qr > 32 && !fa2 && G > 32)
+        return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most 32)", G, c->hd);
+    if (max_qr > 32 && fa2) {
         // Chunked prefill / long verify: FA2 tiles of 128 query rows.
-        if (128 % G != 0)
-            return fail(RLX_ERR_UNSUPPORTED, "prefill needs 128 %% (heads per kv head = %d) == 0", G);
         std::vector<AttRow> rows;
         std::vector<int2> unused;
         int total_q = 0, mnq = 0, parts = 0;
@@ -774,12 +785,19 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         HIP_TRY(launch_prefill(c->stream, kSrcPaged, c->hd, a, (int)work.size(), e0, e1));
         return RLX_OK;
     }
+    const int qtile = max_qr > 32 ? 32 / G : 0;
     const int nqt = max_qr > 16 ? 2 : 1;
-    const int chunk = choose_chunk(lens, c->kvh, (int64_t)c->cus * gqa_decode_wgs_per_cu(c->hd, nqt));
+    std::vector<int> units_lens;  // one entry per query tile
+    for (int i = 0; i < n_seqs; i++) {
+        const int nq = n_q ? n_q[i] : 1;
+        const int tiles = qtile ? (nq + qtile - 1) / qtile : 1;
+        for (int t = 0; t < tiles; t++) units_lens.push_back(lens[i]);
+    }
+    const int chunk = choose_chunk(units_lens, c->kvh, (int64_t)c->cus * gqa_decode_wgs_per_cu(c->hd, nqt));
     std::vector<AttRow> rows;
     std::vector<int2> work;
     int total_q = 0, mnq = 0, parts = 0;
-    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts)))
+    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts, qtile)))
         return rc;
     if ((rc = flush_patches(c))) return rc;
     const int QRP = 16 * nqt;
@@ -795,12 +813,12 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
     HIP_TRY(launch_gqa_decode(c->stream, ls.pool0, ls.pool1, c->d_table,
-                              (const AttRow *)((char *)dev + o_r), n_seqs,
+                              (const AttRow *)((char *)dev + o_r), (int)rows.size(),
                               (const int2 *)((char *)dev + o_w), (int)work.size(), q,
                               q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
                               chunk, qscale, mask_mode, nqt, (float *)c->ws,
                               (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
-                              max_qr, e0, e1));
+                              std::min(max_qr, 32), e0, e1));
     return RLX_OK;
 }
 

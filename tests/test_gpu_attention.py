@@ -69,6 +69,9 @@ def _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=2):
     (8, 8, 64, [5, 129, 1000], 2, "none"),
     (16, 4, 64, [7, 7, 40], 7, "ref"),                               # reference mask rule
     (16, 4, 128, [3, 12], 3, "ref"),
+    (4, 2, 16, [8, 23, 300], 1, "causal"),                           # config-1 head_dim 16
+    (4, 2, 16, [8, 9], 8, "ref"),
+    (8, 2, 32, [17, 500], 4, "causal"),                              # head_dim 32
 ])
 def test_gqa_attend_matches_oracle(gpu, H, KVH, D, lens, nq, mask):
     from relux_amd import KVCache
@@ -283,6 +286,11 @@ def test_mla_config3_full_shape(gpu):
     (32, 4, 64, [257, 129], [200, 129], "causal"),          # G = 8, D = 64
     (8, 8, 128, [90, 70], [90, 30], "ref"),                 # reference mask rule both ways
     (16, 16, 128, [150], [150], "none"),
+    # shapes the FA2 kernel does not take: query tiles through the decode kernel
+    (4, 2, 16, [300, 40], [70, 40], "causal"),             # head_dim 16
+    (8, 2, 32, [280, 100], [120, 100], "ref"),             # head_dim 32
+    (12, 4, 64, [290, 50], [60, 50], "causal"),            # G = 3 does not divide 128
+    (6, 2, 128, [260], [260], "none"),
 ])
 def test_gqa_prefill_matches_oracle(gpu, H, KVH, D, lens, nqs, mask):
     from relux_amd import KVCache
@@ -311,6 +319,25 @@ def test_gqa_prefill_matches_oracle(gpu, H, KVH, D, lens, nqs, mask):
         if len(rows):
             _check(got[:, rows], ref[:, rows], TOL_ORACLE, f"seq {i} vs oracle (rows >= 256 keys)")
         off += nqs[i]
+
+
+def test_gqa_query_tiles_layouts(gpu):
+    """Query-tiled attention (head_dim 16, 40 queries x 2 heads per kv head)
+    gives the same rows in both q/out layouts."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(47)
+    H, KVH, D, lens, nqs = 4, 2, 16, [60, 45], [40, 45]
+    c = KVCache(num_layers=1, max_len=64, num_kv_heads=KVH, head_dim=D, max_seqs=2,
+                device=gpu.index)
+    _fill_gqa(c, rng, gpu, lens, KVH, D)
+    q = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    shd = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=[0, 1], n_q=nqs).cpu().numpy()
+    qh = np.concatenate([q[:40].transpose(1, 0, 2).reshape(-1), q[40:].transpose(1, 0, 2).reshape(-1)])
+    hsd = c.Attend(0, torch.from_numpy(qh).to(gpu), H, seq_ids=[0, 1], n_q=nqs,
+                   layout="HSD").cpu().numpy()
+    back = np.concatenate([hsd[:40 * H * D].reshape(H, 40, D).transpose(1, 0, 2),
+                           hsd[40 * H * D:].reshape(H, 45, D).transpose(1, 0, 2)])
+    np.testing.assert_array_equal(back, shd)
 
 
 def test_gqa_prefill_rows_equal_decode_after_rollback(gpu):
@@ -398,3 +425,67 @@ def test_mla_config4_shape_sampled(gpu):
         s = s.masked_fill(~mask, float("-inf"))
         ref = torch.softmax(s, dim=-1) @ v
         _check(out[:, h].cpu().numpy(), ref.cpu().numpy(), (1e-2, 1e-3), f"head {h}")
+
+
+def test_spec_verify_stress_small(gpu):
+    """Config 5 at small scale: every step appends 4 drafts per sequence,
+    verifies them (4 drafts x 8 heads = 32 rows per kv head), rolls back a
+    random suffix; every 8 steps the oldest 25% of full pages are evicted
+    and the table compacted.  Attention is checked each step against exact
+    f64 attention over the logical surviving tokens, and the integer state
+    against the page-table model."""
+    from relux_amd import KVCache
+    from oracle.paged import PagedModel
+    rng = np.random.default_rng(55)
+    B, H, KVH, D, P, nd = 6, 64, 8, 128, 16, 4
+    lens = [int(x) for x in np.exp(rng.uniform(np.log(40), np.log(700), size=B))]
+    maxp = 80
+    c = KVCache(num_layers=1, max_len=maxp * P, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=B, pool_pages=B * maxp, device=gpu.index)
+    m = PagedModel(1, P, B * maxp, B, maxp)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    for ci in range(2):  # the same two multi-sequence Append calls _fill_gqa made
+        m.append(0, list(range(B)), [(L * (ci + 1)) // 2 - (L * ci) // 2 for L in lens])
+    Kl = [list(K[i].transpose(1, 0, 2)) for i in range(B)]  # per-token [KVH, D]
+    Vl = [list(V[i].transpose(1, 0, 2)) for i in range(B)]
+    seqs = list(range(B))
+    g = H // KVH
+    for step in range(24):
+        kd = rng.standard_normal((B * nd, KVH, D), dtype=np.float32)
+        vd = rng.standard_normal((B * nd, KVH, D), dtype=np.float32)
+        c.Append(0, torch.from_numpy(kd).to(gpu), torch.from_numpy(vd).to(gpu), seq_ids=seqs,
+                 n_tok=[nd] * B, layout="SHD")
+        m.append(0, seqs, [nd] * B)
+        for i in range(B):
+            Kl[i].extend(oracle.round_bf16(kd[i * nd:(i + 1) * nd]))
+            Vl[i].extend(oracle.round_bf16(vd[i * nd:(i + 1) * nd]))
+        q = rng.standard_normal((B * nd, H, D), dtype=np.float32)
+        out = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=seqs, n_q=[nd] * B).cpu().numpy()
+        for i in (step % B, (step + 3) % B):
+            Ki = np.repeat(np.stack(Kl[i], axis=1), g, 0)
+            Vi = np.repeat(np.stack(Vl[i], axis=1), g, 0)
+            T = Ki.shape[1]
+            exact = oracle.exact_attention_f64(q[i * nd:(i + 1) * nd].transpose(1, 0, 2), Ki, Vi,
+                                               [T - nd + j for j in range(nd)])
+            _check(out[i * nd:(i + 1) * nd].transpose(1, 0, 2), exact, TOL_EXACT,
+                   f"step {step} seq {i} T {T}")
+        r = [int(x) for x in rng.integers(0, nd + 1, size=B)]
+        c.Rollback(seqs, r)
+        for i in range(B):
+            m.rollback(0, i, r[i])
+            if r[i]:
+                del Kl[i][len(Kl[i]) - r[i]:]
+                del Vl[i][len(Vl[i]) - r[i]:]
+        if step % 8 == 7:
+            ev = [int(m.len[0, i] // P) // 4 for i in range(B)]
+            c.Evict(seqs, ev)
+            c.Compact()
+            for i in range(B):
+                m.evict(0, i, ev[i])
+                del Kl[i][: ev[i] * P]
+                del Vl[i][: ev[i] * P]
+            m.compact(0)
+        for i in range(B):
+            assert c.SeqState(0, i) == m.state(0, i)
+            assert c.PageTable(0, i) == list(m.table[0][i])
+        assert c.FreeList(0) == m.free[0]

@@ -208,3 +208,51 @@ def test_mla_append_gather_bit_exact(gpu):
         want_kr = oracle.bf16_from_f32(np.concatenate([r[1] for r in rows[s]]))
         assert np.array_equal(got_c.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_c)
         assert np.array_equal(got_kr.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_kr)
+
+
+def test_paged_script_matches_golden(gpu):
+    """Replay the committed append / rollback / evict / compact / release
+    script (tests/golden/paged_script.npz, written from oracle/paged.py):
+    page table, length, first entry, position offset and free stack after
+    every operation, and the live bytes, all exact."""
+    import os
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "paged_script.npz"))
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "make_fixtures", os.path.join(os.path.dirname(__file__), "golden", "make_fixtures.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    PAGED_SCRIPT, cfg = mk.PAGED_SCRIPT, mk.PAGED_CFG
+    KVH, D = 2, 64
+    c = _kv(gpu, num_layers=1, max_len=cfg["max_pages"] * cfg["P"], num_kv_heads=KVH, head_dim=D,
+            page_tokens=cfg["P"], max_seqs=cfg["max_seqs"], pool_pages=cfg["pool_pages"])
+    rng = np.random.default_rng(5)
+    rows = [[] for _ in range(cfg["max_seqs"])]  # live bf16 K rows [KVH, D] per token
+    for i, (op, seq, n) in enumerate(PAGED_SCRIPT):
+        if op == "append":
+            k = rng.standard_normal((n, KVH, D), dtype=np.float32)
+            kt = torch.from_numpy(k).to(gpu)
+            c.Append(0, kt, -kt, seq_ids=[seq], n_tok=[n], layout="SHD")
+            rows[seq].extend(oracle.bf16_from_f32(k))
+        elif op == "rollback":
+            c.Rollback(seq, n)
+            del rows[seq][len(rows[seq]) - n:]
+        elif op == "evict":
+            c.Evict(seq, n)
+            del rows[seq][: n * cfg["P"]]
+        elif op == "compact":
+            c.Compact()
+        elif op == "release":
+            c.Release(seq)
+            rows[seq] = []
+        for s in range(cfg["max_seqs"]):
+            st = c.SeqState(0, s)
+            assert st["len"] == fx["lens"][i, s] and st["first"] == fx["firsts"][i, s], (i, op, s)
+            assert st["pos_offset"] == fx["pos_offsets"][i, s], (i, op, s)
+            assert c.PageTable(0, s) == fx["tables"][i, s].tolist(), (i, op, s)
+            if st["len"]:
+                kv, _ = c.View(0, s)
+                got = kv[0].view(torch.int16).cpu().numpy().view(np.uint16)
+                np.testing.assert_array_equal(got, np.stack(rows[s]).transpose(1, 0, 2))
+        free = fx["free"][i]
+        assert c.FreeList(0) == free[free >= 0].tolist(), (i, op)
