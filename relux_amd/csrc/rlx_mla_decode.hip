@@ -21,9 +21,6 @@
 
 namespace rlx {
 
-constexpr int kPitch = kMlaRow + 4;  // 580 bf16 = 1160 B: 8-byte aligned rows,
-                                     // and 4-row strides fall on distinct banks
-
 __device__ __forceinline__ float mla_max16(float v) {
     v = fmaxf(v, __shfl_xor(v, 16));
     v = fmaxf(v, __shfl_xor(v, 32));
@@ -102,15 +99,52 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
     }
 }
 
+// LDS tile layout: 16 token rows x 72 chunks of 16 B (576 bf16), no padding.
+// Logical chunk c of row r lives at physical chunk c ^ mla_swz(r), which
+// stays inside the row's aligned group of 8 chunks.  The swizzle keeps the
+// two read patterns free of bank conflicts: score reads (8 lanes = 8 rows,
+// one chunk each) see 8 distinct chunk slots, and transpose reads (16 lanes
+// = 4 rows x one 32-B chunk pair) see 4 distinct chunk pairs.
+__device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// [15:14], expcnt[6:4], lgkmcnt[11:8]).
+#define RLX_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// 16 bytes per lane from global memory straight into LDS at lds_base +
+// 16 * lane (global_load_lds_dwordx4, non-temporal).  Written as inline asm
+// so that the compiler does not see an LDS write it cannot place: it would
+// otherwise wait for every outstanding load before each LDS read, which
+// serialises the ring.  The kernel orders these loads itself (explicit
+// vmcnt waits, then a barrier) and the "memory" clobber keeps the compiler
+// from moving LDS accesses across them.
+__device__ __forceinline__ void lds_dma16(const void *gptr, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, off nt"
+        :
+        : "v"(gptr), "s"(lds_base)
+        : "memory", "m0");
+}
+
+// Work-group barrier for the ring: this wave's LDS accesses complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for outstanding
+// global loads, so ring loads stay in flight across it.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int NQT>
-__global__ __launch_bounds__(256) void mla_decode_kernel(
+__global__ __launch_bounds__(256, 2) void mla_decode_kernel(
     const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
     const AttRow *__restrict__ rows, const int2 *__restrict__ work,
     const uint16_t *__restrict__ qlat, int H, int P, int chunk, int mask_mode,
     float *__restrict__ part_o, float *__restrict__ part_ml) {
     constexpr int QRP = 16 * NQT;
-    constexpr int CHUNKS = 16 * kMlaRow / 8;  // 16-byte pieces per tile: 1152
-    __shared__ uint16_t tile[2][16 * kPitch];
+    constexpr int S = (NQT == 1) ? 4 : 3;  // LDS ring stages (2 work-groups per CU)
+    constexpr int TILE = 16 * kMlaRow;     // bf16 per stage
+    __shared__ __attribute__((aligned(16))) uint16_t ring[S * TILE];
     __shared__ fl4 spart[4][NQT][64];
 
     const int tid = threadIdx.x;
@@ -123,27 +157,8 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
     const int QR = H * R.nq;
     const int t_begin = wk.y * chunk;
     const int t_end = min(R.len, t_begin + chunk);
-
-    // B operand of the score product for this wave's 9 k-steps.
-    sh4 qb[NQT][9];
-    int klim[NQT];
-#pragma unroll
-    for (int nt = 0; nt < NQT; nt++) {
-        const int qr = nt * 16 + col;
-        klim[nt] = R.len - 1;
-        if (qr < QR) {
-            const int qi = qr / H;
-            const int h = qr - qi * H;
-            klim[nt] = mla_key_limit(mask_mode, R.len, R.nq, qi);
-            const uint16_t *qp = qlat + ((int64_t)(R.qrow + qi) * H + h) * kMlaRow + grp * 4;
-#pragma unroll
-            for (int kk = 0; kk < 9; kk++)
-                qb[nt][kk] = __builtin_bit_cast(sh4, *(const u32x2 *)(qp + (wave * 9 + kk) * 16));
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < 9; kk++) qb[nt][kk] = sh4{0, 0, 0, 0};
-        }
-    }
+    const int ntiles = (t_end - t_begin + 15) / 16;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)ring;
 
     float m_run[NQT], l_part[NQT];
     fl4 acc[NQT][8];
@@ -155,53 +170,101 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
         for (int mt = 0; mt < 8; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // Rows past the live length are staged as zeros.
-    u32x4 pre[5];
-    auto load_tile = [&](int t0) {
+    // Tile j (16 tokens) streams straight from HBM into ring stage j % S
+    // (global_load_lds, 16 B per lane, non-temporal).  One instruction fills
+    // 64 consecutive physical chunks: waves 0-1 issue 5 per tile, waves 2-3
+    // issue 4 (1152 chunks).  Rows past the live length re-read the last
+    // live row, so every staged value is a finite cache value and masked
+    // tokens contribute exact zeros.
+    auto issue_tile = [&](int j) {
+        const int t0 = t_begin + 16 * j;
         const int page = table[R.tab + t0 / P];
-        const uint16_t *src = pool + ((int64_t)page * P + (t0 % P)) * kMlaRow;
+        const int slot0 = t0 % P;
+        const uint16_t *src = pool + (int64_t)page * P * kMlaRow;
+        const uint32_t dst = ring_lds + (uint32_t)((j % S) * TILE * 2);
 #pragma unroll
         for (int k = 0; k < 5; k++) {
-            const int c = tid + 256 * k;
-            pre[k] = u32x4{0, 0, 0, 0};
-            if (c < CHUNKS && t0 + c / 72 < R.len) pre[k] = __builtin_nontemporal_load((const u32x4 *)(src + (int64_t)c * 8));
+            if (k == 4 && wave >= 2) break;
+            const int base = 256 * k + 64 * wave;  // first physical chunk (wave-uniform)
+            const int pch = base + lane;
+            const int r = pch / 72;
+            const int lc = (pch - r * 72) ^ mla_swz(r);
+            const int tok = min(t0 + r, R.len - 1);
+            const uint16_t *g = src + (int64_t)(slot0 + tok - t0) * kMlaRow + lc * 8;
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(dst + (uint32_t)base * 16));
         }
     };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int k = 0; k < 5; k++) {
-            const int c = tid + 256 * k;
-            if (c < CHUNKS) {
-                const int r = c / 72, cc = c - r * 72;
-                uint16_t *d = &tile[buf][r * kPitch + cc * 8];
-                *(u32x2 *)d = u32x2{pre[k][0], pre[k][1]};
-                *(u32x2 *)(d + 4) = u32x2{pre[k][2], pre[k][3]};
-            }
+    // Wait until this wave's loads of the awaited tile landed, given how many
+    // tiles it issued after that one (loads retire in issue order).
+    auto wait_tile = [&](int ahead) {
+        if (ahead >= 2) {
+            if (wave < 2) RLX_WAIT_VM(10); else RLX_WAIT_VM(8);
+        } else if (ahead == 1) {
+            if (wave < 2) RLX_WAIT_VM(5); else RLX_WAIT_VM(4);
+        } else {
+            RLX_WAIT_VM(0);
         }
     };
 
-    int buf = 0;
-    if (t_begin < t_end) {
-        load_tile(t_begin);
-        store_tile(0);
+    for (int j = 0; j < S - 1 && j < ntiles; j++) issue_tile(j);
+
+    // Score k-steps (MFMA 16x16x32, 32 channels each): 18 per tile, split
+    // 5/5/4/4 over the waves.  B operand = q_lat^T, 8 channels per lane.
+    const int ks0 = wave < 2 ? 5 * wave : 2 + 4 * wave;
+    const int nks = wave < 2 ? 5 : 4;
+    u32x4 qb[NQT][5];
+    int klim[NQT];
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+        const int qr = nt * 16 + col;
+        klim[nt] = R.len - 1;
+#pragma unroll
+        for (int kk = 0; kk < 5; kk++) qb[nt][kk] = u32x4{0, 0, 0, 0};
+        if (qr < QR) {
+            const int qi = qr / H;
+            const int h = qr - qi * H;
+            klim[nt] = mla_key_limit(mask_mode, R.len, R.nq, qi);
+            const uint16_t *qp = qlat + ((int64_t)(R.qrow + qi) * H + h) * kMlaRow + grp * 8;
+#pragma unroll
+            for (int kk = 0; kk < 5; kk++)
+                if (kk < nks) qb[nt][kk] = *(const u32x4 *)(qp + (ks0 + kk) * 32);
+        }
     }
-    __syncthreads();
-    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-        const bool has_next = t0 + 16 < t_end;
-        if (has_next) load_tile(t0 + 16);
-        const uint16_t *T = tile[buf];
-        // Partial scores over this wave's quarter of the 576 channels.
+
+    // Make the compiler complete the q loads here, once: the ring loads are
+    // invisible to it, so a wait it placed inside the loop would also drain
+    // the ring on every tile.
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++)
+#pragma unroll
+        for (int kk = 0; kk < 5; kk++) asm volatile("" ::"v"(qb[nt][kk]));
+
+    for (int j = 0; j < ntiles; j++) {
+        wait_tile(min(S - 2, ntiles - 1 - j));
+        // Tile j is visible to every wave, and stage (j-1) % S is no longer read.
+        ring_barrier();
+        if (j + S - 1 < ntiles) issue_tile(j + S - 1);
+        const int t0 = t_begin + 16 * j;
+        const uint16_t *T = ring + (j % S) * TILE;
+
+        // Partial scores over this wave's k-steps.
+        const uint16_t *trow = T + col * kMlaRow;
+        const int sw = mla_swz(col);
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
             fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kk = 0; kk < 9; kk++) {
-                const sh4 a = __builtin_bit_cast(sh4, *(const u32x2 *)(T + col * kPitch + (wave * 9 + kk) * 16 + grp * 4));
-                s = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, qb[nt][kk], s, 0, 0, 0);
+            for (int kk = 0; kk < 5; kk++) {
+                if (kk < nks) {
+                    const int lc = (ks0 + kk) * 4 + grp;
+                    const u32x4 a = *(const u32x4 *)(trow + ((lc ^ sw) << 3));
+                    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                                __builtin_bit_cast(bf16x8, qb[nt][kk]), s, 0, 0, 0);
+                }
             }
             spart[wave][nt][lane] = s;
         }
-        __syncthreads();
+        ring_barrier();
         sh4 pb[NQT];
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
@@ -239,22 +302,23 @@ __global__ __launch_bounds__(256) void mla_decode_kernel(
             pw[1] = (uint32_t)bf16_rne(p[2]) | ((uint32_t)bf16_rne(p[3]) << 16);
             pb[nt] = __builtin_bit_cast(sh4, pw);
         }
-        // O^T += C^T . P^T over this wave's 128 latent channels.
+        // O^T += C^T . P^T over this wave's 128 latent channels.  The A operand
+        // (4 consecutive tokens of one channel per lane) comes from the
+        // row-major tile with the LDS transpose read: lane (g, j) fetches 4
+        // channels of row 4g + j/4 and the 16-lane group exchanges them so
+        // that lane j ends up with channel j of rows 4g..4g+3.
+        const int trr = 4 * grp + (col >> 2);
+        const uint16_t *tr = T + trr * kMlaRow + (col & 1) * 4;
+        const int tsw = mla_swz(trr);
 #pragma unroll
         for (int mt = 0; mt < 8; mt++) {
-            const int ch = wave * 128 + mt * 16 + col;
-            const uint16_t *tc = T + (grp * 4) * kPitch + ch;
-            u32x2 w;
-            w[0] = (uint32_t)tc[0] | ((uint32_t)tc[kPitch] << 16);
-            w[1] = (uint32_t)tc[2 * kPitch] | ((uint32_t)tc[3 * kPitch] << 16);
-            const sh4 a = __builtin_bit_cast(sh4, w);
+            const int lc = (wave * 128 + mt * 16) / 8 + ((col >> 1) & 1);
+            const sh4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) sh4 *)(tr + ((lc ^ tsw) << 3)));
 #pragma unroll
             for (int nt = 0; nt < NQT; nt++)
                 acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[nt], acc[nt][mt], 0, 0, 0);
         }
-        if (has_next) store_tile(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
     }
 
     const int pidx = R.part + wk.y;
