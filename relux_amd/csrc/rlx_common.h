@@ -130,6 +130,36 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
 constexpr int kSrcPaged = 0;
 constexpr int kSrcDense = 1;
 
+// ---- global-to-LDS rings ----------------------------------------------
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// [15:14], expcnt[6:4], lgkmcnt[11:8]).
+#define RLX_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// 16 bytes per lane from global memory straight into LDS at lds_base +
+// 16 * lane (global_load_lds_dwordx4, non-temporal).  Written as inline asm
+// so that the compiler does not see an LDS write it cannot place: it would
+// otherwise wait for every outstanding load before each LDS read, which
+// serialises the ring.  The kernel orders these loads itself (explicit
+// vmcnt waits, then a barrier) and the "memory" clobber keeps the compiler
+// from moving LDS accesses across them.
+__device__ __forceinline__ void lds_dma16(const void *gptr, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, off nt"
+        :
+        : "v"(gptr), "s"(lds_base)
+        : "memory", "m0");
+}
+
+// Work-group barrier for the ring: this wave's LDS accesses complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for outstanding
+// global loads, so ring loads stay in flight across it.
+__device__ __forceinline__ void ring_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 struct PrefillArgs {
     const uint16_t *kpool;  // paged: K row pages; dense: latent pool (rope keys)
     const uint16_t *vpool;  // paged: V dim-major pages

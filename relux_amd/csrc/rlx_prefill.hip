@@ -8,21 +8,26 @@
 // so the G heads that share a kv head share every K/V byte the tile loads.
 // 4 waves, wave w owns rows [32w, 32w+32) as two 16-wide N tiles.
 //
-// Per 32-key block, staged in LDS (double buffered through registers):
-//   S^T[32 keys][16 rows] = K . Q^T      MFMA 16x16x32 bf16, A = K rows (LDS),
-//                                         B = Q^T in registers (pre-scaled)
-//   online softmax per row, lane-local (the S^T result layout is the P^T
-//   B-operand layout: the lane's 8 keys are {4g..4g+3, 16+4g..16+4g+3})
-//   O^T[DV][16 rows] += V^T . P^T        MFMA 16x16x32 bf16, A = V^T rows (LDS,
-//                                         the same 8 keys per lane)
+// Keys stream in 32-key blocks through a 3-stage LDS ring filled straight
+// from memory (16-byte global-to-LDS loads); each stage holds the block's K
+// rows and its V^T rows, both swizzled in 16-byte chunks so that the MFMA
+// operand reads are free of bank conflicts.  Per block and wave:
+//   S^T[32 keys][16 rows] = K . Q^T    MFMA 16x16x32 bf16 (2 key tiles), A = K
+//                                       rows from LDS, B = Q^T in registers
+//   online softmax per row, lane-local.  Key tile mt's row m is key
+//   8(m/4) + 4mt + m%4, so a lane's S^T values are the 8 consecutive keys
+//   8g..8g+7: exactly the B operand P^T of the next product and one 16-byte
+//   chunk of a V^T row.
+//   O^T[DV][16 rows] += V^T . P^T       MFMA 16x16x32 bf16, A = V^T rows (LDS)
 //
 // Sources (SRC):
 //   kSrcPaged : GQA paged cache, K row pages and dim-major V pages, DQK = DV = D.
 //   kSrcDense : MLA, per sequence decompressed K_c [H][Tp][128] and
 //               V^T [H][128][Tp] (Tp = T rounded up to 128) plus the rope key
 //               k^R read from the paged latent rows; DQK = 192, DV = 128.
-// Keys at or past the live length are never read: their K rows and V columns
-// are staged as zeros and their scores masked.
+// Keys at or past the live length are masked; the K rows staged for them
+// repeat the last live key and their V^T entries are zeroed in LDS, so
+// nothing past the live length can reach the output.
 #include "rlx_common.h"
 
 namespace rlx {
@@ -47,26 +52,99 @@ __device__ __forceinline__ int pf_limit(int mask_mode, int len, int nq, int qi) 
 }
 
 
+// Swizzles of the ring stages (16-byte chunk index XOR, within aligned
+// groups of 8 chunks).  K: the 8 rows one pass of a b128 read touches
+// ({0-3, 8-11} + 4mt, and +16) get 8 distinct chunk slots.  V^T (rows of 4
+// chunks): 8 consecutive rows get 8 distinct slots.
+__device__ __forceinline__ int pf_kswz(int row) { return (row & 3) | ((row >> 1) & 4); }
+__device__ __forceinline__ int pf_vswz(int row) { return (row >> 1) & 3; }
+
 template <int DQK, int DV, int SRC>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-    constexpr int KS = DQK / 32;          // score k-steps
-    constexpr int MD = DV / 16;           // value m-tiles
-    constexpr int KP = DQK + 8;           // K row pitch (bf16): 16-byte pad
-    constexpr int VP = kKeyBlock + 4;     // V^T row pitch (bf16): 8-byte pad
-    constexpr int KCH = kKeyBlock * DQK / 8;  // 16-byte chunks of a K block
-    constexpr int VCH = DV * kKeyBlock / 8;   // 16-byte chunks of a V^T block
-    constexpr int KPER = (KCH + 255) / 256;
-    constexpr int VPER = (VCH + 255) / 256;
-    __shared__ uint16_t Ks[2][kKeyBlock * KP];
-    __shared__ uint16_t Vs[2][DV * VP];
+// The page table is a separate __restrict__ argument so that the compiler
+// may read it through the scalar cache: a vector load would be ordered
+// behind the in-flight ring loads by the waits the compiler inserts.
+__global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
+                                                         const int32_t *__restrict__ table) {
+    constexpr int KS = DQK / 32;             // score k-steps
+    constexpr int MD = DV / 16;              // value m-tiles
+    constexpr int KCH = DQK / 8;             // 16-byte chunks per K row
+    constexpr int K_CH = kKeyBlock * KCH;    // K chunks per stage
+    constexpr int V_CH = DV * kKeyBlock / 8; // V^T chunks per stage
+    constexpr int ST_CH = K_CH + V_CH;
+    constexpr int PER_WAVE = ST_CH / 256;    // ring loads per wave per block
+    constexpr int S = 3;                     // ring stages
+    static_assert(ST_CH % 256 == 0 && K_CH % 64 == 0 && KCH % 8 == 0, "stage shape");
+    __shared__ __attribute__((aligned(16))) uint16_t ring[S * ST_CH * 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int4 wk = a.work[blockIdx.x];
+    if (wk.x < 0) return;  // padding item of the XCD-balanced work order
     const AttRow R = a.rows[wk.x];
     const int hg = wk.y;
     const int G = (SRC == kSrcPaged) ? a.H / a.KVH : 1;
     const int toks = kTileRows / G;  // query tokens per tile
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)ring;
+
+    // Keys the tile needs: up to the largest limit of its rows.
+    int kend;
+    {
+        const int jmax = min(R.nq - 1, wk.z * toks + toks - 1);
+        kend = min(R.len, pf_limit(a.mask_mode, R.len, R.nq, jmax) + 1);
+        if (a.mask_mode == kMaskRef && R.nq != R.len) kend = R.len;
+    }
+    const int nblk = (kend + kKeyBlock - 1) / kKeyBlock;
+
+    // ---- ring loads of key block j into stage j % S -------------------------
+    auto issue_block = [&](int j) {
+        const int k0 = j * kKeyBlock;
+        // Keys k0..k0+15 and k0+16..k0+31 each lie in one page (P is a
+        // multiple of 16); both page ids are wave-uniform scalar loads.
+        int pg0 = 0, pg1 = 0;
+        if (SRC == kSrcPaged || DQK > 128) {  // dense: rope keys live in the pages
+            pg0 = table[R.tab + k0 / a.P];
+            pg1 = (k0 + 16 < R.len) ? table[R.tab + (k0 + 16) / a.P] : pg0;
+        }
+        const uint32_t stage = ring_lds + (uint32_t)((j % S) * ST_CH * 16);
+#pragma unroll
+        for (int i = 0; i < PER_WAVE; i++) {
+            const int base = (i * 4 + wave) * 64;  // first physical chunk (wave-uniform)
+            const int p = base + lane;
+            const uint16_t *g;
+            if (base < K_CH) {
+                const int row = p / KCH;
+                const int lc = (p - row * KCH) ^ pf_kswz(row);
+                const int t = min(k0 + row, R.len - 1);
+                const int pg = (t - k0 < 16) ? pg0 : pg1;
+                if (SRC == kSrcPaged)
+                    g = a.kpool + (((int64_t)pg * a.KVH + hg) * a.P + (t % a.P)) * DQK + lc * 8;
+                else if (lc < 16)
+                    g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
+                else
+                    g = a.kpool + ((int64_t)pg * a.P + (t % a.P)) * kMlaRow + kMlaDc + (lc - 16) * 8;
+            } else {
+                const int q = p - K_CH;
+                const int d = q >> 2;
+                const int lc = (q & 3) ^ pf_vswz(d);
+                int t = k0 + lc * 8;
+                if (t >= R.len) t = k0;  // whole chunk past the end: its entries get zeroed
+                if (SRC == kSrcPaged) {
+                    const int pg = (t - k0 < 16) ? pg0 : pg1;
+                    g = a.vpool + (((int64_t)pg * a.KVH + hg) * DV + d) * a.P + (t % a.P);
+                } else {
+                    g = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
+                }
+            }
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)base * 16));
+        }
+    };
+    // Wait for this wave's loads of a block, given how many blocks it issued
+    // after it (loads retire in issue order).
+    auto wait_block = [&](int ahead) {
+        if (ahead >= 1) RLX_WAIT_VM(PER_WAVE); else RLX_WAIT_VM(0);
+    };
+
+    for (int j = 0; j < S - 1 && j < nblk; j++) issue_block(j);
 
     // ---- query operand and per-row key limits -----------------------------
     bf16x8 qb[2][KS];
@@ -120,85 +198,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
             qb[nt][ks] = __builtin_bit_cast(bf16x8, w);
         }
     }
-
-    // Keys the tile needs: up to the largest limit of its rows.
-    int kend;
-    {
-        const int jmax = min(R.nq - 1, wk.z * toks + toks - 1);
-        kend = min(R.len, pf_limit(a.mask_mode, R.len, R.nq, jmax) + 1);
-        if (a.mask_mode == kMaskRef && R.nq != R.len) kend = R.len;
-    }
-
-    // ---- staging of one 32-key block --------------------------------------
-    u32x4 kreg[KPER], vreg[VPER];
-    auto load_block = [&](int k0) {
+    // Make the compiler complete the query loads here, once: the ring loads
+    // are invisible to it, so a wait it placed inside the key loop would
+    // also drain the ring on every block.
 #pragma unroll
-        for (int u = 0; u < KPER; u++) {
-            const int c = tid + 256 * u;
-            kreg[u] = u32x4{0, 0, 0, 0};
-            if (c < KCH) {
-                const int r = c / (DQK / 8), cc = c % (DQK / 8);
-                const int t = k0 + r;
-                if (t < R.len) {
-                    const uint16_t *src;
-                    if (SRC == kSrcPaged) {
-                        const int page = a.table[R.tab + t / a.P];
-                        src = a.kpool + (((int64_t)page * a.KVH + hg) * a.P + (t % a.P)) * DQK + cc * 8;
-                    } else if (cc < 16) {
-                        src = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + cc * 8;
-                    } else {
-                        const int page = a.table[R.tab + t / a.P];
-                        src = a.kpool + ((int64_t)page * a.P + (t % a.P)) * kMlaRow + kMlaDc + (cc - 16) * 8;
-                    }
-                    kreg[u] = __builtin_nontemporal_load((const u32x4 *)src);
-                }
-            }
-        }
+    for (int nt = 0; nt < 2; nt++)
 #pragma unroll
-        for (int u = 0; u < VPER; u++) {
-            const int c = tid + 256 * u;
-            vreg[u] = u32x4{0, 0, 0, 0};
-            if (c < VCH) {
-                const int d = c / (kKeyBlock / 8), part = c % (kKeyBlock / 8);  // 8 keys per chunk
-                const int t = k0 + part * 8;
-                if (t < R.len) {
-                    const uint16_t *src;
-                    if (SRC == kSrcPaged) {
-                        const int page = a.table[R.tab + t / a.P];
-                        src = a.vpool + (((int64_t)page * a.KVH + hg) * DV + d) * a.P + (t % a.P);
-                    } else {
-                        src = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
-                    }
-                    u32x4 v = __builtin_nontemporal_load((const u32x4 *)src);
-                    // zero the keys of this chunk that lie past the live length
-#pragma unroll
-                    for (int i = 0; i < 8; i++)
-                        if (t + i >= R.len) v[i >> 1] &= (i & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                    vreg[u] = v;
-                }
-            }
-        }
-    };
-    auto store_block = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < KPER; u++) {
-            const int c = tid + 256 * u;
-            if (c < KCH) {
-                const int r = c / (DQK / 8), cc = c % (DQK / 8);
-                *(u32x4 *)&Ks[buf][r * KP + cc * 8] = kreg[u];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < VPER; u++) {
-            const int c = tid + 256 * u;
-            if (c < VCH) {
-                const int d = c / (kKeyBlock / 8), part = c % (kKeyBlock / 8);
-                uint16_t *dst = &Vs[buf][d * VP + part * 8];
-                *(u32x2 *)dst = u32x2{vreg[u][0], vreg[u][1]};
-                *(u32x2 *)(dst + 4) = u32x2{vreg[u][2], vreg[u][3]};
-            }
-        }
-    };
+        for (int ks = 0; ks < KS; ks++) asm volatile("" ::"v"(qb[nt][ks]));
 
     float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.f, 0.f};
     fl4 acc[2][MD];
@@ -207,17 +213,31 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
 #pragma unroll
         for (int md = 0; md < MD; md++) acc[nt][md] = fl4{0.f, 0.f, 0.f, 0.f};
 
-    int buf = 0;
-    if (kend > 0) {
-        load_block(0);
-        store_block(0);
-    }
-    __syncthreads();
-    for (int k0 = 0; k0 < kend; k0 += kKeyBlock) {
-        const bool has_next = k0 + kKeyBlock < kend;
-        if (has_next) load_block(k0 + kKeyBlock);
-        const uint16_t *Kb = Ks[buf];
-        const uint16_t *Vb = Vs[buf];
+    // LDS row of key tile mt's m-th row, and this lane's read offsets.
+    int krow[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++) krow[mt] = (col >> 2) * 8 + mt * 4 + (col & 3);
+
+    for (int j = 0; j < nblk; j++) {
+        wait_block(min(S - 2, nblk - 1 - j));
+        // Block j is visible to every wave; stage (j-1) % S is no longer read.
+        ring_barrier();
+        if (j + S - 1 < nblk) issue_block(j + S - 1);
+        const int k0 = j * kKeyBlock;
+        const uint16_t *Kb = ring + (j % S) * ST_CH * 8;
+        const uint16_t *Vb = Kb + K_CH * 8;
+        if (k0 + kKeyBlock > R.len) {
+            // Last block of the sequence: zero the V^T entries of keys past
+            // the live length (they hold stale or repeated cache bytes).
+            uint16_t *Vw = ring + (j % S) * ST_CH * 8 + K_CH * 8;
+            const int live = R.len - k0;
+            for (int e = tid; e < DV * kKeyBlock; e += 256) {
+                const int d = e / kKeyBlock, kk = e - d * kKeyBlock;
+                if (kk >= live) Vw[d * kKeyBlock + (((kk >> 3) ^ pf_vswz(d)) << 3) + (kk & 7)] = 0;
+            }
+            ring_barrier();
+        }
+
         fl4 s[2][2];
 #pragma unroll
         for (int mt = 0; mt < 2; mt++)
@@ -227,7 +247,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         for (int ks = 0; ks < KS; ks++) {
 #pragma unroll
             for (int mt = 0; mt < 2; mt++) {
-                const bf16x8 ka = __builtin_bit_cast(bf16x8, *(const u32x4 *)&Kb[(mt * 16 + col) * KP + ks * 32 + grp * 8]);
+                const int row = krow[mt];
+                const int pc = (ks * 4 + grp) ^ pf_kswz(row);
+                const bf16x8 ka = __builtin_bit_cast(bf16x8, *(const u32x4 *)&Kb[row * DQK + pc * 8]);
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++)
                     s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], s[mt][nt], 0, 0, 0);
@@ -236,13 +258,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         bf16x8 pb[2];
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            float p[8];
+            float p[8];  // keys k0 + 8*grp + i
             float mx = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int t = k0 + mt * 16 + grp * 4 + i;
+                    const int t = k0 + grp * 8 + mt * 4 + i;
                     const float v = (t <= klim[nt]) ? s[mt][nt][i] : -INFINITY;
                     p[mt * 4 + i] = v;
                     mx = fmaxf(mx, v);
@@ -276,17 +298,13 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
         }
 #pragma unroll
         for (int md = 0; md < MD; md++) {
-            const uint16_t *vr = &Vb[(md * 16 + col) * VP + grp * 4];
-            const u32x2 lo = *(const u32x2 *)vr;         // keys 4g .. 4g+3
-            const u32x2 hi = *(const u32x2 *)(vr + 16);  // keys 16+4g .. 16+4g+3
-            const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            const int d = md * 16 + col;
+            const bf16x8 va = __builtin_bit_cast(
+                bf16x8, *(const u32x4 *)&Vb[d * kKeyBlock + ((grp ^ pf_vswz(d)) << 3)]);
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 acc[nt][md] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt], acc[nt][md], 0, 0, 0);
         }
-        if (has_next) store_block(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
     }
 
     // ---- normalise and write ----------------------------------------------
@@ -320,11 +338,11 @@ hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, 
     if (n_work <= 0) return hipSuccess;
     if (ev0) (void)hipEventRecord(ev0, s);
     if (src == kSrcPaged && hd == 128)
-        prefill_kernel<128, 128, kSrcPaged><<<n_work, 256, 0, s>>>(a);
+        prefill_kernel<128, 128, kSrcPaged><<<n_work, 256, 0, s>>>(a, a.table);
     else if (src == kSrcPaged && hd == 64)
-        prefill_kernel<64, 64, kSrcPaged><<<n_work, 256, 0, s>>>(a);
+        prefill_kernel<64, 64, kSrcPaged><<<n_work, 256, 0, s>>>(a, a.table);
     else if (src == kSrcDense && hd == 128)
-        prefill_kernel<192, 128, kSrcDense><<<n_work, 256, 0, s>>>(a);
+        prefill_kernel<192, 128, kSrcDense><<<n_work, 256, 0, s>>>(a, a.table);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

@@ -383,6 +383,41 @@ int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
     return best;
 }
 
+// Prefill work order for the 8 XCDs.  Work-group b runs on XCD b % 8 and
+// each XCD has its own L2, so all query tiles of one (sequence, head group)
+// -- which stream the same K/V blocks in the same order -- are placed on one
+// XCD at consecutive positions: the XCD then fetches each block from HBM once.
+// Groups go to the least-loaded XCD, largest first; shorter XCD lists are
+// padded with empty items (row -1).
+constexpr int kXcds = 8;
+std::vector<int4> xcd_order(const std::vector<std::vector<int4>> &groups,
+                            const std::vector<double> &cost) {
+    std::vector<int> idx(groups.size());
+    for (size_t i = 0; i < idx.size(); i++) idx[i] = (int)i;
+    std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return cost[a] > cost[b]; });
+    std::vector<std::vector<int4>> lists(kXcds);
+    std::vector<double> load(kXcds, 0.0);
+    for (int g : idx) {
+        const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+        load[x] += cost[g];
+        lists[x].insert(lists[x].end(), groups[g].begin(), groups[g].end());
+    }
+    size_t n = 0;
+    for (auto &l : lists) n = std::max(n, l.size());
+    std::vector<int4> out(n * kXcds, int4{-1, 0, 0, 0});
+    for (int x = 0; x < kXcds; x++)
+        for (size_t i = 0; i < lists[x].size(); i++) out[i * kXcds + x] = lists[x][i];
+    return out;
+}
+
+// Keys a prefill query tile attends (its work is proportional).
+int tile_keys(const AttRow &r, int mask_mode, int toks, int qt) {
+    const int jmax = std::min(r.nq - 1, qt * toks + toks - 1);
+    if (mask_mode == RLX_MASK_CAUSAL) return std::min(r.len, r.len - r.nq + jmax + 1);
+    if (mask_mode == RLX_MASK_REF && r.nq == r.len) return jmax + 1;
+    return r.len;
+}
+
 // One AttRow per sequence, or -- with qtile > 0 (GQA decode kernel only) --
 // one per tile of at most qtile queries, each with its own context splits.
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
@@ -752,12 +787,20 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
             return rc;
         const int toks = 128 / G;
-        std::vector<int4> work;
+        std::vector<std::vector<int4>> groups;
+        std::vector<double> cost;
         for (int i = 0; i < n_seqs; i++) {
             const int tiles = (rows[i].nq + toks - 1) / toks;
-            for (int kvh = 0; kvh < c->kvh; kvh++)
-                for (int qt = tiles - 1; qt >= 0; qt--) work.push_back(int4{i, kvh, qt, 0});
+            for (int kvh = 0; kvh < c->kvh; kvh++) {
+                groups.emplace_back();
+                cost.push_back(0.0);
+                for (int qt = tiles - 1; qt >= 0; qt--) {
+                    groups.back().push_back(int4{i, kvh, qt, 0});
+                    cost.back() += tile_keys(rows[i], mask_mode, toks, qt);
+                }
+            }
         }
+        const std::vector<int4> work = xcd_order(groups, cost);
         if ((rc = flush_patches(c))) return rc;
         Blob b;
         size_t o_r = b.add(rows), o_w = b.add(work);
@@ -859,7 +902,8 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
             return rc;
         std::vector<int2> dwork;
-        std::vector<int4> pwork;
+        std::vector<std::vector<int4>> pgroups;
+        std::vector<double> pcost;
         int64_t tok_off = 0;
         for (int i = 0; i < n_seqs; i++) {
             const int Tp = (rows[i].len + 127) / 128 * 128;
@@ -867,10 +911,17 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
             rows[i].nsplit = Tp;              // padded length (row pitch of V^T)
             for (int t0 = 0; t0 < Tp; t0 += 128) dwork.push_back(int2{i, t0});
             const int tiles = (rows[i].nq + 127) / 128;
-            for (int h = 0; h < num_heads; h++)
-                for (int qt = tiles - 1; qt >= 0; qt--) pwork.push_back(int4{i, h, qt, 0});
+            for (int h = 0; h < num_heads; h++) {
+                pgroups.emplace_back();
+                pcost.push_back(0.0);
+                for (int qt = tiles - 1; qt >= 0; qt--) {
+                    pgroups.back().push_back(int4{i, h, qt, 0});
+                    pcost.back() += tile_keys(rows[i], mask_mode, 128, qt);
+                }
+            }
             tok_off += Tp;
         }
+        const std::vector<int4> pwork = xcd_order(pgroups, pcost);
         if (tok_off * num_heads * 128 > INT32_MAX)
             return fail(RLX_ERR_UNSUPPORTED, "MLA prefill call too large (%lld expanded rows)", (long long)tok_off);
         if ((rc = flush_patches(c))) return rc;
