@@ -440,17 +440,21 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": r["desc"],
-        "hbm_gbs": round(r["step_hbm_gbs"], 1),
-        "hbm_frac": round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4),
         "roofline": {"bound": r["bound"], "achieved": round(r["kernel_rate"], 1),
                      "peak": HBM_PEAK_GBS if r["bound"] == "hbm" else MFMA_BF16_PEAK_TFS,
                      "unit": r["rate_unit"], "frac": round(r["rate_frac"], 4),
                      "traffic": traffic, "kernel": r["kernel"],
                      "kernel_avg_us": round(r["kernel_avg_us"], 2),
-                     "algorithmic_bytes": r["kernel_bytes"]},
+                     ("algorithmic_flops" if r["bound"] == "mfma" else "algorithmic_bytes"): r["kernel_bytes"]},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
+    if r["bound"] == "hbm":
+        # whole-step cache bytes over wall time (append, attend, merge, rollback)
+        line["hbm_gbs"] = round(r["step_hbm_gbs"], 1)
+        line["hbm_frac"] = round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4)
+    else:
+        line["step_tflops_declared"] = round(r["step_tflops"], 1)
     print(json.dumps(line), flush=True)
 
 
