@@ -130,6 +130,18 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
 constexpr int kSrcPaged = 0;
 constexpr int kSrcDense = 1;
 
+// Two floats to packed bf16 with the hardware conversion (v_cvt_pk_bf16_f32,
+// round to nearest even): the same bits as bf16_rne for every non-NaN
+// input.  For attention weights only; cache bytes keep bf16_rne, whose NaN
+// behaviour is the reference's.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+    const bf16x2_t v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
 // ---- global-to-LDS rings ----------------------------------------------
 
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and

@@ -96,6 +96,39 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
     const int nblk = (kend + kKeyBlock - 1) / kKeyBlock;
 
     // ---- ring loads of key block j into stage j % S -------------------------
+    // Load i of a wave fills physical chunks (4i + wave) * 64 + lane of a
+    // stage: loads i < NK carry K rows, the rest V^T rows.  The same lane
+    // fetches the same (row, chunk) of every block, so its offsets are fixed
+    // here and each block only adds wave-uniform page bases.
+    constexpr int NK = K_CH / 256;
+    constexpr int NV = PER_WAVE - NK;
+    static_assert(K_CH % 256 == 0, "K loads must not straddle the V^T rows");
+    int k_row[NK], k_lc[NK];
+    int v_d[NV], v_lc[NV];
+    int64_t k_off[NK], v_off[NV];
+#pragma unroll
+    for (int i = 0; i < NK; i++) {
+        const int p = (i * 4 + wave) * 64 + lane;
+        k_row[i] = p / KCH;
+        k_lc[i] = (p - k_row[i] * KCH) ^ pf_kswz(k_row[i]);
+        const int r16 = k_row[i] & 15;
+        if (SRC == kSrcPaged)
+            k_off[i] = (int64_t)r16 * DQK + k_lc[i] * 8;
+        else if (k_lc[i] < 16)
+            k_off[i] = (int64_t)k_row[i] * 128 + k_lc[i] * 8;
+        else
+            k_off[i] = (int64_t)r16 * kMlaRow + kMlaDc + (k_lc[i] - 16) * 8;
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int q = ((NK + i) * 4 + wave) * 64 + lane - K_CH;
+        v_d[i] = q >> 2;
+        v_lc[i] = (q & 3) ^ pf_vswz(v_d[i]);
+        if (SRC == kSrcPaged)
+            v_off[i] = (int64_t)v_d[i] * a.P + (v_lc[i] & 1) * 8;
+        else
+            v_off[i] = (int64_t)v_d[i] * R.nsplit + v_lc[i] * 8;
+    }
     auto issue_block = [&](int j) {
         const int k0 = j * kKeyBlock;
         // Keys k0..k0+15 and k0+16..k0+31 each lie in one page (P is a
@@ -105,37 +138,72 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
             pg0 = table[R.tab + k0 / a.P];
             pg1 = (k0 + 16 < R.len) ? table[R.tab + (k0 + 16) / a.P] : pg0;
         }
+        const int s0 = k0 % a.P, s1 = (k0 + 16) % a.P;
         const uint32_t stage = ring_lds + (uint32_t)((j % S) * ST_CH * 16);
+        if (k0 + kKeyBlock <= R.len) {
+            // Every key of the block is live.
 #pragma unroll
-        for (int i = 0; i < PER_WAVE; i++) {
-            const int base = (i * 4 + wave) * 64;  // first physical chunk (wave-uniform)
-            const int p = base + lane;
-            const uint16_t *g;
-            if (base < K_CH) {
-                const int row = p / KCH;
-                const int lc = (p - row * KCH) ^ pf_kswz(row);
-                const int t = min(k0 + row, R.len - 1);
-                const int pg = (t - k0 < 16) ? pg0 : pg1;
-                if (SRC == kSrcPaged)
-                    g = a.kpool + (((int64_t)pg * a.KVH + hg) * a.P + (t % a.P)) * DQK + lc * 8;
-                else if (lc < 16)
-                    g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
-                else
-                    g = a.kpool + ((int64_t)pg * a.P + (t % a.P)) * kMlaRow + kMlaDc + (lc - 16) * 8;
-            } else {
-                const int q = p - K_CH;
-                const int d = q >> 2;
-                const int lc = (q & 3) ^ pf_vswz(d);
-                int t = k0 + lc * 8;
-                if (t >= R.len) t = k0;  // whole chunk past the end: its entries get zeroed
+            for (int i = 0; i < NK; i++) {
+                const bool hi = k_row[i] >= 16;
+                const uint16_t *g;
                 if (SRC == kSrcPaged) {
-                    const int pg = (t - k0 < 16) ? pg0 : pg1;
-                    g = a.vpool + (((int64_t)pg * a.KVH + hg) * DV + d) * a.P + (t % a.P);
+                    const uint16_t *b0 = a.kpool + (((int64_t)pg0 * a.KVH + hg) * a.P + s0) * DQK;
+                    const uint16_t *b1 = a.kpool + (((int64_t)pg1 * a.KVH + hg) * a.P + s1) * DQK;
+                    g = (hi ? b1 : b0) + k_off[i];
+                } else if (k_lc[i] < 16) {
+                    g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + k0) * 128 + k_off[i];
                 } else {
-                    g = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
+                    const uint16_t *b0 = a.kpool + ((int64_t)pg0 * a.P + s0) * kMlaRow;
+                    const uint16_t *b1 = a.kpool + ((int64_t)pg1 * a.P + s1) * kMlaRow;
+                    g = (hi ? b1 : b0) + k_off[i];
                 }
+                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + wave) * 64) * 16));
             }
-            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)base * 16));
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const uint16_t *g;
+                if (SRC == kSrcPaged) {
+                    const bool hi = v_lc[i] >= 2;
+                    const uint16_t *b0 = a.vpool + ((int64_t)pg0 * a.KVH + hg) * DV * a.P + s0;
+                    const uint16_t *b1 = a.vpool + ((int64_t)pg1 * a.KVH + hg) * DV * a.P + s1;
+                    g = (hi ? b1 : b0) + v_off[i];
+                } else {
+                    g = a.vt + (int64_t)R.part * a.H * 128 + (int64_t)hg * 128 * R.nsplit + k0 + v_off[i];
+                }
+                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(((NK + i) * 4 + wave) * 64) * 16));
+            }
+            return;
+        }
+        // Last block of the sequence: rows past the live length repeat the
+        // last live key; V^T chunks wholly past it load chunk 0 (their
+        // entries are zeroed in LDS before use).
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+            const int row = k_row[i], lc = k_lc[i];
+            const int t = min(k0 + row, R.len - 1);
+            const int pg = (t - k0 < 16) ? pg0 : pg1;
+            const uint16_t *g;
+            if (SRC == kSrcPaged)
+                g = a.kpool + (((int64_t)pg * a.KVH + hg) * a.P + (t % a.P)) * DQK + lc * 8;
+            else if (lc < 16)
+                g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
+            else
+                g = a.kpool + ((int64_t)pg * a.P + (t % a.P)) * kMlaRow + kMlaDc + (lc - 16) * 8;
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + wave) * 64) * 16));
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int d = v_d[i];
+            int t = k0 + v_lc[i] * 8;
+            if (t >= R.len) t = k0;
+            const uint16_t *g;
+            if (SRC == kSrcPaged) {
+                const int pg = (t - k0 < 16) ? pg0 : pg1;
+                g = a.vpool + (((int64_t)pg * a.KVH + hg) * DV + d) * a.P + (t % a.P);
+            } else {
+                g = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
+            }
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(((NK + i) * 4 + wave) * 64) * 16));
         }
     };
     // Wait for this wave's loads of a block, given how many blocks it issued
@@ -147,6 +215,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
     for (int j = 0; j < S - 1 && j < nblk; j++) issue_block(j);
 
     // ---- query operand and per-row key limits -----------------------------
+    // Rows past the tile's queries load a valid row (no divergent branch
+    // around the loads) and are zeroed after.
     bf16x8 qb[2][KS];
     int klim[2];
     bool rvalid[2];
@@ -160,44 +230,53 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
         rhead[nt] = h;
         rvalid[nt] = j < R.nq;
         klim[nt] = rvalid[nt] ? pf_limit(a.mask_mode, R.len, R.nq, j) : -1;
+        const int jc = min(j, R.nq - 1);
+        const float zs = rvalid[nt] ? a.qscale : 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
             const int d0 = ks * 32 + grp * 8;
-            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (rvalid[nt]) {
-                const void *src;
-                int64_t off;
-                if (SRC == kSrcPaged || d0 < 128) {
-                    const int D = (SRC == kSrcPaged) ? DQK : 128;
-                    src = a.q;
-                    off = (a.layout == kLayoutSHD || SRC == kSrcDense)
-                              ? ((int64_t)(R.qrow + j) * a.H + h) * D + d0
-                              : ((int64_t)R.qrow * a.H + (int64_t)h * R.nq + j) * D + d0;
-                } else {
-                    src = a.q2;
-                    off = ((int64_t)(R.qrow + j) * a.H + h) * kMlaDr + (d0 - 128);
-                }
-                if (a.q_bf16) {
-                    const u32x4 raw = *(const u32x4 *)((const uint16_t *)src + off);
+            float v[8];
+            const void *src;
+            int64_t off;
+            if (SRC == kSrcPaged || d0 < 128) {
+                const int D = (SRC == kSrcPaged) ? DQK : 128;
+                src = a.q;
+                off = (a.layout == kLayoutSHD || SRC == kSrcDense)
+                          ? ((int64_t)(R.qrow + jc) * a.H + h) * D + d0
+                          : ((int64_t)R.qrow * a.H + (int64_t)h * R.nq + jc) * D + d0;
+            } else {
+                src = a.q2;
+                off = ((int64_t)(R.qrow + jc) * a.H + h) * kMlaDr + (d0 - 128);
+            }
+            if (a.q_bf16) {
+                const u32x4 raw = *(const u32x4 *)((const uint16_t *)src + off);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        v[2 * i] = bf16_f32((uint16_t)(raw[i] & 0xFFFFu));
-                        v[2 * i + 1] = bf16_f32((uint16_t)(raw[i] >> 16));
-                    }
-                } else {
-                    const float4 *f = (const float4 *)((const float *)src + off);
-                    const float4 x = f[0], y = f[1];
-                    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-                    v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+                for (int i = 0; i < 4; i++) {
+                    v[2 * i] = bf16_f32((uint16_t)(raw[i] & 0xFFFFu));
+                    v[2 * i + 1] = bf16_f32((uint16_t)(raw[i] >> 16));
                 }
+            } else {
+                const float4 *f = (const float4 *)((const float *)src + off);
+                const float4 x = f[0], y = f[1];
+                v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+                v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
             }
             u32x4 w;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                w[i] = (uint32_t)bf16_rne(v[2 * i] * a.qscale) | ((uint32_t)bf16_rne(v[2 * i + 1] * a.qscale) << 16);
+                w[i] = (uint32_t)bf16_rne(v[2 * i] * zs) | ((uint32_t)bf16_rne(v[2 * i + 1] * zs) << 16);
             qb[nt][ks] = __builtin_bit_cast(bf16x8, w);
         }
     }
+    // Smallest key limit over this wave's valid rows: blocks entirely below
+    // it need no mask.
+    int kmin = 0x7fffffff;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+        if (rvalid[nt]) kmin = min(kmin, klim[nt]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) kmin = min(kmin, __shfl_xor(kmin, off));
+    kmin = __builtin_amdgcn_readfirstlane(kmin);
     // Make the compiler complete the query loads here, once: the ring loads
     // are invisible to it, so a wait it placed inside the key loop would
     // also drain the ring on every block.
@@ -255,6 +334,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
                     s[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], s[mt][nt], 0, 0, 0);
             }
         }
+        const bool need_mask = k0 + kKeyBlock - 1 > kmin;
         bf16x8 pb[2];
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
@@ -263,12 +343,14 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
 #pragma unroll
             for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int t = k0 + grp * 8 + mt * 4 + i;
-                    const float v = (t <= klim[nt]) ? s[mt][nt][i] : -INFINITY;
-                    p[mt * 4 + i] = v;
-                    mx = fmaxf(mx, v);
-                }
+                for (int i = 0; i < 4; i++) p[mt * 4 + i] = s[mt][nt][i];
+            if (need_mask) {
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (k0 + grp * 8 + i > klim[nt]) p[i] = -INFINITY;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) mx = fmaxf(mx, p[i]);
             mx = pf_max16(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             float c = 1.f;
@@ -281,19 +363,19 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
                 for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(p[i] - m_new);
             }
             // The P.V product consumes bf16 weights: normalise by the same ones.
-            float ps = 0.f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                p[i] = bf16_f32(bf16_rne(p[i]));
-                ps += p[i];
-            }
-            l_part[nt] = l_part[nt] * c + ps;
-            m_run[nt] = m_new;
-#pragma unroll
-            for (int md = 0; md < MD; md++) acc[nt][md] *= c;
             u32x4 w;
 #pragma unroll
-            for (int i = 0; i < 4; i++) w[i] = (uint32_t)bf16_rne(p[2 * i]) | ((uint32_t)bf16_rne(p[2 * i + 1]) << 16);
+            for (int i = 0; i < 4; i++) w[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
+            float ps = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ps += bf16_lo(w[i]) + bf16_hi(w[i]);
+            l_part[nt] = l_part[nt] * c + ps;
+            m_run[nt] = m_new;
+            // Rescale only when some row's running max moved (c != 1).
+            if (__builtin_amdgcn_ballot_w64(c != 1.f)) {
+#pragma unroll
+                for (int md = 0; md < MD; md++) acc[nt][md] *= c;
+            }
             pb[nt] = __builtin_bit_cast(bf16x8, w);
         }
 #pragma unroll
