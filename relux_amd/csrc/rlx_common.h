@@ -172,6 +172,9 @@ __device__ __forceinline__ void ring_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Query rows (token x head pairs of one head group) per prefill work-group.
+constexpr int kPrefillRows = 256;
+
 struct PrefillArgs {
     const uint16_t *kpool;  // paged: K row pages; dense: latent pool (rope keys)
     const uint16_t *vpool;  // paged: V dim-major pages

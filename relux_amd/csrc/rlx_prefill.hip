@@ -4,11 +4,11 @@
 //
 // Work item = (sequence, head group, query tile).  A head group is one kv
 // head with its G = H/KVH query heads (GQA) or one head (MLA, decompressed).
-// A tile holds 128 query rows, query-major: row r = (token r / G, head r % G),
+// A tile holds 256 query rows, query-major: row r = (token r / G, head r % G),
 // so the G heads that share a kv head share every K/V byte the tile loads.
-// 4 waves, wave w owns rows [32w, 32w+32) as two 16-wide N tiles.
+// 8 waves, wave w owns rows [32w, 32w+32) as two 16-wide N tiles.
 //
-// Keys stream in 32-key blocks through a 3-stage LDS ring filled straight
+// Keys stream in 32-key blocks through a 4-stage LDS ring filled straight
 // from memory (16-byte global-to-LDS loads); each stage holds the block's K
 // rows and its V^T rows, both swizzled in 16-byte chunks so that the MFMA
 // operand reads are free of bank conflicts.  Per block and wave:
@@ -32,7 +32,8 @@
 
 namespace rlx {
 
-constexpr int kTileRows = 128;
+constexpr int kWaves = 8;                // 512 threads, 32 query rows per wave
+constexpr int kTileRows = 32 * kWaves;   // 256
 constexpr int kKeyBlock = 32;
 
 __device__ __forceinline__ float pf_max16(float v) {
@@ -63,7 +64,7 @@ template <int DQK, int DV, int SRC>
 // The page table is a separate __restrict__ argument so that the compiler
 // may read it through the scalar cache: a vector load would be ordered
 // behind the in-flight ring loads by the waits the compiler inserts.
-__global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
+__global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs a,
                                                          const int32_t *__restrict__ table) {
     constexpr int KS = DQK / 32;             // score k-steps
     constexpr int MD = DV / 16;              // value m-tiles
@@ -71,9 +72,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
     constexpr int K_CH = kKeyBlock * KCH;    // K chunks per stage
     constexpr int V_CH = DV * kKeyBlock / 8; // V^T chunks per stage
     constexpr int ST_CH = K_CH + V_CH;
-    constexpr int PER_WAVE = ST_CH / 256;    // ring loads per wave per block
-    constexpr int S = 3;                     // ring stages
-    static_assert(ST_CH % 256 == 0 && K_CH % 64 == 0 && KCH % 8 == 0, "stage shape");
+    // Waves 0-3 load the K rows of a block, waves 4-7 its V^T rows.
+    constexpr int NK = K_CH / 256;           // K ring loads per K wave per block
+    constexpr int NV = V_CH / 256;           // V^T ring loads per V wave per block
+    constexpr int S = 4;                     // ring stages (one work-group per CU)
+    static_assert(K_CH % 256 == 0 && V_CH % 256 == 0 && KCH % 8 == 0, "stage shape");
     __shared__ __attribute__((aligned(16))) uint16_t ring[S * ST_CH * 8];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -96,19 +99,18 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
     const int nblk = (kend + kKeyBlock - 1) / kKeyBlock;
 
     // ---- ring loads of key block j into stage j % S -------------------------
-    // Load i of a wave fills physical chunks (4i + wave) * 64 + lane of a
-    // stage: loads i < NK carry K rows, the rest V^T rows.  The same lane
+    // K wave w (0-3) fills K chunks (4i + w) * 64 + lane of a stage, V wave
+    // w (4-7) fills V^T chunks (4i + w - 4) * 64 + lane.  The same lane
     // fetches the same (row, chunk) of every block, so its offsets are fixed
     // here and each block only adds wave-uniform page bases.
-    constexpr int NK = K_CH / 256;
-    constexpr int NV = PER_WAVE - NK;
-    static_assert(K_CH % 256 == 0, "K loads must not straddle the V^T rows");
+    const bool kwave = wave < 4;
+    const int w4 = wave & 3;
     int k_row[NK], k_lc[NK];
     int v_d[NV], v_lc[NV];
     int64_t k_off[NK], v_off[NV];
 #pragma unroll
     for (int i = 0; i < NK; i++) {
-        const int p = (i * 4 + wave) * 64 + lane;
+        const int p = (i * 4 + w4) * 64 + lane;
         k_row[i] = p / KCH;
         k_lc[i] = (p - k_row[i] * KCH) ^ pf_kswz(k_row[i]);
         const int r16 = k_row[i] & 15;
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
     }
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int q = ((NK + i) * 4 + wave) * 64 + lane - K_CH;
+        const int q = (i * 4 + w4) * 64 + lane;
         v_d[i] = q >> 2;
         v_lc[i] = (q & 3) ^ pf_vswz(v_d[i]);
         if (SRC == kSrcPaged)
@@ -142,6 +144,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
         const uint32_t stage = ring_lds + (uint32_t)((j % S) * ST_CH * 16);
         if (k0 + kKeyBlock <= R.len) {
             // Every key of the block is live.
+            if (kwave) {
 #pragma unroll
             for (int i = 0; i < NK; i++) {
                 const bool hi = k_row[i] >= 16;
@@ -157,8 +160,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
                     const uint16_t *b1 = a.kpool + ((int64_t)pg1 * a.P + s1) * kMlaRow;
                     g = (hi ? b1 : b0) + k_off[i];
                 }
-                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + wave) * 64) * 16));
+                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + w4) * 64) * 16));
             }
+            } else {
 #pragma unroll
             for (int i = 0; i < NV; i++) {
                 const uint16_t *g;
@@ -170,13 +174,15 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
                 } else {
                     g = a.vt + (int64_t)R.part * a.H * 128 + (int64_t)hg * 128 * R.nsplit + k0 + v_off[i];
                 }
-                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(((NK + i) * 4 + wave) * 64) * 16));
+                lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(K_CH + (i * 4 + w4) * 64) * 16));
+            }
             }
             return;
         }
         // Last block of the sequence: rows past the live length repeat the
         // last live key; V^T chunks wholly past it load chunk 0 (their
         // entries are zeroed in LDS before use).
+        if (kwave) {
 #pragma unroll
         for (int i = 0; i < NK; i++) {
             const int row = k_row[i], lc = k_lc[i];
@@ -189,8 +195,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
                 g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
             else
                 g = a.kpool + ((int64_t)pg * a.P + (t % a.P)) * kMlaRow + kMlaDc + (lc - 16) * 8;
-            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + wave) * 64) * 16));
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + w4) * 64) * 16));
         }
+        } else {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int d = v_d[i];
@@ -203,14 +210,26 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
             } else {
                 g = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
             }
-            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(((NK + i) * 4 + wave) * 64) * 16));
+            lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)(K_CH + (i * 4 + w4) * 64) * 16));
+        }
         }
     };
     // Wait for this wave's loads of a block, given how many blocks it issued
     // after it (loads retire in issue order).
     auto wait_block = [&](int ahead) {
-        if (ahead >= 1) RLX_WAIT_VM(PER_WAVE); else RLX_WAIT_VM(0);
+        const int n = ahead * (kwave ? NK : NV);
+        switch (n) {
+            case 0: RLX_WAIT_VM(0); break;
+            case 1: RLX_WAIT_VM(1); break;
+            case 2: RLX_WAIT_VM(2); break;
+            case 3: RLX_WAIT_VM(3); break;
+            case 4: RLX_WAIT_VM(4); break;
+            case 6: RLX_WAIT_VM(6); break;
+            case 8: RLX_WAIT_VM(8); break;
+            default: RLX_WAIT_VM(0); break;
+        }
     };
+    static_assert((S - 2) * NK <= 6 && (S - 2) * NV <= 6, "wait table");
 
     for (int j = 0; j < S - 1 && j < nblk; j++) issue_block(j);
 
@@ -310,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a,
             // the live length (they hold stale or repeated cache bytes).
             uint16_t *Vw = ring + (j % S) * ST_CH * 8 + K_CH * 8;
             const int live = R.len - k0;
-            for (int e = tid; e < DV * kKeyBlock; e += 256) {
+            for (int e = tid; e < DV * kKeyBlock; e += 64 * kWaves) {
                 const int d = e / kKeyBlock, kk = e - d * kKeyBlock;
                 if (kk >= live) Vw[d * kKeyBlock + (((kk >> 3) ^ pf_vswz(d)) << 3) + (kk & 7)] = 0;
             }
@@ -420,11 +439,11 @@ hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, 
     if (n_work <= 0) return hipSuccess;
     if (ev0) (void)hipEventRecord(ev0, s);
     if (src == kSrcPaged && hd == 128)
-        prefill_kernel<128, 128, kSrcPaged><<<n_work, 256, 0, s>>>(a, a.table);
+        prefill_kernel<128, 128, kSrcPaged><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
     else if (src == kSrcPaged && hd == 64)
-        prefill_kernel<64, 64, kSrcPaged><<<n_work, 256, 0, s>>>(a, a.table);
+        prefill_kernel<64, 64, kSrcPaged><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
     else if (src == kSrcDense && hd == 128)
-        prefill_kernel<192, 128, kSrcDense><<<n_work, 256, 0, s>>>(a, a.table);
+        prefill_kernel<192, 128, kSrcDense><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
     else
         return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

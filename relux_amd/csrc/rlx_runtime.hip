@@ -392,6 +392,15 @@ int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
 constexpr int kXcds = 8;
 std::vector<int4> xcd_order(const std::vector<std::vector<int4>> &groups,
                             const std::vector<double> &cost) {
+    static const bool plain = [] {
+        const char *e = getenv("RLX_PREFILL_ORDER");  // tuning override: "plain"
+        return e && strcmp(e, "plain") == 0;
+    }();
+    if (plain) {
+        std::vector<int4> out;
+        for (auto &g : groups) out.insert(out.end(), g.begin(), g.end());
+        return out;
+    }
     std::vector<int> idx(groups.size());
     for (size_t i = 0; i < idx.size(); i++) idx[i] = (int)i;
     std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return cost[a] > cost[b]; });
@@ -776,17 +785,17 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     // The FA2 prefill kernel covers head_dim 64/128 with G dividing 128;
     // other shapes tile their queries through the decode kernel, whose
     // work-group holds at most 32 query rows of one kv head.
-    const bool fa2 = (c->hd == 64 || c->hd == 128) && 128 % G == 0;
+    const bool fa2 = (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
     if (max_qr > 32 && !fa2 && G > 32)
         return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most 32)", G, c->hd);
     if (max_qr > 32 && fa2) {
-        // Chunked prefill / long verify: FA2 tiles of 128 query rows.
+        // Chunked prefill / long verify: FA2 tiles of kPrefillRows query rows.
         std::vector<AttRow> rows;
         std::vector<int2> unused;
         int total_q = 0, mnq = 0, parts = 0;
         if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
             return rc;
-        const int toks = 128 / G;
+        const int toks = kPrefillRows / G;
         std::vector<std::vector<int4>> groups;
         std::vector<double> cost;
         for (int i = 0; i < n_seqs; i++) {
@@ -893,7 +902,7 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const int max_qr = num_heads * max_nq;
     if (max_qr > 32) {
         // Chunked prefill: expand the latents into per-head K_c / V^T, then
-        // FA2 tiles of 128 query tokens per head.
+        // FA2 tiles of kPrefillRows query tokens per head.
         if (head_dim != 128)
             return fail(RLX_ERR_UNSUPPORTED, "MLA prefill supports head_dim 128 (got %d)", head_dim);
         std::vector<AttRow> rows;
@@ -910,13 +919,13 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
             rows[i].part = (int32_t)tok_off;  // token offset in the expanded buffers
             rows[i].nsplit = Tp;              // padded length (row pitch of V^T)
             for (int t0 = 0; t0 < Tp; t0 += 128) dwork.push_back(int2{i, t0});
-            const int tiles = (rows[i].nq + 127) / 128;
+            const int tiles = (rows[i].nq + kPrefillRows - 1) / kPrefillRows;
             for (int h = 0; h < num_heads; h++) {
                 pgroups.emplace_back();
                 pcost.push_back(0.0);
                 for (int qt = tiles - 1; qt >= 0; qt--) {
                     pgroups.back().push_back(int4{i, h, qt, 0});
-                    pcost.back() += tile_keys(rows[i], mask_mode, 128, qt);
+                    pcost.back() += tile_keys(rows[i], mask_mode, kPrefillRows, qt);
                 }
             }
             tok_off += Tp;
