@@ -354,7 +354,15 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             }
         }
         const bool need_mask = k0 + kKeyBlock - 1 > kmin;
-        bf16x8 pb[2];
+        // V^T fragments of the block (issued early: their LDS latency hides
+        // behind the softmax); each N tile's P.V follows its own softmax so
+        // that tile 0's MFMAs overlap tile 1's softmax.
+        bf16x8 va[MD];
+#pragma unroll
+        for (int md = 0; md < MD; md++) {
+            const int d = md * 16 + col;
+            va[md] = __builtin_bit_cast(bf16x8, *(const u32x4 *)&Vb[d * kKeyBlock + ((grp ^ pf_vswz(d)) << 3)]);
+        }
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
             float p[8];  // keys k0 + 8*grp + i
@@ -395,16 +403,10 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 #pragma unroll
                 for (int md = 0; md < MD; md++) acc[nt][md] *= c;
             }
-            pb[nt] = __builtin_bit_cast(bf16x8, w);
-        }
+            const bf16x8 pbt = __builtin_bit_cast(bf16x8, w);
 #pragma unroll
-        for (int md = 0; md < MD; md++) {
-            const int d = md * 16 + col;
-            const bf16x8 va = __builtin_bit_cast(
-                bf16x8, *(const u32x4 *)&Vb[d * kKeyBlock + ((grp ^ pf_vswz(d)) << 3)]);
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++)
-                acc[nt][md] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nt], acc[nt][md], 0, 0, 0);
+            for (int md = 0; md < MD; md++)
+                acc[nt][md] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[md], pbt, acc[nt][md], 0, 0, 0);
         }
     }
 
