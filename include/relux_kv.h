@@ -98,7 +98,7 @@ int32_t rlx_cache_kernel_time(void *cache, float *total_ms, int32_t *count);
  * NewKVCacheSized(numLayers, maxLen, numKVHeads, headDim, BFloat16)
  * (kvcache.go:66-93): capacity per sequence is max_pages_per_seq *
  * page_tokens tokens; pool_pages pages per layer are shared by up to
- * max_seqs sequences.  head_dim in {64, 128}; page_tokens a multiple of 16. */
+ * max_seqs sequences.  head_dim in {16, 32, 64, 128}; page_tokens a multiple of 16. */
 int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t page_tokens,
                       int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
 
