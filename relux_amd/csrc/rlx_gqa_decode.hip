@@ -106,6 +106,15 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
         }
     }
 
+    // Smallest key limit of the work-group's columns: blocks entirely below
+    // it need no mask.
+    int kmin = klim[0];
+#pragma unroll
+    for (int nt = 1; nt < NQT; nt++) kmin = min(kmin, klim[nt]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) kmin = min(kmin, __shfl_xor(kmin, off));
+    kmin = __builtin_amdgcn_readfirstlane(kmin);
+
     float m_run[NQT], l_part[NQT];
     fl4 acc[NQT][MT];
 #pragma unroll
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
             }
         }
 
-        sh4 pb[NQT];
+        const bool need_mask = t0 + 15 > kmin;
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
             fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
@@ -163,13 +172,12 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
                     s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[ks]),
                                                                 __builtin_bit_cast(bf16x8, qb[nt][ks]), s, 0, 0, 0);
             }
-            float mx = -INFINITY;
+            if (need_mask) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int t = t0 + grp * 4 + i;
-                s[i] = (t <= klim[nt]) ? s[i] : -INFINITY;
-                mx = fmaxf(mx, s[i]);
+                for (int i = 0; i < 4; i++)
+                    if (t0 + grp * 4 + i > klim[nt]) s[i] = -INFINITY;
             }
+            float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
             mx = wave_max16(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             float c, p[4];
@@ -182,22 +190,21 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
                 for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
             }
             // The P.V product consumes bf16 weights: normalise by the same ones.
-#pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = bf16_f32(bf16_rne(p[i]));
-            l_part[nt] = l_part[nt] * c + ((p[0] + p[1]) + (p[2] + p[3]));
-            m_run[nt] = m_new;
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[nt][mt] *= c;
             u32x2 pw;
-            pw[0] = (uint32_t)bf16_rne(p[0]) | ((uint32_t)bf16_rne(p[1]) << 16);
-            pw[1] = (uint32_t)bf16_rne(p[2]) | ((uint32_t)bf16_rne(p[3]) << 16);
-            pb[nt] = __builtin_bit_cast(sh4, pw);
-        }
+            pw[0] = pack_bf16x2(p[0], p[1]);
+            pw[1] = pack_bf16x2(p[2], p[3]);
+            l_part[nt] = l_part[nt] * c + ((bf16_lo(pw[0]) + bf16_hi(pw[0])) + (bf16_lo(pw[1]) + bf16_hi(pw[1])));
+            m_run[nt] = m_new;
+            // Rescale only when some column's running max moved (c != 1).
+            if (__builtin_amdgcn_ballot_w64(c != 1.f)) {
 #pragma unroll
-        for (int nt = 0; nt < NQT; nt++)
+                for (int mt = 0; mt < MT; mt++) acc[nt][mt] *= c;
+            }
+            const sh4 pb = __builtin_bit_cast(sh4, pw);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
-                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(sh4, vr[mt]), pb[nt], acc[nt][mt], 0, 0, 0);
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(sh4, vr[mt]), pb, acc[nt][mt], 0, 0, 0);
+        }
     }
 
     // ---- merge the 4 waves of the work-group -------------------------------
