@@ -66,6 +66,76 @@ struct AttRow {
     int32_t qn;      // ... and its query count (q0 = 0, qn = nq untiled)
 };
 
+// ---- per-call plans in the kernel arguments --------------------------------
+// A small plan (the row list of a decode call, the patches and token
+// destinations of an append) travels inside the kernel arguments instead of
+// a staged host-to-device copy: one copy dispatch and one dependency less
+// per call.  Kernels that take a plan take it as their FIRST argument, so it
+// sits at offset 0 of the kernel-argument segment.
+constexpr int kPlanArgBytes = 2048;
+struct alignas(16) PlanArg {
+    unsigned char b[kPlanArgBytes];
+};
+struct NoPlan {
+    int unused;
+};
+template <bool ARG>
+struct PlanSel {
+    using T = NoPlan;
+};
+template <>
+struct PlanSel<true> {
+    using T = PlanArg;
+};
+typedef __attribute__((address_space(4))) const unsigned char kplan_byte;
+__device__ __forceinline__ kplan_byte *kernarg_plan() {
+    return (kplan_byte *)__builtin_amdgcn_kernarg_segment_ptr();
+}
+static_assert(sizeof(AttRow) == 32, "AttRow is 8 int32");
+template <bool ARG>
+__device__ __forceinline__ AttRow plan_row(const AttRow *rows, int i) {
+    if constexpr (ARG) {
+        const __attribute__((address_space(4))) int32_t *p =
+            (const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + i * sizeof(AttRow));
+        AttRow r;
+        r.tab = p[0];
+        r.len = p[1];
+        r.nq = p[2];
+        r.qrow = p[3];
+        r.nsplit = p[4];
+        r.part = p[5];
+        r.q0 = p[6];
+        r.qn = p[7];
+        return r;
+    } else {
+        return rows[i];
+    }
+}
+// (row, split) of a decode work-group: from the device work list, or -- plan
+// in the arguments -- by binary search of the rows' first partial slots
+// (wave-uniform scalar loads).
+template <bool ARG>
+__device__ __forceinline__ int2 plan_work(const int2 *work, int n_rows) {
+    if constexpr (ARG) {
+        // part is field 5 of each 8-int row
+        const __attribute__((address_space(4))) int32_t *p =
+            (const __attribute__((address_space(4))) int32_t *)kernarg_plan();
+        const int b = blockIdx.x;
+        int lo = 0, hi = n_rows - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (p[mid * 8 + 5] <= b)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        return int2{lo, b - p[lo * 8 + 5]};
+    } else {
+        return work[blockIdx.x];
+    }
+}
+
+
 // Upper bound on context splits of one sequence (the runtime sizes splits so
 // that it holds).
 constexpr int kMaxSplits = 1024;
@@ -118,8 +188,10 @@ hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t 
                              const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
                              uint16_t *kr_out, int P);
 
-hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
-                             const int32_t *table, const AttRow *rows, int n_rows,
+// plan: the rows in the kernel arguments (nullptr: rows and work on the device).
+hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
+                             const uint16_t *vpool, const int32_t *table, const AttRow *rows,
+                             int n_rows,
                              const int2 *work, int n_work, const void *q, int q_bf16,
                              int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,

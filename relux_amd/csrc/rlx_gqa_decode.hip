@@ -41,13 +41,13 @@ __device__ __forceinline__ int key_limit(int mask_mode, int len, int nq, int qi)
     return len - 1;
 }
 
-template <int D, int NQT>
+template <int D, int NQT, bool ARG>
 __global__ __launch_bounds__(256) void gqa_decode_kernel(
-    const uint16_t *__restrict__ kpool, const uint16_t *__restrict__ vpool,
-    const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
-    const int2 *__restrict__ work, const void *__restrict__ q, int q_bf16, int layout, int H,
-    int KVH, int P, int chunk, float qscale, int mask_mode, float *__restrict__ part_o,
-    float *__restrict__ part_ml) {
+    typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ kpool,
+    const uint16_t *__restrict__ vpool, const int32_t *__restrict__ table,
+    const AttRow *__restrict__ rows, const int2 *__restrict__ work, int n_rows,
+    const void *__restrict__ q, int q_bf16, int layout, int H, int KVH, int P, int chunk,
+    float qscale, int mask_mode, float *__restrict__ part_o, float *__restrict__ part_ml) {
     // head_dim 16 holds only 4 dims per lane: its score step is one MFMA
     // 16x16x16 (4 bf16 per lane); wider heads use 16x16x32 k-steps.
     constexpr bool K16 = (D == 16);
@@ -59,8 +59,8 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     const int wave = threadIdx.x >> 6;
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int2 wk = work[blockIdx.x];
-    const AttRow R = rows[wk.x];
+    const int2 wk = plan_work<ARG>(work, n_rows);
+    const AttRow R = plan_row<ARG>(rows, wk.x);
     const int kvh = blockIdx.y;
     const int G = H / KVH;
     const int QR = G * R.qn;  // query rows of this (tile of a) sequence
@@ -257,11 +257,12 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
 // 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the caller's layout and
 // dtype.  One block of D threads per query row; the merge weights are
 // computed once in LDS and every thread streams its dim across the splits.
+template <bool ARG>
 __global__ __launch_bounds__(128) void gqa_combine_kernel(
-    const AttRow *__restrict__ rows, const float *__restrict__ part_o,
-    const float *__restrict__ part_ml, void *__restrict__ out, int out_bf16, int layout, int H,
-    int KVH, int D, int QRP) {
-    const AttRow R = rows[blockIdx.x];
+    typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
+    const float *__restrict__ part_o, const float *__restrict__ part_ml, void *__restrict__ out,
+    int out_bf16, int layout, int H, int KVH, int D, int QRP) {
+    const AttRow R = plan_row<ARG>(rows, blockIdx.x);
     const int kvh = blockIdx.y;
     const int qr = blockIdx.z;
     const int G = H / KVH;
@@ -289,38 +290,43 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
     }
 }
 
-template <int D, int NQT>
-static hipError_t launch_gqa_t(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+template <int D, int NQT, bool ARG>
+static hipError_t launch_gqa_t(hipStream_t s, typename PlanSel<ARG>::T plan,
+                               const uint16_t *kpool, const uint16_t *vpool,
                                const int32_t *table, const AttRow *rows, int n_rows,
                                const int2 *work, int n_work, const void *q, int q_bf16,
                                int layout, int H, int KVH, int P, int chunk, float qscale,
                                int mask_mode, float *part_o, float *part_ml, void *out,
                                int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (ev0) (void)hipEventRecord(ev0, s);
-    gqa_decode_kernel<D, NQT><<<dim3(n_work, KVH), 256, 0, s>>>(
-        kpool, vpool, table, rows, work, q, q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode,
-        part_o, part_ml);
+    gqa_decode_kernel<D, NQT, ARG><<<dim3(n_work, KVH), 256, 0, s>>>(
+        plan, kpool, vpool, table, rows, work, n_rows, q, q_bf16, layout, H, KVH, P, chunk, qscale,
+        mask_mode, part_o, part_ml);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
-    gqa_combine_kernel<<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(rows, part_o, part_ml, out,
-                                                               out_bf16, layout, H, KVH, D,
-                                                               16 * NQT);
+    gqa_combine_kernel<ARG><<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(
+        plan, rows, part_o, part_ml, out, out_bf16, layout, H, KVH, D, 16 * NQT);
     return hipGetLastError();
 }
 
-hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
-                             const int32_t *table, const AttRow *rows, int n_rows,
-                             const int2 *work, int n_work, const void *q, int q_bf16,
+hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
+                             const uint16_t *vpool, const int32_t *table, const AttRow *rows,
+                             int n_rows, const int2 *work, int n_work, const void *q, int q_bf16,
                              int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
                              int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
 #define RLX_GQA_CASE(DD, NN)                                                                    \
     if (hd == DD && nqt == NN)                                                                  \
-        return launch_gqa_t<DD, NN>(s, kpool, vpool, table, rows, n_rows, work, n_work, q,      \
-                                    q_bf16, layout, H, KVH, P, chunk, qscale, mask_mode, part_o, \
-                                    part_ml, out, out_bf16, max_qr, ev0, ev1);
+        return plan ? launch_gqa_t<DD, NN, true>(s, *plan, kpool, vpool, table, rows, n_rows, work, \
+                                                 n_work, q, q_bf16, layout, H, KVH, P, chunk,   \
+                                                 qscale, mask_mode, part_o, part_ml, out,       \
+                                                 out_bf16, max_qr, ev0, ev1)                    \
+                    : launch_gqa_t<DD, NN, false>(s, NoPlan{0}, kpool, vpool, table, rows,      \
+                                                  n_rows, work, n_work, q, q_bf16, layout, H,   \
+                                                  KVH, P, chunk, qscale, mask_mode, part_o,     \
+                                                  part_ml, out, out_bf16, max_qr, ev0, ev1);
     RLX_GQA_CASE(128, 1)
     RLX_GQA_CASE(128, 2)
     RLX_GQA_CASE(64, 1)
@@ -336,14 +342,14 @@ hipError_t launch_gqa_decode(hipStream_t s, const uint16_t *kpool, const uint16_
 int gqa_decode_wgs_per_cu(int hd, int nqt) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
-    if (hd == 128 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 1>, 256, 0);
-    if (hd == 128 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 2>, 256, 0);
-    if (hd == 64 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 1>, 256, 0);
-    if (hd == 64 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 2>, 256, 0);
-    if (hd == 32 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 1>, 256, 0);
-    if (hd == 32 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 2>, 256, 0);
-    if (hd == 16 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 1>, 256, 0);
-    if (hd == 16 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 2>, 256, 0);
+    if (hd == 128 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 1, true>, 256, 0);
+    if (hd == 128 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 2, true>, 256, 0);
+    if (hd == 64 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 1, true>, 256, 0);
+    if (hd == 64 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 2, true>, 256, 0);
+    if (hd == 32 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 1, true>, 256, 0);
+    if (hd == 32 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 2, true>, 256, 0);
+    if (hd == 16 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 1, true>, 256, 0);
+    if (hd == 16 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 2, true>, 256, 0);
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 

@@ -856,17 +856,29 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const size_t po_bytes = (size_t)parts * c->kvh * QRP * c->hd * sizeof(float);
     const size_t pm_bytes = (size_t)parts * c->kvh * QRP * 2 * sizeof(float);
     if ((rc = ensure_ws(c, po_bytes + pm_bytes))) return rc;
-    Blob b;
-    size_t o_r = b.add(rows), o_w = b.add(work);
-    void *dev;
-    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    // Rows travel in the kernel arguments when they fit; otherwise rows and
+    // the work list are staged to the device.
+    PlanArg plan_arg;
+    const PlanArg *plan = nullptr;
+    const AttRow *d_rows = nullptr;
+    const int2 *d_work = nullptr;
+    if (rows.size() * sizeof(AttRow) <= sizeof(PlanArg)) {
+        memcpy(plan_arg.b, rows.data(), rows.size() * sizeof(AttRow));
+        plan = &plan_arg;
+    } else {
+        Blob b;
+        size_t o_r = b.add(rows), o_w = b.add(work);
+        void *dev;
+        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+        d_rows = (const AttRow *)((char *)dev + o_r);
+        d_work = (const int2 *)((char *)dev + o_w);
+    }
     if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
     const float qscale = scale * 1.4426950408889634f;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
-    HIP_TRY(launch_gqa_decode(c->stream, ls.pool0, ls.pool1, c->d_table,
-                              (const AttRow *)((char *)dev + o_r), (int)rows.size(),
-                              (const int2 *)((char *)dev + o_w), (int)work.size(), q,
+    HIP_TRY(launch_gqa_decode(c->stream, plan, ls.pool0, ls.pool1, c->d_table, d_rows,
+                              (int)rows.size(), d_work, (int)work.size(), q,
                               q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
                               chunk, qscale, mask_mode, nqt, (float *)c->ws,
                               (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
