@@ -51,13 +51,18 @@ __device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src
 // with one 16-byte store; V goes to a dim-major page (8 strided 2-byte
 // stores).  The first n_patch threads also apply the table patches; the
 // scatter itself takes its destinations from the plan, not the table.
-__global__ void kv_append_kernel(uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool,
-                                 int32_t *__restrict__ table, const Patch *__restrict__ patches,
-                                 int n_patch, const AppendTok *__restrict__ toks, int n_tok,
+template <bool ARG>
+__global__ void kv_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__restrict__ kpool,
+                                 uint16_t *__restrict__ vpool, int32_t *__restrict__ table,
+                                 const Patch *__restrict__ patches, int n_patch,
+                                 const AppendTok *__restrict__ toks, int tok_off, int n_tok,
                                  const void *__restrict__ k_src, const void *__restrict__ v_src,
                                  int src_bf16, int layout, int kvh, int hd, int P) {
     int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid < n_patch) table[patches[gid].idx] = patches[gid].val;
+    if (gid < n_patch) {
+        const Patch pt = plan_patch<ARG>(patches, (int)gid);
+        table[pt.idx] = pt.val;
+    }
     const int chunks = hd >> 3;
     const int64_t per_tok = (int64_t)kvh * chunks;
     if (gid >= (int64_t)n_tok * per_tok) return;
@@ -65,7 +70,7 @@ __global__ void kv_append_kernel(uint16_t *__restrict__ kpool, uint16_t *__restr
     const int rem = (int)(gid - (int64_t)t * per_tok);
     const int h = rem / chunks;
     const int d0 = (rem - h * chunks) * 8;
-    const AppendTok tk = toks[t];
+    const AppendTok tk = plan_tok<ARG>(toks, tok_off, t);
     const int j = t - tk.seq_row0;  // row within its sequence
     int64_t src_off;
     if (layout == kLayoutSHD)
@@ -85,33 +90,43 @@ __global__ void kv_append_kernel(uint16_t *__restrict__ kpool, uint16_t *__restr
     for (int i = 0; i < 8; i++) vd[(int64_t)i * P] = vv[i];
 }
 
-hipError_t launch_kv_append(hipStream_t s, uint16_t *kpool, uint16_t *vpool, int32_t *table,
-                            const Patch *patches, int n_patch, const AppendTok *toks, int n_tok,
-                            const void *k_src, const void *v_src, int src_bf16, int layout,
-                            int kvh, int hd, int P) {
+hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *kpool,
+                            uint16_t *vpool, int32_t *table, const Patch *patches, int n_patch,
+                            const AppendTok *toks, int n_tok, const void *k_src, const void *v_src,
+                            int src_bf16, int layout, int kvh, int hd, int P) {
     int64_t work = (int64_t)n_tok * kvh * (hd / 8);
     if (work < n_patch) work = n_patch;
     if (work <= 0) return hipSuccess;
-    kv_append_kernel<<<(unsigned)((work + 255) / 256), 256, 0, s>>>(
-        kpool, vpool, table, patches, n_patch, toks, n_tok, k_src, v_src, src_bf16, layout, kvh,
-        hd, P);
+    const unsigned grid = (unsigned)((work + 255) / 256);
+    if (plan)
+        kv_append_kernel<true><<<grid, 256, 0, s>>>(*plan, kpool, vpool, table, patches, n_patch,
+                                                    toks, tok_off, n_tok, k_src, v_src, src_bf16,
+                                                    layout, kvh, hd, P);
+    else
+        kv_append_kernel<false><<<grid, 256, 0, s>>>(NoPlan{0}, kpool, vpool, table, patches,
+                                                     n_patch, toks, tok_off, n_tok, k_src, v_src,
+                                                     src_bf16, layout, kvh, hd, P);
     return hipGetLastError();
 }
 
 // MLA append.  Thread = (token, 8-element chunk of the 576-element row);
 // chunks 0..63 come from c_src, 64..71 from kr_src.
-__global__ void mla_append_kernel(uint16_t *__restrict__ pool, int32_t *__restrict__ table,
-                                  const Patch *__restrict__ patches, int n_patch,
-                                  const AppendTok *__restrict__ toks, int n_tok,
-                                  const void *__restrict__ c_src, const void *__restrict__ kr_src,
-                                  int src_bf16, int P) {
+template <bool ARG>
+__global__ void mla_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__restrict__ pool,
+                                  int32_t *__restrict__ table, const Patch *__restrict__ patches,
+                                  int n_patch, const AppendTok *__restrict__ toks, int tok_off,
+                                  int n_tok, const void *__restrict__ c_src,
+                                  const void *__restrict__ kr_src, int src_bf16, int P) {
     int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid < n_patch) table[patches[gid].idx] = patches[gid].val;
+    if (gid < n_patch) {
+        const Patch pt = plan_patch<ARG>(patches, (int)gid);
+        table[pt.idx] = pt.val;
+    }
     constexpr int chunks = kMlaRow / 8;  // 72
     if (gid >= (int64_t)n_tok * chunks) return;
     const int t = (int)(gid / chunks);
     const int ch = (int)(gid - (int64_t)t * chunks);
-    const AppendTok tk = toks[t];
+    const AppendTok tk = plan_tok<ARG>(toks, tok_off, t);
     uint16_t v[8];
     if (ch < kMlaDc / 8)
         load8_bf16(c_src, (int64_t)t * kMlaDc + ch * 8, src_bf16, v);
@@ -123,14 +138,21 @@ __global__ void mla_append_kernel(uint16_t *__restrict__ pool, int32_t *__restri
     *(u32x4 *)(pool + ((int64_t)tk.page * P + tk.slot) * kMlaRow + ch * 8) = pk;
 }
 
-hipError_t launch_mla_append(hipStream_t s, uint16_t *pool, int32_t *table, const Patch *patches,
-                             int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
+hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *pool,
+                             int32_t *table, const Patch *patches, int n_patch,
+                             const AppendTok *toks, int n_tok, const void *c_src,
                              const void *kr_src, int src_bf16, int P) {
     int64_t work = (int64_t)n_tok * (kMlaRow / 8);
     if (work < n_patch) work = n_patch;
     if (work <= 0) return hipSuccess;
-    mla_append_kernel<<<(unsigned)((work + 255) / 256), 256, 0, s>>>(
-        pool, table, patches, n_patch, toks, n_tok, c_src, kr_src, src_bf16, P);
+    const unsigned grid = (unsigned)((work + 255) / 256);
+    if (plan)
+        mla_append_kernel<true><<<grid, 256, 0, s>>>(*plan, pool, table, patches, n_patch, toks,
+                                                     tok_off, n_tok, c_src, kr_src, src_bf16, P);
+    else
+        mla_append_kernel<false><<<grid, 256, 0, s>>>(NoPlan{0}, pool, table, patches, n_patch,
+                                                      toks, tok_off, n_tok, c_src, kr_src,
+                                                      src_bf16, P);
     return hipGetLastError();
 }
 

@@ -111,6 +111,28 @@ __device__ __forceinline__ AttRow plan_row(const AttRow *rows, int i) {
         return rows[i];
     }
 }
+// Append plans: patches at byte 0, tokens at byte tok_off of the plan.
+template <bool ARG>
+__device__ __forceinline__ Patch plan_patch(const Patch *patches, int i) {
+    if constexpr (ARG) {
+        const __attribute__((address_space(4))) int32_t *p =
+            (const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + i * sizeof(Patch));
+        return Patch{p[0], p[1]};
+    } else {
+        return patches[i];
+    }
+}
+template <bool ARG>
+__device__ __forceinline__ AppendTok plan_tok(const AppendTok *toks, int tok_off, int i) {
+    if constexpr (ARG) {
+        const __attribute__((address_space(4))) int32_t *p =
+            (const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + tok_off +
+                                                                i * sizeof(AppendTok));
+        return AppendTok{p[0], p[1], p[2], p[3]};
+    } else {
+        return toks[i];
+    }
+}
 // (row, split) of a decode work-group: from the device work list, or -- plan
 // in the arguments -- by binary search of the rows' first partial slots
 // (wave-uniform scalar loads).
@@ -173,11 +195,15 @@ __device__ __forceinline__ void merge_weights(const float *__restrict__ ml, int6
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
 hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n);
 
-hipError_t launch_kv_append(hipStream_t s, uint16_t *kpool, uint16_t *vpool, int32_t *table,
+// plan: patches and tokens in the kernel arguments (tokens at byte tok_off);
+// nullptr: patches / toks are device arrays.
+hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *kpool,
+                            uint16_t *vpool, int32_t *table,
                             const Patch *patches, int n_patch, const AppendTok *toks, int n_tok,
                             const void *k_src, const void *v_src, int src_bf16, int layout,
                             int kvh, int hd, int P);
-hipError_t launch_mla_append(hipStream_t s, uint16_t *pool, int32_t *table, const Patch *patches,
+hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *pool,
+                             int32_t *table, const Patch *patches,
                              int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
                              const void *kr_src, int src_bf16, int P);
 
@@ -274,8 +300,9 @@ hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t 
 int gqa_decode_wgs_per_cu(int hd, int nqt);
 int mla_decode_wgs_per_cu(int nqt);
 
-hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, int n_rows, const int2 *work, int n_work,
+hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,
+                             const int32_t *table, const AttRow *rows, int n_rows,
+                             const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
                              int total_q, int max_nq, int P, int chunk, float qscale,

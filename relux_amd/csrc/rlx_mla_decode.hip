@@ -107,12 +107,12 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
 // = 4 rows x one 32-B chunk pair) see 4 distinct chunk pairs.
 __device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-template <int NQT>
+template <int NQT, bool ARG>
 __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
-    const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
-    const AttRow *__restrict__ rows, const int2 *__restrict__ work,
-    const uint16_t *__restrict__ qlat, int H, int P, int chunk, int mask_mode,
-    float *__restrict__ part_o, float *__restrict__ part_ml) {
+    typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ pool,
+    const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
+    const int2 *__restrict__ work, int n_rows, const uint16_t *__restrict__ qlat, int H, int P,
+    int chunk, int mask_mode, float *__restrict__ part_o, float *__restrict__ part_ml) {
     constexpr int QRP = 16 * NQT;
     constexpr int S = (NQT == 1) ? 4 : 3;  // LDS ring stages (2 work-groups per CU)
     constexpr int TILE = 16 * kMlaRow;     // bf16 per stage
@@ -124,8 +124,8 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
     const int wave = tid >> 6;
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int2 wk = work[blockIdx.x];
-    const AttRow R = rows[wk.x];
+    const int2 wk = plan_work<ARG>(work, n_rows);
+    const AttRow R = plan_row<ARG>(rows, wk.x);
     const int QR = H * R.nq;
     const int t_begin = wk.y * chunk;
     const int t_end = min(R.len, t_begin + chunk);
@@ -313,10 +313,12 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
 // output o_lat[row][h][0:512] (f32 workspace).  One 256-thread block per
 // query row: wave 0 computes the merge weights in LDS, then every thread
 // streams two latent channels across the splits.
+template <bool ARG>
 __global__ __launch_bounds__(256) void mla_combine_kernel(
-    const AttRow *__restrict__ rows, const float *__restrict__ part_o,
-    const float *__restrict__ part_ml, int H, int QRP, float *__restrict__ olat) {
-    const AttRow R = rows[blockIdx.x];
+    typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
+    const float *__restrict__ part_o, const float *__restrict__ part_ml, int H, int QRP,
+    float *__restrict__ olat) {
+    const AttRow R = plan_row<ARG>(rows, blockIdx.x);
     const int qi = blockIdx.y / H;
     const int h = blockIdx.y - qi * H;
     if (qi >= R.nq) return;
@@ -382,8 +384,18 @@ __global__ __launch_bounds__(256) void mla_proj_kernel(const float *__restrict__
     }
 }
 
-hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, int n_rows, const int2 *work, int n_work,
+template <int NQT, bool ARG>
+static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uint16_t *pool,
+                         const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
+                         int n_work, const uint16_t *qlat, int H, int P, int chunk, int mask_mode,
+                         float *part_o, float *part_ml) {
+    mla_decode_kernel<NQT, ARG><<<n_work, 256, 0, s>>>(plan, pool, table, rows, work, n_rows, qlat,
+                                                        H, P, chunk, mask_mode, part_o, part_ml);
+}
+
+hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,
+                             const int32_t *table, const AttRow *rows, int n_rows,
+                             const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
                              int total_q, int max_nq, int P, int chunk, float qscale,
@@ -397,19 +409,28 @@ hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev0) (void)hipEventRecord(ev0, s);
-    if (nqt == 1)
-        mla_decode_kernel<1><<<n_work, 256, 0, s>>>(pool, table, rows, work, qlat, H, P, chunk,
-                                                    mask_mode, part_o, part_ml);
-    else if (nqt == 2)
-        mla_decode_kernel<2><<<n_work, 256, 0, s>>>(pool, table, rows, work, qlat, H, P, chunk,
-                                                    mask_mode, part_o, part_ml);
+    if (nqt != 1 && nqt != 2) return hipErrorInvalidValue;
+    if (plan && nqt == 1)
+        launch_mla_t<1, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P, chunk,
+                              mask_mode, part_o, part_ml);
+    else if (plan)
+        launch_mla_t<2, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P, chunk,
+                              mask_mode, part_o, part_ml);
+    else if (nqt == 1)
+        launch_mla_t<1, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+                               chunk, mask_mode, part_o, part_ml);
     else
-        return hipErrorInvalidValue;
+        launch_mla_t<2, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+                               chunk, mask_mode, part_o, part_ml);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
-    mla_combine_kernel<<<dim3(n_rows, max_nq * H), 256, 0, s>>>(rows, part_o, part_ml, H,
-                                                                16 * nqt, olat);
+    if (plan)
+        mla_combine_kernel<true><<<dim3(n_rows, max_nq * H), 256, 0, s>>>(*plan, rows, part_o,
+                                                                          part_ml, H, 16 * nqt, olat);
+    else
+        mla_combine_kernel<false><<<dim3(n_rows, max_nq * H), 256, 0, s>>>(
+            NoPlan{0}, rows, part_o, part_ml, H, 16 * nqt, olat);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     mla_proj_kernel<<<dim3(H, (total_q + 7) / 8, hd / 32), 256, 0, s>>>(olat, w_uv, H, hd,
@@ -420,8 +441,8 @@ hipError_t launch_mla_decode(hipStream_t s, const uint16_t *pool, const int32_t 
 int mla_decode_wgs_per_cu(int nqt) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
-    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1>, 256, 0);
-    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2>, 256, 0);
+    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1, true>, 256, 0);
+    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2, true>, 256, 0);
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 

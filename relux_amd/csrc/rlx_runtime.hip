@@ -138,6 +138,33 @@ int32_t stage(Cache *c, const void *data, size_t bytes, void **dev_out) {
     return RLX_OK;
 }
 
+// Append plans: patches then tokens (16-byte aligned), in the kernel
+// arguments when they fit, else staged.  Fills *plan or the device pointers.
+int32_t append_plan(Cache *c, const std::vector<Patch> &patches,
+                    const std::vector<AppendTok> &toks, PlanArg *plan_arg, const PlanArg **plan,
+                    int *tok_off, const Patch **d_patches, const AppendTok **d_toks) {
+    const size_t off = (patches.size() * sizeof(Patch) + 15) & ~(size_t)15;
+    *plan = nullptr;
+    *d_patches = nullptr;
+    *d_toks = nullptr;
+    *tok_off = (int)off;
+    if (off + toks.size() * sizeof(AppendTok) <= sizeof(PlanArg)) {
+        if (!patches.empty()) memcpy(plan_arg->b, patches.data(), patches.size() * sizeof(Patch));
+        if (!toks.empty()) memcpy(plan_arg->b + off, toks.data(), toks.size() * sizeof(AppendTok));
+        *plan = plan_arg;
+        return RLX_OK;
+    }
+    std::vector<char> bytes(off + toks.size() * sizeof(AppendTok));
+    if (!patches.empty()) memcpy(bytes.data(), patches.data(), patches.size() * sizeof(Patch));
+    if (!toks.empty()) memcpy(bytes.data() + off, toks.data(), toks.size() * sizeof(AppendTok));
+    void *dev;
+    int32_t rc = stage(c, bytes.data(), bytes.size(), &dev);
+    if (rc) return rc;
+    *d_patches = (const Patch *)dev;
+    *d_toks = (const AppendTok *)((char *)dev + off);
+    return RLX_OK;
+}
+
 // Serialise a list of PODs into one byte blob with 16-byte aligned parts.
 struct Blob {
     std::vector<char> bytes;
@@ -651,15 +678,17 @@ int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     if (!toks.empty() && (!k_src || !v_src)) return fail(RLX_ERR_INVALID, "null K/V source");
     std::vector<Patch> patches = take_pending(c);
-    Blob b;
-    size_t o_p = b.add(patches), o_t = b.add(toks);
-    void *dev;
-    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    PlanArg plan_arg;
+    const PlanArg *plan;
+    int tok_off;
+    const Patch *d_patches;
+    const AppendTok *d_toks;
+    if ((rc = append_plan(c, patches, toks, &plan_arg, &plan, &tok_off, &d_patches, &d_toks)))
+        return rc;
     LayerState &ls = c->L[layer];
-    HIP_TRY(launch_kv_append(c->stream, ls.pool0, ls.pool1, c->d_table,
-                             (const Patch *)((char *)dev + o_p), (int)patches.size(),
-                             (const AppendTok *)((char *)dev + o_t), (int)toks.size(), k_src,
-                             v_src, src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->P));
+    HIP_TRY(launch_kv_append(c->stream, plan, tok_off, ls.pool0, ls.pool1, c->d_table, d_patches,
+                             (int)patches.size(), d_toks, (int)toks.size(), k_src, v_src,
+                             src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->P));
     return RLX_OK;
 }
 
@@ -677,14 +706,16 @@ int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     if (!toks.empty() && (!c_src || !kr_src)) return fail(RLX_ERR_INVALID, "null latent source");
     std::vector<Patch> patches = take_pending(c);
-    Blob b;
-    size_t o_p = b.add(patches), o_t = b.add(toks);
-    void *dev;
-    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
-    HIP_TRY(launch_mla_append(c->stream, c->L[layer].pool0, c->d_table,
-                              (const Patch *)((char *)dev + o_p), (int)patches.size(),
-                              (const AppendTok *)((char *)dev + o_t), (int)toks.size(), c_src,
-                              kr_src, src_dtype == RLX_BF16, c->P));
+    PlanArg plan_arg;
+    const PlanArg *plan;
+    int tok_off;
+    const Patch *d_patches;
+    const AppendTok *d_toks;
+    if ((rc = append_plan(c, patches, toks, &plan_arg, &plan, &tok_off, &d_patches, &d_toks)))
+        return rc;
+    HIP_TRY(launch_mla_append(c->stream, plan, tok_off, c->L[layer].pool0, c->d_table, d_patches,
+                              (int)patches.size(), d_toks, (int)toks.size(), c_src, kr_src,
+                              src_dtype == RLX_BF16, c->P));
     return RLX_OK;
 }
 
@@ -1000,17 +1031,28 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const size_t pm_bytes = ((size_t)parts * QRP * 2 * sizeof(float) + 255) & ~(size_t)255;
     const size_t ol_bytes = (size_t)total_q * num_heads * kMlaDc * sizeof(float);
     if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes + ol_bytes))) return rc;
-    Blob b;
-    size_t o_r = b.add(rows), o_w = b.add(work);
-    void *dev;
-    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    PlanArg plan_arg;
+    const PlanArg *plan = nullptr;
+    const AttRow *d_rows = nullptr;
+    const int2 *d_work = nullptr;
+    if (rows.size() * sizeof(AttRow) <= sizeof(PlanArg)) {
+        memcpy(plan_arg.b, rows.data(), rows.size() * sizeof(AttRow));
+        plan = &plan_arg;
+    } else {
+        Blob b;
+        size_t o_r = b.add(rows), o_w = b.add(work);
+        void *dev;
+        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+        d_rows = (const AttRow *)((char *)dev + o_r);
+        d_work = (const int2 *)((char *)dev + o_w);
+    }
     if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
     const float qscale = scale * 1.4426950408889634f;
     char *ws = (char *)c->ws;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
-    HIP_TRY(launch_mla_decode(c->stream, ls.pool0, c->d_table, (const AttRow *)((char *)dev + o_r),
-                              n_seqs, (const int2 *)((char *)dev + o_w), (int)work.size(), q_nope,
+    HIP_TRY(launch_mla_decode(c->stream, plan, ls.pool0, c->d_table, d_rows, n_seqs, d_work,
+                              (int)work.size(), q_nope,
                               q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
                               (const uint16_t *)w_uv, num_heads, head_dim, total_q, max_nq, c->P,
                               chunk, qscale, mask_mode, nqt, (uint16_t *)ws,
