@@ -67,6 +67,17 @@ extern "C" {
 #define RLX_MASK_REF 1
 #define RLX_MASK_NONE 2
 
+/* RoPE position rule of rlx_gqa_project_append:
+ *   RLX_ROPE_OFFSET: token j of a sequence at absolute position
+ *                    pos_offset + live_len + j (eviction keeps positions);
+ *   RLX_ROPE_REF:    the reference's Apply(x, cacheLen): every row at
+ *                    cacheLen when cacheLen > 0, else row j at j
+ *                    (rope.go:151-158);
+ *   RLX_ROPE_NONE:   no rotation. */
+#define RLX_ROPE_OFFSET 0
+#define RLX_ROPE_REF 1
+#define RLX_ROPE_NONE 2
+
 /* ---- runtime ---------------------------------------------------------- */
 /* Select the device for this thread; must be a gfx950 GPU.  Replaces the
  * rnxa engine bring-up the ladder does (internal/compute/factory.go:32-85). */
@@ -132,6 +143,31 @@ int32_t rlx_cache_set_stream(void *cache, void *stream);
 int32_t rlx_kv_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                       const int32_t *n_tok, const void *k_src, const void *v_src,
                       int32_t src_dtype, int32_t src_layout);
+
+/* ---- fused pre-attention step (projection + RoPE + append) ------------- */
+/* Pack a GQA layer's W_q [d_model][H*D], W_k and W_v [d_model][KVH*D] (the
+ * reference's in-row/out-col layout, mha.go:84-100, bf16 or f32) into one
+ * bf16 matrix out [(H + 2*KVH)*D][d_model] (device buffer of that size) for
+ * rlx_gqa_project_append.  Runs on the null stream.  No reference
+ * counterpart: a one-time weight preparation. */
+int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t w_dtype,
+                     int32_t d_model, int32_t num_heads, int32_t kv_heads, int32_t head_dim,
+                     void *out);
+/* q = x.W_q, k = x.W_k, v = x.W_v for the n_tok[i] new tokens of each
+ * sequence (x [sum n][d_model], f32 or bf16), RoPE of q and k with the
+ * caller's tables rope_cos/rope_sin [rope_rows][head_dim/2] (f32, device) at
+ * the positions rope_mode selects, then the paged append of k and v (bf16
+ * round-to-nearest-even); q_out [sum n][num_heads][head_dim] receives the
+ * rotated queries for rlx_gqa_attend.  Replaces mha.go:250-289
+ * (matmulBatched3D x3, rearrange, RotaryEmbedding.Apply, KVCache.Append).
+ * Projections run on MFMA (bf16 operands, f32 sums): results match the
+ * reference's f32 loops within tolerance, not bit for bit.  A position at
+ * or past rope_rows fails with RLX_ERR_OVERFLOW (the reference panics). */
+int32_t rlx_gqa_project_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_tok, const void *x, int32_t x_dtype,
+                               int32_t d_model, const void *w_packed, int32_t num_heads,
+                               const float *rope_cos, const float *rope_sin, int32_t rope_rows,
+                               int32_t rope_mode, void *q_out, int32_t q_dtype);
 
 /* MLA: c_src [sum n][d_c], kr_src [sum n][d_r] (post-RoPE).  Replaces
  * MLACache.Append (mla_cache.go:152-182). */

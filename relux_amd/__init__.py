@@ -2,17 +2,18 @@
 
 librelux_kv.so (HIP, built in-tree by relux_amd.build) implements paged GQA
 and MLA caches, append, gather, rollback/evict/compact, and decode /
-verify attention over the paged cache.  `KVCache` and `MLACache` mirror the
+verify / chunked-prefill attention over the paged cache, and the fused
+Q/K/V projection + RoPE + append step.  `KVCache` and `MLACache` mirror the
 reference's Go cache types (internal/transformer/kvcache.go, mla_cache.go).
 """
 from ._lib import ReluxError, ReluxPanic, load  # noqa: F401
 
-__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load"]
+__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "rope_tables"]
 
 
 def __getattr__(name):
     # Lazy: importing the package must not touch the GPU or require torch.
-    if name in ("KVCache", "MLACache", "default_scale"):
+    if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "rope_tables"):
         from . import kvcache
         return getattr(kvcache, name)
     raise AttributeError(name)

@@ -33,6 +33,9 @@ RLX_LAYOUT_SHD = 1
 RLX_MASK_CAUSAL = 0
 RLX_MASK_REF = 1
 RLX_MASK_NONE = 2
+RLX_ROPE_OFFSET = 0
+RLX_ROPE_REF = 1
+RLX_ROPE_NONE = 2
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64
@@ -60,6 +63,9 @@ SIGNATURES = {
     "rlx_cache_sync": [_vp],
     "rlx_cache_set_stream": [_vp, _vp],
     "rlx_kv_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32, _i32],
+    "rlx_pack_qkv": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
+    "rlx_gqa_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _vp, _vp,
+                               _i32, _i32, _vp, _i32],
     "rlx_mla_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32],
     "rlx_kv_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],
     "rlx_mla_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],

@@ -1,0 +1,186 @@
+// Fused pre-attention step of a GQA layer: Q/K/V projection of the new
+// tokens' hidden states, RoPE on Q and K, and the paged append of K and V.
+//
+// Reference restated (mha.go:250-289): q = x.W_q, k = x.W_k, v = x.W_v
+// (matmulBatched3D, bf16 weights widened, f32 sums), RoPE of q and k at the
+// cache position (rope.go:130-180: pairs (2i, 2i+1) rotated by
+// (cos, sin)[pos][i]), then Append of k and v (kvcache.go:240-316, bf16
+// round-to-nearest-even).  Here the three projections are one GEMM against
+// a packed weight matrix Wp[n][k] (rows = the H q-heads, then the KVH k-heads,
+// then the KVH v-heads, each D features; k contiguous so that 8 consecutive
+// k of one output feature are one 16-byte MFMA operand load).
+//
+// Work-group = 16 output features x all rows (at most 64); its 4 waves take
+// the 32-wide k-steps round-robin and meet in LDS.  MFMA 16x16x32: A = x
+// rows (converted to bf16), B = Wp rows.  The result lane holds 4 rows of
+// one feature, so a RoPE pair partner (feature ^ 1) is one lane away.
+#include "rlx_common.h"
+
+namespace rlx {
+
+constexpr int kProjMaxRows = 64;
+
+// Packed rows: Wp[n][k] for n < H*D from w_q[k][n], then w_k, then w_v.
+__global__ void pack_qkv_kernel(const void *__restrict__ w_q, const void *__restrict__ w_k,
+                                const void *__restrict__ w_v, int w_bf16, int K, int NQ, int NK,
+                                uint16_t *__restrict__ out) {
+    __shared__ uint16_t tile[32][33];
+    const int N = NQ + 2 * NK;
+    const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int r = ty; r < 32; r += 8) {
+        const int k = k0 + r, n = n0 + tx;
+        uint16_t v = 0;
+        if (k < K && n < N) {
+            const void *src;
+            int nn, ld;
+            if (n < NQ) { src = w_q; nn = n; ld = NQ; }
+            else if (n < NQ + NK) { src = w_k; nn = n - NQ; ld = NK; }
+            else { src = w_v; nn = n - NQ - NK; ld = NK; }
+            const int64_t off = (int64_t)k * ld + nn;
+            v = w_bf16 ? ((const uint16_t *)src)[off] : bf16_rne(((const float *)src)[off]);
+        }
+        tile[r][tx] = v;
+    }
+    __syncthreads();
+    for (int r = ty; r < 32; r += 8) {
+        const int n = n0 + r, k = k0 + tx;
+        if (n < N && k < K) out[(int64_t)n * K + k] = tile[tx][r];
+    }
+}
+
+template <bool ARG>
+__global__ __launch_bounds__(256) void qkv_project_kernel(
+    typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
+    const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
+    int pos_off, int rows, const void *__restrict__ x, int x_bf16, int K,
+    const uint16_t *__restrict__ wp, int H, int KVH, int D, const float *__restrict__ rcos,
+    const float *__restrict__ rsin, void *__restrict__ q_out, int q_bf16,
+    uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool, int32_t *__restrict__ table,
+    int P) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    if (blockIdx.x == 0) {
+        for (int i = tid; i < n_patch; i += 256) {
+            const Patch pt = plan_patch<ARG>(patches, i);
+            table[pt.idx] = pt.val;
+        }
+    }
+    const int n0 = blockIdx.x * 16;
+    const int MT = (rows + 15) / 16;
+    const int KS = K / 32;
+    fl4 acc[kProjMaxRows / 16];
+#pragma unroll
+    for (int m = 0; m < kProjMaxRows / 16; m++) acc[m] = fl4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t *wrow = wp + (int64_t)(n0 + col) * K + grp * 8;
+#pragma unroll 4
+    for (int ks = wave; ks < KS; ks += 4) {
+        const bf16x8 b = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load((const u32x4 *)(wrow + ks * 32)));
+#pragma unroll
+        for (int m = 0; m < kProjMaxRows / 16; m++) {
+            if (m < MT) {
+                const int r = min(m * 16 + col, rows - 1);
+                const int64_t off = (int64_t)r * K + ks * 32 + grp * 8;
+                u32x4 a;
+                if (x_bf16) {
+                    a = *(const u32x4 *)((const uint16_t *)x + off);
+                } else {
+                    const float4 f0 = *(const float4 *)((const float *)x + off);
+                    const float4 f1 = *(const float4 *)((const float *)x + off + 4);
+                    a[0] = pack_bf16x2(f0.x, f0.y);
+                    a[1] = pack_bf16x2(f0.z, f0.w);
+                    a[2] = pack_bf16x2(f1.x, f1.y);
+                    a[3] = pack_bf16x2(f1.z, f1.w);
+                }
+                // C[m = row][n = feature]: A = x rows, B = Wp rows.
+                acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, acc[m], 0, 0, 0);
+            }
+        }
+    }
+    // ---- k-split merge: waves 1-3 hand their sums to wave 0 ----------------
+    __shared__ fl4 red[3][kProjMaxRows / 16][64];
+    if (wave > 0) {
+#pragma unroll
+        for (int m = 0; m < kProjMaxRows / 16; m++)
+            if (m < MT) red[wave - 1][m][lane] = acc[m];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    const int n = n0 + col;
+    const int NQ = H * D, NK = KVH * D;
+    const int part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);  // q, k, v (uniform per work-group)
+    const int nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
+    const int head = nn / D, d = nn - head * D;
+#pragma unroll
+    for (int m = 0; m < kProjMaxRows / 16; m++) {
+        if (m >= MT) break;
+        fl4 y = acc[m];
+#pragma unroll
+        for (int w = 0; w < 3; w++) y += red[w][m][lane];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = m * 16 + grp * 4 + i;  // C row of element i
+            float v = y[i];
+            const float partner = __shfl_xor(v, 1);
+            const bool live = r < rows;
+            if (part < 2) {
+                // RoPE: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), products rounded
+                // separately as in rope.go.
+                const int p = live ? (ARG ? ((const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + pos_off))[r]
+                                           : pos_dev[r])
+                                   : 0;
+                if (p >= 0) {
+                    const float c = rcos[(int64_t)p * (D / 2) + (d >> 1)];
+                    const float s = rsin[(int64_t)p * (D / 2) + (d >> 1)];
+                    v = (d & 1) ? __fadd_rn(__fmul_rn(v, c), __fmul_rn(partner, s))
+                                : __fsub_rn(__fmul_rn(v, c), __fmul_rn(partner, s));
+                }
+            }
+            if (!live) continue;
+            if (part == 0) {
+                const int64_t o = ((int64_t)r * H + head) * D + d;
+                if (q_bf16)
+                    ((uint16_t *)q_out)[o] = bf16_rne(v);
+                else
+                    ((float *)q_out)[o] = v;
+            } else {
+                const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
+                if (part == 1)
+                    kpool[(((int64_t)tk.page * KVH + head) * P + tk.slot) * D + d] = bf16_rne(v);
+                else
+                    vpool[(((int64_t)tk.page * KVH + head) * D + d) * P + tk.slot] = bf16_rne(v);
+            }
+        }
+    }
+}
+
+hipError_t launch_pack_qkv(hipStream_t s, const void *w_q, const void *w_k, const void *w_v,
+                           int w_bf16, int K, int NQ, int NK, uint16_t *out) {
+    const int N = NQ + 2 * NK;
+    pack_qkv_kernel<<<dim3((N + 31) / 32, (K + 31) / 32), 256, 0, s>>>(w_q, w_k, w_v, w_bf16, K, NQ,
+                                                                      NK, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_qkv_project(hipStream_t s, const PlanArg *plan, const Patch *patches,
+                              int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
+                              int pos_off, int rows, const void *x, int x_bf16, int K,
+                              const uint16_t *wp, int H, int KVH, int D, const float *rcos,
+                              const float *rsin, void *q_out, int q_bf16, uint16_t *kpool,
+                              uint16_t *vpool, int32_t *table, int P) {
+    if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
+    const int N = (H + 2 * KVH) * D;
+    if (plan)
+        qkv_project_kernel<true><<<N / 16, 256, 0, s>>>(*plan, patches, n_patch, toks, pos, tok_off,
+                                                        pos_off, rows, x, x_bf16, K, wp, H, KVH, D,
+                                                        rcos, rsin, q_out, q_bf16, kpool, vpool,
+                                                        table, P);
+    else
+        qkv_project_kernel<false><<<N / 16, 256, 0, s>>>(NoPlan{0}, patches, n_patch, toks, pos,
+                                                         tok_off, pos_off, rows, x, x_bf16, K, wp,
+                                                         H, KVH, D, rcos, rsin, q_out, q_bf16,
+                                                         kpool, vpool, table, P);
+    return hipGetLastError();
+}
+
+}  // namespace rlx

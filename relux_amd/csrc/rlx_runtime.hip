@@ -692,6 +692,96 @@ int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     return RLX_OK;
 }
 
+int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t w_dtype,
+                     int32_t d_model, int32_t num_heads, int32_t kv_heads, int32_t head_dim,
+                     void *out) {
+    if (!w_q || !w_k || !w_v || !out) return fail(RLX_ERR_INVALID, "null weight pointer");
+    if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
+    if (d_model <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0)
+        return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
+    HIP_TRY(launch_pack_qkv(nullptr, w_q, w_k, w_v, w_dtype == RLX_BF16, d_model,
+                            num_heads * head_dim, kv_heads * head_dim, (uint16_t *)out));
+    return RLX_OK;
+}
+
+int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_tok, const void *x, int32_t x_dtype,
+                               int32_t d_model, const void *w_packed, int32_t num_heads,
+                               const float *rope_cos, const float *rope_sin, int32_t rope_rows,
+                               int32_t rope_mode, void *q_out, int32_t q_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (x_dtype != RLX_F32 && x_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "x_dtype");
+    if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
+    if (rope_mode < RLX_ROPE_OFFSET || rope_mode > RLX_ROPE_NONE) return fail(RLX_ERR_INVALID, "rope_mode");
+    if (num_heads <= 0 || num_heads % c->kvh != 0)
+        return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
+    if (d_model <= 0 || d_model % 32 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "d_model=%d must be a positive multiple of 32", d_model);
+    if (rope_mode != RLX_ROPE_NONE && (!rope_cos || !rope_sin || rope_rows <= 0))
+        return fail(RLX_ERR_INVALID, "RoPE tables required");
+    LayerState &ls = c->L[layer];
+    // RoPE position of every new token (rope.go:151-158 for the reference rule).
+    std::vector<int32_t> pos;
+    int total = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        if (!n_tok || n_tok[i] < 0) return fail(RLX_ERR_INVALID, "negative token count");
+        const SeqState &st = ls.seqs[seq_ids[i]];
+        for (int j = 0; j < n_tok[i]; j++) {
+            int p = -1;
+            if (rope_mode == RLX_ROPE_OFFSET) p = st.pos_offset + st.len + j;
+            if (rope_mode == RLX_ROPE_REF) p = st.len > 0 ? st.len : j;
+            if (p >= 0 && p >= rope_rows)
+                return fail(RLX_ERR_OVERFLOW, "RotaryEmbedding.Apply: position %d >= maxSeqLen %d", p, rope_rows);
+            pos.push_back(p);
+        }
+        total += n_tok[i];
+    }
+    if (total == 0) return RLX_OK;
+    if (!x || !w_packed || !q_out) return fail(RLX_ERR_INVALID, "null x / weights / q_out");
+    std::vector<AppendTok> toks;
+    if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
+    std::vector<Patch> patches = take_pending(c);
+    const int xb = x_dtype == RLX_BF16 ? 2 : 4, qb = q_dtype == RLX_BF16 ? 2 : 4;
+    for (int r0 = 0; r0 < total; r0 += kProjRows) {
+        const int rows = std::min(kProjRows, total - r0);
+        const std::vector<Patch> none;
+        const std::vector<Patch> &pt = (r0 == 0) ? patches : none;
+        const size_t toff = (pt.size() * sizeof(Patch) + 15) & ~(size_t)15;
+        const size_t poff = toff + rows * sizeof(AppendTok);
+        std::vector<char> bytes(poff + rows * sizeof(int32_t));
+        if (!pt.empty()) memcpy(bytes.data(), pt.data(), pt.size() * sizeof(Patch));
+        memcpy(bytes.data() + toff, toks.data() + r0, rows * sizeof(AppendTok));
+        memcpy(bytes.data() + poff, pos.data() + r0, rows * sizeof(int32_t));
+        PlanArg plan_arg;
+        const PlanArg *plan = nullptr;
+        const Patch *d_p = nullptr;
+        const AppendTok *d_t = nullptr;
+        const int32_t *d_pos = nullptr;
+        if (bytes.size() <= sizeof(PlanArg)) {
+            memcpy(plan_arg.b, bytes.data(), bytes.size());
+            plan = &plan_arg;
+        } else {
+            void *dev;
+            if ((rc = stage(c, bytes.data(), bytes.size(), &dev))) return rc;
+            d_p = (const Patch *)dev;
+            d_t = (const AppendTok *)((char *)dev + toff);
+            d_pos = (const int32_t *)((char *)dev + poff);
+        }
+        HIP_TRY(launch_qkv_project(c->stream, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
+                                   (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
+                                   x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed,
+                                   num_heads, c->kvh, c->hd, rope_cos, rope_sin,
+                                   (char *)q_out + (size_t)r0 * num_heads * c->hd * qb,
+                                   q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P));
+    }
+    return RLX_OK;
+}
+
 int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                        const int32_t *n_tok, const void *c_src, const void *kr_src,
                        int32_t src_dtype) {

@@ -19,6 +19,7 @@ from ._lib import check, i32_array
 
 _MASKS = {"causal": _lib.RLX_MASK_CAUSAL, "ref": _lib.RLX_MASK_REF, "none": _lib.RLX_MASK_NONE}
 _LAYOUTS = {"HSD": _lib.RLX_LAYOUT_HSD, "SHD": _lib.RLX_LAYOUT_SHD}
+_ROPE = {"offset": _lib.RLX_ROPE_OFFSET, "ref": _lib.RLX_ROPE_REF, "none": _lib.RLX_ROPE_NONE}
 
 
 def _dtype_code(t):
@@ -231,6 +232,65 @@ class KVCache(_PagedCache):
                                        _LAYOUTS[layout], float(scale or 0.0), _MASKS[mask],
                                        _dev(out, "out"), _dtype_code(out)))
         return out
+
+
+    def ProjectAppend(self, layer_idx, x, w_packed, num_heads, rope=None, seq_ids=(0,), n_tok=None,
+                      rope_mode="offset", q_dtype=torch.float32):
+        """Fused pre-attention step (mha.go:250-289): q/k/v projection of the
+        new tokens' hidden states x [sum n][d_model] with weights packed by
+        pack_qkv, RoPE of q and k (rope = (cos, sin) tables from rope_tables),
+        append of k and v.  Returns the rotated q [sum n][num_heads][head_dim]."""
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [x.shape[0]]
+        rows, d_model = x.shape[0], x.shape[-1]
+        if rows != sum(n_tok):
+            raise ValueError("x rows do not match sum(n_tok)")
+        q = torch.empty((rows, num_heads, self.head_dim), dtype=q_dtype, device=x.device)
+        if rope is None:
+            rope_mode = "none"
+            cos_t = sin_t = None
+            rope_rows = 0
+        else:
+            cos_t, sin_t = rope
+            rope_rows = cos_t.shape[0]
+        check(self._lib.rlx_gqa_project_append(
+            self._h, layer_idx, len(seq_ids), i32_array(seq_ids), i32_array(n_tok), _dev(x, "x"),
+            _dtype_code(x), d_model, _dev(w_packed, "w_packed"), num_heads,
+            _dev(cos_t, "rope_cos") if cos_t is not None else None,
+            _dev(sin_t, "rope_sin") if sin_t is not None else None, rope_rows, _ROPE[rope_mode],
+            _dev(q, "q_out"), _dtype_code(q)))
+        return q
+
+
+def pack_qkv(w_q, w_k, w_v, num_heads, kv_heads, head_dim):
+    """W_q [d_model][H*D], W_k/W_v [d_model][KVH*D] (bf16 or f32, device) ->
+    packed bf16 [(H + 2 KVH) * D][d_model] for KVCache.ProjectAppend."""
+    d_model = w_q.shape[0]
+    out = torch.empty(((num_heads + 2 * kv_heads) * head_dim, d_model), dtype=torch.bfloat16,
+                      device=w_q.device)
+    check(_lib.load().rlx_pack_qkv(_dev(w_q, "w_q"), _dev(w_k, "w_k"), _dev(w_v, "w_v"),
+                                   _dtype_code(w_q), d_model, num_heads, kv_heads, head_dim,
+                                   _dev(out, "out")))
+    return out
+
+
+def rope_tables(head_dim, base, max_seq, device):
+    """RotaryEmbedding tables (rope.go:50-75): theta_i = f32(1/f32(base^(2i/d))),
+    angle = f32(pos * theta) in f64, cos/sin in f64 rounded to f32.  Returns
+    device f32 (cos, sin), each [max_seq][head_dim/2]."""
+    import numpy as np
+    half = head_dim // 2
+    i = np.arange(half, dtype=np.float64)
+    p = np.power(np.float64(np.float32(base)), 2.0 * i / head_dim).astype(np.float32)
+    theta = (np.float32(1.0) / p).astype(np.float32)
+    pos = np.arange(max_seq, dtype=np.float64)[:, None]
+    angle = (pos * theta.astype(np.float64)[None, :]).astype(np.float32)
+    cos_t = np.cos(angle.astype(np.float64)).astype(np.float32)
+    sin_t = np.sin(angle.astype(np.float64)).astype(np.float32)
+    return (torch.from_numpy(cos_t).to(device), torch.from_numpy(sin_t).to(device))
 
 
 class MLACache(_PagedCache):

@@ -1,0 +1,149 @@
+"""Fused pre-attention step (rlx_pack_qkv + rlx_gqa_project_append):
+projection of the new tokens' hidden states, RoPE of q and k, paged append
+of k and v, checked against the oracle's restatement of mha.go:250-289
+(matmul_bf16w, rope_apply, BF16FromF32).
+
+The kernel feeds MFMA with bf16 activations, so the tight checks compare
+with the oracle run on bf16-rounded x (only the f32 summation order
+differs); the reference's f32-activation result is checked at the
+north-star tolerance."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import tiny_decoder as td
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_tensor(u16, gpu):
+    return torch.from_numpy(np.ascontiguousarray(u16).view(np.int16)).to(gpu).view(torch.bfloat16)
+
+
+def _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, positions):
+    """Per-row reference step: projections, then RoPE of each head row at its
+    position (positions[r] = -1: no rotation).  Returns q [R,H,D], k, v [R,KVH,D]."""
+    R = x.shape[0]
+    q = oracle.matmul_bf16w(x, wq).reshape(R, H, D)
+    k = oracle.matmul_bf16w(x, wk).reshape(R, KVH, D)
+    v = oracle.matmul_bf16w(x, wv).reshape(R, KVH, D)
+    for r in range(R):
+        if positions[r] >= 0:
+            # [heads, 1, D]: every head row of token r at positions[r]
+            q[r] = oracle.rope_apply(q[r][:, None, :], positions[r], tables, max_seq)[:, 0, :]
+            k[r] = oracle.rope_apply(k[r][:, None, :], positions[r], tables, max_seq)[:, 0, :]
+    return q, k, v
+
+
+@pytest.mark.parametrize("d_model,H,KVH,D,lens,ntok,x_dtype,mode", [
+    (256, 8, 2, 64, [0, 5, 40], [3, 1, 70], torch.float32, "offset"),   # > 64 rows: two launches
+    (512, 16, 4, 128, [17, 0], [1, 9], torch.bfloat16, "offset"),
+    (64, 4, 2, 16, [0], [8], torch.float32, "offset"),                   # config-1 shapes
+    (128, 4, 4, 32, [6, 3], [4, 2], torch.float32, "ref"),               # reference RoPE rule
+])
+def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dtype, mode):
+    from relux_amd import KVCache, pack_qkv, rope_tables
+    rng = np.random.default_rng(d_model + H + D)
+    S = len(lens)
+    max_seq = 256
+    c = KVCache(num_layers=1, max_len=max_seq, num_kv_heads=KVH, head_dim=D, max_seqs=S,
+                device=gpu.index)
+    wq = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, H * D)).astype(np.float32))
+    wk = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
+    wv = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
+    wp = pack_qkv(_bf16_tensor(wq, gpu), _bf16_tensor(wk, gpu), _bf16_tensor(wv, gpu), H, KVH, D)
+    # packed layout: rows = output features, k contiguous
+    np.testing.assert_array_equal(wp.view(torch.int16).cpu().numpy().view(np.uint16),
+                                  np.concatenate([wq, wk, wv], axis=1).T)
+    rope = rope_tables(D, 10000.0, max_seq, gpu)
+    tables = oracle.rope_tables(D, 10000.0, max_seq)
+    # existing context through the plain append
+    for i, L in enumerate(lens):
+        if L:
+            kv = torch.from_numpy(rng.standard_normal((L, KVH, D), dtype=np.float32)).to(gpu)
+            c.Append(0, kv, kv, seq_ids=[i], n_tok=[L], layout="SHD")
+    R = sum(ntok)
+    x = rng.standard_normal((R, d_model), dtype=np.float32)
+    xt = torch.from_numpy(x).to(gpu).to(x_dtype)
+    q = c.ProjectAppend(0, xt, wp, H, rope=rope, seq_ids=list(range(S)), n_tok=ntok,
+                        rope_mode=mode).cpu().numpy()
+    pos = []
+    for L, n in zip(lens, ntok):
+        pos += [L + j for j in range(n)] if mode == "offset" else [L if L > 0 else j for j in range(n)]
+    xr = oracle.round_bf16(xt.float().cpu().numpy())
+    q_o, k_o, v_o = _oracle_qkv(xr, wq, wk, wv, H, KVH, D, tables, max_seq, pos)
+    np.testing.assert_allclose(q, q_o, atol=2e-4, rtol=1e-4)
+    # against the f32-activation reference at the north-star tolerance
+    q_f, _, _ = _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, pos)
+    err = np.abs(q - q_f)
+    assert err.max() < 2e-2 and err.mean() < 2e-3, (err.max(), err.mean())
+    # cache bytes of the new tokens
+    off = 0
+    for i, (L, n) in enumerate(zip(lens, ntok)):
+        kg, vg = c.View(0, i)
+        kg = kg[0].view(torch.int16).cpu().numpy().view(np.uint16)[:, L:, :]  # [KVH, n, D]
+        vg = vg[0].view(torch.int16).cpu().numpy().view(np.uint16)[:, L:, :]
+        kw = oracle.bf16_from_f32(k_o[off:off + n].transpose(1, 0, 2))
+        vw = oracle.bf16_from_f32(v_o[off:off + n].transpose(1, 0, 2))
+        for got, want in ((kg, kw), (vg, vw)):
+            same = (got == want).mean()
+            assert same > 0.99, same
+            np.testing.assert_allclose(oracle.f32_from_bf16(got), oracle.f32_from_bf16(want),
+                                       atol=1e-2, rtol=1e-2)
+        off += n
+    assert [c.TotalLen(0, i) for i in range(S)] == [L + n for L, n in zip(lens, ntok)]
+
+
+def test_rope_position_overflow_panics(gpu):
+    from relux_amd import KVCache, ReluxPanic, pack_qkv, rope_tables
+    c = KVCache(num_layers=1, max_len=64, num_kv_heads=1, head_dim=16, device=gpu.index)
+    w = torch.zeros((64, 16), dtype=torch.bfloat16, device=gpu)
+    wp = pack_qkv(w, w, w, 1, 1, 16)
+    rope = rope_tables(16, 10000.0, 8, gpu)  # positions 0..7 only
+    x = torch.zeros((9, 64), device=gpu)
+    with pytest.raises(ReluxPanic):
+        c.ProjectAppend(0, x, wp, 1, rope=rope)
+    assert c.TotalLen(0) == 0  # nothing appended
+
+
+class FusedGpuDecoder(td.TinyDecoder):
+    """Config-1 decoder whose attention layers run the fused device step:
+    ProjectAppend (projection, RoPE, append) then Attend."""
+
+    def __init__(self, device):
+        super().__init__(td.CFG1, seed=0)
+        from relux_amd import KVCache, pack_qkv, rope_tables
+        cfg = self.cfg
+        self.dev = device
+        self.cache = KVCache(num_layers=cfg["layers"], max_len=cfg["max_seq"],
+                             num_kv_heads=self.KVH, head_dim=self.D, device=device.index)
+        self.wp = [pack_qkv(_bf16_tensor(Wl["wq"], device), _bf16_tensor(Wl["wk"], device),
+                            _bf16_tensor(Wl["wv"], device), self.H, self.KVH, self.D)
+                   for Wl in self.W["layers"]]
+        self.rope_dev = rope_tables(self.D, cfg["rope_base"], cfg["max_seq"], device)
+
+    def _attention(self, layer, x, cache):
+        S = x.shape[0]
+        q = self.cache.ProjectAppend(layer, torch.from_numpy(np.ascontiguousarray(x)).to(self.dev),
+                                     self.wp[layer], self.H, rope=self.rope_dev)
+        o = self.cache.Attend(layer, q, self.H, n_q=[S], layout="SHD", mask="causal")
+        o = o.cpu().numpy().reshape(S, self.H * self.D)
+        return oracle.matmul_bf16w(o, self.W["layers"][layer]["wo"])
+
+
+def test_cfg1_generate_with_fused_step(gpu):
+    """Config 1 end to end with the projection, RoPE and append on the GPU:
+    logits within 2e-2 / 2e-3 of the oracle over the same tokens."""
+    m = FusedGpuDecoder(gpu)
+    prompt = td.prompt_ids(td.CFG1)
+    toks, logits, _ = m.generate(prompt, 16, None)
+    ref = td.TinyDecoder(td.CFG1, seed=0)
+    logical = td.LogicalCache(ref.cfg)
+    want = [ref.forward(prompt, logical)[-1]]
+    for t in toks[len(prompt):-1]:
+        want.append(ref.forward([t], logical)[-1])
+    d = np.abs(logits - np.stack(want))
+    print(f"cfg1 fused logits max {d.max():.3e} mean {d.mean():.3e}")
+    assert d.max() < 2e-2 and d.mean() < 2e-3
+    assert m.cache.TotalLen(0) == len(toks) - 1
