@@ -40,6 +40,10 @@ WORKLOADS = {
     # evict oldest 25% of pages + compact every 256 steps
     "spec_stress": dict(kind="spec", B=64, H=64, KVH=8, D=128, P=16, drafts=4, evict_every=256,
                         layers=1),
+    # next row after the path (rank 1): the fused pre-attention step --
+    # Q/K/V projection (d_model 4096) + RoPE + append -- before the 8k decode
+    "fused8k": dict(kind="gqa_fused", B=16, H=32, KVH=8, D=128, P=16, T=8192, d_model=4096,
+                    layers=2, time="project"),
 }
 MFMA_BF16_PEAK_TFS = 2500.0
 
@@ -99,6 +103,43 @@ def setup_gqa(cfg, torch, dev, rng):
             "batch": B, "query_heads": H, "kv_heads": KVH, "head_dim": D, "page_tokens": P,
             "context_mean": sum(lens) / B, "layers_rotated": L, "pages": "randomly interleaved pool"}
     return c, step, B, kernel_bytes, step_bytes, desc, "gqa_decode_kernel", lens
+
+
+def setup_gqa_fused(cfg, torch, dev, rng):
+    """Config 2' with the step before attention on the device: per layer,
+    hidden states x [B][d_model] -> ProjectAppend (packed W_q|W_k|W_v bf16,
+    RoPE at the cache position, append) -> Attend -> Rollback.  The timed
+    kernel is the projection (HBM-bound on the 50 MB of packed weights)."""
+    from relux_amd import pack_qkv, rope_tables
+    c, _, B, _, _, desc, _, lens = setup_gqa(cfg, torch, dev, rng)
+    H, KVH, D, L, dm = cfg["H"], cfg["KVH"], cfg["D"], cfg["layers"], cfg["d_model"]
+    wp = []
+    for layer in range(L):
+        wq = (torch.randn(dm, H * D, device=dev) * 0.02).to(torch.bfloat16)
+        wk = (torch.randn(dm, KVH * D, device=dev) * 0.02).to(torch.bfloat16)
+        wv = (torch.randn(dm, KVH * D, device=dev) * 0.02).to(torch.bfloat16)
+        wp.append(pack_qkv(wq, wk, wv, H, KVH, D))
+    rope = rope_tables(D, 10000.0, max(lens) + 64, dev)
+    x = torch.randn(B, dm, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+    seqs, ones = list(range(B)), [1] * B
+
+    def step(i):
+        layer = i % L
+        q = c.ProjectAppend(layer, x, wp[layer], H, rope=rope, seq_ids=seqs, n_tok=ones,
+                            q_dtype=torch.bfloat16)
+        c.Attend(layer, q, H, seq_ids=seqs, out=out)
+        c.Rollback(seqs, ones)
+
+    w_bytes = (H + 2 * KVH) * D * dm * 2
+    kernel_bytes = w_bytes + B * dm * 2 + B * H * D * 2 + B * KVH * D * 2 * 2
+    Tatt = [T + 1 for T in lens]
+    step_bytes = kernel_bytes + sum(Tatt) * KVH * D * 2 * 2 + 2 * B * H * D * 2
+    desc = dict(desc)
+    desc["workload"] = (f"gqa_fused_step B{B} H{H} KVH{KVH} D{D} d_model{dm} P{cfg['P']} "
+                        f"T{cfg['T']} (projection+RoPE+append, then decode)")
+    desc["d_model"] = dm
+    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel", lens
 
 
 def setup_mla(cfg, torch, dev, rng):
@@ -239,9 +280,9 @@ def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
-                                 "spec_stress": 5}[name])
+                                 "spec_stress": 5, "fused8k": 2}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
-             "spec": setup_spec}[cfg["kind"]]
+             "spec": setup_spec, "gqa_fused": setup_gqa_fused}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
@@ -252,7 +293,7 @@ def run_workload(name, steps, warmup, torch, dev):
     if st is not None:  # context lengths drift: count what the timed steps attend
         st["attended"] = 0
         st["steps"] = 0
-    c.Timing(True)
+    c.Timing(True, kernels=cfg.get("time", "attend"))
     t0 = time.perf_counter()
     for i in range(steps):
         step(warmup + i)
@@ -395,8 +436,8 @@ def main():
           f"{r['kernel_rate']:.0f} {r['rate_unit']}", file=sys.stderr, flush=True)
     secondary = []
     if not args.no_secondary:
-        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress")
-                     if w != args.workload]:
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
+                                 "fused8k") if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact
             n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
             s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)

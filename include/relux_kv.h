@@ -96,12 +96,16 @@ int32_t rlx_d2h(void *dst, const void *src, int64_t bytes);
 int32_t rlx_device_sync(void);
 
 /* ---- instrumentation (no reference counterpart) ----------------------- */
-/* enable != 0: bracket the main attention kernel of every later attend call
- * on this handle with HIP events (on the handle's stream); 0 disables.
- * Either way the recorded intervals are discarded. */
+/* enable is a mask: RLX_TIME_ATTEND brackets the main attention kernel of
+ * every later attend call on this handle with HIP events (on the handle's
+ * stream), RLX_TIME_PROJECT every projection kernel of
+ * rlx_gqa_project_append; 0 disables.  Either way the recorded intervals
+ * are discarded. */
+#define RLX_TIME_ATTEND 1
+#define RLX_TIME_PROJECT 2
 int32_t rlx_cache_timing(void *cache, int32_t enable);
 /* Synchronise, then report the summed duration (ms) and number of the
- * attention-kernel launches recorded since the last call, and clear them. */
+ * timed kernel launches recorded since the last call, and clear them. */
 int32_t rlx_cache_kernel_time(void *cache, float *total_ms, int32_t *count);
 
 /* ---- cache lifetime --------------------------------------------------- */
@@ -146,10 +150,12 @@ int32_t rlx_kv_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t 
 
 /* ---- fused pre-attention step (projection + RoPE + append) ------------- */
 /* Pack a GQA layer's W_q [d_model][H*D], W_k and W_v [d_model][KVH*D] (the
- * reference's in-row/out-col layout, mha.go:84-100, bf16 or f32) into one
- * bf16 matrix out [(H + 2*KVH)*D][d_model] (device buffer of that size) for
- * rlx_gqa_project_append.  Runs on the null stream.  No reference
- * counterpart: a one-time weight preparation. */
+ * reference's in-row/out-col layout, mha.go:84-100, bf16 or f32) into the
+ * bf16 layout rlx_gqa_project_append streams: N = (H + 2*KVH)*D output
+ * features (q heads, then k heads, then v heads); element (n, k) at
+ * ((n/16 * d_model/32 + k/32) * 16 + n%16) * 32 + k%32 of out (N * d_model
+ * bf16).  Runs on the null stream.  No reference counterpart: a one-time
+ * weight preparation. */
 int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t w_dtype,
                      int32_t d_model, int32_t num_heads, int32_t kv_heads, int32_t head_dim,
                      void *out);

@@ -6,12 +6,13 @@
 // cache position (rope.go:130-180: pairs (2i, 2i+1) rotated by
 // (cos, sin)[pos][i]), then Append of k and v (kvcache.go:240-316, bf16
 // round-to-nearest-even).  Here the three projections are one GEMM against
-// a packed weight matrix Wp[n][k] (rows = the H q-heads, then the KVH k-heads,
-// then the KVH v-heads, each D features; k contiguous so that 8 consecutive
-// k of one output feature are one 16-byte MFMA operand load).
+// a packed weight matrix (features = the H q-heads, then the KVH k-heads,
+// then the KVH v-heads, each D features), stored as 1 KB MFMA fragments of
+// 16 features x 32 k so that every weight load streams contiguous memory.
 //
 // Work-group = 16 output features x all rows (at most 64); its 4 waves take
-// the 32-wide k-steps round-robin and meet in LDS.  MFMA 16x16x32: A = x
+// contiguous ranges of the 32-wide k-steps (software-pipelined chunks of 8
+// weight fragments) and meet in LDS.  MFMA 16x16x32: A = x
 // rows (converted to bf16), B = Wp rows.  The result lane holds 4 rows of
 // one feature, so a RoPE pair partner (feature ^ 1) is one lane away.
 #include "rlx_common.h"
@@ -20,7 +21,10 @@ namespace rlx {
 
 constexpr int kProjMaxRows = 64;
 
-// Packed rows: Wp[n][k] for n < H*D from w_q[k][n], then w_k, then w_v.
+// Packed weights: feature n < H*D from w_q[k][n], then w_k, then w_v, in
+// MFMA-fragment blocks: element (n, k) at ((n/16 * K/32 + k/32) * 16 + n%16)
+// * 32 + k%32, so the B fragment of one (16-feature, 32-k) step is 1 KB of
+// contiguous memory.
 __global__ void pack_qkv_kernel(const void *__restrict__ w_q, const void *__restrict__ w_k,
                                 const void *__restrict__ w_v, int w_bf16, int K, int NQ, int NK,
                                 uint16_t *__restrict__ out) {
@@ -43,14 +47,19 @@ __global__ void pack_qkv_kernel(const void *__restrict__ w_q, const void *__rest
         tile[r][tx] = v;
     }
     __syncthreads();
+    const int KS = K / 32;
     for (int r = ty; r < 32; r += 8) {
         const int n = n0 + r, k = k0 + tx;
-        if (n < N && k < K) out[(int64_t)n * K + k] = tile[tx][r];
+        if (n < N && k < K)
+            out[(((int64_t)(n >> 4) * KS + (k >> 5)) * 16 + (n & 15)) * 32 + (k & 31)] = tile[tx][r];
     }
 }
 
-template <bool ARG>
-__global__ __launch_bounds__(256) void qkv_project_kernel(
+constexpr int kProjWaves = 4;   // k split over the waves of a work-group
+constexpr int kProjChunk = 8;   // k-steps of W held in registers at once per wave
+
+template <bool ARG, bool XBF16>
+__global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
     const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
     int pos_off, int rows, const void *__restrict__ x, int x_bf16, int K,
@@ -61,7 +70,7 @@ __global__ __launch_bounds__(256) void qkv_project_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     if (blockIdx.x == 0) {
-        for (int i = tid; i < n_patch; i += 256) {
+        for (int i = tid; i < n_patch; i += 64 * kProjWaves) {
             const Patch pt = plan_patch<ARG>(patches, i);
             table[pt.idx] = pt.val;
         }
@@ -72,33 +81,68 @@ __global__ __launch_bounds__(256) void qkv_project_kernel(
     fl4 acc[kProjMaxRows / 16];
 #pragma unroll
     for (int m = 0; m < kProjMaxRows / 16; m++) acc[m] = fl4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t *wrow = wp + (int64_t)(n0 + col) * K + grp * 8;
-#pragma unroll 4
-    for (int ks = wave; ks < KS; ks += 4) {
-        const bf16x8 b = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load((const u32x4 *)(wrow + ks * 32)));
+    // This work-group's weight blocks: KS fragments of 1 KB, contiguous.
+    const uint16_t *wblk = wp + (int64_t)blockIdx.x * KS * 512 + (col * 32 + grp * 8);
+    // Wave w takes a contiguous range of k-steps, in chunks of kProjChunk
+    // fragments.  Software pipeline: the activations of chunk c are loaded,
+    // then the weights of chunk c + 1, then chunk c is multiplied -- loads
+    // retire in order, so waiting for chunk c's operands leaves chunk c + 1's
+    // weights in flight.
+    // Wave-uniform bounds (scalar registers).  Loads past a wave's range are
+    // clamped to its last k-step (in bounds) and their products skipped, so
+    // no load sits in a branch.
+    const int per = (KS + kProjWaves - 1) / kProjWaves;
+    const int ks_lo = __builtin_amdgcn_readfirstlane(wave * per);
+    const int ks_hi = __builtin_amdgcn_readfirstlane(min(KS, wave * per + per));
+    auto load_w = [&](u32x4 (&wf)[kProjChunk], int base) {
 #pragma unroll
-        for (int m = 0; m < kProjMaxRows / 16; m++) {
-            if (m < MT) {
-                const int r = min(m * 16 + col, rows - 1);
-                const int64_t off = (int64_t)r * K + ks * 32 + grp * 8;
-                u32x4 a;
-                if (x_bf16) {
-                    a = *(const u32x4 *)((const uint16_t *)x + off);
-                } else {
-                    const float4 f0 = *(const float4 *)((const float *)x + off);
-                    const float4 f1 = *(const float4 *)((const float *)x + off + 4);
-                    a[0] = pack_bf16x2(f0.x, f0.y);
-                    a[1] = pack_bf16x2(f0.z, f0.w);
-                    a[2] = pack_bf16x2(f1.x, f1.y);
-                    a[3] = pack_bf16x2(f1.z, f1.w);
-                }
-                // C[m = row][n = feature]: A = x rows, B = Wp rows.
-                acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), b, acc[m], 0, 0, 0);
+        for (int j = 0; j < kProjChunk; j++)
+            wf[j] = __builtin_nontemporal_load((const u32x4 *)(wblk + (int64_t)min(base + j, ks_hi - 1) * 512));
+    };
+    auto load_x = [&](u32x4 (&xf)[kProjChunk], int base, int m) {
+        const int r = min(m * 16 + col, rows - 1);
+#pragma unroll
+        for (int j = 0; j < kProjChunk; j++) {
+            const int64_t off = (int64_t)r * K + min(base + j, ks_hi - 1) * 32 + grp * 8;
+            if constexpr (XBF16) {
+                xf[j] = *(const u32x4 *)((const uint16_t *)x + off);
+            } else {
+                const float4 f0 = *(const float4 *)((const float *)x + off);
+                const float4 f1 = *(const float4 *)((const float *)x + off + 4);
+                xf[j][0] = pack_bf16x2(f0.x, f0.y);
+                xf[j][1] = pack_bf16x2(f0.z, f0.w);
+                xf[j][2] = pack_bf16x2(f1.x, f1.y);
+                xf[j][3] = pack_bf16x2(f1.z, f1.w);
             }
         }
+    };
+    auto mul = [&](const u32x4 (&wf)[kProjChunk], const u32x4 (&xf)[kProjChunk], int base, int m) {
+#pragma unroll
+        for (int j = 0; j < kProjChunk; j++)
+            if (base + j < ks_hi)
+                // C[m = row][n = feature]: A = x rows, B = Wp rows.
+                acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[j]),
+                                                                 __builtin_bit_cast(bf16x8, wf[j]), acc[m], 0, 0, 0);
+    };
+    u32x4 wa[kProjChunk], wb[kProjChunk], xf[kProjChunk];
+    if (ks_lo < ks_hi) load_w(wa, ks_lo);
+    for (int base = ks_lo; base < ks_hi; base += 2 * kProjChunk) {
+        // chunk at base in wa; next chunk into wb
+        for (int m = 0; m < MT; m++) {
+            load_x(xf, base, m);
+            if (m == MT - 1 && base + kProjChunk < ks_hi) load_w(wb, base + kProjChunk);
+            mul(wa, xf, base, m);
+        }
+        const int b2 = base + kProjChunk;
+        if (b2 >= ks_hi) break;
+        for (int m = 0; m < MT; m++) {
+            load_x(xf, b2, m);
+            if (m == MT - 1 && b2 + kProjChunk < ks_hi) load_w(wa, b2 + kProjChunk);
+            mul(wb, xf, b2, m);
+        }
     }
-    // ---- k-split merge: waves 1-3 hand their sums to wave 0 ----------------
-    __shared__ fl4 red[3][kProjMaxRows / 16][64];
+    // ---- k-split merge: the other waves hand their sums to wave 0 ----------
+    __shared__ fl4 red[kProjWaves - 1][kProjMaxRows / 16][64];
     if (wave > 0) {
 #pragma unroll
         for (int m = 0; m < kProjMaxRows / 16; m++)
@@ -116,7 +160,7 @@ __global__ __launch_bounds__(256) void qkv_project_kernel(
         if (m >= MT) break;
         fl4 y = acc[m];
 #pragma unroll
-        for (int w = 0; w < 3; w++) y += red[w][m][lane];
+        for (int w = 0; w < kProjWaves - 1; w++) y += red[w][m][lane];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = m * 16 + grp * 4 + i;  // C row of element i
@@ -170,16 +214,19 @@ hipError_t launch_qkv_project(hipStream_t s, const PlanArg *plan, const Patch *p
                               uint16_t *vpool, int32_t *table, int P) {
     if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
     const int N = (H + 2 * KVH) * D;
-    if (plan)
-        qkv_project_kernel<true><<<N / 16, 256, 0, s>>>(*plan, patches, n_patch, toks, pos, tok_off,
-                                                        pos_off, rows, x, x_bf16, K, wp, H, KVH, D,
-                                                        rcos, rsin, q_out, q_bf16, kpool, vpool,
-                                                        table, P);
+#define RLX_PROJ_LAUNCH(ARGV, XB, PLANV)                                                          \
+    qkv_project_kernel<ARGV, XB><<<N / 16, 64 * kProjWaves, 0, s>>>(                              \
+        PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x, x_bf16, K, wp, H, KVH, D,  \
+        rcos, rsin, q_out, q_bf16, kpool, vpool, table, P)
+    if (plan && x_bf16)
+        RLX_PROJ_LAUNCH(true, true, *plan);
+    else if (plan)
+        RLX_PROJ_LAUNCH(true, false, *plan);
+    else if (x_bf16)
+        RLX_PROJ_LAUNCH(false, true, NoPlan{0});
     else
-        qkv_project_kernel<false><<<N / 16, 256, 0, s>>>(NoPlan{0}, patches, n_patch, toks, pos,
-                                                         tok_off, pos_off, rows, x, x_bf16, K, wp,
-                                                         H, KVH, D, rcos, rsin, q_out, q_bf16,
-                                                         kpool, vpool, table, P);
+        RLX_PROJ_LAUNCH(false, false, NoPlan{0});
+#undef RLX_PROJ_LAUNCH
     return hipGetLastError();
 }
 

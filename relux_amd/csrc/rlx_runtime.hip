@@ -89,7 +89,7 @@ struct Cache {
     void *ws = nullptr;
     size_t ws_cap = 0;
     // Attention-kernel timing: event pairs, reused across reports.
-    bool timing = false;
+    int timing = 0;  // RLX_TIME_* mask
     std::vector<std::pair<hipEvent_t, hipEvent_t>> tev;
     size_t tev_used = 0;
 
@@ -213,10 +213,11 @@ int32_t ensure_ws(Cache *c, size_t bytes) {
 
 Cache *as_cache(void *h) { return static_cast<Cache *>(h); }
 
-// Next event pair bracketing an attention kernel, or nulls when timing is off.
-int32_t timing_events(Cache *c, hipEvent_t *e0, hipEvent_t *e1) {
+// Next event pair bracketing a kernel of the given kind (RLX_TIME_*), or
+// nulls when that kind is not being timed.
+int32_t timing_events(Cache *c, hipEvent_t *e0, hipEvent_t *e1, int kind = RLX_TIME_ATTEND) {
     *e0 = *e1 = nullptr;
-    if (!c->timing) return RLX_OK;
+    if (!(c->timing & kind)) return RLX_OK;
     if (c->tev_used == c->tev.size()) {
         hipEvent_t a, b;
         HIP_TRY(hipEventCreate(&a));
@@ -642,7 +643,7 @@ int32_t rlx_cache_timing(void *h, int32_t enable) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     HIP_TRY(hipStreamSynchronize(c->stream));
-    c->timing = enable != 0;
+    c->timing = enable;
     c->tev_used = 0;
     return RLX_OK;
 }
@@ -772,12 +773,16 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
             d_t = (const AppendTok *)((char *)dev + toff);
             d_pos = (const int32_t *)((char *)dev + poff);
         }
+        hipEvent_t e0, e1;
+        if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
+        if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
         HIP_TRY(launch_qkv_project(c->stream, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
                                    (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
                                    x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed,
                                    num_heads, c->kvh, c->hd, rope_cos, rope_sin,
                                    (char *)q_out + (size_t)r0 * num_heads * c->hd * qb,
                                    q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P));
+        if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     }
     return RLX_OK;
 }

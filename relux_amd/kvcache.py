@@ -76,9 +76,11 @@ class _PagedCache:
     def Sync(self):
         check(self._lib.rlx_cache_sync(self._h))
 
-    def Timing(self, enable=True):
-        """Bracket every later attention kernel with HIP events."""
-        check(self._lib.rlx_cache_timing(self._h, 1 if enable else 0))
+    def Timing(self, enable=True, kernels="attend"):
+        """Bracket every later attention kernel ("attend") or projection
+        kernel ("project") with HIP events."""
+        mask = {"attend": _lib.RLX_TIME_ATTEND, "project": _lib.RLX_TIME_PROJECT}[kernels]
+        check(self._lib.rlx_cache_timing(self._h, mask if enable else 0))
 
     def KernelTime(self):
         """(total ms, launches) of the attention kernels timed since the last
@@ -267,7 +269,8 @@ class KVCache(_PagedCache):
 
 def pack_qkv(w_q, w_k, w_v, num_heads, kv_heads, head_dim):
     """W_q [d_model][H*D], W_k/W_v [d_model][KVH*D] (bf16 or f32, device) ->
-    packed bf16 [(H + 2 KVH) * D][d_model] for KVCache.ProjectAppend."""
+    packed bf16 weights for KVCache.ProjectAppend: N = (H + 2 KVH) * D
+    features in 16-feature x 32-k fragments (rlx_pack_qkv)."""
     d_model = w_q.shape[0]
     out = torch.empty(((num_heads + 2 * kv_heads) * head_dim, d_model), dtype=torch.bfloat16,
                       device=w_q.device)

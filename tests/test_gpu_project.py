@@ -53,9 +53,11 @@ def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dt
     wk = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
     wv = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
     wp = pack_qkv(_bf16_tensor(wq, gpu), _bf16_tensor(wk, gpu), _bf16_tensor(wv, gpu), H, KVH, D)
-    # packed layout: rows = output features, k contiguous
-    np.testing.assert_array_equal(wp.view(torch.int16).cpu().numpy().view(np.uint16),
-                                  np.concatenate([wq, wk, wv], axis=1).T)
+    # packed layout: (16-feature x 32-k) fragments of W^T, fragment-major
+    wt = np.concatenate([wq, wk, wv], axis=1).T  # [N][d_model]
+    N = wt.shape[0]
+    blk = wt.reshape(N // 16, 16, d_model // 32, 32).transpose(0, 2, 1, 3).reshape(N, d_model)
+    np.testing.assert_array_equal(wp.view(torch.int16).cpu().numpy().view(np.uint16).reshape(N, d_model), blk)
     rope = rope_tables(D, 10000.0, max_seq, gpu)
     tables = oracle.rope_tables(D, 10000.0, max_seq)
     # existing context through the plain append
