@@ -44,6 +44,9 @@ WORKLOADS = {
     # Q/K/V projection (d_model 4096) + RoPE + append -- before the 8k decode
     "fused8k": dict(kind="gqa_fused", B=16, H=32, KVH=8, D=128, P=16, T=8192, d_model=4096,
                     layers=2, time="project"),
+    # the same for the MLA layer of config 3 (DeepSeek-V2-Lite d_model 2048)
+    "mla_fused8k": dict(kind="mla_fused", B=32, H=16, D=128, P=64, T=8192, d_model=2048,
+                        layers=4, time="project"),
 }
 MFMA_BF16_PEAK_TFS = 2500.0
 
@@ -139,7 +142,7 @@ def setup_gqa_fused(cfg, torch, dev, rng):
     desc["workload"] = (f"gqa_fused_step B{B} H{H} KVH{KVH} D{D} d_model{dm} P{cfg['P']} "
                         f"T{cfg['T']} (projection+RoPE+append, then decode)")
     desc["d_model"] = dm
-    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel", lens
+    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel<gqa>", lens
 
 
 def setup_mla(cfg, torch, dev, rng):
@@ -181,6 +184,43 @@ def setup_mla(cfg, torch, dev, rng):
             "batch": B, "heads": H, "kv_lora_rank": 512, "rope_dim": 64, "head_dim": D,
             "page_tokens": P, "context_mean": sum(lens) / B, "layers_rotated": L}
     return c, step, B, kernel_bytes, step_bytes, desc, "mla_decode_kernel", lens
+
+
+def setup_mla_fused(cfg, torch, dev, rng):
+    """Config 3 with the step before attention on the device: x [B][d_model]
+    -> MLA ProjectAppend (packed W_Q|W_QR|W_DKV|W_KR, RoPE of q^R and k^R,
+    latent append) -> Attend -> Rollback.  Timed kernel: the projection."""
+    from relux_amd import pack_mla_proj, rope_tables
+    c, _, B, _, _, desc, _, lens = setup_mla(cfg, torch, dev, rng)
+    H, D, L, dm = cfg["H"], cfg["D"], cfg["layers"], cfg["d_model"]
+    wp = []
+    for layer in range(L):
+        mats = [(torch.randn(dm, w, device=dev) * 0.02).to(torch.bfloat16)
+                for w in (H * D, H * 64, 512, 64)]
+        wp.append(pack_mla_proj(*mats, H, D))
+    rope = rope_tables(64, 10000.0, max(lens) + 64, dev)
+    x = torch.randn(B, dm, device=dev, dtype=torch.bfloat16)
+    w_uk = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    w_uv = (torch.randn(512, H * D, device=dev) * 0.02).bfloat16()
+    out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
+    seqs, ones = list(range(B)), [1] * B
+
+    def step(i):
+        layer = i % L
+        qn, qr = c.ProjectAppend(layer, x, wp[layer], H, D, rope=rope, seq_ids=seqs, n_tok=ones,
+                                 q_dtype=torch.bfloat16)
+        c.Attend(layer, qn, qr, w_uk, w_uv, H, D, seq_ids=seqs, out=out)
+        c.Rollback(seqs, ones)
+
+    n_feat = H * (D + 64) + 576
+    kernel_bytes = n_feat * dm * 2 + B * dm * 2 + B * H * (D + 64) * 2 + B * 576 * 2
+    Tatt = [T + 1 for T in lens]
+    step_bytes = kernel_bytes + sum(Tatt) * 576 * 2 + 2 * 512 * H * D * 2 + B * H * D * 2
+    desc = dict(desc)
+    desc["workload"] = (f"mla_fused_step B{B} H{H} D{D} d_model{dm} P{cfg['P']} T{cfg['T']} "
+                        f"(projection+RoPE+latent append, then decode)")
+    desc["d_model"] = dm
+    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel<mla>", lens
 
 
 def setup_mla_prefill(cfg, torch, dev, rng):
@@ -280,9 +320,10 @@ def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
-                                 "spec_stress": 5, "fused8k": 2}[name])
+                                 "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
-             "spec": setup_spec, "gqa_fused": setup_gqa_fused}[cfg["kind"]]
+             "spec": setup_spec, "gqa_fused": setup_gqa_fused,
+             "mla_fused": setup_mla_fused}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
@@ -437,7 +478,7 @@ def main():
     secondary = []
     if not args.no_secondary:
         for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
-                                 "fused8k") if w != args.workload]:
+                                 "fused8k", "mla_fused8k") if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact
             n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
             s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)

@@ -175,6 +175,28 @@ int32_t rlx_gqa_project_append(void *cache, int32_t layer, int32_t n_seqs, const
                                const float *rope_cos, const float *rope_sin, int32_t rope_rows,
                                int32_t rope_mode, void *q_out, int32_t q_dtype);
 
+/* MLA layer: pack W_Q [d_model][H*D], W_QR [d_model][H*d_r], W_DKV
+ * [d_model][d_c] and W_KR [d_model][d_r] (mla.go:39-44, bf16 or f32) into
+ * out (N = H*(D + d_r) + d_c + d_r features, the same fragment layout as
+ * rlx_pack_qkv) for rlx_mla_project_append.  Null stream.  No reference
+ * counterpart: a one-time weight preparation. */
+int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
+                          int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,
+                          void *out);
+/* q_c = x.W_Q -> q_nope_out [sum n][H][head_dim]; q_r = RoPE(x.W_QR) ->
+ * q_rope_out [sum n][H][d_r]; c = x.W_DKV and k^R = RoPE(x.W_KR) appended
+ * as the tokens' latent rows (bf16).  Tables [rope_rows][d_r/2] (f32,
+ * device), positions as for rlx_gqa_project_append.  The q outputs are the
+ * inputs of rlx_mla_attend.  Replaces mla.go:279-314 (four
+ * matmulBatched3D, RotaryEmbedding.Apply of q^R and k^R, MLACache.Append);
+ * within tolerance of the reference's f32 loops, not bit for bit. */
+int32_t rlx_mla_project_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_tok, const void *x, int32_t x_dtype,
+                               int32_t d_model, const void *w_packed, int32_t num_heads,
+                               int32_t head_dim, const float *rope_cos, const float *rope_sin,
+                               int32_t rope_rows, int32_t rope_mode, void *q_nope_out,
+                               void *q_rope_out, int32_t q_dtype);
+
 /* MLA: c_src [sum n][d_c], kr_src [sum n][d_r] (post-RoPE).  Replaces
  * MLACache.Append (mla_cache.go:152-182). */
 int32_t rlx_mla_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,

@@ -8,12 +8,12 @@ reference's Go cache types (internal/transformer/kvcache.go, mla_cache.go).
 """
 from ._lib import ReluxError, ReluxPanic, load  # noqa: F401
 
-__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "rope_tables"]
+__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "pack_mla_proj", "rope_tables"]
 
 
 def __getattr__(name):
     # Lazy: importing the package must not touch the GPU or require torch.
-    if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "rope_tables"):
+    if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "pack_mla_proj", "rope_tables"):
         from . import kvcache
         return getattr(kvcache, name)
     raise AttributeError(name)

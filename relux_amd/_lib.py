@@ -68,6 +68,9 @@ SIGNATURES = {
     "rlx_pack_qkv": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "rlx_gqa_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _vp, _vp,
                                _i32, _i32, _vp, _i32],
+    "rlx_pack_mla_proj": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "rlx_mla_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _i32, _vp,
+                               _vp, _i32, _i32, _vp, _vp, _i32],
     "rlx_mla_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32],
     "rlx_kv_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],
     "rlx_mla_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],

@@ -296,16 +296,18 @@ hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t 
                              const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
                              uint16_t *wt_v, uint16_t *kc, uint16_t *vt);
 
-// Fused Q/K/V projection + RoPE + paged append (at most 64 rows per launch).
+// Fused projection + RoPE + paged append (at most 64 rows per launch).
 constexpr int kProjRows = 64;
-hipError_t launch_pack_qkv(hipStream_t s, const void *w_q, const void *w_k, const void *w_v,
-                           int w_bf16, int K, int NQ, int NK, uint16_t *out);
-hipError_t launch_qkv_project(hipStream_t s, const PlanArg *plan, const Patch *patches,
-                              int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
-                              int pos_off, int rows, const void *x, int x_bf16, int K,
-                              const uint16_t *wp, int H, int KVH, int D, const float *rcos,
-                              const float *rsin, void *q_out, int q_bf16, uint16_t *kpool,
-                              uint16_t *vpool, int32_t *table, int P);
+constexpr int kProjModelGQA = 0;
+constexpr int kProjModelMLA = 1;
+hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
+                            int w_bf16, int K, uint16_t *out);
+hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patch *patches,
+                       int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
+                       int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
+                       int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
+                       void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
+                       int P);
 
 // Work-groups of the decode kernels one CU holds at once (occupancy).
 int gqa_decode_wgs_per_cu(int hd, int nqt);

@@ -1,7 +1,9 @@
-// Fused pre-attention step of a GQA layer: Q/K/V projection of the new
-// tokens' hidden states, RoPE on Q and K, and the paged append of K and V.
+// Fused pre-attention step: projection of the new tokens' hidden states,
+// RoPE, and the paged append -- for a GQA layer (Q/K/V; RoPE on Q and K) and
+// for an MLA layer (q_c, q_r, c^KV, k^R; RoPE on q_r and k^R, the latent row
+// appended).
 //
-// Reference restated (mha.go:250-289): q = x.W_q, k = x.W_k, v = x.W_v
+// Reference restated (GQA mha.go:250-289, MLA mla.go:279-314): q = x.W_q, k = x.W_k, v = x.W_v
 // (matmulBatched3D, bf16 weights widened, f32 sums), RoPE of q and k at the
 // cache position (rope.go:130-180: pairs (2i, 2i+1) rotated by
 // (cos, sin)[pos][i]), then Append of k and v (kvcache.go:240-316, bf16
@@ -21,28 +23,27 @@ namespace rlx {
 
 constexpr int kProjMaxRows = 64;
 
-// Packed weights: feature n < H*D from w_q[k][n], then w_k, then w_v, in
+// Packed weights: the output features of up to 4 matrices m[k][n] (widths
+// wd[i], the reference's in-row/out-col layout), concatenated, in
 // MFMA-fragment blocks: element (n, k) at ((n/16 * K/32 + k/32) * 16 + n%16)
 // * 32 + k%32, so the B fragment of one (16-feature, 32-k) step is 1 KB of
 // contiguous memory.
-__global__ void pack_qkv_kernel(const void *__restrict__ w_q, const void *__restrict__ w_k,
-                                const void *__restrict__ w_v, int w_bf16, int K, int NQ, int NK,
-                                uint16_t *__restrict__ out) {
+struct PackSrc {
+    const void *m[4];
+    int wd[4];
+};
+__global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int N, uint16_t *__restrict__ out) {
     __shared__ uint16_t tile[32][33];
-    const int N = NQ + 2 * NK;
     const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
     for (int r = ty; r < 32; r += 8) {
         const int k = k0 + r, n = n0 + tx;
         uint16_t v = 0;
         if (k < K && n < N) {
-            const void *src;
-            int nn, ld;
-            if (n < NQ) { src = w_q; nn = n; ld = NQ; }
-            else if (n < NQ + NK) { src = w_k; nn = n - NQ; ld = NK; }
-            else { src = w_v; nn = n - NQ - NK; ld = NK; }
-            const int64_t off = (int64_t)k * ld + nn;
-            v = w_bf16 ? ((const uint16_t *)src)[off] : bf16_rne(((const float *)src)[off]);
+            int i = 0, nn = n;
+            while (i < 3 && nn >= src.wd[i]) nn -= src.wd[i++];
+            const int64_t off = (int64_t)k * src.wd[i] + nn;
+            v = w_bf16 ? ((const uint16_t *)src.m[i])[off] : bf16_rne(((const float *)src.m[i])[off]);
         }
         tile[r][tx] = v;
     }
@@ -58,15 +59,26 @@ __global__ void pack_qkv_kernel(const void *__restrict__ w_q, const void *__rest
 constexpr int kProjWaves = 4;   // k split over the waves of a work-group
 constexpr int kProjChunk = 8;   // k-steps of W held in registers at once per wave
 
-template <bool ARG, bool XBF16>
+// Output layouts (features in packed order, each part a multiple of 16):
+//   kProjGQA: q (H heads x D, RoPE)    -> q_out [rows][H][D]
+//             k (KVH x D, RoPE)        -> K row pages
+//             v (KVH x D)              -> dim-major V pages
+//   kProjMLA: q_c (H x D)              -> q_out  [rows][H][D]
+//             q_r (H x d_r, RoPE)      -> q_out2 [rows][H][d_r]
+//             c^KV (d_c)               -> latent rows [0, d_c)
+//             k^R (d_r, RoPE)          -> latent rows [d_c, d_c + d_r)
+constexpr int kProjGQA = 0;
+constexpr int kProjMLA = 1;
+
+template <bool ARG, bool XBF16, int MODEL>
 __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
     const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
     int pos_off, int rows, const void *__restrict__ x, int x_bf16, int K,
     const uint16_t *__restrict__ wp, int H, int KVH, int D, const float *__restrict__ rcos,
-    const float *__restrict__ rsin, void *__restrict__ q_out, int q_bf16,
-    uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool, int32_t *__restrict__ table,
-    int P) {
+    const float *__restrict__ rsin, void *__restrict__ q_out, void *__restrict__ q_out2,
+    int q_bf16, uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool,
+    int32_t *__restrict__ table, int P) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, grp = lane >> 4;
     if (blockIdx.x == 0) {
@@ -151,10 +163,23 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     __syncthreads();
     if (wave != 0) return;
     const int n = n0 + col;
-    const int NQ = H * D, NK = KVH * D;
-    const int part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);  // q, k, v (uniform per work-group)
-    const int nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
-    const int head = nn / D, d = nn - head * D;
+    // part of the output this work-group's 16 features belong to (uniform),
+    // feature index within the part, RoPE head width (0: no rotation)
+    int part, nn, hw;
+    if constexpr (MODEL == kProjGQA) {
+        const int NQ = H * D, NK = KVH * D;
+        part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
+        nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
+        hw = part < 2 ? D : 0;
+    } else {
+        const int NQC = H * D, NQR = H * kMlaDr;
+        part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + kMlaDc ? 2 : 3));
+        nn = n - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
+        hw = (part == 1 || part == 3) ? kMlaDr : 0;
+    }
+    const int hdim = (MODEL == kProjGQA) ? D : (part == 1 ? kMlaDr : D);
+    const int head = nn / hdim, d = nn - head * hdim;
+    const int dr = hw ? nn % hw : 0;  // dim within the rotated head
 #pragma unroll
     for (int m = 0; m < kProjMaxRows / 16; m++) {
         if (m >= MT) break;
@@ -167,65 +192,83 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
             float v = y[i];
             const float partner = __shfl_xor(v, 1);
             const bool live = r < rows;
-            if (part < 2) {
+            if (hw) {
                 // RoPE: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), products rounded
                 // separately as in rope.go.
                 const int p = live ? (ARG ? ((const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + pos_off))[r]
                                            : pos_dev[r])
                                    : 0;
                 if (p >= 0) {
-                    const float c = rcos[(int64_t)p * (D / 2) + (d >> 1)];
-                    const float s = rsin[(int64_t)p * (D / 2) + (d >> 1)];
-                    v = (d & 1) ? __fadd_rn(__fmul_rn(v, c), __fmul_rn(partner, s))
-                                : __fsub_rn(__fmul_rn(v, c), __fmul_rn(partner, s));
+                    const float c = rcos[(int64_t)p * (hw / 2) + (dr >> 1)];
+                    const float s = rsin[(int64_t)p * (hw / 2) + (dr >> 1)];
+                    v = (dr & 1) ? __fadd_rn(__fmul_rn(v, c), __fmul_rn(partner, s))
+                                 : __fsub_rn(__fmul_rn(v, c), __fmul_rn(partner, s));
                 }
             }
             if (!live) continue;
-            if (part == 0) {
-                const int64_t o = ((int64_t)r * H + head) * D + d;
+            const bool to_q = (MODEL == kProjGQA) ? part == 0 : part < 2;
+            if (to_q) {
+                void *dst = (MODEL == kProjMLA && part == 1) ? q_out2 : q_out;
+                const int64_t o = ((int64_t)r * H + head) * hdim + d;
                 if (q_bf16)
-                    ((uint16_t *)q_out)[o] = bf16_rne(v);
+                    ((uint16_t *)dst)[o] = bf16_rne(v);
                 else
-                    ((float *)q_out)[o] = v;
-            } else {
-                const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
+                    ((float *)dst)[o] = v;
+                continue;
+            }
+            const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
+            if constexpr (MODEL == kProjGQA) {
                 if (part == 1)
                     kpool[(((int64_t)tk.page * KVH + head) * P + tk.slot) * D + d] = bf16_rne(v);
                 else
                     vpool[(((int64_t)tk.page * KVH + head) * D + d) * P + tk.slot] = bf16_rne(v);
+            } else {
+                kpool[((int64_t)tk.page * P + tk.slot) * kMlaRow + (part == 2 ? 0 : kMlaDc) + nn] = bf16_rne(v);
             }
         }
     }
 }
 
-hipError_t launch_pack_qkv(hipStream_t s, const void *w_q, const void *w_k, const void *w_v,
-                           int w_bf16, int K, int NQ, int NK, uint16_t *out) {
-    const int N = NQ + 2 * NK;
-    pack_qkv_kernel<<<dim3((N + 31) / 32, (K + 31) / 32), 256, 0, s>>>(w_q, w_k, w_v, w_bf16, K, NQ,
-                                                                      NK, out);
+hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
+                            int w_bf16, int K, uint16_t *out) {
+    PackSrc src{};
+    int N = 0;
+    for (int i = 0; i < 4; i++) {
+        src.m[i] = i < n_mats ? mats[i] : mats[0];
+        src.wd[i] = i < n_mats ? widths[i] : 0;
+        N += src.wd[i];
+    }
+    pack_proj_kernel<<<dim3((N + 31) / 32, (K + 31) / 32), 256, 0, s>>>(src, w_bf16, K, N, out);
     return hipGetLastError();
 }
 
-hipError_t launch_qkv_project(hipStream_t s, const PlanArg *plan, const Patch *patches,
-                              int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
-                              int pos_off, int rows, const void *x, int x_bf16, int K,
-                              const uint16_t *wp, int H, int KVH, int D, const float *rcos,
-                              const float *rsin, void *q_out, int q_bf16, uint16_t *kpool,
-                              uint16_t *vpool, int32_t *table, int P) {
+hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patch *patches,
+                       int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
+                       int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
+                       int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
+                       void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
+                       int P) {
     if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
-    const int N = (H + 2 * KVH) * D;
-#define RLX_PROJ_LAUNCH(ARGV, XB, PLANV)                                                          \
-    qkv_project_kernel<ARGV, XB><<<N / 16, 64 * kProjWaves, 0, s>>>(                              \
+    const int N = model == kProjGQA ? (H + 2 * KVH) * D : H * (D + kMlaDr) + kMlaRow;
+#define RLX_PROJ_LAUNCH(ARGV, XB, MODELV, PLANV)                                                  \
+    qkv_project_kernel<ARGV, XB, MODELV><<<N / 16, 64 * kProjWaves, 0, s>>>(                      \
         PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x, x_bf16, K, wp, H, KVH, D,  \
-        rcos, rsin, q_out, q_bf16, kpool, vpool, table, P)
-    if (plan && x_bf16)
-        RLX_PROJ_LAUNCH(true, true, *plan);
-    else if (plan)
-        RLX_PROJ_LAUNCH(true, false, *plan);
-    else if (x_bf16)
-        RLX_PROJ_LAUNCH(false, true, NoPlan{0});
-    else
-        RLX_PROJ_LAUNCH(false, false, NoPlan{0});
+        rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, table, P)
+#define RLX_PROJ_MODEL(MODELV)                                                                    \
+    if (plan && x_bf16)                                                                           \
+        RLX_PROJ_LAUNCH(true, true, MODELV, *plan);                                               \
+    else if (plan)                                                                                \
+        RLX_PROJ_LAUNCH(true, false, MODELV, *plan);                                              \
+    else if (x_bf16)                                                                              \
+        RLX_PROJ_LAUNCH(false, true, MODELV, NoPlan{0});                                          \
+    else                                                                                          \
+        RLX_PROJ_LAUNCH(false, false, MODELV, NoPlan{0});
+    if (model == kProjGQA) {
+        RLX_PROJ_MODEL(kProjGQA)
+    } else {
+        RLX_PROJ_MODEL(kProjMLA)
+    }
+#undef RLX_PROJ_MODEL
 #undef RLX_PROJ_LAUNCH
     return hipGetLastError();
 }

@@ -700,27 +700,39 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
     if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
     if (d_model <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0)
         return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
-    HIP_TRY(launch_pack_qkv(nullptr, w_q, w_k, w_v, w_dtype == RLX_BF16, d_model,
-                            num_heads * head_dim, kv_heads * head_dim, (uint16_t *)out));
+    const void *mats[3] = {w_q, w_k, w_v};
+    const int wd[3] = {num_heads * head_dim, kv_heads * head_dim, kv_heads * head_dim};
+    HIP_TRY(launch_pack_proj(nullptr, 3, mats, wd, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
     return RLX_OK;
 }
 
-int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                               const int32_t *n_tok, const void *x, int32_t x_dtype,
-                               int32_t d_model, const void *w_packed, int32_t num_heads,
-                               const float *rope_cos, const float *rope_sin, int32_t rope_rows,
-                               int32_t rope_mode, void *q_out, int32_t q_dtype) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
+int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
+                          int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,
+                          void *out) {
+    if (!w_q || !w_qr || !w_dkv || !w_kr || !out) return fail(RLX_ERR_INVALID, "null weight pointer");
+    if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
+    if (d_model <= 0 || num_heads <= 0 || head_dim <= 0)
+        return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
+    const void *mats[4] = {w_q, w_qr, w_dkv, w_kr};
+    const int wd[4] = {num_heads * head_dim, num_heads * kMlaDr, kMlaDc, kMlaDr};
+    HIP_TRY(launch_pack_proj(nullptr, 4, mats, wd, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
+    return RLX_OK;
+}
+
+namespace {
+
+// Shared body of the fused projection + RoPE + append entry points.
+int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_tok, const void *x, int32_t x_dtype, int32_t d_model,
+                       const void *w_packed, int32_t num_heads, int32_t head_dim,
+                       const float *rope_cos, const float *rope_sin, int32_t rope_rows,
+                       int32_t rope_mode, void *q_out, void *q_out2, int32_t q_dtype) {
     int32_t rc = check_layer(c, layer, false);
     if (rc) return rc;
     if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
     if (x_dtype != RLX_F32 && x_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "x_dtype");
     if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
     if (rope_mode < RLX_ROPE_OFFSET || rope_mode > RLX_ROPE_NONE) return fail(RLX_ERR_INVALID, "rope_mode");
-    if (num_heads <= 0 || num_heads % c->kvh != 0)
-        return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
     if (d_model <= 0 || d_model % 32 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "d_model=%d must be a positive multiple of 32", d_model);
     if (rope_mode != RLX_ROPE_NONE && (!rope_cos || !rope_sin || rope_rows <= 0))
@@ -743,7 +755,8 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
         total += n_tok[i];
     }
     if (total == 0) return RLX_OK;
-    if (!x || !w_packed || !q_out) return fail(RLX_ERR_INVALID, "null x / weights / q_out");
+    if (!x || !w_packed || !q_out || (model == kProjModelMLA && !q_out2))
+        return fail(RLX_ERR_INVALID, "null x / weights / q_out");
     std::vector<AppendTok> toks;
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     std::vector<Patch> patches = take_pending(c);
@@ -776,15 +789,50 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
         if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-        HIP_TRY(launch_qkv_project(c->stream, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
-                                   (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
-                                   x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed,
-                                   num_heads, c->kvh, c->hd, rope_cos, rope_sin,
-                                   (char *)q_out + (size_t)r0 * num_heads * c->hd * qb,
-                                   q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P));
+        char *q2 = model == kProjModelMLA ? (char *)q_out2 + (size_t)r0 * num_heads * kMlaDr * qb : nullptr;
+        HIP_TRY(launch_proj(c->stream, model, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
+                            (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
+                            x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed, num_heads,
+                            c->kvh, head_dim, rope_cos, rope_sin,
+                            (char *)q_out + (size_t)r0 * num_heads * head_dim * qb, q2,
+                            q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P));
         if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     }
     return RLX_OK;
+}
+
+}  // namespace
+
+int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_tok, const void *x, int32_t x_dtype,
+                               int32_t d_model, const void *w_packed, int32_t num_heads,
+                               const float *rope_cos, const float *rope_sin, int32_t rope_rows,
+                               int32_t rope_mode, void *q_out, int32_t q_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
+    if (num_heads <= 0 || num_heads % c->kvh != 0)
+        return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
+    return project_append(c, kProjModelGQA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
+                          w_packed, num_heads, c->hd, rope_cos, rope_sin, rope_rows, rope_mode,
+                          q_out, nullptr, q_dtype);
+}
+
+int32_t rlx_mla_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_tok, const void *x, int32_t x_dtype,
+                               int32_t d_model, const void *w_packed, int32_t num_heads,
+                               int32_t head_dim, const float *rope_cos, const float *rope_sin,
+                               int32_t rope_rows, int32_t rope_mode, void *q_nope_out,
+                               void *q_rope_out, int32_t q_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_project_append on a GQA cache");
+    if (num_heads <= 0 || head_dim <= 0 || head_dim % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim a multiple of 16)",
+                    num_heads, head_dim);
+    return project_append(c, kProjModelMLA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
+                          w_packed, num_heads, head_dim, rope_cos, rope_sin, rope_rows, rope_mode,
+                          q_nope_out, q_rope_out, q_dtype);
 }
 
 int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,

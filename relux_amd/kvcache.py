@@ -338,6 +338,36 @@ class MLACache(_PagedCache):
                                        i32_array(n_tok), _dev(new_c, "c"), _dev(new_kr, "kr"),
                                        _dtype_code(new_c)))
 
+    def ProjectAppend(self, layer_idx, x, w_packed, num_heads, head_dim, rope=None, seq_ids=(0,),
+                      n_tok=None, rope_mode="offset", q_dtype=torch.float32):
+        """Fused pre-attention step of an MLA layer (mla.go:279-314): q_c, q_r,
+        c^KV, k^R projections of x [sum n][d_model] with weights packed by
+        pack_mla_proj, RoPE of q_r and k^R (rope = (cos, sin) tables for
+        d_r), append of the latent rows.  Returns (q_nope [sum n][H][D],
+        q_rope [sum n][H][d_r]) for Attend."""
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [x.shape[0]]
+        rows, d_model = x.shape[0], x.shape[-1]
+        if rows != sum(n_tok):
+            raise ValueError("x rows do not match sum(n_tok)")
+        qn = torch.empty((rows, num_heads, head_dim), dtype=q_dtype, device=x.device)
+        qr = torch.empty((rows, num_heads, self.d_r), dtype=q_dtype, device=x.device)
+        if rope is None:
+            rope_mode, cos_t, sin_t, rope_rows = "none", None, None, 0
+        else:
+            cos_t, sin_t = rope
+            rope_rows = cos_t.shape[0]
+        check(self._lib.rlx_mla_project_append(
+            self._h, layer_idx, len(seq_ids), i32_array(seq_ids), i32_array(n_tok), _dev(x, "x"),
+            _dtype_code(x), d_model, _dev(w_packed, "w_packed"), num_heads, head_dim,
+            _dev(cos_t, "rope_cos") if cos_t is not None else None,
+            _dev(sin_t, "rope_sin") if sin_t is not None else None, rope_rows, _ROPE[rope_mode],
+            _dev(qn, "q_nope"), _dev(qr, "q_rope"), _dtype_code(qn)))
+        return qn, qr
+
     def View(self, layer_idx, seq=0):
         """Dense bf16 (c [1, T, d_c], kr [1, T, d_r]) (mla_cache.go:222-233)."""
         if not 0 <= layer_idx < self.num_layers:
@@ -375,6 +405,19 @@ class MLACache(_PagedCache):
                                        _dev(w_uk, "w_uk"), _dev(w_uv, "w_uv"), float(scale or 0.0),
                                        _MASKS[mask], _dev(out, "out"), _dtype_code(out)))
         return out
+
+
+def pack_mla_proj(w_q, w_qr, w_dkv, w_kr, num_heads, head_dim):
+    """W_Q [d_model][H*D], W_QR [d_model][H*d_r], W_DKV [d_model][d_c], W_KR
+    [d_model][d_r] (bf16 or f32, device) -> packed bf16 weights for
+    MLACache.ProjectAppend (rlx_pack_mla_proj)."""
+    d_model = w_q.shape[0]
+    n = num_heads * (head_dim + w_kr.shape[1]) + w_dkv.shape[1] + w_kr.shape[1]
+    out = torch.empty((n, d_model), dtype=torch.bfloat16, device=w_q.device)
+    check(_lib.load().rlx_pack_mla_proj(_dev(w_q, "w_q"), _dev(w_qr, "w_qr"), _dev(w_dkv, "w_dkv"),
+                                        _dev(w_kr, "w_kr"), _dtype_code(w_q), d_model, num_heads,
+                                        head_dim, _dev(out, "out")))
+    return out
 
 
 def default_scale(head_dim, d_r=0):

@@ -149,3 +149,57 @@ def test_cfg1_generate_with_fused_step(gpu):
     print(f"cfg1 fused logits max {d.max():.3e} mean {d.mean():.3e}")
     assert d.max() < 2e-2 and d.mean() < 2e-3
     assert m.cache.TotalLen(0) == len(toks) - 1
+
+
+@pytest.mark.parametrize("d_model,H,D,lens,ntok,mode", [
+    (256, 4, 128, [0, 70], [5, 2], "offset"),
+    (512, 16, 128, [9], [66], "offset"),     # > 64 rows: two launches
+    (128, 2, 64, [3, 0], [3, 4], "ref"),
+])
+def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode):
+    """mla.go:279-314: q_c = x.W_Q, q_r = RoPE(x.W_QR), c = x.W_DKV,
+    k^R = RoPE(x.W_KR) appended as latent rows."""
+    from relux_amd import MLACache, pack_mla_proj, rope_tables
+    rng = np.random.default_rng(7 + d_model + H)
+    S, dC, dR = len(lens), 512, 64
+    max_seq = 256
+    c = MLACache(num_layers=1, max_len=max_seq, max_seqs=S, device=gpu.index)
+    mats = [oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, w)).astype(np.float32))
+            for w in (H * D, H * dR, dC, dR)]
+    wp = pack_mla_proj(*[_bf16_tensor(m, gpu) for m in mats], H, D)
+    rope = rope_tables(dR, 10000.0, max_seq, gpu)
+    tables = oracle.rope_tables(dR, 10000.0, max_seq)
+    for i, L in enumerate(lens):
+        if L:
+            cc = torch.from_numpy(rng.standard_normal((L, dC), dtype=np.float32)).to(gpu)
+            kr = torch.from_numpy(rng.standard_normal((L, dR), dtype=np.float32)).to(gpu)
+            c.Append(0, cc, kr, seq_ids=[i], n_tok=[L])
+    R = sum(ntok)
+    x = rng.standard_normal((R, d_model), dtype=np.float32)
+    qn, qr = c.ProjectAppend(0, torch.from_numpy(x).to(gpu), wp, H, D, rope=rope,
+                             seq_ids=list(range(S)), n_tok=ntok, rope_mode=mode)
+    qn, qr = qn.cpu().numpy(), qr.cpu().numpy()
+    pos = []
+    for L, n in zip(lens, ntok):
+        pos += [L + j for j in range(n)] if mode == "offset" else [L if L > 0 else j for j in range(n)]
+    xr = oracle.round_bf16(x)
+    qc_o = oracle.matmul_bf16w(xr, mats[0]).reshape(R, H, D)
+    qr_o = oracle.matmul_bf16w(xr, mats[1]).reshape(R, H, dR)
+    c_o = oracle.matmul_bf16w(xr, mats[2])
+    kr_o = oracle.matmul_bf16w(xr, mats[3])
+    for r in range(R):
+        qr_o[r] = oracle.rope_apply(qr_o[r][:, None, :], pos[r], tables, max_seq)[:, 0, :]
+        kr_o[r] = oracle.rope_apply(kr_o[r][None, None, :], pos[r], tables, max_seq)[0, 0, :]
+    np.testing.assert_allclose(qn, qc_o, atol=2e-4, rtol=1e-4)
+    np.testing.assert_allclose(qr, qr_o, atol=2e-4, rtol=1e-4)
+    off = 0
+    for i, (L, n) in enumerate(zip(lens, ntok)):
+        cg, krg = c.View(0, i)
+        cg = cg[0].view(torch.int16).cpu().numpy().view(np.uint16)[L:]
+        krg = krg[0].view(torch.int16).cpu().numpy().view(np.uint16)[L:]
+        for got, want in ((cg, oracle.bf16_from_f32(c_o[off:off + n])),
+                          (krg, oracle.bf16_from_f32(kr_o[off:off + n]))):
+            assert (got == want).mean() > 0.99
+            np.testing.assert_allclose(oracle.f32_from_bf16(got), oracle.f32_from_bf16(want),
+                                       atol=1e-2, rtol=1e-2)
+        off += n
