@@ -47,8 +47,8 @@ __device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src
     }
 }
 
-// GQA append.  Thread = (token, kv head, 8-dim chunk).  K goes to a row page
-// with one 16-byte store; V goes to a dim-major page (8 strided 2-byte
+// GQA append.  Thread = (token, kv head, 8-dim chunk).  K goes to its page
+// (k_page_off layout) with one 16-byte store; V goes to a dim-major page (8 strided 2-byte
 // stores).  The first n_patch threads also apply the table patches; the
 // scatter itself takes its destinations from the plan, not the table.
 template <bool ARG>
@@ -80,7 +80,7 @@ __global__ void kv_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__rest
     uint16_t kv[8], vv[8];
     load8_bf16(k_src, src_off, src_bf16, kv);
     load8_bf16(v_src, src_off, src_bf16, vv);
-    uint16_t *kd = kpool + (((int64_t)tk.page * kvh + h) * P + tk.slot) * hd + d0;
+    uint16_t *kd = kpool + ((int64_t)tk.page * kvh + h) * P * hd + k_page_off(tk.slot, d0, hd);
     u32x4 pk;
 #pragma unroll
     for (int i = 0; i < 4; i++) pk[i] = (uint32_t)kv[2 * i] | ((uint32_t)kv[2 * i + 1] << 16);
@@ -177,7 +177,7 @@ __global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
         const int d0 = (rem - h * chunks) * 8;
         const int page = table[R.tab + t / P];
         const int slot = t % P;
-        u32x4 v = *(const u32x4 *)(kpool + (((int64_t)page * kvh + h) * P + slot) * hd + d0);
+        u32x4 v = *(const u32x4 *)(kpool + ((int64_t)page * kvh + h) * P * hd + k_page_off(slot, d0, hd));
         *(u32x4 *)(k_out + base + ((int64_t)h * R.len + t) * hd + d0) = v;
     }
     const int tchunks = (R.len + 7) >> 3;

@@ -39,6 +39,19 @@ constexpr int kMlaDc = 512;
 constexpr int kMlaDr = 64;
 constexpr int kMlaRow = kMlaDc + kMlaDr;  // 576 bf16 = 1152 B per token
 
+// Element offset of (slot s, dim d) inside one kv head's K page.  Each
+// 16-token block of the page is stored k-step-major: D/32 slabs of
+// [16 tokens][32 dims] (head_dim <= 32: plain [16 tokens][D] rows).  A
+// decode wave's MFMA A operand for one 32-wide k-step (16 rows x 64 B) is
+// then 1 KB of contiguous memory per load instruction instead of 16
+// half-lines, which is what lets the K stream reach the same HBM rate as
+// the V stream.  Blocks start where row-major blocks would (block b at
+// 16 * b * D), so page and block addressing are unchanged.
+__host__ __device__ __forceinline__ int64_t k_page_off(int s, int d, int D) {
+    if (D <= 32) return (int64_t)s * D + d;
+    return ((int64_t)(s >> 4) * (D >> 5) + (d >> 5)) * 512 + (s & 15) * 32 + (d & 31);
+}
+
 // One table write: table[idx] = val.  Indices in one batch are unique.
 struct Patch {
     int32_t idx;
@@ -310,7 +323,6 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        int P);
 
 // Work-groups of the decode kernels one CU holds at once (occupancy).
-int gqa_decode_wgs_per_cu(int hd, int nqt);
 int mla_decode_wgs_per_cu(int nqt);
 
 hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,

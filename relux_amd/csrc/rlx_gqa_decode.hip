@@ -42,7 +42,7 @@ __device__ __forceinline__ int key_limit(int mask_mode, int len, int nq, int qi)
 }
 
 template <int D, int NQT, bool ARG>
-__global__ __launch_bounds__(256) void gqa_decode_kernel(
+__global__ __launch_bounds__(256, NQT == 1 ? 3 : 2) void gqa_decode_kernel(
     typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ kpool,
     const uint16_t *__restrict__ vpool, const int32_t *__restrict__ table,
     const AttRow *__restrict__ rows, const int2 *__restrict__ work, int n_rows,
@@ -126,34 +126,52 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
     }
 
     const int64_t kstride = (int64_t)P * D;  // one kv head of one page
-    for (int t0 = t_begin + 16 * wave; t0 < t_end; t0 += 64) {
-        // The cache is streamed once: non-temporal loads keep it from
-        // displacing reusable lines (measured ~12% more read bandwidth).
-        const int page = table[R.tab + t0 / P];
+    // Wave w walks blocks t0 = tw0 + 64 j (j < nb) of 16 tokens.  Block
+    // indices are wave-uniform (scalar), and the page ids of 64 blocks are
+    // fetched at once, one per lane, and read back with readlane: no table
+    // load sits between one block's K/V loads and the next's.
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int tw0 = t_begin + 16 * wv;
+    const int nb = (t_end > tw0) ? (t_end - tw0 + 63) / 64 : 0;
+    // K blocks are k-step-major (k_page_off): k-step ks of row col sits at
+    // ks * 512 + col * 32; head_dim 16 keeps plain rows.
+    const int64_t k_lane = K16 ? (int64_t)col * D + grp * KW : (int64_t)col * 32 + grp * 8;
+    const int64_t v_lane = (int64_t)col * P + grp * 4;
+    auto fetch_pages = [&](int j0) {
+        const int j = j0 + lane;
+        return (j < nb) ? table[R.tab + (tw0 + 64 * j) / P] : 0;
+    };
+    // The cache is streamed once: non-temporal loads keep it from
+    // displacing reusable lines (measured ~12% more read bandwidth).
+    auto load_block = [&](int j, int pg, u32x4(&kr)[KS], u32x2(&vr)[MT]) {
+        const int t0 = tw0 + 64 * j;
+        const int page = __builtin_amdgcn_readlane(pg, j & 63);
         const int slot0 = t0 % P;
-        const uint16_t *kp = kpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)(slot0 + col) * D + grp * KW;
-        const uint16_t *vp = vpool + ((int64_t)page * KVH + kvh) * kstride + (int64_t)col * P + slot0 + grp * 4;
-        u32x4 kr[KS];
-        u32x2 vr[MT];
+        const int64_t pbase = ((int64_t)page * KVH + kvh) * kstride;
+        const uint16_t *kp = kpool + pbase + (int64_t)slot0 * D + k_lane;
+        const uint16_t *vp = vpool + pbase + slot0 + v_lane;
         if constexpr (K16) {
             const u32x2 k2 = __builtin_nontemporal_load((const u32x2 *)kp);
             kr[0] = u32x4{k2[0], k2[1], 0, 0};
         } else {
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) kr[ks] = __builtin_nontemporal_load((const u32x4 *)(kp + ks * 32));
+            for (int ks = 0; ks < KS; ks++) kr[ks] = __builtin_nontemporal_load((const u32x4 *)(kp + ks * 512));
         }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) vr[mt] = __builtin_nontemporal_load((const u32x2 *)(vp + (int64_t)mt * 16 * P));
+    };
 
+    auto consume = [&](int j, u32x4(&kr)[KS], u32x2(&vr)[MT]) {
+        const int t0 = tw0 + 64 * j;
         // Tokens past the live length sit in the tail page's unused slots:
         // their V must contribute exact zeros whatever bytes they hold.
         if (t0 + 16 > R.len) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (t0 + grp * 4 + j >= R.len) {
-                    const uint32_t keep = (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+            for (int jj = 0; jj < 4; jj++) {
+                if (t0 + grp * 4 + jj >= R.len) {
+                    const uint32_t keep = (jj & 1) ? 0x0000FFFFu : 0xFFFF0000u;
 #pragma unroll
-                    for (int mt = 0; mt < MT; mt++) vr[mt][j >> 1] &= keep;
+                    for (int mt = 0; mt < MT; mt++) vr[mt][jj >> 1] &= keep;
                 }
             }
         }
@@ -205,6 +223,39 @@ __global__ __launch_bounds__(256) void gqa_decode_kernel(
             for (int mt = 0; mt < MT; mt++)
                 acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(sh4, vr[mt]), pb, acc[nt][mt], 0, 0, 0);
         }
+    };
+
+    // Two register sets, A and B, alternate without copies so that the next
+    // block's loads are always in flight while one block is consumed; the
+    // loop is peeled so that every load it issues is unconditional (the
+    // waits then count exactly one block of loads still outstanding).
+    int pg = fetch_pages(0);
+    asm volatile("" ::"v"(pg));
+    auto load_next = [&](int j, u32x4(&kr)[KS], u32x2(&vr)[MT]) {
+        if ((j & 63) == 0) {
+            // Once per 64 blocks: wait for the new ids here, inside the
+            // branch, so that no wait for them sits on the common path.
+            pg = fetch_pages(j);
+            asm volatile("" ::"v"(pg));
+        }
+        load_block(j, pg, kr, vr);
+    };
+    u32x4 ka[KS], kb[KS];
+    u32x2 va[MT], vb[MT];
+    if (nb > 0) load_block(0, pg, ka, va);
+    int j = 0;
+    for (; j + 2 < nb; j += 2) {
+        load_next(j + 1, kb, vb);
+        consume(j, ka, va);
+        load_next(j + 2, ka, va);
+        consume(j + 1, kb, vb);
+    }
+    if (j + 1 < nb) {
+        load_next(j + 1, kb, vb);
+        consume(j, ka, va);
+        consume(j + 1, kb, vb);
+    } else if (j < nb) {
+        consume(j, ka, va);
     }
 
     // ---- merge the 4 waves of the work-group -------------------------------
@@ -337,20 +388,6 @@ hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     RLX_GQA_CASE(16, 2)
 #undef RLX_GQA_CASE
     return hipErrorInvalidValue;
-}
-
-int gqa_decode_wgs_per_cu(int hd, int nqt) {
-    int n = 0;
-    hipError_t e = hipErrorInvalidValue;
-    if (hd == 128 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 1, true>, 256, 0);
-    if (hd == 128 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<128, 2, true>, 256, 0);
-    if (hd == 64 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 1, true>, 256, 0);
-    if (hd == 64 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<64, 2, true>, 256, 0);
-    if (hd == 32 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 1, true>, 256, 0);
-    if (hd == 32 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<32, 2, true>, 256, 0);
-    if (hd == 16 && nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 1, true>, 256, 0);
-    if (hd == 16 && nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gqa_decode_kernel<16, 2, true>, 256, 0);
-    return (e == hipSuccess && n > 0) ? n : 1;
 }
 
 }  // namespace rlx

@@ -37,59 +37,85 @@ __device__ __forceinline__ int mla_key_limit(int mask_mode, int len, int nq, int
     return len - 1;
 }
 
+// Split an f32 into a bf16 pair with hi + lo = x to ~16 more bits than hi
+// alone (x - hi is exact in f32; non-finite x keeps lo = 0).  MFMA products
+// of bf16 operands are exact in f32, so W.hi + W.lo accumulated in f32
+// follows the f32 product sum closely.
+__device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) {
+    hi = bf16_rne(x);
+    const float h = bf16_f32(hi);
+    lo = (fabsf(h) < INFINITY) ? bf16_rne(x - h) : (uint16_t)0;
+}
+
 // q_lat[row][h][c] = bf16(qscale * sum_d q_nope[row][h][d] * W_UK[c][h*D+d])
 // for c < 512 and q_lat[row][h][512+r] = bf16(qscale * q_rope[row][h][r]).
-// Block = (head, 8 query rows, 64 latent channels).  Four adjacent lanes share
-// a channel and split its D weights (16-byte loads, 4 lanes cover the head's
-// whole W_UK row segment); their partial dots meet by two lane swaps.
+// Block = (head, 64 latent channels, 16 query rows); wave w computes
+// C[16 channels][16 rows] = W_UK_h[c0+16w .., :] . q^T with MFMA 16x16x32
+// over the head's D dims: A = 8 consecutive W_UK dims of one channel per
+// lane, B = 8 consecutive query dims of one row per lane (f32 queries as
+// hi + lo bf16 pairs).  Every load is issued before the first product, so
+// the kernel costs one memory round trip.
+template <int D>
 __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
                                                          const void *__restrict__ q_rope,
                                                          int q_bf16,
                                                          const uint16_t *__restrict__ w_uk,
-                                                         int H, int D, int total_q, float qscale,
+                                                         int H, int total_q, float qscale,
                                                          uint16_t *__restrict__ qlat) {
-    const int h = blockIdx.x, r0 = blockIdx.y * 8;
-    __shared__ float qn[8][256];
-    for (int i = threadIdx.x; i < 8 * D; i += blockDim.x) {
-        const int r = i / D, d = i - r * D;
-        const int64_t off = ((int64_t)(r0 + r) * H + h) * D + d;
-        float x = 0.f;
-        if (r0 + r < total_q)
-            x = q_bf16 ? bf16_f32(((const uint16_t *)q_nope)[off]) : ((const float *)q_nope)[off];
-        qn[r][d] = x;
-    }
-    __syncthreads();
-    const int c = blockIdx.z * 64 + (threadIdx.x >> 2);
-    const int g = threadIdx.x & 3;
-    const int dq = D / 4;  // dims per lane: 16..64, a multiple of 8
-    const uint16_t *w = w_uk + (int64_t)c * H * D + (int64_t)h * D + g * dq;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int d = 0; d < dq; d += 8) {
-        const u32x4 v = *(const u32x4 *)(w + d);
-        float wv[8];
+    constexpr int KS = D / 32;
+    const int h = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int c0 = blockIdx.y * 64 + wave * 16;
+    const int r0 = blockIdx.z * 16;
+    const int row = min(r0 + col, total_q - 1);  // rows past the end load the last row
+    const uint16_t *wa = w_uk + (int64_t)(c0 + col) * H * D + (int64_t)h * D + grp * 8;
+    u32x4 a[KS], bh[KS], bl[KS];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            wv[2 * i] = bf16_f32((uint16_t)(v[i] & 0xFFFFu));
-            wv[2 * i + 1] = bf16_f32((uint16_t)(v[i] >> 16));
+    for (int ks = 0; ks < KS; ks++) a[ks] = *(const u32x4 *)(wa + ks * 32);
+    const int64_t qoff = ((int64_t)row * H + h) * D + grp * 8;
+    if (q_bf16) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) {
+            bh[ks] = *(const u32x4 *)((const uint16_t *)q_nope + qoff + ks * 32);
+            bl[ks] = u32x4{0, 0, 0, 0};
         }
+    } else {
 #pragma unroll
-        for (int r = 0; r < 8; r++)
+        for (int ks = 0; ks < KS; ks++) {
+            const float *qf = (const float *)q_nope + qoff + ks * 32;
+            const float4 f0 = *(const float4 *)qf, f1 = *(const float4 *)(qf + 4);
+            const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 #pragma unroll
-            for (int j = 0; j < 8; j++) acc[r] += qn[r][g * dq + d + j] * wv[j];
+            for (int i = 0; i < 4; i++) {
+                uint16_t h0, l0, h1, l1;
+                split_bf16(v[2 * i], h0, l0);
+                split_bf16(v[2 * i + 1], h1, l1);
+                bh[ks][i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                bl[ks][i] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            }
+        }
     }
+    fl4 acc = fl4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-        acc[r] += __shfl_xor(acc[r], 1);
-        acc[r] += __shfl_xor(acc[r], 2);
-    }
-    if (g == 0) {
+    for (int ks = 0; ks < KS; ks++)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[ks]),
+                                                      __builtin_bit_cast(bf16x8, bh[ks]), acc, 0, 0, 0);
+    if (!q_bf16) {
 #pragma unroll
-        for (int r = 0; r < 8; r++)
-            if (r0 + r < total_q)
-                qlat[((int64_t)(r0 + r) * H + h) * kMlaRow + c] = bf16_rne(acc[r] * qscale);
+        for (int ks = 0; ks < KS; ks++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[ks]),
+                                                          __builtin_bit_cast(bf16x8, bl[ks]), acc, 0, 0, 0);
     }
-    if (blockIdx.z == 0) {
-        for (int i = threadIdx.x; i < 8 * kMlaDr; i += blockDim.x) {
+    // C[4 grp + i][col]: channels c0 + 4 grp + i of row r0 + col.
+    if (r0 + col < total_q) {
+        u32x2 o;
+        o[0] = (uint32_t)bf16_rne(acc[0] * qscale) | ((uint32_t)bf16_rne(acc[1] * qscale) << 16);
+        o[1] = (uint32_t)bf16_rne(acc[2] * qscale) | ((uint32_t)bf16_rne(acc[3] * qscale) << 16);
+        *(u32x2 *)(qlat + ((int64_t)(r0 + col) * H + h) * kMlaRow + c0 + 4 * grp) = o;
+    }
+    if (blockIdx.y == 0) {
+        for (int i = threadIdx.x; i < 16 * kMlaDr; i += blockDim.x) {
             const int r = i / kMlaDr, k = i - r * kMlaDr;
             if (r0 + r >= total_q) continue;
             const int64_t off = ((int64_t)(r0 + r) * H + h) * kMlaDr + k;
@@ -311,13 +337,15 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
 
 // Merge the splits of one (sequence, query, head) into the normalised latent
 // output o_lat[row][h][0:512] (f32 workspace).  One 256-thread block per
-// query row: wave 0 computes the merge weights in LDS, then every thread
-// streams two latent channels across the splits.
+// query row; each thread owns channels t and t + 256 and loads them from up
+// to 16 splits at once (issued before the merge weights are read, so the two
+// round trips overlap); wave 0 computes the merge weights in LDS.
 template <bool ARG>
 __global__ __launch_bounds__(256) void mla_combine_kernel(
     typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
     const float *__restrict__ part_o, const float *__restrict__ part_ml, int H, int QRP,
     float *__restrict__ olat) {
+    constexpr int SB = 16;  // splits per batch of loads
     const AttRow R = plan_row<ARG>(rows, blockIdx.x);
     const int qi = blockIdx.y / H;
     const int h = blockIdx.y - qi * H;
@@ -326,60 +354,111 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(
     __shared__ float fac[kMaxSplits];
     __shared__ float inv_l;
     const int64_t b0 = (int64_t)R.part * QRP + qr;
+    const int c = threadIdx.x;
+    const float *src = part_o + b0 * kMlaDc + c;
+    const int64_t sstride = (int64_t)QRP * kMlaDc;
+    float v0[SB], v1[SB];
+#pragma unroll
+    for (int i = 0; i < SB; i++) {
+        const int64_t o = (int64_t)min(i, R.nsplit - 1) * sstride;
+        v0[i] = src[o];
+        v1[i] = src[o + 256];
+    }
     merge_weights(part_ml + b0 * 2, QRP, R.nsplit, fac, &inv_l);
     __syncthreads();
-    float *dst = olat + ((int64_t)(R.qrow + qi) * H + h) * kMlaDc;
-    for (int c = threadIdx.x; c < kMlaDc; c += blockDim.x) {
-        float o = 0.f;
-        for (int s = 0; s < R.nsplit; s++) o += fac[s] * part_o[(b0 + (int64_t)s * QRP) * kMlaDc + c];
-        dst[c] = o * inv_l;
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < SB; i++) {
+        if (i < R.nsplit) {
+            o0 += fac[i] * v0[i];
+            o1 += fac[i] * v1[i];
+        }
     }
+    for (int s0 = SB; s0 < R.nsplit; s0 += SB) {
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            const int64_t o = (int64_t)min(s0 + i, R.nsplit - 1) * sstride;
+            v0[i] = src[o];
+            v1[i] = src[o + 256];
+        }
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            if (s0 + i < R.nsplit) {
+                o0 += fac[s0 + i] * v0[i];
+                o1 += fac[s0 + i] * v1[i];
+            }
+        }
+    }
+    float *dst = olat + ((int64_t)(R.qrow + qi) * H + h) * kMlaDc;
+    dst[c] = o0 * inv_l;
+    dst[c + 256] = o1 * inv_l;
 }
 
 // out[row][h][d] = sum_c o_lat[row][h][c] * W_UV[c][h*D + d].  Block = (head,
-// 8 query rows, 32 output dims); thread = (dim, group of 64 channels), so each
-// W_UV element is loaded once per 8 rows, coalesced over the 32 dims.  The 8
-// channel-group partials meet in LDS and are added in a fixed order.
+// 16 output dims, 16 query rows); wave w takes latent channels
+// [128w, 128w + 128) of the C[16 dims][16 rows] tile (MFMA 16x16x16) and the
+// four partial tiles are summed in LDS.  A = 4 consecutive channels of one
+// dim per lane, from the block's W_UV slice [512 c][16 d] staged in LDS and
+// read with the LDS transpose read; B = 4 consecutive channels of one o_lat
+// row per lane straight from memory (f32, entered as hi + lo bf16).  All
+// global loads are issued before the first product.
 __global__ __launch_bounds__(256) void mla_proj_kernel(const float *__restrict__ olat,
                                                        const uint16_t *__restrict__ w_uv,
                                                        int H, int D, int total_q,
                                                        void *__restrict__ out, int out_bf16) {
+    constexpr int KB = kMlaDc / 16 / 4;  // k-steps per wave
+    __shared__ __attribute__((aligned(16))) uint16_t wt[kMlaDc * 16];
+    __shared__ fl4 red[3][64];
     const int h = blockIdx.x;
-    const int r0 = blockIdx.y * 8;
-    const int d = blockIdx.z * 32 + (threadIdx.x & 31);
-    const int cg = threadIdx.x >> 5;  // channels [64cg, 64cg+64)
-    __shared__ float tile[8][kMlaDc];
-    __shared__ float red[8][8][32];
-    for (int i = threadIdx.x; i < 8 * kMlaDc; i += blockDim.x) {
-        const int r = i / kMlaDc, c = i - r * kMlaDc;
-        tile[r][c] = (r0 + r < total_q) ? olat[((int64_t)(r0 + r) * H + h) * kMlaDc + c] : 0.f;
-    }
+    const int d0 = blockIdx.y * 16;
+    const int r0 = blockIdx.z * 16;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    u32x4 w[4];
+    const uint16_t *ws = w_uv + (int64_t)h * D + d0 + (t & 1) * 8;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = *(const u32x4 *)(ws + (int64_t)((t >> 1) + 128 * i) * H * D);
+    const int row = min(r0 + col, total_q - 1);
+    const float *ob = olat + ((int64_t)row * H + h) * kMlaDc + wave * 128 + grp * 4;
+    float4 f[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) f[kb] = *(const float4 *)(ob + kb * 16);
+#pragma unroll
+    for (int i = 0; i < 4; i++) *(u32x4 *)(wt + ((t >> 1) + 128 * i) * 16 + (t & 1) * 8) = w[i];
     __syncthreads();
-    const int64_t wpitch = (int64_t)H * D;
-    const uint16_t *w = w_uv + (int64_t)(cg * 64) * wpitch + (int64_t)h * D + d;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 16
-    for (int k = 0; k < 64; k++) {
-        const float wv = bf16_f32(w[(int64_t)k * wpitch]);
+    // Transpose read: lane (grp, col) fetches 4 dims of channel row
+    // 4 grp + col / 4 and receives dim col of channels 4 grp .. 4 grp + 3.
+    const uint16_t *tr = wt + (wave * 128 + 4 * grp + (col >> 2)) * 16 + (col & 3) * 4;
+    fl4 acc = fl4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 8; r++) acc[r] += tile[r][cg * 64 + k] * wv;
+    for (int kb = 0; kb < KB; kb++) {
+        const sh4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) sh4 *)(tr + kb * 16 * 16));
+        uint16_t hx, lx, hy, ly, hz, lz, hw, lw;
+        split_bf16(f[kb].x, hx, lx);
+        split_bf16(f[kb].y, hy, ly);
+        split_bf16(f[kb].z, hz, lz);
+        split_bf16(f[kb].w, hw, lw);
+        const u32x2 bh = u32x2{(uint32_t)hx | ((uint32_t)hy << 16), (uint32_t)hz | ((uint32_t)hw << 16)};
+        const u32x2 bl = u32x2{(uint32_t)lx | ((uint32_t)ly << 16), (uint32_t)lz | ((uint32_t)lw << 16)};
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(sh4, bh), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(sh4, bl), acc, 0, 0, 0);
     }
-#pragma unroll
-    for (int r = 0; r < 8; r++) red[cg][r][threadIdx.x & 31] = acc[r];
+    if (wave > 0) red[wave - 1][lane] = acc;
     __syncthreads();
-    if (threadIdx.x < 32 * 8) {
-        const int r = threadIdx.x >> 5;  // row handled in the final sum
-        const int dl = threadIdx.x & 31;
-        const int row = r0 + r;
-        if (row < total_q) {
-            float v = 0.f;
-#pragma unroll
-            for (int g = 0; g < 8; g++) v += red[g][r][dl];
-            const int64_t o = ((int64_t)row * H + h) * D + blockIdx.z * 32 + dl;
-            if (out_bf16)
-                ((uint16_t *)out)[o] = bf16_rne(v);
-            else
-                ((float *)out)[o] = v;
+    if (wave > 0) return;
+    acc = ((acc + red[0][lane]) + red[1][lane]) + red[2][lane];
+    // C[4 grp + i][col]: dims d0 + 4 grp + i of row r0 + col.
+    if (r0 + col < total_q) {
+        const int64_t o = ((int64_t)(r0 + col) * H + h) * D + d0 + 4 * grp;
+        if (out_bf16) {
+            u32x2 o2;
+            o2[0] = (uint32_t)bf16_rne(acc[0]) | ((uint32_t)bf16_rne(acc[1]) << 16);
+            o2[1] = (uint32_t)bf16_rne(acc[2]) | ((uint32_t)bf16_rne(acc[3]) << 16);
+            *(u32x2 *)((uint16_t *)out + o) = o2;
+        } else {
+            *(fl4 *)((float *)out + o) = acc;
         }
     }
 }
@@ -404,8 +483,13 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
     if (hd > 256 || hd % 64 != 0) return hipErrorInvalidValue;
-    mla_absorb_kernel<<<dim3(H, (total_q + 7) / 8, kMlaDc / 64), 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H,
-                                                                  hd, total_q, qscale, qlat);
+    const dim3 ag(H, kMlaDc / 64, (total_q + 15) / 16);
+    switch (hd) {
+        case 64: mla_absorb_kernel<64><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
+        case 128: mla_absorb_kernel<128><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
+        case 192: mla_absorb_kernel<192><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
+        default: mla_absorb_kernel<256><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev0) (void)hipEventRecord(ev0, s);
@@ -433,8 +517,8 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
             NoPlan{0}, rows, part_o, part_ml, H, 16 * nqt, olat);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    mla_proj_kernel<<<dim3(H, (total_q + 7) / 8, hd / 32), 256, 0, s>>>(olat, w_uv, H, hd,
-                                                                        total_q, out, out_bf16);
+    mla_proj_kernel<<<dim3(H, hd / 16, (total_q + 15) / 16), 256, 0, s>>>(olat, w_uv, H, hd,
+                                                                         total_q, out, out_bf16);
     return hipGetLastError();
 }
 

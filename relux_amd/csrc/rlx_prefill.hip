@@ -115,7 +115,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         k_lc[i] = (p - k_row[i] * KCH) ^ pf_kswz(k_row[i]);
         const int r16 = k_row[i] & 15;
         if (SRC == kSrcPaged)
-            k_off[i] = (int64_t)r16 * DQK + k_lc[i] * 8;
+            k_off[i] = k_page_off(r16, k_lc[i] * 8, DQK);
         else if (k_lc[i] < 16)
             k_off[i] = (int64_t)k_row[i] * 128 + k_lc[i] * 8;
         else
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             const int pg = (t - k0 < 16) ? pg0 : pg1;
             const uint16_t *g;
             if (SRC == kSrcPaged)
-                g = a.kpool + (((int64_t)pg * a.KVH + hg) * a.P + (t % a.P)) * DQK + lc * 8;
+                g = a.kpool + ((int64_t)pg * a.KVH + hg) * a.P * DQK + k_page_off(t % a.P, lc * 8, DQK);
             else if (lc < 16)
                 g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
             else

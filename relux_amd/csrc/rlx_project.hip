@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
             const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
             if constexpr (MODEL == kProjGQA) {
                 if (part == 1)
-                    kpool[(((int64_t)tk.page * KVH + head) * P + tk.slot) * D + d] = bf16_rne(v);
+                    kpool[((int64_t)tk.page * KVH + head) * P * D + k_page_off(tk.slot, d, D)] = bf16_rne(v);
                 else
                     vpool[(((int64_t)tk.page * KVH + head) * D + d) * P + tk.slot] = bf16_rne(v);
             } else {

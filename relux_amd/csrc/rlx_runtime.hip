@@ -1019,7 +1019,11 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         const int tiles = qtile ? (nq + qtile - 1) / qtile : 1;
         for (int t = 0; t < tiles; t++) units_lens.push_back(lens[i]);
     }
-    const int chunk = choose_chunk(units_lens, c->kvh, (int64_t)c->cus * gqa_decode_wgs_per_cu(c->hd, nqt));
+    // One residency slot per CU: a GQA decode work-group keeps two 16-token
+    // blocks per wave in flight, and a sweep of 1, 2 and 3 work-groups per
+    // CU (8k and mixed-length contexts) found one per CU, with longer splits,
+    // as fast or faster (fewer work-group start-ups and partials).
+    const int chunk = choose_chunk(units_lens, c->kvh, (int64_t)c->cus);
     std::vector<AttRow> rows;
     std::vector<int2> work;
     int total_q = 0, mnq = 0, parts = 0;
