@@ -259,6 +259,54 @@ int32_t rlx_compact(void *cache, int32_t layer);
 /* Free every page of one sequence (layer -1: every layer). */
 int32_t rlx_seq_release(void *cache, int32_t layer, int32_t seq);
 
+/* ---- token selection on the device (synchronising) -------------------- */
+/* Sampler fields (sampler.go:33-43) except Rand: every rng.Float32() draw
+ * is passed in.  NewSampler's defaults are temperature 1, top_p 1, the
+ * rest 0.  Clamps as the reference: temperature <= 0 -> 1e-5, top_k < 0 or
+ * >= vocab -> off, top_p outside (0, 1) -> off. */
+typedef struct {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    float repeat_penalty;
+    float frequency_penalty;
+    float presence_penalty;
+    int32_t repeat_window;
+} rlx_sampler_t;
+
+/* The calls below run on `cache`'s stream (any GQA or MLA handle) and copy
+ * their small results to host memory before returning.  logits are DEVICE
+ * f32 rows (row_stride elements apart); every other array is host memory. */
+
+/* Sampler.Greedy (sampler.go:56-68) per row: first index of the maximum. */
+int32_t rlx_greedy(void *cache, const float *logits, int32_t n_rows, int32_t vocab,
+                   int64_t row_stride, int32_t *out_tokens);
+/* Sampler.Sample (sampler.go:73-210) per row: penalties over the row's
+ * previous tokens prev_tokens[prev_offsets[r] .. prev_offsets[r+1]) (both
+ * may be NULL: no penalties; with penalties, vocab <= 262144 and at most
+ * 4096 distinct tokens per window), temperature, top-k, fastexp32 softmax,
+ * top-p, min-p, then the draw uniforms[r].  Sums are block-parallel, so a
+ * draw within a few ulp of a cumulative boundary may land one token over;
+ * top-p keeps every token tied with the cutoff probability. */
+int32_t rlx_sample(void *cache, const float *logits, int32_t n_rows, int32_t vocab,
+                   int64_t row_stride, const rlx_sampler_t *params, const int32_t *prev_tokens,
+                   const int32_t *prev_offsets, const float *uniforms, int32_t *out_tokens);
+/* SpeculativeDecoder.acceptPhase + resampleRejected (speculative.go:203-290)
+ * for n_rows sequences at once.  draft_logits [n_rows][max_k][vocab] and
+ * target_logits [n_rows][max_k+1][vocab] (device f32; target row i scores
+ * draft i, row n_draft the token after the last draft); draft_tokens
+ * [n_rows][max_k], n_draft [n_rows] (<= max_k); uniforms [n_rows][max_k+1],
+ * consumed in the reference's order: one acceptance test per draft up to
+ * the first rejection, then one draw for the resample (or, all accepted,
+ * for Sample over the next target row with `params`, no penalties).
+ * Outputs per row: accepted drafts and the next token.  The caller then
+ * rolls its caches back (rlx_rollback) to the committed prefix. */
+int32_t rlx_spec_accept(void *cache, const float *draft_logits, const float *target_logits,
+                        const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
+                        int32_t max_k, int32_t vocab, const float *uniforms,
+                        const rlx_sampler_t *params, int32_t *n_accepted, int32_t *next_token);
+
 /* ---- state queries (synchronising) ------------------------------------ */
 /* Live token count; replaces TotalLen (kvcache.go:383-388). */
 int32_t rlx_seq_len(void *cache, int32_t layer, int32_t seq, int32_t *len_out);

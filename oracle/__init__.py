@@ -20,6 +20,11 @@ Parity status per function (what pins it; see tests/test_oracle.py):
   gqa_attend / mla_attend        pinned: independent f64 exact-softmax numpy
                                  attention within the fastexp32 band; MLA
                                  decompress-all == absorbed form.
+  greedy / sample / spec_accept  pinned: sampler_test.go cases, r-sweep
+                                 frequencies against each stage's stated
+                                 distribution, hand-computed penalties,
+                                 acceptance / resample distributions
+                                 (oracle/sampling.py, tests/test_sampling.py).
   paged model                    pinned: invariants (append(a||b);
                                  rollback(|b|) == append(a); gather after
                                  compact == before; eviction == dense
@@ -37,6 +42,7 @@ _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
 _i = ctypes.c_int
 _i64 = ctypes.c_int64
 
@@ -70,6 +76,11 @@ def lib():
             "orc_rmsnorm": ([_f32p, _u16p, ctypes.c_float, _i, _i, _f32p], None),
             "orc_gelu_n": ([_f32p, _f32p, _i64], None),
             "orc_add_bias": ([_f32p, _u16p, _i, _i], None),
+            "orc_greedy": ([_f32p, _i], _i),
+            "orc_sample": ([_f32p, _i, _f32p, _i32p, ctypes.c_void_p, _i, ctypes.c_float,
+                            ctypes.c_void_p], _i),
+            "orc_spec_accept": ([_f32p, _f32p, _i32p, _i, _i, _f32p, _f32p, _i32p,
+                                 ctypes.POINTER(ctypes.c_int)], _i),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)

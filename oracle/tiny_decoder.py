@@ -126,9 +126,22 @@ class LogicalCache:
     def attend(self, layer, q):
         return gqa_attend(q, self.k[layer], self.v[layer], mask="causal")
 
+    def rollback(self, layer, n):
+        """Drop the newest n tokens (the device cache's rlx_rollback)."""
+        if n:
+            T = self.total_len(layer)
+            assert 0 <= n <= T
+            self.k[layer] = self.k[layer][:, :T - n]
+            self.v[layer] = self.v[layer][:, :T - n]
+
 
 class TinyDecoder:
-    def __init__(self, cfg=CFG1, weights=None, seed=0):
+    def __init__(self, cfg=CFG1, weights=None, seed=0, rope_rule="ref"):
+        """rope_rule "ref": RotaryEmbedding.Apply's rule (rope.go:152-153:
+        with startPos > 0 every row of a call takes position startPos, which
+        Generate's one-token steps never trigger); "offset": row j of a call
+        takes position start + j (the positions a chunked verify needs)."""
+        self.rope_rule = rope_rule
         self.cfg = dict(cfg)
         self.W = weights if weights is not None else make_weights(self.cfg, seed)
         self.H, self.KVH = cfg["heads"], cfg["kv_heads"]
@@ -144,13 +157,20 @@ class TinyDecoder:
         k = matmul_bf16w(x, Wl["wk"]).reshape(S, KVH, D).transpose(1, 0, 2)
         v = matmul_bf16w(x, Wl["wv"]).reshape(S, KVH, D).transpose(1, 0, 2)
         start = cache.total_len(layer)
-        q = rope_apply(np.ascontiguousarray(q), start, self.rope, self.cfg["max_seq"])
-        k = rope_apply(np.ascontiguousarray(k), start, self.rope, self.cfg["max_seq"])
+        q = self._rope(np.ascontiguousarray(q), start)
+        k = self._rope(np.ascontiguousarray(k), start)
         v = np.ascontiguousarray(v, np.float32)
         cache.append(layer, k, v)
         o = cache.attend(layer, q)  # [H, S, D]
         o = np.ascontiguousarray(np.asarray(o, np.float32).transpose(1, 0, 2)).reshape(S, H * D)
         return matmul_bf16w(o, Wl["wo"])
+
+    def _rope(self, x, start):
+        """x [heads, S, D] at cache position start."""
+        if self.rope_rule == "ref" or start == 0:
+            return rope_apply(x, start, self.rope, self.cfg["max_seq"])
+        return np.concatenate([rope_apply(np.ascontiguousarray(x[:, j:j + 1]), start + j, self.rope,
+                                          self.cfg["max_seq"]) for j in range(x.shape[1])], axis=1)
 
     def forward(self, ids, cache):
         """Transformer.Forward(ids, 1) with the caches wired in: logits [S, vocab]."""

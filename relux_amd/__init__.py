@@ -3,12 +3,14 @@
 librelux_kv.so (HIP, built in-tree by relux_amd.build) implements paged GQA
 and MLA caches, append, gather, rollback/evict/compact, and decode /
 verify / chunked-prefill attention over the paged cache, and the fused
-Q/K/V projection + RoPE + append step.  `KVCache` and `MLACache` mirror the
+Q/K/V projection + RoPE + append step, and token selection (greedy,
+sampling, speculative acceptance) on logits that stay on the device.  `KVCache` and `MLACache` mirror the
 reference's Go cache types (internal/transformer/kvcache.go, mla_cache.go).
 """
 from ._lib import ReluxError, ReluxPanic, load  # noqa: F401
 
-__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "pack_mla_proj", "rope_tables"]
+__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "pack_mla_proj", "rope_tables",
+           "Sampler", "SpeculativeDecoder", "Draws", "spec_accept"]
 
 
 def __getattr__(name):
@@ -16,4 +18,7 @@ def __getattr__(name):
     if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "pack_mla_proj", "rope_tables"):
         from . import kvcache
         return getattr(kvcache, name)
+    if name in ("Sampler", "SpeculativeDecoder", "Draws", "spec_accept"):
+        from . import sampling
+        return getattr(sampling, name)
     raise AttributeError(name)

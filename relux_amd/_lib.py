@@ -45,6 +45,15 @@ _vp = ctypes.c_void_p
 _pi32 = ctypes.POINTER(ctypes.c_int32)
 _f32 = ctypes.c_float
 
+class SamplerParams(ctypes.Structure):
+    """rlx_sampler_t: Sampler (sampler.go:33-43) without Rand."""
+    _fields_ = [("temperature", _f32), ("top_k", _i32), ("top_p", _f32), ("min_p", _f32),
+                ("repeat_penalty", _f32), ("frequency_penalty", _f32),
+                ("presence_penalty", _f32), ("repeat_window", _i32)]
+
+
+_psp = ctypes.POINTER(SamplerParams)
+
 # name -> argument types; every entry returns int32.  Kept in the order of
 # include/relux_kv.h.
 SIGNATURES = {
@@ -81,6 +90,10 @@ SIGNATURES = {
     "rlx_evict": [_vp, _i32, _i32, _pi32, _pi32],
     "rlx_compact": [_vp, _i32],
     "rlx_seq_release": [_vp, _i32, _i32],
+    "rlx_greedy": [_vp, _vp, _i32, _i32, _i64, _pi32],
+    "rlx_sample": [_vp, _vp, _i32, _i32, _i64, _psp, _pi32, _pi32, ctypes.POINTER(_f32), _pi32],
+    "rlx_spec_accept": [_vp, _vp, _vp, _pi32, _pi32, _i32, _i32, _i32, ctypes.POINTER(_f32), _psp,
+                        _pi32, _pi32],
     "rlx_seq_len": [_vp, _i32, _i32, _pi32],
     "rlx_seq_state": [_vp, _i32, _i32, _pi32],
     "rlx_page_table": [_vp, _i32, _i32, _pi32],

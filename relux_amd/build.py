@@ -16,7 +16,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "librelux_kv.so")
 SOURCES = ["rlx_runtime.hip", "rlx_cache_kernels.hip", "rlx_gqa_decode.hip", "rlx_mla_decode.hip",
-           "rlx_prefill.hip", "rlx_mla_prefill.hip", "rlx_project.hip"]
+           "rlx_prefill.hip", "rlx_mla_prefill.hip", "rlx_project.hip", "rlx_sampling.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -204,6 +204,43 @@ __device__ __forceinline__ void merge_weights(const float *__restrict__ ml, int6
     if (lane == 0) *inv_l = (L > 0.f) ? 1.f / L : 0.f;
 }
 
+// ---- token selection (rlx_sampling.hip) ------------------------------------
+constexpr int kSampMaxVocab = 1 << 18;  // seen-token bitmap: 32 KB of LDS
+constexpr int kSampMaxSeen = 4096;      // distinct tokens of a repetition window
+
+struct SampleArgs {
+    const float *logits;
+    int64_t stride;  // elements between rows
+    int V;
+    float temperature;
+    int top_k;
+    float top_p, min_p;
+    float rp, fp, pp;          // repeat / frequency / presence penalty
+    const int32_t *seen_tok;   // per row: distinct window tokens, ascending
+    const int32_t *seen_freq;  // ... and their counts
+    const int32_t *seen_off;   // n_rows + 1 offsets; nullptr: no penalties
+    const float *u;            // one draw per row
+    int32_t *out;
+};
+
+struct SpecArgs {
+    const float *d_logits;  // [rows][max_k][V]
+    const float *t_logits;  // [rows][max_k + 1][V]
+    const int32_t *d_tok;   // [rows][max_k]
+    const int32_t *n_draft;  // [rows]
+    int max_k, V;
+    const float *u;  // [rows][max_k + 1] draws in order
+    float temperature;
+    int top_k;
+    float top_p, min_p;
+    int32_t *n_acc, *next;
+};
+
+hipError_t launch_sample(hipStream_t s, const SampleArgs &a, int n_rows);
+hipError_t launch_greedy(hipStream_t s, const float *logits, int64_t stride, int V, int n_rows,
+                         int32_t *out);
+hipError_t launch_spec_accept(hipStream_t s, const SpecArgs &a, int n_rows);
+
 // ---- launchers (stream-ordered, return hipError_t of the launch) ----------
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
 hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n);

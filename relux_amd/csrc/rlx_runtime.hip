@@ -1375,6 +1375,156 @@ int32_t rlx_free_list(void *h, int32_t layer, int32_t *out, int32_t cap, int32_t
     return RLX_OK;
 }
 
+// ---- token selection ------------------------------------------------------
+
+int32_t rlx_greedy(void *h, const float *logits, int32_t n_rows, int32_t vocab, int64_t row_stride,
+                   int32_t *out_tokens) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (n_rows < 0 || vocab <= 0 || row_stride < vocab)
+        return fail(RLX_ERR_INVALID, "rlx_greedy: n_rows=%d vocab=%d row_stride=%lld", n_rows, vocab,
+                    (long long)row_stride);
+    if (n_rows == 0) return RLX_OK;
+    if (!logits || !out_tokens) return fail(RLX_ERR_INVALID, "rlx_greedy: null pointer");
+    int32_t rc = ensure_ws(c, (size_t)n_rows * 4);
+    if (rc) return rc;
+    HIP_TRY(launch_greedy(c->stream, logits, row_stride, vocab, n_rows, (int32_t *)c->ws));
+    HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
+int32_t rlx_sample(void *h, const float *logits, int32_t n_rows, int32_t vocab, int64_t row_stride,
+                   const rlx_sampler_t *p, const int32_t *prev_tokens, const int32_t *prev_offsets,
+                   const float *uniforms, int32_t *out_tokens) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (n_rows < 0 || vocab <= 0 || row_stride < vocab || !p)
+        return fail(RLX_ERR_INVALID, "rlx_sample: n_rows=%d vocab=%d row_stride=%lld params=%p",
+                    n_rows, vocab, (long long)row_stride, (const void *)p);
+    if (n_rows == 0) return RLX_OK;
+    if (!logits || !uniforms || !out_tokens) return fail(RLX_ERR_INVALID, "rlx_sample: null pointer");
+    // Penalties touch only the distinct tokens of each row's window
+    // (sampler.go:213-262): they are counted here and applied on the device.
+    const bool pen = prev_offsets && prev_tokens &&
+                     ((p->repeat_penalty != 1.f && p->repeat_penalty != 0.f) ||
+                      p->frequency_penalty != 0.f || p->presence_penalty != 0.f);
+    std::vector<int32_t> st, sf, so;
+    if (pen) {
+        if (vocab > kSampMaxVocab)
+            return fail(RLX_ERR_UNSUPPORTED, "rlx_sample: penalties with vocab %d > %d", vocab,
+                        kSampMaxVocab);
+        so.push_back(0);
+        std::vector<int32_t> w;
+        for (int b = 0; b < n_rows; b++) {
+            int32_t lo = prev_offsets[b], hi = prev_offsets[b + 1];
+            if (lo < 0 || hi < lo) return fail(RLX_ERR_INVALID, "rlx_sample: prev_offsets row %d", b);
+            if (p->repeat_window > 0 && hi - lo > p->repeat_window) lo = hi - p->repeat_window;
+            w.clear();
+            for (int32_t i = lo; i < hi; i++)
+                if (prev_tokens[i] >= 0 && prev_tokens[i] < vocab) w.push_back(prev_tokens[i]);
+            std::sort(w.begin(), w.end());
+            for (size_t i = 0; i < w.size();) {
+                size_t j = i;
+                while (j < w.size() && w[j] == w[i]) j++;
+                st.push_back(w[i]);
+                sf.push_back((int32_t)(j - i));
+                i = j;
+            }
+            if ((int)st.size() - so.back() > kSampMaxSeen)
+                return fail(RLX_ERR_UNSUPPORTED, "rlx_sample: row %d has %d distinct window tokens (max %d)",
+                            b, (int)st.size() - so.back(), kSampMaxSeen);
+            so.push_back((int32_t)st.size());
+        }
+    }
+    Blob b;
+    const size_t o_u = b.add(std::vector<float>(uniforms, uniforms + n_rows));
+    size_t o_t = 0, o_f = 0, o_o = 0;
+    if (pen) {
+        o_t = b.add(st);
+        o_f = b.add(sf);
+        o_o = b.add(so);
+    }
+    void *dev;
+    int32_t rc = ensure_ws(c, (size_t)n_rows * 4);
+    if (rc) return rc;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    char *d = (char *)dev;
+    SampleArgs a{};
+    a.logits = logits;
+    a.stride = row_stride;
+    a.V = vocab;
+    a.temperature = p->temperature;
+    a.top_k = p->top_k;
+    a.top_p = p->top_p;
+    a.min_p = p->min_p;
+    a.rp = p->repeat_penalty;
+    a.fp = p->frequency_penalty;
+    a.pp = p->presence_penalty;
+    a.seen_tok = pen ? (const int32_t *)(d + o_t) : nullptr;
+    a.seen_freq = pen ? (const int32_t *)(d + o_f) : nullptr;
+    a.seen_off = pen ? (const int32_t *)(d + o_o) : nullptr;
+    a.u = (const float *)(d + o_u);
+    a.out = (int32_t *)c->ws;
+    HIP_TRY(launch_sample(c->stream, a, n_rows));
+    HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
+int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_logits,
+                        const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
+                        int32_t max_k, int32_t vocab, const float *uniforms, const rlx_sampler_t *p,
+                        int32_t *n_accepted, int32_t *next_token) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (n_rows < 0 || max_k < 0 || vocab <= 0 || !p)
+        return fail(RLX_ERR_INVALID, "rlx_spec_accept: n_rows=%d max_k=%d vocab=%d", n_rows, max_k, vocab);
+    if (n_rows == 0) return RLX_OK;
+    if (!target_logits || !n_draft || !uniforms || !n_accepted || !next_token ||
+        (max_k > 0 && (!draft_logits || !draft_tokens)))
+        return fail(RLX_ERR_INVALID, "rlx_spec_accept: null pointer");
+    // Token ids index the logit rows on the device: check them here.
+    for (int b = 0; b < n_rows; b++) {
+        if (n_draft[b] < 0 || n_draft[b] > max_k)
+            return fail(RLX_ERR_INVALID, "rlx_spec_accept: n_draft[%d]=%d outside [0, %d]", b, n_draft[b], max_k);
+        for (int i = 0; i < n_draft[b]; i++) {
+            const int32_t t = draft_tokens[(int64_t)b * max_k + i];
+            if (t < 0 || t >= vocab)
+                return fail(RLX_ERR_INVALID, "rlx_spec_accept: draft token %d of row %d = %d outside [0, %d)",
+                            i, b, t, vocab);
+        }
+    }
+    Blob bl;
+    const size_t o_d = bl.add(std::vector<int32_t>(draft_tokens, draft_tokens + (size_t)n_rows * max_k));
+    const size_t o_n = bl.add(std::vector<int32_t>(n_draft, n_draft + n_rows));
+    const size_t o_u = bl.add(std::vector<float>(uniforms, uniforms + (size_t)n_rows * (max_k + 1)));
+    void *dev;
+    int32_t rc = ensure_ws(c, (size_t)n_rows * 8);
+    if (rc) return rc;
+    if ((rc = stage(c, bl.bytes.data(), bl.bytes.size(), &dev))) return rc;
+    char *d = (char *)dev;
+    SpecArgs a{};
+    a.d_logits = draft_logits;
+    a.t_logits = target_logits;
+    a.d_tok = (const int32_t *)(d + o_d);
+    a.n_draft = (const int32_t *)(d + o_n);
+    a.max_k = max_k;
+    a.V = vocab;
+    a.u = (const float *)(d + o_u);
+    a.temperature = p->temperature;
+    a.top_k = p->top_k;
+    a.top_p = p->top_p;
+    a.min_p = p->min_p;
+    a.n_acc = (int32_t *)c->ws;
+    a.next = (int32_t *)c->ws + n_rows;
+    HIP_TRY(launch_spec_accept(c->stream, a, n_rows));
+    HIP_TRY(hipMemcpyAsync(n_accepted, a.n_acc, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipMemcpyAsync(next_token, a.next, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
 int32_t rlx_pool_ptr(void *h, int32_t layer, void **k_pool, void **v_pool) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);

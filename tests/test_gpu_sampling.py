@@ -1,0 +1,243 @@
+"""Token selection on the device (rlx_greedy, rlx_sample, rlx_spec_accept)
+against the oracle's restatement of sampler.go / speculative.go on the same
+logits and draws, and the speculative decoder end to end on the paged GPU
+caches.
+
+Bar: token ids equal.  The device sums the vocabulary block-parallel, the
+reference sequentially, so a draw that lies within a few ulp of a
+cumulative boundary may land on the neighbouring token; a case counts only
+when the oracle's own answer is unchanged with the draws moved by +-1e-5
+(every case drawn here is such a case in practice: the test reports how
+many were excluded and requires that to be a small minority).
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sampling as S
+from oracle import tiny_decoder as td
+
+pytestmark = pytest.mark.gpu
+
+DELTA = 1e-5
+
+
+@pytest.fixture(scope="module")
+def handle(gpu):
+    from relux_amd import KVCache
+    return KVCache(num_layers=1, max_len=64, num_kv_heads=1, head_dim=64, page_tokens=16,
+                   device=gpu.index)
+
+
+def dev(x, gpu):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(gpu)
+
+
+def make_sampler(p, draws=None):
+    from relux_amd import Sampler
+    return Sampler(temperature=p.temperature, top_k=p.top_k, top_p=p.top_p, min_p=p.min_p,
+                   repeat_penalty=p.repeat_penalty, frequency_penalty=p.frequency_penalty,
+                   presence_penalty=p.presence_penalty, repeat_window=p.repeat_window, rand=draws)
+
+
+def test_greedy(gpu, handle):
+    from relux_amd import Sampler
+    rng = np.random.default_rng(11)
+    for V in (7, 1000, 32000):
+        x = rng.normal(0, 1, (9, V)).astype(np.float32)
+        x[1, [3, V - 1]] = 50.0  # tie: first index wins
+        x[2, :] = 0.0
+        got = Sampler().Greedy(dev(x, gpu), handle)
+        assert got == [S.greedy(r) for r in x], V
+
+
+PARAMS = {
+    "plain": S.SamplerParams(),
+    "temp0.7": S.SamplerParams(temperature=0.7),
+    "temp0": S.SamplerParams(temperature=0.0),
+    "topk5": S.SamplerParams(top_k=5),
+    "topk50_t1.3": S.SamplerParams(top_k=50, temperature=1.3),
+    "topp0.9": S.SamplerParams(top_p=0.9),
+    "minp0.05": S.SamplerParams(min_p=0.05),
+    "all": S.SamplerParams(temperature=0.8, top_k=40, top_p=0.95, min_p=0.02),
+    "penalties": S.SamplerParams(repeat_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.3,
+                                 repeat_window=16),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PARAMS))
+@pytest.mark.parametrize("V", [100, 4096])
+def test_sample(gpu, handle, name, V):
+    p = PARAMS[name]
+    rng = np.random.default_rng(zlib.crc32(name.encode()) + V)
+    rows = 24
+    x = rng.normal(0, 2.5, (rows, V)).astype(np.float32)
+    u = rng.random(rows, dtype=np.float32)
+    prev = [list(rng.integers(0, V, rng.integers(0, 40))) for _ in range(rows)]
+    got = make_sampler(p, S.Draws(u)).Sample(dev(x, gpu), prev, handle)
+    kept = 0
+    for i in range(rows):
+        want = S.sample(x[i], p, u[i], prev=prev[i])
+        if S.sample(x[i], p, u[i] - DELTA, prev=prev[i]) != want or \
+                S.sample(x[i], p, u[i] + DELTA, prev=prev[i]) != want:
+            continue
+        kept += 1
+        assert got[i] == want, (name, V, i, got[i], want)
+    print(f"sample {name} V{V}: {kept}/{rows} robust rows compared")
+    assert kept >= rows - 2
+
+
+@pytest.mark.parametrize("V", [100, 4096])
+def test_spec_accept(gpu, handle, V):
+    from relux_amd import spec_accept
+    rng = np.random.default_rng(V)
+    B, K = 16, 4
+    d = rng.normal(0, 1.5, (B, K, V)).astype(np.float32)
+    t = np.concatenate([d + rng.normal(0, 0.7, (B, K, V)).astype(np.float32),
+                        rng.normal(0, 1.5, (B, 1, V)).astype(np.float32)], axis=1)
+    nd = np.array([K] * 10 + [2, 3, 1, 0, K, K], np.int32)
+    tok = np.zeros((B, K), np.int32)
+    for b in range(B):  # drafts drawn from the draft distribution
+        for i in range(K):
+            tok[b, i] = S.sample(d[b, i], S.SamplerParams(), float(rng.random()))
+    u = rng.random((B, K + 1), dtype=np.float32)
+    params = S.SamplerParams(temperature=0.9, top_k=30)
+    acc, nxt = spec_accept(handle, dev(d, gpu), dev(t, gpu), tok, nd, u, make_sampler(params))
+    kept = 0
+    outcomes = set()
+    for b in range(B):
+        k = nd[b]
+        want = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1], params)
+        lo = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1] - DELTA, params)
+        hi = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1] + DELTA, params)
+        if lo != want or hi != want:
+            continue
+        kept += 1
+        outcomes.add(want[0] == k)
+        assert (acc[b], nxt[b]) == want, (V, b, acc[b], nxt[b], want)
+    print(f"spec_accept V{V}: {kept}/{B} robust rows compared")
+    assert kept >= B - 2
+    assert outcomes == {True, False}  # both the rejection and the all-accepted paths ran
+
+
+def test_spec_accept_rejects_bad_tokens(gpu, handle):
+    from relux_amd import ReluxError, spec_accept
+    d = torch.zeros(1, 2, 10, device=gpu)
+    t = torch.zeros(1, 3, 10, device=gpu)
+    with pytest.raises(ReluxError):
+        spec_accept(handle, d, t, [[1, 10]], [2], np.full(3, 0.5), make_sampler(S.SamplerParams()))
+    with pytest.raises(ReluxError):
+        spec_accept(handle, d, t, [[1, 2]], [3], np.full(3, 0.5), make_sampler(S.SamplerParams()))
+
+
+# ---- speculative decoding end to end on the GPU caches -----------------------
+
+class GpuLM:
+    """A config-1 decoder (CPU math for the non-attention modules, as in
+    test_gpu_tiny_decoder) whose attention cache is the paged GPU cache;
+    records every forward / rollback with the logits it returned."""
+
+    def __init__(self, model, gpu):
+        from relux_amd import KVCache
+        self.m, self.gpu = model, gpu
+        cfg = model.cfg
+        self.cache = KVCache(num_layers=cfg["layers"], max_len=cfg["max_seq"], num_kv_heads=cfg["kv_heads"],
+                             head_dim=cfg["d_model"] // cfg["heads"], page_tokens=16, device=gpu.index)
+        self.H = cfg["heads"]
+        self.calls = []
+
+    # the three cache calls TinyDecoder makes
+    def total_len(self, layer):
+        return self.cache.TotalLen(layer)
+
+    def append(self, layer, k, v):
+        self.cache.Append(layer, torch.from_numpy(k).to(self.gpu), torch.from_numpy(v).to(self.gpu), layout="HSD")
+
+    def attend(self, layer, q):
+        S_ = q.shape[1]
+        out = self.cache.Attend(layer, torch.from_numpy(np.ascontiguousarray(q)).to(self.gpu),
+                                num_heads=self.H, n_q=[S_], layout="HSD", mask="causal")
+        return out.cpu().numpy()
+
+    # the model interface SpeculativeDecoder drives
+    def forward(self, ids):
+        lg = self.m.forward(list(ids), self)
+        self.calls.append(("f", list(ids), lg))
+        return torch.from_numpy(lg).to(self.gpu)
+
+    def rollback(self, n):
+        self.calls.append(("r", n, None))
+        if n:
+            self.cache.Rollback(0, n)
+
+    def reset(self):
+        self.cache.Reset()
+
+
+class ReplayLM:
+    """Returns the logits a GpuLM produced, in call order, checking that the
+    oracle loop makes the same calls."""
+
+    def __init__(self, calls):
+        self.calls = list(calls)
+
+    def forward(self, ids):
+        kind, want_ids, lg = self.calls.pop(0)
+        assert kind == "f" and want_ids == list(ids), (kind, want_ids, ids)
+        return lg
+
+    def rollback(self, n):
+        kind, want_n, _ = self.calls.pop(0)
+        assert kind == "r" and want_n == n, (kind, want_n, n)
+
+
+def test_speculative_same_model_is_greedy(gpu):
+    from relux_amd import Draws, Sampler, SpeculativeDecoder
+    m = td.TinyDecoder(td.CFG1, seed=0, rope_rule="offset")
+    prompt = td.prompt_ids(td.CFG1)
+    lm = GpuLM(m, gpu)
+    want, _, _ = m.generate(prompt, 12, lm)
+    sd = SpeculativeDecoder(GpuLM(m, gpu), GpuLM(m, gpu), 4, Sampler(temperature=0.0, rand=Draws(seed=1)))
+    gen, rate = sd.Generate(prompt, 12)
+    assert gen == want[len(prompt):] and rate == 1.0
+
+
+def test_speculative_decoder_replays_on_oracle(gpu):
+    from relux_amd import Draws, SpeculativeDecoder
+    target = GpuLM(td.TinyDecoder(td.CFG1, seed=0, rope_rule="offset"), gpu)
+    draft = GpuLM(td.TinyDecoder(td.CFG1, seed=1, rope_rule="offset"), gpu)
+    prompt = td.prompt_ids(td.CFG1)
+    draws = np.random.default_rng(5).random(600, dtype=np.float32)
+    params = S.SamplerParams(temperature=0.9, top_k=40, repeat_penalty=1.1, repeat_window=8)
+    sd = SpeculativeDecoder(draft, target, 3, make_sampler(params, Draws(values=draws)))
+    gen, rate = sd.Generate(prompt, 20)
+    assert len(gen) == 20
+    # 1. Decisions: the oracle loop over the same logits and draws makes the
+    #    same calls (ids, rollback counts) and commits the same tokens.
+    og, orate = S.speculative_generate(ReplayLM(draft.calls), ReplayLM(target.calls), prompt, 20, 3,
+                                       params, S.Draws(draws))
+    assert og == gen and orate == rate
+    rolled = [c[1] for c in target.calls if c[0] == "r"]
+    print(f"acceptance {rate:.2f}; target rollbacks {rolled}")
+    assert any(rolled)  # some drafts were rejected and rolled back
+    # 2. Cache semantics: the oracle model on a logical cache, driven by the
+    #    same call sequence, gives the same logits at every call.
+    for lm in (draft, target):
+        logical = td.LogicalCache(td.CFG1)
+        for kind, arg, lg in lm.calls:
+            if kind == "r":
+                for layer in range(td.CFG1["layers"]):
+                    logical.rollback(layer, arg)
+                continue
+            want = lm.m.forward(arg, logical)
+            d = np.abs(lg - want)
+            assert d.max() < 2e-2 and d.mean() < 2e-3, (d.max(), d.mean())
+        # 3. The paged cache holds exactly the committed prefix: layer 0 K/V
+        #    (position-only inputs) bit-exact against the logical cache.
+        T = logical.total_len(0)
+        assert lm.cache.TotalLen(0) == T
+        k_dev, v_dev = lm.cache.View(0)
+        np.testing.assert_array_equal(k_dev.cpu().float().numpy()[0], logical.k[0])
+        np.testing.assert_array_equal(v_dev.cpu().float().numpy()[0], logical.v[0])
