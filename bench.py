@@ -47,6 +47,12 @@ WORKLOADS = {
     # the same for the MLA layer of config 3 (DeepSeek-V2-Lite d_model 2048)
     "mla_fused8k": dict(kind="mla_fused", B=32, H=16, D=128, P=64, T=8192, d_model=2048,
                         layers=4, time="project"),
+    # next rows after the path (ranks 2-3): token selection on device logits --
+    # batched speculative acceptance (4 drafts, 32k vocabulary) ...
+    "spec_accept": dict(kind="accept", B=64, K=4, V=32000, layers=1, time="select"),
+    # ... and Sampler.Sample (penalties over a 64-token window, T 0.8,
+    # top-k 50, top-p 0.9, min-p 0.02) over 64 rows of a 32k vocabulary
+    "sample": dict(kind="sample", B=64, V=32000, layers=1, time="select"),
 }
 MFMA_BF16_PEAK_TFS = 2500.0
 
@@ -316,14 +322,81 @@ def setup_spec(cfg, torch, dev, rng, max_steps=4096):
     return c, step, B * nd, kernel_bytes, kernel_bytes, desc, "gqa_decode_kernel<128,2>", lens
 
 
+def _select_handle(dev):
+    from relux_amd import KVCache
+    return KVCache(num_layers=1, max_len=16, num_kv_heads=1, head_dim=64, page_tokens=16,
+                   device=dev.index)
+
+
+def setup_accept(cfg, torch, dev, rng):
+    """Batched acceptPhase: 64 sequences x 4 drafts over a 32k vocabulary.
+    Target rows are the draft rows plus noise (acceptance varies by row);
+    drafts are drawn from the draft rows.  Algorithmic bytes per call: the
+    logit rows the reference's acceptPhase examines (draft and target row of
+    each tested draft, plus the next target row when all are accepted),
+    counted from each call's results."""
+    import numpy as np
+    from relux_amd import Sampler, spec_accept
+    B, K, V = cfg["B"], cfg["K"], cfg["V"]
+    c = _select_handle(dev)
+    g = torch.Generator(device=dev).manual_seed(6)
+    d = torch.randn(B, K, V, device=dev, generator=g) * 2.0
+    t = torch.cat([d + torch.randn(B, K, V, device=dev, generator=g) * 0.6,
+                   torch.randn(B, 1, V, device=dev, generator=g) * 2.0], dim=1)
+    tok = torch.multinomial(torch.softmax(d.reshape(B * K, V), dim=-1), 1, generator=g)
+    tok = tok.reshape(B, K).cpu().numpy().astype(np.int32)
+    smp = Sampler(temperature=0.8, top_k=50, top_p=0.9)
+    nd = [K] * B
+    state = {"bytes": 0, "steps": 0, "accepted": 0}
+
+    def step(i):
+        u = rng.random((B, K + 1), dtype=np.float32)
+        acc, _ = spec_accept(c, d, t, tok, nd, u, smp)
+        state["steps"] += 1
+        state["accepted"] += sum(acc)
+        state["bytes"] += sum((min(a + 1, K) * 2 + (a == K)) * V * 4 for a in acc)
+
+    def finish():
+        b = state["bytes"] // max(state["steps"], 1)
+        return b, b, {"acceptance_timed": state["accepted"] / max(state["steps"] * B * K, 1)}
+
+    desc = {"workload": f"spec_accept B{B} drafts{K} V{V} (acceptPhase + resample, T0.8 top-k50 top-p0.9)",
+            "batch": B, "drafts": K, "vocab": V, "state": state, "finish": finish}
+    return c, step, B, 0, 0, desc, "spec_accept_kernel", None
+
+
+def setup_sample(cfg, torch, dev, rng):
+    """Sampler.Sample over 64 rows of a 32k vocabulary with every stage on:
+    penalties (64-token window), temperature, top-k, top-p, min-p.
+    Algorithmic bytes: each logit row once."""
+    import numpy as np
+    from relux_amd import Draws, Sampler
+    B, V = cfg["B"], cfg["V"]
+    c = _select_handle(dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    x = torch.randn(B, V, device=dev, generator=g) * 3.0
+    prev = [list(rng.integers(0, V, 64)) for _ in range(B)]
+    smp = Sampler(temperature=0.8, top_k=50, top_p=0.9, min_p=0.02, repeat_penalty=1.1,
+                  frequency_penalty=0.1, presence_penalty=0.1, repeat_window=64, rand=Draws(seed=8))
+
+    def step(i):
+        smp.Sample(x, prev, c)
+
+    b = B * V * 4
+    desc = {"workload": f"sample B{B} V{V} (penalties/64, T0.8, top-k50, top-p0.9, min-p0.02)",
+            "batch": B, "vocab": V}
+    return c, step, B, b, b, desc, "sample_kernel", None
+
+
 def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
-                                 "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3}[name])
+                                 "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3,
+                                 "spec_accept": 6, "sample": 7}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
              "spec": setup_spec, "gqa_fused": setup_gqa_fused,
-             "mla_fused": setup_mla_fused}[cfg["kind"]]
+             "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
@@ -332,8 +405,9 @@ def run_workload(name, steps, warmup, torch, dev):
     torch.cuda.synchronize(dev)
     st = desc.get("state")
     if st is not None:  # context lengths drift: count what the timed steps attend
-        st["attended"] = 0
-        st["steps"] = 0
+        for key in ("attended", "steps", "bytes", "accepted"):
+            if key in st:
+                st[key] = 0
     c.Timing(True, kernels=cfg.get("time", "attend"))
     t0 = time.perf_counter()
     for i in range(steps):
@@ -344,7 +418,12 @@ def run_workload(name, steps, warmup, torch, dev):
     kms, kn = c.KernelTime()
     c.Timing(False)
     kavg_s = kms / max(kn, 1) / 1e3
-    if st is not None and st["steps"]:
+    finish = desc.pop("finish", None)
+    if finish is not None:  # bytes counted from the timed calls' results
+        kbytes, sbytes, extra = finish()
+        desc = {k: v for k, v in desc.items() if k != "state"}
+        desc.update(extra)
+    elif st is not None and st["steps"]:
         per_step_tokens = st["attended"] / st["steps"]
         extra = kbytes - sum(T + cfg["drafts"] for T in lens) * cfg["KVH"] * cfg["D"] * 4
         kbytes = sbytes = int(per_step_tokens * cfg["KVH"] * cfg["D"] * 4 + extra)
@@ -478,7 +557,8 @@ def main():
     secondary = []
     if not args.no_secondary:
         for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
-                                 "fused8k", "mla_fused8k") if w != args.workload]:
+                                 "fused8k", "mla_fused8k", "spec_accept", "sample")
+                     if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact
             n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
             s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)

@@ -99,10 +99,12 @@ int32_t rlx_device_sync(void);
 /* enable is a mask: RLX_TIME_ATTEND brackets the main attention kernel of
  * every later attend call on this handle with HIP events (on the handle's
  * stream), RLX_TIME_PROJECT every projection kernel of
- * rlx_gqa_project_append; 0 disables.  Either way the recorded intervals
- * are discarded. */
+ * rlx_gqa_project_append / rlx_mla_project_append, RLX_TIME_SELECT the
+ * kernel of rlx_greedy / rlx_sample / rlx_spec_accept; 0 disables.  Either
+ * way the recorded intervals are discarded. */
 #define RLX_TIME_ATTEND 1
 #define RLX_TIME_PROJECT 2
+#define RLX_TIME_SELECT 4
 int32_t rlx_cache_timing(void *cache, int32_t enable);
 /* Synchronise, then report the summed duration (ms) and number of the
  * timed kernel launches recorded since the last call, and clear them. */

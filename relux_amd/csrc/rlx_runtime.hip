@@ -1388,7 +1388,11 @@ int32_t rlx_greedy(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
     if (!logits || !out_tokens) return fail(RLX_ERR_INVALID, "rlx_greedy: null pointer");
     int32_t rc = ensure_ws(c, (size_t)n_rows * 4);
     if (rc) return rc;
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
     HIP_TRY(launch_greedy(c->stream, logits, row_stride, vocab, n_rows, (int32_t *)c->ws));
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     return RLX_OK;
@@ -1466,7 +1470,11 @@ int32_t rlx_sample(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
     a.seen_off = pen ? (const int32_t *)(d + o_o) : nullptr;
     a.u = (const float *)(d + o_u);
     a.out = (int32_t *)c->ws;
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
     HIP_TRY(launch_sample(c->stream, a, n_rows));
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     return RLX_OK;
@@ -1518,7 +1526,11 @@ int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_
     a.min_p = p->min_p;
     a.n_acc = (int32_t *)c->ws;
     a.next = (int32_t *)c->ws + n_rows;
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
     HIP_TRY(launch_spec_accept(c->stream, a, n_rows));
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     HIP_TRY(hipMemcpyAsync(n_accepted, a.n_acc, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipMemcpyAsync(next_token, a.next, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));

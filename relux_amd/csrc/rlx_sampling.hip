@@ -1,5 +1,5 @@
 // Token selection on the device: Sampler.Greedy, Sampler.Sample and the
-// speculative decoder's acceptPhase / resampleRejected, one 256-thread
+// speculative decoder's acceptPhase / resampleRejected, one 512-thread
 // work-group per row of logits.
 //
 // Reference: sampler.go:56-68 (Greedy), 73-210 (Sample: penalties ->
@@ -8,21 +8,36 @@
 // r < min(1, p_t/p_d), resample from norm(max(0, p_t - p_d))), 344-368
 // (softmaxAlloc).  Each rng.Float32() draw is an input.
 //
+// Working set.  Sample first brings the row's scratch values (logits after
+// penalties and temperature, sampler.go:80-97) into LDS when the vocabulary
+// fits (<= 32768 entries: 128 KB), applying the penalties in place on the
+// row's distinct window tokens; larger vocabularies are re-read from memory
+// each pass, with the penalised tokens found through an LDS bitmap.  With
+// top-k on, the tokens at or above the k-th largest value are compacted, in
+// index order, into an LDS candidate list (<= 2048 entries) and every later
+// stage runs over that list only (its top-p search by one wave, with the
+// probabilities in registers).  Once the softmax is known the working set
+// holds probabilities in place.
+//
 // The reference sorts (argsortDescF32, kthLargest: selection sorts) and sums
-// the vocabulary sequentially.  Here every stage is a pass over the row:
-//   * the top-k threshold (k-th largest value) is a radix select on the
-//     float's order-preserving key, 8 bits per pass, integer counts;
+// the vocabulary sequentially.  Here:
+//   * the top-k threshold (k-th largest value) is found one key bit at a
+//     time on the float's order-preserving key (32 counting steps): first
+//     on the per-thread maxima, whose k-th largest bounds it from below,
+//     then on the short list of entries at or above that bound;
 //   * the top-p cutoff is the key tau of the item where the descending
-//     cumulative probability first reaches p: a radix walk, 4 bits per
-//     pass, over per-bin probability sums; every item with key >= tau is
-//     kept (the reference keeps only as many items tied at tau as its sort
-//     order reaches: the one place the results can differ besides rounding);
-//   * sums are per-thread sequential partials combined in a fixed order, so
-//     a call is deterministic; they round differently from a sequential sum
-//     by a few ulp, which moves a draw only when r lies within that of a
-//     cumulative boundary;
+//     cumulative probability first reaches p, i.e. the largest tau whose
+//     tail sum still reaches p: 31 bisection steps over probabilities kept
+//     in LDS; every item with key >= tau is kept (the reference keeps only
+//     as many items tied at tau as its sort order reaches: the one place
+//     the results can differ besides rounding);
+//   * sums are per-thread sequential partials combined in a fixed order
+//     (64-lane trees, then the 8 wave results in order), so a call is
+//     deterministic; they round differently from a sequential sum by a few
+//     ulp, which moves a draw only when r lies within that of a cumulative
+//     boundary;
 //   * the categorical draw: per-thread chunk sums, an ordered exclusive
-//     prefix, then each thread walks its chunk; the lowest hit wins.
+//     scan, then each thread walks its chunk; the lowest hit wins.
 // Arithmetic follows the reference's f32 order with explicitly rounded
 // operations (no fused multiply-add): s/temp, fastexp32(x - max) with one
 // multiply and one add (mha.go:823-833), p * f32(1/sum).
@@ -30,7 +45,16 @@
 
 namespace rlx {
 
-constexpr int kSampThreads = 256;
+constexpr int kST = 512;            // threads per row
+constexpr int kSW = kST / 64;       // waves per row
+constexpr int kRowCap = 32768;      // LDS row region (floats)
+constexpr int kCandCap = 2048;      // compacted top-k candidates
+constexpr int kSeenOff = 8192;      // region words: bitmap [0, 8192), seen tokens, values
+constexpr int kTileOff = 16384;     // region words: tile counts of a memory-resident row
+static_assert(kSampMaxVocab / 32 <= kSeenOff, "bitmap must fit before the seen list");
+static_assert(kSeenOff + 2 * kSampMaxSeen <= kTileOff, "seen list must fit before the tile counts");
+static_assert(kTileOff + kSampMaxVocab / 64 <= kRowCap, "tile counts must fit in the region");
+static_assert(kRowCap / 64 <= kST, "LDS-row tile counts use one slot per thread");
 
 __device__ __forceinline__ float fastexp32_dev(float x) {
     if (x < -87.f) return 0.f;
@@ -48,49 +72,160 @@ __device__ __forceinline__ uint32_t fkey(float f) {
 __device__ __forceinline__ float funkey(uint32_t k) {
     return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
 }
+// Lanes below this one whose bit is set in m.
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
 
 struct SampLds {
-    float red[4];
-    int hist[256];
-    float bins[16][kSampThreads];
-    float tot[16];
-    float pre[kSampThreads];
+    float red[2][kSW];
+    int cnt[kST];
+    uint32_t key[kST];
+    int tiles[kRowCap / 64];
     int sel_i[2];
     float sel_f;
     int best;
-    int stok[kSampMaxSeen];
-    float sval[kSampMaxSeen];
+    float cv[kCandCap];
+    int ci[kCandCap];
+    float region[kRowCap];
 };
 
-// Block reductions: per-thread values, 64-lane tree, then the 4 wave
-// results in a fixed order; every thread returns the same value.
-__device__ __forceinline__ float blk_sum(float v, SampLds &s) {
+// ---- block-wide reductions and scans: fixed combination order, every
+// thread gets the same result --------------------------------------------
+// Wave reductions in the VALU pipeline: DPP row shifts 1, 2, 4, 8 leave each
+// 16-lane row's total in its lane 15, row_bcast 15 / 31 carry them up; lane
+// 63 ends with the wave's total.
+#define RLX_DPP(v, ctrl, rmask, ident)                                                              \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, (float)(ident)),   \
+                                                          __builtin_bit_cast(int, v), ctrl, rmask, 0xF, false))
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += RLX_DPP(v, 0x111, 0xF, 0.f);
+    v += RLX_DPP(v, 0x112, 0xF, 0.f);
+    v += RLX_DPP(v, 0x114, 0xF, 0.f);
+    v += RLX_DPP(v, 0x118, 0xF, 0.f);
+    v += RLX_DPP(v, 0x142, 0xA, 0.f);
+    v += RLX_DPP(v, 0x143, 0xC, 0.f);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, RLX_DPP(v, 0x111, 0xF, -INFINITY));
+    v = fmaxf(v, RLX_DPP(v, 0x112, 0xF, -INFINITY));
+    v = fmaxf(v, RLX_DPP(v, 0x114, 0xF, -INFINITY));
+    v = fmaxf(v, RLX_DPP(v, 0x118, 0xF, -INFINITY));
+    v = fmaxf(v, RLX_DPP(v, 0x142, 0xA, -INFINITY));
+    v = fmaxf(v, RLX_DPP(v, 0x143, 0xC, -INFINITY));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ void blk_sum2(float &a, float &b, SampLds &s) {
+    a = wave_sum_dpp(a);
+    b = wave_sum_dpp(b);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        s.red[0][threadIdx.x >> 6] = a;
+        s.red[1][threadIdx.x >> 6] = b;
+    }
+    __syncthreads();
+    a = s.red[0][0];
+    b = s.red[1][0];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_down(v, o);
+    for (int w = 1; w < kSW; w++) {
+        a += s.red[0][w];
+        b += s.red[1][w];
+    }
+}
+__device__ __forceinline__ void blk_max2(float &a, float &b, SampLds &s) {
+    a = wave_max_dpp(a);
+    b = wave_max_dpp(b);
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) s.red[threadIdx.x >> 6] = v;
+    if ((threadIdx.x & 63) == 0) {
+        s.red[0][threadIdx.x >> 6] = a;
+        s.red[1][threadIdx.x >> 6] = b;
+    }
     __syncthreads();
-    return ((s.red[0] + s.red[1]) + s.red[2]) + s.red[3];
+    a = s.red[0][0];
+    b = s.red[1][0];
+#pragma unroll
+    for (int w = 1; w < kSW; w++) {
+        a = fmaxf(a, s.red[0][w]);
+        b = fmaxf(b, s.red[1][w]);
+    }
+}
+__device__ __forceinline__ float blk_sum(float v, SampLds &s) {
+    float z = 0.f;
+    blk_sum2(v, z, s);
+    return v;
 }
 __device__ __forceinline__ float blk_max(float v, SampLds &s) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_down(v, o));
+    float z = -INFINITY;
+    blk_max2(v, z, s);
+    return v;
+}
+// The same DPP sequence leaves every lane with its inclusive prefix.
+__device__ __forceinline__ float wave_scan_dpp(float v) {
+    v += RLX_DPP(v, 0x111, 0xF, 0.f);
+    v += RLX_DPP(v, 0x112, 0xF, 0.f);
+    v += RLX_DPP(v, 0x114, 0xF, 0.f);
+    v += RLX_DPP(v, 0x118, 0xF, 0.f);
+    v += RLX_DPP(v, 0x142, 0xA, 0.f);
+    v += RLX_DPP(v, 0x143, 0xC, 0.f);
+    return v;
+}
+#define RLX_DPPI(v, ctrl, rmask) __builtin_amdgcn_update_dpp(0, v, ctrl, rmask, 0xF, false)
+__device__ __forceinline__ int wave_iscan_dpp(int v) {
+    v += RLX_DPPI(v, 0x111, 0xF);
+    v += RLX_DPPI(v, 0x112, 0xF);
+    v += RLX_DPPI(v, 0x114, 0xF);
+    v += RLX_DPPI(v, 0x118, 0xF);
+    v += RLX_DPPI(v, 0x142, 0xA);
+    v += RLX_DPPI(v, 0x143, 0xC);
+    return v;
+}
+__device__ __forceinline__ float blk_scan_excl(float v, SampLds &s, float *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float inc = wave_scan_dpp(v);
+    const float exc = RLX_DPP(inc, 0x138, 0xF, 0.f);  // wave_shr:1, lane 0 gets 0
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) s.red[threadIdx.x >> 6] = v;
+    if (lane == 63) s.red[0][w] = inc;
     __syncthreads();
-    return fmaxf(fmaxf(s.red[0], s.red[1]), fmaxf(s.red[2], s.red[3]));
+    float base = 0.f, tot = 0.f;
+    for (int i = 0; i < kSW; i++) {
+        if (i < w) base += s.red[0][i];
+        tot += s.red[0][i];
+    }
+    *total = tot;
+    return base + exc;
+}
+__device__ __forceinline__ int blk_iscan_excl(int v, SampLds &s, int *total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int inc = wave_iscan_dpp(v);
+    __syncthreads();
+    if (lane == 63) s.cnt[w] = inc;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int i = 0; i < kSW; i++) {
+        if (i < w) base += s.cnt[i];
+        tot += s.cnt[i];
+    }
+    __syncthreads();
+    *total = tot;
+    return base + inc - v;
+}
+__device__ __forceinline__ int blk_isum(int v, SampLds &s) {
+    int t;
+    blk_iscan_excl(v, s, &t);
+    return t;
 }
 
-// One row's sampling state: the value function (penalties, temperature,
-// top-k mask) and the normalisation factors of each enabled stage.
-struct RowCtx {
+// ---- the working set ------------------------------------------------------
+struct Src {
+    int mode;  // 0: LDS row region, 1: LDS candidate list, 2: memory
+    int n;     // entries
     const float *row;
     int V;
-    const uint32_t *bits;  // seen-token bitmap (nseen > 0)
-    int nseen;
+    int nseen;  // mode 2: penalised tokens (bitmap + list in the region)
     float temp;
     bool div;
-    bool topk;
+    bool topk;  // mode 2 without compaction: mask below kthr
     float kthr;
     float m;
     bool n1;
@@ -105,32 +240,53 @@ struct RowCtx {
     float i3;
 };
 
-// scratch[v] after penalties and temperature, -inf if top-k drops it.
-__device__ __forceinline__ float samp_val(const RowCtx &c, const SampLds &s, int v) {
+// Scratch value of working-set entry i (sampler.go:80-114).  M is the
+// storage mode as a template parameter, so each pass compiles to plain LDS
+// reads (modes 0, 1) or to the memory path (mode 2) alone.
+template <int M>
+__device__ __forceinline__ float wval(const Src &c, const SampLds &s, int i) {
+    if constexpr (M == 0) return s.region[i];
+    if constexpr (M == 1) return s.cv[i];
     float x;
-    if (c.nseen > 0 && ((c.bits[v >> 5] >> (v & 31)) & 1u)) {
+    const uint32_t *bits = (const uint32_t *)s.region;
+    if (c.nseen > 0 && ((bits[i >> 5] >> (i & 31)) & 1u)) {
+        const int *stok = (const int *)(s.region + kSeenOff);
+        const float *sv = s.region + kSeenOff + kSampMaxSeen;
         int lo = 0, hi = c.nseen - 1;
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
-            if (s.stok[mid] < v)
+            if (stok[mid] < i)
                 lo = mid + 1;
             else
                 hi = mid;
         }
-        x = s.sval[lo];
+        x = sv[lo];
     } else {
-        x = c.row[v];
+        x = c.row[i];
     }
     if (c.div) x = __fdiv_rn(x, c.temp);
     if (c.topk && x < c.kthr) x = -INFINITY;
     return x;
 }
-
-// Probability of v after stage `stage` (1 softmax, 2 top-p, 3 min-p).
-__device__ __forceinline__ float samp_prob(const RowCtx &c, const SampLds &s, int v, int stage) {
-    const float x = samp_val(c, s, v);
-    float p = (x == -INFINITY) ? 0.f : fastexp32_dev(__fsub_rn(x, c.m));
-    if (c.n1) p = __fmul_rn(p, c.i1);
+template <int M>
+__device__ __forceinline__ int widx(const SampLds &s, int i) {
+    if constexpr (M == 1) return s.ci[i];
+    return i;
+}
+// Stage-1 probability of entry i: stored in place once the softmax is known
+// (modes 0 and 1), recomputed from the value in mode 2.
+template <int M>
+__device__ __forceinline__ float wp1(const Src &c, const SampLds &s, int i) {
+    if constexpr (M == 0) return s.region[i];
+    if constexpr (M == 1) return s.cv[i];
+    const float x = wval<2>(c, s, i);
+    const float p = (x == -INFINITY) ? 0.f : fastexp32_dev(__fsub_rn(x, c.m));
+    return c.n1 ? __fmul_rn(p, c.i1) : p;
+}
+// Probability after stage `stage` (1 softmax, 2 top-p, 3 min-p).
+template <int M>
+__device__ __forceinline__ float wprob(const Src &c, const SampLds &s, int i, int stage) {
+    float p = wp1<M>(c, s, i);
     if (stage >= 2 && c.topp) {
         p = (fkey(p) >= c.tau) ? p : 0.f;
         if (c.n2) p = __fmul_rn(p, c.i2);
@@ -142,138 +298,286 @@ __device__ __forceinline__ float samp_prob(const RowCtx &c, const SampLds &s, in
     return p;
 }
 
-// First index v (in index order) at which the running sum of w(v) exceeds
-// r; `dflt` when none does.
-template <class W>
-__device__ int samp_draw(int V, float r, int dflt, SampLds &s, W w) {
-    const int tid = threadIdx.x;
-    const int C = (V + kSampThreads - 1) / kSampThreads;
-    const int v0 = min(V, tid * C), v1 = min(V, v0 + C);
-    float cs = 0.f;
-    for (int v = v0; v < v1; v++) cs += w(v);
-    __syncthreads();
-    s.pre[tid] = cs;
-    if (tid == 0) s.best = INT_MAX;
-    __syncthreads();
-    if (tid == 0) {
-        float a = 0.f;
-        for (int i = 0; i < kSampThreads; i++) {
-            const float t = s.pre[i];
-            s.pre[i] = a;
-            a += t;
+// ---- selection building blocks --------------------------------------------
+
+// Largest key t with #{i < n : key(i) >= t} >= k (the k-th largest key),
+// one bit per step, by wave 0 with the n <= kCandCap keys in registers.
+template <class K>
+__device__ uint32_t kth_key_w0(int n, int k, SampLds &s, K key) {
+    constexpr int R = kCandCap / 64;
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
+        uint32_t kk[R];
+#pragma unroll
+        for (int j = 0; j < R; j++) kk[j] = (lane + 64 * j < n) ? key(lane + 64 * j) : 0u;
+        uint32_t res = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = res | (1u << bit);
+            int cnt = 0;  // per-key ballots, counted on the scalar unit
+#pragma unroll
+            for (int j = 0; j < R; j++) cnt += (int)__popcll(__ballot(kk[j] >= cand));
+            if (cnt >= k) res = cand;
         }
+        if (lane == 0) s.sel_i[0] = (int)res;
     }
     __syncthreads();
-    float cum = s.pre[tid];
-    for (int v = v0; v < v1; v++) {
-        cum += w(v);
-        if (r < cum) {
-            atomicMin(&s.best, v);
-            break;
-        }
-    }
+    const uint32_t r = (uint32_t)s.sel_i[0];
     __syncthreads();
-    const int b = s.best;
-    return b == INT_MAX ? dflt : b;
+    return r;
+}
+// The same over the whole working set with every thread (n entries).
+template <class K>
+__device__ uint32_t kth_key_blk(int n, int k, SampLds &s, K key) {
+    uint32_t res = 0;
+    for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t cand = res | (1u << bit);
+        int cnt = 0;
+        for (int i = threadIdx.x; i < n; i += kST) cnt += key(i) >= cand;
+        if (blk_isum(cnt, s) >= k) res = cand;
+    }
+    return res;
 }
 
-// Sampler.Sample for one row (the row context's value function set up).
-__device__ int sample_row(RowCtx &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
-    const int tid = threadIdx.x, V = c.V;
-    c.topk = false;
-    c.topp = false;
-    c.minp = false;
-    // Top-k threshold: the k-th largest value (sampler.go:100-114).
-    if (top_k > 0) {
-        uint32_t prefix = 0, mask = 0;
-        int kk = top_k;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = tid; i < 256; i += kSampThreads) s.hist[i] = 0;
-            __syncthreads();
-            for (int v = tid; v < V; v += kSampThreads) {
-                const uint32_t key = fkey(samp_val(c, s, v));
-                if ((key & mask) == prefix) atomicAdd(&s.hist[(key >> shift) & 255], 1);
-            }
-            __syncthreads();
-            if (tid == 0) {
-                int cum = 0, d = 255;
-                for (; d > 0; d--) {
-                    if (cum + s.hist[d] >= kk) break;
-                    cum += s.hist[d];
-                }
-                s.sel_i[0] = d;
-                s.sel_i[1] = kk - cum;
-            }
-            __syncthreads();
-            prefix |= (uint32_t)s.sel_i[0] << shift;
-            mask |= 0xFFu << shift;
-            kk = s.sel_i[1];
-        }
-        c.kthr = funkey(prefix);
-        c.topk = true;
+// Entries i < n with keep(i), in index order, into the candidate list
+// (value val(i), index idx(i)); returns their count and writes nothing if
+// it exceeds kCandCap.  64-entry tiles: a ballot per tile, an ordered scan
+// of the tile counts, then each kept entry's slot is its tile's offset plus
+// the kept lanes below it.
+template <class P, class Vf, class If>
+__device__ int compact_blk(int n, int *tc, SampLds &s, P keep, Vf val, If idx) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int T = (n + 63) / 64;
+#pragma unroll 8
+    for (int t = wave; t < T; t += kSW) {
+        const int i = 64 * t + lane;
+        const uint64_t m = __ballot(i < n && keep(i));
+        if (lane == 0) tc[t] = (int)__popcll(m);
     }
+    __syncthreads();
+    const int TP = (T + kST - 1) / kST;
+    const int t0 = min(T, (int)threadIdx.x * TP), t1 = min(T, t0 + TP);
+    int mine = 0;
+    for (int t = t0; t < t1; t++) mine += tc[t];
+    int total;
+    int off = blk_iscan_excl(mine, s, &total);
+    for (int t = t0; t < t1; t++) {
+        const int c = tc[t];
+        tc[t] = off;
+        off += c;
+    }
+    __syncthreads();
+    if (total > kCandCap) return total;
+#pragma unroll 8
+    for (int t = wave; t < T; t += kSW) {
+        const int i = 64 * t + lane;
+        const bool k = i < n && keep(i);
+        const uint64_t m = __ballot(k);
+        if (k) {
+            const int pos = tc[t] + lanes_below(m);
+            s.cv[pos] = val(i);
+            s.ci[pos] = idx(i);
+        }
+    }
+    __syncthreads();
+    return total;
+}
+
+// Filter the candidate list in place, in order (wave 0, one 64-entry tile
+// after another: a tile is read before any slot at or below it is written).
+template <class P>
+__device__ int filter_w0(int n, SampLds &s, P keep) {
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
+        int out = 0;
+        for (int t = 0; t < n; t += 64) {
+            const int i = t + lane;
+            const bool in = i < n;
+            const float v = in ? s.cv[i] : 0.f;
+            const int x = in ? s.ci[i] : 0;
+            const bool k = in && keep(v);
+            const uint64_t m = __ballot(k);
+            if (k) {
+                s.cv[out + lanes_below(m)] = v;
+                s.ci[out + lanes_below(m)] = x;
+            }
+            out += (int)__popcll(m);
+        }
+        if (lane == 0) s.sel_i[0] = out;
+    }
+    __syncthreads();
+    const int r = s.sel_i[0];
+    __syncthreads();
+    return r;
+}
+
+// First entry (in order) at which the running sum of w exceeds r, mapped
+// through idx; `dflt` when none does.  Chunk sums per thread (contiguous
+// chunks), an ordered exclusive scan, then only the thread whose chunk
+// holds r walks it; should rounding leave that walk without a hit, every
+// later chunk is walked.
+template <class W, class I>
+__device__ int samp_draw(int n, float r, int dflt, SampLds &s, W w, I idx) {
+    const int tid = threadIdx.x;
+    const int C = (n + kST - 1) / kST;
+    const int i0 = min(n, tid * C), i1 = min(n, i0 + C);
+    float cs = 0.f;
+#pragma unroll 8
+    for (int i = i0; i < i1; i++) cs += w(i);
+    float tot;
+    const float start = blk_scan_excl(cs, s, &tot);
+    if (tid == 0) s.best = INT_MAX;
+    __syncthreads();
+    auto walk = [&]() {
+        float cum = start;
+        for (int i = i0; i < i1; i++) {
+            cum += w(i);
+            if (r < cum) {
+                atomicMin(&s.best, i);
+                break;
+            }
+        }
+    };
+    if (!(r < start) && r < start + cs) walk();
+    __syncthreads();
+    if (s.best == INT_MAX) {
+        if (r < start + cs) walk();
+        __syncthreads();
+    }
+    const int b = s.best;
+    return b == INT_MAX ? dflt : idx(b);
+}
+
+// ---- Sampler.Sample ---------------------------------------------------------
+
+// Top-k (sampler.go:100-114) on a row in mode M (0 or 2): keep the values >=
+// the k-th largest.  Lower bound: the k-th largest of the per-thread maxima
+// (k distinct entries, so <= the k-th largest of all); the entries at or
+// above it are compacted in index order and the exact threshold is found
+// within that list, which then becomes the working set (mode 1).  If the
+// list would not fit, the threshold is searched over the whole row.
+template <int M>
+__device__ void topk_select(Src &c, int top_k, SampLds &s) {
+    const int tid = threadIdx.x;
+    auto vkey = [&](int i) { return fkey(wval<M>(c, s, i)); };
+    if (top_k <= kST) {
+        uint32_t mk = 0;
+#pragma unroll 8
+        for (int i = tid; i < c.n; i += kST) mk = max(mk, vkey(i));
+        s.key[tid] = mk;
+        __syncthreads();
+        const uint32_t lb = kth_key_w0(kST, top_k, s, [&](int i) { return s.key[i]; });
+        int *tiles = M == 2 ? (int *)(s.region + kTileOff) : s.tiles;
+        const int total = compact_blk(
+            c.n, tiles, s, [&](int i) { return vkey(i) >= lb; }, [&](int i) { return wval<M>(c, s, i); },
+            [&](int i) { return i; });
+        if (total <= kCandCap) {
+            c.mode = 1;
+            c.n = total;
+            c.div = false;
+            c.topk = false;
+            const uint32_t tk = kth_key_w0(c.n, top_k, s, [&](int i) { return fkey(s.cv[i]); });
+            c.n = filter_w0(c.n, s, [&](float v) { return fkey(v) >= tk; });
+            return;
+        }
+    }
+    const float thr = funkey(kth_key_blk(c.n, top_k, s, vkey));
+    if (M == 0) {
+        for (int i = tid; i < c.n; i += kST)
+            if (s.region[i] < thr) s.region[i] = -INFINITY;
+        __syncthreads();
+    } else {
+        c.topk = true;
+        c.kthr = thr;
+    }
+}
+
+// Softmax, top-p, min-p and the draw (sampler.go:117-206) over a working
+// set in mode M.
+template <int M>
+__device__ int sample_finish(Src &c, float top_p, float min_p, float r, SampLds &s) {
+    const int tid = threadIdx.x;
     // Softmax with fastexp32 (sampler.go:117-138).
     float mx = -INFINITY;
-    for (int v = tid; v < V; v += kSampThreads) mx = fmaxf(mx, samp_val(c, s, v));
+#pragma unroll 8
+    for (int i = tid; i < c.n; i += kST) mx = fmaxf(mx, wval<M>(c, s, i));
     c.m = blk_max(mx, s);
     float sm = 0.f;
-    for (int v = tid; v < V; v += kSampThreads) {
-        const float x = samp_val(c, s, v);
-        if (x != -INFINITY) sm += fastexp32_dev(__fsub_rn(x, c.m));
+#pragma unroll 8
+    for (int i = tid; i < c.n; i += kST) {
+        const float x = wval<M>(c, s, i);
+        sm += (x == -INFINITY) ? 0.f : fastexp32_dev(__fsub_rn(x, c.m));
     }
     const float S1 = blk_sum(sm, s);
     c.n1 = S1 > 0.f;
     c.i1 = c.n1 ? __fdiv_rn(1.f, S1) : 1.f;
-    // Top-p (sampler.go:141-165): radix walk for the cutoff key.
-    if (top_p > 0.f && top_p < 1.f) {
-        uint32_t prefix = 0, mask = 0;
-        float above = 0.f;
-        bool all = false;
-        for (int shift = 28; shift >= 0 && !all; shift -= 4) {
-#pragma unroll
-            for (int j = 0; j < 16; j++) s.bins[j][tid] = 0.f;
-            for (int v = tid; v < V; v += kSampThreads) {
-                const float p = samp_prob(c, s, v, 1);
-                const uint32_t key = fkey(p);
-                if ((key & mask) == prefix) s.bins[(key >> shift) & 15][tid] += p;
-            }
-            __syncthreads();
-            if (tid < 16) {
-                float t = 0.f;
-                for (int i = 0; i < kSampThreads; i++) t += s.bins[tid][i];
-                s.tot[tid] = t;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                float acc = above;
-                int d = 15;
-                for (; d >= 0; d--) {
-                    if (acc + s.tot[d] >= top_p) break;
-                    acc += s.tot[d];
-                }
-                // Nothing reaches p: on the first pass the whole row is kept
-                // (the reference's cutoff stays n); deeper, rounding of the
-                // sub-bin sums: keep the whole bin.
-                s.sel_i[0] = (d < 0) ? 0 : d;
-                s.sel_i[1] = (d < 0 && shift == 28) ? 1 : 0;
-                s.sel_f = (d < 0) ? above : acc;
-            }
-            __syncthreads();
-            if (s.sel_i[1]) {
-                all = true;
-                prefix = 0;
-            } else {
-                prefix |= (uint32_t)s.sel_i[0] << shift;
-                mask |= 0xFu << shift;
-                above = s.sel_f;
-            }
-            __syncthreads();
+    if constexpr (M != 2) {  // values -> stage-1 probabilities, in place
+        float *lw = M == 0 ? s.region : s.cv;
+#pragma unroll 8
+        for (int i = tid; i < c.n; i += kST) {
+            const float x = lw[i];
+            const float p = (x == -INFINITY) ? 0.f : fastexp32_dev(__fsub_rn(x, c.m));
+            lw[i] = c.n1 ? __fmul_rn(p, c.i1) : p;
         }
-        c.tau = prefix;
+        __syncthreads();
+    }
+    // Top-p (sampler.go:141-165): the cutoff is the item where the
+    // descending cumulative probability first reaches p, i.e. the largest
+    // key tau whose tail sum sum(p : key(p) >= tau) still reaches p.
+    if (top_p > 0.f && top_p < 1.f) {
+        uint32_t res;
+        if constexpr (M == 1) {  // short list: wave 0, probabilities in registers
+            constexpr int R = kCandCap / 64;
+            const int lane = tid & 63;
+            if (tid < 64) {
+                float pv[R];
+#pragma unroll
+                for (int j = 0; j < R; j++) pv[j] = (lane + 64 * j < c.n) ? s.cv[lane + 64 * j] : 0.f;
+                auto tail = [&](uint32_t t) {
+                    float a = 0.f;
+#pragma unroll
+                    for (int j = 0; j < R; j++) a += (fkey(pv[j]) >= t) ? pv[j] : 0.f;
+                    return wave_sum_dpp(a);
+                };
+                uint32_t rr = 0x80000000u;  // key of +0: the whole set
+                if (tail(rr) >= top_p) {
+                    for (int bit = 30; bit >= 0; bit--) {
+                        const uint32_t cand = rr | (1u << bit);
+                        if (tail(cand) >= top_p) rr = cand;
+                    }
+                } else {
+                    rr = 0;  // never reached: keep everything
+                }
+                if (lane == 0) s.sel_i[0] = (int)rr;
+            }
+            __syncthreads();
+            res = (uint32_t)s.sel_i[0];
+            __syncthreads();
+        } else {
+            auto tail = [&](uint32_t t) {
+                float a = 0.f;
+#pragma unroll 8
+                for (int i = tid; i < c.n; i += kST) {
+                    const float p = wp1<M>(c, s, i);
+                    a += (fkey(p) >= t) ? p : 0.f;
+                }
+                return blk_sum(a, s);
+            };
+            res = 0x80000000u;
+            if (tail(res) >= top_p) {
+                for (int bit = 30; bit >= 0; bit--) {
+                    const uint32_t cand = res | (1u << bit);
+                    if (tail(cand) >= top_p) res = cand;
+                }
+            } else {
+                res = 0;
+            }
+        }
+        c.tau = res;
         c.topp = true;
         c.n2 = false;
         float k2 = 0.f;
-        for (int v = tid; v < V; v += kSampThreads) k2 += samp_prob(c, s, v, 2);
+#pragma unroll 8
+        for (int i = tid; i < c.n; i += kST) k2 += wprob<M>(c, s, i, 2);
         const float S2 = blk_sum(k2, s);
         c.n2 = S2 > 0.f;
         c.i2 = c.n2 ? __fdiv_rn(1.f, S2) : 1.f;
@@ -281,25 +585,46 @@ __device__ int sample_row(RowCtx &c, int top_k, float top_p, float min_p, float 
     // Min-p (sampler.go:168-191).
     if (min_p > 0.f) {
         float mp = 0.f;
-        for (int v = tid; v < V; v += kSampThreads) mp = fmaxf(mp, samp_prob(c, s, v, 2));
+#pragma unroll 8
+        for (int i = tid; i < c.n; i += kST) mp = fmaxf(mp, wprob<M>(c, s, i, 2));
         mp = blk_max(mp, s);
         c.thr3 = __fmul_rn(mp, min_p);
         c.minp = true;
         c.n3 = false;
         float k3 = 0.f;
-        for (int v = tid; v < V; v += kSampThreads) k3 += samp_prob(c, s, v, 3);
+#pragma unroll 8
+        for (int i = tid; i < c.n; i += kST) k3 += wprob<M>(c, s, i, 3);
         const float S3 = blk_sum(k3, s);
         c.n3 = S3 > 0.f;
         c.i3 = c.n3 ? __fdiv_rn(1.f, S3) : 1.f;
     }
-    // Categorical draw (sampler.go:194-206), n-1 if r is never reached.
-    return samp_draw(V, r, V - 1, s, [&](int v) { return samp_prob(c, s, v, 3); });
+    // Categorical draw (sampler.go:194-206), vocab - 1 if r is never reached.
+    return samp_draw(
+        c.n, r, c.V - 1, s, [&](int i) { return wprob<M>(c, s, i, 3); }, [&](int i) { return widx<M>(s, i); });
 }
 
-__device__ void row_init(RowCtx &c, const float *row, int V, float temperature) {
+__device__ int sample_set(Src &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
+    if (top_k > 0 && top_k < c.n) {
+        if (c.mode == 0)
+            topk_select<0>(c, top_k, s);
+        else
+            topk_select<2>(c, top_k, s);
+    }
+    if (c.mode == 0) return sample_finish<0>(c, top_p, min_p, r, s);
+    if (c.mode == 1) return sample_finish<1>(c, top_p, min_p, r, s);
+    return sample_finish<2>(c, top_p, min_p, r, s);
+}
+
+// Bring a row into the working set: LDS values (penalties applied in place,
+// then divided by the temperature) when it fits, else memory reads with the
+// penalised tokens in an LDS bitmap and list.  seen/freq: the row's
+// distinct window tokens (ascending) and counts; ns of them.
+__device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temperature,
+                         const int32_t *seen, const int32_t *freq, int ns, float rp, float fp, float pp) {
+    const int tid = threadIdx.x;
     c.row = row;
     c.V = V;
-    c.bits = nullptr;
+    c.n = V;
     c.nseen = 0;
     float t = temperature;
     if (t <= 0.f) t = 1e-5f;
@@ -307,55 +632,76 @@ __device__ void row_init(RowCtx &c, const float *row, int V, float temperature) 
     c.div = (t != 1.f);
     c.topk = c.topp = c.minp = false;
     c.n1 = c.n2 = c.n3 = false;
+    auto pen = [&](float x, int f) {
+        if (rp != 1.f && rp != 0.f) x = (x > 0.f) ? __fdiv_rn(x, rp) : __fmul_rn(x, rp);
+        if (fp != 0.f) x = __fsub_rn(x, __fmul_rn(fp, (float)f));
+        if (pp != 0.f) x = __fsub_rn(x, pp);
+        return x;
+    };
+    if (V <= kRowCap) {
+        c.mode = 0;
+        if ((((uintptr_t)row) & 15) == 0 && (V & 3) == 0) {
+            const float4 *r4 = (const float4 *)row;
+#pragma unroll 8
+            for (int v = tid; v < V / 4; v += kST) ((float4 *)s.region)[v] = r4[v];
+        } else {
+#pragma unroll 8
+            for (int v = tid; v < V; v += kST) s.region[v] = row[v];
+        }
+        __syncthreads();
+        for (int i = tid; i < ns; i += kST) s.region[seen[i]] = pen(s.region[seen[i]], freq[i]);
+        __syncthreads();
+        if (c.div) {
+#pragma unroll 8
+            for (int v = tid; v < V; v += kST) s.region[v] = __fdiv_rn(s.region[v], c.temp);
+            __syncthreads();
+            c.div = false;
+        }
+        return;
+    }
+    c.mode = 2;
+    if (ns > 0) {
+        uint32_t *bits = (uint32_t *)s.region;
+        int *stok = (int *)(s.region + kSeenOff);
+        float *sv = s.region + kSeenOff + kSampMaxSeen;
+        for (int i = tid; i < (V + 31) >> 5; i += kST) bits[i] = 0u;
+        __syncthreads();
+        for (int i = tid; i < ns; i += kST) {
+            stok[i] = seen[i];
+            sv[i] = pen(row[seen[i]], freq[i]);
+            atomicOr(&bits[seen[i] >> 5], 1u << (seen[i] & 31));
+        }
+        __syncthreads();
+        c.nseen = ns;
+    }
 }
 
 // top_k / top_p clamped as sampler.go:100-106, 141-144.
 __device__ __forceinline__ int clamp_topk(int k, int V) { return (k < 0 || k >= V) ? 0 : k; }
 __device__ __forceinline__ float clamp_topp(float p) { return (p <= 0.f || p > 1.f) ? 1.f : p; }
 
-__global__ __launch_bounds__(kSampThreads) void sample_kernel(const SampleArgs a) {
+__global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs a) {
     __shared__ SampLds s;
-    extern __shared__ uint32_t seen_bits[];
-    const int b = blockIdx.x, tid = threadIdx.x;
-    RowCtx c;
-    row_init(c, a.logits + (int64_t)b * a.stride, a.V, a.temperature);
-    // Penalties (sampler.go:213-262) on the row's distinct window tokens,
-    // given sorted with their counts; looked up through a bitmap.
+    const int b = blockIdx.x;
     const int n0 = a.seen_off ? a.seen_off[b] : 0;
     const int ns = a.seen_off ? a.seen_off[b + 1] - n0 : 0;
-    if (ns > 0) {
-        const int words = (a.V + 31) >> 5;
-        for (int i = tid; i < words; i += kSampThreads) seen_bits[i] = 0u;
-        __syncthreads();
-        for (int i = tid; i < ns; i += kSampThreads) {
-            const int tok = a.seen_tok[n0 + i];
-            float x = c.row[tok];
-            if (a.rp != 1.f && a.rp != 0.f) x = (x > 0.f) ? __fdiv_rn(x, a.rp) : __fmul_rn(x, a.rp);
-            if (a.fp != 0.f) x = __fsub_rn(x, __fmul_rn(a.fp, (float)a.seen_freq[n0 + i]));
-            if (a.pp != 0.f) x = __fsub_rn(x, a.pp);
-            s.stok[i] = tok;
-            s.sval[i] = x;
-            atomicOr(&seen_bits[tok >> 5], 1u << (tok & 31));
-        }
-        __syncthreads();
-        c.bits = seen_bits;
-        c.nseen = ns;
-    }
-    const int t = sample_row(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
-    if (tid == 0) a.out[b] = t;
+    Src c;
+    load_row(c, s, a.logits + (int64_t)b * a.stride, a.V, a.temperature, a.seen_tok + n0,
+             a.seen_freq + n0, ns, a.rp, a.fp, a.pp);
+    const int t = sample_set(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
+    if (threadIdx.x == 0) a.out[b] = t;
 }
 
 // First index of the largest value (sampler.go:56-68).
-__global__ __launch_bounds__(kSampThreads) void greedy_kernel(const float *__restrict__ logits,
-                                                               int64_t stride, int V,
-                                                               int32_t *__restrict__ out) {
-    __shared__ float bv[kSampThreads];
-    __shared__ int bi[kSampThreads];
+__global__ __launch_bounds__(kST) void greedy_kernel(const float *__restrict__ logits, int64_t stride,
+                                                      int V, int32_t *__restrict__ out) {
+    __shared__ float bv[kST];
+    __shared__ int bi[kST];
     const float *row = logits + (int64_t)blockIdx.x * stride;
     const int tid = threadIdx.x;
     float best = -INFINITY;
     int idx = INT_MAX;
-    for (int v = tid; v < V; v += kSampThreads) {
+    for (int v = tid; v < V; v += kST) {
         const float x = row[v];
         if (idx == INT_MAX || x > best) {
             best = x;
@@ -365,7 +711,7 @@ __global__ __launch_bounds__(kSampThreads) void greedy_kernel(const float *__res
     bv[tid] = best;
     bi[tid] = idx;
     __syncthreads();
-    for (int o = kSampThreads / 2; o > 0; o >>= 1) {
+    for (int o = kST / 2; o > 0; o >>= 1) {
         if (tid < o) {
             const float x = bv[tid + o];
             const int j = bi[tid + o];
@@ -379,18 +725,7 @@ __global__ __launch_bounds__(kSampThreads) void greedy_kernel(const float *__res
     if (tid == 0) out[blockIdx.x] = bi[0];
 }
 
-// softmaxAlloc of one row (speculative.go:344-368): max and f32(1/sum).
-__device__ void spec_softmax(const float *row, int V, SampLds &s, float *m, bool *norm, float *inv) {
-    float mx = -INFINITY;
-    for (int v = threadIdx.x; v < V; v += kSampThreads) mx = fmaxf(mx, row[v]);
-    *m = blk_max(mx, s);
-    float sm = 0.f;
-    for (int v = threadIdx.x; v < V; v += kSampThreads) sm += fastexp32_dev(__fsub_rn(row[v], *m));
-    const float S = blk_sum(sm, s);
-    *norm = S > 0.f;
-    *inv = *norm ? __fdiv_rn(1.f, S) : 1.f;
-}
-
+// ---- speculative acceptance ---------------------------------------------------
 __device__ __forceinline__ float spec_p(const float *row, int v, float m, bool norm, float inv) {
     const float e = fastexp32_dev(__fsub_rn(row[v], m));
     return norm ? __fmul_rn(e, inv) : e;
@@ -400,20 +735,62 @@ __device__ __forceinline__ float spec_p(const float *row, int v, float m, bool n
 // while u_i < min(1, p_t/max(p_d, 1e-10)); on the first rejection draw the
 // replacement from norm(max(0, p_t - p_d)) (resampleRejected 247-290, the
 // target distribution if that is empty); all accepted: Sample the target's
-// next row without penalties.
-__global__ __launch_bounds__(kSampThreads) void spec_accept_kernel(const SpecArgs a) {
+// next row without penalties.  The draft and target rows of a position are
+// reduced together (softmaxAlloc, speculative.go:344-368: max, then the sum
+// of fastexp32 weights) with 16-byte loads; the resample weights are staged
+// in LDS for the draw when the vocabulary fits.
+__global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
     __shared__ SampLds s;
     const int b = blockIdx.x, tid = threadIdx.x;
-    const int k = a.n_draft[b];
+    const int k = a.n_draft[b], V = a.V;
     const float *u = a.u + (int64_t)b * (a.max_k + 1);
-    const float *dl = a.d_logits + (int64_t)b * a.max_k * a.V;
-    const float *tl = a.t_logits + (int64_t)b * (a.max_k + 1) * a.V;
+    const float *dl = a.d_logits + (int64_t)b * a.max_k * V;
+    const float *tl = a.t_logits + (int64_t)b * (a.max_k + 1) * V;
     for (int i = 0; i < k; i++) {
-        const float *dr = dl + (int64_t)i * a.V, *tr = tl + (int64_t)i * a.V;
-        float dm, di, tm, ti;
-        bool dn, tn;
-        spec_softmax(dr, a.V, s, &dm, &dn, &di);
-        spec_softmax(tr, a.V, s, &tm, &tn, &ti);
+        const float *dr = dl + (int64_t)i * V, *tr = tl + (int64_t)i * V;
+        const bool vec = ((((uintptr_t)dr) | ((uintptr_t)tr)) & 15) == 0 && (V & 3) == 0;
+        float dm = -INFINITY, tm = -INFINITY;
+        if (vec) {
+            const float4 *d4 = (const float4 *)dr, *t4 = (const float4 *)tr;
+#pragma unroll 8
+            for (int v = tid; v < V / 4; v += kST) {
+                const float4 x = d4[v], y = t4[v];
+                dm = fmaxf(dm, fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)));
+                tm = fmaxf(tm, fmaxf(fmaxf(y.x, y.y), fmaxf(y.z, y.w)));
+            }
+        } else {
+#pragma unroll 8
+            for (int v = tid; v < V; v += kST) {
+                dm = fmaxf(dm, dr[v]);
+                tm = fmaxf(tm, tr[v]);
+            }
+        }
+        blk_max2(dm, tm, s);
+        float ds = 0.f, ts = 0.f;
+        if (vec) {
+            const float4 *d4 = (const float4 *)dr, *t4 = (const float4 *)tr;
+#pragma unroll 8
+            for (int v = tid; v < V / 4; v += kST) {
+                const float4 x = d4[v], y = t4[v];
+                ds += fastexp32_dev(__fsub_rn(x.x, dm));
+                ds += fastexp32_dev(__fsub_rn(x.y, dm));
+                ds += fastexp32_dev(__fsub_rn(x.z, dm));
+                ds += fastexp32_dev(__fsub_rn(x.w, dm));
+                ts += fastexp32_dev(__fsub_rn(y.x, tm));
+                ts += fastexp32_dev(__fsub_rn(y.y, tm));
+                ts += fastexp32_dev(__fsub_rn(y.z, tm));
+                ts += fastexp32_dev(__fsub_rn(y.w, tm));
+            }
+        } else {
+#pragma unroll 8
+            for (int v = tid; v < V; v += kST) {
+                ds += fastexp32_dev(__fsub_rn(dr[v], dm));
+                ts += fastexp32_dev(__fsub_rn(tr[v], tm));
+            }
+        }
+        blk_sum2(ds, ts, s);
+        const bool dn = ds > 0.f, tn = ts > 0.f;
+        const float di = dn ? __fdiv_rn(1.f, ds) : 1.f, ti = tn ? __fdiv_rn(1.f, ts) : 1.f;
         const int tok = a.d_tok[(int64_t)b * a.max_k + i];
         const float dP = spec_p(dr, tok, dm, dn, di), tP = spec_p(tr, tok, tm, tn, ti);
         float acc = __fdiv_rn(tP, dP > 1e-10f ? dP : 1e-10f);
@@ -423,15 +800,25 @@ __global__ __launch_bounds__(kSampThreads) void spec_accept_kernel(const SpecArg
             const float d = __fsub_rn(spec_p(tr, v, tm, tn, ti), spec_p(dr, v, dm, dn, di));
             return d < 0.f ? 0.f : d;
         };
+        const bool lds = V <= kRowCap;
         float sa = 0.f;
-        for (int v = tid; v < a.V; v += kSampThreads) sa += adj(v);
-        const float SA = blk_sum(sa, s);
+#pragma unroll 4
+        for (int v = tid; v < V; v += kST) {
+            const float x = adj(v);
+            if (lds) s.region[v] = x;
+            sa += x;
+        }
+        const float SA = blk_sum(sa, s);  // (its barriers also publish the region)
+        auto ident = [](int v) { return v; };
         int res;
         if (SA > 0.f) {
             const float inv = __fdiv_rn(1.f, SA);
-            res = samp_draw(a.V, u[i + 1], 0, s, [&](int v) { return __fmul_rn(adj(v), inv); });
+            if (lds)
+                res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return __fmul_rn(s.region[v], inv); }, ident);
+            else
+                res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return __fmul_rn(adj(v), inv); }, ident);
         } else {
-            res = samp_draw(a.V, u[i + 1], 0, s, [&](int v) { return spec_p(tr, v, tm, tn, ti); });
+            res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return spec_p(tr, v, tm, tn, ti); }, ident);
         }
         if (tid == 0) {
             a.n_acc[b] = i;
@@ -439,9 +826,9 @@ __global__ __launch_bounds__(kSampThreads) void spec_accept_kernel(const SpecArg
         }
         return;
     }
-    RowCtx c;
-    row_init(c, tl + (int64_t)k * a.V, a.V, a.temperature);
-    const int t = sample_row(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, u[k], s);
+    Src c;
+    load_row(c, s, tl + (int64_t)k * V, V, a.temperature, nullptr, nullptr, 0, 0.f, 0.f, 0.f);
+    const int t = sample_set(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
     if (tid == 0) {
         a.n_acc[b] = k;
         a.next[b] = t;
@@ -449,19 +836,18 @@ __global__ __launch_bounds__(kSampThreads) void spec_accept_kernel(const SpecArg
 }
 
 hipError_t launch_sample(hipStream_t st, const SampleArgs &a, int n_rows) {
-    const size_t dyn = a.seen_off ? (size_t)((a.V + 31) >> 5) * 4 : 0;
-    sample_kernel<<<n_rows, kSampThreads, dyn, st>>>(a);
+    sample_kernel<<<n_rows, kST, 0, st>>>(a);
     return hipGetLastError();
 }
 
 hipError_t launch_greedy(hipStream_t st, const float *logits, int64_t stride, int V, int n_rows,
                          int32_t *out) {
-    greedy_kernel<<<n_rows, kSampThreads, 0, st>>>(logits, stride, V, out);
+    greedy_kernel<<<n_rows, kST, 0, st>>>(logits, stride, V, out);
     return hipGetLastError();
 }
 
 hipError_t launch_spec_accept(hipStream_t st, const SpecArgs &a, int n_rows) {
-    spec_accept_kernel<<<n_rows, kSampThreads, 0, st>>>(a);
+    spec_accept_kernel<<<n_rows, kST, 0, st>>>(a);
     return hipGetLastError();
 }
 

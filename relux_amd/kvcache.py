@@ -77,9 +77,11 @@ class _PagedCache:
         check(self._lib.rlx_cache_sync(self._h))
 
     def Timing(self, enable=True, kernels="attend"):
-        """Bracket every later attention kernel ("attend") or projection
-        kernel ("project") with HIP events."""
-        mask = {"attend": _lib.RLX_TIME_ATTEND, "project": _lib.RLX_TIME_PROJECT}[kernels]
+        """Bracket every later attention kernel ("attend"), projection
+        kernel ("project") or token-selection kernel ("select") with HIP
+        events."""
+        mask = {"attend": _lib.RLX_TIME_ATTEND, "project": _lib.RLX_TIME_PROJECT,
+                "select": _lib.RLX_TIME_SELECT}[kernels]
         check(self._lib.rlx_cache_timing(self._h, mask if enable else 0))
 
     def KernelTime(self):
