@@ -44,6 +44,10 @@ WORKLOADS = {
     # Q/K/V projection (d_model 4096) + RoPE + append -- before the 8k decode
     "fused8k": dict(kind="gqa_fused", B=16, H=32, KVH=8, D=128, P=16, T=8192, d_model=4096,
                     layers=2, time="project"),
+    # the whole attention block of a layer on the device: the fused step,
+    # the 8k decode, then W_O + residual (timed kernel: the decode)
+    "block8k": dict(kind="gqa_fused", B=16, H=32, KVH=8, D=128, P=16, T=8192, d_model=4096,
+                    layers=2, out_proj=True),
     # the same for the MLA layer of config 3 (DeepSeek-V2-Lite d_model 2048)
     "mla_fused8k": dict(kind="mla_fused", B=32, H=16, D=128, P=64, T=8192, d_model=2048,
                         layers=4, time="project"),
@@ -119,15 +123,18 @@ def setup_gqa_fused(cfg, torch, dev, rng):
     hidden states x [B][d_model] -> ProjectAppend (packed W_q|W_k|W_v bf16,
     RoPE at the cache position, append) -> Attend -> Rollback.  The timed
     kernel is the projection (HBM-bound on the 50 MB of packed weights)."""
-    from relux_amd import pack_qkv, rope_tables
-    c, _, B, _, _, desc, _, lens = setup_gqa(cfg, torch, dev, rng)
+    from relux_amd import pack_out, pack_qkv, rope_tables
+    c, _, B, att_bytes, _, desc, att_kname, lens = setup_gqa(cfg, torch, dev, rng)
     H, KVH, D, L, dm = cfg["H"], cfg["KVH"], cfg["D"], cfg["layers"], cfg["d_model"]
-    wp = []
+    out_proj = cfg.get("out_proj", False)
+    wp, wo = [], []
     for layer in range(L):
         wq = (torch.randn(dm, H * D, device=dev) * 0.02).to(torch.bfloat16)
         wk = (torch.randn(dm, KVH * D, device=dev) * 0.02).to(torch.bfloat16)
         wv = (torch.randn(dm, KVH * D, device=dev) * 0.02).to(torch.bfloat16)
         wp.append(pack_qkv(wq, wk, wv, H, KVH, D))
+        if out_proj:
+            wo.append(pack_out((torch.randn(H * D, dm, device=dev) * 0.02).to(torch.bfloat16)))
     rope = rope_tables(D, 10000.0, max(lens) + 64, dev)
     x = torch.randn(B, dm, device=dev, dtype=torch.bfloat16)
     out = torch.empty(B, H, D, device=dev, dtype=torch.bfloat16)
@@ -138,16 +145,24 @@ def setup_gqa_fused(cfg, torch, dev, rng):
         q = c.ProjectAppend(layer, x, wp[layer], H, rope=rope, seq_ids=seqs, n_tok=ones,
                             q_dtype=torch.bfloat16)
         c.Attend(layer, q, H, seq_ids=seqs, out=out)
+        if out_proj:
+            c.OutProject(out.view(B, H * D), wo[layer], dm, residual=x, out=y)
         c.Rollback(seqs, ones)
 
+    y = torch.empty(B, dm, device=dev, dtype=torch.bfloat16)
     w_bytes = (H + 2 * KVH) * D * dm * 2
     kernel_bytes = w_bytes + B * dm * 2 + B * H * D * 2 + B * KVH * D * 2 * 2
     Tatt = [T + 1 for T in lens]
     step_bytes = kernel_bytes + sum(Tatt) * KVH * D * 2 * 2 + 2 * B * H * D * 2
     desc = dict(desc)
+    desc["d_model"] = dm
+    if out_proj:  # timed kernel: the decode; step bytes add W_O, x and y
+        step_bytes += H * D * dm * 2 + B * H * D * 2 + 2 * B * dm * 2
+        desc["workload"] = (f"gqa_attention_block B{B} H{H} KVH{KVH} D{D} d_model{dm} P{cfg['P']} "
+                            f"T{cfg['T']} (projection+RoPE+append, decode, W_O + residual)")
+        return c, step, B, att_bytes, step_bytes, desc, att_kname, lens
     desc["workload"] = (f"gqa_fused_step B{B} H{H} KVH{KVH} D{D} d_model{dm} P{cfg['P']} "
                         f"T{cfg['T']} (projection+RoPE+append, then decode)")
-    desc["d_model"] = dm
     return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel<gqa>", lens
 
 
@@ -393,7 +408,7 @@ def run_workload(name, steps, warmup, torch, dev):
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
                                  "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3,
-                                 "spec_accept": 6, "sample": 7}[name])
+                                 "spec_accept": 6, "sample": 7, "block8k": 2}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
              "spec": setup_spec, "gqa_fused": setup_gqa_fused,
              "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample}[cfg["kind"]]
@@ -557,7 +572,7 @@ def main():
     secondary = []
     if not args.no_secondary:
         for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
-                                 "fused8k", "mla_fused8k", "spec_accept", "sample")
+                                 "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample")
                      if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact
             n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))

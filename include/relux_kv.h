@@ -199,6 +199,20 @@ int32_t rlx_mla_project_append(void *cache, int32_t layer, int32_t n_seqs, const
                                int32_t rope_rows, int32_t rope_mode, void *q_nope_out,
                                void *q_rope_out, int32_t q_dtype);
 
+/* The step after attention: out[r] = x[r] . W (+ residual[r]) for `rows`
+ * rows -- the output projection (mha.go:356-360 W_O, x = the attention
+ * output [rows][H*D]; mla.go:384-389) and the transformer block's residual
+ * add (transformer_block.go:119-142), which the reference runs on the host.
+ * W [k_in][n_out] (the reference's in-row/out-col layout, bf16 or f32) is
+ * packed once by rlx_pack_out into k_in*n_out bf16; k_in % 32 == 0,
+ * n_out % 16 == 0.  x: device [rows][k_in] (RLX_F32 / RLX_BF16; f32 rows are
+ * used at f32 precision); residual: NULL or device [rows][n_out] in
+ * out_dtype; out: device [rows][n_out].  Runs on cache's stream. */
+int32_t rlx_pack_out(const void *w, int32_t w_dtype, int32_t k_in, int32_t n_out, void *out);
+int32_t rlx_out_project(void *cache, int32_t rows, const void *x, int32_t x_dtype, int32_t k_in,
+                        const void *w_packed, int32_t n_out, const void *residual, void *out,
+                        int32_t out_dtype);
+
 /* MLA: c_src [sum n][d_c], kr_src [sum n][d_r] (post-RoPE).  Replaces
  * MLACache.Append (mla_cache.go:152-182). */
 int32_t rlx_mla_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,

@@ -81,6 +81,8 @@ SIGNATURES = {
     "rlx_pack_mla_proj": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
     "rlx_mla_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _i32, _vp,
                                _vp, _i32, _i32, _vp, _vp, _i32],
+    "rlx_pack_out": [_vp, _i32, _i32, _i32, _vp],
+    "rlx_out_project": [_vp, _i32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _i32],
     "rlx_mla_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32],
     "rlx_kv_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],
     "rlx_mla_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],

@@ -350,6 +350,7 @@ hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t 
 constexpr int kProjRows = 64;
 constexpr int kProjModelGQA = 0;
 constexpr int kProjModelMLA = 1;
+constexpr int kProjModelOut = 2;  // out = x.W (+ residual): D = output features
 hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
                             int w_bf16, int K, uint16_t *out);
 hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patch *patches,

@@ -12,11 +12,20 @@
 // then the KVH v-heads, each D features), stored as 1 KB MFMA fragments of
 // 16 features x 32 k so that every weight load streams contiguous memory.
 //
+// The same kernel runs the step after attention (mha.go:356-360 W_O,
+// mla.go:384-389; the transformer block's residual add): out = x.W (+ the
+// residual), no RoPE, no append.
+//
 // Work-group = 16 output features x all rows (at most 64); its 4 waves take
 // contiguous ranges of the 32-wide k-steps (software-pipelined chunks of 8
-// weight fragments) and meet in LDS.  MFMA 16x16x32: A = x
-// rows (converted to bf16), B = Wp rows.  The result lane holds 4 rows of
-// one feature, so a RoPE pair partner (feature ^ 1) is one lane away.
+// weight fragments) and meet in LDS.  MFMA 16x16x32: A = x rows, B = Wp
+// rows.  bf16 activations enter as they are; f32 activations as a pair
+// hi = bf16(x), lo = bf16(x - hi) multiplied separately into the same f32
+// accumulator (bf16 products are exact in f32), which keeps the product sum
+// within ~2^-17 of the f32-activation one -- the kernel streams the weights
+// from HBM, so the second product costs no time.  The result lane holds 4
+// rows of one feature, so a RoPE pair partner (feature ^ 1) is one lane
+// away.
 #include "rlx_common.h"
 
 namespace rlx {
@@ -67,8 +76,11 @@ constexpr int kProjChunk = 8;   // k-steps of W held in registers at once per wa
 //             q_r (H x d_r, RoPE)      -> q_out2 [rows][H][d_r]
 //             c^KV (d_c)               -> latent rows [0, d_c)
 //             k^R (d_r, RoPE)          -> latent rows [d_c, d_c + d_r)
+//   kProjOut:  out (N = features)      -> q_out [rows][N] (+ q_out2, the
+//                                         residual, in the same dtype)
 constexpr int kProjGQA = 0;
 constexpr int kProjMLA = 1;
+constexpr int kProjOut = 2;
 
 template <bool ARG, bool XBF16, int MODEL>
 __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
@@ -111,7 +123,15 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
         for (int j = 0; j < kProjChunk; j++)
             wf[j] = __builtin_nontemporal_load((const u32x4 *)(wblk + (int64_t)min(base + j, ks_hi - 1) * 512));
     };
-    auto load_x = [&](u32x4 (&xf)[kProjChunk], int base, int m) {
+    // Activations of row tile m: bf16 as loaded, or f32 split into hi + lo.
+    auto split2 = [](float a, float b) {  // {hi pair, lo pair}
+        const uint16_t ha = bf16_rne(a), hb = bf16_rne(b);
+        const float ra = bf16_f32(ha), rb = bf16_f32(hb);
+        const uint16_t la = (fabsf(ra) < INFINITY) ? bf16_rne(a - ra) : (uint16_t)0;
+        const uint16_t lb = (fabsf(rb) < INFINITY) ? bf16_rne(b - rb) : (uint16_t)0;
+        return u32x2{(uint32_t)ha | ((uint32_t)hb << 16), (uint32_t)la | ((uint32_t)lb << 16)};
+    };
+    auto load_x = [&](u32x4 (&xf)[kProjChunk], u32x4 (&xl)[kProjChunk], int base, int m) {
         const int r = min(m * 16 + col, rows - 1);
 #pragma unroll
         for (int j = 0; j < kProjChunk; j++) {
@@ -121,36 +141,41 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
             } else {
                 const float4 f0 = *(const float4 *)((const float *)x + off);
                 const float4 f1 = *(const float4 *)((const float *)x + off + 4);
-                xf[j][0] = pack_bf16x2(f0.x, f0.y);
-                xf[j][1] = pack_bf16x2(f0.z, f0.w);
-                xf[j][2] = pack_bf16x2(f1.x, f1.y);
-                xf[j][3] = pack_bf16x2(f1.z, f1.w);
+                const u32x2 p0 = split2(f0.x, f0.y), p1 = split2(f0.z, f0.w);
+                const u32x2 p2 = split2(f1.x, f1.y), p3 = split2(f1.z, f1.w);
+                xf[j] = u32x4{p0[0], p1[0], p2[0], p3[0]};
+                xl[j] = u32x4{p0[1], p1[1], p2[1], p3[1]};
             }
         }
     };
-    auto mul = [&](const u32x4 (&wf)[kProjChunk], const u32x4 (&xf)[kProjChunk], int base, int m) {
+    auto mul = [&](const u32x4 (&wf)[kProjChunk], const u32x4 (&xf)[kProjChunk],
+                   const u32x4 (&xl)[kProjChunk], int base, int m) {
 #pragma unroll
         for (int j = 0; j < kProjChunk; j++)
-            if (base + j < ks_hi)
+            if (base + j < ks_hi) {
                 // C[m = row][n = feature]: A = x rows, B = Wp rows.
                 acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xf[j]),
                                                                  __builtin_bit_cast(bf16x8, wf[j]), acc[m], 0, 0, 0);
+                if constexpr (!XBF16)
+                    acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xl[j]),
+                                                                     __builtin_bit_cast(bf16x8, wf[j]), acc[m], 0, 0, 0);
+            }
     };
-    u32x4 wa[kProjChunk], wb[kProjChunk], xf[kProjChunk];
+    u32x4 wa[kProjChunk], wb[kProjChunk], xf[kProjChunk], xl[kProjChunk];
     if (ks_lo < ks_hi) load_w(wa, ks_lo);
     for (int base = ks_lo; base < ks_hi; base += 2 * kProjChunk) {
         // chunk at base in wa; next chunk into wb
         for (int m = 0; m < MT; m++) {
-            load_x(xf, base, m);
+            load_x(xf, xl, base, m);
             if (m == MT - 1 && base + kProjChunk < ks_hi) load_w(wb, base + kProjChunk);
-            mul(wa, xf, base, m);
+            mul(wa, xf, xl, base, m);
         }
         const int b2 = base + kProjChunk;
         if (b2 >= ks_hi) break;
         for (int m = 0; m < MT; m++) {
-            load_x(xf, b2, m);
+            load_x(xf, xl, b2, m);
             if (m == MT - 1 && b2 + kProjChunk < ks_hi) load_w(wa, b2 + kProjChunk);
-            mul(wb, xf, b2, m);
+            mul(wb, xf, xl, b2, m);
         }
     }
     // ---- k-split merge: the other waves hand their sums to wave 0 ----------
@@ -163,6 +188,31 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     __syncthreads();
     if (wave != 0) return;
     const int n = n0 + col;
+    if constexpr (MODEL == kProjOut) {
+        // out[r][n] = x.W (+ residual[r][n]), in q_bf16's dtype.
+        const int N = gridDim.x * 16;
+#pragma unroll
+        for (int m = 0; m < kProjMaxRows / 16; m++) {
+            if (m >= MT) break;
+            fl4 y = acc[m];
+#pragma unroll
+            for (int w = 0; w < kProjWaves - 1; w++) y += red[w][m][lane];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = m * 16 + grp * 4 + i;
+                if (r >= rows) continue;
+                const int64_t o = (int64_t)r * N + n;
+                float v = y[i];
+                if (q_out2)
+                    v += q_bf16 ? bf16_f32(((const uint16_t *)q_out2)[o]) : ((const float *)q_out2)[o];
+                if (q_bf16)
+                    ((uint16_t *)q_out)[o] = bf16_rne(v);
+                else
+                    ((float *)q_out)[o] = v;
+            }
+        }
+        return;
+    }
     // part of the output this work-group's 16 features belong to (uniform),
     // feature index within the part, RoPE head width (0: no rotation)
     int part, nn, hw;
@@ -249,7 +299,9 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
                        int P) {
     if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
-    const int N = model == kProjGQA ? (H + 2 * KVH) * D : H * (D + kMlaDr) + kMlaRow;
+    // kProjOut: N = D (the output features), H and KVH unused.
+    const int N = model == kProjGQA ? (H + 2 * KVH) * D
+                                    : (model == kProjMLA ? H * (D + kMlaDr) + kMlaRow : D);
 #define RLX_PROJ_LAUNCH(ARGV, XB, MODELV, PLANV)                                                  \
     qkv_project_kernel<ARGV, XB, MODELV><<<N / 16, 64 * kProjWaves, 0, s>>>(                      \
         PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x, x_bf16, K, wp, H, KVH, D,  \
@@ -265,8 +317,10 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
         RLX_PROJ_LAUNCH(false, false, MODELV, NoPlan{0});
     if (model == kProjGQA) {
         RLX_PROJ_MODEL(kProjGQA)
-    } else {
+    } else if (model == kProjMLA) {
         RLX_PROJ_MODEL(kProjMLA)
+    } else {
+        RLX_PROJ_MODEL(kProjOut)
     }
 #undef RLX_PROJ_MODEL
 #undef RLX_PROJ_LAUNCH

@@ -706,6 +706,49 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
     return RLX_OK;
 }
 
+int32_t rlx_pack_out(const void *w, int32_t w_dtype, int32_t k_in, int32_t n_out, void *out) {
+    if (!w || !out) return fail(RLX_ERR_INVALID, "null weight pointer");
+    if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
+    if (k_in <= 0 || n_out <= 0) return fail(RLX_ERR_INVALID, "k_in and n_out must be > 0");
+    if (k_in % 32 != 0 || n_out % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_pack_out: k_in %% 32 and n_out %% 16 must be 0 (k_in=%d n_out=%d)",
+                    k_in, n_out);
+    const void *mats[1] = {w};
+    const int wd[1] = {n_out};
+    HIP_TRY(launch_pack_proj(nullptr, 1, mats, wd, w_dtype == RLX_BF16, k_in, (uint16_t *)out));
+    return RLX_OK;
+}
+
+int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, int32_t k_in,
+                        const void *w_packed, int32_t n_out, const void *residual, void *out,
+                        int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (rows < 0 || k_in <= 0 || n_out <= 0) return fail(RLX_ERR_INVALID, "rlx_out_project: rows/k_in/n_out");
+    if (rows == 0) return RLX_OK;
+    if (!x || !w_packed || !out) return fail(RLX_ERR_INVALID, "rlx_out_project: null pointer");
+    if ((x_dtype != RLX_F32 && x_dtype != RLX_BF16) || (out_dtype != RLX_F32 && out_dtype != RLX_BF16))
+        return fail(RLX_ERR_INVALID, "rlx_out_project: dtype");
+    if (k_in % 32 != 0 || n_out % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_out_project: k_in %% 32 and n_out %% 16 must be 0");
+    const size_t xb = x_dtype == RLX_BF16 ? 2 : 4, ob = out_dtype == RLX_BF16 ? 2 : 4;
+    int32_t rc;
+    for (int r0 = 0; r0 < rows; r0 += kProjRows) {
+        const int n = std::min(kProjRows, rows - r0);
+        hipEvent_t e0, e1;
+        if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
+        if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
+        HIP_TRY(launch_proj(c->stream, kProjModelOut, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, n,
+                            (const char *)x + (size_t)r0 * k_in * xb, x_dtype == RLX_BF16, k_in,
+                            (const uint16_t *)w_packed, 0, 0, n_out, nullptr, nullptr,
+                            (char *)out + (size_t)r0 * n_out * ob,
+                            residual ? (void *)((const char *)residual + (size_t)r0 * n_out * ob) : nullptr,
+                            out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0));
+        if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    }
+    return RLX_OK;
+}
+
 int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
                           int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,
                           void *out) {

@@ -144,6 +144,23 @@ class _PagedCache:
         check(self._lib.rlx_free_list(self._h, layer, buf, n.value, ctypes.byref(n)))
         return list(buf)[: n.value]
 
+    def OutProject(self, x, w_packed, n_out, residual=None, out=None, out_dtype=None):
+        """The step after attention on this cache's stream: out = x . W
+        (+ residual) -- the output projection (mha.go:356-360, mla.go:384-389)
+        and the block's residual add.  x [rows][k_in] f32 or bf16 (device),
+        w_packed from pack_out, residual None or [rows][n_out] in out's dtype."""
+        rows, k_in = x.shape[0], x.shape[-1]
+        if out is None:
+            dt = out_dtype or (residual.dtype if residual is not None else torch.float32)
+            out = torch.empty((rows, n_out), dtype=dt, device=x.device)
+        if residual is not None and (residual.dtype != out.dtype or residual.shape[-1] != n_out):
+            raise ValueError("residual must be [rows][n_out] in the output dtype")
+        check(self._lib.rlx_out_project(self._h, rows, _dev(x, "x"), _dtype_code(x), k_in,
+                                        _dev(w_packed, "w_packed"), n_out,
+                                        _dev(residual, "residual") if residual is not None else None,
+                                        _dev(out, "out"), _dtype_code(out)))
+        return out
+
     def _lens(self, layer_idx, seq_ids):
         return [self.TotalLen(layer_idx, s) for s in seq_ids]
 
@@ -279,6 +296,16 @@ def pack_qkv(w_q, w_k, w_v, num_heads, kv_heads, head_dim):
     check(_lib.load().rlx_pack_qkv(_dev(w_q, "w_q"), _dev(w_k, "w_k"), _dev(w_v, "w_v"),
                                    _dtype_code(w_q), d_model, num_heads, kv_heads, head_dim,
                                    _dev(out, "out")))
+    return out
+
+
+def pack_out(w, k_in=None, n_out=None):
+    """W [k_in][n_out] (bf16 or f32, device; e.g. W_O [H*D][d_model]) ->
+    packed bf16 weights for OutProject (rlx_pack_out)."""
+    k_in = k_in or w.shape[0]
+    n_out = n_out or w.shape[1]
+    out = torch.empty((n_out, k_in), dtype=torch.bfloat16, device=w.device)
+    check(_lib.load().rlx_pack_out(_dev(w, "w"), _dtype_code(w), k_in, n_out, _dev(out, "out")))
     return out
 
 
