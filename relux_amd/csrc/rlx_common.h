@@ -278,6 +278,26 @@ hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
 constexpr int kSrcPaged = 0;
 constexpr int kSrcDense = 1;
 
+// Max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48),
+// delivered to every lane, with gfx950's row swaps: v_permlane16_swap
+// exchanges the odd rows of its first operand with the even rows of its
+// second, v_permlane32_swap the upper half of the first with the lower half
+// of the second.  Swapping a value with itself pairs each row with its
+// neighbour, then each half with the other -- VALU lane exchanges with no
+// LDS round trip.  The sum is (x0 + x1) + (x2 + x3) in every lane.
+__device__ __forceinline__ float rows4_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Two floats to packed bf16 with the hardware conversion (v_cvt_pk_bf16_f32,
 // round to nearest even): the same bits as bf16_rne for every non-NaN
 // input.  For attention weights only; cache bytes keep bf16_rne, whose NaN
@@ -310,6 +330,17 @@ __device__ __forceinline__ void lds_dma16(const void *gptr, uint32_t lds_base) {
         "global_load_lds_dwordx4 %0, off nt"
         :
         : "v"(gptr), "s"(lds_base)
+        : "memory", "m0");
+}
+// The same load addressed as a wave-uniform base (SGPR pair) plus a 32-bit
+// per-lane byte offset: no 64-bit address arithmetic per lane.
+__device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1 nt"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds_base)
         : "memory", "m0");
 }
 

@@ -23,16 +23,6 @@
 
 namespace rlx {
 
-__device__ __forceinline__ float wave_max16(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-__device__ __forceinline__ float wave_sum16(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
 
 // Last key (inclusive, live index) query qi of a sequence may attend.
 __device__ __forceinline__ int key_limit(int mask_mode, int len, int nq, int qi) {
@@ -196,7 +186,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 2) void gqa_decode_kernel(
                     if (t0 + grp * 4 + i > klim[nt]) s[i] = -INFINITY;
             }
             float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-            mx = wave_max16(mx);
+            mx = rows4_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             float c, p[4];
             if (m_new == -INFINITY) {
@@ -263,7 +253,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 2) void gqa_decode_kernel(
     __shared__ fl4 so[3][NQT][MT][64];
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++) {
-        const float lt = wave_sum16(l_part[nt]);
+        const float lt = rows4_sum(l_part[nt]);
         if (grp == 0) {
             sm[wave][nt * 16 + col] = m_run[nt];
             sl[wave][nt * 16 + col] = lt;

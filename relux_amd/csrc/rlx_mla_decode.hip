@@ -9,28 +9,19 @@
 //   o[h]     = W_UV[:,h]^T o_lat[h]         (once per query)
 // which reads each cached row once instead of expanding it H*D*2 times.
 //
-// Work item = (sequence, context split); one 256-thread work-group (4 waves).
-// A 16-token tile of cache rows (16 x 1152 B) is staged in LDS (double
-// buffered from registers).  Scores: the 36 k-steps of S^T[16 tok][16 rows]
-// are split 9 per wave (MFMA 16x16x16, A = tile rows read from LDS) and the
-// four partial S^T are summed in LDS.  Every wave then runs the same online
-// softmax; wave w owns latent channels [128w, 128w+128) of
-// O^T[512][16 rows] += C^T . P^T (MFMA 16x16x16, A = tile columns read
-// transposed from LDS, B = P^T straight from the score registers).
+// Work item = (sequence, context split); one work-group of NW waves.
+// 16-token tiles of cache rows (16 x 1152 B) stream from HBM straight into
+// an LDS ring (global_load_lds).  Scores: the 18 k-steps of S^T[16 tok][16 rows] are split over the waves
+// (MFMA 16x16x32, A = tile rows read from LDS) and the partial S^T are
+// summed in LDS, one tile ahead of their use.  Every wave then runs the same
+// online softmax; wave w owns latent channels [w*CH, (w+1)*CH), CH =
+// 512 / NW, of O^T[512][16 rows] += C^T . P^T (MFMA 16x16x16, A = tile
+// columns read transposed from LDS, B = P^T straight from the softmax
+// registers).
 #include "rlx_common.h"
 
 namespace rlx {
 
-__device__ __forceinline__ float mla_max16(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-__device__ __forceinline__ float mla_sum16(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
 __device__ __forceinline__ int mla_key_limit(int mask_mode, int len, int nq, int qi) {
     if (mask_mode == kMaskCausal) return len - nq + qi;
     if (mask_mode == kMaskRef) return (nq == len) ? qi : len - 1;
@@ -133,17 +124,32 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
 // = 4 rows x one 32-B chunk pair) see 4 distinct chunk pairs.
 __device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
+// Shape per query-row tile count: 4 waves and two work-groups per CU (80 KB
+// of LDS each); a 4-stage ring for up to 16 query rows, 3 stages for 32.
+template <int NQT> struct MlaShape {
+    static constexpr int NW = 4;                      // waves
+    static constexpr int S = NQT == 1 ? 4 : 3;        // LDS ring stages
+    static constexpr int WGS = 2;                     // resident work-groups per CU
+    static constexpr int LOADS = 16 * kMlaRow / 8 / 64;  // 64-lane loads per tile (18)
+    static constexpr int CH = kMlaDc / NW;            // latent channels per wave
+};
+
 template <int NQT, bool ARG>
-__global__ __launch_bounds__(256, 2) void mla_decode_kernel(
+__global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void mla_decode_kernel(
     typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ pool,
     const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
     const int2 *__restrict__ work, int n_rows, const uint16_t *__restrict__ qlat, int H, int P,
     int chunk, int mask_mode, float *__restrict__ part_o, float *__restrict__ part_ml) {
+    using SH = MlaShape<NQT>;
+    constexpr int NW = SH::NW, S = SH::S, CH = SH::CH, MT = CH / 16;
     constexpr int QRP = 16 * NQT;
-    constexpr int S = (NQT == 1) ? 4 : 3;  // LDS ring stages (2 work-groups per CU)
-    constexpr int TILE = 16 * kMlaRow;     // bf16 per stage
+    constexpr int TILE = 16 * kMlaRow;  // bf16 per stage
+    // Tile loads per wave: the 18 64-lane loads of a tile go round-robin to
+    // the waves, so the first 18 % NW waves issue one more.
+    constexpr int LB = SH::LOADS / NW + 1, LS = SH::LOADS / NW;
+    constexpr int KB = 18 / NW + 1, KSM = 18 / NW;  // score k-steps per wave
     __shared__ __attribute__((aligned(16))) uint16_t ring[S * TILE];
-    __shared__ fl4 spart[4][NQT][64];
+    __shared__ fl4 spart[2][NW][NQT][64];  // [tile parity][wave] partial scores
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -159,72 +165,107 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)ring;
 
     float m_run[NQT], l_part[NQT];
-    fl4 acc[NQT][8];
+    fl4 acc[NQT][MT];
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++) {
         m_run[nt] = -INFINITY;
         l_part[nt] = 0.f;
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
     }
 
     // Tile j (16 tokens) streams straight from HBM into ring stage j % S
     // (global_load_lds, 16 B per lane, non-temporal).  One instruction fills
-    // 64 consecutive physical chunks: waves 0-1 issue 5 per tile, waves 2-3
-    // issue 4 (1152 chunks).  Rows past the live length re-read the last
-    // live row, so every staged value is a finite cache value and masked
-    // tokens contribute exact zeros.
-    auto issue_tile = [&](int j) {
-        const int t0 = t_begin + 16 * j;
-        const int page = table[R.tab + t0 / P];
-        const int slot0 = t0 % P;
-        const uint16_t *src = pool + (int64_t)page * P * kMlaRow;
-        const uint32_t dst = ring_lds + (uint32_t)((j % S) * TILE * 2);
+    // 64 consecutive physical chunks; load i of the tile's 18 (1152 chunks)
+    // is issued by wave i % NW.  A lane's chunk (row, swizzled column) is
+    // the same in every tile, so its byte offset is computed once; rows past
+    // the live length (last tile only) re-read the last live row, so every
+    // staged value is a finite cache value and masked tokens contribute
+    // exact zeros.  The page of tile j0 + l is fetched by lane l, 64 tiles at
+    // a time, and read back with readlane: no table load in the loop.
+    int lrow[LB], lcol[LB];
+    uint32_t loff[LB];
 #pragma unroll
-        for (int k = 0; k < 5; k++) {
-            if (k == 4 && wave >= 2) break;
-            const int base = 256 * k + 64 * wave;  // first physical chunk (wave-uniform)
-            const int pch = base + lane;
-            const int r = pch / 72;
-            const int lc = (pch - r * 72) ^ mla_swz(r);
-            const int tok = min(t0 + r, R.len - 1);
-            const uint16_t *g = src + (int64_t)(slot0 + tok - t0) * kMlaRow + lc * 8;
-            lds_dma16(g, __builtin_amdgcn_readfirstlane(dst + (uint32_t)base * 16));
+    for (int k = 0; k < LB; k++) {
+        const int pch = 64 * (NW * k + wave) + lane;
+        const int r = min(pch / 72, 15);  // (waves that skip load k never use it)
+        lrow[k] = r;
+        lcol[k] = ((pch - (pch / 72) * 72) ^ mla_swz(r)) * 8;
+        loff[k] = (uint32_t)(r * kMlaRow + lcol[k]) * 2;
+    }
+    const uint32_t ring0 = __builtin_amdgcn_readfirstlane(ring_lds);
+    auto fetch_pages = [&](int j0) {
+        const int j = j0 + lane;
+        return (j < ntiles) ? table[R.tab + (t_begin + 16 * j) / P] : 0;
+    };
+    int pg = fetch_pages(0);
+    auto issue_tile = [&](int j) {
+        if ((j & 63) == 0 && j > 0) {
+            pg = fetch_pages(j);
+            asm volatile("" ::"v"(pg));  // wait for the refill here (rare)
+        }
+        const int t0 = t_begin + 16 * j;
+        const int page = __builtin_amdgcn_readlane(pg, j & 63);
+        const uint16_t *src = pool + ((int64_t)page * P + t0 % P) * kMlaRow;
+        const uint32_t dst = ring0 + (uint32_t)((j % S) * TILE * 2);
+        const int lim = R.len - 1 - t0;  // last live row of the tile
+        if (lim >= 15) {
+#pragma unroll
+            for (int k = 0; k < LB; k++) {
+                if (k == LS && wave >= SH::LOADS % NW) break;
+                lds_dma16(src, loff[k], __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < LB; k++) {
+                if (k == LS && wave >= SH::LOADS % NW) break;
+                const uint32_t off = (uint32_t)(min(lrow[k], lim) * kMlaRow + lcol[k]) * 2;
+                lds_dma16(src, off, __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+            }
         }
     };
     // Wait until this wave's loads of the awaited tile landed, given how many
     // tiles it issued after that one (loads retire in issue order).
     auto wait_tile = [&](int ahead) {
-        if (ahead >= 2) {
-            if (wave < 2) RLX_WAIT_VM(10); else RLX_WAIT_VM(8);
-        } else if (ahead == 1) {
-            if (wave < 2) RLX_WAIT_VM(5); else RLX_WAIT_VM(4);
-        } else {
-            RLX_WAIT_VM(0);
+        const bool big = wave < SH::LOADS % NW;
+        switch (ahead) {
+#define RLX_MLA_WAIT(A)                                        \
+    case A:                                                    \
+        if (big) RLX_WAIT_VM(A * LB); else RLX_WAIT_VM(A * LS); \
+        break;
+            RLX_MLA_WAIT(1)
+            RLX_MLA_WAIT(2)
+            RLX_MLA_WAIT(3)
+            RLX_MLA_WAIT(4)
+            RLX_MLA_WAIT(5)
+#undef RLX_MLA_WAIT
+            default: RLX_WAIT_VM(0); break;
         }
     };
+    static_assert(S - 3 <= 5, "wait_tile covers at most 5 tiles ahead");
 
     for (int j = 0; j < S - 1 && j < ntiles; j++) issue_tile(j);
 
     // Score k-steps (MFMA 16x16x32, 32 channels each): 18 per tile, split
-    // 5/5/4/4 over the waves.  B operand = q_lat^T, 8 channels per lane.
-    const int ks0 = wave < 2 ? 5 * wave : 2 + 4 * wave;
-    const int nks = wave < 2 ? 5 : 4;
-    u32x4 qb[NQT][5];
+    // over the waves (5/5/4/4 or 3/3/2/2/2/2/2/2).  B operand = q_lat^T, 8
+    // channels per lane.
+    const int ks0 = wave * KSM + min(wave, 18 % NW);
+    const int nks = wave < 18 % NW ? KB : KSM;
+    u32x4 qb[NQT][KB];
     int klim[NQT];
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++) {
         const int qr = nt * 16 + col;
         klim[nt] = R.len - 1;
 #pragma unroll
-        for (int kk = 0; kk < 5; kk++) qb[nt][kk] = u32x4{0, 0, 0, 0};
+        for (int kk = 0; kk < KB; kk++) qb[nt][kk] = u32x4{0, 0, 0, 0};
         if (qr < QR) {
             const int qi = qr / H;
             const int h = qr - qi * H;
             klim[nt] = mla_key_limit(mask_mode, R.len, R.nq, qi);
             const uint16_t *qp = qlat + ((int64_t)(R.qrow + qi) * H + h) * kMlaRow + grp * 8;
 #pragma unroll
-            for (int kk = 0; kk < 5; kk++)
+            for (int kk = 0; kk < KB; kk++)
                 if (kk < nks) qb[nt][kk] = *(const u32x4 *)(qp + (ks0 + kk) * 32);
         }
     }
@@ -235,49 +276,97 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++)
 #pragma unroll
-        for (int kk = 0; kk < 5; kk++) asm volatile("" ::"v"(qb[nt][kk]));
+        for (int kk = 0; kk < KB; kk++) asm volatile("" ::"v"(qb[nt][kk]));
 
+    // Partial scores of tile j over this wave's k-steps: A operands read from
+    // ring stage j % S, products into sc[nt].
+    const int sw = mla_swz(col);
+    auto score_reads = [&](int j, u32x4(&a)[KB]) {
+        const uint16_t *trow = ring + (j % S) * TILE + col * kMlaRow;
+#pragma unroll
+        for (int kk = 0; kk < KB; kk++) {
+            const int kc = kk < nks ? kk : nks - 1;  // (a wave with fewer k-steps re-reads its last)
+            a[kk] = *(const u32x4 *)(trow + ((((ks0 + kc) * 4 + grp) ^ sw) << 3));
+        }
+    };
+    auto score_mfma = [&](const u32x4(&a)[KB], fl4(&sc)[NQT]) {
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++) {
+            sc[nt] = fl4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KB; kk++)
+                if (kk < nks)
+                    sc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[kk]),
+                                                                     __builtin_bit_cast(bf16x8, qb[nt][kk]), sc[nt], 0, 0, 0);
+        }
+    };
+    // P.V operand: 4 consecutive tokens of one channel per lane, from the
+    // row-major tile with the LDS transpose read (lane (g, j) fetches 4
+    // channels of row 4g + j/4 and the 16-lane group exchanges them so that
+    // lane j ends up with channel j of rows 4g..4g+3).
+    const int trr = 4 * grp + (col >> 2);
+    const int tsw = mla_swz(trr);
+    const int tr_off = trr * kMlaRow + (col & 1) * 4;
+
+    // Software pipeline, one barrier per tile: iteration j scores tile j + 1
+    // while it runs the softmax and P.V of tile j (whose partial scores were
+    // written in iteration j - 1).  The barrier at the top of iteration j
+    // publishes tile j + 1 and spart[j & 1], and retires iteration j - 1's
+    // reads of ring stage (j - 1) % S (refilled here with tile j + S - 1) and
+    // of spart[(j + 1) & 1] (rewritten here).  Ring stages in use: tile j
+    // (P.V), tile j + 1 (scores), tiles j + 2 .. j + S - 1 (in flight).
+    // Every LDS read of an iteration is issued before its first use, so one
+    // wait covers the partial scores, the next tile's score operands and the
+    // P.V operands.
+    if (ntiles > 0) {
+        wait_tile(min(S - 2, ntiles - 1));
+        ring_barrier();
+        u32x4 a0[KB];
+        fl4 sc0[NQT];
+        score_reads(0, a0);
+        score_mfma(a0, sc0);
+#pragma unroll
+        for (int nt = 0; nt < NQT; nt++) spart[0][wave][nt][lane] = sc0[nt];
+    }
     for (int j = 0; j < ntiles; j++) {
-        wait_tile(min(S - 2, ntiles - 1 - j));
-        // Tile j is visible to every wave, and stage (j-1) % S is no longer read.
+        const bool more = j + 1 < ntiles;
+        if (more) wait_tile(min(S - 3, ntiles - 2 - j));
         ring_barrier();
         if (j + S - 1 < ntiles) issue_tile(j + S - 1);
         const int t0 = t_begin + 16 * j;
         const uint16_t *T = ring + (j % S) * TILE;
-
-        // Partial scores over this wave's k-steps.
-        const uint16_t *trow = T + col * kMlaRow;
-        const int sw = mla_swz(col);
+        fl4 sp[NW][NQT];
 #pragma unroll
-        for (int nt = 0; nt < NQT; nt++) {
-            fl4 s = fl4{0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < NW; w++)
 #pragma unroll
-            for (int kk = 0; kk < 5; kk++) {
-                if (kk < nks) {
-                    const int lc = (ks0 + kk) * 4 + grp;
-                    const u32x4 a = *(const u32x4 *)(trow + ((lc ^ sw) << 3));
-                    s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                                __builtin_bit_cast(bf16x8, qb[nt][kk]), s, 0, 0, 0);
-                }
-            }
-            spart[wave][nt][lane] = s;
+            for (int nt = 0; nt < NQT; nt++) sp[w][nt] = spart[j & 1][w][nt][lane];
+        // (On the last tile stage (j + 1) % S holds a consumed tile and no
+        // load in flight: reading it is harmless and its scores are dropped.)
+        u32x4 an[KB];
+        score_reads(j + 1, an);
+        sh4 av[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int lc = (wave * CH + mt * 16) / 8 + ((col >> 1) & 1);
+            av[mt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) sh4 *)(T + tr_off + ((lc ^ tsw) << 3)));
         }
-        ring_barrier();
+        fl4 sn[NQT];
+        score_mfma(an, sn);
         sh4 pb[NQT];
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
-            fl4 s = spart[0][nt][lane];
-            s += spart[1][nt][lane];
-            s += spart[2][nt][lane];
-            s += spart[3][nt][lane];
+            fl4 sc = sp[0][nt];
+#pragma unroll
+            for (int w = 1; w < NW; w++) sc += sp[w][nt];
             float mx = -INFINITY;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int t = t0 + grp * 4 + i;
-                s[i] = (t <= klim[nt]) ? s[i] : -INFINITY;
-                mx = fmaxf(mx, s[i]);
+                sc[i] = (t <= klim[nt]) ? sc[i] : -INFINITY;
+                mx = fmaxf(mx, sc[i]);
             }
-            mx = mla_max16(mx);
+            mx = rows4_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             float c, p[4];
             if (m_new == -INFINITY) {
@@ -286,47 +375,40 @@ __global__ __launch_bounds__(256, 2) void mla_decode_kernel(
             } else {
                 c = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
 #pragma unroll
-                for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(s[i] - m_new);
+                for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
             }
             // The P.V product consumes bf16 weights: normalise by the same ones.
-#pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = bf16_f32(bf16_rne(p[i]));
-            l_part[nt] = l_part[nt] * c + ((p[0] + p[1]) + (p[2] + p[3]));
-            m_run[nt] = m_new;
-#pragma unroll
-            for (int mt = 0; mt < 8; mt++) acc[nt][mt] *= c;
             u32x2 pw;
-            pw[0] = (uint32_t)bf16_rne(p[0]) | ((uint32_t)bf16_rne(p[1]) << 16);
-            pw[1] = (uint32_t)bf16_rne(p[2]) | ((uint32_t)bf16_rne(p[3]) << 16);
+            pw[0] = pack_bf16x2(p[0], p[1]);
+            pw[1] = pack_bf16x2(p[2], p[3]);
+            l_part[nt] = l_part[nt] * c + ((bf16_lo(pw[0]) + bf16_hi(pw[0])) + (bf16_lo(pw[1]) + bf16_hi(pw[1])));
+            m_run[nt] = m_new;
+            if (__builtin_amdgcn_ballot_w64(c != 1.f)) {  // some head's max moved
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) acc[nt][mt] *= c;
+            }
             pb[nt] = __builtin_bit_cast(sh4, pw);
         }
-        // O^T += C^T . P^T over this wave's 128 latent channels.  The A operand
-        // (4 consecutive tokens of one channel per lane) comes from the
-        // row-major tile with the LDS transpose read: lane (g, j) fetches 4
-        // channels of row 4g + j/4 and the 16-lane group exchanges them so
-        // that lane j ends up with channel j of rows 4g..4g+3.
-        const int trr = 4 * grp + (col >> 2);
-        const uint16_t *tr = T + trr * kMlaRow + (col & 1) * 4;
-        const int tsw = mla_swz(trr);
+        if (more) {
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++) {
-            const int lc = (wave * 128 + mt * 16) / 8 + ((col >> 1) & 1);
-            const sh4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) sh4 *)(tr + ((lc ^ tsw) << 3)));
+            for (int nt = 0; nt < NQT; nt++) spart[(j + 1) & 1][wave][nt][lane] = sn[nt];
+        }
+        // O^T += C^T . P^T over this wave's CH latent channels.
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int nt = 0; nt < NQT; nt++)
-                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[nt], acc[nt][mt], 0, 0, 0);
-        }
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av[mt], pb[nt], acc[nt][mt], 0, 0, 0);
     }
 
     const int pidx = R.part + wk.y;
 #pragma unroll
     for (int nt = 0; nt < NQT; nt++) {
         const int qr = nt * 16 + col;
-        const float lt = mla_sum16(l_part[nt]);
-        float *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * 128;
+        const float lt = rows4_sum(l_part[nt]);
+        float *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * CH;
 #pragma unroll
-        for (int mt = 0; mt < 8; mt++) *(fl4 *)(po + mt * 16 + grp * 4) = acc[nt][mt];
+        for (int mt = 0; mt < MT; mt++) __builtin_nontemporal_store(acc[nt][mt], (fl4 *)(po + mt * 16 + grp * 4));
         if (wave == 0 && grp == 0) {
             float *pm = part_ml + ((int64_t)pidx * QRP + qr) * 2;
             pm[0] = m_run[nt];
@@ -468,7 +550,7 @@ static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uin
                          const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
                          int n_work, const uint16_t *qlat, int H, int P, int chunk, int mask_mode,
                          float *part_o, float *part_ml) {
-    mla_decode_kernel<NQT, ARG><<<n_work, 256, 0, s>>>(plan, pool, table, rows, work, n_rows, qlat,
+    mla_decode_kernel<NQT, ARG><<<n_work, 64 * MlaShape<NQT>::NW, 0, s>>>(plan, pool, table, rows, work, n_rows, qlat,
                                                         H, P, chunk, mask_mode, part_o, part_ml);
 }
 
@@ -525,8 +607,8 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
 int mla_decode_wgs_per_cu(int nqt) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
-    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1, true>, 256, 0);
-    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2, true>, 256, 0);
+    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1, true>, 64 * MlaShape<1>::NW, 0);
+    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2, true>, 64 * MlaShape<2>::NW, 0);
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 

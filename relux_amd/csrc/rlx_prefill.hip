@@ -36,16 +36,6 @@ constexpr int kWaves = 8;                // 512 threads, 32 query rows per wave
 constexpr int kTileRows = 32 * kWaves;   // 256
 constexpr int kKeyBlock = 32;
 
-__device__ __forceinline__ float pf_max16(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
-}
-__device__ __forceinline__ float pf_sum16(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
 __device__ __forceinline__ int pf_limit(int mask_mode, int len, int nq, int qi) {
     if (mask_mode == kMaskCausal) return len - nq + qi;
     if (mask_mode == kMaskRef) return (nq == len) ? qi : len - 1;
@@ -378,7 +368,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             }
 #pragma unroll
             for (int i = 0; i < 8; i++) mx = fmaxf(mx, p[i]);
-            mx = pf_max16(mx);
+            mx = rows4_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
             float c = 1.f;
             if (m_new == -INFINITY) {
@@ -413,7 +403,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     // ---- normalise and write ----------------------------------------------
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
-        const float lt = pf_sum16(l_part[nt]);
+        const float lt = rows4_sum(l_part[nt]);
         if (!rvalid[nt]) continue;
         const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
         const int j = rtok[nt], h = rhead[nt];
