@@ -375,7 +375,7 @@ hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, 
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, const int2 *work, int n_work, const uint16_t *w_uk,
                              const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
-                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt);
+                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt, int cus);
 
 // Fused projection + RoPE + paged append (at most 64 rows per launch).
 constexpr int kProjRows = 64;

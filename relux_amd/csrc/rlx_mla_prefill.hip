@@ -9,13 +9,13 @@
 //
 // C rows come straight from the paged latent pool.  MFMA needs the contracted
 // index (c) contiguous per lane in both operands, so W is first transposed to
-// W^T[h*D+d][c].  GEMM tile: 128 tokens x 128 features per 256-thread
-// work-group, 32-wide c steps staged in LDS (double buffered), each wave a
-// 64 x 64 block of 4 x 4 MFMA 16x16x32 tiles.  The K_c launch puts features
-// on the MFMA M side (a lane ends with 4 consecutive dims of one token: one
-// 8-byte store into the row-major K_c); the V^T launch puts tokens there (4
-// consecutive tokens of one dim: one 8-byte store into the dim-major V^T).
+// W^T[h*D+d][c].  The K_c launch puts features on the MFMA M side (a lane
+// ends with consecutive dims of one token: row-major K_c); the V^T launch
+// puts tokens there (consecutive tokens of one dim: dim-major V^T).  The
+// GEMM itself is mla_expand_kernel below.
 #include "rlx_common.h"
+
+#include <algorithm>
 
 namespace rlx {
 
@@ -36,52 +36,117 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t *__r
     }
 }
 
-constexpr int kDT = 128;  // tokens per tile
-constexpr int kDF = 128;  // features per tile
-constexpr int kDK = 32;   // c per step
-constexpr int kDP = kDK + 8;  // LDS row pitch (bf16)
+// Expansion GEMM, persistent: one 8-wave work-group per CU walks the tiles
+// blockIdx.x, blockIdx.x + gridDim.x, ...  A tile is 256 features (W^T rows)
+// x 128 tokens (latent rows), c in 8 ring stages of 64; the ring runs on
+// across tile boundaries, so only the first tile of a work-group waits for
+// memory.  Stage = A [256][64] + B [128][64] bf16 (48 KB), 3 stages, filled
+// by global_load_lds (6 per wave per stage); chunk c of an LDS row r sits at
+// physical chunk c ^ (r & 7), which keeps the MFMA fragment reads
+// conflict-free.  Wave (wf, wt) = (wave & 3, wave >> 2) owns features
+// [64 wf, 64 wf + 64) x tokens [64 wt, 64 wt + 64): 4 x 4 MFMA 16x16x32
+// tiles, two k-steps per stage.  Tile t = (work item t / n_mt, feature tile
+// t % n_mt): with gridDim.x a multiple of n_mt a work-group keeps one
+// feature tile, and the work-groups of one XCD (b mod 8) share a few, which
+// stay in that XCD's L2 while the token tiles stream past.  (The output,
+// 1 GB per launch on config 4, costs about as much as the GEMM itself: 0.42
+// ms without the stores against 0.73-0.87 ms with them.)
+constexpr int kXM = 256;               // features per tile
+constexpr int kXN = 128;               // tokens per tile
+constexpr int kXK = 64;                // c per stage
+constexpr int kXS = 3;                 // ring stages
+constexpr int kXSteps = kMlaDc / kXK;  // stages per tile
+constexpr int kXStage = (kXM + kXN) * kXK;  // bf16 per stage
+constexpr int kXLoadsA = kXM * kXK / 8 / 64 / 8;  // 64-lane A loads per wave per stage (4)
+constexpr int kXLoadsB = kXN * kXK / 8 / 64 / 8;  // B loads (2)
+constexpr int kXLoads = kXLoadsA + kXLoadsB;
 
-// work[i] = (call row, first token of the tile).  out_kind 0: K_c, 1: V^T.
 template <int OUT_V>
-__global__ __launch_bounds__(256) void mla_decompress_kernel(
+__global__ __launch_bounds__(512, 1) void mla_expand_kernel(
     const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
-    const AttRow *__restrict__ rows, const int2 *__restrict__ work,
-    const uint16_t *__restrict__ wt, int H, int P, uint16_t *__restrict__ dst) {
-    __shared__ uint16_t As[2][kDT * kDP];  // latent rows [token][c]
-    __shared__ uint16_t Bs[2][kDF * kDP];  // W^T rows [feature][c]
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const AttRow *__restrict__ rows, const int2 *__restrict__ work, int n_work,
+    const uint16_t *__restrict__ wt, int N, int H, int P, uint16_t *__restrict__ dst) {
+    __shared__ __attribute__((aligned(16))) uint16_t ring[kXS * kXStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar registers)
     const int col = lane & 15, grp = lane >> 4;
-    const int2 wk = work[blockIdx.x];
-    const AttRow R = rows[wk.x];
-    const int t0 = wk.y;
-    const int f0 = blockIdx.y * kDF;
-    const int wt_m = (wave >> 1) * 64;  // this wave's 64 x 64 block
-    const int wt_n = (wave & 1) * 64;
+    const int wf = wave & 3, wtk = wave >> 2;
+    const int n_mt = (N + kXM - 1) / kXM;
+    const int n_tiles = n_mt * n_work;
+    const int my_tiles = (n_tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int G = my_tiles * kXSteps;  // ring stages this work-group runs
+    const uint32_t ring0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)ring);
 
-    u32x4 ra[2], rb[2];
-    auto load = [&](int c0) {
+    // Per-lane load geometry (the same in every stage): load i of this wave
+    // fills 64 consecutive physical chunks of the stage.
+    uint32_t a_off[kXLoadsA];  // byte offset of this lane's W^T chunk in a feature tile
+    int a_row[kXLoadsA];
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int c = tid + 256 * u;  // 512 chunks: row = c / 4, part = c % 4
-            const int r = c >> 2, part = c & 3;
-            const int t = t0 + r;
-            ra[u] = u32x4{0, 0, 0, 0};
-            if (t < R.len) {
-                const int page = table[R.tab + t / P];
-                ra[u] = *(const u32x4 *)(pool + ((int64_t)page * P + t % P) * kMlaRow + c0 + part * 8);
+    for (int i = 0; i < kXLoadsA; i++) {
+        const int q = (wave * kXLoadsA + i) * 64 + lane;
+        const int r = q >> 3, c = (q & 7) ^ (r & 7);
+        a_row[i] = r;
+        a_off[i] = (uint32_t)(r * kMlaDc + c * 8) * 2;
+    }
+    int b_row[kXLoadsB], b_chunk[kXLoadsB];
+#pragma unroll
+    for (int i = 0; i < kXLoadsB; i++) {
+        const int q = (wave * kXLoadsB + i) * 64 + lane;
+        const int r = q >> 3;
+        b_row[i] = r;
+        b_chunk[i] = (q & 7) ^ (r & 7);
+    }
+
+    // Issue side: state of the tile whose stages are being loaded.
+    const uint16_t *b_ptr[kXLoadsB];
+    const uint16_t *a_base = wt;
+    int a_lim = kXM - 1;  // last live feature row of the tile
+    auto issue_tile_setup = [&](int ti) {
+        const int t = (int)blockIdx.x + ti * (int)gridDim.x;
+        const int m = t % n_mt;
+        const int2 wk = work[t / n_mt];
+        const AttRow R = rows[wk.x];
+        a_base = wt + (int64_t)m * kXM * kMlaDc;
+        a_lim = min(kXM, N - m * kXM) - 1;
+        // Pages of the tile's 128 tokens (at most 9: P is a multiple of 16),
+        // read as wave-uniform scalars and selected per lane.
+        const int t_hi = min(wk.y + kXN, R.len) - 1;
+        const int p_lo = wk.y / P, p_hi = t_hi / P;
+        int pg[9];
+#pragma unroll
+        for (int k = 0; k < 9; k++) pg[k] = table[R.tab + min(p_lo + k, p_hi)];
+#pragma unroll
+        for (int i = 0; i < kXLoadsB; i++) {
+            const int tok = min(wk.y + b_row[i], t_hi);
+            const int k = tok / P - p_lo;
+            int page = pg[0];
+#pragma unroll
+            for (int kk = 1; kk < 9; kk++) page = (k == kk) ? pg[kk] : page;
+            b_ptr[i] = pool + ((int64_t)page * P + tok % P) * kMlaRow + b_chunk[i] * 8;
+        }
+    };
+    auto issue = [&](int g) {
+        if (g % kXSteps == 0) issue_tile_setup(g / kXSteps);
+        const int c0 = (g % kXSteps) * kXK;
+        const uint32_t st = ring0 + (uint32_t)((g % kXS) * kXStage * 2);
+        const uint16_t *ab = a_base + c0;
+        if (a_lim == kXM - 1) {
+#pragma unroll
+            for (int i = 0; i < kXLoadsA; i++)
+                lds_dma16(ab, a_off[i], st + (uint32_t)((wave * kXLoadsA + i) * 64 * 16));
+        } else {  // last feature tile of an N that is not a multiple of 256
+#pragma unroll
+            for (int i = 0; i < kXLoadsA; i++) {
+                const uint32_t off = a_off[i] - (uint32_t)((a_row[i] - min(a_row[i], a_lim)) * kMlaDc * 2);
+                lds_dma16(ab, off, st + (uint32_t)((wave * kXLoadsA + i) * 64 * 16));
             }
-            rb[u] = *(const u32x4 *)(wt + (int64_t)(f0 + r) * kMlaDc + c0 + part * 8);
         }
-    };
-    auto store = [&](int buf) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int c = tid + 256 * u;
-            const int r = c >> 2, part = c & 3;
-            *(u32x4 *)&As[buf][r * kDP + part * 8] = ra[u];
-            *(u32x4 *)&Bs[buf][r * kDP + part * 8] = rb[u];
-        }
+        for (int i = 0; i < kXLoadsB; i++)
+            lds_dma16(b_ptr[i] + c0, st + (uint32_t)(kXM * kXK * 2 + (wave * kXLoadsB + i) * 64 * 16));
     };
+    static_assert(kXS == 3, "the stage wait covers one stage ahead");
 
     fl4 acc[4][4];
 #pragma unroll
@@ -89,64 +154,83 @@ __global__ __launch_bounds__(256) void mla_decompress_kernel(
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = fl4{0.f, 0.f, 0.f, 0.f};
 
-    load(0);
-    store(0);
-    __syncthreads();
-    int buf = 0;
-    for (int c0 = 0; c0 < kMlaDc; c0 += kDK) {
-        const bool has_next = c0 + kDK < kMlaDc;
-        if (has_next) load(c0 + kDK);
-        // M side: features (K_c) or tokens (V^T); N side: the other.
-        const uint16_t *Ms = OUT_V ? As[buf] : Bs[buf];
-        const uint16_t *Ns = OUT_V ? Bs[buf] : As[buf];
-        const int mbase = OUT_V ? wt_m : wt_n;
-        const int nbase = OUT_V ? wt_n : wt_m;
-        bf16x8 am[4], bn[4];
+    const int mo = 8 * (grp >> 1) + 16 * (grp & 1);
+    for (int g = 0; g < kXS - 1 && g < G; g++) issue(g);
+    for (int g = 0; g < G; g++) {
+        // This wave's loads of stage g landed (stage g + 1, issued after it,
+        // may still be in flight; loads retire in issue order).
+        if (g + 1 < G) RLX_WAIT_VM(kXLoads); else RLX_WAIT_VM(0);
+        ring_barrier();  // stage g visible; stage (g - 1) % kXS no longer read
+        if (g + kXS - 1 < G) issue(g + kXS - 1);
+        const uint16_t *A = ring + (g % kXS) * kXStage;
+        const uint16_t *B = A + kXM * kXK;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            am[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)&Ms[(mbase + i * 16 + col) * kDP + grp * 8]);
-            bn[i] = __builtin_bit_cast(bf16x8, *(const u32x4 *)&Ns[(nbase + i * 16 + col) * kDP + grp * 8]);
-        }
+        for (int kk = 0; kk < kXK / 32; kk++) {
+            u32x4 fa[4], fb[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am[i], bn[j], acc[i][j], 0, 0, 0);
-        if (has_next) store(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-    }
-
-    // acc[i][j][e] = out[m = mbase + 16i + 4grp + e][n = nbase + 16j + col]
-    const int Tp = R.nsplit;
-    const int64_t seq_base = (int64_t)R.part * H * 128;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            u32x2 w;
-            w[0] = (uint32_t)bf16_rne(acc[i][j][0]) | ((uint32_t)bf16_rne(acc[i][j][1]) << 16);
-            w[1] = (uint32_t)bf16_rne(acc[i][j][2]) | ((uint32_t)bf16_rne(acc[i][j][3]) << 16);
-            if (OUT_V) {
-                // m = token (4 consecutive), n = feature
-                const int t = t0 + wt_m + i * 16 + grp * 4;
-                const int f = f0 + wt_n + j * 16 + col;
-                const int h = f / 128, d = f % 128;
-                *(u32x2 *)(dst + seq_base + ((int64_t)h * 128 + d) * Tp + t) = w;
-            } else {
-                // m = feature (4 consecutive), n = token
-                const int f = f0 + wt_n + i * 16 + grp * 4;
-                const int t = t0 + wt_m + j * 16 + col;
-                const int h = f / 128, d = f % 128;
-                *(u32x2 *)(dst + seq_base + ((int64_t)h * Tp + t) * 128 + d) = w;
+            for (int i = 0; i < 4; i++) {
+                const int ra = wf * 64 + i * 16 + col, rb = wtk * 64 + i * 16 + col;
+                fa[i] = *(const u32x4 *)(A + ra * kXK + (((kk * 4 + grp) ^ (ra & 7)) << 3));
+                fb[i] = *(const u32x4 *)(B + rb * kXK + (((kk * 4 + grp) ^ (rb & 7)) << 3));
             }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = OUT_V ? __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                            __builtin_bit_cast(bf16x8, fb[i]), __builtin_bit_cast(bf16x8, fa[j]), acc[i][j], 0, 0, 0)
+                                      : __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                            __builtin_bit_cast(bf16x8, fa[i]), __builtin_bit_cast(bf16x8, fb[j]), acc[i][j], 0, 0, 0);
         }
+        if (g % kXSteps != kXSteps - 1) continue;
+        // Tile done: acc[i][j][e] = out[m = 16 i + 4 grp + e][n = 16 j + col]
+        // of this wave's block, m = feature (K_c) or token (V^T), contiguous
+        // in memory.  Sub-tiles i and i + 1 are paired with one row swap
+        // (v_permlane16_swap: odd 16-lane rows of the first operand <-> even
+        // rows of the second), after which lane (col, grp) holds the 8
+        // consecutive m 16 i + 8 (grp >> 1) + 16 (grp & 1) .. + 7: one
+        // 16-byte store, 64 contiguous bytes per output row per instruction.
+        const int t = (int)blockIdx.x + (g / kXSteps) * (int)gridDim.x;
+        const int f0 = (t % n_mt) * kXM + wf * 64;
+        const int2 wk = work[t / n_mt];
+        const AttRow R = rows[wk.x];
+        const int tk0 = wk.y + wtk * 64;
+        const int Tp = R.nsplit;
+        uint16_t *db = dst + (int64_t)R.part * H * 128;
+#pragma unroll
+        for (int i = 0; i < 4; i += 2)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t x[2], y[2];
+                x[0] = pack_bf16x2(acc[i][j][0], acc[i][j][1]);
+                x[1] = pack_bf16x2(acc[i][j][2], acc[i][j][3]);
+                y[0] = pack_bf16x2(acc[i + 1][j][0], acc[i + 1][j][1]);
+                y[1] = pack_bf16x2(acc[i + 1][j][2], acc[i + 1][j][3]);
+                acc[i][j] = fl4{0.f, 0.f, 0.f, 0.f};
+                acc[i + 1][j] = fl4{0.f, 0.f, 0.f, 0.f};
+                u32x4 w;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const auto sw = __builtin_amdgcn_permlane16_swap(x[h], y[h], false, false);
+                    w[h] = sw[0];
+                    w[2 + h] = sw[1];
+                }
+                const int m = 16 * i + mo, n = 16 * j + col;
+                if (OUT_V) {
+                    const int f = f0 + n, tk = tk0 + m;
+                    if (f < N) *(u32x4 *)(db + (int64_t)f * Tp + tk) = w;
+                } else {
+                    const int f = f0 + m, tk = tk0 + n;
+                    if (f < N) *(u32x4 *)(db + ((int64_t)(f >> 7) * Tp + tk) * 128 + (f & 127)) = w;
+                }
+            }
+    }
 }
 
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, const int2 *work, int n_work, const uint16_t *w_uk,
                              const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
-                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt) {
+                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt, int cus) {
     if (D != 128) return hipErrorInvalidValue;
     const int N = H * D;
     dim3 tg((N + 63) / 64, (kMlaDc + 63) / 64);
@@ -155,9 +239,10 @@ hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_work <= 0) return hipSuccess;
-    dim3 g(n_work, N / kDF);
-    mla_decompress_kernel<0><<<g, 256, 0, s>>>(pool, table, rows, work, wt_k, H, P, kc);
-    mla_decompress_kernel<1><<<g, 256, 0, s>>>(pool, table, rows, work, wt_v, H, P, vt);
+    const int tiles = (N + kXM - 1) / kXM * n_work;
+    const int grid = std::max(1, std::min(tiles, cus));
+    mla_expand_kernel<0><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_k, N, H, P, kc);
+    mla_expand_kernel<1><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_v, N, H, P, vt);
     return hipGetLastError();
 }
 

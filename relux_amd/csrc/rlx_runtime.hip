@@ -1181,7 +1181,7 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         HIP_TRY(launch_mla_expand(c->stream, ls.pool0, c->d_table, drows,
                                   (const int2 *)((char *)dev + o_d), (int)dwork.size(),
                                   (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
-                                  c->P, wt_k, wt_v, kc, vt));
+                                  c->P, wt_k, wt_v, kc, vt, c->cus));
         if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
         PrefillArgs a{};
         a.kpool = ls.pool0;
