@@ -272,8 +272,48 @@ int32_t rlx_evict(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq
 /* Rewrite page-table rows so live pages start at entry 0, logical order
  * kept; K/V bytes do not move (layer -1: every layer). */
 int32_t rlx_compact(void *cache, int32_t layer);
-/* Free every page of one sequence (layer -1: every layer). */
+/* Free every page of one sequence, spilled pages included (layer -1: every
+ * layer). */
 int32_t rlx_seq_release(void *cache, int32_t layer, int32_t seq);
+
+/* ---- host spill tier (no reference counterpart) ----------------------- */
+/* The reference's file-backed caches (NewKVCacheFile, kvcache.go:95-166;
+ * the MLA variant, mla_cache.go:61-113) keep the whole cache in a file
+ * mapped MAP_SHARED.  Here the file (or pinned host memory) is a second
+ * tier below the HBM pool: pages spilled to it leave attention exactly as
+ * evicted pages do, and can be put back in front of their sequence.
+ *
+ * Attach a tier of host_pages slots, one layer's page each (GQA: the K page
+ * then the V page of every kv head, as stored in HBM; MLA: the latent
+ * rows); slot bytes and counts via rlx_spill_info.  path NULL or "":
+ * pinned host memory; otherwise the file is created or truncated to size
+ * and mapped MAP_SHARED -- the caller owns the file (it is not deleted).
+ * host_pages 0 detaches.  Fails while the tier holds pages. */
+int32_t rlx_spill_attach(void *cache, const char *path, int64_t host_pages);
+/* Move the oldest n_pages[i] full pages of sequence seq_ids[i] (layer -1:
+ * every layer) to the tier: the device state afterwards is exactly that of
+ * rlx_evict with the same arguments (pages pushed oldest first, first and
+ * pos_offset advance).  Slots are taken 0, 1, 2, ... from a LIFO free list.
+ * With a file tier the bytes are in the file when the call returns.
+ * RLX_ERR_POOL when the tier has too few free slots (no change). */
+int32_t rlx_spill(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                  const int32_t *n_pages);
+/* Put the n_pages[i] most recently spilled pages of sequence seq_ids[i]
+ * back in front of it (layer -1: every layer): newest spilled page first,
+ * each into a page popped from the free list; len grows and pos_offset
+ * shrinks by n_pages*page_tokens, so the sequence's bytes and positions
+ * are those before the spill.  Live table entries move right when fewer
+ * than n_pages entries precede them.  A later rlx_evict of the sequence
+ * drops its spilled pages too (they would no longer adjoin its resident
+ * tokens).  RLX_ERR_STATE / RLX_ERR_POOL / RLX_ERR_OVERFLOW, no change. */
+int32_t rlx_restore(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                    const int32_t *n_pages);
+/* Tier slots holding (layer, seq)'s spilled pages, oldest first (at most
+ * cap written); *n_out = their count. */
+int32_t rlx_spill_slots(void *cache, int32_t layer, int32_t seq, int64_t *slots_out, int32_t cap,
+                        int32_t *n_out);
+/* info[0..3] = slots, bytes per slot, free slots, 1 if file-backed. */
+int32_t rlx_spill_info(void *cache, int64_t *info);
 
 /* ---- token selection on the device (synchronising) -------------------- */
 /* Sampler fields (sampler.go:33-43) except Rand: every rng.Float32() draw

@@ -93,6 +93,11 @@ SIGNATURES = {
     "rlx_evict": [_vp, _i32, _i32, _pi32, _pi32],
     "rlx_compact": [_vp, _i32],
     "rlx_seq_release": [_vp, _i32, _i32],
+    "rlx_spill_attach": [_vp, ctypes.c_char_p, _i64],
+    "rlx_spill": [_vp, _i32, _i32, _pi32, _pi32],
+    "rlx_restore": [_vp, _i32, _i32, _pi32, _pi32],
+    "rlx_spill_slots": [_vp, _i32, _i32, ctypes.POINTER(ctypes.c_int64), _i32, _pi32],
+    "rlx_spill_info": [_vp, ctypes.POINTER(ctypes.c_int64)],
     "rlx_greedy": [_vp, _vp, _i32, _i32, _i64, _pi32],
     "rlx_sample": [_vp, _vp, _i32, _i32, _i64, _psp, _pi32, _pi32, ctypes.POINTER(_f32), _pi32],
     "rlx_spec_accept": [_vp, _vp, _vp, _pi32, _pi32, _i32, _i32, _i32, ctypes.POINTER(_f32), _psp,

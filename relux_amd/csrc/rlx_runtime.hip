@@ -17,6 +17,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <unistd.h>
+
 #include <map>
 #include <string>
 #include <vector>
@@ -74,6 +78,19 @@ struct Slot {
 
 constexpr int kSlots = 8;
 
+// Host spill tier: slots of one layer's page each, holding the page's bytes
+// exactly as stored in HBM (GQA: the K page then the V page of every kv
+// head; MLA: the latent rows).  Backed by pinned host memory or by a file
+// mapped MAP_SHARED (the reference's file-backed caches, kvcache.go:95-166).
+struct SpillTier {
+    uint8_t *base = nullptr;
+    int64_t slots = 0;
+    size_t slot_bytes = 0;
+    size_t map_bytes = 0;  // non-zero: file mapping
+    std::vector<int64_t> free_stack;                   // back() is the next slot handed out
+    std::vector<std::vector<std::vector<int64_t>>> held;  // [layer][seq]: slots, oldest page first
+};
+
 struct Cache {
     int kind = kGQA;
     int layers = 0, kvh = 0, hd = 0, P = 0, pool_pages = 0, max_seqs = 0, max_pages = 0;
@@ -88,6 +105,7 @@ struct Cache {
     int next_slot = 0;
     void *ws = nullptr;
     size_t ws_cap = 0;
+    SpillTier spill;
     // Attention-kernel timing: event pairs, reused across reports.
     int timing = 0;  // RLX_TIME_* mask
     std::vector<std::pair<hipEvent_t, hipEvent_t>> tev;
@@ -301,9 +319,37 @@ void destroy_cache(Cache *c) {
         if (s.dev) (void)hipFree(s.dev);
         if (s.ev) (void)hipEventDestroy(s.ev);
     }
+    if (c->spill.base) {
+        if (c->spill.map_bytes)
+            (void)munmap(c->spill.base, c->spill.map_bytes);
+        else
+            (void)hipHostFree(c->spill.base);
+    }
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
 }
+
+// Give the spilled slots of (layer, seq) back to the tier, newest first.
+void release_spilled(Cache *c, int layer, int seq) {
+    if (c->spill.held.empty()) return;
+    auto &h = c->spill.held[layer][seq];
+    for (auto it = h.rbegin(); it != h.rend(); ++it) c->spill.free_stack.push_back(*it);
+    h.clear();
+}
+
+void reset_spill(Cache *c) {
+    SpillTier &t = c->spill;
+    if (!t.base) return;
+    t.free_stack.resize(t.slots);
+    for (int64_t i = 0; i < t.slots; i++) t.free_stack[i] = t.slots - 1 - i;  // slots 0, 1, 2, ...
+    t.held.assign(c->layers, std::vector<std::vector<int64_t>>(c->max_seqs));
+}
+
+// Bytes of one layer's page in the K (or latent) pool and in the V pool.
+size_t page_bytes0(const Cache *c) {
+    return (c->kind == kGQA) ? (size_t)c->kvh * c->P * c->hd * 2 : (size_t)c->P * kMlaRow * 2;
+}
+size_t page_bytes1(const Cache *c) { return (c->kind == kGQA) ? page_bytes0(c) : 0; }
 
 // Plan the page allocations of one append call on one layer.  Validates
 // everything first so that a failing call changes no state.
@@ -619,6 +665,7 @@ int32_t rlx_cache_reset(void *h) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     for (auto &ls : c->L) reset_layer_state(c, ls);
+    reset_spill(c);
     c->pending.clear();
     HIP_TRY(launch_fill_i32(c->stream, c->d_table, -1, (int64_t)c->layers * c->max_seqs * c->max_pages));
     return RLX_OK;
@@ -1314,6 +1361,10 @@ int32_t rlx_evict(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids
         for (int l = lo; l < hi; l++) {
             LayerState &ls = c->L[l];
             SeqState &s = ls.seqs[seq];
+            // Spilled pages are older than every resident one: once the
+            // oldest resident pages are dropped they can no longer be put
+            // back in front of the sequence, so they go as well.
+            if (n_pages[i] > 0) release_spilled(c, l, seq);
             for (int k = 0; k < n_pages[i]; k++) {
                 ls.free_stack.push_back(c->entry(l, seq, s.first + k));
                 c->set_entry(l, seq, s.first + k, -1);
@@ -1346,6 +1397,192 @@ int32_t rlx_compact(void *h, int32_t layer) {
     return RLX_OK;
 }
 
+int32_t rlx_spill_attach(void *h, const char *path, int64_t host_pages) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    SpillTier &t = c->spill;
+    for (auto &per_layer : t.held)
+        for (auto &v : per_layer)
+            if (!v.empty()) return fail(RLX_ERR_STATE, "the spill tier still holds pages");
+    if (host_pages < 0) return fail(RLX_ERR_INVALID, "host_pages=%lld", (long long)host_pages);
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    if (t.base) {
+        if (t.map_bytes)
+            munmap(t.base, t.map_bytes);
+        else
+            HIP_TRY(hipHostFree(t.base));
+    }
+    t = SpillTier{};
+    if (host_pages == 0) return RLX_OK;
+    const size_t slot_bytes = page_bytes0(c) + page_bytes1(c);
+    const size_t bytes = slot_bytes * (size_t)host_pages;
+    if (path && *path) {
+        const int fd = open(path, O_RDWR | O_CREAT | O_TRUNC, 0644);
+        if (fd < 0) return fail(RLX_ERR_INVALID, "rlx_spill_attach: open %s failed", path);
+        void *m = MAP_FAILED;
+        if (ftruncate(fd, (off_t)bytes) == 0) m = mmap(nullptr, bytes, PROT_READ | PROT_WRITE, MAP_SHARED, fd, 0);
+        close(fd);  // the mapping keeps the file; the caller owns its lifetime
+        if (m == MAP_FAILED) return fail(RLX_ERR_INVALID, "rlx_spill_attach: cannot map %zu bytes of %s", bytes, path);
+        t.base = (uint8_t *)m;
+        t.map_bytes = bytes;
+    } else {
+        void *m = nullptr;
+        HIP_TRY(hipHostMalloc(&m, bytes, hipHostMallocDefault));
+        t.base = (uint8_t *)m;
+    }
+    t.slots = host_pages;
+    t.slot_bytes = slot_bytes;
+    reset_spill(c);
+    return RLX_OK;
+}
+
+int32_t rlx_spill(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids, const int32_t *n_pages) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    SpillTier &t = c->spill;
+    if (!t.base) return fail(RLX_ERR_STATE, "no spill tier attached");
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (n_seqs > 0 && !n_pages) return fail(RLX_ERR_INVALID, "null page counts");
+    int64_t need = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        if (n_pages[i] < 0) return fail(RLX_ERR_INVALID, "negative spill");
+        for (int l = lo; l < hi; l++)
+            if (n_pages[i] > c->L[l].seqs[seq_ids[i]].len / c->P)
+                return fail(RLX_ERR_STATE, "spilling %d pages of seq %d on layer %d with %d full pages",
+                            n_pages[i], seq_ids[i], l, c->L[l].seqs[seq_ids[i]].len / c->P);
+        need += (int64_t)n_pages[i] * (hi - lo);
+    }
+    if (need > (int64_t)t.free_stack.size())
+        return fail(RLX_ERR_POOL, "spill tier: %lld slots needed, %zu free", (long long)need, t.free_stack.size());
+    const size_t b0 = page_bytes0(c), b1 = page_bytes1(c);
+    for (int i = 0; i < n_seqs; i++) {
+        const int seq = seq_ids[i];
+        for (int l = lo; l < hi; l++) {
+            LayerState &ls = c->L[l];
+            SeqState &s = ls.seqs[seq];
+            for (int k = 0; k < n_pages[i]; k++) {
+                const int32_t page = c->entry(l, seq, s.first + k);
+                const int64_t slot = t.free_stack.back();
+                t.free_stack.pop_back();
+                uint8_t *dst = t.base + (size_t)slot * t.slot_bytes;
+                HIP_TRY(hipMemcpyAsync(dst, (const uint8_t *)ls.pool0 + (size_t)page * b0, b0,
+                                       hipMemcpyDeviceToHost, c->stream));
+                if (b1)
+                    HIP_TRY(hipMemcpyAsync(dst + b0, (const uint8_t *)ls.pool1 + (size_t)page * b1, b1,
+                                           hipMemcpyDeviceToHost, c->stream));
+                t.held[l][seq].push_back(slot);
+                // The page is reused only by later work on this stream, which
+                // runs after the copy.
+                ls.free_stack.push_back(page);
+                c->set_entry(l, seq, s.first + k, -1);
+            }
+            s.first += n_pages[i];
+            s.pages -= n_pages[i];
+            s.len -= n_pages[i] * c->P;
+            s.pos_offset += n_pages[i] * c->P;
+        }
+    }
+    // A file tier holds the bytes once the call returns.
+    if (t.map_bytes) HIP_TRY(hipStreamSynchronize(c->stream));
+    return RLX_OK;
+}
+
+int32_t rlx_restore(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids, const int32_t *n_pages) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    SpillTier &t = c->spill;
+    if (!t.base) return fail(RLX_ERR_STATE, "no spill tier attached");
+    int lo, hi;
+    int32_t rc = layer_range(c, layer, &lo, &hi);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (n_seqs > 0 && !n_pages) return fail(RLX_ERR_INVALID, "null page counts");
+    for (int l = lo; l < hi; l++) {
+        int64_t need = 0;
+        for (int i = 0; i < n_seqs; i++) {
+            const int seq = seq_ids[i];
+            const SeqState &s = c->L[l].seqs[seq];
+            if (n_pages[i] < 0) return fail(RLX_ERR_INVALID, "negative restore");
+            if (n_pages[i] > (int)t.held[l][seq].size())
+                return fail(RLX_ERR_STATE, "restoring %d pages of seq %d on layer %d with %zu spilled",
+                            n_pages[i], seq, l, t.held[l][seq].size());
+            if (std::max(s.first, n_pages[i]) + s.pages > c->max_pages)
+                return fail(RLX_ERR_OVERFLOW, "restore of seq %d on layer %d exceeds %d table entries", seq,
+                            l, c->max_pages);
+            need += n_pages[i];
+        }
+        for (int i = 0; i < n_seqs; i++)  // a sequence listed twice
+            for (int j = 0; j < i; j++)
+                if (seq_ids[i] == seq_ids[j]) return fail(RLX_ERR_INVALID, "seq %d listed twice", seq_ids[i]);
+        if (need > (int64_t)c->L[l].free_stack.size())
+            return fail(RLX_ERR_POOL, "restore needs %lld pages on layer %d, %zu free", (long long)need, l,
+                        c->L[l].free_stack.size());
+    }
+    const size_t b0 = page_bytes0(c), b1 = page_bytes1(c);
+    for (int i = 0; i < n_seqs; i++) {
+        const int seq = seq_ids[i], n = n_pages[i];
+        if (n == 0) continue;
+        for (int l = lo; l < hi; l++) {
+            LayerState &ls = c->L[l];
+            SeqState &s = ls.seqs[seq];
+            if (s.first < n) {  // make room in front: live entries move to [n, n + pages)
+                for (int k = s.pages - 1; k >= 0; k--) c->set_entry(l, seq, n + k, c->entry(l, seq, s.first + k));
+                for (int k = s.first; k < n && k < s.first + s.pages; k++) c->set_entry(l, seq, k, -1);
+                s.first = n;
+            }
+            auto &held = t.held[l][seq];
+            for (int k = n - 1; k >= 0; k--) {  // the newest spilled page first
+                const int64_t slot = held.back();
+                held.pop_back();
+                const int32_t page = ls.free_stack.back();
+                ls.free_stack.pop_back();
+                c->set_entry(l, seq, s.first - n + k, page);
+                const uint8_t *src = t.base + (size_t)slot * t.slot_bytes;
+                HIP_TRY(hipMemcpyAsync((uint8_t *)ls.pool0 + (size_t)page * b0, src, b0, hipMemcpyHostToDevice,
+                                       c->stream));
+                if (b1)
+                    HIP_TRY(hipMemcpyAsync((uint8_t *)ls.pool1 + (size_t)page * b1, src + b0, b1,
+                                           hipMemcpyHostToDevice, c->stream));
+                t.free_stack.push_back(slot);
+            }
+            s.first -= n;
+            s.pages += n;
+            s.len += n * c->P;
+            s.pos_offset -= n * c->P;
+        }
+    }
+    // The slots may be handed out again by the next spill, whose copies
+    // queue behind these on the same stream.
+    return RLX_OK;
+}
+
+int32_t rlx_spill_slots(void *h, int32_t layer, int32_t seq, int64_t *slots_out, int32_t cap, int32_t *n_out) {
+    if (!h || !n_out) return fail(RLX_ERR_INVALID, "null argument");
+    Cache *c = as_cache(h);
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if (seq < 0 || seq >= c->max_seqs) return fail(RLX_ERR_INVALID, "seq id %d", seq);
+    const SpillTier &t = c->spill;
+    const int n = t.held.empty() ? 0 : (int)t.held[layer][seq].size();
+    *n_out = n;
+    if (slots_out)
+        for (int k = 0; k < n && k < cap; k++) slots_out[k] = t.held[layer][seq][k];
+    return RLX_OK;
+}
+
+int32_t rlx_spill_info(void *h, int64_t *info) {
+    if (!h || !info) return fail(RLX_ERR_INVALID, "null argument");
+    const SpillTier &t = as_cache(h)->spill;
+    info[0] = t.slots;
+    info[1] = (int64_t)t.slot_bytes;
+    info[2] = (int64_t)t.free_stack.size();
+    info[3] = t.map_bytes ? 1 : 0;
+    return RLX_OK;
+}
+
 int32_t rlx_seq_release(void *h, int32_t layer, int32_t seq) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
@@ -1360,6 +1597,7 @@ int32_t rlx_seq_release(void *h, int32_t layer, int32_t seq) {
             ls.free_stack.push_back(c->entry(l, seq, s.first + k));
             c->set_entry(l, seq, s.first + k, -1);
         }
+        release_spilled(c, l, seq);
         s = SeqState{};
     }
     return RLX_OK;

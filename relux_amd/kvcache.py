@@ -126,6 +126,42 @@ class _PagedCache:
     def Release(self, seq, layer=-1):
         check(self._lib.rlx_seq_release(self._h, layer, seq))
 
+    # -- host spill tier (no reference counterpart) --------------------------
+    def AttachSpill(self, host_pages, path=None):
+        """Attach a host tier of `host_pages` page slots below the HBM pool:
+        pinned host memory, or -- with `path` -- a file created at that size
+        and mapped MAP_SHARED, as the reference's NewKVCacheFile
+        (kvcache.go:95-166) maps its whole cache.  The file is not deleted.
+        host_pages 0 detaches."""
+        check(self._lib.rlx_spill_attach(self._h, path.encode() if path else None, int(host_pages)))
+
+    def Spill(self, seq, n_pages, layer=-1):
+        """Move the oldest n_pages full pages of `seq` (int or list) to the
+        host tier; the device state is that of Evict with the same
+        arguments."""
+        seqs, ns = _as_lists(seq, n_pages)
+        check(self._lib.rlx_spill(self._h, layer, len(seqs), i32_array(seqs), i32_array(ns)))
+
+    def Restore(self, seq, n_pages, layer=-1):
+        """Put the n_pages most recently spilled pages of `seq` back in
+        front of it (bytes and positions as before the spill)."""
+        seqs, ns = _as_lists(seq, n_pages)
+        check(self._lib.rlx_restore(self._h, layer, len(seqs), i32_array(seqs), i32_array(ns)))
+
+    def SpilledSlots(self, layer, seq):
+        """Tier slots of (layer, seq)'s spilled pages, oldest first."""
+        n = ctypes.c_int32()
+        check(self._lib.rlx_spill_slots(self._h, layer, seq, None, 0, ctypes.byref(n)))
+        out = (ctypes.c_int64 * max(n.value, 1))()
+        check(self._lib.rlx_spill_slots(self._h, layer, seq, out, n.value, ctypes.byref(n)))
+        return list(out[:n.value])
+
+    def SpillInfo(self):
+        """{slots, slot_bytes, free, file} of the host tier."""
+        info = (ctypes.c_int64 * 4)()
+        check(self._lib.rlx_spill_info(self._h, info))
+        return {"slots": info[0], "slot_bytes": info[1], "free": info[2], "file": bool(info[3])}
+
     # -- state dumps ---------------------------------------------------------
     def SeqState(self, layer, seq):
         st = (ctypes.c_int32 * 4)()

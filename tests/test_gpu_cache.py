@@ -256,3 +256,145 @@ def test_paged_script_matches_golden(gpu):
                 np.testing.assert_array_equal(got, np.stack(rows[s]).transpose(1, 0, 2))
         free = fx["free"][i]
         assert c.FreeList(0) == free[free >= 0].tolist(), (i, op)
+
+
+# ---- host spill tier ---------------------------------------------------------
+
+def _k_page(rows, KVH, D, P):
+    """One layer's K page as stored in HBM: per kv head P x D in the
+    k-step-major order (k_page_off)."""
+    out = np.zeros((KVH, P * D), np.uint16)
+    s_ = np.arange(P)[:, None]
+    d = np.arange(D)[None, :]
+    off = s_ * D + d if D <= 32 else ((s_ >> 4) * (D >> 5) + (d >> 5)) * 512 + (s_ & 15) * 32 + (d & 31)
+    blk = np.stack(rows)  # [P][KVH][D]
+    for h in range(KVH):
+        out[h, off.ravel()] = blk[:, h, :].ravel()
+    return out.ravel()
+
+
+def _v_page(rows, KVH, D, P):
+    """One layer's V page as stored in HBM: per kv head D x P (dim-major)."""
+    return np.stack(rows).transpose(1, 2, 0).ravel()  # [KVH][D][P]
+
+
+@pytest.mark.parametrize("tier", ["pinned", "file"])
+def test_spill_restore_state_and_bytes(gpu, tier, tmp_path):
+    """Spill / restore / evict / release against oracle/paged.py: free
+    lists, table rows, sequence state, tier slots and the gathered bytes
+    bit-exact at every step; with a file tier, every spilled slot of the
+    file holds the page's K and V bytes as stored in HBM."""
+    rng = np.random.default_rng(21)
+    KVH, D, P, S, POOL, MAXP, SLOTS = 2, 64, 16, 3, 48, 16, 40
+    c = _kv(gpu, num_layers=2, max_len=MAXP * P, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+            max_seqs=S, pool_pages=POOL)
+    path = str(tmp_path / "spill.bin") if tier == "file" else None
+    c.AttachSpill(SLOTS, path=path)
+    slot_bytes = 2 * KVH * P * D * 2
+    assert c.SpillInfo() == {"slots": SLOTS, "slot_bytes": slot_bytes, "free": SLOTS, "file": tier == "file"}
+    m = PagedModel(2, P, POOL, S, MAXP, host_slots=SLOTS)
+    seqs = list(range(S))
+
+    def append(n):
+        for layer in range(2):
+            kk = rng.normal(size=(sum(n), KVH, D)).astype(np.float32)
+            vv = rng.normal(size=(sum(n), KVH, D)).astype(np.float32)
+            c.Append(layer, torch.from_numpy(kk).to(gpu), torch.from_numpy(vv).to(gpu), seq_ids=seqs,
+                     n_tok=n, layout="SHD")
+            kb, vb = oracle.bf16_from_f32(kk), oracle.bf16_from_f32(vv)
+            pay, off = [], 0
+            for ni in n:
+                pay.append([(kb[off + t], vb[off + t]) for t in range(ni)])
+                off += ni
+            m.append(layer, seqs, n, payloads=pay)
+
+    def check():
+        for layer in range(2):
+            assert c.FreeList(layer) == m.free[layer]
+            for s in seqs:
+                assert c.SeqState(layer, s) == m.state(layer, s)
+                assert c.PageTable(layer, s) == list(m.table[layer][s])
+                assert c.SpilledSlots(layer, s) == [slot for slot, _ in m.spilled[layer][s]]
+                ck, cv = c.View(layer, s)
+                rows = m.rows[layer][s]
+                if not rows:
+                    assert ck is None
+                    continue
+                got_k = ck.view(torch.int16).cpu().numpy().view(np.uint16)[0]
+                got_v = cv.view(torch.int16).cpu().numpy().view(np.uint16)[0]
+                assert np.array_equal(got_k, np.stack([r[0] for r in rows]).transpose(1, 0, 2))
+                assert np.array_equal(got_v, np.stack([r[1] for r in rows]).transpose(1, 0, 2))
+        assert c.SpillInfo()["free"] == len(m.host_free)
+        if tier == "file":
+            c.Sync()
+            f = np.fromfile(path, dtype=np.uint16)
+            assert f.size == SLOTS * slot_bytes // 2
+            half = slot_bytes // 4
+            for layer in range(2):
+                for s in seqs:
+                    for slot, prow in m.spilled[layer][s]:
+                        got = f[slot * 2 * half:(slot + 1) * 2 * half]
+                        assert np.array_equal(got[:half], _k_page([r[0] for r in prow], KVH, D, P))
+                        assert np.array_equal(got[half:], _v_page([r[1] for r in prow], KVH, D, P))
+
+    append([70, 100, 35]); check()
+    c.Spill(seqs, [2, 3, 1]); m.spill(-1, seqs, [2, 3, 1]); check()
+    append([20, 5, 40]); check()
+    c.Restore(seqs, [1, 2, 1]); m.restore(-1, seqs, [1, 2, 1]); check()
+    c.Spill([1], [2], layer=1); m.spill(1, [1], [2]); check()
+    c.Compact(); m.compact(-1)
+    c.Restore([0, 1], [1, 1]); m.restore(-1, [0, 1], [1, 1]); check()  # seq 0: live entries move right
+    c.Restore([1], [2], layer=1); m.restore(1, [1], [2]); check()
+    c.Spill(seqs, [1, 1, 1]); m.spill(-1, seqs, [1, 1, 1]); check()
+    c.Evict([1], [1]); m.evict(-1, 1, 1); check()  # drops seq 1's spilled pages
+    c.Release(0); m.release(-1, 0); check()
+    from relux_amd import ReluxError
+    with pytest.raises(ReluxError):
+        c.Restore([2], [5])
+    check()
+
+
+def test_attention_after_restore_is_bit_exact(gpu):
+    """Spilling leaves attention exactly as Evict does; restoring brings the
+    pre-spill output back bit for bit (same bytes, same positions, other
+    page ids)."""
+    rng = np.random.default_rng(22)
+    KVH, H, D, P = 2, 8, 128, 16
+    c = _kv(gpu, num_layers=1, max_len=1024, num_kv_heads=KVH, head_dim=D, page_tokens=P, max_seqs=2,
+            pool_pages=80)
+    e = _kv(gpu, num_layers=1, max_len=1024, num_kv_heads=KVH, head_dim=D, page_tokens=P, max_seqs=2,
+            pool_pages=80)
+    c.AttachSpill(16)
+    n = [300, 211]
+    kk = torch.from_numpy(rng.normal(size=(sum(n), KVH, D)).astype(np.float32)).to(gpu)
+    vv = torch.from_numpy(rng.normal(size=(sum(n), KVH, D)).astype(np.float32)).to(gpu)
+    for cc in (c, e):
+        cc.Append(0, kk, vv, seq_ids=[0, 1], n_tok=n, layout="SHD")
+    q = torch.from_numpy(rng.normal(size=(2, H, D)).astype(np.float32)).to(gpu)
+    before = c.Attend(0, q, H, seq_ids=[0, 1]).cpu()
+    c.Spill([0, 1], [5, 3])
+    e.Evict([0, 1], [5, 3])
+    assert torch.equal(c.Attend(0, q, H, seq_ids=[0, 1]).cpu(), e.Attend(0, q, H, seq_ids=[0, 1]).cpu())
+    c.Restore([0, 1], [5, 3])
+    assert torch.equal(c.Attend(0, q, H, seq_ids=[0, 1]).cpu(), before)
+
+
+def test_mla_spill_restore_roundtrip(gpu, tmp_path):
+    """Latent pages through a file tier and back, bytes bit-exact."""
+    rng = np.random.default_rng(23)
+    P = 64
+    c = _mla(gpu, num_layers=2, max_len=1024, page_tokens=P, max_seqs=2, pool_pages=24)
+    c.AttachSpill(12, path=str(tmp_path / "mla.bin"))
+    n = [200, 150]
+    for layer in range(2):
+        cc = torch.from_numpy(rng.normal(size=(sum(n), 512)).astype(np.float32)).to(gpu)
+        kr = torch.from_numpy(rng.normal(size=(sum(n), 64)).astype(np.float32)).to(gpu)
+        c.Append(layer, cc, kr, seq_ids=[0, 1], n_tok=n)
+    views = [[t.clone() for t in c.View(l, s)] for l in range(2) for s in range(2)]
+    c.Spill([0, 1], [3, 2])
+    assert c.TotalLen(0, 0) == 200 - 3 * P and c.SeqState(1, 1)["pos_offset"] == 2 * P
+    assert c.SpillInfo()["free"] == 12 - 2 * 5
+    c.Restore([0, 1], [3, 2])
+    after = [[t.clone() for t in c.View(l, s)] for l in range(2) for s in range(2)]
+    for a, b in zip(views, after):
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

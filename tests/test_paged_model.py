@@ -110,3 +110,100 @@ def test_release_and_reset_return_every_page():
     m2 = copy.deepcopy(m)
     m2.reset()
     assert m2.free[0] == list(range(15, -1, -1))
+
+
+# ---- host spill tier -------------------------------------------------------
+
+def _device_state(m, layer):
+    return _snapshot(m, layer) + (m.rows[layer],)
+
+
+def _fill(m, rng, seqs, lo=20, hi=120):
+    n = rng.integers(lo, hi, size=len(seqs)).tolist()
+    for layer in range(m.layers):
+        m.append(layer, seqs, n, payloads=[[(layer, s, t) for t in range(int(m.len[layer, s]), int(m.len[layer, s]) + k)]
+                                          for s, k in zip(seqs, n)])
+    return n
+
+
+def test_spill_is_evict_on_the_device_and_restore_undoes_it():
+    rng = np.random.default_rng(7)
+    for trial in range(40):
+        m = PagedModel(2, 16, 64, 3, 12, host_slots=48)
+        _fill(m, rng, [0, 1, 2])
+        before = copy.deepcopy(m)
+        n = [int(rng.integers(0, int(m.len[0, s]) // 16 + 1)) for s in range(3)]
+        e = copy.deepcopy(m)
+        m.spill(-1, [0, 1, 2], n)
+        for s in range(3):
+            e.evict(-1, s, n[s])
+        for layer in range(2):
+            assert _same(_device_state(m, layer), _device_state(e, layer))
+        assert len(m.host_free) == 48 - 2 * sum(n)
+        assert [slot for slot, _ in m.spilled[0][0]] == list(range(n[0]))  # slots 0, 1, 2, ... in order
+        m.restore(-1, [0, 1, 2], n)
+        for layer in range(2):
+            for s in range(3):
+                assert m.rows[layer][s] == before.rows[layer][s]
+                assert m.state(layer, s) == before.state(layer, s)
+        assert sorted(m.host_free) == list(range(48))
+        # every page is live or free, and the live pages are distinct
+        live = [int(p) for s in range(3) for p in m.table[0][s] if p >= 0]
+        assert len(set(live)) == len(live) == int(m.pages[0].sum())
+        assert len(live) + len(m.free[0]) == 64
+
+
+def test_restore_moves_live_entries_right_when_the_front_is_short():
+    m = PagedModel(1, 16, 32, 1, 8, host_slots=8)
+    m.append(0, [0], [80], payloads=[list(range(80))])
+    m.spill(0, [0], [3])
+    m.compact(0)                         # first = 0: no room in front
+    assert m.state(0, 0)["first"] == 0
+    live = list(m.table[0][0][:2])
+    m.restore(0, [0], [2])
+    assert m.state(0, 0) == {"len": 64, "first": 0, "pos_offset": 16, "pages": 4}
+    assert list(m.table[0][0][2:4]) == live
+    assert m.rows[0][0] == list(range(16, 80))
+    m.restore(0, [0], [1])
+    assert m.rows[0][0] == list(range(80)) and m.state(0, 0)["pos_offset"] == 0
+
+
+def test_evict_after_spill_drops_the_spilled_pages():
+    m = PagedModel(1, 16, 32, 2, 10, host_slots=6)
+    m.append(0, [0, 1], [96, 40])
+    m.spill(0, [0], [2])
+    m.evict(0, 0, 1)
+    assert m.spilled[0][0] == [] and sorted(m.host_free) == list(range(6))
+    assert m.state(0, 0)["pos_offset"] == 48
+    with pytest.raises(PagedStateError):
+        m.restore(0, [0], [1])
+
+
+def test_spill_and_restore_failures_leave_state_unchanged():
+    m = PagedModel(1, 16, 12, 2, 6, host_slots=3)
+    m.append(0, [0, 1], [64, 80])
+    snap = copy.deepcopy(m)
+    with pytest.raises(PagedPoolExhausted):
+        m.spill(0, [0, 1], [2, 2])       # 4 slots needed, 3 free
+    with pytest.raises(PagedStateError):
+        m.spill(0, [0], [5])             # 4 full pages
+    assert _same(_device_state(m, 0), _device_state(snap, 0)) and m.host_free == snap.host_free
+    m.spill(0, [0, 1], [1, 2])
+    snap = copy.deepcopy(m)
+    with pytest.raises(PagedStateError):
+        m.restore(0, [0], [2])           # one spilled page
+    with pytest.raises(PagedStateError):
+        m.restore(0, [1, 1], [1, 1])
+    m.append(0, [0], [16 * 2])           # first 1 + 5 pages == max_pages
+    m.compact(0)
+    m.append(0, [0], [16])               # first 0 + 6 pages == max_pages
+    snap = copy.deepcopy(m)
+    with pytest.raises(PagedOverflow):
+        m.restore(0, [0], [1])           # 6 live pages + 1 restored > 6 entries
+    assert _same(_device_state(m, 0), _device_state(snap, 0))
+    m2 = copy.deepcopy(snap)
+    m2.free[0] = []
+    with pytest.raises(PagedPoolExhausted):
+        m2.restore(0, [1], [1])
+    m.release(0, 1)
+    assert [s for s, _ in m.spilled[0][1]] == [] and len(m.host_free) == 2
