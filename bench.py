@@ -57,7 +57,11 @@ WORKLOADS = {
     # ... and Sampler.Sample (penalties over a 64-token window, T 0.8,
     # top-k 50, top-p 0.9, min-p 0.02) over 64 rows of a 32k vocabulary
     "sample": dict(kind="sample", B=64, V=32000, layers=1, time="select"),
+    # next row (rank 4): the host spill tier -- a quarter of every sequence's
+    # pages of the 8k GQA batch spilled to pinned host memory and restored
+    "spill8k": dict(kind="spill", B=16, KVH=8, D=128, P=16, T=8192, frac=0.25, layers=1, time="copy"),
 }
+HOST_LINK_GBS = 64.0  # PCIe 5.0 x16, one direction
 MFMA_BF16_PEAK_TFS = 2500.0
 
 
@@ -403,15 +407,47 @@ def setup_sample(cfg, torch, dev, rng):
     return c, step, B, b, b, desc, "sample_kernel", None
 
 
+def setup_spill(cfg, torch, dev, rng):
+    """Spill the oldest quarter of every sequence's pages to pinned host
+    memory, then restore them (rlx_spill / rlx_restore).  Algorithmic bytes
+    per timed call: the pages' K and V bytes, each crossing the host link
+    once."""
+    from relux_amd import KVCache
+    B, KVH, D, P, T = cfg["B"], cfg["KVH"], cfg["D"], cfg["P"], cfg["T"]
+    pages = T // P
+    n = int(pages * cfg["frac"])
+    c = KVCache(num_layers=1, max_len=T + P, num_kv_heads=KVH, head_dim=D, page_tokens=P, max_seqs=B,
+                pool_pages=B * (pages + 1) + 8, device=dev.index)
+
+    def app(order, k_n):
+        k = torch.randn(sum(k_n), KVH, D, device=dev, dtype=torch.bfloat16)
+        c.Append(0, k, k, seq_ids=order, n_tok=k_n, layout="SHD")
+    _fill_interleaved(app, [T] * B, P, rng)
+    c.AttachSpill(B * n)
+    seqs = list(range(B))
+    counts = [n] * B
+
+    def step(i):
+        c.Spill(seqs, counts)
+        c.Restore(seqs, counts)
+
+    moved = B * n * 2 * KVH * P * D * 2
+    desc = {"workload": f"spill_restore B{B} KVH{KVH} D{D} P{P} T{T}: {n} of {pages} pages per sequence "
+                        "to pinned host memory and back",
+            "batch": B, "pages_per_call": B * n, "bytes_per_call": moved}
+    return c, step, B, moved, 2 * moved, desc, "page_copy_kernel (per call)", None
+
+
 def run_workload(name, steps, warmup, torch, dev):
     import numpy as np
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
                                  "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3,
-                                 "spec_accept": 6, "sample": 7, "block8k": 2}[name])
+                                 "spec_accept": 6, "sample": 7, "block8k": 2, "spill8k": 2}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
              "spec": setup_spec, "gqa_fused": setup_gqa_fused,
-             "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample}[cfg["kind"]]
+             "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample,
+             "spill": setup_spill}[cfg["kind"]]
     c, step, B, kbytes, sbytes, desc, kname, lens = setup(cfg, torch, dev, rng)
     torch.cuda.synchronize(dev)
     for i in range(warmup):
@@ -447,11 +483,13 @@ def run_workload(name, steps, warmup, torch, dev):
         desc = {k: v for k, v in desc.items() if k != "state"}
     achieved = kbytes / kavg_s / 1e9
     mfma = cfg["kind"] == "mla_prefill"  # compute-bound: kbytes holds FLOPs
+    link = cfg["kind"] == "spill"  # bound by the host link
     res = {
-        "bound": "mfma" if mfma else "hbm",
+        "bound": "mfma" if mfma else ("host link" if link else "hbm"),
         "kernel_rate": kbytes / kavg_s / (1e12 if mfma else 1e9),
         "rate_unit": "TFLOP/s" if mfma else "GB/s",
-        "rate_frac": kbytes / kavg_s / (1e12 * MFMA_BF16_PEAK_TFS if mfma else 1e9 * HBM_PEAK_GBS),
+        "rate_frac": kbytes / kavg_s / (1e12 * MFMA_BF16_PEAK_TFS if mfma else
+                                        1e9 * (HOST_LINK_GBS if link else HBM_PEAK_GBS)),
         "step_tflops": sbytes * steps / elapsed / 1e12 if mfma else None,
         "tokens_per_s": B * steps / elapsed,
         "ms_per_step": elapsed / steps * 1e3,
@@ -572,7 +610,8 @@ def main():
     secondary = []
     if not args.no_secondary:
         for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
-                                 "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample")
+                                 "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample",
+                                 "spill8k")
                      if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact
             n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
@@ -586,9 +625,11 @@ def main():
                      "rate_unit": s["rate_unit"], "kernel_frac_of_peak": round(s["rate_frac"], 4)}
             if s["bound"] == "hbm":
                 entry["step_hbm_gbs"] = round(s["step_hbm_gbs"], 1)
-            else:
+            elif s["bound"] == "mfma":
                 entry["step_tflops_declared"] = round(s["step_tflops"], 1)
                 entry["flops_declared"] = s["desc"]["flops_declared"]
+            else:
+                entry["bytes_per_call"] = s["desc"]["bytes_per_call"]
             secondary.append(entry)
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -618,7 +659,7 @@ def main():
         "data": "synthetic",
         "config": r["desc"],
         "roofline": {"bound": r["bound"], "achieved": round(r["kernel_rate"], 1),
-                     "peak": HBM_PEAK_GBS if r["bound"] == "hbm" else MFMA_BF16_PEAK_TFS,
+                     "peak": {"hbm": HBM_PEAK_GBS, "mfma": MFMA_BF16_PEAK_TFS}.get(r["bound"], HOST_LINK_GBS),
                      "unit": r["rate_unit"], "frac": round(r["rate_frac"], 4),
                      "traffic": traffic, "kernel": r["kernel"],
                      "kernel_avg_us": round(r["kernel_avg_us"], 2),
@@ -630,7 +671,7 @@ def main():
         # whole-step cache bytes over wall time (append, attend, merge, rollback)
         line["hbm_gbs"] = round(r["step_hbm_gbs"], 1)
         line["hbm_frac"] = round(r["step_hbm_gbs"] / HBM_PEAK_GBS, 4)
-    else:
+    elif r["bound"] == "mfma":
         line["step_tflops_declared"] = round(r["step_tflops"], 1)
     print(json.dumps(line), flush=True)
 

@@ -100,11 +100,13 @@ int32_t rlx_device_sync(void);
  * every later attend call on this handle with HIP events (on the handle's
  * stream), RLX_TIME_PROJECT every projection kernel of
  * rlx_gqa_project_append / rlx_mla_project_append, RLX_TIME_SELECT the
- * kernel of rlx_greedy / rlx_sample / rlx_spec_accept; 0 disables.  Either
- * way the recorded intervals are discarded. */
+ * kernel of rlx_greedy / rlx_sample / rlx_spec_accept, RLX_TIME_COPY the
+ * page copies of rlx_spill / rlx_restore (one interval per call); 0
+ * disables.  Either way the recorded intervals are discarded. */
 #define RLX_TIME_ATTEND 1
 #define RLX_TIME_PROJECT 2
 #define RLX_TIME_SELECT 4
+#define RLX_TIME_COPY 8
 int32_t rlx_cache_timing(void *cache, int32_t enable);
 /* Synchronise, then report the summed duration (ms) and number of the
  * timed kernel launches recorded since the last call, and clear them. */

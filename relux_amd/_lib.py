@@ -39,6 +39,7 @@ RLX_ROPE_NONE = 2
 RLX_TIME_ATTEND = 1
 RLX_TIME_PROJECT = 2
 RLX_TIME_SELECT = 4
+RLX_TIME_COPY = 8
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64

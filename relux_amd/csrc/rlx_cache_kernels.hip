@@ -28,6 +28,37 @@ hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n) 
     return hipGetLastError();
 }
 
+// Whole-page copies between the HBM pools and the host spill tier (pinned
+// host memory, which the device addresses directly): copy i moves `bytes`
+// (a multiple of 16) from src[i] to dst[i], one work-group per page.  One
+// side of every copy crosses the host link, so each thread puts 8 loads in
+// flight before its stores.
+__global__ __launch_bounds__(256) void page_copy_kernel(const uint64_t *__restrict__ src,
+                                                        const uint64_t *__restrict__ dst, int64_t bytes) {
+    const u32x4 *s = (const u32x4 *)src[blockIdx.x];
+    u32x4 *d = (u32x4 *)dst[blockIdx.x];
+    const int64_t n = bytes / 16;
+    for (int64_t i0 = 0; i0 < n; i0 += 8 * 256) {
+        u32x4 r[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t i = i0 + u * 256 + threadIdx.x;
+            if (i < n) r[u] = s[i];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t i = i0 + u * 256 + threadIdx.x;
+            if (i < n) d[i] = r[u];
+        }
+    }
+}
+
+hipError_t launch_page_copy(hipStream_t s, const uint64_t *src, const uint64_t *dst, int n, int64_t bytes) {
+    if (n <= 0 || bytes <= 0) return hipSuccess;
+    page_copy_kernel<<<n, 256, 0, s>>>(src, dst, bytes);
+    return hipGetLastError();
+}
+
 // Load 8 consecutive source elements (f32 or bf16) and convert them to bf16
 // with the reference's integer RNE rule (dtype_convert.go:15-24).
 __device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src_bf16,

@@ -83,7 +83,11 @@ constexpr int kSlots = 8;
 // head; MLA: the latent rows).  Backed by pinned host memory or by a file
 // mapped MAP_SHARED (the reference's file-backed caches, kvcache.go:95-166).
 struct SpillTier {
-    uint8_t *base = nullptr;
+    uint8_t *base = nullptr;      // host address of slot 0
+    uint8_t *dev_base = nullptr;  // the same memory as the device addresses it (pinned tier)
+    uint8_t *bounce = nullptr;    // file tier: pinned staging the copy kernel reads / writes
+    uint8_t *dev_bounce = nullptr;
+    int64_t bounce_slots = 0;
     int64_t slots = 0;
     size_t slot_bytes = 0;
     size_t map_bytes = 0;  // non-zero: file mapping
@@ -325,6 +329,7 @@ void destroy_cache(Cache *c) {
         else
             (void)hipHostFree(c->spill.base);
     }
+    if (c->spill.bounce) (void)hipHostFree(c->spill.bounce);
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
 }
@@ -535,6 +540,56 @@ int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, cons
     *total_q = qrow;
     *max_nq = mx;
     *total_parts = part;
+    return RLX_OK;
+}
+
+// One layer's page moving between its pool page and a tier slot.
+struct PageMove {
+    int layer;
+    int32_t page;
+    int64_t slot;
+};
+
+// Copy the pages of `mv` to the tier (to_host) or back, with the page copy
+// kernel: pinned slots are addressed directly; a file tier goes through the
+// pinned staging buffer in chunks, the host copying between it and the
+// mapping around each kernel.
+int32_t copy_spill_pages(Cache *c, const std::vector<PageMove> &mv, bool to_host) {
+    SpillTier &t = c->spill;
+    if (mv.empty()) return RLX_OK;
+    const size_t b0 = page_bytes0(c), b1 = page_bytes1(c), sb = t.slot_bytes;
+    hipEvent_t e0, e1;
+    int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_COPY);
+    if (rc) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
+    const size_t chunk = t.map_bytes ? (size_t)t.bounce_slots : mv.size();
+    for (size_t i0 = 0; i0 < mv.size(); i0 += chunk) {
+        const size_t n = std::min(chunk, mv.size() - i0);
+        if (t.map_bytes && !to_host)
+            for (size_t j = 0; j < n; j++) memcpy(t.bounce + j * sb, t.base + (size_t)mv[i0 + j].slot * sb, sb);
+        std::vector<uint64_t> addr(4 * n);  // src0, dst0, src1, dst1
+        for (size_t j = 0; j < n; j++) {
+            const PageMove &m = mv[i0 + j];
+            const uint8_t *host = t.map_bytes ? t.dev_bounce + j * sb : t.dev_base + (size_t)m.slot * sb;
+            const uint8_t *d0 = (const uint8_t *)c->L[m.layer].pool0 + (size_t)m.page * b0;
+            const uint8_t *d1 = b1 ? (const uint8_t *)c->L[m.layer].pool1 + (size_t)m.page * b1 : nullptr;
+            addr[j] = (uint64_t)(to_host ? d0 : host);
+            addr[n + j] = (uint64_t)(to_host ? host : d0);
+            addr[2 * n + j] = (uint64_t)(to_host ? d1 : host + b0);
+            addr[3 * n + j] = (uint64_t)(to_host ? host + b0 : d1);
+        }
+        void *dev;
+        if ((rc = stage(c, addr.data(), addr.size() * sizeof(uint64_t), &dev))) return rc;
+        const uint64_t *a = (const uint64_t *)dev;
+        HIP_TRY(launch_page_copy(c->stream, a, a + n, (int)n, (int64_t)b0));
+        if (b1) HIP_TRY(launch_page_copy(c->stream, a + 2 * n, a + 3 * n, (int)n, (int64_t)b1));
+        if (t.map_bytes) {
+            HIP_TRY(hipStreamSynchronize(c->stream));
+            if (to_host)
+                for (size_t j = 0; j < n; j++) memcpy(t.base + (size_t)mv[i0 + j].slot * sb, t.bounce + j * sb, sb);
+        }
+    }
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
     return RLX_OK;
 }
 
@@ -809,6 +864,8 @@ int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, 
     return RLX_OK;
 }
 
+}  // extern "C"
+
 namespace {
 
 // Shared body of the fused projection + RoPE + append entry points.
@@ -892,6 +949,8 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
 }
 
 }  // namespace
+
+extern "C" {
 
 int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                                const int32_t *n_tok, const void *x, int32_t x_dtype,
@@ -1412,6 +1471,7 @@ int32_t rlx_spill_attach(void *h, const char *path, int64_t host_pages) {
         else
             HIP_TRY(hipHostFree(t.base));
     }
+    if (t.bounce) HIP_TRY(hipHostFree(t.bounce));
     t = SpillTier{};
     if (host_pages == 0) return RLX_OK;
     const size_t slot_bytes = page_bytes0(c) + page_bytes1(c);
@@ -1425,10 +1485,22 @@ int32_t rlx_spill_attach(void *h, const char *path, int64_t host_pages) {
         if (m == MAP_FAILED) return fail(RLX_ERR_INVALID, "rlx_spill_attach: cannot map %zu bytes of %s", bytes, path);
         t.base = (uint8_t *)m;
         t.map_bytes = bytes;
+        // The copy kernel cannot address a file mapping: pages pass through
+        // a pinned staging buffer of up to 64 MB.
+        t.bounce_slots = std::max<int64_t>(1, std::min<int64_t>(host_pages, (64 << 20) / (int64_t)slot_bytes));
+        void *b = nullptr;
+        HIP_TRY(hipHostMalloc(&b, (size_t)t.bounce_slots * slot_bytes, hipHostMallocDefault));
+        t.bounce = (uint8_t *)b;
+        void *db = nullptr;
+        HIP_TRY(hipHostGetDevicePointer(&db, b, 0));
+        t.dev_bounce = (uint8_t *)db;
     } else {
         void *m = nullptr;
         HIP_TRY(hipHostMalloc(&m, bytes, hipHostMallocDefault));
         t.base = (uint8_t *)m;
+        void *dm = nullptr;
+        HIP_TRY(hipHostGetDevicePointer(&dm, m, 0));
+        t.dev_base = (uint8_t *)dm;
     }
     t.slots = host_pages;
     t.slot_bytes = slot_bytes;
@@ -1457,7 +1529,7 @@ int32_t rlx_spill(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids
     }
     if (need > (int64_t)t.free_stack.size())
         return fail(RLX_ERR_POOL, "spill tier: %lld slots needed, %zu free", (long long)need, t.free_stack.size());
-    const size_t b0 = page_bytes0(c), b1 = page_bytes1(c);
+    std::vector<PageMove> mv;
     for (int i = 0; i < n_seqs; i++) {
         const int seq = seq_ids[i];
         for (int l = lo; l < hi; l++) {
@@ -1467,12 +1539,7 @@ int32_t rlx_spill(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids
                 const int32_t page = c->entry(l, seq, s.first + k);
                 const int64_t slot = t.free_stack.back();
                 t.free_stack.pop_back();
-                uint8_t *dst = t.base + (size_t)slot * t.slot_bytes;
-                HIP_TRY(hipMemcpyAsync(dst, (const uint8_t *)ls.pool0 + (size_t)page * b0, b0,
-                                       hipMemcpyDeviceToHost, c->stream));
-                if (b1)
-                    HIP_TRY(hipMemcpyAsync(dst + b0, (const uint8_t *)ls.pool1 + (size_t)page * b1, b1,
-                                           hipMemcpyDeviceToHost, c->stream));
+                mv.push_back(PageMove{l, page, slot});
                 t.held[l][seq].push_back(slot);
                 // The page is reused only by later work on this stream, which
                 // runs after the copy.
@@ -1485,9 +1552,8 @@ int32_t rlx_spill(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids
             s.pos_offset += n_pages[i] * c->P;
         }
     }
-    // A file tier holds the bytes once the call returns.
-    if (t.map_bytes) HIP_TRY(hipStreamSynchronize(c->stream));
-    return RLX_OK;
+    // (A file tier holds the bytes once this returns: the copies synchronise.)
+    return copy_spill_pages(c, mv, true);
 }
 
 int32_t rlx_restore(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids, const int32_t *n_pages) {
@@ -1521,7 +1587,7 @@ int32_t rlx_restore(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_i
             return fail(RLX_ERR_POOL, "restore needs %lld pages on layer %d, %zu free", (long long)need, l,
                         c->L[l].free_stack.size());
     }
-    const size_t b0 = page_bytes0(c), b1 = page_bytes1(c);
+    std::vector<PageMove> mv;
     for (int i = 0; i < n_seqs; i++) {
         const int seq = seq_ids[i], n = n_pages[i];
         if (n == 0) continue;
@@ -1540,12 +1606,7 @@ int32_t rlx_restore(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_i
                 const int32_t page = ls.free_stack.back();
                 ls.free_stack.pop_back();
                 c->set_entry(l, seq, s.first - n + k, page);
-                const uint8_t *src = t.base + (size_t)slot * t.slot_bytes;
-                HIP_TRY(hipMemcpyAsync((uint8_t *)ls.pool0 + (size_t)page * b0, src, b0, hipMemcpyHostToDevice,
-                                       c->stream));
-                if (b1)
-                    HIP_TRY(hipMemcpyAsync((uint8_t *)ls.pool1 + (size_t)page * b1, src + b0, b1,
-                                           hipMemcpyHostToDevice, c->stream));
+                mv.push_back(PageMove{l, page, slot});
                 t.free_stack.push_back(slot);
             }
             s.first -= n;
@@ -1556,7 +1617,7 @@ int32_t rlx_restore(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_i
     }
     // The slots may be handed out again by the next spill, whose copies
     // queue behind these on the same stream.
-    return RLX_OK;
+    return copy_spill_pages(c, mv, false);
 }
 
 int32_t rlx_spill_slots(void *h, int32_t layer, int32_t seq, int64_t *slots_out, int32_t cap, int32_t *n_out) {

@@ -78,10 +78,10 @@ class _PagedCache:
 
     def Timing(self, enable=True, kernels="attend"):
         """Bracket every later attention kernel ("attend"), projection
-        kernel ("project") or token-selection kernel ("select") with HIP
-        events."""
+        kernel ("project"), token-selection kernel ("select") or spill /
+        restore page copy ("copy") with HIP events."""
         mask = {"attend": _lib.RLX_TIME_ATTEND, "project": _lib.RLX_TIME_PROJECT,
-                "select": _lib.RLX_TIME_SELECT}[kernels]
+                "select": _lib.RLX_TIME_SELECT, "copy": _lib.RLX_TIME_COPY}[kernels]
         check(self._lib.rlx_cache_timing(self._h, mask if enable else 0))
 
     def KernelTime(self):
