@@ -34,6 +34,9 @@ WORKLOADS = {
     "gqa_cfg2": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=None, layers=8),
     # BASELINE config 3 (headline, 8k context): MLA latent decode
     "mla8k": dict(kind="mla", B=32, H=16, D=128, P=64, T=8192, layers=4),
+    # the top of the target's 8k-32k context range, same shapes at 32k
+    "gqa32k": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=32768, layers=1),
+    "mla32k": dict(kind="mla", B=32, H=16, D=128, P=64, T=32768, layers=1),
     # MLA chunked prefill, 2048 new tokens on 6144 cached
     "mla_prefill": dict(kind="mla_prefill", B=4, H=128, D=128, P=64, T=6144, n_new=2048, layers=1),
     # speculative verify stress, 4 drafts, rollback U{0..4},
@@ -443,7 +446,8 @@ def run_workload(name, steps, warmup, torch, dev):
     cfg = WORKLOADS[name]
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
                                  "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3,
-                                 "spec_accept": 6, "sample": 7, "block8k": 2, "spill8k": 2}[name])
+                                 "spec_accept": 6, "sample": 7, "block8k": 2, "spill8k": 2,
+                                 "gqa32k": 2, "mla32k": 3}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
              "spec": setup_spec, "gqa_fused": setup_gqa_fused,
              "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample,
@@ -609,7 +613,8 @@ def main():
           f"{r['kernel_rate']:.0f} {r['rate_unit']}", file=sys.stderr, flush=True)
     secondary = []
     if not args.no_secondary:
-        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "mla_prefill", "spec_stress",
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "gqa32k", "mla32k", "mla_prefill",
+                                 "spec_stress",
                                  "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample",
                                  "spill8k")
                      if w != args.workload]:
