@@ -150,12 +150,11 @@ __device__ __forceinline__ AppendTok plan_tok(const AppendTok *toks, int tok_off
 // in the arguments -- by binary search of the rows' first partial slots
 // (wave-uniform scalar loads).
 template <bool ARG>
-__device__ __forceinline__ int2 plan_work(const int2 *work, int n_rows) {
+__device__ __forceinline__ int2 plan_work(const int2 *work, int n_rows, int b) {
     if constexpr (ARG) {
         // part is field 5 of each 8-int row
         const __attribute__((address_space(4))) int32_t *p =
             (const __attribute__((address_space(4))) int32_t *)kernarg_plan();
-        const int b = blockIdx.x;
         int lo = 0, hi = n_rows - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -166,7 +165,7 @@ __device__ __forceinline__ int2 plan_work(const int2 *work, int n_rows) {
         }
         return int2{lo, b - p[lo * 8 + 5]};
     } else {
-        return work[blockIdx.x];
+        return work[b];
     }
 }
 
@@ -270,9 +269,9 @@ hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t 
 // plan: the rows in the kernel arguments (nullptr: rows and work on the device).
 hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
                              const uint16_t *vpool, const int32_t *table, const AttRow *rows,
-                             int n_rows,
-                             const int2 *work, int n_work, const void *q, int q_bf16,
-                             int layout, int H, int KVH, int hd, int P, int chunk, float qscale,
+                             int n_rows, const int4 *ranges, int n_ranges, const void *q, int q_bf16,
+                             int layout, int H, int KVH, int hd, int P, int total64, int snap64,
+                             int ranges_off, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
                              int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1);
 
@@ -312,6 +311,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+// acc + lo + hi of a packed bf16 pair in one VALU op (v_dot2c_f32_bf16
+// against (1, 1): the products are exact, f32 accumulation).
+__device__ __forceinline__ float add_bf16x2(uint32_t w, float acc) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                           __builtin_bit_cast(bf16x2_t, 0x3F803F80u), acc, false);
+}
 
 // ---- global-to-LDS rings ----------------------------------------------
 

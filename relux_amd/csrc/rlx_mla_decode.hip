@@ -156,7 +156,7 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     const int wave = tid >> 6;
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const int2 wk = plan_work<ARG>(work, n_rows);
+    const int2 wk = plan_work<ARG>(work, n_rows, blockIdx.x);
     const AttRow R = plan_row<ARG>(rows, wk.x);
     const int QR = H * R.nq;
     const int t_begin = wk.y * chunk;

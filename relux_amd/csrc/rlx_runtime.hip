@@ -508,6 +508,24 @@ int tile_keys(const AttRow &r, int mask_mode, int toks, int qt) {
 
 // One AttRow per sequence, or -- with qtile > 0 (GQA decode kernel only) --
 // one per tile of at most qtile queries, each with its own context splits.
+// Cuts of the GQA decode ranges, in units of 64 padded positions: cut i is
+// floor(i * total / n), moved onto the nearer row boundary when one lies
+// within snap units (pre: the rows' padded starts, pre.back() = total).  The
+// decode kernel computes the same cuts when its rows travel in the arguments.
+std::vector<int> gqa_range_cuts(const std::vector<int> &pre, int n, int snap) {
+    const int total = pre.back();
+    std::vector<int> cuts(n + 1);
+    for (int i = 0; i <= n; i++) {
+        const int b = (int)((int64_t)i * total / n);
+        cuts[i] = b;
+        if (b <= 0 || b >= total) continue;
+        const int r = (int)(std::upper_bound(pre.begin(), pre.end(), b) - pre.begin()) - 1;
+        const int d0 = b - pre[r], d1 = pre[r + 1] - b;
+        if (std::min(d0, d1) <= snap) cuts[i] = d0 <= d1 ? pre[r] : pre[r + 1];
+    }
+    return cuts;
+}
+
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
                    int chunk, std::vector<AttRow> &rows, std::vector<int2> &work,
                    int *total_q, int *max_nq, int *total_parts, int qtile = 0) {
@@ -1162,52 +1180,80 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     }
     const int qtile = max_qr > 32 ? 32 / G : 0;
     const int nqt = max_qr > 16 ? 2 : 1;
-    std::vector<int> units_lens;  // one entry per query tile
-    for (int i = 0; i < n_seqs; i++) {
-        const int nq = n_q ? n_q[i] : 1;
-        const int tiles = qtile ? (nq + qtile - 1) / qtile : 1;
-        for (int t = 0; t < tiles; t++) units_lens.push_back(lens[i]);
-    }
-    // One residency slot per CU: a GQA decode work-group keeps two 16-token
-    // blocks per wave in flight, and a sweep of 1, 2 and 3 work-groups per
-    // CU (8k and mixed-length contexts) found one per CU, with longer splits,
-    // as fast or faster (fewer work-group start-ups and partials).
-    const int chunk = choose_chunk(units_lens, c->kvh, (int64_t)c->cus);
     std::vector<AttRow> rows;
-    std::vector<int2> work;
+    std::vector<int2> unused;
     int total_q = 0, mnq = 0, parts = 0;
-    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts, qtile)))
+    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts, qtile)))
         return rc;
+    // Balanced ranges: the rows' tokens, each row padded to a multiple of 64,
+    // laid end to end and cut into one near-equal range per CU's worth of kv
+    // heads (work-groups = ranges x kv heads ~ CUs), cuts within 256 tokens
+    // of a row boundary moved onto it.  Every work-group then streams about
+    // the same number of tokens whatever the length mix, and one work-group
+    // per CU is the residency that measured fastest (splits by one fixed
+    // chunk left work-groups of very different sizes, and some CUs with
+    // several of them).  Partial slot of (row r, range i) = r + i.
+    std::vector<int> pre(rows.size() + 1, 0);
+    for (size_t i = 0; i < rows.size(); i++) pre[i + 1] = pre[i] + (rows[i].len + 63) / 64;
+    const int total64 = pre.back();
+    const int n_ranges = std::max(1, std::min(c->cus / c->kvh, total64));
+    constexpr int kSnap64 = 4;
+    const std::vector<int> cuts = gqa_range_cuts(pre, n_ranges, kSnap64);
+    std::vector<int4> ranges(n_ranges);
+    {
+        std::vector<int> first(rows.size(), -1);  // first range of each row
+        size_t r = 0;
+        for (int i = 0; i < n_ranges; i++) {
+            const int lo = cuts[i], hi = cuts[i + 1];
+            // first row with live tokens past lo
+            while (r < rows.size() && (int64_t)pre[r] * 64 + rows[r].len <= (int64_t)lo * 64) r++;
+            ranges[i] = int4{(int)r, r < rows.size() ? pre[r] : total64, lo, hi};
+            for (size_t k = r; k < rows.size() && pre[k] < hi; k++) {
+                if (first[k] < 0) first[k] = i;
+                rows[k].part = (int32_t)(k + first[k]);
+                rows[k].nsplit = i - first[k] + 1;
+            }
+        }
+    }
+    parts = (int)rows.size() + n_ranges;
     if ((rc = flush_patches(c))) return rc;
     const int QRP = 16 * nqt;
     const size_t po_bytes = (size_t)parts * c->kvh * QRP * c->hd * sizeof(float);
     const size_t pm_bytes = (size_t)parts * c->kvh * QRP * 2 * sizeof(float);
     if ((rc = ensure_ws(c, po_bytes + pm_bytes))) return rc;
-    // Rows travel in the kernel arguments when they fit; otherwise rows and
-    // the work list are staged to the device.
+    // Rows travel in the kernel arguments when they fit, followed by the
+    // ranges when those fit too (else the kernel recomputes its range from
+    // the rows: <= 64 rows, one per lane); otherwise rows and ranges are
+    // staged to the device.
     PlanArg plan_arg;
     const PlanArg *plan = nullptr;
     const AttRow *d_rows = nullptr;
-    const int2 *d_work = nullptr;
-    if (rows.size() * sizeof(AttRow) <= sizeof(PlanArg)) {
-        memcpy(plan_arg.b, rows.data(), rows.size() * sizeof(AttRow));
+    const int4 *d_ranges = nullptr;
+    int ranges_off = -1;
+    const size_t rows_bytes = rows.size() * sizeof(AttRow);
+    if (rows_bytes <= sizeof(PlanArg)) {
+        memcpy(plan_arg.b, rows.data(), rows_bytes);
+        if (rows_bytes + ranges.size() * sizeof(int4) <= sizeof(PlanArg)) {
+            memcpy(plan_arg.b + rows_bytes, ranges.data(), ranges.size() * sizeof(int4));
+            ranges_off = (int)rows_bytes;
+        }
         plan = &plan_arg;
     } else {
         Blob b;
-        size_t o_r = b.add(rows), o_w = b.add(work);
+        size_t o_r = b.add(rows), o_w = b.add(ranges);
         void *dev;
         if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
         d_rows = (const AttRow *)((char *)dev + o_r);
-        d_work = (const int2 *)((char *)dev + o_w);
+        d_ranges = (const int4 *)((char *)dev + o_w);
     }
     if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
     const float qscale = scale * 1.4426950408889634f;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
     HIP_TRY(launch_gqa_decode(c->stream, plan, ls.pool0, ls.pool1, c->d_table, d_rows,
-                              (int)rows.size(), d_work, (int)work.size(), q,
+                              (int)rows.size(), d_ranges, n_ranges, q,
                               q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
-                              chunk, qscale, mask_mode, nqt, (float *)c->ws,
+                              total64, kSnap64, ranges_off, qscale, mask_mode, nqt, (float *)c->ws,
                               (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
                               std::min(max_qr, 32), e0, e1));
     return RLX_OK;
