@@ -157,6 +157,42 @@ def _torch_gqa_ref(k_list, v_list, q, H, KVH):
     return torch.stack(outs)
 
 
+@pytest.mark.parametrize("n_rows,H,KVH,nq", [
+    (40, 32, 8, 1),   # rows and ranges both in the kernel arguments
+    (60, 32, 8, 1),   # rows in the arguments, ranges recomputed per work-group
+    (60, 64, 8, 4),   # the same with 32 query rows per kv head
+    (50, 8, 2, 2),    # 128 ranges: many cuts, rows shorter than a range
+    (80, 32, 8, 1),   # rows and ranges staged to the device
+])
+def test_gqa_balanced_ranges_many_rows(gpu, n_rows, H, KVH, nq):
+    """The decode work split cuts the batch's tokens into equal ranges that
+    straddle rows: ragged lengths (a few tokens to ~1.5k, some next to the
+    64-token pad boundaries where cuts snap), every plan route."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(n_rows * 10 + KVH + nq)
+    D, P = 128, 16
+    lens = rng.integers(1, 1500, size=n_rows)
+    lens[::7] = rng.integers(1, 30, size=len(lens[::7]))
+    lens[3::11] = 64 * rng.integers(1, 20, size=len(lens[3::11])) + rng.integers(-3, 4, size=len(lens[3::11]))
+    lens = [int(max(L, nq)) for L in lens]
+    c = KVCache(num_layers=1, max_len=max(lens) + 32, num_kv_heads=KVH, head_dim=D,
+                page_tokens=P, max_seqs=n_rows, device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    nqs = [nq] * n_rows
+    q = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    out = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=list(range(n_rows)), n_q=nqs,
+                   mask="causal").cpu().numpy()
+    g = H // KVH
+    off = 0
+    for i, L in enumerate(lens):
+        qs = q[off:off + nq].transpose(1, 0, 2)
+        got = out[off:off + nq].transpose(1, 0, 2)
+        exact = oracle.exact_attention_f64(qs, np.repeat(K[i], g, 0), np.repeat(V[i], g, 0),
+                                           _limits("causal", nq, L))
+        _check(got, exact, TOL_EXACT, f"row {i} len {L} vs exact")
+        off += nq
+
+
 def test_gqa_config2_full_shape(gpu):
     """B 16, H 32, KVH 8, D 128, T ~ U[512, 4096], 16-token
     pages randomly permuted in a shared pool, one append then one query."""
