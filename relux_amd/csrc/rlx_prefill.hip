@@ -370,23 +370,20 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             for (int i = 0; i < 8; i++) mx = fmaxf(mx, p[i]);
             mx = rows4_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
-            float c = 1.f;
-            if (m_new == -INFINITY) {
+            // A row that has seen only masked keys keeps m = -inf: its
+            // weights and factor come out as exact zeros (acc and l are zero).
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            const float c = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
 #pragma unroll
-                for (int i = 0; i < 8; i++) p[i] = 0.f;
-            } else {
-                c = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
-#pragma unroll
-                for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(p[i] - m_new);
-            }
+            for (int i = 0; i < 8; i++) p[i] = __builtin_amdgcn_exp2f(p[i] - m_use);
             // The P.V product consumes bf16 weights: normalise by the same ones.
             u32x4 w;
 #pragma unroll
             for (int i = 0; i < 4; i++) w[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-            float ps = 0.f;
+            float lsum = l_part[nt] * c;
 #pragma unroll
-            for (int i = 0; i < 4; i++) ps += bf16_lo(w[i]) + bf16_hi(w[i]);
-            l_part[nt] = l_part[nt] * c + ps;
+            for (int i = 0; i < 4; i++) lsum = add_bf16x2(w[i], lsum);
+            l_part[nt] = lsum;
             m_run[nt] = m_new;
             // Rescale only when some row's running max moved (c != 1).
             if (__builtin_amdgcn_ballot_w64(c != 1.f)) {
