@@ -368,20 +368,18 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
             }
             mx = rows4_max(mx);
             const float m_new = fmaxf(m_run[nt], mx);
-            float c, p[4];
-            if (m_new == -INFINITY) {
-                c = 1.f;
-                p[0] = p[1] = p[2] = p[3] = 0.f;
-            } else {
-                c = __builtin_amdgcn_exp2f(m_run[nt] - m_new);
+            // A head that has seen only masked keys keeps m = -inf: its
+            // weights and factor come out as exact zeros (acc and l are zero).
+            const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+            float p[4];
+            const float c = __builtin_amdgcn_exp2f(m_run[nt] - m_use);
 #pragma unroll
-                for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_new);
-            }
+            for (int i = 0; i < 4; i++) p[i] = __builtin_amdgcn_exp2f(sc[i] - m_use);
             // The P.V product consumes bf16 weights: normalise by the same ones.
             u32x2 pw;
             pw[0] = pack_bf16x2(p[0], p[1]);
             pw[1] = pack_bf16x2(p[2], p[3]);
-            l_part[nt] = l_part[nt] * c + ((bf16_lo(pw[0]) + bf16_hi(pw[0])) + (bf16_lo(pw[1]) + bf16_hi(pw[1])));
+            l_part[nt] = add_bf16x2(pw[1], add_bf16x2(pw[0], l_part[nt] * c));
             m_run[nt] = m_new;
             if (__builtin_amdgcn_ballot_w64(c != 1.f)) {  // some head's max moved
 #pragma unroll
