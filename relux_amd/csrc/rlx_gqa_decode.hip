@@ -143,44 +143,93 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
         first = false;
         const int QR = G * R.qn;  // query rows of this (tile of a) sequence
 
+        // Wave w walks blocks t0 = tw0 + 64 j (j < nb) of 16 tokens.  Block
+        // indices are wave-uniform (scalar), and the page ids of 64 blocks
+        // are fetched at once, one per lane, and read back with readlane: no
+        // table load sits between one block's K/V loads and the next's.
+        const int tw0 = t_begin + 16 * wv;
+        const int nb = (t_end > tw0) ? (t_end - tw0 + 63) / 64 : 0;
+        auto fetch_pages = [&](int j0) {
+            const int j = j0 + lane;
+            return (j < nb) ? table[R.tab + (tw0 + 64 * j) / P] : 0;
+        };
+        // The first page ids are requested before the query loads so that
+        // the two latencies overlap (the first block's loads wait for both).
+        int pg = fetch_pages(0);
+
         // Q^T operand (B of the score product), pre-scaled by scale*log2(e);
         // KW consecutive dims per lane (the upper half stays zero when KW = 4).
+        // Columns past the tile's query rows load row 0 (no branch around
+        // the loads, so they are all in flight together) and are zeroed.
         u32x4 qb[NQT][KS];
         int klim[NQT];
+        bool qv[NQT];
+        int64_t qbase[NQT];
 #pragma unroll
         for (int nt = 0; nt < NQT; nt++) {
             const int qr = nt * 16 + col;
-            klim[nt] = R.len - 1;
+            qv[nt] = qr < QR;
+            const int qrc = qv[nt] ? qr : 0;
+            const int ql = qrc / G;
+            const int h = kvh * G + (qrc - ql * G);
+            const int qi = R.q0 + ql;
+            klim[nt] = qv[nt] ? key_limit(mask_mode, R.len, R.nq, qi) : R.len - 1;
+            qbase[nt] = ((layout == kLayoutSHD) ? ((int64_t)(R.qrow + qi) * H + h) * D
+                                                : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D) +
+                        grp * KW;
+        }
+        auto pack_q = [&](const float (&v)[8], bool valid) {
+            u32x4 w = u32x4{0, 0, 0, 0};
+            const float sc = valid ? qscale : 0.f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) qb[nt][ks] = u32x4{0, 0, 0, 0};
-            if (qr < QR) {
-                const int ql = qr / G;
-                const int h = kvh * G + (qr - ql * G);
-                const int qi = R.q0 + ql;
-                klim[nt] = key_limit(mask_mode, R.len, R.nq, qi);
-                const int64_t base = (layout == kLayoutSHD)
-                                         ? ((int64_t)(R.qrow + qi) * H + h) * D
-                                         : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D;
+            for (int i = 0; i < KW / 2; i++)
+                w[i] = (uint32_t)bf16_rne(v[2 * i] * sc) | ((uint32_t)bf16_rne(v[2 * i + 1] * sc) << 16);
+            return w;
+        };
+        if (q_bf16) {
+            u32x4 raw[NQT][KS];
+#pragma unroll
+            for (int nt = 0; nt < NQT; nt++)
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
-                    const int64_t off = base + ks * 32 + grp * KW;
-                    float v[8];
-                    if (q_bf16) {
-#pragma unroll
-                        for (int i = 0; i < KW; i++) v[i] = bf16_f32(((const uint16_t *)q)[off + i]);
+                    const uint16_t *src = (const uint16_t *)q + qbase[nt] + ks * 32;
+                    if constexpr (K16) {
+                        const u32x2 r2 = *(const u32x2 *)src;
+                        raw[nt][ks] = u32x4{r2[0], r2[1], 0, 0};
                     } else {
-#pragma unroll
-                        for (int i = 0; i < KW; i += 4) {
-                            const float4 f = *(const float4 *)((const float *)q + off + i);
-                            v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
-                        }
+                        raw[nt][ks] = *(const u32x4 *)src;
                     }
-#pragma unroll
-                    for (int i = 0; i < KW / 2; i++)
-                        qb[nt][ks][i] = (uint32_t)bf16_rne(v[2 * i] * qscale) |
-                                        ((uint32_t)bf16_rne(v[2 * i + 1] * qscale) << 16);
                 }
-            }
+#pragma unroll
+            for (int nt = 0; nt < NQT; nt++)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    float v[8];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        v[2 * i] = bf16_lo(raw[nt][ks][i]);
+                        v[2 * i + 1] = bf16_hi(raw[nt][ks][i]);
+                    }
+                    qb[nt][ks] = pack_q(v, qv[nt]);
+                }
+        } else {
+            float4 raw[NQT][KS][2];
+#pragma unroll
+            for (int nt = 0; nt < NQT; nt++)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const float4 *src = (const float4 *)((const float *)q + qbase[nt] + ks * 32);
+                    raw[nt][ks][0] = src[0];
+                    raw[nt][ks][1] = K16 ? float4{0.f, 0.f, 0.f, 0.f} : src[1];
+                }
+#pragma unroll
+            for (int nt = 0; nt < NQT; nt++)
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const float4 x = raw[nt][ks][0], y = raw[nt][ks][1];
+                    const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+                    qb[nt][ks] = pack_q(v, qv[nt]);
+                }
         }
 
         // Smallest key limit of the work-group's columns: blocks entirely
@@ -202,16 +251,6 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
             for (int mt = 0; mt < MT; mt++) acc[nt][mt] = fl4{0.f, 0.f, 0.f, 0.f};
         }
 
-        // Wave w walks blocks t0 = tw0 + 64 j (j < nb) of 16 tokens.  Block
-        // indices are wave-uniform (scalar), and the page ids of 64 blocks
-        // are fetched at once, one per lane, and read back with readlane: no
-        // table load sits between one block's K/V loads and the next's.
-        const int tw0 = t_begin + 16 * wv;
-        const int nb = (t_end > tw0) ? (t_end - tw0 + 63) / 64 : 0;
-        auto fetch_pages = [&](int j0) {
-            const int j = j0 + lane;
-            return (j < nb) ? table[R.tab + (tw0 + 64 * j) / P] : 0;
-        };
         // The cache is streamed once: non-temporal loads keep it from
         // displacing reusable lines (measured ~12% more read bandwidth).
         auto load_block = [&](int j, int pg, u32x4(&kr)[KS], u32x2(&vr)[MT]) {
@@ -322,7 +361,6 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
         // consumed; the loop is peeled so that every load it issues is
         // unconditional (the waits then count exactly one block of loads
         // still outstanding).
-        int pg = fetch_pages(0);
         asm volatile("" ::"v"(pg));
         auto load_next = [&](int j, u32x4(&kr)[KS], u32x2(&vr)[MT]) {
             if ((j & 63) == 0) {
