@@ -438,10 +438,10 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
     }
 }
 
-// Merge the splits of one (sequence, kv head, query row): O = sum_s
-// 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the caller's layout and
-// dtype.  One block of D threads per query row; the merge weights are
-// computed once in LDS and every thread streams its dim across the splits.
+// Merge the partials (one per segment of the row) of one (row, kv head,
+// query row): O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the
+// caller's layout and dtype.  One block of D threads per query row; the merge weights are
+// computed once in LDS and every thread streams its dim across the partials.
 template <bool ARG>
 __global__ __launch_bounds__(128) void gqa_combine_kernel(
     typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
@@ -454,8 +454,8 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
     if (qr >= G * R.qn) return;
     __shared__ float fac[kMaxSplits];
     __shared__ float inv_l;
-    const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // split 0
-    const int64_t sstride = (int64_t)KVH * QRP;                    // between splits
+    const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // first partial
+    const int64_t sstride = (int64_t)KVH * QRP;                    // between partials
     merge_weights(part_ml + b0 * 2, sstride, R.nsplit, fac, &inv_l);
     __syncthreads();
     const int ql = qr / G;
