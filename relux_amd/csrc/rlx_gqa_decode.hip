@@ -442,6 +442,8 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
 // query row): O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the
 // caller's layout and dtype.  One block of D threads per query row; the merge weights are
 // computed once in LDS and every thread streams its dim across the partials.
+constexpr int kFewParts = 8;  // partials merged without LDS (one round trip)
+
 template <bool ARG>
 __global__ __launch_bounds__(128) void gqa_combine_kernel(
     typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
@@ -456,11 +458,48 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
     __shared__ float inv_l;
     const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // first partial
     const int64_t sstride = (int64_t)KVH * QRP;                    // between partials
-    merge_weights(part_ml + b0 * 2, sstride, R.nsplit, fac, &inv_l);
-    __syncthreads();
     const int ql = qr / G;
     const int h = kvh * G + (qr - ql * G);
     const int qi = R.q0 + ql;
+    const int n = R.nsplit;
+    if (n <= kFewParts) {
+        // Few partials (the usual case): every thread loads all (m, l) pairs
+        // and its dim of every partial at once -- one memory round trip, no
+        // LDS; partials past n re-read the last one and get weight 0.
+        const int d = threadIdx.x;
+        float mv[kFewParts], lv[kFewParts], ov[kFewParts];
+#pragma unroll
+        for (int s = 0; s < kFewParts; s++) {
+            const int64_t bs = b0 + (int64_t)min(s, n - 1) * sstride;
+            mv[s] = part_ml[bs * 2];
+            lv[s] = part_ml[bs * 2 + 1];
+            ov[s] = d < D ? part_o[bs * D + d] : 0.f;
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kFewParts; s++)
+            if (s < n) M = fmaxf(M, mv[s]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int s = 0; s < kFewParts; s++) {
+            const float f = (s < n && mv[s] != -INFINITY) ? __builtin_amdgcn_exp2f(mv[s] - M) : 0.f;
+            L += f * lv[s];
+            O += f * ov[s];
+        }
+        if (d < D) {
+            const float v = O * (L > 0.f ? 1.f / L : 0.f);
+            const int64_t o = (layout == kLayoutSHD)
+                                  ? ((int64_t)(R.qrow + qi) * H + h) * D + d
+                                  : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D + d;
+            if (out_bf16)
+                ((uint16_t *)out)[o] = bf16_rne(v);
+            else
+                ((float *)out)[o] = v;
+        }
+        return;
+    }
+    merge_weights(part_ml + b0 * 2, sstride, n, fac, &inv_l);
+    __syncthreads();
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float O = 0.f;
         for (int s = 0; s < R.nsplit; s++) O += fac[s] * part_o[(b0 + s * sstride) * D + d];
