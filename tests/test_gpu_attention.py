@@ -245,6 +245,11 @@ def _mla_exact(qc, qr, c, kr, w_uk, w_uv, limits):
 
 @pytest.mark.parametrize("H,lens,nq,mask", [
     (16, [1, 15, 64, 65, 200, 300], 1, "causal"),
+    # many ragged rows: decode ranges straddle rows (rows in the kernel
+    # arguments, ranges recomputed per work-group) ...
+    (16, [int(x) for x in np.random.default_rng(5).integers(1, 400, 40)], 1, "causal"),
+    # ... and more rows than the arguments hold (rows and ranges staged)
+    (8, [int(x) for x in np.random.default_rng(6).integers(2, 300, 70)], 2, "causal"),
     (16, [260, 7], 2, "causal"),
     (8, [90, 3], 3, "ref"),
     (16, [128], 1, "none"),
