@@ -14,6 +14,19 @@ Parity status per function (what pins it; see tests/test_oracle.py):
                                  error band against exp, exact value at 0.
   softmax_rows                   pinned: normalisation, -20 cutoff, argmax.
   matmul / matmul_transb         pinned: f64 brute force.
+  matmul_bf16w                   pinned: f64 brute force on non-square shapes
+                                 (a planted transposed-index read fails it),
+                                 exact integer products, k-ascending f32 sum.
+  rmsnorm                        pinned: rmsnorm_test.go known answers, f64
+                                 restatement, constant-row closed form
+                                 gamma*c/sqrt(c^2+eps) and its eps->0 limit.
+  gelu                           pinned: mlp_test.go values, f64
+                                 0.5*x*(1+erf(x/sqrt2)) via math.erf,
+                                 gelu(x)-gelu(-x) = x.
+  add_bias                       pinned: exact f32 add of widened bias.
+  ref_gqa_decode_step            pinned: equals gqa_attend and exact f64
+                                 attention at one kv head; with two, the
+                                 reference's flat head-major read.
   rope_tables / rope_apply       pinned: rope_test.go known answers, norm
                                  invariance, overflow error.
   kv_copy_into                   pinned: kvcache_test.go known answers.

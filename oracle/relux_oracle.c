@@ -18,7 +18,12 @@
  *   orc_fastexp32     - closed form 2^(x/ln2) error band and the reference's
  *        documented constants (tests/test_oracle.py).
  *   orc_softmax_rows  - rows sum to 1, cutoff at diff<-20, fastexp weights.
- *   orc_matmul*       - brute-force f64 products on small shapes.
+ *   orc_matmul*       - brute-force f64 products on small shapes
+ *        (orc_matmul_bf16w also against a planted transposed read).
+ *   orc_rmsnorm / orc_gelu_n / orc_add_bias - rmsnorm_test.go and
+ *        mlp_test.go known answers, f64 closed forms (constant row,
+ *        erf), exact bias adds.
+ *   orc_ref_gqa_decode_step - equals orc_gqa_attend at one kv head.
  *   orc_rope_*        - reference rope_test.go:10-63 known answers,
  *        rotation-norm invariance, overflow error (rope_test.go:84-95).
  *   orc_kv_copy_into  - reference kvcache_test.go:16-106 known answers.

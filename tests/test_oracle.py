@@ -268,3 +268,191 @@ def test_mla_decompress_equals_absorbed():
     # the reference's head-major read of token-major buffers differs (H > 1)
     compat = oracle.mla_attend(qc, qr, c, kr, w_uk, w_uv, "causal", head_major_compat=True)
     assert np.abs(compat - got).max() > 0.05
+
+
+# ---- matmulBatched3D (mha.go:759-785), RMSNorm, GELU, bias ---------------
+
+def _bf16w_f64(a, w_bf16):
+    """f64 brute force of a[M,K] @ widen(w[K,N]): every product and sum in
+    f64 from the widened weight bits, written as explicit loops over the
+    index roles (row i of a, column j of w) so that no library routine can
+    hide a transposition."""
+    wf = oracle.f32_from_bf16(w_bf16).astype(np.float64)
+    a64 = a.astype(np.float64)
+    M, K = a64.shape
+    N = wf.shape[1]
+    out = np.zeros((M, N))
+    for i in range(M):
+        for k in range(K):
+            out[i, :] += a64[i, k] * wf[k, :]
+    return out
+
+
+def _close_to_f64(got, want, K):
+    # f32 accumulation of K products with |terms| <~ 3: error << 1e-5 * sqrt(K)
+    return np.abs(got - want).max() <= 2e-6 * K
+
+
+def test_matmul_bf16w_against_f64_brute_force():
+    rng = np.random.default_rng(20)
+    for M, K, N in [(1, 7, 3), (5, 33, 11), (9, 64, 40), (3, 130, 17)]:
+        a = rng.normal(size=(M, K)).astype(np.float32)
+        w = oracle.bf16_from_f32(rng.normal(size=(K, N)))
+        got = oracle.matmul_bf16w(a, w)
+        assert got.shape == (M, N)
+        assert _close_to_f64(got, _bf16w_f64(a, w), K)
+        # A planted transposed-index mistake (w read as [N,K] row-major, the
+        # slip a checker and a kernel could share) fails the same check.
+        w_t = np.ascontiguousarray(w.reshape(-1)[: K * N].reshape(N, K).T)
+        bad = oracle.matmul_bf16w(a, w_t)
+        assert not _close_to_f64(bad, _bf16w_f64(a, w), K)
+    # Widening is exact: weights that are bf16 integers and integer
+    # activations give exact integer products (no rounding anywhere).
+    a = rng.integers(-8, 9, size=(4, 16)).astype(np.float32)
+    w = oracle.bf16_from_f32(rng.integers(-8, 9, size=(16, 6)).astype(np.float32))
+    assert np.array_equal(oracle.matmul_bf16w(a, w),
+                          a.astype(np.int64) @ oracle.f32_from_bf16(w).astype(np.int64))
+
+
+def test_matmul_bf16w_sums_k_ascending_in_f32():
+    # Go's loop adds k ascending in f32 (ulp(1e8) = 8, so a 1 added to 1e8
+    # is lost): the three orders below give 0, 0 and 1; a k-descending loop
+    # would give 1 for the second.
+    a = np.array([[1e8, 1.0, -1e8]], np.float32)
+    w = oracle.bf16_from_f32(np.ones((3, 1), np.float32))
+    assert oracle.matmul_bf16w(a, w)[0, 0] == 0.0
+    a = np.array([[1.0, 1e8, -1e8]], np.float32)
+    assert oracle.matmul_bf16w(a, w)[0, 0] == 0.0
+    a = np.array([[1e8, -1e8, 1.0]], np.float32)
+    assert oracle.matmul_bf16w(a, w)[0, 0] == 1.0
+
+
+def test_rmsnorm_known_answers_rmsnorm_test():
+    one = oracle.bf16_from_f32(np.ones(4, np.float32))
+    two = oracle.bf16_from_f32(np.full(4, 2.0, np.float32))
+    # rmsnorm_test.go:14-25 (hand computed), :27-39, :41-60, :62-75
+    y = oracle.rmsnorm(np.array([[1, 2, 3, 4]], np.float32), one, eps=0.0)
+    assert np.allclose(y[0], [0.3651, 0.7303, 1.0954, 1.4606], atol=1e-3)
+    y = oracle.rmsnorm(np.array([[2, 2, 2, 2]], np.float32), one, eps=0.0)
+    assert np.allclose(y[0], 1.0, atol=1e-3)
+    y = oracle.rmsnorm(np.array([[1, 2, 3, 4], [2, 2, 2, 2]], np.float32), one, eps=0.0)
+    assert np.allclose(y[0], [0.3651, 0.7303, 1.0954, 1.4606], atol=1e-3)
+    assert np.allclose(y[1], 1.0, atol=1e-3)
+    y = oracle.rmsnorm(np.array([[2, 2, 2, 2]], np.float32), two, eps=0.0)
+    assert np.allclose(y[0], 2.0, atol=1e-3)
+
+
+def test_rmsnorm_against_f64_and_closed_forms():
+    rng = np.random.default_rng(21)
+    rows, d, eps = 6, 48, 1e-5
+    x = rng.normal(0, 3, size=(rows, d)).astype(np.float32)
+    g = oracle.bf16_from_f32(rng.normal(1, 0.3, size=d))
+    gf = oracle.f32_from_bf16(g).astype(np.float64)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + eps) * gf[None, :]
+    got = oracle.rmsnorm(x, g, eps)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    # constant row c: gamma * c / sqrt(c^2 + eps)
+    for c in (0.5, -3.0, 40.0):
+        xr = np.full((1, d), c, np.float32)
+        want_c = gf * c / math.sqrt(c * c + eps)
+        assert np.allclose(oracle.rmsnorm(xr, g, eps)[0], want_c, rtol=2e-6, atol=0)
+        # eps -> 0 (here exactly 0): +-gamma by the sign of c
+        assert np.allclose(oracle.rmsnorm(xr, g, 0.0)[0], np.sign(c) * gf, rtol=2e-6, atol=0)
+    # eps enters under the root: a planted eps-outside-the-root variant
+    # (x / (rms + eps)) misses the constant-row closed form at small c.
+    c, big_eps = 0.01, 1e-4
+    xr = np.full((1, d), c, np.float32)
+    ok = gf * c / math.sqrt(c * c + big_eps)
+    planted = gf * c / (abs(c) + big_eps)
+    assert np.allclose(oracle.rmsnorm(xr, g, big_eps)[0], ok, rtol=2e-6)
+    assert not np.allclose(planted, ok, rtol=1e-3)
+    # rows are normalised independently and scale-invariant (eps = 0)
+    y1 = oracle.rmsnorm(x, g, 0.0)
+    y2 = oracle.rmsnorm(x * np.float32(4.0), g, 0.0)
+    assert np.allclose(y1, y2, rtol=1e-6, atol=1e-6)
+
+
+def test_gelu_against_erf_closed_form():
+    # mlp_test.go:30-52: gelu(1) ~ 0.8413; gelu(0) = 0; gelu(-1) ~ -0.1587
+    assert abs(oracle.gelu(np.array([1.0], np.float32))[0] - 0.8413) < 1e-4
+    assert abs(oracle.gelu(np.array([-1.0], np.float32))[0] + 0.1587) < 1e-4
+    assert oracle.gelu(np.array([0.0], np.float32))[0] == 0.0
+    x = np.linspace(-8, 8, 4001, dtype=np.float32)
+    want = np.array([0.5 * float(v) * (1 + math.erf(float(v) / math.sqrt(2))) for v in x])
+    got = oracle.gelu(x)
+    assert np.abs(got - want).max() <= 4e-7 * np.abs(x).max()
+    # gelu(x) - gelu(-x) = x (odd part of x*Phi(x)); exact up to f32 rounding
+    assert np.allclose(got - oracle.gelu(-x), x, rtol=0, atol=2e-6)
+    # large |x|: identity and zero tails
+    assert oracle.gelu(np.array([10.0], np.float32))[0] == 10.0
+    assert oracle.gelu(np.array([-10.0], np.float32))[0] == 0.0
+
+
+def test_add_bias_exact():
+    rng = np.random.default_rng(22)
+    y = rng.normal(size=(5, 9)).astype(np.float32)
+    b = oracle.bf16_from_f32(rng.normal(size=9))
+    got = oracle.add_bias(y, b)
+    want = (y + oracle.f32_from_bf16(b)[None, :]).astype(np.float32)   # one f32 add each
+    assert np.array_equal(got, want)
+    # the bias broadcasts over rows by column (i % outDim in linear.go:99-101)
+    assert not np.array_equal(got, (y + oracle.f32_from_bf16(b)[:5, None].repeat(9, 1)))
+
+
+# ---- the CPU-baseline port (mha.go:283-348) ------------------------------
+
+def _baseline_case(KVH, H, D, T, cap, seed):
+    rng = np.random.default_rng(seed)
+    rows = rng.normal(size=(T, KVH * D)).astype(np.float32)
+    kb = np.zeros(cap * KVH * D, np.uint16)
+    vb = np.zeros(cap * KVH * D, np.uint16)
+    vrows = rng.normal(size=(T, KVH * D)).astype(np.float32)
+    oracle.kv_copy_into(kb, rows[: T - 1], 0, T - 1, KVH * D)
+    oracle.kv_copy_into(vb, vrows[: T - 1], 0, T - 1, KVH * D)
+    q = rng.normal(size=(H, D)).astype(np.float32)
+    return rows, vrows, kb, vb, q
+
+
+@pytest.mark.parametrize("H,T", [(4, 33), (8, 100)])
+def test_ref_gqa_decode_step_one_kv_head(H, T):
+    # With one kv head the reference's head-major read of its token-major
+    # buffer is the logical layout, so one decode step is plain attention of
+    # q over all T cached rows (the new row included).
+    KVH, D, cap = 1, 16, 160
+    rows, vrows, kb, vb, q = _baseline_case(KVH, H, D, T, cap, 23)
+    newlen, out = oracle.ref_gqa_decode_step(kb, vb, cap, T - 1, rows[T - 1], vrows[T - 1], q,
+                                             H, KVH, D)
+    assert newlen == T
+    k = oracle.round_bf16(rows).reshape(1, T, D)
+    v = oracle.round_bf16(vrows).reshape(1, T, D)
+    # the appended row's bytes are BF16FromF32 of the new row
+    assert np.array_equal(kb[(T - 1) * D: T * D], oracle.bf16_from_f32(rows[T - 1]))
+    same = oracle.gqa_attend(q[:, None, :], k, v, "causal")[:, 0, :]
+    assert np.array_equal(out, same)
+    exact = oracle.exact_attention_f64(q[:, None, :], np.repeat(k, H, 0), np.repeat(v, H, 0),
+                                       [T - 1])[:, 0, :]
+    err = np.abs(out - exact)
+    assert err.max() < 0.1 and err.mean() < 0.02
+
+
+def test_ref_gqa_decode_step_reads_flat_buffer_head_major():
+    # With two kv heads the reference indexes the widened buffer as
+    # [KVH][T][D] although rows were stored token-major: kv head h reads the
+    # flat elements [h*T*D, (h+1)*T*D).  The port reproduces that read.
+    KVH, H, D, T, cap = 2, 4, 8, 21, 64
+    rows, vrows, kb, vb, q = _baseline_case(KVH, H, D, T, cap, 24)
+    _, out = oracle.ref_gqa_decode_step(kb, vb, cap, T - 1, rows[T - 1], vrows[T - 1], q,
+                                        H, KVH, D)
+    kflat = oracle.round_bf16(rows).reshape(-1)[: KVH * T * D].reshape(KVH, T, D)
+    vflat = oracle.round_bf16(vrows).reshape(-1)[: KVH * T * D].reshape(KVH, T, D)
+    g = H // KVH
+    exact = oracle.exact_attention_f64(q[:, None, :], np.repeat(kflat, g, 0),
+                                       np.repeat(vflat, g, 0), [T - 1])[:, 0, :]
+    err = np.abs(out - exact)
+    assert err.max() < 0.1 and err.mean() < 0.02
+    logical = oracle.round_bf16(rows).reshape(T, KVH, D).transpose(1, 0, 2)
+    vlog = oracle.round_bf16(vrows).reshape(T, KVH, D).transpose(1, 0, 2)
+    corrected = oracle.exact_attention_f64(q[:, None, :], np.repeat(logical, g, 0),
+                                           np.repeat(vlog, g, 0), [T - 1])[:, 0, :]
+    assert np.abs(out - corrected).max() > 0.1
