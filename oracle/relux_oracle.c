@@ -95,14 +95,21 @@ void orc_softmax_rows(float *m, int rows, int cols) {
     }
 }
 
-/* matmul.go:15-27 -- C[M,N] = A[M,K] @ B[K,N], k ascending, f32 acc. */
+/* matmul.go:15-27 -- C[M,N] = A[M,K] @ B[K,N], k ascending, f32 acc.
+ * Every C[i][j] is the reference's `sum += a*b` chain (0 first, then k
+ * ascending, one f32 multiply and one f32 add per step); the loops only run
+ * the chains of one row side by side (k outer, j inner) so that B is read
+ * row by row.  The result is bit-identical to the i,j,k loop. */
 void orc_matmul(float *out, const float *a, const float *b, int M, int K, int N) {
-    for (int i = 0; i < M; i++)
-        for (int j = 0; j < N; j++) {
-            float sum = 0.0f;
-            for (int k = 0; k < K; k++) sum += a[(int64_t)i * K + k] * b[(int64_t)k * N + j];
-            out[(int64_t)i * N + j] = sum;
+    for (int i = 0; i < M; i++) {
+        float *o = out + (int64_t)i * N;
+        for (int j = 0; j < N; j++) o[j] = 0.0f;
+        for (int k = 0; k < K; k++) {
+            const float aik = a[(int64_t)i * K + k];
+            const float *bk = b + (int64_t)k * N;
+            for (int j = 0; j < N; j++) o[j] += aik * bk[j];
         }
+    }
 }
 
 /* matmul.go:32-44 -- C[M,N] = A[M,K] @ B[N,K]^T, k ascending. */
@@ -115,15 +122,14 @@ void orc_matmul_transb(float *out, const float *a, const float *b, int M, int K,
         }
 }
 
-/* mha.go:759-785 (pure-Go branch) -- out[M,N] = a[M,K] @ widen(bf16 b[K,N]). */
+/* mha.go:759-785 (pure-Go branch) -- out[M,N] = a[M,K] @ widen(bf16 b[K,N]).
+ * Same chains as orc_matmul (k ascending from 0, separate f32 multiply and
+ * add), run row-side-by-side on a widened copy of b. */
 void orc_matmul_bf16w(float *out, const float *a, const uint16_t *b, int M, int K, int N) {
-    for (int i = 0; i < M; i++)
-        for (int j = 0; j < N; j++) {
-            float sum = 0.0f;
-            for (int k = 0; k < K; k++)
-                sum += a[(int64_t)i * K + k] * orc_f32_from_bf16(b[(int64_t)k * N + j]);
-            out[(int64_t)i * N + j] = sum;
-        }
+    float *bw = (float *)malloc(sizeof(float) * (size_t)K * N);
+    for (int64_t e = 0; e < (int64_t)K * N; e++) bw[e] = orc_f32_from_bf16(b[e]);
+    orc_matmul(out, a, bw, M, K, N);
+    free(bw);
 }
 
 /* rope.go:50-75 -- theta_i = f32(1 / f32(pow(base, 2i/d))), angle =
