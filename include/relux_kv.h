@@ -244,6 +244,23 @@ int32_t rlx_gqa_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t
                        int32_t qo_layout, float scale, int32_t mask_mode, void *out,
                        int32_t out_dtype);
 
+/* rlx_gqa_attend for decode and verify calls, allocating nothing: no
+ * reference counterpart.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as rlx_gqa_attend; the
+ * split partials go to a fixed 32 MiB scratch array per device (held until
+ * the process ends) instead of the cache's workspace, pending page-table
+ * writes travel in kernel arguments, and no staging buffer is used.  Limits
+ * (RLX_ERR_UNSUPPORTED beyond them, nothing launched): at most 32 query rows
+ * per kv head, at most 64 rows (sequences, or query tiles of head_dim 16/32
+ * calls), partials within the scratch.  rlx_init(device) must have run.
+ * Every call on a device shares its scratch: calls that overlap on one
+ * device (different streams) race. */
+int32_t rlx_gqa_attend_noalloc(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_q, int32_t num_heads, const void *q,
+                               int32_t q_dtype, int32_t qo_layout, float scale, int32_t mask_mode,
+                               void *out, int32_t out_dtype);
+
 /* MLA absorbed decode / chunked prefill.  q_nope [rows][num_heads][head_dim],
  * q_rope [rows][num_heads][d_r] (post-RoPE), w_uk and w_uv bf16
  * [d_c][num_heads*head_dim] exactly as MLA.W_UK/W_UV are stored (mla.go:42-43),

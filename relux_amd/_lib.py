@@ -88,6 +88,8 @@ SIGNATURES = {
     "rlx_kv_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],
     "rlx_mla_gather": [_vp, _i32, _i32, _pi32, _vp, _vp],
     "rlx_gqa_attend": [_vp, _i32, _i32, _pi32, _pi32, _i32, _vp, _i32, _i32, _f32, _i32, _vp, _i32],
+    "rlx_gqa_attend_noalloc": [_vp, _i32, _i32, _pi32, _pi32, _i32, _vp, _i32, _i32, _f32, _i32,
+                               _vp, _i32],
     "rlx_mla_attend": [_vp, _i32, _i32, _pi32, _pi32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _f32,
                        _i32, _vp, _i32],
     "rlx_rollback": [_vp, _i32, _i32, _pi32, _pi32],

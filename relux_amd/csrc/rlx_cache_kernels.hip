@@ -22,6 +22,23 @@ hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n) {
     return hipGetLastError();
 }
 
+// Table patches carried in the kernel arguments (at most kPlanArgBytes / 8
+// per launch): no device copy of the patch list is needed.
+__global__ __launch_bounds__(256) void patch_plan_kernel(PlanArg plan, int32_t *__restrict__ table, int n) {
+    const int i = threadIdx.x;
+    if (i < n) {
+        const Patch p = plan_patch<true>(nullptr, i);
+        table[p.idx] = p.val;
+    }
+}
+
+hipError_t launch_patch_plan(hipStream_t s, int32_t *table, const PlanArg &plan, int n) {
+    if (n <= 0) return hipSuccess;
+    if (n > kPlanArgBytes / (int)sizeof(Patch)) return hipErrorInvalidValue;
+    patch_plan_kernel<<<1, 256, 0, s>>>(plan, table, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n) {
     if (n <= 0) return hipSuccess;
     fill_i32_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dst, val, n);

@@ -242,6 +242,7 @@ hipError_t launch_spec_accept(hipStream_t s, const SpecArgs &a, int n_rows);
 
 // ---- launchers (stream-ordered, return hipError_t of the launch) ----------
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
+hipError_t launch_patch_plan(hipStream_t s, int32_t *table, const PlanArg &plan, int n);
 hipError_t launch_fill_i32(hipStream_t s, int32_t *dst, int32_t val, int64_t n);
 // Page copies (spill tier): copy i moves `bytes` from src[i] to dst[i]; the
 // pointer arrays are device-readable.

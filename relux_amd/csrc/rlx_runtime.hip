@@ -30,7 +30,19 @@
 
 using namespace rlx;
 
+// Scratch of rlx_gqa_attend_noalloc: the split partials of a decode call
+// live here instead of in a workspace the library allocates.  One copy per
+// device, held until the process ends; every no-alloc call on a device
+// shares it, so calls that overlap on one device (different streams) race.
+// Host code never uses the array's name as an address: rlx_init looks up
+// each device's copy with hipGetSymbolAddress and keeps it in g_scratch.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+void *g_scratch[kMaxDevices];  // per device: address of its `scratch` copy
 
 thread_local std::string g_err;
 
@@ -217,6 +229,24 @@ int32_t flush_patches(Cache *c) {
     int32_t rc = stage(c, b.bytes.data(), b.bytes.size(), &dev);
     if (rc) return rc;
     HIP_TRY(launch_patch(c->stream, c->d_table, (const Patch *)dev, (int)p.size()));
+    return RLX_OK;
+}
+
+// Apply pending table patches through the kernel arguments (up to 256 per
+// launch): no staging slot, so nothing is allocated.
+int32_t flush_patches_inline(Cache *c) {
+    constexpr int kPer = kPlanArgBytes / (int)sizeof(Patch);
+    while (!c->pending.empty()) {
+        PlanArg pa;
+        int n = 0;
+        auto it = c->pending.begin();
+        for (; it != c->pending.end() && n < kPer; ++it, ++n) {
+            const Patch p{(int32_t)it->first, it->second};
+            memcpy(pa.b + n * sizeof(Patch), &p, sizeof p);
+        }
+        HIP_TRY(launch_patch_plan(c->stream, c->d_table, pa, n));
+        c->pending.erase(c->pending.begin(), it);
+    }
     return RLX_OK;
 }
 
@@ -512,18 +542,83 @@ int tile_keys(const AttRow &r, int mask_mode, int toks, int qt) {
 // floor(i * total / n), moved onto the nearer row boundary when one lies
 // within snap units (pre: the rows' padded starts, pre.back() = total).  The
 // decode kernel computes the same cuts when its rows travel in the arguments.
-std::vector<int> gqa_range_cuts(const std::vector<int> &pre, int n, int snap) {
-    const int total = pre.back();
-    std::vector<int> cuts(n + 1);
+void gqa_range_cuts(const int *pre, int n_rows, int n, int snap, int *cuts) {
+    const int total = pre[n_rows];
     for (int i = 0; i <= n; i++) {
         const int b = (int)((int64_t)i * total / n);
         cuts[i] = b;
         if (b <= 0 || b >= total) continue;
-        const int r = (int)(std::upper_bound(pre.begin(), pre.end(), b) - pre.begin()) - 1;
+        const int r = (int)(std::upper_bound(pre, pre + n_rows + 1, b) - pre) - 1;
         const int d0 = b - pre[r], d1 = pre[r + 1] - b;
         if (std::min(d0, d1) <= snap) cuts[i] = d0 <= d1 ? pre[r] : pre[r + 1];
     }
-    return cuts;
+}
+
+// Rows of a GQA decode call: one AttRow per sequence or, with qtile > 0,
+// per tile of at most qtile queries.  Writes the first `cap` rows into
+// rows[] and the number needed into *n_out (callers size or reject by it).
+int32_t gqa_decode_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
+                        int qtile, AttRow *rows, int cap, int *n_out) {
+    const LayerState &ls = c->L[layer];
+    int n = 0, qrow = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        const SeqState &s = ls.seqs[seq_ids[i]];
+        const int nq = n_q ? n_q[i] : 1;
+        if (s.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
+        if (nq < 1 || nq > s.len)
+            return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, s.len);
+        const int step = qtile > 0 ? qtile : nq;
+        for (int q0 = 0; q0 < nq; q0 += step, n++) {
+            if (n >= cap) continue;
+            AttRow &r = rows[n];
+            r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
+            r.len = s.len;
+            r.nq = nq;
+            r.qrow = qrow;
+            r.nsplit = 1;
+            r.part = n;
+            r.q0 = q0;
+            r.qn = std::min(step, nq - q0);
+        }
+        qrow += nq;
+    }
+    *n_out = n;
+    return RLX_OK;
+}
+
+// Balanced ranges of the GQA decode split: the rows' tokens, each row padded
+// to a multiple of 64, laid end to end and cut into one near-equal range per
+// CU's worth of kv heads (work-groups = ranges x kv heads ~ CUs), cuts within
+// kGqaSnap64 units of a row boundary moved onto it.  Every work-group then
+// streams about the same number of tokens whatever the length mix, and one
+// work-group per CU is the residency that measured fastest (splits by one
+// fixed chunk left work-groups of very different sizes, and some CUs with
+// several of them).  Fills ranges[] (first row, its padded start, [lo, hi)
+// in 64-position units) and every row's part / nsplit (partial slot of
+// (row r, range i) = r + i); pre[n_rows + 1] and cuts[n_ranges + 1] are the
+// caller's scratch.  Returns the number of ranges (at most cus / kvh).
+constexpr int kGqaSnap64 = 4;
+int gqa_decode_split(const Cache *c, AttRow *rows, int n_rows, int *pre, int *cuts, int4 *ranges,
+                     int *total64_out) {
+    pre[0] = 0;
+    for (int i = 0; i < n_rows; i++) pre[i + 1] = pre[i] + (rows[i].len + 63) / 64;
+    const int total64 = pre[n_rows];
+    const int n_ranges = std::max(1, std::min(c->cus / c->kvh, total64));
+    gqa_range_cuts(pre, n_rows, n_ranges, kGqaSnap64, cuts);
+    for (int k = 0; k < n_rows; k++) rows[k].part = -1;
+    int r = 0;
+    for (int i = 0; i < n_ranges; i++) {
+        const int lo = cuts[i], hi = cuts[i + 1];
+        // first row with live tokens past lo
+        while (r < n_rows && (int64_t)pre[r] * 64 + rows[r].len <= (int64_t)lo * 64) r++;
+        ranges[i] = int4{r, r < n_rows ? pre[r] : total64, lo, hi};
+        for (int k = r; k < n_rows && pre[k] < hi; k++) {
+            if (rows[k].part < 0) rows[k].part = k + i;
+            rows[k].nsplit = i - (rows[k].part - k) + 1;
+        }
+    }
+    *total64_out = total64;
+    return n_ranges;
 }
 
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
@@ -625,6 +720,14 @@ int32_t rlx_init(int32_t device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(RLX_ERR_UNSUPPORTED, "device %d is %s; librelux_kv is built for gfx950", device,
                     prop.gcnArchName);
+    if (device >= kMaxDevices) return fail(RLX_ERR_UNSUPPORTED, "device %d >= %d", device, kMaxDevices);
+    if (!g_scratch[device]) {
+        // This device's copy of the no-alloc scratch (the device is current).
+        void *p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(RLX_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+        g_scratch[device] = p;
+    }
     return RLX_OK;
 }
 
@@ -1096,13 +1199,14 @@ int32_t rlx_mla_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     return RLX_OK;
 }
 
-int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
-                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
-                       int32_t out_dtype) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_attend on an MLA cache");
+}  // extern "C"
+
+namespace {
+// Argument checks shared by the GQA attention entry points.
+int32_t check_gqa_attend(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                         int32_t num_heads, int32_t q_dtype, int32_t qo_layout, int32_t mask_mode,
+                         int32_t out_dtype) {
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "GQA attention on an MLA cache");
     int32_t rc = check_layer(c, layer, false);
     if (rc) return rc;
     if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
@@ -1112,6 +1216,21 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
     if (qo_layout != RLX_LAYOUT_HSD && qo_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "qo_layout");
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
+    return RLX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                       int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout,
+                                  mask_mode, out_dtype);
+    if (rc) return rc;
     if (n_seqs == 0) return RLX_OK;
     if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
     const int G = num_heads / c->kvh;
@@ -1180,42 +1299,18 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     }
     const int qtile = max_qr > 32 ? 32 / G : 0;
     const int nqt = max_qr > 16 ? 2 : 1;
-    std::vector<AttRow> rows;
-    std::vector<int2> unused;
-    int total_q = 0, mnq = 0, parts = 0;
-    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts, qtile)))
+    int n_rows = 0;
+    if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, nullptr, 0, &n_rows))) return rc;
+    std::vector<AttRow> rows(n_rows);
+    if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, rows.data(), n_rows, &n_rows)))
         return rc;
-    // Balanced ranges: the rows' tokens, each row padded to a multiple of 64,
-    // laid end to end and cut into one near-equal range per CU's worth of kv
-    // heads (work-groups = ranges x kv heads ~ CUs), cuts within 256 tokens
-    // of a row boundary moved onto it.  Every work-group then streams about
-    // the same number of tokens whatever the length mix, and one work-group
-    // per CU is the residency that measured fastest (splits by one fixed
-    // chunk left work-groups of very different sizes, and some CUs with
-    // several of them).  Partial slot of (row r, range i) = r + i.
-    std::vector<int> pre(rows.size() + 1, 0);
-    for (size_t i = 0; i < rows.size(); i++) pre[i + 1] = pre[i] + (rows[i].len + 63) / 64;
-    const int total64 = pre.back();
-    const int n_ranges = std::max(1, std::min(c->cus / c->kvh, total64));
-    constexpr int kSnap64 = 4;
-    const std::vector<int> cuts = gqa_range_cuts(pre, n_ranges, kSnap64);
-    std::vector<int4> ranges(n_ranges);
-    {
-        std::vector<int> first(rows.size(), -1);  // first range of each row
-        size_t r = 0;
-        for (int i = 0; i < n_ranges; i++) {
-            const int lo = cuts[i], hi = cuts[i + 1];
-            // first row with live tokens past lo
-            while (r < rows.size() && (int64_t)pre[r] * 64 + rows[r].len <= (int64_t)lo * 64) r++;
-            ranges[i] = int4{(int)r, r < rows.size() ? pre[r] : total64, lo, hi};
-            for (size_t k = r; k < rows.size() && pre[k] < hi; k++) {
-                if (first[k] < 0) first[k] = i;
-                rows[k].part = (int32_t)(k + first[k]);
-                rows[k].nsplit = i - first[k] + 1;
-            }
-        }
-    }
-    parts = (int)rows.size() + n_ranges;
+    std::vector<int> pre(n_rows + 1), cuts(c->cus + 2);
+    std::vector<int4> ranges(c->cus + 1);
+    int total64 = 0;
+    const int n_ranges = gqa_decode_split(c, rows.data(), n_rows, pre.data(), cuts.data(),
+                                          ranges.data(), &total64);
+    ranges.resize(n_ranges);
+    const int parts = n_rows + n_ranges;
     if ((rc = flush_patches(c))) return rc;
     const int QRP = 16 * nqt;
     const size_t po_bytes = (size_t)parts * c->kvh * QRP * c->hd * sizeof(float);
@@ -1250,12 +1345,78 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const float qscale = scale * 1.4426950408889634f;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
-    HIP_TRY(launch_gqa_decode(c->stream, plan, ls.pool0, ls.pool1, c->d_table, d_rows,
-                              (int)rows.size(), d_ranges, n_ranges, q,
-                              q_dtype == RLX_BF16, qo_layout, num_heads, c->kvh, c->hd, c->P,
-                              total64, kSnap64, ranges_off, qscale, mask_mode, nqt, (float *)c->ws,
-                              (float *)((char *)c->ws + po_bytes), out, out_dtype == RLX_BF16,
-                              std::min(max_qr, 32), e0, e1));
+    HIP_TRY(launch_gqa_decode(c->stream, plan, ls.pool0, ls.pool1, c->d_table, d_rows, n_rows,
+                              d_ranges, n_ranges, q, q_dtype == RLX_BF16, qo_layout, num_heads,
+                              c->kvh, c->hd, c->P, total64, kGqaSnap64, ranges_off, qscale,
+                              mask_mode, nqt, (float *)c->ws, (float *)((char *)c->ws + po_bytes),
+                              out, out_dtype == RLX_BF16, std::min(max_qr, 32), e0, e1));
+    return RLX_OK;
+}
+
+int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                               int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                               int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout,
+                                  mask_mode, out_dtype);
+    if (rc) return rc;
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    void *scr = (c->device >= 0 && c->device < kMaxDevices) ? g_scratch[c->device] : nullptr;
+    if (!scr) return fail(RLX_ERR_STATE, "no scratch address for device %d (rlx_init not run)", c->device);
+    const int G = num_heads / c->kvh;
+    int max_nq = 0;
+    for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    const int max_qr = G * max_nq;
+    // Decode and verify calls only: the FA2 path's work lists are staged.
+    const bool fa2 = (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
+    if (max_qr > 32 && (fa2 || G > 32))
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_attend_noalloc takes at most 32 query rows per kv head (got %d); "
+                    "use rlx_gqa_attend", max_qr);
+    const int qtile = max_qr > 32 ? 32 / G : 0;
+    const int nqt = max_qr > 16 ? 2 : 1;
+    // Rows (and ranges when they fit) travel in the kernel arguments.
+    constexpr int kRowCap = kPlanArgBytes / (int)sizeof(AttRow);
+    constexpr int kRangeCap = 1024;
+    AttRow rows[kRowCap];
+    int n_rows = 0;
+    if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, rows, kRowCap, &n_rows))) return rc;
+    if (n_rows > kRowCap)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_attend_noalloc takes at most %d rows (sequences or query tiles), got %d",
+                    kRowCap, n_rows);
+    if (c->cus / c->kvh > kRangeCap) return fail(RLX_ERR_UNSUPPORTED, "%d CUs", c->cus);
+    int pre[kRowCap + 1], cuts[kRangeCap + 1];
+    int4 ranges[kRangeCap];
+    int total64 = 0;
+    const int n_ranges = gqa_decode_split(c, rows, n_rows, pre, cuts, ranges, &total64);
+    const int QRP = 16 * nqt;
+    const size_t parts = (size_t)n_rows + n_ranges;
+    const size_t po_bytes = parts * c->kvh * QRP * c->hd * sizeof(float);
+    const size_t pm_bytes = parts * c->kvh * QRP * 2 * sizeof(float);
+    if (po_bytes + pm_bytes > kNoAllocScratchBytes)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_attend_noalloc: call needs %zu scratch bytes, the scratch holds %zu",
+                    po_bytes + pm_bytes, kNoAllocScratchBytes);
+    if ((rc = flush_patches_inline(c))) return rc;
+    PlanArg plan;
+    const size_t rows_bytes = (size_t)n_rows * sizeof(AttRow);
+    memcpy(plan.b, rows, rows_bytes);
+    int ranges_off = -1;
+    if (rows_bytes + (size_t)n_ranges * sizeof(int4) <= sizeof(PlanArg)) {
+        memcpy(plan.b + rows_bytes, ranges, (size_t)n_ranges * sizeof(int4));
+        ranges_off = (int)rows_bytes;
+    }
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+    HIP_TRY(launch_gqa_decode(c->stream, &plan, c->L[layer].pool0, c->L[layer].pool1, c->d_table,
+                              nullptr, n_rows, nullptr, n_ranges, q, q_dtype == RLX_BF16, qo_layout,
+                              num_heads, c->kvh, c->hd, c->P, total64, kGqaSnap64, ranges_off,
+                              scale * 1.4426950408889634f, mask_mode, nqt, (float *)scr,
+                              (float *)((char *)scr + po_bytes), out, out_dtype == RLX_BF16,
+                              std::min(max_qr, 32), nullptr, nullptr));
     return RLX_OK;
 }
 

@@ -290,6 +290,23 @@ class KVCache(_PagedCache):
                                        _dev(out, "out"), _dtype_code(out)))
         return out
 
+    def AttendNoAlloc(self, layer_idx, q, num_heads, out, seq_ids=(0,), n_q=None, layout="SHD",
+                      scale=None, mask="causal"):
+        """Attend for decode / verify calls through rlx_gqa_attend_noalloc:
+        the library allocates nothing (split partials in its fixed per-device
+        scratch).  The caller provides `out`.  Same results as Attend."""
+        seq_ids = list(seq_ids)
+        if n_q is None:
+            n_q = [1] * len(seq_ids)
+        if q.numel() != sum(n_q) * num_heads * self.head_dim or out.numel() != q.numel():
+            raise ValueError("q / out size does not match sum(n_q) x num_heads x head_dim")
+        check(self._lib.rlx_gqa_attend_noalloc(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                               i32_array(n_q), num_heads, _dev(q, "q"),
+                                               _dtype_code(q), _LAYOUTS[layout],
+                                               float(scale or 0.0), _MASKS[mask], _dev(out, "out"),
+                                               _dtype_code(out)))
+        return out
+
 
     def ProjectAppend(self, layer_idx, x, w_packed, num_heads, rope=None, seq_ids=(0,), n_tok=None,
                       rope_mode="offset", q_dtype=torch.float32):
