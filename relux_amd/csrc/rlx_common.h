@@ -409,9 +409,9 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
-                             int total_q, int max_nq, int P, int chunk, float qscale,
-                             int mask_mode, int nqt, uint16_t *qlat, float *part_o,
-                             float *part_ml, float *olat, void *out, int out_bf16,
+                             int total_q, int max_nq, int P, float qscale,
+                             int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
+                             float *part_ml, void *out, int out_bf16, int cus,
                              hipEvent_t ev0, hipEvent_t ev1);
 
 }  // namespace rlx

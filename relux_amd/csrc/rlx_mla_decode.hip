@@ -124,6 +124,14 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
 // = 4 rows x one 32-B chunk pair) see 4 distinct chunk pairs.
 __device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
+// Token bounds of a row's splits: split s of n covers [b(s), b(s + 1)) with
+// b(s) = floor(s * len / n) rounded down to a 16-token tile (b(n) = len), so
+// a row's splits differ by at most one tile.  The host keeps n <= len / 64,
+// so no split is empty.
+__device__ __forceinline__ int mla_split_bound(int len, int n, int s) {
+    return s >= n ? len : (int)(((int64_t)s * len / n) & ~(int64_t)15);
+}
+
 // Shape per query-row tile count: 4 waves and two work-groups per CU (80 KB
 // of LDS each); a 4-stage ring for up to 16 query rows, 3 stages for 32.
 template <int NQT> struct MlaShape {
@@ -139,7 +147,7 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ pool,
     const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
     const int2 *__restrict__ work, int n_rows, const uint16_t *__restrict__ qlat, int H, int P,
-    int chunk, int mask_mode, float *__restrict__ part_o, float *__restrict__ part_ml) {
+    int mask_mode, uint16_t *__restrict__ part_o, float *__restrict__ part_ml) {
     using SH = MlaShape<NQT>;
     constexpr int NW = SH::NW, S = SH::S, CH = SH::CH, MT = CH / 16;
     constexpr int QRP = 16 * NQT;
@@ -159,8 +167,8 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     const int2 wk = plan_work<ARG>(work, n_rows, blockIdx.x);
     const AttRow R = plan_row<ARG>(rows, wk.x);
     const int QR = H * R.nq;
-    const int t_begin = wk.y * chunk;
-    const int t_end = min(R.len, t_begin + chunk);
+    const int t_begin = mla_split_bound(R.len, R.nsplit, wk.y);
+    const int t_end = mla_split_bound(R.len, R.nsplit, wk.y + 1);
     const int ntiles = (t_end - t_begin + 15) / 16;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t *)ring;
 
@@ -404,9 +412,15 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     for (int nt = 0; nt < NQT; nt++) {
         const int qr = nt * 16 + col;
         const float lt = rows4_sum(l_part[nt]);
-        float *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * CH;
+        // The unnormalised latent partial is stored as bf16 (the merge weighs
+        // and sums it in f32): half the bytes of the split's write burst.
+        uint16_t *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * CH;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) __builtin_nontemporal_store(acc[nt][mt], (fl4 *)(po + mt * 16 + grp * 4));
+        for (int mt = 0; mt < MT; mt++) {
+            const u32x2 pk = {pack_bf16x2(acc[nt][mt][0], acc[nt][mt][1]),
+                              pack_bf16x2(acc[nt][mt][2], acc[nt][mt][3])};
+            __builtin_nontemporal_store(pk, (u32x2 *)(po + mt * 16 + grp * 4));
+        }
         if (wave == 0 && grp == 0) {
             float *pm = part_ml + ((int64_t)pidx * QRP + qr) * 2;
             pm[0] = m_run[nt];
@@ -415,130 +429,202 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     }
 }
 
-// Merge the splits of one (sequence, query, head) into the normalised latent
-// output o_lat[row][h][0:512] (f32 workspace).  One 256-thread block per
-// query row; each thread owns channels t and t + 256 and loads them from up
-// to 16 splits at once (issued before the merge weights are read, so the two
-// round trips overlap); wave 0 computes the merge weights in LDS.
+// Row of the call that holds global query row q: binary search on the
+// rows' first query rows (field qrow), from the arguments or the device.
 template <bool ARG>
-__global__ __launch_bounds__(256) void mla_combine_kernel(
-    typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
-    const float *__restrict__ part_o, const float *__restrict__ part_ml, int H, int QRP,
-    float *__restrict__ olat) {
-    constexpr int SB = 16;  // splits per batch of loads
-    const AttRow R = plan_row<ARG>(rows, blockIdx.x);
-    const int qi = blockIdx.y / H;
-    const int h = blockIdx.y - qi * H;
-    if (qi >= R.nq) return;
-    const int qr = qi * H + h;
-    __shared__ float fac[kMaxSplits];
-    __shared__ float inv_l;
-    const int64_t b0 = (int64_t)R.part * QRP + qr;
-    const int c = threadIdx.x;
-    const float *src = part_o + b0 * kMlaDc + c;
-    const int64_t sstride = (int64_t)QRP * kMlaDc;
-    float v0[SB], v1[SB];
-#pragma unroll
-    for (int i = 0; i < SB; i++) {
-        const int64_t o = (int64_t)min(i, R.nsplit - 1) * sstride;
-        v0[i] = src[o];
-        v1[i] = src[o + 256];
-    }
-    merge_weights(part_ml + b0 * 2, QRP, R.nsplit, fac, &inv_l);
-    __syncthreads();
-    float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < SB; i++) {
-        if (i < R.nsplit) {
-            o0 += fac[i] * v0[i];
-            o1 += fac[i] * v1[i];
+__device__ __forceinline__ int plan_qrow_row(const AttRow *rows, int n_rows, int q) {
+    int lo = 0, hi = n_rows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        int first;
+        if constexpr (ARG) {
+            const __attribute__((address_space(4))) int32_t *p =
+                (const __attribute__((address_space(4))) int32_t *)kernarg_plan();
+            first = p[mid * 8 + 3];
+        } else {
+            first = rows[mid].qrow;
         }
+        if (first <= q)
+            lo = mid;
+        else
+            hi = mid - 1;
     }
-    for (int s0 = SB; s0 < R.nsplit; s0 += SB) {
-#pragma unroll
-        for (int i = 0; i < SB; i++) {
-            const int64_t o = (int64_t)min(s0 + i, R.nsplit - 1) * sstride;
-            v0[i] = src[o];
-            v1[i] = src[o + 256];
-        }
-#pragma unroll
-        for (int i = 0; i < SB; i++) {
-            if (s0 + i < R.nsplit) {
-                o0 += fac[s0 + i] * v0[i];
-                o1 += fac[s0 + i] * v1[i];
-            }
-        }
-    }
-    float *dst = olat + ((int64_t)(R.qrow + qi) * H + h) * kMlaDc;
-    dst[c] = o0 * inv_l;
-    dst[c + 256] = o1 * inv_l;
+    return lo;
 }
 
-// out[row][h][d] = sum_c o_lat[row][h][c] * W_UV[c][h*D + d].  Block = (head,
-// 16 output dims, 16 query rows); wave w takes latent channels
-// [128w, 128w + 128) of the C[16 dims][16 rows] tile (MFMA 16x16x16) and the
-// four partial tiles are summed in LDS.  A = 4 consecutive channels of one
-// dim per lane, from the block's W_UV slice [512 c][16 d] staged in LDS and
-// read with the LDS transpose read; B = 4 consecutive channels of one o_lat
-// row per lane straight from memory (f32, entered as hi + lo bf16).  All
-// global loads are issued before the first product.
-__global__ __launch_bounds__(256) void mla_proj_kernel(const float *__restrict__ olat,
-                                                       const uint16_t *__restrict__ w_uv,
-                                                       int H, int D, int total_q,
-                                                       void *__restrict__ out, int out_bf16) {
-    constexpr int KB = kMlaDc / 16 / 4;  // k-steps per wave
-    __shared__ __attribute__((aligned(16))) uint16_t wt[kMlaDc * 16];
-    __shared__ fl4 red[3][64];
+// The step after the split loop, for head h and RPB consecutive query rows
+// of the call: merge each query row's split partials into the normalised
+// latent output
+//   o_lat = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s     (512 channels)
+// and project it, out[d] = sum_c o_lat[c] * W_UV[c][h*D + d] (mla.go:384-389
+// applies W_UV to P.V; here it applies to the merged latent, the same sum
+// by linearity).  The RPB rows share one read of the head's W_UV slice.
+// Every global load is issued at the start, so the block costs one memory
+// round trip: thread t loads channels 2t, 2t+1 (bf16 pair) of up to 16
+// splits per row, and -- as thread (g, o) of G channel groups x D/8 dim
+// octets -- 8 consecutive W_UV dims of each of its group's first WB
+// channels (16 B per load).  Wave j computes row j's merge weights in LDS,
+// o_lat goes to LDS, each thread accumulates its 8 dims over its channels
+// with f32 FMAs of the exactly widened bf16 weights, and the groups are
+// summed in LDS.
+template <int D>
+struct MlaOutShape {
+    static constexpr int OCT = D / 8;                              // dim octets
+    static constexpr int G = (256 / OCT >= 32) ? 32 : (256 / OCT >= 16) ? 16 : 8;  // channel groups
+    static constexpr int CPG = kMlaDc / G;                         // channels per group
+    static constexpr int WB = CPG < 32 ? CPG : (D >= 192 ? 16 : 32);  // weight rows loaded up front
+};
+
+template <int D, int RPB, bool ARG>
+__global__ __launch_bounds__(256) void mla_out_kernel(
+    typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows, int n_rows, int total_q, int one_q,
+    const uint16_t *__restrict__ part_o, const float *__restrict__ part_ml,
+    const uint16_t *__restrict__ w_uv, int H, int QRP, void *__restrict__ out, int out_bf16) {
+    using SH = MlaOutShape<D>;
+    constexpr int SB = 16;  // splits per batch of loads
+    constexpr int OCT = SH::OCT, G = SH::G, CPG = SH::CPG, WB = SH::WB;
+    static_assert(G * CPG == kMlaDc && G * OCT <= 256, "groups x octets must fit the block");
+    static_assert(RPB <= 4, "one wave computes each row's merge weights");
     const int h = blockIdx.x;
-    const int d0 = blockIdx.y * 16;
-    const int r0 = blockIdx.z * 16;
+    const int q0 = blockIdx.y * RPB;
+    __shared__ float fac[RPB][kMaxSplits];
+    __shared__ float inv_l[RPB];
+    __shared__ float olat[RPB][kMlaDc];
+    __shared__ float red[G][RPB][D];
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int col = lane & 15, grp = lane >> 4;
-    u32x4 w[4];
-    const uint16_t *ws = w_uv + (int64_t)h * D + d0 + (t & 1) * 8;
+    const int g = t / OCT, o = t - g * OCT;
+    const bool wt = g < G;  // thread takes part in the projection
+    // W_UV rows g * CPG + k, dims h*D + 8 o .. + 8
+    const uint16_t *wp = w_uv + (int64_t)(wt ? g : 0) * CPG * H * D + (int64_t)h * D + o * 8;
+    const int64_t wstride = (int64_t)H * D;
+    u32x4 w[WB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) w[i] = *(const u32x4 *)(ws + (int64_t)((t >> 1) + 128 * i) * H * D);
-    const int row = min(r0 + col, total_q - 1);
-    const float *ob = olat + ((int64_t)row * H + h) * kMlaDc + wave * 128 + grp * 4;
-    float4 f[KB];
+    for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + k * wstride);
+    // The block's query rows: row (sequence) of the call, query index, first
+    // partial (query row qr of slot part), splits.
+    int64_t b0[RPB];
+    int ns[RPB];
+    int64_t ob[RPB];
+    bool live[RPB];
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++) f[kb] = *(const float4 *)(ob + kb * 16);
-#pragma unroll
-    for (int i = 0; i < 4; i++) *(u32x4 *)(wt + ((t >> 1) + 128 * i) * 16 + (t & 1) * 8) = w[i];
-    __syncthreads();
-    // Transpose read: lane (grp, col) fetches 4 dims of channel row
-    // 4 grp + col / 4 and receives dim col of channels 4 grp .. 4 grp + 3.
-    const uint16_t *tr = wt + (wave * 128 + 4 * grp + (col >> 2)) * 16 + (col & 3) * 4;
-    fl4 acc = fl4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < KB; kb++) {
-        const sh4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) sh4 *)(tr + kb * 16 * 16));
-        uint16_t hx, lx, hy, ly, hz, lz, hw, lw;
-        split_bf16(f[kb].x, hx, lx);
-        split_bf16(f[kb].y, hy, ly);
-        split_bf16(f[kb].z, hz, lz);
-        split_bf16(f[kb].w, hw, lw);
-        const u32x2 bh = u32x2{(uint32_t)hx | ((uint32_t)hy << 16), (uint32_t)hz | ((uint32_t)hw << 16)};
-        const u32x2 bl = u32x2{(uint32_t)lx | ((uint32_t)ly << 16), (uint32_t)lz | ((uint32_t)lw << 16)};
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(sh4, bh), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, __builtin_bit_cast(sh4, bl), acc, 0, 0, 0);
+    for (int j = 0; j < RPB; j++) {
+        const int q = min(q0 + j, total_q - 1);
+        live[j] = q0 + j < total_q;
+        // one query per row (decode): query row q is row q
+        const AttRow R = plan_row<ARG>(rows, one_q ? q : plan_qrow_row<ARG>(rows, n_rows, q));
+        const int qi = q - R.qrow;
+        b0[j] = (int64_t)R.part * QRP + qi * H + h;
+        ns[j] = R.nsplit;
+        ob[j] = ((int64_t)q * H + h) * D;
     }
-    if (wave > 0) red[wave - 1][lane] = acc;
+    const int64_t sstride = (int64_t)QRP * kMlaDc;  // bf16 between split slots
+    uint32_t v[RPB][SB];
+#pragma unroll
+    for (int j = 0; j < RPB; j++) {
+        const uint16_t *src = part_o + b0[j] * kMlaDc + 2 * t;
+#pragma unroll
+        for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(i, ns[j] - 1) * sstride);
+    }
+    // merge weights of row j by wave j: fac = 2^(m_s - M), inv_l = 1 / sum fac l
+    if (wave < RPB) {
+        // (m, l) of split s0 = lane (+ 64 k): one 8-byte load each
+        const int j = wave;
+        const float2 *ml = (const float2 *)(part_ml + b0[j] * 2);
+        const int64_t st = QRP;
+        float M = -INFINITY;
+        float2 ml0 = make_float2(-INFINITY, 0.f);
+        if (lane < ns[j]) ml0 = ml[lane * st];
+        M = ml0.x;
+        for (int s0 = lane + 64; s0 < ns[j]; s0 += 64) M = fmaxf(M, ml[s0 * st].x);
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
+        float L = 0.f;
+        if (lane < ns[j]) {
+            const float f = (ml0.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml0.x - M);
+            fac[j][lane] = f;
+            L = f * ml0.y;
+        }
+        for (int s0 = lane + 64; s0 < ns[j]; s0 += 64) {
+            const float2 e = ml[s0 * st];
+            const float f = (e.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(e.x - M);
+            fac[j][s0] = f;
+            L += f * e.y;
+        }
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) L += __shfl_xor(L, k);
+        if (lane == 0) inv_l[j] = (L > 0.f) ? 1.f / L : 0.f;
+    }
     __syncthreads();
-    if (wave > 0) return;
-    acc = ((acc + red[0][lane]) + red[1][lane]) + red[2][lane];
-    // C[4 grp + i][col]: dims d0 + 4 grp + i of row r0 + col.
-    if (r0 + col < total_q) {
-        const int64_t o = ((int64_t)(r0 + col) * H + h) * D + d0 + 4 * grp;
-        if (out_bf16) {
-            u32x2 o2;
-            o2[0] = (uint32_t)bf16_rne(acc[0]) | ((uint32_t)bf16_rne(acc[1]) << 16);
-            o2[1] = (uint32_t)bf16_rne(acc[2]) | ((uint32_t)bf16_rne(acc[3]) << 16);
-            *(u32x2 *)((uint16_t *)out + o) = o2;
-        } else {
-            *(fl4 *)((float *)out + o) = acc;
+#pragma unroll
+    for (int j = 0; j < RPB; j++) {
+        const uint16_t *src = part_o + b0[j] * kMlaDc + 2 * t;
+        float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            if (i < ns[j]) {
+                o0 += fac[j][i] * bf16_lo(v[j][i]);
+                o1 += fac[j][i] * bf16_hi(v[j][i]);
+            }
+        }
+        for (int s0 = SB; s0 < ns[j]; s0 += SB) {
+#pragma unroll
+            for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(s0 + i, ns[j] - 1) * sstride);
+#pragma unroll
+            for (int i = 0; i < SB; i++) {
+                if (s0 + i < ns[j]) {
+                    o0 += fac[j][s0 + i] * bf16_lo(v[j][i]);
+                    o1 += fac[j][s0 + i] * bf16_hi(v[j][i]);
+                }
+            }
+        }
+        olat[j][2 * t] = o0 * inv_l[j];
+        olat[j][2 * t + 1] = o1 * inv_l[j];
+    }
+    __syncthreads();
+    float a[RPB][8];
+#pragma unroll
+    for (int j = 0; j < RPB; j++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[j][i] = 0.f;
+    const int cb = (wt ? g : 0) * CPG;
+    auto fma8 = [&](const u32x4 &wv, int c) {
+#pragma unroll
+        for (int j = 0; j < RPB; j++) {
+            const float x = olat[j][c];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[j][2 * i] += x * bf16_lo(wv[i]);
+                a[j][2 * i + 1] += x * bf16_hi(wv[i]);
+            }
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < WB; k++) fma8(w[k], cb + k);
+    for (int k0 = WB; k0 < CPG; k0 += WB) {
+#pragma unroll
+        for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + (k0 + k) * wstride);
+#pragma unroll
+        for (int k = 0; k < WB; k++) fma8(w[k], cb + k0 + k);
+    }
+    if (wt) {
+#pragma unroll
+        for (int j = 0; j < RPB; j++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) red[g][j][o * 8 + i] = a[j][i];
+    }
+    __syncthreads();
+    if (t < D) {
+#pragma unroll
+        for (int j = 0; j < RPB; j++) {
+            if (!live[j]) continue;
+            float val = red[0][j][t];
+#pragma unroll
+            for (int k = 1; k < G; k++) val += red[k][j][t];
+            if (out_bf16)
+                ((uint16_t *)out)[ob[j] + t] = bf16_rne(val);
+            else
+                ((float *)out)[ob[j] + t] = val;
         }
     }
 }
@@ -546,10 +632,37 @@ __global__ __launch_bounds__(256) void mla_proj_kernel(const float *__restrict__
 template <int NQT, bool ARG>
 static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uint16_t *pool,
                          const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
-                         int n_work, const uint16_t *qlat, int H, int P, int chunk, int mask_mode,
-                         float *part_o, float *part_ml) {
-    mla_decode_kernel<NQT, ARG><<<n_work, 64 * MlaShape<NQT>::NW, 0, s>>>(plan, pool, table, rows, work, n_rows, qlat,
-                                                        H, P, chunk, mask_mode, part_o, part_ml);
+                         int n_work, const uint16_t *qlat, int H, int P, int mask_mode,
+                         uint16_t *part_o, float *part_ml) {
+    mla_decode_kernel<NQT, ARG><<<n_work, 64 * MlaShape<NQT>::NW, 0, s>>>(
+        plan, pool, table, rows, work, n_rows, qlat, H, P, mask_mode, part_o, part_ml);
+}
+
+template <int D, bool ARG>
+static void launch_mla_out_d(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
+                             int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
+                             const uint16_t *w_uv, int H, int QRP, void *out, int out_bf16, int cus) {
+    // Two query rows per block share the W_UV read when that still leaves a
+    // block per CU.
+    if ((int64_t)H * ((total_q + 1) / 2) >= cus)
+        mla_out_kernel<D, 2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
+            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, QRP, out, out_bf16);
+    else
+        mla_out_kernel<D, 1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
+            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, QRP, out, out_bf16);
+}
+
+template <bool ARG>
+static void launch_mla_out(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
+                           int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
+                           const uint16_t *w_uv, int H, int hd, int QRP, void *out, int out_bf16,
+                           int cus) {
+    switch (hd) {
+        case 64: launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
+        case 128: launch_mla_out_d<128, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
+        case 192: launch_mla_out_d<192, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
+        default: launch_mla_out_d<256, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
+    }
 }
 
 hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,
@@ -557,9 +670,9 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
                              const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
-                             int total_q, int max_nq, int P, int chunk, float qscale,
-                             int mask_mode, int nqt, uint16_t *qlat, float *part_o,
-                             float *part_ml, float *olat, void *out, int out_bf16,
+                             int total_q, int max_nq, int P, float qscale,
+                             int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
+                             float *part_ml, void *out, int out_bf16, int cus,
                              hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
     if (hd > 256 || hd % 64 != 0) return hipErrorInvalidValue;
@@ -575,30 +688,26 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     if (ev0) (void)hipEventRecord(ev0, s);
     if (nqt != 1 && nqt != 2) return hipErrorInvalidValue;
     if (plan && nqt == 1)
-        launch_mla_t<1, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P, chunk,
+        launch_mla_t<1, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                               mask_mode, part_o, part_ml);
     else if (plan)
-        launch_mla_t<2, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P, chunk,
+        launch_mla_t<2, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                               mask_mode, part_o, part_ml);
     else if (nqt == 1)
         launch_mla_t<1, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                               chunk, mask_mode, part_o, part_ml);
+                               mask_mode, part_o, part_ml);
     else
         launch_mla_t<2, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                               chunk, mask_mode, part_o, part_ml);
+                               mask_mode, part_o, part_ml);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
     if (plan)
-        mla_combine_kernel<true><<<dim3(n_rows, max_nq * H), 256, 0, s>>>(*plan, rows, part_o,
-                                                                          part_ml, H, 16 * nqt, olat);
+        launch_mla_out<true>(s, *plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd,
+                             16 * nqt, out, out_bf16, cus);
     else
-        mla_combine_kernel<false><<<dim3(n_rows, max_nq * H), 256, 0, s>>>(
-            NoPlan{0}, rows, part_o, part_ml, H, 16 * nqt, olat);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    mla_proj_kernel<<<dim3(H, hd / 16, (total_q + 15) / 16), 256, 0, s>>>(olat, w_uv, H, hd,
-                                                                         total_q, out, out_bf16);
+        launch_mla_out<false>(s, NoPlan{0}, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd,
+                              16 * nqt, out, out_bf16, cus);
     return hipGetLastError();
 }
 

@@ -427,69 +427,35 @@ int32_t plan_append(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, con
     return RLX_OK;
 }
 
-// Context split (tokens per work-group, a multiple of 64).  A decode launch
-// is bandwidth-bound with few work-groups per CU, so the best split is the
-// smallest one whose work-groups all fit in ONE residency round of the GPU
-// (slots = CUs x resident work-groups per CU): every CU then streams until
-// the end and none idles behind a partial last round.  When even one split
-// per sequence overflows the slots, splits are sized for about four rounds
-// so that unequal sequence lengths still balance.  At most kMaxSplits splits
-// per sequence (the merge kernel's weight buffer).
-int choose_chunk(const std::vector<int> &lens, int units, int64_t slots) {
+// Context splits of the MLA decode, per row: nsplit_r = ceil(len_r /
+// target) with target = ceil(sum of lengths / (slots - rows)) tokens (at
+// least kMlaMinSplit), so that the work-groups -- sum of nsplit_r <= slots,
+// the CUs times the work-groups one CU holds -- fit one residency round and
+// none holds more than `target` tokens, whatever the mix of lengths.  A
+// row's splits are near-equal (mla_split_bound in the kernel); at most
+// len / 64 and kMaxSplits splits per row.
+constexpr int kMlaMinSplit = 128;
+std::vector<int> mla_splits(const std::vector<int> &lens, int64_t slots) {
     static const int64_t slot_override = [] {
         const char *e = getenv("RLX_DECODE_SLOTS");  // tuning override
         return e ? (int64_t)atoll(e) : (int64_t)0;
     }();
-    if (slot_override > 0) slots = slot_override;
-    static const int chunk_override = [] {
-        const char *e = getenv("RLX_DECODE_CHUNK");  // tuning override
+    static const int min_override = [] {
+        const char *e = getenv("RLX_DECODE_MIN_SPLIT");  // tuning override
         return e ? atoi(e) : 0;
     }();
-    int max_len = 1;
-    for (int L : lens) max_len = std::max(max_len, L);
-    auto r64 = [](int64_t x) { return (int)((x + 63) / 64 * 64); };
-    const int lo_chunk = std::max(64, r64(((int64_t)max_len + kMaxSplits - 1) / kMaxSplits));
-    const int hi_chunk = std::max(lo_chunk, r64(max_len));
-    if (chunk_override > 0) return std::min(hi_chunk, std::max(lo_chunk, r64(chunk_override)));
-    auto count = [&](int ch) {
-        int64_t n = 0;
-        for (int L : lens) n += (L + ch - 1) / ch;
-        return n * units;
-    };
-    // Cost model in token units per slot: a work-group costs its tokens plus
-    // a fixed c0 (Q load, wave merge, partial write); one residency round
-    // lasts as long as its largest split; several rounds cost the average
-    // per-slot work plus one split of tail.
-    constexpr double c0 = 400.0;
-    double work = 0.0;
-    for (int L : lens) work += (double)L * units;
-    int best = hi_chunk;
-    double best_est = 1e300;
-    if (count(hi_chunk) <= slots) {
-        int lo = lo_chunk / 64, hi = hi_chunk / 64;
-        if (count(lo_chunk) <= slots) {
-            hi = lo;
-        } else {
-            while (hi - lo > 1) {  // smallest split that still fits one round
-                const int mid = (lo + hi) / 2;
-                if (count(mid * 64) <= slots)
-                    hi = mid;
-                else
-                    lo = mid;
-            }
-        }
-        best = hi * 64;
-        best_est = best + c0;
+    if (slot_override > 0) slots = slot_override;
+    const int min_split = min_override > 0 ? min_override : kMlaMinSplit;
+    int64_t total = 0;
+    for (int L : lens) total += L;
+    const int64_t free_slots = std::max<int64_t>(1, slots - (int64_t)lens.size());
+    const int64_t target = std::max<int64_t>(min_split, (total + free_slots - 1) / free_slots);
+    std::vector<int> n(lens.size());
+    for (size_t i = 0; i < lens.size(); i++) {
+        const int64_t want = (lens[i] + target - 1) / target;
+        n[i] = (int)std::max<int64_t>(1, std::min<int64_t>({want, lens[i] / 64, kMaxSplits}));
     }
-    for (int ch = 256; ch <= hi_chunk; ch *= 2) {
-        if (ch < lo_chunk) continue;
-        const double est = (work + c0 * (double)count(ch)) / (double)slots + ch + c0;
-        if (est < best_est) {
-            best_est = est;
-            best = ch;
-        }
-    }
-    return best;
+    return n;
 }
 
 // Prefill work order for the 8 XCDs.  Work-group b runs on XCD b % 8 and
@@ -621,9 +587,11 @@ int gqa_decode_split(const Cache *c, AttRow *rows, int n_rows, int *pre, int *cu
     return n_ranges;
 }
 
+// One AttRow per sequence of an attention call, with nsplit[i] context
+// splits (nullptr: one) and its work items (row, split).
 int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, const int32_t *n_q,
-                   int chunk, std::vector<AttRow> &rows, std::vector<int2> &work,
-                   int *total_q, int *max_nq, int *total_parts, int qtile = 0) {
+                   const int *nsplit, std::vector<AttRow> &rows, std::vector<int2> &work,
+                   int *total_q, int *max_nq, int *total_parts) {
     LayerState &ls = c->L[layer];
     int qrow = 0, part = 0, mx = 0;
     for (int i = 0; i < n_seqs; i++) {
@@ -632,21 +600,18 @@ int32_t build_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, cons
         if (s.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
         if (nq < 1 || nq > s.len)
             return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, s.len);
-        const int step = qtile > 0 ? qtile : nq;
-        for (int q0 = 0; q0 < nq; q0 += step) {
-            AttRow r;
-            r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
-            r.len = s.len;
-            r.nq = nq;
-            r.qrow = qrow;
-            r.nsplit = chunk > 0 ? (s.len + chunk - 1) / chunk : 1;
-            r.part = part;
-            r.q0 = q0;
-            r.qn = std::min(step, nq - q0);
-            for (int sp = 0; sp < r.nsplit; sp++) work.push_back(int2{(int)rows.size(), sp});
-            rows.push_back(r);
-            part += r.nsplit;
-        }
+        AttRow r;
+        r.tab = (int32_t)(c->row_base(layer, seq_ids[i]) + s.first);
+        r.len = s.len;
+        r.nq = nq;
+        r.qrow = qrow;
+        r.nsplit = nsplit ? nsplit[i] : 1;
+        r.part = part;
+        r.q0 = 0;
+        r.qn = nq;
+        for (int sp = 0; sp < r.nsplit; sp++) work.push_back(int2{(int)rows.size(), sp});
+        rows.push_back(r);
+        part += r.nsplit;
         qrow += nq;
         mx = std::max(mx, nq);
     }
@@ -1253,7 +1218,7 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         std::vector<AttRow> rows;
         std::vector<int2> unused;
         int total_q = 0, mnq = 0, parts = 0;
-        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
+        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, nullptr, rows, unused, &total_q, &mnq, &parts)))
             return rc;
         const int toks = kPrefillRows / G;
         std::vector<std::vector<int4>> groups;
@@ -1454,7 +1419,7 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         std::vector<AttRow> rows;
         std::vector<int2> unused;
         int total_q = 0, mnq = 0, parts = 0;
-        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, 0, rows, unused, &total_q, &mnq, &parts)))
+        if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, nullptr, rows, unused, &total_q, &mnq, &parts)))
             return rc;
         std::vector<int2> dwork;
         std::vector<std::vector<int4>> pgroups;
@@ -1521,19 +1486,21 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     }
     const int nqt = max_qr > 16 ? 2 : 1;
     // One work-group covers every head of a sequence's split.
-    const int chunk = choose_chunk(lens, 1, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
+    for (int i = 0; i < n_seqs; i++)
+        if (lens[i] <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
+    const std::vector<int> nsplit = mla_splits(lens, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
     std::vector<AttRow> rows;
     std::vector<int2> work;
     int total_q = 0, mnq = 0, parts = 0;
-    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, chunk, rows, work, &total_q, &mnq, &parts)))
+    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, nsplit.data(), rows, work, &total_q, &mnq,
+                         &parts)))
         return rc;
     if ((rc = flush_patches(c))) return rc;
     const int QRP = 16 * nqt;
     const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
-    const size_t po_bytes = (size_t)parts * QRP * kMlaDc * sizeof(float);
+    const size_t po_bytes = ((size_t)parts * QRP * kMlaDc * sizeof(uint16_t) + 255) & ~(size_t)255;
     const size_t pm_bytes = ((size_t)parts * QRP * 2 * sizeof(float) + 255) & ~(size_t)255;
-    const size_t ol_bytes = (size_t)total_q * num_heads * kMlaDc * sizeof(float);
-    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes + ol_bytes))) return rc;
+    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes))) return rc;
     PlanArg plan_arg;
     const PlanArg *plan = nullptr;
     const AttRow *d_rows = nullptr;
@@ -1558,10 +1525,9 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                               (int)work.size(), q_nope,
                               q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
                               (const uint16_t *)w_uv, num_heads, head_dim, total_q, max_nq, c->P,
-                              chunk, qscale, mask_mode, nqt, (uint16_t *)ws,
-                              (float *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes),
-                              (float *)(ws + ql_bytes + po_bytes + pm_bytes), out,
-                              out_dtype == RLX_BF16, e0, e1));
+                              qscale, mask_mode, nqt, (uint16_t *)ws,
+                              (uint16_t *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes), out,
+                              out_dtype == RLX_BF16, c->cus, e0, e1));
     return RLX_OK;
 }
 
