@@ -377,6 +377,7 @@ struct PrefillArgs {
     void *out;
     int q_bf16, layout, out_bf16, mask_mode;
     int H, KVH, P;
+    int pshift;  // log2(P) when P is a power of two, else -1
     float qscale;
 };
 

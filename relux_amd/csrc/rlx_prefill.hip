@@ -69,7 +69,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     static_assert(K_CH % 256 == 0 && V_CH % 256 == 0 && KCH % 8 == 0, "stage shape");
     __shared__ __attribute__((aligned(16))) uint16_t ring[S * ST_CH * 8];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // wave is uniform: branches on it are scalar branches, not exec masks
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, grp = lane >> 4;
     const int4 wk = a.work[blockIdx.x];
     if (wk.x < 0) return;  // padding item of the XCD-balanced work order
@@ -121,16 +122,20 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         else
             v_off[i] = (int64_t)v_d[i] * R.nsplit + v_lc[i] * 8;
     }
+    // Page index and slot of key t: shifts when the page size is a power of
+    // two (a.pshift >= 0), else a division.
+    auto pdiv = [&](int t) { return a.pshift >= 0 ? t >> a.pshift : t / a.P; };
+    auto pmod = [&](int t) { return a.pshift >= 0 ? t & (a.P - 1) : t % a.P; };
     auto issue_block = [&](int j) {
         const int k0 = j * kKeyBlock;
         // Keys k0..k0+15 and k0+16..k0+31 each lie in one page (P is a
         // multiple of 16); both page ids are wave-uniform scalar loads.
         int pg0 = 0, pg1 = 0;
         if (SRC == kSrcPaged || DQK > 128) {  // dense: rope keys live in the pages
-            pg0 = table[R.tab + k0 / a.P];
-            pg1 = (k0 + 16 < R.len) ? table[R.tab + (k0 + 16) / a.P] : pg0;
+            pg0 = table[R.tab + pdiv(k0)];
+            pg1 = (k0 + 16 < R.len) ? table[R.tab + pdiv(k0 + 16)] : pg0;
         }
-        const int s0 = k0 % a.P, s1 = (k0 + 16) % a.P;
+        const int s0 = pmod(k0), s1 = pmod(k0 + 16);
         const uint32_t stage = ring_lds + (uint32_t)((j % S) * ST_CH * 16);
         if (k0 + kKeyBlock <= R.len) {
             // Every key of the block is live.
@@ -180,11 +185,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             const int pg = (t - k0 < 16) ? pg0 : pg1;
             const uint16_t *g;
             if (SRC == kSrcPaged)
-                g = a.kpool + ((int64_t)pg * a.KVH + hg) * a.P * DQK + k_page_off(t % a.P, lc * 8, DQK);
+                g = a.kpool + ((int64_t)pg * a.KVH + hg) * a.P * DQK + k_page_off(pmod(t), lc * 8, DQK);
             else if (lc < 16)
                 g = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit + t) * 128 + lc * 8;
             else
-                g = a.kpool + ((int64_t)pg * a.P + (t % a.P)) * kMlaRow + kMlaDc + (lc - 16) * 8;
+                g = a.kpool + ((int64_t)pg * a.P + pmod(t)) * kMlaRow + kMlaDc + (lc - 16) * 8;
             lds_dma16(g, __builtin_amdgcn_readfirstlane(stage + (uint32_t)((i * 4 + w4) * 64) * 16));
         }
         } else {
@@ -196,7 +201,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             const uint16_t *g;
             if (SRC == kSrcPaged) {
                 const int pg = (t - k0 < 16) ? pg0 : pg1;
-                g = a.vpool + (((int64_t)pg * a.KVH + hg) * DV + d) * a.P + (t % a.P);
+                g = a.vpool + (((int64_t)pg * a.KVH + hg) * DV + d) * a.P + pmod(t);
             } else {
                 g = a.vt + (int64_t)R.part * a.H * 128 + ((int64_t)hg * 128 + d) * R.nsplit + t;
             }

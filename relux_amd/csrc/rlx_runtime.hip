@@ -1256,6 +1256,7 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         a.H = num_heads;
         a.KVH = c->kvh;
         a.P = c->P;
+        a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
         a.qscale = scale * 1.4426950408889634f;
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
@@ -1478,6 +1479,7 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         a.H = num_heads;
         a.KVH = num_heads;
         a.P = c->P;
+        a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
         a.qscale = scale * 1.4426950408889634f;
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
