@@ -95,17 +95,20 @@ __device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src
     }
 }
 
-// GQA append.  Thread = (token, kv head, 8-dim chunk).  K goes to its page
-// (k_page_off layout) with one 16-byte store; V goes to a dim-major page (8 strided 2-byte
-// stores).  The first n_patch threads also apply the table patches; the
-// scatter itself takes its destinations from the plan, not the table.
+// GQA append.  Thread = (token, kv head, 8-dim chunk of the stored head
+// dim hd).  K goes to its page (k_page_off layout) with one 16-byte store; V
+// goes to a dim-major page (8 strided 2-byte stores).  The caller's rows
+// hold hdi <= hd dims (a multiple of 8); the stored dims past hdi are
+// written as zeros.  The first n_patch threads also apply the table
+// patches; the scatter itself takes its destinations from the plan, not the
+// table.
 template <bool ARG>
 __global__ void kv_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__restrict__ kpool,
                                  uint16_t *__restrict__ vpool, int32_t *__restrict__ table,
                                  const Patch *__restrict__ patches, int n_patch,
                                  const AppendTok *__restrict__ toks, int tok_off, int n_tok,
                                  const void *__restrict__ k_src, const void *__restrict__ v_src,
-                                 int src_bf16, int layout, int kvh, int hd, int P) {
+                                 int src_bf16, int layout, int kvh, int hd, int hdi, int P) {
     int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid < n_patch) {
         const Patch pt = plan_patch<ARG>(patches, (int)gid);
@@ -122,12 +125,14 @@ __global__ void kv_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__rest
     const int j = t - tk.seq_row0;  // row within its sequence
     int64_t src_off;
     if (layout == kLayoutSHD)
-        src_off = ((int64_t)t * kvh + h) * hd + d0;
+        src_off = ((int64_t)t * kvh + h) * hdi + d0;
     else
-        src_off = (int64_t)tk.seq_row0 * kvh * hd + ((int64_t)h * tk.seq_n + j) * hd + d0;
-    uint16_t kv[8], vv[8];
-    load8_bf16(k_src, src_off, src_bf16, kv);
-    load8_bf16(v_src, src_off, src_bf16, vv);
+        src_off = (int64_t)tk.seq_row0 * kvh * hdi + ((int64_t)h * tk.seq_n + j) * hdi + d0;
+    uint16_t kv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, vv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (d0 < hdi) {
+        load8_bf16(k_src, src_off, src_bf16, kv);
+        load8_bf16(v_src, src_off, src_bf16, vv);
+    }
     uint16_t *kd = kpool + ((int64_t)tk.page * kvh + h) * P * hd + k_page_off(tk.slot, d0, hd);
     u32x4 pk;
 #pragma unroll
@@ -141,7 +146,7 @@ __global__ void kv_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__rest
 hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *kpool,
                             uint16_t *vpool, int32_t *table, const Patch *patches, int n_patch,
                             const AppendTok *toks, int n_tok, const void *k_src, const void *v_src,
-                            int src_bf16, int layout, int kvh, int hd, int P) {
+                            int src_bf16, int layout, int kvh, int hd, int hdi, int P) {
     int64_t work = (int64_t)n_tok * kvh * (hd / 8);
     if (work < n_patch) work = n_patch;
     if (work <= 0) return hipSuccess;
@@ -149,11 +154,11 @@ hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uin
     if (plan)
         kv_append_kernel<true><<<grid, 256, 0, s>>>(*plan, kpool, vpool, table, patches, n_patch,
                                                     toks, tok_off, n_tok, k_src, v_src, src_bf16,
-                                                    layout, kvh, hd, P);
+                                                    layout, kvh, hd, hdi, P);
     else
         kv_append_kernel<false><<<grid, 256, 0, s>>>(NoPlan{0}, kpool, vpool, table, patches,
                                                      n_patch, toks, tok_off, n_tok, k_src, v_src,
-                                                     src_bf16, layout, kvh, hd, P);
+                                                     src_bf16, layout, kvh, hd, hdi, P);
     return hipGetLastError();
 }
 
@@ -212,11 +217,13 @@ __global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
                                  const uint16_t *__restrict__ vpool,
                                  const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
                                  uint16_t *__restrict__ k_out, uint16_t *__restrict__ v_out,
-                                 int kvh, int hd, int P) {
+                                 int kvh, int hd, int hdi, int P) {
+    // Stored pages hold hd dims per head; the dense output holds the
+    // caller's hdi (<= hd, a multiple of 8) and drops the zero padding.
     const AttRow R = rows[blockIdx.y];
-    const int chunks = hd >> 3;
+    const int chunks = hdi >> 3;
     const int64_t nk = (int64_t)R.len * kvh * chunks;
-    const int64_t base = (int64_t)R.qrow * kvh * hd;  // qrow holds the output token offset
+    const int64_t base = (int64_t)R.qrow * kvh * hdi;  // qrow holds the output token offset
     for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < nk;
          gid += (int64_t)gridDim.x * blockDim.x) {
         const int t = (int)(gid / ((int64_t)kvh * chunks));
@@ -226,16 +233,16 @@ __global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
         const int page = table[R.tab + t / P];
         const int slot = t % P;
         u32x4 v = *(const u32x4 *)(kpool + ((int64_t)page * kvh + h) * P * hd + k_page_off(slot, d0, hd));
-        *(u32x4 *)(k_out + base + ((int64_t)h * R.len + t) * hd + d0) = v;
+        *(u32x4 *)(k_out + base + ((int64_t)h * R.len + t) * hdi + d0) = v;
     }
     const int tchunks = (R.len + 7) >> 3;
-    const int64_t nv = (int64_t)kvh * hd * tchunks;
+    const int64_t nv = (int64_t)kvh * hdi * tchunks;
     for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < nv;
          gid += (int64_t)gridDim.x * blockDim.x) {
         const int tc = (int)(gid % tchunks);
         const int hd_i = (int)(gid / tchunks);
-        const int h = hd_i / hd;
-        const int d = hd_i - h * hd;
+        const int h = hd_i / hdi;
+        const int d = hd_i - h * hdi;
         const int t0 = tc * 8;
         const int page = table[R.tab + t0 / P];
         const int slot = t0 % P;
@@ -244,7 +251,7 @@ __global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
         for (int i = 0; i < 8; i++) {
             if (t0 + i < R.len) {
                 uint32_t w = v[i >> 1];
-                v_out[base + ((int64_t)h * R.len + t0 + i) * hd + d] =
+                v_out[base + ((int64_t)h * R.len + t0 + i) * hdi + d] =
                     (uint16_t)((i & 1) ? (w >> 16) : (w & 0xFFFFu));
             }
         }
@@ -253,13 +260,13 @@ __global__ void kv_gather_kernel(const uint16_t *__restrict__ kpool,
 
 hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
                             const int32_t *table, const AttRow *rows, int n_rows, int max_len,
-                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int P) {
+                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int hdi, int P) {
     if (n_rows <= 0 || max_len <= 0) return hipSuccess;
     int64_t work = (int64_t)max_len * kvh * (hd / 8);
     int blocks = (int)((work + 255) / 256);
     if (blocks > 4096) blocks = 4096;
     kv_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(kpool, vpool, table, rows, k_out, v_out,
-                                                          kvh, hd, P);
+                                                          kvh, hd, hdi, P);
     return hipGetLastError();
 }
 

@@ -1,7 +1,10 @@
 // Shared device types, plan records and launcher declarations of librelux_kv.
 //
 // HBM layout of the paged caches (bf16 = uint16 bit patterns):
-//   GQA K pool : [pool_pages][kv_heads][page_tokens][head_dim]   (row pages)
+//   GQA K pool : [pool_pages][kv_heads][page_tokens/16][head_dim/32][16][32]
+//                (16-token blocks stored k-step-major, see k_page_off; head_dim
+//                <= 32: plain [16][head_dim] rows; head_dim is the stored one,
+//                16/32/64/96/128/256, zero padded past the caller's)
 //   GQA V pool : [pool_pages][kv_heads][head_dim][page_tokens]   (dim-major pages:
 //                the tokens of one dim are contiguous, which is the operand
 //                order the P.V matrix-core step consumes)
@@ -254,7 +257,7 @@ hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uin
                             uint16_t *vpool, int32_t *table,
                             const Patch *patches, int n_patch, const AppendTok *toks, int n_tok,
                             const void *k_src, const void *v_src, int src_bf16, int layout,
-                            int kvh, int hd, int P);
+                            int kvh, int hd, int hdi, int P);
 hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *pool,
                              int32_t *table, const Patch *patches,
                              int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
@@ -262,7 +265,7 @@ hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, ui
 
 hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
                             const int32_t *table, const AttRow *rows, int n_rows, int max_len,
-                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int P);
+                            uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int hdi, int P);
 hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
                              uint16_t *kr_out, int P);
@@ -271,8 +274,8 @@ hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t 
 hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
                              const uint16_t *vpool, const int32_t *table, const AttRow *rows,
                              int n_rows, const int4 *ranges, int n_ranges, const void *q, int q_bf16,
-                             int layout, int H, int KVH, int hd, int P, int total64, int snap64,
-                             int ranges_off, float qscale,
+                             int layout, int H, int KVH, int hd, int hdi, int P, int total64,
+                             int snap64, int ranges_off, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
                              int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1);
 

@@ -10,9 +10,11 @@
 //   online softmax per q-row column (lane-local state, exp2 domain)
 //   O^T[D][16 q-rows]    += V_blk^T[D x 16 tok] . P^T     (D/16 MFMA 16x16x16 bf16)
 //
-// The K rows are the A operand straight from a row page (8 consecutive dims
-// per lane, 16-byte loads); the V^T tile is the A operand straight from a
-// dim-major page (4 consecutive tokens per lane, 8-byte loads); the MFMA
+// The K block is the A operand straight from its k-step-major page block
+// (k_page_off: each 32-dim k-step of 16 tokens is 1 KB contiguous, 8
+// consecutive dims per lane, 16-byte loads); the V^T tile is the A operand
+// straight from a dim-major page (4 consecutive tokens per lane, 8-byte
+// loads); the MFMA
 // result layout of S^T is exactly the B-operand layout P^T needs, so no LDS
 // and no shuffles sit between the two products.  The query rows of a kv head
 // (H/KVH heads x n_q queries) fill the 16-wide N dimension; a second N tile
@@ -35,13 +37,19 @@ __device__ __forceinline__ int key_limit(int mask_mode, int len, int nq, int qi)
     return len - 1;
 }
 
+// head_dim 256 takes one 16-row query tile with the whole register file
+// (its two block register sets alone are 128 VGPRs).
+template <int D, int NQT>
+constexpr int gqa_min_waves() { return D >= 256 ? 1 : (NQT == 1 ? 3 : 1); }
+
 template <int D, int NQT, bool ARG>
-__global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
+__global__ __launch_bounds__(256, (gqa_min_waves<D, NQT>())) void gqa_decode_kernel(
     typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ kpool,
     const uint16_t *__restrict__ vpool, const int32_t *__restrict__ table,
     const AttRow *__restrict__ rows, const int4 *__restrict__ ranges, int n_rows,
-    const void *__restrict__ q, int q_bf16, int layout, int H, int KVH, int P, int total64, int snap64,
-    int ranges_off, float qscale, int mask_mode, float *__restrict__ part_o, float *__restrict__ part_ml) {
+    const void *__restrict__ q, int q_bf16, int layout, int H, int KVH, int DQ, int P, int total64,
+    int snap64, int ranges_off, float qscale, int mask_mode, float *__restrict__ part_o,
+    float *__restrict__ part_ml) {
     // head_dim 16 holds only 4 dims per lane: its score step is one MFMA
     // 16x16x16 (4 bf16 per lane); wider heads use 16x16x32 k-steps.
     constexpr bool K16 = (D == 16);
@@ -174,10 +182,15 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
             const int h = kvh * G + (qrc - ql * G);
             const int qi = R.q0 + ql;
             klim[nt] = qv[nt] ? key_limit(mask_mode, R.len, R.nq, qi) : R.len - 1;
-            qbase[nt] = ((layout == kLayoutSHD) ? ((int64_t)(R.qrow + qi) * H + h) * D
-                                                : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D) +
-                        grp * KW;
+            // q rows hold the caller's DQ dims (the pages may store more,
+            // zero-padded): dims at or past DQ load nothing and stay zero.
+            qbase[nt] = (layout == kLayoutSHD) ? ((int64_t)(R.qrow + qi) * H + h) * DQ
+                                               : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ;
         }
+        bool dv[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) dv[ks] = ks * 32 + grp * KW < DQ;
+        auto qoff = [&](int ks) { return dv[ks] ? ks * 32 + grp * KW : 0; };
         auto pack_q = [&](const float (&v)[8], bool valid) {
             u32x4 w = u32x4{0, 0, 0, 0};
             const float sc = valid ? qscale : 0.f;
@@ -192,7 +205,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
             for (int nt = 0; nt < NQT; nt++)
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
-                    const uint16_t *src = (const uint16_t *)q + qbase[nt] + ks * 32;
+                    const uint16_t *src = (const uint16_t *)q + qbase[nt] + qoff(ks);
                     if constexpr (K16) {
                         const u32x2 r2 = *(const u32x2 *)src;
                         raw[nt][ks] = u32x4{r2[0], r2[1], 0, 0};
@@ -210,7 +223,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
                         v[2 * i] = bf16_lo(raw[nt][ks][i]);
                         v[2 * i + 1] = bf16_hi(raw[nt][ks][i]);
                     }
-                    qb[nt][ks] = pack_q(v, qv[nt]);
+                    qb[nt][ks] = pack_q(v, qv[nt] && dv[ks]);
                 }
         } else {
             float4 raw[NQT][KS][2];
@@ -218,7 +231,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
             for (int nt = 0; nt < NQT; nt++)
 #pragma unroll
                 for (int ks = 0; ks < KS; ks++) {
-                    const float4 *src = (const float4 *)((const float *)q + qbase[nt] + ks * 32);
+                    const float4 *src = (const float4 *)((const float *)q + qbase[nt] + qoff(ks));
                     raw[nt][ks][0] = src[0];
                     raw[nt][ks][1] = K16 ? float4{0.f, 0.f, 0.f, 0.f} : src[1];
                 }
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
                 for (int ks = 0; ks < KS; ks++) {
                     const float4 x = raw[nt][ks][0], y = raw[nt][ks][1];
                     const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-                    qb[nt][ks] = pack_q(v, qv[nt]);
+                    qb[nt][ks] = pack_q(v, qv[nt] && dv[ks]);
                 }
         }
 
@@ -440,15 +453,18 @@ __global__ __launch_bounds__(256, NQT == 1 ? 3 : 1) void gqa_decode_kernel(
 
 // Merge the partials (one per segment of the row) of one (row, kv head,
 // query row): O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the
-// caller's layout and dtype.  One block of D threads per query row; the merge weights are
-// computed once in LDS and every thread streams its dim across the partials.
+// caller's layout and dtype.  One block of max(D, 64) threads per query row,
+// thread d owning dim d.  With at most kFewParts partials (the usual case)
+// every thread loads all (m, l) pairs and its dim of every partial at once
+// and computes the weights itself (no LDS); with more, wave 0 computes the
+// weights once in LDS and every thread streams its dim across the partials.
 constexpr int kFewParts = 8;  // partials merged without LDS (one round trip)
 
 template <bool ARG>
-__global__ __launch_bounds__(128) void gqa_combine_kernel(
+__global__ __launch_bounds__(256) void gqa_combine_kernel(
     typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows,
     const float *__restrict__ part_o, const float *__restrict__ part_ml, void *__restrict__ out,
-    int out_bf16, int layout, int H, int KVH, int D, int QRP) {
+    int out_bf16, int layout, int H, int KVH, int D, int DQ, int QRP) {
     const AttRow R = plan_row<ARG>(rows, blockIdx.x);
     const int kvh = blockIdx.y;
     const int qr = blockIdx.z;
@@ -486,11 +502,11 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
             L += f * lv[s];
             O += f * ov[s];
         }
-        if (d < D) {
+        if (d < DQ) {
             const float v = O * (L > 0.f ? 1.f / L : 0.f);
             const int64_t o = (layout == kLayoutSHD)
-                                  ? ((int64_t)(R.qrow + qi) * H + h) * D + d
-                                  : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D + d;
+                                  ? ((int64_t)(R.qrow + qi) * H + h) * DQ + d
+                                  : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ + d;
             if (out_bf16)
                 ((uint16_t *)out)[o] = bf16_rne(v);
             else
@@ -500,13 +516,13 @@ __global__ __launch_bounds__(128) void gqa_combine_kernel(
     }
     merge_weights(part_ml + b0 * 2, sstride, n, fac, &inv_l);
     __syncthreads();
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    for (int d = threadIdx.x; d < DQ; d += blockDim.x) {
         float O = 0.f;
         for (int s = 0; s < R.nsplit; s++) O += fac[s] * part_o[(b0 + s * sstride) * D + d];
         const float v = O * inv_l;
         const int64_t o = (layout == kLayoutSHD)
-                              ? ((int64_t)(R.qrow + qi) * H + h) * D + d
-                              : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * D + d;
+                              ? ((int64_t)(R.qrow + qi) * H + h) * DQ + d
+                              : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ + d;
         if (out_bf16)
             ((uint16_t *)out)[o] = bf16_rne(v);
         else
@@ -519,44 +535,42 @@ static hipError_t launch_gqa_t(hipStream_t s, typename PlanSel<ARG>::T plan,
                                const uint16_t *kpool, const uint16_t *vpool,
                                const int32_t *table, const AttRow *rows, int n_rows,
                                const int4 *ranges, int n_ranges, const void *q, int q_bf16,
-                               int layout, int H, int KVH, int P, int total64, int snap64,
+                               int layout, int H, int KVH, int DQ, int P, int total64, int snap64,
                                int ranges_off, float qscale,
                                int mask_mode, float *part_o, float *part_ml, void *out,
                                int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (ev0) (void)hipEventRecord(ev0, s);
     gqa_decode_kernel<D, NQT, ARG><<<dim3(n_ranges * KVH), 256, 0, s>>>(
-        plan, kpool, vpool, table, rows, ranges, n_rows, q, q_bf16, layout, H, KVH, P, total64, snap64,
-        ranges_off, qscale,
-        mask_mode, part_o, part_ml);
+        plan, kpool, vpool, table, rows, ranges, n_rows, q, q_bf16, layout, H, KVH, DQ, P, total64,
+        snap64, ranges_off, qscale, mask_mode, part_o, part_ml);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
     gqa_combine_kernel<ARG><<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(
-        plan, rows, part_o, part_ml, out, out_bf16, layout, H, KVH, D, 16 * NQT);
+        plan, rows, part_o, part_ml, out, out_bf16, layout, H, KVH, D, DQ, 16 * NQT);
     return hipGetLastError();
 }
 
 hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
                              const uint16_t *vpool, const int32_t *table, const AttRow *rows,
                              int n_rows, const int4 *ranges, int n_ranges, const void *q, int q_bf16,
-                             int layout, int H, int KVH, int hd, int P, int total64, int snap64,
-                             int ranges_off, float qscale,
+                             int layout, int H, int KVH, int hd, int hdi, int P, int total64,
+                             int snap64, int ranges_off, float qscale,
                              int mask_mode, int nqt, float *part_o, float *part_ml, void *out,
                              int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
     if (n_ranges <= 0) return hipSuccess;
 #define RLX_GQA_CASE(DD, NN)                                                                    \
     if (hd == DD && nqt == NN)                                                                  \
         return plan ? launch_gqa_t<DD, NN, true>(s, *plan, kpool, vpool, table, rows, n_rows,   \
-                                                 ranges, n_ranges, q, q_bf16, layout, H, KVH, P, \
-                                                 total64, snap64, ranges_off,                   \
+                                                 ranges, n_ranges, q, q_bf16, layout, H, KVH,   \
+                                                 hdi, P, total64, snap64, ranges_off,           \
                                                  qscale, mask_mode, part_o, part_ml, out,       \
                                                  out_bf16, max_qr, ev0, ev1)                    \
                     : launch_gqa_t<DD, NN, false>(s, NoPlan{0}, kpool, vpool, table, rows,      \
                                                   n_rows, ranges, n_ranges, q, q_bf16, layout,  \
-                                                  H, KVH, P, total64, snap64, -1, qscale,       \
-                                                  mask_mode,                                    \
-                                                  part_o,                                       \
-                                                  part_ml, out, out_bf16, max_qr, ev0, ev1);
+                                                  H, KVH, hdi, P, total64, snap64, -1, qscale,  \
+                                                  mask_mode, part_o, part_ml, out, out_bf16,    \
+                                                  max_qr, ev0, ev1);
     RLX_GQA_CASE(128, 1)
     RLX_GQA_CASE(128, 2)
     RLX_GQA_CASE(64, 1)
@@ -565,6 +579,9 @@ hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     RLX_GQA_CASE(32, 2)
     RLX_GQA_CASE(16, 1)
     RLX_GQA_CASE(16, 2)
+    RLX_GQA_CASE(96, 1)
+    RLX_GQA_CASE(96, 2)
+    RLX_GQA_CASE(256, 1)
 #undef RLX_GQA_CASE
     return hipErrorInvalidValue;
 }

@@ -110,6 +110,7 @@ struct SpillTier {
 struct Cache {
     int kind = kGQA;
     int layers = 0, kvh = 0, hd = 0, P = 0, pool_pages = 0, max_seqs = 0, max_pages = 0;
+    int hdi = 0;  // GQA: the caller's head dim (hd, the stored one, may be larger: zero padding)
     int dc = 0, dr = 0;
     int device = 0;
     int cus = 256;  // compute units of the device
@@ -744,15 +745,23 @@ int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_
     if (layers <= 0) return fail(RLX_ERR_INVALID, "NewKVCacheSized: numLayers=%d, must be > 0", layers);
     if (kv_heads <= 0 || pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
         return fail(RLX_ERR_INVALID, "kv_heads, pool_pages, max_seqs, max_pages must be > 0");
-    if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
-        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: 16, 32, 64, 128)", head_dim);
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: multiples of 8 up to 256)", head_dim);
     if (page_tokens <= 0 || page_tokens % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
     Cache *c = new Cache;
     c->kind = kGQA;
     c->layers = layers;
     c->kvh = kv_heads;
-    c->hd = head_dim;
+    // Pages store the smallest supported head dim >= head_dim; the dims past
+    // head_dim hold zeros (written by every append).
+    static const int kStoredDims[] = {16, 32, 64, 96, 128, 256};
+    for (int d : kStoredDims)
+        if (d >= head_dim) {
+            c->hd = d;
+            break;
+        }
+    c->hdi = head_dim;
     c->P = page_tokens;
     c->pool_pages = pool_pages;
     c->max_seqs = max_seqs;
@@ -877,7 +886,7 @@ int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     LayerState &ls = c->L[layer];
     HIP_TRY(launch_kv_append(c->stream, plan, tok_off, ls.pool0, ls.pool1, c->d_table, d_patches,
                              (int)patches.size(), d_toks, (int)toks.size(), k_src, v_src,
-                             src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->P));
+                             src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->hdi, c->P));
     return RLX_OK;
 }
 
@@ -1046,6 +1055,9 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
+    if (c->hd != c->hdi)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_gqa_project_append: head_dim %d is stored padded to %d",
+                    c->hdi, c->hd);
     if (num_heads <= 0 || num_heads % c->kvh != 0)
         return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
     return project_append(c, kProjModelGQA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
@@ -1136,7 +1148,7 @@ int32_t rlx_kv_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     LayerState &ls = c->L[layer];
     HIP_TRY(launch_kv_gather(c->stream, ls.pool0, ls.pool1, c->d_table,
                              (const AttRow *)((char *)dev + o_r), n_seqs, max_len,
-                             (uint16_t *)k_out, (uint16_t *)v_out, c->kvh, c->hd, c->P));
+                             (uint16_t *)k_out, (uint16_t *)v_out, c->kvh, c->hd, c->hdi, c->P));
     return RLX_OK;
 }
 
@@ -1167,6 +1179,11 @@ int32_t rlx_mla_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
 }  // extern "C"
 
 namespace {
+// Query rows of one kv head one decode work-group holds: 32 (two 16-wide
+// tiles), 16 for head_dim 256 (whose work-group needs the register file for
+// one tile).
+int gqa_rows_cap(const Cache *c) { return c->hd >= 256 ? 16 : 32; }
+
 // Argument checks shared by the GQA attention entry points.
 int32_t check_gqa_attend(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                          int32_t num_heads, int32_t q_dtype, int32_t qo_layout, int32_t mask_mode,
@@ -1209,11 +1226,13 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     const int max_qr = G * max_nq;
     // The FA2 prefill kernel covers head_dim 64/128 with G dividing 128;
     // other shapes tile their queries through the decode kernel, whose
-    // work-group holds at most 32 query rows of one kv head.
-    const bool fa2 = (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
-    if (max_qr > 32 && !fa2 && G > 32)
-        return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most 32)", G, c->hd);
-    if (max_qr > 32 && fa2) {
+    // work-group holds at most cap query rows of one kv head.
+    const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
+    const int cap = gqa_rows_cap(c);
+    if (max_qr > cap && !fa2 && G > cap)
+        return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", G,
+                    c->hdi, cap);
+    if (max_qr > cap && fa2) {
         // Chunked prefill / long verify: FA2 tiles of kPrefillRows query rows.
         std::vector<AttRow> rows;
         std::vector<int2> unused;
@@ -1240,7 +1259,7 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         size_t o_r = b.add(rows), o_w = b.add(work);
         void *dev;
         if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
-        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
         PrefillArgs a{};
         a.kpool = ls.pool0;
         a.vpool = ls.pool1;
@@ -1263,8 +1282,8 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         HIP_TRY(launch_prefill(c->stream, kSrcPaged, c->hd, a, (int)work.size(), e0, e1));
         return RLX_OK;
     }
-    const int qtile = max_qr > 32 ? 32 / G : 0;
-    const int nqt = max_qr > 16 ? 2 : 1;
+    const int qtile = max_qr > cap ? cap / G : 0;
+    const int nqt = std::min(max_qr, cap) > 16 ? 2 : 1;
     int n_rows = 0;
     if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, nullptr, 0, &n_rows))) return rc;
     std::vector<AttRow> rows(n_rows);
@@ -1307,15 +1326,15 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         d_rows = (const AttRow *)((char *)dev + o_r);
         d_ranges = (const int4 *)((char *)dev + o_w);
     }
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
     const float qscale = scale * 1.4426950408889634f;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
     HIP_TRY(launch_gqa_decode(c->stream, plan, ls.pool0, ls.pool1, c->d_table, d_rows, n_rows,
                               d_ranges, n_ranges, q, q_dtype == RLX_BF16, qo_layout, num_heads,
-                              c->kvh, c->hd, c->P, total64, kGqaSnap64, ranges_off, qscale,
+                              c->kvh, c->hd, c->hdi, c->P, total64, kGqaSnap64, ranges_off, qscale,
                               mask_mode, nqt, (float *)c->ws, (float *)((char *)c->ws + po_bytes),
-                              out, out_dtype == RLX_BF16, std::min(max_qr, 32), e0, e1));
+                              out, out_dtype == RLX_BF16, std::min(max_qr, cap), e0, e1));
     return RLX_OK;
 }
 
@@ -1337,13 +1356,14 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     const int max_qr = G * max_nq;
     // Decode and verify calls only: the FA2 path's work lists are staged.
-    const bool fa2 = (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
-    if (max_qr > 32 && (fa2 || G > 32))
+    const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
+    const int cap = gqa_rows_cap(c);
+    if (max_qr > cap && (fa2 || G > cap))
         return fail(RLX_ERR_UNSUPPORTED,
-                    "rlx_gqa_attend_noalloc takes at most 32 query rows per kv head (got %d); "
-                    "use rlx_gqa_attend", max_qr);
-    const int qtile = max_qr > 32 ? 32 / G : 0;
-    const int nqt = max_qr > 16 ? 2 : 1;
+                    "rlx_gqa_attend_noalloc takes at most %d query rows per kv head (got %d); "
+                    "use rlx_gqa_attend", cap, max_qr);
+    const int qtile = max_qr > cap ? cap / G : 0;
+    const int nqt = std::min(max_qr, cap) > 16 ? 2 : 1;
     // Rows (and ranges when they fit) travel in the kernel arguments.
     constexpr int kRowCap = kPlanArgBytes / (int)sizeof(AttRow);
     constexpr int kRangeCap = 1024;
@@ -1376,13 +1396,13 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
         memcpy(plan.b + rows_bytes, ranges, (size_t)n_ranges * sizeof(int4));
         ranges_off = (int)rows_bytes;
     }
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hd));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
     HIP_TRY(launch_gqa_decode(c->stream, &plan, c->L[layer].pool0, c->L[layer].pool1, c->d_table,
                               nullptr, n_rows, nullptr, n_ranges, q, q_dtype == RLX_BF16, qo_layout,
-                              num_heads, c->kvh, c->hd, c->P, total64, kGqaSnap64, ranges_off,
+                              num_heads, c->kvh, c->hd, c->hdi, c->P, total64, kGqaSnap64, ranges_off,
                               scale * 1.4426950408889634f, mask_mode, nqt, (float *)scr,
                               (float *)((char *)scr + po_bytes), out, out_dtype == RLX_BF16,
-                              std::min(max_qr, 32), nullptr, nullptr));
+                              std::min(max_qr, cap), nullptr, nullptr));
     return RLX_OK;
 }
 

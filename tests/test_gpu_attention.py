@@ -72,6 +72,11 @@ def _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=2):
     (4, 2, 16, [8, 23, 300], 1, "causal"),                           # config-1 head_dim 16
     (4, 2, 16, [8, 9], 8, "ref"),
     (8, 2, 32, [17, 500], 4, "causal"),                              # head_dim 32
+    (16, 4, 80, [300, 17, 1], 1, "causal"),                          # 80: stored as 96
+    (32, 8, 96, [600, 33], 4, "causal"),                             # 96
+    (16, 2, 256, [400, 65], 2, "causal"),                            # 256: 16-row tiles
+    (4, 2, 8, [8, 23, 300], 1, "causal"),                            # 8: stored as 16
+    (8, 2, 48, [260, 9], 3, "ref"),                                  # 48: stored as 64
 ])
 def test_gqa_attend_matches_oracle(gpu, H, KVH, D, lens, nq, mask):
     from relux_amd import KVCache
@@ -245,10 +250,10 @@ def _mla_exact(qc, qr, c, kr, w_uk, w_uv, limits):
 
 @pytest.mark.parametrize("H,lens,nq,mask", [
     (16, [1, 15, 64, 65, 200, 300], 1, "causal"),
-    # many ragged rows: decode ranges straddle rows (rows in the kernel
-    # arguments, ranges recomputed per work-group) ...
+    # many ragged rows, each split into its own near-equal splits (rows in
+    # the kernel arguments, work items found by search) ...
     (16, [int(x) for x in np.random.default_rng(5).integers(1, 400, 40)], 1, "causal"),
-    # ... and more rows than the arguments hold (rows and ranges staged)
+    # ... and more rows than the arguments hold (rows and work list staged)
     (8, [int(x) for x in np.random.default_rng(6).integers(2, 300, 70)], 2, "causal"),
     (16, [260, 7], 2, "causal"),
     (8, [90, 3], 3, "ref"),
@@ -306,6 +311,9 @@ def test_mla_attend_matches_oracle(gpu, H, lens, nq, mask):
     (8, 2, 32, [280, 100], [120, 100], "ref"),             # head_dim 32
     (12, 4, 64, [290, 50], [60, 50], "causal"),            # G = 3 does not divide 128
     (6, 2, 128, [260], [260], "none"),
+    (16, 4, 80, [300, 40], [70, 40], "causal"),            # padded head_dim: query tiles
+    (8, 2, 256, [290, 50], [60, 50], "causal"),            # head_dim 256: 16-row tiles
+    (8, 8, 96, [270], [40], "ref"),
 ])
 def test_gqa_prefill_matches_oracle(gpu, H, KVH, D, lens, nqs, mask):
     from relux_amd import KVCache

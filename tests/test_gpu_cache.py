@@ -66,9 +66,11 @@ def test_errors_mirror_reference_panics(gpu):
 
 @pytest.mark.parametrize("src_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("layout", ["HSD", "SHD"])
-def test_multi_sequence_append_gather_bit_exact(gpu, src_dtype, layout):
-    rng = np.random.default_rng(11)
-    KVH, D, P, S = 4, 128, 16, 5
+@pytest.mark.parametrize("D", [128, 80])
+def test_multi_sequence_append_gather_bit_exact(gpu, src_dtype, layout, D):
+    """D 80 is stored padded to 96 dims per head: the padding never shows."""
+    rng = np.random.default_rng(11 + D)
+    KVH, P, S = 4, 16, 5
     c = _kv(gpu, num_layers=2, max_len=512, num_kv_heads=KVH, head_dim=D, page_tokens=P,
             max_seqs=S, pool_pages=120)
     model = PagedModel(2, P, 120, S, 32)
@@ -107,6 +109,38 @@ def test_multi_sequence_append_gather_bit_exact(gpu, src_dtype, layout):
             want_v = np.concatenate([p[1] for p in parts]).transpose(1, 0, 2)
             assert np.array_equal(ck.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_k)
             assert np.array_equal(cv.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_v)
+
+
+@pytest.mark.parametrize("D", [8, 48, 96, 256])
+def test_append_gather_other_head_dims(gpu, D):
+    """head_dim any multiple of 8 up to 256 (NewKVCacheSized takes any,
+    kvcache.go:66-93): stored as 16/32/64/96/128/256 dims, zero padded;
+    View returns exactly the appended rows, across pages and two calls."""
+    rng = np.random.default_rng(D)
+    KVH, P = 2, 16
+    c = _kv(gpu, num_layers=1, max_len=128, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+            max_seqs=2)
+    rows = [[], []]
+    for n in ([37, 5], [20, 60]):
+        k = rng.normal(size=(sum(n), KVH, D)).astype(np.float32)
+        v = rng.normal(size=(sum(n), KVH, D)).astype(np.float32)
+        c.Append(0, torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), seq_ids=[0, 1],
+                 n_tok=n, layout="SHD")
+        rows[0].append((k[:n[0]], v[:n[0]]))
+        rows[1].append((k[n[0]:], v[n[0]:]))
+    for s in range(2):
+        ck, cv = c.View(0, s)
+        assert tuple(ck.shape) == (1, KVH, sum(r[0].shape[0] for r in rows[s]), D)
+        want_k = oracle.bf16_from_f32(np.concatenate([r[0] for r in rows[s]])).transpose(1, 0, 2)
+        want_v = oracle.bf16_from_f32(np.concatenate([r[1] for r in rows[s]])).transpose(1, 0, 2)
+        assert np.array_equal(ck.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_k)
+        assert np.array_equal(cv.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_v)
+    c.close()
+    from relux_amd import _lib
+    for bad in (12, 264, 0):
+        with pytest.raises(_lib.ReluxError) as e:
+            _kv(gpu, num_layers=1, max_len=16, num_kv_heads=1, head_dim=bad)
+        assert e.value.code in (_lib.RLX_ERR_UNSUPPORTED, _lib.RLX_ERR_INVALID)
 
 
 def test_append_conversion_edge_bits(gpu):
