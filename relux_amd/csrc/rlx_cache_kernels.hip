@@ -162,14 +162,23 @@ hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uin
     return hipGetLastError();
 }
 
-// MLA append.  Thread = (token, 8-element chunk of the 576-element row);
-// chunks 0..63 come from c_src, 64..71 from kr_src.
+// One source element as bf16 bits (f32 sources: BF16FromF32, dtype_convert.go:15-24).
+__device__ __forceinline__ uint16_t load1_bf16(const void *src, int64_t i, int src_bf16) {
+    return src_bf16 ? ((const uint16_t *)src)[i] : bf16_rne(((const float *)src)[i]);
+}
+
+// MLA append.  Thread = (token, 8-element chunk of the stored 576-element
+// row): elements [0, 512) hold the latent c (the caller's d_c of them, then
+// zeros), [512, 576) the rope key (d_r, then zeros).  Chunks wholly inside
+// the caller's data take one 8-element load when the source row stride
+// allows it; the rest go element by element.
 template <bool ARG>
 __global__ void mla_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__restrict__ pool,
                                   int32_t *__restrict__ table, const Patch *__restrict__ patches,
                                   int n_patch, const AppendTok *__restrict__ toks, int tok_off,
                                   int n_tok, const void *__restrict__ c_src,
-                                  const void *__restrict__ kr_src, int src_bf16, int P) {
+                                  const void *__restrict__ kr_src, int src_bf16, int dc, int dr,
+                                  int P) {
     int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid < n_patch) {
         const Patch pt = plan_patch<ARG>(patches, (int)gid);
@@ -180,11 +189,18 @@ __global__ void mla_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__res
     const int t = (int)(gid / chunks);
     const int ch = (int)(gid - (int64_t)t * chunks);
     const AppendTok tk = plan_tok<ARG>(toks, tok_off, t);
+    const bool lat = ch < kMlaDc / 8;
+    const void *src = lat ? c_src : kr_src;
+    const int width = lat ? dc : dr;                     // caller's elements per row
+    const int e0 = lat ? ch * 8 : (ch - kMlaDc / 8) * 8;  // first element of the chunk
     uint16_t v[8];
-    if (ch < kMlaDc / 8)
-        load8_bf16(c_src, (int64_t)t * kMlaDc + ch * 8, src_bf16, v);
-    else
-        load8_bf16(kr_src, (int64_t)t * kMlaDr + (ch - kMlaDc / 8) * 8, src_bf16, v);
+    if (e0 + 8 <= width && width % 8 == 0) {
+        load8_bf16(src, (int64_t)t * width + e0, src_bf16, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = (e0 + i < width) ? load1_bf16(src, (int64_t)t * width + e0 + i, src_bf16) : (uint16_t)0;
+    }
     u32x4 pk;
 #pragma unroll
     for (int i = 0; i < 4; i++) pk[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
@@ -194,18 +210,18 @@ __global__ void mla_append_kernel(typename PlanSel<ARG>::T plan, uint16_t *__res
 hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *pool,
                              int32_t *table, const Patch *patches, int n_patch,
                              const AppendTok *toks, int n_tok, const void *c_src,
-                             const void *kr_src, int src_bf16, int P) {
+                             const void *kr_src, int src_bf16, int dc, int dr, int P) {
     int64_t work = (int64_t)n_tok * (kMlaRow / 8);
     if (work < n_patch) work = n_patch;
     if (work <= 0) return hipSuccess;
     const unsigned grid = (unsigned)((work + 255) / 256);
     if (plan)
         mla_append_kernel<true><<<grid, 256, 0, s>>>(*plan, pool, table, patches, n_patch, toks,
-                                                     tok_off, n_tok, c_src, kr_src, src_bf16, P);
+                                                     tok_off, n_tok, c_src, kr_src, src_bf16, dc, dr, P);
     else
         mla_append_kernel<false><<<grid, 256, 0, s>>>(NoPlan{0}, pool, table, patches, n_patch,
                                                       toks, tok_off, n_tok, c_src, kr_src,
-                                                      src_bf16, P);
+                                                      src_bf16, dc, dr, P);
     return hipGetLastError();
 }
 
@@ -270,11 +286,13 @@ hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t
     return hipGetLastError();
 }
 
-// Paged gather of MLA rows into dense c [T][512] and kr [T][64].
+// Paged gather of MLA rows into dense c [T][d_c] and kr [T][d_r] (the
+// stored rows' zero padding dropped).  Thread = (token, 8-element chunk of
+// the stored row).
 __global__ void mla_gather_kernel(const uint16_t *__restrict__ pool,
                                   const int32_t *__restrict__ table,
                                   const AttRow *__restrict__ rows, uint16_t *__restrict__ c_out,
-                                  uint16_t *__restrict__ kr_out, int P) {
+                                  uint16_t *__restrict__ kr_out, int dc, int dr, int P) {
     const AttRow R = rows[blockIdx.y];
     constexpr int chunks = kMlaRow / 8;
     const int64_t n = (int64_t)R.len * chunks;
@@ -282,24 +300,31 @@ __global__ void mla_gather_kernel(const uint16_t *__restrict__ pool,
          gid += (int64_t)gridDim.x * blockDim.x) {
         const int t = (int)(gid / chunks);
         const int ch = (int)(gid - (int64_t)t * chunks);
+        const bool lat = ch < kMlaDc / 8;
+        const int width = lat ? dc : dr;
+        const int e0 = lat ? ch * 8 : (ch - kMlaDc / 8) * 8;
+        if (e0 >= width) continue;  // padding only
         const int page = table[R.tab + t / P];
-        u32x4 v = *(const u32x4 *)(pool + ((int64_t)page * P + t % P) * kMlaRow + ch * 8);
+        const u32x4 v = *(const u32x4 *)(pool + ((int64_t)page * P + t % P) * kMlaRow + ch * 8);
         const int64_t row = (int64_t)R.qrow + t;
-        if (ch < kMlaDc / 8)
-            *(u32x4 *)(c_out + row * kMlaDc + ch * 8) = v;
-        else
-            *(u32x4 *)(kr_out + row * kMlaDr + (ch - kMlaDc / 8) * 8) = v;
+        uint16_t *dst = (lat ? c_out : kr_out) + row * width + e0;
+        if (e0 + 8 <= width && width % 8 == 0) {
+            *(u32x4 *)dst = v;
+        } else {
+            for (int i = 0; i < 8 && e0 + i < width; i++)
+                dst[i] = (uint16_t)((i & 1) ? (v[i >> 1] >> 16) : (v[i >> 1] & 0xFFFFu));
+        }
     }
 }
 
 hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
-                             uint16_t *kr_out, int P) {
+                             uint16_t *kr_out, int dc, int dr, int P) {
     if (n_rows <= 0 || max_len <= 0) return hipSuccess;
     int64_t work = (int64_t)max_len * (kMlaRow / 8);
     int blocks = (int)((work + 255) / 256);
     if (blocks > 4096) blocks = 4096;
-    mla_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(pool, table, rows, c_out, kr_out, P);
+    mla_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(pool, table, rows, c_out, kr_out, dc, dr, P);
     return hipGetLastError();
 }
 

@@ -8,7 +8,8 @@
 //   GQA V pool : [pool_pages][kv_heads][head_dim][page_tokens]   (dim-major pages:
 //                the tokens of one dim are contiguous, which is the operand
 //                order the P.V matrix-core step consumes)
-//   MLA pool   : [pool_pages][page_tokens][d_c + d_r]            (latent | rope key)
+//   MLA pool   : [pool_pages][page_tokens][512 + 64]             (latent | rope key:
+//                the caller's d_c <= 512 and d_r <= 64 elements, each zero padded)
 //   page table : int32 [layers][max_seqs][max_pages_per_seq], -1 = empty entry
 #pragma once
 #include <hip/hip_runtime.h>
@@ -261,14 +262,14 @@ hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uin
 hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, uint16_t *pool,
                              int32_t *table, const Patch *patches,
                              int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
-                             const void *kr_src, int src_bf16, int P);
+                             const void *kr_src, int src_bf16, int dc, int dr, int P);
 
 hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
                             const int32_t *table, const AttRow *rows, int n_rows, int max_len,
                             uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int hdi, int P);
 hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
-                             uint16_t *kr_out, int P);
+                             uint16_t *kr_out, int dc, int dr, int P);
 
 // plan: the rows in the kernel arguments (nullptr: rows and work on the device).
 hipError_t launch_gqa_decode(hipStream_t s, const PlanArg *plan, const uint16_t *kpool,
@@ -412,8 +413,8 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              const int32_t *table, const AttRow *rows, int n_rows,
                              const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
-                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
-                             int total_q, int max_nq, int P, float qscale,
+                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd, int dc,
+                             int dr, int total_q, int max_nq, int P, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
                              float *part_ml, void *out, int out_bf16, int cus,
                              hipEvent_t ev0, hipEvent_t ev1);

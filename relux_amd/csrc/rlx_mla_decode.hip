@@ -39,44 +39,55 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) 
 }
 
 // q_lat[row][h][c] = bf16(qscale * sum_d q_nope[row][h][d] * W_UK[c][h*D+d])
-// for c < 512 and q_lat[row][h][512+r] = bf16(qscale * q_rope[row][h][r]).
-// Block = (head, 64 latent channels, 16 query rows); wave w computes
-// C[16 channels][16 rows] = W_UK_h[c0+16w .., :] . q^T with MFMA 16x16x32
-// over the head's D dims: A = 8 consecutive W_UK dims of one channel per
-// lane, B = 8 consecutive query dims of one row per lane (f32 queries as
-// hi + lo bf16 pairs).  Every load is issued before the first product, so
-// the kernel costs one memory round trip.
-template <int D>
+// for c < d_c (0 for d_c <= c < 512: the stored latent rows are zero there)
+// and q_lat[row][h][512+r] = bf16(qscale * q_rope[row][h][r]) for r < d_r (0
+// past it).  Block = (head, 64 latent channels, 16 query rows); wave w
+// computes C[16 channels][16 rows] = W_UK_h[c0+16w .., :] . q^T with MFMA
+// 16x16x32 over the head's D dims (KS = ceil(D / 32) k-steps, dims past D
+// load zeros): A = 8 consecutive W_UK dims of one channel per lane, B = 8
+// consecutive query dims of one row per lane (f32 queries as hi + lo bf16
+// pairs).  Every load is issued before the first product, so the kernel
+// costs one memory round trip.
+template <int KS>
 __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
                                                          const void *__restrict__ q_rope,
                                                          int q_bf16,
                                                          const uint16_t *__restrict__ w_uk,
-                                                         int H, int total_q, float qscale,
-                                                         uint16_t *__restrict__ qlat) {
-    constexpr int KS = D / 32;
+                                                         int H, int D, int dc, int dr, int total_q,
+                                                         float qscale, uint16_t *__restrict__ qlat) {
     const int h = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
     const int c0 = blockIdx.y * 64 + wave * 16;
     const int r0 = blockIdx.z * 16;
     const int row = min(r0 + col, total_q - 1);  // rows past the end load the last row
-    const uint16_t *wa = w_uk + (int64_t)(c0 + col) * H * D + (int64_t)h * D + grp * 8;
+    const bool cv = c0 + col < dc;
+    const uint16_t *wa = w_uk + (int64_t)(cv ? c0 + col : 0) * H * D + (int64_t)h * D + grp * 8;
     u32x4 a[KS], bh[KS], bl[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) a[ks] = *(const u32x4 *)(wa + ks * 32);
+    for (int ks = 0; ks < KS; ks++) {
+        const bool dv = ks * 32 + grp * 8 < D;
+        a[ks] = (cv && dv) ? *(const u32x4 *)(wa + ks * 32) : u32x4{0, 0, 0, 0};
+    }
     const int64_t qoff = ((int64_t)row * H + h) * D + grp * 8;
     if (q_bf16) {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            bh[ks] = *(const u32x4 *)((const uint16_t *)q_nope + qoff + ks * 32);
+            const bool dv = ks * 32 + grp * 8 < D;
+            bh[ks] = dv ? *(const u32x4 *)((const uint16_t *)q_nope + qoff + ks * 32) : u32x4{0, 0, 0, 0};
             bl[ks] = u32x4{0, 0, 0, 0};
         }
     } else {
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
-            const float *qf = (const float *)q_nope + qoff + ks * 32;
-            const float4 f0 = *(const float4 *)qf, f1 = *(const float4 *)(qf + 4);
-            const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+            const bool dv = ks * 32 + grp * 8 < D;
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (dv) {
+                const float *qf = (const float *)q_nope + qoff + ks * 32;
+                const float4 f0 = *(const float4 *)qf, f1 = *(const float4 *)(qf + 4);
+                v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+                v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+            }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 uint16_t h0, l0, h1, l1;
@@ -109,8 +120,11 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
         for (int i = threadIdx.x; i < 16 * kMlaDr; i += blockDim.x) {
             const int r = i / kMlaDr, k = i - r * kMlaDr;
             if (r0 + r >= total_q) continue;
-            const int64_t off = ((int64_t)(r0 + r) * H + h) * kMlaDr + k;
-            const float x = q_bf16 ? bf16_f32(((const uint16_t *)q_rope)[off]) : ((const float *)q_rope)[off];
+            float x = 0.f;
+            if (k < dr) {
+                const int64_t off = ((int64_t)(r0 + r) * H + h) * dr + k;
+                x = q_bf16 ? bf16_f32(((const uint16_t *)q_rope)[off]) : ((const float *)q_rope)[off];
+            }
             qlat[((int64_t)(r0 + r) * H + h) * kMlaRow + kMlaDc + k] = bf16_rne(x * qscale);
         }
     }
@@ -459,6 +473,8 @@ __device__ __forceinline__ int plan_qrow_row(const AttRow *rows, int n_rows, int
 // and project it, out[d] = sum_c o_lat[c] * W_UV[c][h*D + d] (mla.go:384-389
 // applies W_UV to P.V; here it applies to the merged latent, the same sum
 // by linearity).  The RPB rows share one read of the head's W_UV slice.
+// D (the head dim, a multiple of 8 up to DMAX) and d_c are runtime values:
+// octets past D and channels past d_c take no part.
 // Every global load is issued at the start, so the block costs one memory
 // round trip: thread t loads channels 2t, 2t+1 (bf16 pair) of up to 16
 // splits per row, and -- as thread (g, o) of G channel groups x D/8 dim
@@ -467,20 +483,21 @@ __device__ __forceinline__ int plan_qrow_row(const AttRow *rows, int n_rows, int
 // o_lat goes to LDS, each thread accumulates its 8 dims over its channels
 // with f32 FMAs of the exactly widened bf16 weights, and the groups are
 // summed in LDS.
-template <int D>
+template <int DMAX>
 struct MlaOutShape {
-    static constexpr int OCT = D / 8;                              // dim octets
+    static constexpr int OCT = DMAX / 8;                           // dim octets
     static constexpr int G = (256 / OCT >= 32) ? 32 : (256 / OCT >= 16) ? 16 : 8;  // channel groups
     static constexpr int CPG = kMlaDc / G;                         // channels per group
-    static constexpr int WB = CPG < 32 ? CPG : (D >= 192 ? 16 : 32);  // weight rows loaded up front
+    static constexpr int WB = CPG < 32 ? CPG : (DMAX >= 192 ? 16 : 32);  // weight rows loaded up front
 };
 
-template <int D, int RPB, bool ARG>
+template <int DMAX, int RPB, bool ARG>
 __global__ __launch_bounds__(256) void mla_out_kernel(
     typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows, int n_rows, int total_q, int one_q,
     const uint16_t *__restrict__ part_o, const float *__restrict__ part_ml,
-    const uint16_t *__restrict__ w_uv, int H, int QRP, void *__restrict__ out, int out_bf16) {
-    using SH = MlaOutShape<D>;
+    const uint16_t *__restrict__ w_uv, int H, int D, int dc, int QRP, void *__restrict__ out,
+    int out_bf16) {
+    using SH = MlaOutShape<DMAX>;
     constexpr int SB = 16;  // splits per batch of loads
     constexpr int OCT = SH::OCT, G = SH::G, CPG = SH::CPG, WB = SH::WB;
     static_assert(G * CPG == kMlaDc && G * OCT <= 256, "groups x octets must fit the block");
@@ -490,17 +507,19 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     __shared__ float fac[RPB][kMaxSplits];
     __shared__ float inv_l[RPB];
     __shared__ float olat[RPB][kMlaDc];
-    __shared__ float red[G][RPB][D];
+    __shared__ float red[G][RPB][DMAX];
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int g = t / OCT, o = t - g * OCT;
-    const bool wt = g < G;  // thread takes part in the projection
-    // W_UV rows g * CPG + k, dims h*D + 8 o .. + 8
-    const uint16_t *wp = w_uv + (int64_t)(wt ? g : 0) * CPG * H * D + (int64_t)h * D + o * 8;
+    const bool wt = g < G && o * 8 < D;  // thread takes part in the projection
+    // W_UV rows g * CPG + k (< d_c), dims h*D + 8 o .. + 8
+    const int cb = (g < G ? g : 0) * CPG;
+    const uint16_t *wp = w_uv + (int64_t)cb * H * D + (int64_t)h * D + (wt ? o * 8 : 0);
     const int64_t wstride = (int64_t)H * D;
     u32x4 w[WB];
 #pragma unroll
-    for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + k * wstride);
+    for (int k = 0; k < WB; k++)
+        w[k] = (wt && cb + k < dc) ? *(const u32x4 *)(wp + k * wstride) : u32x4{0u, 0u, 0u, 0u};
     // The block's query rows: row (sequence) of the call, query index, first
     // partial (query row qr of slot part), splits.
     int64_t b0[RPB];
@@ -587,7 +606,6 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     for (int j = 0; j < RPB; j++)
 #pragma unroll
         for (int i = 0; i < 8; i++) a[j][i] = 0.f;
-    const int cb = (wt ? g : 0) * CPG;
     auto fma8 = [&](const u32x4 &wv, int c) {
 #pragma unroll
         for (int j = 0; j < RPB; j++) {
@@ -603,7 +621,8 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     for (int k = 0; k < WB; k++) fma8(w[k], cb + k);
     for (int k0 = WB; k0 < CPG; k0 += WB) {
 #pragma unroll
-        for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + (k0 + k) * wstride);
+        for (int k = 0; k < WB; k++)
+            w[k] = (wt && cb + k0 + k < dc) ? *(const u32x4 *)(wp + (k0 + k) * wstride) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int k = 0; k < WB; k++) fma8(w[k], cb + k0 + k);
     }
@@ -638,50 +657,57 @@ static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uin
         plan, pool, table, rows, work, n_rows, qlat, H, P, mask_mode, part_o, part_ml);
 }
 
-template <int D, bool ARG>
+template <int DMAX, bool ARG>
 static void launch_mla_out_d(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
                              int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
-                             const uint16_t *w_uv, int H, int QRP, void *out, int out_bf16, int cus) {
+                             const uint16_t *w_uv, int H, int D, int dc, int QRP, void *out,
+                             int out_bf16, int cus) {
     // Two query rows per block share the W_UV read when that still leaves a
     // block per CU.
     if ((int64_t)H * ((total_q + 1) / 2) >= cus)
-        mla_out_kernel<D, 2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
-            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, QRP, out, out_bf16);
+        mla_out_kernel<DMAX, 2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
+            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, D, dc, QRP, out,
+            out_bf16);
     else
-        mla_out_kernel<D, 1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
-            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, QRP, out, out_bf16);
+        mla_out_kernel<DMAX, 1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
+            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, D, dc, QRP, out,
+            out_bf16);
 }
 
 template <bool ARG>
 static void launch_mla_out(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
                            int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
-                           const uint16_t *w_uv, int H, int hd, int QRP, void *out, int out_bf16,
-                           int cus) {
-    switch (hd) {
-        case 64: launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
-        case 128: launch_mla_out_d<128, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
-        case 192: launch_mla_out_d<192, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
-        default: launch_mla_out_d<256, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, QRP, out, out_bf16, cus); break;
-    }
+                           const uint16_t *w_uv, int H, int hd, int dc, int QRP, void *out,
+                           int out_bf16, int cus) {
+    if (hd <= 32)
+        launch_mla_out_d<32, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+    else if (hd <= 64)
+        launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+    else if (hd <= 128)
+        launch_mla_out_d<128, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+    else
+        launch_mla_out_d<256, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
 }
 
 hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,
                              const int32_t *table, const AttRow *rows, int n_rows,
                              const int2 *work, int n_work,
                              const void *q_nope, const void *q_rope, int q_bf16,
-                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd,
-                             int total_q, int max_nq, int P, float qscale,
+                             const uint16_t *w_uk, const uint16_t *w_uv, int H, int hd, int dc,
+                             int dr, int total_q, int max_nq, int P, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
                              float *part_ml, void *out, int out_bf16, int cus,
                              hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
-    if (hd > 256 || hd % 64 != 0) return hipErrorInvalidValue;
+    if (hd > 256 || hd % 8 != 0 || dc > kMlaDc || dr > kMlaDr) return hipErrorInvalidValue;
     const dim3 ag(H, kMlaDc / 64, (total_q + 15) / 16);
-    switch (hd) {
-        case 64: mla_absorb_kernel<64><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
-        case 128: mla_absorb_kernel<128><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
-        case 192: mla_absorb_kernel<192><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
-        default: mla_absorb_kernel<256><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, total_q, qscale, qlat); break;
+    switch ((hd + 31) / 32) {
+#define RLX_ABSORB(KS) \
+    case KS: mla_absorb_kernel<KS><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, hd, dc, dr, total_q, qscale, qlat); break;
+        RLX_ABSORB(1) RLX_ABSORB(2) RLX_ABSORB(3) RLX_ABSORB(4)
+        RLX_ABSORB(5) RLX_ABSORB(6) RLX_ABSORB(7) RLX_ABSORB(8)
+#undef RLX_ABSORB
+        default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -703,10 +729,10 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     if (e != hipSuccess) return e;
     if (ev1) (void)hipEventRecord(ev1, s);
     if (plan)
-        launch_mla_out<true>(s, *plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd,
+        launch_mla_out<true>(s, *plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc,
                              16 * nqt, out, out_bf16, cus);
     else
-        launch_mla_out<false>(s, NoPlan{0}, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd,
+        launch_mla_out<false>(s, NoPlan{0}, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc,
                               16 * nqt, out, out_bf16, cus);
     return hipGetLastError();
 }

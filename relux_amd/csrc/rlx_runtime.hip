@@ -783,8 +783,13 @@ int32_t rlx_mla_create(int32_t layers, int32_t d_c, int32_t d_r, int32_t page_to
     if (layers <= 0) return fail(RLX_ERR_INVALID, "NewMLACache: numLayers=%d, must be > 0", layers);
     if (pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
         return fail(RLX_ERR_INVALID, "pool_pages, max_seqs, max_pages must be > 0");
-    if (d_c != kMlaDc || d_r != kMlaDr)
-        return fail(RLX_ERR_UNSUPPORTED, "MLA d_c=%d d_r=%d (supported: 512, 64)", d_c, d_r);
+    // NewMLA (mla.go:67-79) takes any dC and an even dHR; the stored row is
+    // the 512 + 64 layout, zero padded past the caller's dims.
+    if (d_c <= 0 || d_r <= 0 || d_r % 2 != 0)
+        return fail(RLX_ERR_INVALID, "NewMLACache: dC=%d dHR=%d (both > 0, dHR even)", d_c, d_r);
+    if (d_c > kMlaDc || d_r > kMlaDr)
+        return fail(RLX_ERR_UNSUPPORTED, "MLA d_c=%d d_r=%d (at most %d and %d)", d_c, d_r, kMlaDc,
+                    kMlaDr);
     if (page_tokens <= 0 || page_tokens % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
     Cache *c = new Cache;
@@ -1074,6 +1079,9 @@ int32_t rlx_mla_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_project_append on a GQA cache");
+    if (c->dc != kMlaDc || c->dr != kMlaDr)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_mla_project_append takes d_c %d and d_r %d (cache: %d, %d)",
+                    kMlaDc, kMlaDr, c->dc, c->dr);
     if (num_heads <= 0 || head_dim <= 0 || head_dim % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim a multiple of 16)",
                     num_heads, head_dim);
@@ -1105,7 +1113,7 @@ int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         return rc;
     HIP_TRY(launch_mla_append(c->stream, plan, tok_off, c->L[layer].pool0, c->d_table, d_patches,
                               (int)patches.size(), d_toks, (int)toks.size(), c_src, kr_src,
-                              src_dtype == RLX_BF16, c->P));
+                              src_dtype == RLX_BF16, c->dc, c->dr, c->P));
     return RLX_OK;
 }
 
@@ -1172,7 +1180,7 @@ int32_t rlx_mla_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
     HIP_TRY(launch_mla_gather(c->stream, c->L[layer].pool0, c->d_table,
                               (const AttRow *)((char *)dev + o_r), n_seqs, max_len,
-                              (uint16_t *)c_out, (uint16_t *)kr_out, c->P));
+                              (uint16_t *)c_out, (uint16_t *)kr_out, c->dc, c->dr, c->P));
     return RLX_OK;
 }
 
@@ -1416,9 +1424,9 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     int32_t rc = check_layer(c, layer, false);
     if (rc) return rc;
     if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
-    if (num_heads <= 0 || head_dim <= 0 || head_dim % 64 != 0 || head_dim > 256)
-        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim in {64,128,192,256})",
-                    num_heads, head_dim);
+    if (num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "num_heads=%d head_dim=%d (head_dim a multiple of 8 up to 256)", num_heads, head_dim);
     if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
     if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
@@ -1432,11 +1440,9 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = num_heads * max_nq;
-    if (max_qr > 32) {
+    if (max_qr > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr) {
         // Chunked prefill: expand the latents into per-head K_c / V^T, then
         // FA2 tiles of kPrefillRows query tokens per head.
-        if (head_dim != 128)
-            return fail(RLX_ERR_UNSUPPORTED, "MLA prefill supports head_dim 128 (got %d)", head_dim);
         std::vector<AttRow> rows;
         std::vector<int2> unused;
         int total_q = 0, mnq = 0, parts = 0;
@@ -1506,17 +1512,64 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         HIP_TRY(launch_prefill(c->stream, kSrcDense, head_dim, a, (int)pwork.size(), e0, e1));
         return RLX_OK;
     }
-    const int nqt = max_qr > 16 ? 2 : 1;
-    // One work-group covers every head of a sequence's split.
-    for (int i = 0; i < n_seqs; i++)
-        if (lens[i] <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
-    const std::vector<int> nsplit = mla_splits(lens, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
+    // Decode / verify -- and chunked prefill for the shapes the FA2 path
+    // does not take: one work-group covers every head of a row's split, at
+    // most 32 query rows (heads x queries) per row.  A call with more query
+    // rows is cut into rows of at most 32 / H queries: the causal chunk
+    // [q0, q0 + qn) of n_q queries on a sequence of len tokens is the row
+    // (len - n_q + q0 + qn tokens, qn queries), which has the same key
+    // limits; an unmasked query is a row of its own (len tokens, 1 query).
+    const bool chunked = max_qr > 32;
+    if (chunked && num_heads > 32)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "MLA attention with more than 32 query rows takes head_dim 128, d_c 512 and d_r 64 "
+                    "when num_heads > 32 (got %d heads, head_dim %d, d_c %d, d_r %d)",
+                    num_heads, head_dim, c->dc, c->dr);
+    const int qc = chunked ? 32 / num_heads : 0;
     std::vector<AttRow> rows;
+    std::vector<int> rlen;
+    int total_q = 0, row_nq = 0;
+    for (int i = 0; i < n_seqs; i++) {
+        const SeqState &st = ls.seqs[seq_ids[i]];
+        const int nq = n_q ? n_q[i] : 1;
+        if (st.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
+        if (nq < 1 || nq > st.len) return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, st.len);
+        const int32_t tab = (int32_t)(c->row_base(layer, seq_ids[i]) + st.first);
+        auto add = [&](int len, int n, int qrow) {
+            AttRow r{};
+            r.tab = tab;
+            r.len = len;
+            r.nq = n;
+            r.qrow = qrow;
+            r.q0 = 0;
+            r.qn = n;
+            rows.push_back(r);
+            rlen.push_back(len);
+            row_nq = std::max(row_nq, n);
+        };
+        if (!chunked) {
+            add(st.len, nq, total_q);
+        } else if (mask_mode == RLX_MASK_CAUSAL || (mask_mode == RLX_MASK_REF && nq == st.len)) {
+            for (int q0 = 0; q0 < nq; q0 += qc) {
+                const int qn = std::min(qc, nq - q0);
+                add(st.len - nq + q0 + qn, qn, total_q + q0);
+            }
+        } else {
+            for (int q = 0; q < nq; q++) add(st.len, 1, total_q + q);
+        }
+        total_q += nq;
+    }
+    const int kmask = chunked ? RLX_MASK_CAUSAL : mask_mode;
+    const int nqt = num_heads * row_nq > 16 ? 2 : 1;
+    const std::vector<int> nsplit = mla_splits(rlen, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
     std::vector<int2> work;
-    int total_q = 0, mnq = 0, parts = 0;
-    if ((rc = build_rows(c, layer, n_seqs, seq_ids, n_q, nsplit.data(), rows, work, &total_q, &mnq,
-                         &parts)))
-        return rc;
+    int parts = 0;
+    for (size_t r = 0; r < rows.size(); r++) {
+        rows[r].nsplit = nsplit[r];
+        rows[r].part = parts;
+        for (int sp = 0; sp < nsplit[r]; sp++) work.push_back(int2{(int)r, sp});
+        parts += nsplit[r];
+    }
     if ((rc = flush_patches(c))) return rc;
     const int QRP = 16 * nqt;
     const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
@@ -1538,16 +1591,16 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         d_rows = (const AttRow *)((char *)dev + o_r);
         d_work = (const int2 *)((char *)dev + o_w);
     }
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + c->dr)));
     const float qscale = scale * 1.4426950408889634f;
     char *ws = (char *)c->ws;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
-    HIP_TRY(launch_mla_decode(c->stream, plan, ls.pool0, c->d_table, d_rows, n_seqs, d_work,
+    HIP_TRY(launch_mla_decode(c->stream, plan, ls.pool0, c->d_table, d_rows, (int)rows.size(), d_work,
                               (int)work.size(), q_nope,
                               q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
-                              (const uint16_t *)w_uv, num_heads, head_dim, total_q, max_nq, c->P,
-                              qscale, mask_mode, nqt, (uint16_t *)ws,
+                              (const uint16_t *)w_uv, num_heads, head_dim, c->dc, c->dr, total_q,
+                              row_nq, c->P, qscale, kmask, nqt, (uint16_t *)ws,
                               (uint16_t *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes), out,
                               out_dtype == RLX_BF16, c->cus, e0, e1));
     return RLX_OK;

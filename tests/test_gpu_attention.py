@@ -298,6 +298,65 @@ def test_mla_attend_matches_oracle(gpu, H, lens, nq, mask):
         toff += L
 
 
+@pytest.mark.parametrize("H,D,dC,dR,lens,nq,mask", [
+    (4, 8, 32, 4, [8, 23, 300], 1, "causal"),      # TestTransformer_MLA's dims (transformer_test.go:1012-1027)
+    (4, 16, 64, 8, [9, 100, 260], 4, "causal"),    # config-1-sized layer, 4-query verify
+    (8, 64, 256, 32, [300, 17], 2, "causal"),
+    (4, 32, 128, 16, [290, 64], 40, "causal"),     # 160 query rows: causal chunks of 8 queries
+    (4, 16, 64, 8, [70, 40], 40, "none"),          # unmasked: a row per query
+    (2, 8, 32, 4, [50], 50, "ref"),                # reference rule with n_q == len: causal
+    (16, 128, 512, 64, [300, 65], 1, "causal"),    # default DeepSeek dims, generic absorb / out
+    (16, 96, 384, 48, [260], 2, "causal"),
+    (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128 prefill through FA2 (240 rows)
+])
+def test_mla_other_dims_match_oracle(gpu, H, D, dC, dR, lens, nq, mask):
+    """MLA at the reference's default dims (dC = 4 headDim, dHR = headDim/2,
+    transformer.go:223-233) and others: latent rows stored zero padded,
+    absorb and W_UV projection at any head_dim multiple of 8, and calls with
+    more than 32 query rows cut into causal query chunks (or single-query
+    rows when unmasked) through the decode kernel."""
+    from relux_amd import MLACache
+    rng = np.random.default_rng(61 + H + D + nq)
+    P = 64 if D >= 64 else 16
+    c = MLACache(num_layers=1, max_len=max(lens) + P, d_c=dC, d_r=dR, page_tokens=P,
+                 max_seqs=len(lens), device=gpu.index)
+    cc = rng.standard_normal((sum(lens), dC), dtype=np.float32)
+    kr = rng.standard_normal((sum(lens), dR), dtype=np.float32)
+    c.Append(0, torch.from_numpy(cc).to(gpu), torch.from_numpy(kr).to(gpu),
+             seq_ids=list(range(len(lens))), n_tok=lens)
+    # weights ~ N(0, 0.5 / sqrt(dC)): scores and outputs of like size at every dC
+    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.5 / math.sqrt(dC), size=(dC, H * D)))
+    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.5 / math.sqrt(dC), size=(dC, H * D)))
+    nqs = [min(nq, L) for L in lens]
+    qn = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    qr = rng.standard_normal((sum(nqs), H, dR), dtype=np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    out = c.Attend(0, t(qn), t(qr), t(w_uk.view(np.int16)).view(torch.bfloat16),
+                   t(w_uv.view(np.int16)).view(torch.bfloat16), H, D,
+                   seq_ids=list(range(len(lens))), n_q=nqs, mask=mask).cpu().numpy()
+    off = toff = 0
+    for i, L in enumerate(lens):
+        cs = oracle.round_bf16(cc[toff:toff + L])
+        ks = oracle.round_bf16(kr[toff:toff + L])
+        qci = qn[off:off + nqs[i]].transpose(1, 0, 2)
+        qri = qr[off:off + nqs[i]].transpose(1, 0, 2)
+        got = out[off:off + nqs[i]].transpose(1, 0, 2)
+        exact = _mla_exact(qci, qri, cs, ks, w_uk, w_uv, _limits(mask, nqs[i], L))
+        # bf16 q_lat and weights P (and, through FA2, bf16 K_c / V) against
+        # exact f64 on outputs of size ~0.1-0.5
+        tol = (2e-2, 2e-3) if nqs[i] * H > 32 else TOL_EXACT
+        _check(got, exact, tol, f"seq {i} len {L} nq {nqs[i]} vs exact")
+        # The oracle's softmax is the reference's fastexp32 (mha.go:823-833,
+        # ~3% per weight): over a few keys its outputs sit ~3e-3 from exact,
+        # so it is compared where many keys average that out.
+        if L >= 200:
+            ref = oracle.mla_attend(qci, qri, cs, ks, w_uk, w_uv, mask)
+            _check(got, ref, TOL_ORACLE, f"seq {i} len {L} nq {nqs[i]} vs oracle")
+        off += nqs[i]
+        toff += L
+    c.close()
+
+
 # ---- chunked prefill (more than 32 query rows per kv head / sequence) -------
 
 @pytest.mark.parametrize("H,KVH,D,lens,nqs,mask", [

@@ -143,6 +143,33 @@ def test_append_gather_other_head_dims(gpu, D):
         assert e.value.code in (_lib.RLX_ERR_UNSUPPORTED, _lib.RLX_ERR_INVALID)
 
 
+@pytest.mark.parametrize("dC,dR", [(32, 4), (64, 8), (256, 32), (100, 6)])
+def test_mla_append_gather_other_dims(gpu, dC, dR):
+    """NewMLACache takes any dC and even dHR (mla_cache.go:38-59): rows are
+    stored zero padded in the 512 + 64 layout and View returns exactly the
+    appended latents and rope keys."""
+    rng = np.random.default_rng(dC + dR)
+    c = _mla(gpu, num_layers=1, max_len=256, d_c=dC, d_r=dR, page_tokens=16, max_seqs=2)
+    rows = [[], []]
+    for n in ([33, 4], [17, 50]):
+        cc = rng.normal(size=(sum(n), dC)).astype(np.float32)
+        kr = rng.normal(size=(sum(n), dR)).astype(np.float32)
+        c.Append(0, torch.from_numpy(cc).to(gpu), torch.from_numpy(kr).to(gpu), seq_ids=[0, 1], n_tok=n)
+        rows[0].append((cc[:n[0]], kr[:n[0]]))
+        rows[1].append((cc[n[0]:], kr[n[0]:]))
+    for s in range(2):
+        gc, gk = c.View(0, s)
+        want_c = oracle.bf16_from_f32(np.concatenate([r[0] for r in rows[s]]))
+        want_k = oracle.bf16_from_f32(np.concatenate([r[1] for r in rows[s]]))
+        assert np.array_equal(gc.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_c)
+        assert np.array_equal(gk.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_k)
+    c.close()
+    from relux_amd import _lib
+    for dc_, dr_ in ((600, 64), (512, 66), (64, 3)):
+        with pytest.raises(_lib.ReluxError):
+            _mla(gpu, num_layers=1, max_len=16, d_c=dc_, d_r=dr_)
+
+
 def test_append_conversion_edge_bits(gpu):
     """NaN / Inf / denormal / tie patterns convert exactly as BF16FromF32."""
     special = np.array([0x7FFFFFFF, 0x7F800001, 0x7FC00000, 0x7F7FFFFF, 0x00000001, 0x00008000,
