@@ -1,4 +1,4 @@
-"""Config-1 tiny GQA decoder on the CPU -- TEST INFRASTRUCTURE ONLY.
+"""Config-1 tiny decoders on the CPU -- TEST INFRASTRUCTURE ONLY.
 
 The README decoder (vocab 100, d_model 64, 4 query heads, 2 KV heads,
 head_dim 16, 2 layers, DFF 128 GELU, MaxSeqLen 64, causal, RoPE base 10000)
@@ -38,10 +38,15 @@ reference output).
 import numpy as np
 
 from . import (add_bias, bf16_from_f32, f32_from_bf16, gelu, gqa_attend, kv_copy_into,
-               matmul_bf16w, rmsnorm, rope_apply, rope_tables)
+               matmul_bf16w, mla_attend, rmsnorm, rope_apply, rope_tables)
 
 CFG1 = dict(vocab=100, d_model=64, heads=4, kv_heads=2, layers=2, dff=128, max_seq=64,
             rope_base=10000.0, eps=1e-5)
+
+# TestTransformer_MLA's configuration (transformer_test.go:1012-1027):
+# head_dim 8, d_c = 4 head_dim, d_r = head_dim / 2.
+CFG_MLA = dict(vocab=100, d_model=32, heads=4, kv_heads=4, layers=2, dff=64, max_seq=32,
+               rope_base=10000.0, eps=1e-5, d_c=32, d_r=4)
 
 
 def make_weights(cfg, seed=0, std=0.02):
@@ -69,6 +74,80 @@ def make_weights(cfg, seed=0, std=0.02):
     W["lm_w"] = mat(d, cfg["vocab"])
     W["lm_b"] = zeros(cfg["vocab"])
     return W
+
+
+def mla_dims(cfg):
+    """(head_dim, d_c, d_r): unset latent dims default to 4 head_dim and
+    head_dim / 2 (transformer.go:223-233)."""
+    D = cfg["d_model"] // cfg["heads"]
+    return D, cfg.get("d_c") or 4 * D, cfg.get("d_r") or D // 2
+
+
+def make_mla_weights(cfg, seed=0, std=0.02):
+    """make_weights' embedding, norms, MLP and head, with each block's
+    attention replaced by the seven MLA matrices of NewMLA (mla.go:110-118),
+    [in, out] layout.  Their values follow NewMLA's initialiser's
+    distribution -- uniform in [-1, 1) scaled by 1/sqrt(rows) (mla.go:84-93)
+    -- drawn from PCG64, so W_UK and W_UV differ (the reference's LCG
+    restarts per matrix, which would make them equal)."""
+    W = make_weights(dict(cfg, kv_heads=cfg["heads"]), seed, std)
+    rng = np.random.default_rng(seed + 1)
+    d, H = cfg["d_model"], cfg["heads"]
+    D, dC, dR = mla_dims(cfg)
+
+    def lin(r, c):
+        return bf16_from_f32((rng.uniform(-1.0, 1.0, (r, c)) / np.sqrt(r)).astype(np.float32))
+
+    for Wl in W["layers"]:
+        for k in ("wq", "wk", "wv", "wo"):
+            del Wl[k]
+        Wl.update(w_q=lin(d, H * D), w_dkv=lin(d, dC), w_uk=lin(dC, H * D), w_uv=lin(dC, H * D),
+                  w_kr=lin(d, dR), w_qr=lin(d, H * dR), w_o=lin(H * D, d))
+    return W
+
+
+class MLARefCache:
+    """The reference MLACache and forwardCached's attention: f32 latent rows
+    (mla_cache.go:171-172), K_c / V decompressed token-major and read
+    head-major (mla.go:326-356, head_major_compat), mask only when
+    seqQ == totalLen (mla.go:368)."""
+
+    def __init__(self, cfg):
+        self.cap = cfg["max_seq"]
+        self.c = [np.zeros((0, mla_dims(cfg)[1]), np.float32) for _ in range(cfg["layers"])]
+        self.kr = [np.zeros((0, mla_dims(cfg)[2]), np.float32) for _ in range(cfg["layers"])]
+
+    def total_len(self, layer):
+        return self.c[layer].shape[0]
+
+    def append(self, layer, c, kr):
+        if self.total_len(layer) + c.shape[0] > self.cap:
+            raise OverflowError("MLACache.Append: overflow")
+        self.c[layer] = np.concatenate([self.c[layer], np.asarray(c, np.float32)])
+        self.kr[layer] = np.concatenate([self.kr[layer], np.asarray(kr, np.float32)])
+
+    def attend(self, layer, qc, qr, w_uk, w_uv):
+        return mla_attend(qc, qr, self.c[layer], self.kr[layer], w_uk, w_uv, mask="ref",
+                          head_major_compat=True)
+
+
+class MLALogicalCache(MLARefCache):
+    """Corrected MLA semantics: head h reads its own slice of the
+    decompressed rows (as the uncached path does, mla.go:159-161), the causal
+    mask is offset by the cached length, and rows are stored bf16 like the
+    device cache (or f32, store_bf16=False)."""
+
+    def __init__(self, cfg, store_bf16=True):
+        super().__init__(cfg)
+        self.store_bf16 = store_bf16
+
+    def append(self, layer, c, kr):
+        if self.store_bf16:
+            c, kr = f32_from_bf16(bf16_from_f32(c)), f32_from_bf16(bf16_from_f32(kr))
+        super().append(layer, c, kr)
+
+    def attend(self, layer, qc, qr, w_uk, w_uv):
+        return mla_attend(qc, qr, self.c[layer], self.kr[layer], w_uk, w_uv, mask="causal")
 
 
 class RefCache:
@@ -165,11 +244,12 @@ class TinyDecoder:
         o = np.ascontiguousarray(np.asarray(o, np.float32).transpose(1, 0, 2)).reshape(S, H * D)
         return matmul_bf16w(o, Wl["wo"])
 
-    def _rope(self, x, start):
-        """x [heads, S, D] at cache position start."""
+    def _rope(self, x, start, tables=None):
+        """x [heads, S, dim] at cache position start."""
+        tables = self.rope if tables is None else tables
         if self.rope_rule == "ref" or start == 0:
-            return rope_apply(x, start, self.rope, self.cfg["max_seq"])
-        return np.concatenate([rope_apply(np.ascontiguousarray(x[:, j:j + 1]), start + j, self.rope,
+            return rope_apply(x, start, tables, self.cfg["max_seq"])
+        return np.concatenate([rope_apply(np.ascontiguousarray(x[:, j:j + 1]), start + j, tables,
                                           self.cfg["max_seq"]) for j in range(x.shape[1])], axis=1)
 
     def forward(self, ids, cache):
@@ -204,6 +284,49 @@ class TinyDecoder:
             out.append(int(np.argmax(steps[-1])))
         gap = min(float(np.diff(np.sort(s)[-2:])[0]) for s in steps)
         return out, np.stack(steps), gap
+
+
+class MLATinyDecoder(TinyDecoder):
+    """The same decoder with AttnType "mla" blocks (transformer_block.go:
+    69-77): each block's attention is MLA.forwardCached (mla.go:272-397) for
+    batch 1 over a pluggable latent cache (MLARefCache, MLALogicalCache or
+    the GPU paged cache in tests, with total_len / append / attend)."""
+
+    def __init__(self, cfg=CFG_MLA, weights=None, seed=0, rope_rule="ref"):
+        cfg = dict(cfg)
+        self.D, self.dC, self.dR = mla_dims(cfg)
+        super().__init__(cfg, weights if weights is not None else make_mla_weights(cfg, seed),
+                         seed, rope_rule)
+        # MLA's own RoPE over d_r dims, base and length of the model's
+        # (NewBlock, transformer_block.go:69-75; NewMLA mla.go:83)
+        self.rope_r = rope_tables(self.dR, cfg["rope_base"], cfg["max_seq"])
+
+    def _attention(self, layer, x, cache):
+        """forwardCached for batch 1; x [S, d_model] -> [S, d_model]."""
+        Wl = self.W["layers"][layer]
+        S = x.shape[0]
+        H, D, dR = self.H, self.D, self.dR
+        # 1. projections (mla.go:286-289)
+        qc = matmul_bf16w(x, Wl["w_q"]).reshape(S, H, D).transpose(1, 0, 2)
+        qr = matmul_bf16w(x, Wl["w_qr"]).reshape(S, H, dR).transpose(1, 0, 2)
+        ckv = matmul_bf16w(x, Wl["w_dkv"])
+        kr = matmul_bf16w(x, Wl["w_kr"])
+        # 3. RoPE of q^R [H, S, dR] and k^R [S, dR] at the cached length
+        # (mla.go:297-310; a rank-2 k^R takes rows as positions)
+        start = cache.total_len(layer)
+        qr = self._rope(np.ascontiguousarray(qr), start, self.rope_r)
+        kr = self._rope(np.ascontiguousarray(kr)[None], start, self.rope_r)[0]
+        # 4-6. append, attention over every cached row (mla.go:312-377)
+        cache.append(layer, np.ascontiguousarray(ckv, np.float32), kr)
+        o = cache.attend(layer, np.ascontiguousarray(qc), qr, Wl["w_uk"], Wl["w_uv"])  # [H, S, D]
+        # 7. back to [S, H*D], W_O (mla.go:385-389)
+        o = np.ascontiguousarray(np.asarray(o, np.float32).transpose(1, 0, 2)).reshape(S, H * D)
+        return matmul_bf16w(o, Wl["w_o"])
+
+    def forward_uncached(self, ids):
+        """The whole sequence in one call at positions 0..S-1 over an f32
+        corrected cache: row t is the exact decode of step t."""
+        return self.forward(ids, MLALogicalCache(self.cfg, store_bf16=False))
 
 
 def ref_byte_image(k_logical, chunks, cap):

@@ -129,3 +129,70 @@ def test_bf16_fixture_known_answers():
     assert m[0x42C90000] == 0x42C9  # 100.5 exact
     assert m[0x80000000] == 0x8000 and m[0x00000001] == 0x0000
     assert m[0x7FFFFFFF] == 0x8000  # NaN payload carries into the sign
+
+
+# ---- AttnType "mla" (TestTransformer_MLA's configuration) ------------------
+
+def test_mla_default_dims():
+    """Unset latent dims default to 4 head_dim and head_dim / 2
+    (transformer.go:223-233); TestTransformer_MLA sets exactly those."""
+    assert td.mla_dims(td.CFG_MLA) == (8, 32, 4)
+    assert td.mla_dims(dict(td.CFG_MLA, d_c=0, d_r=0)) == (8, 32, 4)
+    assert td.mla_dims(dict(td.CFG1, d_c=None, d_r=None)) == (16, 64, 8)
+
+
+@pytest.fixture(scope="module")
+def mla_model():
+    return td.MLATinyDecoder(td.CFG_MLA, seed=0)
+
+
+def test_mla_cached_decode_equals_uncached(mla_model):
+    """Greedy decode over an f32 corrected cache: every step's logits equal
+    the matching row of one uncached forward over the whole sequence
+    (positions 0..S-1 in one call, causal), which pins the cached length,
+    the RoPE offsets of q^R and k^R and the mask."""
+    m = mla_model
+    p = td.prompt_ids(m.cfg)
+    toks, steps, gap = m.generate(p, 16, td.MLALogicalCache(m.cfg, store_bf16=False))
+    full = m.forward_uncached(toks[:-1])
+    np.testing.assert_allclose(steps, full[len(p) - 1:], rtol=0, atol=2e-6)
+    assert gap > 0
+
+
+def test_mla_one_head_compat_equals_corrected():
+    """One head: the reference's head-major read of the decompressed rows is
+    the logical order and its seqQ == totalLen mask is causal, so the
+    reference cache and the corrected f32 cache agree to the bit."""
+    cfg = dict(td.CFG_MLA, d_model=8, heads=1, kv_heads=1)
+    m = td.MLATinyDecoder(cfg, seed=2)
+    p = td.prompt_ids(cfg, seed=2)
+    a, la, _ = m.generate(p, 10, td.MLARefCache(cfg))
+    b, lb, _ = m.generate(p, 10, td.MLALogicalCache(cfg, store_bf16=False))
+    assert a == b
+    np.testing.assert_array_equal(la, lb)
+
+
+def test_mla_four_heads_ref_read_differs(mla_model):
+    """Four heads: forwardCached reads the token-major K_c / V rows
+    head-major (mla.go:348-356), so already the prefill differs from the
+    per-head slices."""
+    m = mla_model
+    p = td.prompt_ids(m.cfg)
+    _, la, _ = m.generate(p, 2, td.MLARefCache(m.cfg))
+    _, lb, _ = m.generate(p, 2, td.MLALogicalCache(m.cfg, store_bf16=False))
+    assert np.abs(la[0] - lb[0]).max() > 1e-3
+
+
+def test_mla_bf16_rows_stay_close(mla_model):
+    """bf16 latent rows (the device cache) against f32 rows (the reference
+    MLACache) over the same tokens: the logits move by the storage rounding
+    only."""
+    m = mla_model
+    p = td.prompt_ids(m.cfg)
+    toks, lf, _ = m.generate(p, 12, td.MLALogicalCache(m.cfg, store_bf16=False))
+    c = td.MLALogicalCache(m.cfg)
+    lb = [m.forward(p, c)[-1]]
+    for t in toks[len(p):-1]:
+        lb.append(m.forward([t], c)[-1])
+    d = np.abs(np.stack(lb) - lf)
+    assert 0 < d.max() < 2e-2 and d.mean() < 2e-3
