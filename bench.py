@@ -389,23 +389,29 @@ def setup_accept(cfg, torch, dev, rng):
 
 def setup_sample(cfg, torch, dev, rng):
     """Sampler.Sample over 64 rows of a 32k vocabulary with every stage on:
-    penalties (64-token window), temperature, top-k, top-p, min-p.
-    Algorithmic bytes: each logit row once."""
-    import numpy as np
-    from relux_amd import Draws, Sampler
-    B, V = cfg["B"], cfg["V"]
+    penalties (64-token window), temperature, top-k, top-p, min-p -- the
+    decode loop's form (rlx_sample_async): logits, each row's token history
+    (256 entries, the last 64 counted), the draws and the chosen tokens all
+    stay on the device, and the windows are counted in the kernel.
+    Algorithmic bytes: each logit row once plus the window ids."""
+    from relux_amd import Sampler
+    B, V, S = cfg["B"], cfg["V"], 256
     c = _select_handle(dev)
     g = torch.Generator(device=dev).manual_seed(7)
     x = torch.randn(B, V, device=dev, generator=g) * 3.0
-    prev = [list(rng.integers(0, V, 64)) for _ in range(B)]
+    hist = torch.randint(0, V, (B, S), device=dev, generator=g, dtype=torch.int32)
+    hist_len = torch.full((B,), S, dtype=torch.int32, device=dev)
+    draws = torch.rand(64, B, device=dev, generator=g)
+    out = torch.empty(B, dtype=torch.int32, device=dev)
     smp = Sampler(temperature=0.8, top_k=50, top_p=0.9, min_p=0.02, repeat_penalty=1.1,
-                  frequency_penalty=0.1, presence_penalty=0.1, repeat_window=64, rand=Draws(seed=8))
+                  frequency_penalty=0.1, presence_penalty=0.1, repeat_window=64)
 
     def step(i):
-        smp.Sample(x, prev, c)
+        smp.SampleAsync(x, hist, hist_len, draws[i % 64], c, out=out)
 
-    b = B * V * 4
-    desc = {"workload": f"sample B{B} V{V} (penalties/64, T0.8, top-k50, top-p0.9, min-p0.02)",
+    b = B * V * 4 + B * 64 * 4
+    desc = {"workload": f"sample B{B} V{V} (penalties/64 of a 256-token device history, T0.8, "
+                        f"top-k50, top-p0.9, min-p0.02; device-resident, no host sync per step)",
             "batch": B, "vocab": V}
     return c, step, B, b, b, desc, "sample_kernel", None
 
@@ -539,27 +545,41 @@ def cpu_baseline_gqa(cfg, lens, budget_s=12.0):
                       f"mha.go:283-348, -O2 -ffp-contract=off, 1 thread), {t_total:.1f} s"}
 
 
-def cpu_baseline_mla(cfg, lens, budget_s=12.0):
+def cpu_baseline_mla(cfg, lens, budget_s=8.0):
     """The reference's MLA decode step (mla.go:309-377: decompress every cached
-    latent through W_UK and W_UV, then attend) restated in C, one thread.
-    Sampled on a subset of heads (cost is linear in heads) and scaled."""
+    latent through W_UK and W_UV, then attend) restated in C, one thread, all
+    heads, one sequence per step (the reference runs batch 1), repeated until
+    the budget is spent."""
     import numpy as np
     import oracle
     H, D, T = cfg["H"], cfg["D"], lens[0] + 1
-    h_s = 1
     rng = np.random.default_rng(8)
     c = oracle.round_bf16(rng.standard_normal((T, 512), dtype=np.float32))
     kr = oracle.round_bf16(rng.standard_normal((T, 64), dtype=np.float32))
-    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, h_s * D)))
-    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, h_s * D)))
-    qc = rng.standard_normal((h_s, 1, D), dtype=np.float32)
-    qr = rng.standard_normal((h_s, 1, 64), dtype=np.float32)
-    t0 = time.perf_counter()
-    oracle.mla_attend(qc, qr, c, kr, w_uk, w_uv, "ref")
-    dt = (time.perf_counter() - t0) * (H / h_s)
-    return {"value": 1.0 / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"1 sequence step at T={T}, {h_s} of {H} heads timed ({dt / (H / h_s):.1f} s) "
-                      f"and scaled x{H // h_s} (decompress-all C restatement of mla.go:309-377, 1 thread)"}
+    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    done, t_total = 0, 0.0
+    while t_total < budget_s and done < 8:
+        qc = rng.standard_normal((H, 1, D), dtype=np.float32)
+        qr = rng.standard_normal((H, 1, 64), dtype=np.float32)
+        t0 = time.perf_counter()
+        oracle.mla_attend(qc, qr, c, kr, w_uk, w_uv, "ref")
+        t_total += time.perf_counter() - t0
+        done += 1
+    return {"value": done / t_total, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{done} single-sequence decode steps at T={T}, all {H} heads (decompress-all C "
+                      f"restatement of mla.go:309-377, -O2 -ffp-contract=off, 1 thread), {t_total:.1f} s"}
+
+
+def host_cores():
+    """The host's core counts, stated beside the single-thread baselines:
+    nproc (the CPUs this process may run on), the machine's logical CPUs,
+    and the parallelism a Go runtime would take by default (GOMAXPROCS
+    defaults to the usable CPU count; the timed loops are single-goroutine
+    whatever it is)."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"host_nproc": nproc, "host_logical_cpus": os.cpu_count(),
+            "gomaxprocs_equiv": int(os.environ.get("GOMAXPROCS", nproc))}
 
 
 def copy_probe(torch, dev, nbytes=1 << 30, reps=20):
@@ -628,6 +648,9 @@ def main():
                      "kernel": s["kernel"], "kernel_avg_us": round(s["kernel_avg_us"], 2),
                      "bound": s["bound"], "kernel_rate": round(s["kernel_rate"], 1),
                      "rate_unit": s["rate_unit"], "kernel_frac_of_peak": round(s["rate_frac"], 4)}
+            if name == "mla8k" and not args.no_cpu:
+                # the reference's MLA decode step timed beside the MLA line
+                entry["cpu_baseline"] = dict(cpu_baseline_mla(WORKLOADS[name], s["lens"]), **host_cores())
             if s["bound"] == "hbm":
                 entry["step_hbm_gbs"] = round(s["step_hbm_gbs"], 1)
             elif s["bound"] == "mfma":
@@ -649,6 +672,8 @@ def main():
             cpu = cpu_baseline_gqa(cfg, r["lens"])
         elif cfg["kind"] == "mla":
             cpu = cpu_baseline_mla(cfg, r["lens"])
+        if cpu is not None:
+            cpu.update(host_cores())
     line = {
         "metric": "decode attn tokens/s + achieved HBM GB/s (% of 8 TB/s) at 1 MI355X, 8k ctx",
         "value": round(r["tokens_per_s"], 1),

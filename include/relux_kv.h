@@ -367,6 +367,23 @@ int32_t rlx_greedy(void *cache, const float *logits, int32_t n_rows, int32_t voc
 int32_t rlx_sample(void *cache, const float *logits, int32_t n_rows, int32_t vocab,
                    int64_t row_stride, const rlx_sampler_t *params, const int32_t *prev_tokens,
                    const int32_t *prev_offsets, const float *uniforms, int32_t *out_tokens);
+/* Sampler.Sample (sampler.go:73-262) over device-resident state, for a
+ * decode loop whose tokens never leave the GPU: the stages of rlx_sample,
+ * with each row's repetition window counted on the device from a token
+ * history.  Row b's history is history[b * hist_stride .. + hist_len[b])
+ * (device int32; hist_len device int32 [n_rows], clamped to
+ * [0, hist_stride]); its window is the last repeat_window entries (all of
+ * them when repeat_window <= 0), and the longest possible window,
+ * min(repeat_window, hist_stride) or hist_stride, must be at most 4096
+ * (RLX_ERR_UNSUPPORTED otherwise).  history NULL: no penalties.  uniforms
+ * (the rng.Float32() draws) are device f32 [n_rows]; out_tokens device
+ * int32 [n_rows].  Enqueued on the cache's stream: nothing is copied to or
+ * from the host and the call does not wait.  Same tokens as rlx_sample
+ * given the same windows and draws. */
+int32_t rlx_sample_async(void *cache, const float *logits, int32_t n_rows, int32_t vocab,
+                         int64_t row_stride, const rlx_sampler_t *params, const int32_t *history,
+                         int64_t hist_stride, const int32_t *hist_len, const float *uniforms,
+                         int32_t *out_tokens);
 /* SpeculativeDecoder.acceptPhase + resampleRejected (speculative.go:203-290)
  * for n_rows sequences at once.  draft_logits [n_rows][max_k][vocab] and
  * target_logits [n_rows][max_k+1][vocab] (device f32; target row i scores

@@ -222,6 +222,13 @@ struct SampleArgs {
     const int32_t *seen_tok;   // per row: distinct window tokens, ascending
     const int32_t *seen_freq;  // ... and their counts
     const int32_t *seen_off;   // n_rows + 1 offsets; nullptr: no penalties
+    // rlx_sample_async: the windows are counted on the device instead, from
+    // row b's history hist[b * hist_stride .. + hist_len[b]) (hist nullptr:
+    // the seen_* lists above, or no penalties)
+    const int32_t *hist;
+    int64_t hist_stride;
+    const int32_t *hist_len;
+    int window;                // repeat_window; <= 0: the whole history
     const float *u;            // one draw per row
     int32_t *out;
 };

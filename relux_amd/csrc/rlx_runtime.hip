@@ -2070,6 +2070,60 @@ int32_t rlx_sample(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
     return RLX_OK;
 }
 
+int32_t rlx_sample_async(void *h, const float *logits, int32_t n_rows, int32_t vocab, int64_t row_stride,
+                         const rlx_sampler_t *p, const int32_t *history, int64_t hist_stride,
+                         const int32_t *hist_len, const float *uniforms, int32_t *out_tokens) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (n_rows < 0 || vocab <= 0 || row_stride < vocab || !p || hist_stride < 0)
+        return fail(RLX_ERR_INVALID, "rlx_sample_async: n_rows=%d vocab=%d row_stride=%lld hist_stride=%lld",
+                    n_rows, vocab, (long long)row_stride, (long long)hist_stride);
+    if (n_rows == 0) return RLX_OK;
+    if (!logits || !uniforms || !out_tokens)
+        return fail(RLX_ERR_INVALID, "rlx_sample_async: null pointer");
+    const bool pen = history && hist_len &&
+                     ((p->repeat_penalty != 1.f && p->repeat_penalty != 0.f) ||
+                      p->frequency_penalty != 0.f || p->presence_penalty != 0.f);
+    if (pen) {
+        if (vocab > kSampMaxVocab)
+            return fail(RLX_ERR_UNSUPPORTED, "rlx_sample_async: penalties with vocab %d > %d", vocab,
+                        kSampMaxVocab);
+        // the longest window a row can have: the last repeat_window entries,
+        // or the whole history row when repeat_window <= 0
+        const int64_t wmax = p->repeat_window > 0 ? std::min<int64_t>(p->repeat_window, hist_stride)
+                                                  : hist_stride;
+        if (wmax > kSampMaxSeen)
+            return fail(RLX_ERR_UNSUPPORTED,
+                        "rlx_sample_async: windows of up to %lld tokens (repeat_window %d, history stride "
+                        "%lld); the device count takes at most %d",
+                        (long long)wmax, p->repeat_window, (long long)hist_stride, kSampMaxSeen);
+    }
+    SampleArgs a{};
+    a.logits = logits;
+    a.stride = row_stride;
+    a.V = vocab;
+    a.temperature = p->temperature;
+    a.top_k = p->top_k;
+    a.top_p = p->top_p;
+    a.min_p = p->min_p;
+    a.rp = p->repeat_penalty;
+    a.fp = p->frequency_penalty;
+    a.pp = p->presence_penalty;
+    a.hist = pen ? history : nullptr;
+    a.hist_stride = hist_stride;
+    a.hist_len = pen ? hist_len : nullptr;
+    a.window = p->repeat_window;
+    a.u = uniforms;
+    a.out = out_tokens;
+    hipEvent_t e0, e1;
+    int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
+    if (rc) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
+    HIP_TRY(launch_sample(c->stream, a, n_rows));
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    return RLX_OK;
+}
+
 int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_logits,
                         const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
                         int32_t max_k, int32_t vocab, const float *uniforms, const rlx_sampler_t *p,

@@ -85,10 +85,19 @@ struct SampLds {
     int sel_i[2];
     float sel_f;
     int best;
-    float cv[kCandCap];
-    int ci[kCandCap];
+    union {
+        struct {
+            float cv[kCandCap];
+            int ci[kCandCap];
+        };
+        // a device-counted repetition window until the row is loaded:
+        // id | count << 18 per distinct id, ascending
+        uint32_t win[2 * kCandCap];
+    };
     float region[kRowCap];
 };
+static_assert(2 * kCandCap == kSampMaxSeen, "the window list fills the candidate arrays");
+static_assert(kSampMaxVocab <= (1 << 18) && kSampMaxSeen < (1 << 13), "id | count << 18 fits 31 bits");
 
 // ---- block-wide reductions and scans: fixed combination order, every
 // thread gets the same result --------------------------------------------
@@ -617,10 +626,11 @@ __device__ int sample_set(Src &c, int top_k, float top_p, float min_p, float r, 
 
 // Bring a row into the working set: LDS values (penalties applied in place,
 // then divided by the temperature) when it fits, else memory reads with the
-// penalised tokens in an LDS bitmap and list.  seen/freq: the row's
+// penalised tokens in an LDS bitmap and list.  seen(i) / freq(i): the row's
 // distinct window tokens (ascending) and counts; ns of them.
+template <class SeenF, class FreqF>
 __device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temperature,
-                         const int32_t *seen, const int32_t *freq, int ns, float rp, float fp, float pp) {
+                         SeenF seen, FreqF freq, int ns, float rp, float fp, float pp) {
     const int tid = threadIdx.x;
     c.row = row;
     c.V = V;
@@ -649,7 +659,10 @@ __device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temp
             for (int v = tid; v < V; v += kST) s.region[v] = row[v];
         }
         __syncthreads();
-        for (int i = tid; i < ns; i += kST) s.region[seen[i]] = pen(s.region[seen[i]], freq[i]);
+        for (int i = tid; i < ns; i += kST) {
+            const int t = seen(i);
+            s.region[t] = pen(s.region[t], freq(i));
+        }
         __syncthreads();
         if (c.div) {
 #pragma unroll 8
@@ -667,9 +680,10 @@ __device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temp
         for (int i = tid; i < (V + 31) >> 5; i += kST) bits[i] = 0u;
         __syncthreads();
         for (int i = tid; i < ns; i += kST) {
-            stok[i] = seen[i];
-            sv[i] = pen(row[seen[i]], freq[i]);
-            atomicOr(&bits[seen[i] >> 5], 1u << (seen[i] & 31));
+            const int t = seen(i);
+            stok[i] = t;
+            sv[i] = pen(row[t], freq(i));
+            atomicOr(&bits[t >> 5], 1u << (t & 31));
         }
         __syncthreads();
         c.nseen = ns;
@@ -680,14 +694,89 @@ __device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temp
 __device__ __forceinline__ int clamp_topk(int k, int V) { return (k < 0 || k >= V) ? 0 : k; }
 __device__ __forceinline__ float clamp_topp(float p) { return (p <= 0.f || p > 1.f) ? 1.f : p; }
 
+// Row b's repetition window counted in LDS (sampler.go:213-262 counts each
+// window token's occurrences; ids outside [0, V) are skipped): the window's
+// ids are set in a bitmap over the vocabulary, an exclusive scan of the
+// bitmap words' popcounts ranks the distinct ids in ascending order, and
+// every window entry adds one to its id's rank.  Leaves s.win[r] = id |
+// count << 18 for ranks r < the returned number of distinct ids; the window
+// holds at most kSampMaxSeen entries (the host checks the bound).
+__device__ int count_window(const SampleArgs &a, int b, SampLds &s) {
+    constexpr int WPT = kSampMaxVocab / 32 / kST;  // bitmap words per thread
+    const int tid = threadIdx.x;
+    const int V = a.V;
+    const int n = (int)max((int64_t)0, min((int64_t)a.hist_len[b], a.hist_stride));
+    const int lo = (a.window > 0 && n > a.window) ? n - a.window : 0;
+    const int w = n - lo;
+    const int32_t *h = a.hist + (int64_t)b * a.hist_stride + lo;
+    const int nw = (V + 31) >> 5;
+    uint32_t *bits = (uint32_t *)s.region;                  // [kSampMaxVocab / 32]
+    int *wpre = (int *)(s.region + kSampMaxVocab / 32);     // rank of each word's first id
+    int *ids = (int *)(s.region + kSampMaxVocab / 16);      // window ids (-1: skipped)
+    int *cnt = ids + kSampMaxSeen;                          // count per rank
+    static_assert(kSampMaxVocab / 16 + 2 * kSampMaxSeen <= kRowCap, "window scratch fits the region");
+    for (int i = tid; i < nw; i += kST) bits[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < w; i += kST) {
+        const int t = h[i];
+        const bool ok = t >= 0 && t < V;
+        ids[i] = ok ? t : -1;
+        if (ok) atomicOr(&bits[t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+    const int w0 = tid * WPT;
+    int local = 0;
+#pragma unroll
+    for (int j = 0; j < WPT; j++)
+        if (w0 + j < nw) local += __popc(bits[w0 + j]);
+    int nd;
+    int base = blk_iscan_excl(local, s, &nd);
+#pragma unroll
+    for (int j = 0; j < WPT; j++)
+        if (w0 + j < nw) {
+            wpre[w0 + j] = base;
+            base += __popc(bits[w0 + j]);
+        }
+    for (int i = tid; i < nd; i += kST) cnt[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < w; i += kST) {
+        const int t = ids[i];
+        if (t >= 0) atomicAdd(&cnt[wpre[t >> 5] + __popc(bits[t >> 5] & ((1u << (t & 31)) - 1u))], 1);
+    }
+    __syncthreads();
+    for (int j = 0; j < WPT; j++) {
+        if (w0 + j >= nw) break;
+        uint32_t m = bits[w0 + j];
+        int r = wpre[w0 + j];
+        while (m) {
+            const int k = __builtin_ctz(m);
+            m &= m - 1u;
+            s.win[r] = (uint32_t)((w0 + j) * 32 + k) | ((uint32_t)cnt[r] << 18);
+            r++;
+        }
+    }
+    __syncthreads();
+    return nd;
+}
+
 __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs a) {
     __shared__ SampLds s;
     const int b = blockIdx.x;
-    const int n0 = a.seen_off ? a.seen_off[b] : 0;
-    const int ns = a.seen_off ? a.seen_off[b + 1] - n0 : 0;
     Src c;
-    load_row(c, s, a.logits + (int64_t)b * a.stride, a.V, a.temperature, a.seen_tok + n0,
-             a.seen_freq + n0, ns, a.rp, a.fp, a.pp);
+    const float *row = a.logits + (int64_t)b * a.stride;
+    if (a.hist) {
+        const int ns = count_window(a, b, s);
+        load_row(
+            c, s, row, a.V, a.temperature, [&](int i) { return (int)(s.win[i] & 0x3FFFFu); },
+            [&](int i) { return (int)(s.win[i] >> 18); }, ns, a.rp, a.fp, a.pp);
+    } else {
+        const int n0 = a.seen_off ? a.seen_off[b] : 0;
+        const int ns = a.seen_off ? a.seen_off[b + 1] - n0 : 0;
+        const int32_t *st = a.seen_tok + n0, *sf = a.seen_freq + n0;
+        load_row(
+            c, s, row, a.V, a.temperature, [&](int i) { return st[i]; }, [&](int i) { return sf[i]; }, ns,
+            a.rp, a.fp, a.pp);
+    }
     const int t = sample_set(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
     if (threadIdx.x == 0) a.out[b] = t;
 }
@@ -827,7 +916,9 @@ __global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
         return;
     }
     Src c;
-    load_row(c, s, tl + (int64_t)k * V, V, a.temperature, nullptr, nullptr, 0, 0.f, 0.f, 0.f);
+    load_row(
+        c, s, tl + (int64_t)k * V, V, a.temperature, [](int) { return 0; }, [](int) { return 0; }, 0, 0.f,
+        0.f, 0.f);
     const int t = sample_set(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
     if (tid == 0) {
         a.n_acc[b] = k;

@@ -97,6 +97,38 @@ class Sampler:
         return out[0] if logits.dim() == 1 else list(out)
 
 
+    def SampleAsync(self, logits, history, hist_len, uniforms, cache, out=None):
+        """Sample over device state (rlx_sample_async): logits [n, V] f32,
+        history [n, S] int32 (each row's previous tokens, hist_len[n] int32
+        of them; None: no penalties), uniforms [n] f32 draws, all device
+        tensors.  Returns (or fills) out [n] int32 on the device; enqueued on
+        the cache's stream without waiting."""
+        x = self._rows(logits)
+        n, V = x.shape[0], x.shape[1]
+        if out is None:
+            out = torch.empty(n, dtype=torch.int32, device=x.device)
+        if out.dtype != torch.int32 or out.numel() != n or not out.is_contiguous():
+            raise ValueError("out must be a contiguous int32 tensor of one entry per row")
+        if uniforms.dtype != torch.float32 or uniforms.numel() != n or not uniforms.is_contiguous():
+            raise ValueError("uniforms must be a contiguous f32 tensor of one draw per row")
+        for name, t in (("out", out), ("uniforms", uniforms), ("history", history), ("hist_len", hist_len)):
+            if t is not None and (not t.is_cuda or t.device != x.device):
+                raise TypeError(f"{name} must be a tensor on the logits' device")
+        hp = hl = None
+        stride = 0
+        if history is not None:
+            if history.dtype != torch.int32 or history.dim() != 2 or history.shape[0] != n or \
+                    history.stride(1) != 1:
+                raise ValueError("history must be int32 [n_rows, S] with unit stride along S")
+            if hist_len.dtype != torch.int32 or hist_len.numel() != n or not hist_len.is_contiguous():
+                raise ValueError("hist_len must be a contiguous int32 tensor of one length per row")
+            hp, hl, stride = history.data_ptr(), hist_len.data_ptr(), history.stride(0)
+        p = self.params()
+        check(_lib.load().rlx_sample_async(cache._h, x.data_ptr(), n, V, x.stride(0), ctypes.byref(p),
+                                           hp, stride, hl, uniforms.data_ptr(), out.data_ptr()))
+        return out
+
+
 def spec_accept(cache, draft_logits, target_logits, draft_tokens, n_draft, uniforms, sampler):
     """Batched acceptPhase (speculative.go:203-290) on the device.
     draft_logits [B, K, V], target_logits [B, K+1, V] (f32 device tensors),

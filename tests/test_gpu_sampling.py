@@ -94,6 +94,79 @@ def test_sample(gpu, handle, name, V):
     assert kept >= rows // 2
 
 
+WINDOW_CASES = [
+    # (V, history stride, repeat_window, id range): ragged histories, ids
+    # outside [0, V) mixed in, windows shorter than, equal to and (0) all of
+    # the history, heavy duplicates from a small id range
+    (100, 40, 16, 100),
+    (4096, 300, 64, 60),
+    (4096, 300, 0, 4096),
+    (32000, 4096, 0, 700),        # whole history at the 4096-entry limit
+    (32000, 5000, 4096, 32000),   # window at the limit inside a longer history
+    (50000, 200, 32, 50000),      # memory-read path (past the LDS row)
+]
+
+
+@pytest.mark.parametrize("V,S_,W,idr", WINDOW_CASES)
+def test_sample_async_equals_host_windows(gpu, handle, V, S_, W, idr):
+    """rlx_sample_async counts each row's window on the device from a device
+    token history; with the same windows and draws it picks the same tokens
+    as rlx_sample, whose windows the host counts."""
+    rng = np.random.default_rng(V + S_ + W)
+    rows = 24
+    p = S.SamplerParams(temperature=0.9, top_k=40, top_p=0.95, repeat_penalty=1.4,
+                        frequency_penalty=0.3, presence_penalty=0.5, repeat_window=W)
+    x = rng.normal(0, 2.5, (rows, V)).astype(np.float32)
+    # make the penalised ids matter: raise the logits of the window ids
+    hist = rng.integers(0, idr, (rows, S_)).astype(np.int32)
+    hist[:, ::7] = -1
+    hist[:, 3::11] = V + 3
+    lens = rng.integers(0, S_ + 1, rows).astype(np.int32)
+    lens[0], lens[1] = 0, S_
+    for b in range(rows):
+        x[b, hist[b, :lens[b]][(hist[b, :lens[b]] >= 0) & (hist[b, :lens[b]] < V)]] += 3.0
+    u = rng.random(rows, dtype=np.float32)
+    smp = make_sampler(p, S.Draws(u))
+    want = smp.Sample(dev(x, gpu), [list(hist[b, :lens[b]]) for b in range(rows)], handle)
+    xd = dev(x, gpu)
+    got = smp.SampleAsync(xd, torch.from_numpy(hist).to(gpu), torch.from_numpy(lens).to(gpu),
+                          torch.from_numpy(u).to(gpu), handle)
+    assert got.cpu().tolist() == list(want)
+    # a strided history (rows of a wider buffer) and an out tensor given
+    wide = torch.zeros(rows, S_ + 9, dtype=torch.int32, device=gpu)
+    wide[:, :S_] = torch.from_numpy(hist).to(gpu)
+    out = torch.full((rows,), -7, dtype=torch.int32, device=gpu)
+    if W == 0 and S_ + 9 > 4096:
+        return
+    smp.SampleAsync(xd, wide[:, :S_], torch.from_numpy(lens).to(gpu), torch.from_numpy(u).to(gpu),
+                    handle, out=out)
+    assert out.cpu().tolist() == list(want)
+
+
+def test_sample_async_no_history_and_limits(gpu, handle):
+    from relux_amd import ReluxError
+    rng = np.random.default_rng(5)
+    V, rows = 1000, 8
+    x = dev(rng.normal(0, 2, (rows, V)), gpu)
+    u = rng.random(rows, dtype=np.float32)
+    p = S.SamplerParams(top_k=20, repeat_penalty=1.3, repeat_window=0)
+    smp = make_sampler(p, S.Draws(u))
+    want = smp.Sample(x, None, handle)
+    got = smp.SampleAsync(x, None, None, torch.from_numpy(u).to(gpu), handle)
+    assert got.cpu().tolist() == list(want)
+    lens = torch.zeros(rows, dtype=torch.int32, device=gpu)
+    ud = torch.from_numpy(u).to(gpu)
+    # longest possible window past 4096 entries: refused before any launch
+    with pytest.raises(ReluxError):
+        smp.SampleAsync(x, torch.zeros(rows, 4097, dtype=torch.int32, device=gpu), lens, ud, handle)
+    smp4097 = make_sampler(S.SamplerParams(repeat_penalty=1.3, repeat_window=4097), S.Draws(u))
+    with pytest.raises(ReluxError):
+        smp4097.SampleAsync(x, torch.zeros(rows, 5000, dtype=torch.int32, device=gpu), lens, ud, handle)
+    # host tensors are refused, not passed to the kernel
+    with pytest.raises(TypeError):
+        smp.SampleAsync(x, None, None, torch.from_numpy(u), handle)
+
+
 @pytest.mark.parametrize("V", [100, 4096, 50000])
 def test_spec_accept(gpu, handle, V):
     from relux_amd import spec_accept
