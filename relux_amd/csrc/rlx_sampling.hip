@@ -22,9 +22,12 @@
 // The reference sorts (argsortDescF32, kthLargest: selection sorts) and sums
 // the vocabulary sequentially.  Here:
 //   * the top-k threshold (k-th largest value) is found one key bit at a
-//     time on the float's order-preserving key (32 counting steps): first
-//     on the per-thread maxima, whose k-th largest bounds it from below,
-//     then on the short list of entries at or above that bound;
+//     time on the float's order-preserving key: first a lower bound, the
+//     k-th largest of the per-thread maxima to 16 key bits, then the exact
+//     value (32 counting steps) on the short list of entries at or above
+//     that bound; the single-wave searches are instantiated for the
+//     64-entry register groups in use, so a list of 100 entries costs one
+//     ballot per step;
 //   * the top-p cutoff is the key tau of the item where the descending
 //     cumulative probability first reaches p, i.e. the largest tau whose
 //     tail sum still reaches p: 31 bisection steps over probabilities kept
@@ -41,6 +44,8 @@
 // Arithmetic follows the reference's f32 order with explicitly rounded
 // operations (no fused multiply-add): s/temp, fastexp32(x - max) with one
 // multiply and one add (mha.go:823-833), p * f32(1/sum).
+#include <type_traits>
+
 #include "rlx_common.h"
 
 namespace rlx {
@@ -311,23 +316,41 @@ __device__ __forceinline__ float wprob(const Src &c, const SampLds &s, int i, in
 
 // Largest key t with #{i < n : key(i) >= t} >= k (the k-th largest key),
 // one bit per step, by wave 0 with the n <= kCandCap keys in registers.
+// Calls f(std::integral_constant<int, G>) with G the power of two >= the
+// number of 64-entry register groups that n entries need (at most R), so
+// the group loops are unrolled to exactly the groups in use.
+template <int R, class F>
+__device__ __forceinline__ void with_groups(int n, F f) {
+    const int g = __builtin_amdgcn_readfirstlane((n + 63) >> 6);
+    if (g <= 1) f(std::integral_constant<int, 1>{});
+    else if (g <= 2) f(std::integral_constant<int, 2>{});
+    else if (g <= 4) f(std::integral_constant<int, 4>{});
+    else if (g <= 8 || R <= 8) f(std::integral_constant<int, (R < 8 ? R : 8)>{});
+    else if (g <= 16 || R <= 16) f(std::integral_constant<int, (R < 16 ? R : 16)>{});
+    else f(std::integral_constant<int, R>{});
+}
+
+// With lo_bit > 0 only the key bits above lo_bit are searched: the result
+// is then a lower bound of the k-th largest key (its low bits zero).
 template <class K>
-__device__ uint32_t kth_key_w0(int n, int k, SampLds &s, K key) {
-    constexpr int R = kCandCap / 64;
+__device__ uint32_t kth_key_w0(int n, int k, SampLds &s, K key, int lo_bit = 0) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
-        uint32_t kk[R];
+        with_groups<kCandCap / 64>(n, [&](auto gc) {
+            constexpr int G = decltype(gc)::value;
+            uint32_t kk[G];
 #pragma unroll
-        for (int j = 0; j < R; j++) kk[j] = (lane + 64 * j < n) ? key(lane + 64 * j) : 0u;
-        uint32_t res = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t cand = res | (1u << bit);
-            int cnt = 0;  // per-key ballots, counted on the scalar unit
+            for (int j = 0; j < G; j++) kk[j] = (lane + 64 * j < n) ? key(lane + 64 * j) : 0u;
+            uint32_t res = 0;
+            for (int bit = 31; bit >= lo_bit; bit--) {
+                const uint32_t cand = res | (1u << bit);
+                int cnt = 0;  // per-key ballots, counted on the scalar unit
 #pragma unroll
-            for (int j = 0; j < R; j++) cnt += (int)__popcll(__ballot(kk[j] >= cand));
-            if (cnt >= k) res = cand;
-        }
-        if (lane == 0) s.sel_i[0] = (int)res;
+                for (int j = 0; j < G; j++) cnt += (int)__popcll(__ballot(kk[j] >= cand));
+                if (cnt >= k) res = cand;
+            }
+            if (lane == 0) s.sel_i[0] = (int)res;
+        });
     }
     __syncthreads();
     const uint32_t r = (uint32_t)s.sel_i[0];
@@ -386,6 +409,36 @@ __device__ int compact_blk(int n, int *tc, SampLds &s, P keep, Vf val, If idx) {
             s.cv[pos] = val(i);
             s.ci[pos] = idx(i);
         }
+    }
+    __syncthreads();
+    return total;
+}
+
+// compact_blk for n <= 64 * kST entries (the LDS row): thread t owns the
+// contiguous entries [t C, t C + C), C = ceil(n / kST) <= 64, marks the kept
+// ones in a 64-bit mask and an ordered exclusive scan of the counts gives
+// its first slot.  One pass over the entries; index order is kept.  (With C
+// odd the lanes of a wave read distinct banks; C = 64, a 32768 row, reads
+// one bank per step.)
+template <class P, class Vf>
+__device__ int compact_chunks(int n, SampLds &s, P keep, Vf val) {
+    const int tid = threadIdx.x;
+    const int C = (n + kST - 1) / kST;
+    const int i0 = tid * C;
+    uint64_t m = 0;
+    for (int j = 0; j < C; j++) {
+        const int i = i0 + j;
+        if (i < n && keep(i)) m |= 1ull << j;
+    }
+    int total;
+    int off = blk_iscan_excl((int)__popcll(m), s, &total);
+    if (total > kCandCap) return total;
+    while (m) {
+        const int j = __builtin_ctzll(m);
+        m &= m - 1;
+        s.cv[off] = val(i0 + j);
+        s.ci[off] = i0 + j;
+        off++;
     }
     __syncthreads();
     return total;
@@ -465,7 +518,7 @@ __device__ int samp_draw(int n, float r, int dflt, SampLds &s, W w, I idx) {
 // within that list, which then becomes the working set (mode 1).  If the
 // list would not fit, the threshold is searched over the whole row.
 template <int M>
-__device__ void topk_select(Src &c, int top_k, SampLds &s) {
+__device__ __forceinline__ void topk_select(Src &c, int top_k, SampLds &s) {
     const int tid = threadIdx.x;
     auto vkey = [&](int i) { return fkey(wval<M>(c, s, i)); };
     if (top_k <= kST) {
@@ -474,11 +527,19 @@ __device__ void topk_select(Src &c, int top_k, SampLds &s) {
         for (int i = tid; i < c.n; i += kST) mk = max(mk, vkey(i));
         s.key[tid] = mk;
         __syncthreads();
-        const uint32_t lb = kth_key_w0(kST, top_k, s, [&](int i) { return s.key[i]; });
-        int *tiles = M == 2 ? (int *)(s.region + kTileOff) : s.tiles;
-        const int total = compact_blk(
-            c.n, tiles, s, [&](int i) { return vkey(i) >= lb; }, [&](int i) { return wval<M>(c, s, i); },
-            [&](int i) { return i; });
+        // a lower bound of the k-th largest maximum is enough here (the
+        // exact threshold is searched in the list): 16 key bits
+        const uint32_t lb = kth_key_w0(kST, top_k, s, [&](int i) { return s.key[i]; }, 16);
+        int total;
+        if constexpr (M == 0) {
+            static_assert(kRowCap <= 64 * kST, "an LDS row is at most 64 entries per thread");
+            total = compact_chunks(
+                c.n, s, [&](int i) { return vkey(i) >= lb; }, [&](int i) { return wval<M>(c, s, i); });
+        } else {
+            total = compact_blk(
+                c.n, (int *)(s.region + kTileOff), s, [&](int i) { return vkey(i) >= lb; },
+                [&](int i) { return wval<M>(c, s, i); }, [&](int i) { return i; });
+        }
         if (total <= kCandCap) {
             c.mode = 1;
             c.n = total;
@@ -503,7 +564,7 @@ __device__ void topk_select(Src &c, int top_k, SampLds &s) {
 // Softmax, top-p, min-p and the draw (sampler.go:117-206) over a working
 // set in mode M.
 template <int M>
-__device__ int sample_finish(Src &c, float top_p, float min_p, float r, SampLds &s) {
+__device__ __forceinline__ int sample_finish(Src &c, float top_p, float min_p, float r, SampLds &s) {
     const int tid = threadIdx.x;
     // Softmax with fastexp32 (sampler.go:117-138).
     float mx = -INFINITY;
@@ -538,25 +599,28 @@ __device__ int sample_finish(Src &c, float top_p, float min_p, float r, SampLds 
             constexpr int R = kCandCap / 64;
             const int lane = tid & 63;
             if (tid < 64) {
-                float pv[R];
+                with_groups<R>(c.n, [&](auto gc) {
+                    constexpr int G = decltype(gc)::value;
+                    float pv[G];
 #pragma unroll
-                for (int j = 0; j < R; j++) pv[j] = (lane + 64 * j < c.n) ? s.cv[lane + 64 * j] : 0.f;
-                auto tail = [&](uint32_t t) {
-                    float a = 0.f;
+                    for (int j = 0; j < G; j++) pv[j] = (lane + 64 * j < c.n) ? s.cv[lane + 64 * j] : 0.f;
+                    auto tail = [&](uint32_t t) {
+                        float a = 0.f;
 #pragma unroll
-                    for (int j = 0; j < R; j++) a += (fkey(pv[j]) >= t) ? pv[j] : 0.f;
-                    return wave_sum_dpp(a);
-                };
-                uint32_t rr = 0x80000000u;  // key of +0: the whole set
-                if (tail(rr) >= top_p) {
-                    for (int bit = 30; bit >= 0; bit--) {
-                        const uint32_t cand = rr | (1u << bit);
-                        if (tail(cand) >= top_p) rr = cand;
+                        for (int j = 0; j < G; j++) a += (fkey(pv[j]) >= t) ? pv[j] : 0.f;
+                        return wave_sum_dpp(a);
+                    };
+                    uint32_t rr = 0x80000000u;  // key of +0: the whole set
+                    if (tail(rr) >= top_p) {
+                        for (int bit = 30; bit >= 0; bit--) {
+                            const uint32_t cand = rr | (1u << bit);
+                            if (tail(cand) >= top_p) rr = cand;
+                        }
+                    } else {
+                        rr = 0;  // never reached: keep everything
                     }
-                } else {
-                    rr = 0;  // never reached: keep everything
-                }
-                if (lane == 0) s.sel_i[0] = (int)rr;
+                    if (lane == 0) s.sel_i[0] = (int)rr;
+                });
             }
             __syncthreads();
             res = (uint32_t)s.sel_i[0];
@@ -612,7 +676,7 @@ __device__ int sample_finish(Src &c, float top_p, float min_p, float r, SampLds 
         c.n, r, c.V - 1, s, [&](int i) { return wprob<M>(c, s, i, 3); }, [&](int i) { return widx<M>(s, i); });
 }
 
-__device__ int sample_set(Src &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
+__device__ __forceinline__ int sample_set(Src &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
     if (top_k > 0 && top_k < c.n) {
         if (c.mode == 0)
             topk_select<0>(c, top_k, s);
@@ -629,7 +693,7 @@ __device__ int sample_set(Src &c, int top_k, float top_p, float min_p, float r, 
 // penalised tokens in an LDS bitmap and list.  seen(i) / freq(i): the row's
 // distinct window tokens (ascending) and counts; ns of them.
 template <class SeenF, class FreqF>
-__device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temperature,
+__device__ __forceinline__ void load_row(Src &c, SampLds &s, const float *row, int V, float temperature,
                          SeenF seen, FreqF freq, int ns, float rp, float fp, float pp) {
     const int tid = threadIdx.x;
     c.row = row;
@@ -649,27 +713,32 @@ __device__ void load_row(Src &c, SampLds &s, const float *row, int V, float temp
         return x;
     };
     if (V <= kRowCap) {
+        // scratch value = pen(x) / temperature (sampler.go:80-97), the
+        // division applied as the row is stored; the penalised entries are
+        // then rewritten from their logits
         c.mode = 0;
+        const bool div = c.div;
+        auto dv = [&](float x) { return div ? __fdiv_rn(x, t) : x; };
         if ((((uintptr_t)row) & 15) == 0 && (V & 3) == 0) {
             const float4 *r4 = (const float4 *)row;
 #pragma unroll 8
-            for (int v = tid; v < V / 4; v += kST) ((float4 *)s.region)[v] = r4[v];
+            for (int v = tid; v < V / 4; v += kST) {
+                const float4 x = r4[v];
+                ((float4 *)s.region)[v] = make_float4(dv(x.x), dv(x.y), dv(x.z), dv(x.w));
+            }
         } else {
 #pragma unroll 8
-            for (int v = tid; v < V; v += kST) s.region[v] = row[v];
+            for (int v = tid; v < V; v += kST) s.region[v] = dv(row[v]);
         }
         __syncthreads();
-        for (int i = tid; i < ns; i += kST) {
-            const int t = seen(i);
-            s.region[t] = pen(s.region[t], freq(i));
-        }
-        __syncthreads();
-        if (c.div) {
-#pragma unroll 8
-            for (int v = tid; v < V; v += kST) s.region[v] = __fdiv_rn(s.region[v], c.temp);
+        if (ns > 0) {
+            for (int i = tid; i < ns; i += kST) {
+                const int k = seen(i);
+                s.region[k] = dv(pen(row[k], freq(i)));
+            }
             __syncthreads();
-            c.div = false;
         }
+        c.div = false;
         return;
     }
     c.mode = 2;
@@ -701,7 +770,7 @@ __device__ __forceinline__ float clamp_topp(float p) { return (p <= 0.f || p > 1
 // every window entry adds one to its id's rank.  Leaves s.win[r] = id |
 // count << 18 for ranks r < the returned number of distinct ids; the window
 // holds at most kSampMaxSeen entries (the host checks the bound).
-__device__ int count_window(const SampleArgs &a, int b, SampLds &s) {
+__device__ __forceinline__ int count_window(const SampleArgs &a, int b, SampLds &s) {
     constexpr int WPT = kSampMaxVocab / 32 / kST;  // bitmap words per thread
     const int tid = threadIdx.x;
     const int V = a.V;
