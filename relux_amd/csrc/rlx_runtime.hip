@@ -565,12 +565,23 @@ int32_t gqa_decode_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids,
 // (row r, range i) = r + i); pre[n_rows + 1] and cuts[n_ranges + 1] are the
 // caller's scratch.  Returns the number of ranges (at most cus / kvh).
 constexpr int kGqaSnap64 = 4;
+// Work-groups per CU of the GQA decode (tuning override RLX_GQA_WG_PER_CU,
+// 1..4; default 1).
+int gqa_wg_per_cu() {
+    static const int v = [] {
+        const char *e = getenv("RLX_GQA_WG_PER_CU");
+        const int x = e ? atoi(e) : 1;
+        return (x >= 1 && x <= 4) ? x : 1;
+    }();
+    return v;
+}
 int gqa_decode_split(const Cache *c, AttRow *rows, int n_rows, int *pre, int *cuts, int4 *ranges,
                      int *total64_out) {
     pre[0] = 0;
     for (int i = 0; i < n_rows; i++) pre[i + 1] = pre[i] + (rows[i].len + 63) / 64;
     const int total64 = pre[n_rows];
-    const int n_ranges = std::max(1, std::min(c->cus / c->kvh, total64));
+    const int n_ranges =
+        std::max(1, std::min({c->cus * gqa_wg_per_cu() / c->kvh, c->cus, total64}));
     gqa_range_cuts(pre, n_rows, n_ranges, kGqaSnap64, cuts);
     for (int k = 0; k < n_rows; k++) rows[k].part = -1;
     int r = 0;
@@ -1382,7 +1393,8 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
         return fail(RLX_ERR_UNSUPPORTED,
                     "rlx_gqa_attend_noalloc takes at most %d rows (sequences or query tiles), got %d",
                     kRowCap, n_rows);
-    if (c->cus / c->kvh > kRangeCap) return fail(RLX_ERR_UNSUPPORTED, "%d CUs", c->cus);
+    if (std::min(c->cus * gqa_wg_per_cu() / c->kvh, c->cus) > kRangeCap)
+        return fail(RLX_ERR_UNSUPPORTED, "%d CUs x %d work-groups per CU", c->cus, gqa_wg_per_cu());
     int pre[kRowCap + 1], cuts[kRangeCap + 1];
     int4 ranges[kRangeCap];
     int total64 = 0;
