@@ -378,7 +378,7 @@ constexpr int kPrefillRows = 256;
 struct PrefillArgs {
     const uint16_t *kpool;  // paged: K row pages; dense: latent pool (rope keys)
     const uint16_t *vpool;  // paged: V dim-major pages
-    const uint16_t *kc;     // dense: K_c [H][Tp][128], sequence s at + part*H*128
+    const uint16_t *kc;     // dense: K_c [H][Tp][128] of the H heads expanded, sequence s at + part*H*128
     const uint16_t *vt;     // dense: V^T [H][128][Tp], same sequence offsets
     const int32_t *table;
     const AttRow *rows;     // dense: part = token offset of the sequence, nsplit = Tp
@@ -388,16 +388,22 @@ struct PrefillArgs {
     void *out;
     int q_bf16, layout, out_bf16, mask_mode;
     int H, KVH, P;
+    int HQ, h0;  // q / out rows hold HQ heads; work-item head h is the caller's head h0 + h
     int pshift;  // log2(P) when P is a power of two, else -1
     float qscale;
 };
 
 hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, int n_work,
                           hipEvent_t ev0, hipEvent_t ev1);
+// W_UK / W_UV [d_c][H*D] transposed to wt [H*D][d_c] (once per call).
+hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_uv, int H, int D,
+                         uint16_t *wt_k, uint16_t *wt_v);
+// K_c / V^T of H heads from their transposed weights (wt_k, wt_v: the
+// heads' rows of the transposed matrices).
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, const int2 *work, int n_work, const uint16_t *w_uk,
-                             const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
-                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt, int cus);
+                             const AttRow *rows, const int2 *work, int n_work, int H, int D, int P,
+                             const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,
+                             int cus);
 
 // Fused projection + RoPE + paged append (at most 64 rows per launch).
 constexpr int kProjRows = 64;

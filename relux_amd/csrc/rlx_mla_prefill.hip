@@ -227,17 +227,21 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
     }
 }
 
-hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, const int2 *work, int n_work, const uint16_t *w_uk,
-                             const uint16_t *w_uv, int H, int D, int P, uint16_t *wt_k,
-                             uint16_t *wt_v, uint16_t *kc, uint16_t *vt, int cus) {
-    if (D != 128) return hipErrorInvalidValue;
+hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_uv, int H, int D,
+                         uint16_t *wt_k, uint16_t *wt_v) {
     const int N = H * D;
     dim3 tg((N + 63) / 64, (kMlaDc + 63) / 64);
     transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uk, wt_k, kMlaDc, N);
     transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uv, wt_v, kMlaDc, N);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    return hipGetLastError();
+}
+
+hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                             const AttRow *rows, const int2 *work, int n_work, int H, int D, int P,
+                             const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,
+                             int cus) {
+    if (D != 128) return hipErrorInvalidValue;
+    const int N = H * D;
     if (n_work <= 0) return hipSuccess;
     const int tiles = (N + kXM - 1) / kXM * n_work;
     const int grid = std::max(1, std::min(tiles, cus));

@@ -256,11 +256,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                 const int D = (SRC == kSrcPaged) ? DQK : 128;
                 src = a.q;
                 off = (a.layout == kLayoutSHD || SRC == kSrcDense)
-                          ? ((int64_t)(R.qrow + jc) * a.H + h) * D + d0
-                          : ((int64_t)R.qrow * a.H + (int64_t)h * R.nq + jc) * D + d0;
+                          ? ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + h) * D + d0
+                          : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + h) * R.nq + jc) * D + d0;
             } else {
                 src = a.q2;
-                off = ((int64_t)(R.qrow + jc) * a.H + h) * kMlaDr + (d0 - 128);
+                off = ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + h) * kMlaDr + (d0 - 128);
             }
             if (a.q_bf16) {
                 const u32x4 raw = *(const u32x4 *)((const uint16_t *)src + off);
@@ -410,8 +410,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
         const int j = rtok[nt], h = rhead[nt];
         const int64_t obase = (a.layout == kLayoutSHD || SRC == kSrcDense)
-                                  ? ((int64_t)(R.qrow + j) * a.H + h) * DV
-                                  : ((int64_t)R.qrow * a.H + (int64_t)h * R.nq + j) * DV;
+                                  ? ((int64_t)(R.qrow + j) * a.HQ + a.h0 + h) * DV
+                                  : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + h) * R.nq + j) * DV;
 #pragma unroll
         for (int md = 0; md < MD; md++) {
             const fl4 o = acc[nt][md] * inv;

@@ -567,6 +567,14 @@ int32_t gqa_decode_rows(Cache *c, int layer, int n_seqs, const int32_t *seq_ids,
 constexpr int kGqaSnap64 = 4;
 // Work-groups per CU of the GQA decode (tuning override RLX_GQA_WG_PER_CU,
 // 1..4; default 1).
+// Bytes the MLA prefill may expand K_c and V^T into at once (4 GiB: config
+// 4's 2.15 GB in one group; tuning override RLX_MLA_EXPAND_MB, read per call).
+int64_t mla_expand_budget() {
+    const char *e = getenv("RLX_MLA_EXPAND_MB");
+    const int64_t mb = e ? atoll(e) : 0;
+    return mb > 0 ? mb << 20 : (int64_t)4 << 30;
+}
+
 int gqa_wg_per_cu() {
     static const int v = [] {
         const char *e = getenv("RLX_GQA_WG_PER_CU");
@@ -1292,6 +1300,8 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         a.out_bf16 = out_dtype == RLX_BF16;
         a.mask_mode = mask_mode;
         a.H = num_heads;
+        a.HQ = num_heads;
+        a.h0 = 0;
         a.KVH = c->kvh;
         a.P = c->P;
         a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
@@ -1480,12 +1490,32 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
             }
             tok_off += Tp;
         }
-        const std::vector<int4> pwork = xcd_order(pgroups, pcost);
-        if (tok_off * num_heads * 128 > INT32_MAX)
-            return fail(RLX_ERR_UNSUPPORTED, "MLA prefill call too large (%lld expanded rows)", (long long)tok_off);
+        // Heads per expansion: the expanded K_c and V^T of hg heads (2 x
+        // tok_off x hg x 128 bf16) stay within the expansion budget and the
+        // kernels' 32-bit element offsets; larger calls run head group by
+        // head group (expansion, then FA2 over the group's heads).
+        const int64_t head_bytes = 2 * tok_off * 128 * 2;
+        const int64_t hg_budget = mla_expand_budget() / head_bytes;
+        const int64_t hg_index = INT32_MAX / (tok_off * 128);
+        const int hg = (int)std::min<int64_t>({(int64_t)num_heads, hg_budget, hg_index});
+        if (hg < 1)
+            return fail(RLX_ERR_UNSUPPORTED,
+                        "MLA prefill call too large: one head expands to %lld bytes over %lld tokens",
+                        (long long)head_bytes, (long long)tok_off);
+        const int n_groups = (num_heads + hg - 1) / hg;
+        // work items of the group of heads [0, hg) (the xcd order), reused by
+        // every group with its heads counted from the group's first
+        std::vector<std::vector<int4>> pg_grp;
+        std::vector<double> pc_grp;
+        for (size_t k = 0; k < pgroups.size(); k++)
+            if (pgroups[k][0].y < hg) {
+                pg_grp.push_back(pgroups[k]);
+                pc_grp.push_back(pcost[k]);
+            }
+        const std::vector<int4> pwork = xcd_order(pg_grp, pc_grp);
         if ((rc = flush_patches(c))) return rc;
         const size_t w_bytes = (size_t)num_heads * 128 * kMlaDc * 2;
-        const size_t e_bytes = (size_t)tok_off * num_heads * 128 * 2;
+        const size_t e_bytes = (size_t)tok_off * hg * 128 * 2;
         if ((rc = ensure_ws(c, 2 * w_bytes + 2 * e_bytes))) return rc;
         Blob b;
         size_t o_r = b.add(rows), o_d = b.add(dwork), o_p = b.add(pwork);
@@ -1495,33 +1525,52 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
         uint16_t *wt_k = (uint16_t *)ws, *wt_v = (uint16_t *)(ws + w_bytes);
         uint16_t *kc = (uint16_t *)(ws + 2 * w_bytes), *vt = (uint16_t *)(ws + 2 * w_bytes + e_bytes);
         const AttRow *drows = (const AttRow *)((char *)dev + o_r);
-        HIP_TRY(launch_mla_expand(c->stream, ls.pool0, c->d_table, drows,
-                                  (const int2 *)((char *)dev + o_d), (int)dwork.size(),
-                                  (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
-                                  c->P, wt_k, wt_v, kc, vt, c->cus));
+        HIP_TRY(launch_mla_wt(c->stream, (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
+                              wt_k, wt_v));
         if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
-        PrefillArgs a{};
-        a.kpool = ls.pool0;
-        a.kc = kc;
-        a.vt = vt;
-        a.table = c->d_table;
-        a.rows = drows;
-        a.work = (const int4 *)((char *)dev + o_p);
-        a.q = q_nope;
-        a.q2 = q_rope;
-        a.out = out;
-        a.q_bf16 = q_dtype == RLX_BF16;
-        a.layout = RLX_LAYOUT_SHD;
-        a.out_bf16 = out_dtype == RLX_BF16;
-        a.mask_mode = mask_mode;
-        a.H = num_heads;
-        a.KVH = num_heads;
-        a.P = c->P;
-        a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
-        a.qscale = scale * 1.4426950408889634f;
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
-        HIP_TRY(launch_prefill(c->stream, kSrcDense, head_dim, a, (int)pwork.size(), e0, e1));
+        for (int g = 0; g < n_groups; g++) {
+            const int h0 = g * hg, nh = std::min(hg, num_heads - h0);
+            HIP_TRY(launch_mla_expand(c->stream, ls.pool0, c->d_table, drows,
+                                      (const int2 *)((char *)dev + o_d), (int)dwork.size(), nh, head_dim,
+                                      c->P, wt_k + (size_t)h0 * 128 * kMlaDc,
+                                      wt_v + (size_t)h0 * 128 * kMlaDc, kc, vt, c->cus));
+            PrefillArgs a{};
+            a.kpool = ls.pool0;
+            a.kc = kc;
+            a.vt = vt;
+            a.table = c->d_table;
+            a.rows = drows;
+            a.work = (const int4 *)((char *)dev + o_p);
+            a.q = q_nope;
+            a.q2 = q_rope;
+            a.out = out;
+            a.q_bf16 = q_dtype == RLX_BF16;
+            a.layout = RLX_LAYOUT_SHD;
+            a.out_bf16 = out_dtype == RLX_BF16;
+            a.mask_mode = mask_mode;
+            a.H = nh;
+            a.KVH = nh;
+            a.HQ = num_heads;
+            a.h0 = h0;
+            a.P = c->P;
+            a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
+            a.qscale = scale * 1.4426950408889634f;
+            // work items of heads >= nh (a last, smaller group) are dropped
+            int n_work = (int)pwork.size();
+            if (nh < hg) {
+                std::vector<int4> part_w;
+                for (const int4 &w : pwork)
+                    if (w.y < nh) part_w.push_back(w);
+                void *dp;
+                if ((rc = stage(c, part_w.data(), part_w.size() * sizeof(int4), &dp))) return rc;
+                a.work = (const int4 *)dp;
+                n_work = (int)part_w.size();
+            }
+            HIP_TRY(launch_prefill(c->stream, kSrcDense, head_dim, a, n_work, g == 0 ? e0 : nullptr,
+                                   g == n_groups - 1 ? e1 : nullptr));
+        }
         return RLX_OK;
     }
     // Decode / verify -- and chunked prefill for the shapes the FA2 path

@@ -481,6 +481,34 @@ def test_mla_prefill_matches_oracle(gpu, H, lens, nqs, mask):
         toff += L
 
 
+@pytest.mark.parametrize("H,budget_mb", [(24, 2), (16, 3)])
+def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
+    """A chunked-prefill call whose expanded K_c / V^T exceed the expansion
+    budget runs head group by head group; each head's attention is the same
+    computation, so the output equals the one-group call bit for bit (here
+    the budget is shrunk to force 8 and 4 groups of 3 / 5 + a smaller last
+    group)."""
+    from relux_amd import MLACache
+    rng = np.random.default_rng(77 + H)
+    D, P, lens, nqs = 128, 64, [700, 300], [200, 120]
+    c = MLACache(num_layers=1, max_len=max(lens) + 64, page_tokens=P, max_seqs=2, device=gpu.index)
+    c.Append(0, torch.from_numpy(rng.standard_normal((sum(lens), 512), dtype=np.float32)).to(gpu),
+             torch.from_numpy(rng.standard_normal((sum(lens), 64), dtype=np.float32)).to(gpu),
+             seq_ids=[0, 1], n_tok=lens)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    w = [t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D))).view(np.int16)).view(torch.bfloat16)
+         for _ in range(2)]
+    qn = t(rng.standard_normal((sum(nqs), H, D), dtype=np.float32))
+    qr = t(rng.standard_normal((sum(nqs), H, 64), dtype=np.float32))
+    args = (0, qn, qr, w[0], w[1], H, D)
+    one = c.Attend(*args, seq_ids=[0, 1], n_q=nqs).cpu()
+    # expanded bytes per head: 2 x (768 + 384 padded tokens) x 128 x 2 B = 0.56 MB
+    monkeypatch.setenv("RLX_MLA_EXPAND_MB", str(budget_mb))
+    grouped = c.Attend(*args, seq_ids=[0, 1], n_q=nqs).cpu()
+    assert torch.equal(one, grouped)
+    c.close()
+
+
 def test_spec_verify_stress_small(gpu):
     """Config 5 at small scale: every step appends 4 drafts per sequence,
     verifies them (4 drafts x 8 heads = 32 rows per kv head), rolls back a
