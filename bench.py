@@ -351,14 +351,17 @@ def _select_handle(dev):
 
 
 def setup_accept(cfg, torch, dev, rng):
-    """Batched acceptPhase: 64 sequences x 4 drafts over a 32k vocabulary.
-    Target rows are the draft rows plus noise (acceptance varies by row);
-    drafts are drawn from the draft rows.  Algorithmic bytes per call: the
-    logit rows the reference's acceptPhase examines (draft and target row of
-    each tested draft, plus the next target row when all are accepted),
-    counted from each call's results."""
+    """Batched acceptPhase: 64 sequences x 4 drafts over a 32k vocabulary,
+    in the speculative loop's device-resident form (rlx_spec_accept_async:
+    drafts, counts, draws and results stay on the GPU).  Target rows are the
+    draft rows plus noise (acceptance varies by row); drafts are drawn from
+    the draft rows.  Algorithmic bytes per call: the logit rows the
+    reference's acceptPhase examines (draft and target row of each tested
+    draft, plus the next target row when all are accepted), counted after
+    the run from each timed call's accepted counts (kept on the device, one
+    row per call)."""
     import numpy as np
-    from relux_amd import Sampler, spec_accept
+    from relux_amd import Sampler, spec_accept_async
     B, K, V = cfg["B"], cfg["K"], cfg["V"]
     c = _select_handle(dev)
     g = torch.Generator(device=dev).manual_seed(6)
@@ -366,23 +369,28 @@ def setup_accept(cfg, torch, dev, rng):
     t = torch.cat([d + torch.randn(B, K, V, device=dev, generator=g) * 0.6,
                    torch.randn(B, 1, V, device=dev, generator=g) * 2.0], dim=1)
     tok = torch.multinomial(torch.softmax(d.reshape(B * K, V), dim=-1), 1, generator=g)
-    tok = tok.reshape(B, K).cpu().numpy().astype(np.int32)
+    tok = tok.reshape(B, K).to(torch.int32).contiguous()
+    nd = torch.full((B,), K, dtype=torch.int32, device=dev)
+    draws = torch.rand(64, B, K + 1, device=dev, generator=g)
+    NS = 8192  # calls recorded (warm-up + timed)
+    acc_all = torch.empty(NS, B, dtype=torch.int32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
     smp = Sampler(temperature=0.8, top_k=50, top_p=0.9)
-    nd = [K] * B
-    state = {"bytes": 0, "steps": 0, "accepted": 0}
+    state = {"bytes": 0, "steps": 0, "accepted": 0, "last": 0}
 
     def step(i):
-        u = rng.random((B, K + 1), dtype=np.float32)
-        acc, _ = spec_accept(c, d, t, tok, nd, u, smp)
+        spec_accept_async(c, d, t, tok, nd, draws[i % 64], smp, n_acc=acc_all[i % NS], next_tok=nxt)
         state["steps"] += 1
-        state["accepted"] += sum(acc)
-        state["bytes"] += sum((min(a + 1, K) * 2 + (a == K)) * V * 4 for a in acc)
+        state["last"] = i
 
     def finish():
-        b = state["bytes"] // max(state["steps"], 1)
-        return b, b, {"acceptance_timed": state["accepted"] / max(state["steps"] * B * K, 1)}
+        n, last = state["steps"], state["last"]
+        acc = acc_all[[(last - j) % NS for j in range(n)]].cpu().numpy()
+        b = int(sum((min(a + 1, K) * 2 + (a == K)) * V * 4 for a in acc.ravel())) // max(n, 1)
+        return b, b, {"acceptance_timed": float(acc.sum()) / max(n * B * K, 1)}
 
-    desc = {"workload": f"spec_accept B{B} drafts{K} V{V} (acceptPhase + resample, T0.8 top-k50 top-p0.9)",
+    desc = {"workload": f"spec_accept B{B} drafts{K} V{V} (acceptPhase + resample, T0.8 top-k50 top-p0.9; "
+                        f"device-resident, no host sync per step)",
             "batch": B, "drafts": K, "vocab": V, "state": state, "finish": finish}
     return c, step, B, 0, 0, desc, "spec_accept_kernel", None
 

@@ -398,6 +398,18 @@ int32_t rlx_spec_accept(void *cache, const float *draft_logits, const float *tar
                         const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
                         int32_t max_k, int32_t vocab, const float *uniforms,
                         const rlx_sampler_t *params, int32_t *n_accepted, int32_t *next_token);
+/* rlx_spec_accept over device-resident state, for a speculative loop whose
+ * drafts and tokens never leave the GPU: draft_tokens [n_rows][max_k],
+ * n_draft [n_rows] and uniforms [n_rows][max_k+1] are device arrays, and
+ * n_accepted / next_token [n_rows] device int32 outputs.  The draft counts
+ * and ids are not seen by the host: a count is clamped to [0, max_k] and
+ * an id outside [0, vocab) is treated as a rejection at its position.
+ * Enqueued on the cache's stream; nothing is copied and the call does not
+ * wait.  Same results as rlx_spec_accept on valid inputs. */
+int32_t rlx_spec_accept_async(void *cache, const float *draft_logits, const float *target_logits,
+                              const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
+                              int32_t max_k, int32_t vocab, const float *uniforms,
+                              const rlx_sampler_t *params, int32_t *n_accepted, int32_t *next_token);
 
 /* ---- state queries (synchronising) ------------------------------------ */
 /* Live token count; replaces TotalLen (kvcache.go:383-388). */

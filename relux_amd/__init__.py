@@ -10,7 +10,7 @@ reference's Go cache types (internal/transformer/kvcache.go, mla_cache.go).
 from ._lib import ReluxError, ReluxPanic, load  # noqa: F401
 
 __all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "pack_mla_proj", "pack_out", "rope_tables",
-           "Sampler", "SpeculativeDecoder", "Draws", "spec_accept"]
+           "Sampler", "SpeculativeDecoder", "Draws", "spec_accept", "spec_accept_async"]
 
 
 def __getattr__(name):
@@ -18,7 +18,7 @@ def __getattr__(name):
     if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "pack_mla_proj", "pack_out", "rope_tables"):
         from . import kvcache
         return getattr(kvcache, name)
-    if name in ("Sampler", "SpeculativeDecoder", "Draws", "spec_accept"):
+    if name in ("Sampler", "SpeculativeDecoder", "Draws", "spec_accept", "spec_accept_async"):
         from . import sampling
         return getattr(sampling, name)
     raise AttributeError(name)

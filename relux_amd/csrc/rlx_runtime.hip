@@ -2185,6 +2185,42 @@ int32_t rlx_sample_async(void *h, const float *logits, int32_t n_rows, int32_t v
     return RLX_OK;
 }
 
+int32_t rlx_spec_accept_async(void *h, const float *draft_logits, const float *target_logits,
+                              const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
+                              int32_t max_k, int32_t vocab, const float *uniforms, const rlx_sampler_t *p,
+                              int32_t *n_accepted, int32_t *next_token) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (n_rows < 0 || max_k < 0 || vocab <= 0 || !p)
+        return fail(RLX_ERR_INVALID, "rlx_spec_accept_async: n_rows=%d max_k=%d vocab=%d", n_rows, max_k,
+                    vocab);
+    if (n_rows == 0) return RLX_OK;
+    if (!target_logits || !n_draft || !uniforms || !n_accepted || !next_token ||
+        (max_k > 0 && (!draft_logits || !draft_tokens)))
+        return fail(RLX_ERR_INVALID, "rlx_spec_accept_async: null pointer");
+    SpecArgs a{};
+    a.d_logits = draft_logits;
+    a.t_logits = target_logits;
+    a.d_tok = draft_tokens;
+    a.n_draft = n_draft;
+    a.max_k = max_k;
+    a.V = vocab;
+    a.u = uniforms;
+    a.temperature = p->temperature;
+    a.top_k = p->top_k;
+    a.top_p = p->top_p;
+    a.min_p = p->min_p;
+    a.n_acc = n_accepted;
+    a.next = next_token;
+    hipEvent_t e0, e1;
+    int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
+    if (rc) return rc;
+    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
+    HIP_TRY(launch_spec_accept(c->stream, a, n_rows));
+    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    return RLX_OK;
+}
+
 int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_logits,
                         const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
                         int32_t max_k, int32_t vocab, const float *uniforms, const rlx_sampler_t *p,

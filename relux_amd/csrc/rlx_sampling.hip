@@ -900,7 +900,11 @@ __device__ __forceinline__ float spec_p(const float *row, int v, float m, bool n
 __global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
     __shared__ SampLds s;
     const int b = blockIdx.x, tid = threadIdx.x;
-    const int k = a.n_draft[b], V = a.V;
+    // draft counts and ids come from the device in rlx_spec_accept_async:
+    // the count is clamped to [0, max_k], an id outside [0, V) is rejected
+    // (rlx_spec_accept checks both on the host)
+    const int V = a.V;
+    const int k = min(max(a.n_draft[b], 0), a.max_k);
     const float *u = a.u + (int64_t)b * (a.max_k + 1);
     const float *dl = a.d_logits + (int64_t)b * a.max_k * V;
     const float *tl = a.t_logits + (int64_t)b * (a.max_k + 1) * V;
@@ -950,10 +954,12 @@ __global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
         const bool dn = ds > 0.f, tn = ts > 0.f;
         const float di = dn ? __fdiv_rn(1.f, ds) : 1.f, ti = tn ? __fdiv_rn(1.f, ts) : 1.f;
         const int tok = a.d_tok[(int64_t)b * a.max_k + i];
-        const float dP = spec_p(dr, tok, dm, dn, di), tP = spec_p(tr, tok, tm, tn, ti);
-        float acc = __fdiv_rn(tP, dP > 1e-10f ? dP : 1e-10f);
-        if (acc > 1.f) acc = 1.f;
-        if (u[i] < acc) continue;
+        if (tok >= 0 && tok < V) {
+            const float dP = spec_p(dr, tok, dm, dn, di), tP = spec_p(tr, tok, tm, tn, ti);
+            float acc = __fdiv_rn(tP, dP > 1e-10f ? dP : 1e-10f);
+            if (acc > 1.f) acc = 1.f;
+            if (u[i] < acc) continue;
+        }
         auto adj = [&](int v) {
             const float d = __fsub_rn(spec_p(tr, v, tm, tn, ti), spec_p(dr, v, dm, dn, di));
             return d < 0.f ? 0.f : d;

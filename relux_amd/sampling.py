@@ -151,6 +151,38 @@ def spec_accept(cache, draft_logits, target_logits, draft_tokens, n_draft, unifo
     return list(acc), list(nxt)
 
 
+
+def spec_accept_async(cache, draft_logits, target_logits, draft_tokens, n_draft, uniforms, sampler,
+                      n_acc=None, next_tok=None):
+    """Batched acceptPhase on device state (rlx_spec_accept_async):
+    draft_logits [B, K, V], target_logits [B, K+1, V] f32, draft_tokens
+    [B, K] int32, n_draft [B] int32, uniforms [B, K+1] f32 -- all tensors
+    on the device.  Returns (or fills) (n_acc [B], next [B]) int32 device
+    tensors; enqueued on the cache's stream without waiting."""
+    B, Kp1, V = target_logits.shape
+    K = Kp1 - 1
+    dev = target_logits.device
+    d = draft_logits.contiguous() if K > 0 else target_logits
+    t = target_logits.contiguous()
+    if n_acc is None:
+        n_acc = torch.empty(B, dtype=torch.int32, device=dev)
+    if next_tok is None:
+        next_tok = torch.empty(B, dtype=torch.int32, device=dev)
+    checks = (("draft_tokens", draft_tokens, torch.int32, B * K), ("n_draft", n_draft, torch.int32, B),
+              ("uniforms", uniforms, torch.float32, B * (K + 1)), ("n_acc", n_acc, torch.int32, B),
+              ("next_tok", next_tok, torch.int32, B))
+    for name, x, dt, n in checks:
+        if not isinstance(x, torch.Tensor) or x.device != dev or x.dtype != dt or x.numel() != n \
+                or not x.is_contiguous():
+            raise TypeError(f"{name} must be a contiguous {dt} tensor of {n} entries on the logits' device")
+    if t.dtype != torch.float32 or d.dtype != torch.float32 or not t.is_cuda:
+        raise TypeError("logits must be float32 device tensors")
+    p = sampler.params()
+    check(_lib.load().rlx_spec_accept_async(cache._h, d.data_ptr(), t.data_ptr(), draft_tokens.data_ptr(),
+                                            n_draft.data_ptr(), B, K, V, uniforms.data_ptr(), ctypes.byref(p),
+                                            n_acc.data_ptr(), next_tok.data_ptr()))
+    return n_acc, next_tok
+
 def spec_draws_used(n_acc, k):
     """Draws acceptPhase consumes: a test per draft up to the first
     rejection, then one for the resample or the final Sample."""

@@ -200,6 +200,49 @@ def test_spec_accept(gpu, handle, V):
     assert outcomes == {True, False}  # both the rejection and the all-accepted paths ran
 
 
+@pytest.mark.parametrize("V", [4096, 50000])
+def test_spec_accept_async_equals_sync(gpu, handle, V):
+    """rlx_spec_accept_async (draft ids, counts and draws on the device)
+    gives rlx_spec_accept's results on valid inputs; a count past max_k is
+    clamped and an id outside [0, V) is a rejection at its position."""
+    from relux_amd import spec_accept, spec_accept_async
+    rng = np.random.default_rng(V + 3)
+    B, K = 12, 4
+    d = rng.normal(0, 1.5, (B, K, V)).astype(np.float32)
+    t = np.concatenate([d + rng.normal(0, 0.7, (B, K, V)).astype(np.float32),
+                        rng.normal(0, 1.5, (B, 1, V)).astype(np.float32)], axis=1)
+    nd = np.array([K, K, 3, 2, 1, 0, K, K, K, 2, K, K], np.int32)
+    tok = rng.integers(0, V, (B, K)).astype(np.int32)
+    for b in range(B):  # mostly draws from the draft rows, so both outcomes occur
+        for i in range(K):
+            tok[b, i] = S.sample(d[b, i], S.SamplerParams(), float(rng.random()))
+    u = rng.random((B, K + 1), dtype=np.float32)
+    params = S.SamplerParams(temperature=0.9, top_k=30)
+    smp = make_sampler(params)
+    acc, nxt = spec_accept(handle, dev(d, gpu), dev(t, gpu), tok, nd, u, smp)
+    it = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    acc_d, nxt_d = spec_accept_async(handle, dev(d, gpu), dev(t, gpu), it(tok), it(nd), dev(u, gpu), smp)
+    assert acc_d.cpu().tolist() == list(acc) and nxt_d.cpu().tolist() == list(nxt)
+    # counts past max_k are clamped; ids outside [0, V) are rejections there
+    nd2 = nd.copy()
+    nd2[0] = K + 5
+    nd2[1] = -3
+    tok2 = tok.copy()
+    tok2[6, 0] = V
+    tok2[7, 2] = -1
+    u2 = u.copy()
+    u2[7, :2] = 0.0  # the first two drafts of row 7 are accepted
+    acc2, nxt2 = spec_accept_async(handle, dev(d, gpu), dev(t, gpu), it(tok2), it(nd2), dev(u2, gpu), smp)
+    acc2, nxt2 = acc2.cpu().tolist(), nxt2.cpu().tolist()
+    ref_acc, ref_nxt = spec_accept(handle, dev(d, gpu), dev(t, gpu), tok, np.clip(nd2, 0, K), u2, smp)
+    for b in range(B):
+        if b in (6, 7):
+            continue
+        assert (acc2[b], nxt2[b]) == (ref_acc[b], ref_nxt[b]), b
+    assert acc2[6] == 0 and 0 <= nxt2[6] < V
+    assert acc2[7] == 2 and 0 <= nxt2[7] < V
+
+
 def test_spec_accept_rejects_bad_tokens(gpu, handle):
     from relux_amd import ReluxError, spec_accept
     d = torch.zeros(1, 2, 10, device=gpu)
