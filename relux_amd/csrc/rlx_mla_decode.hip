@@ -422,19 +422,37 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     }
 
     const int pidx = R.part + wk.y;
+    // The unnormalised latent partial is stored as bf16 (the merge weighs
+    // and sums it in f32).  A lane's accumulators hold 4 channels of one
+    // query row, so stored as they are, each store instruction would write
+    // 16 pieces of 32 bytes, 1 KB apart; the wave's 128 channels x 16 rows
+    // go through LDS instead (the ring, free once every wave is past its
+    // last tile; rows padded by 16 bytes against bank conflicts) and leave
+    // as 256 contiguous bytes per query row.
+    constexpr int SP = CH + 8;  // staging row pitch, bf16
+    static_assert(NW * NQT * 16 * SP <= S * TILE, "the staging rows fit the ring");
+    __syncthreads();
+    uint16_t *stg = ring + wave * NQT * 16 * SP;
 #pragma unroll
-    for (int nt = 0; nt < NQT; nt++) {
-        const int qr = nt * 16 + col;
-        const float lt = rows4_sum(l_part[nt]);
-        // The unnormalised latent partial is stored as bf16 (the merge weighs
-        // and sums it in f32): half the bytes of the split's write burst.
-        uint16_t *po = part_o + ((int64_t)pidx * QRP + qr) * kMlaDc + wave * CH;
+    for (int nt = 0; nt < NQT; nt++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const u32x2 pk = {pack_bf16x2(acc[nt][mt][0], acc[nt][mt][1]),
                               pack_bf16x2(acc[nt][mt][2], acc[nt][mt][3])};
-            __builtin_nontemporal_store(pk, (u32x2 *)(po + mt * 16 + grp * 4));
+            *(u32x2 *)(stg + (nt * 16 + col) * SP + mt * 16 + grp * 4) = pk;
         }
+    __syncthreads();
+#pragma unroll
+    for (int nt = 0; nt < NQT; nt++) {
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int r = it * 4 + (lane >> 4), ch = (lane & 15) * 8;
+            const u32x4 v = *(const u32x4 *)(stg + (nt * 16 + r) * SP + ch);
+            __builtin_nontemporal_store(
+                v, (u32x4 *)(part_o + ((int64_t)pidx * QRP + nt * 16 + r) * kMlaDc + wave * CH + ch));
+        }
+        const int qr = nt * 16 + col;
+        const float lt = rows4_sum(l_part[nt]);
         if (wave == 0 && grp == 0) {
             float *pm = part_ml + ((int64_t)pidx * QRP + qr) * 2;
             pm[0] = m_run[nt];
