@@ -244,6 +244,21 @@ int32_t rlx_gqa_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t
                        int32_t qo_layout, float scale, int32_t mask_mode, void *out,
                        int32_t out_dtype);
 
+/* rlx_gqa_attend reading the keys and values as the reference KVCache
+ * holds them: each Append copies its [KVH, S, D] block raw into the next S
+ * rows of a [cap][KVH*D] buffer (kvcache.go:286-287, copyInto 407-423) and
+ * MHA.forwardCached reads head h at token t from flat row h*T + t
+ * (mha.go:305-310) -- for KVH > 1 a permutation of the logical rows, which
+ * this call reproduces from the sequence's append history (relux's own
+ * decode outputs; RLX_MASK_REF gives its mask rule too).  Sequences whose
+ * tokens are no longer exactly their appends' (evicted, or a rollback that
+ * cut an append in two) give RLX_ERR_STATE.  Same arguments as
+ * rlx_gqa_attend; at most 32 query rows per kv head per work-group (larger
+ * calls are tiled), no FA2 path. */
+int32_t rlx_gqa_attend_ref_image(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                 const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                                 int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                                 int32_t out_dtype);
 /* rlx_gqa_attend for decode and verify calls, allocating nothing: no
  * reference counterpart.  For callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

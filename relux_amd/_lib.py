@@ -104,6 +104,8 @@ SIGNATURES = {
     "rlx_greedy": [_vp, _vp, _i32, _i32, _i64, _pi32],
     "rlx_sample": [_vp, _vp, _i32, _i32, _i64, _psp, _pi32, _pi32, ctypes.POINTER(_f32), _pi32],
     "rlx_sample_async": [_vp, _vp, _i32, _i32, _i64, _psp, _vp, _i64, _vp, _vp, _vp],
+    "rlx_gqa_attend_ref_image": [_vp, _i32, _i32, _pi32, _pi32, _i32, _vp, _i32, _i32, _f32, _i32,
+                                 _vp, _i32],
     "rlx_spec_accept_async": [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _psp, _vp, _vp],
     "rlx_spec_accept": [_vp, _vp, _vp, _pi32, _pi32, _i32, _i32, _i32, ctypes.POINTER(_f32), _psp,
                         _pi32, _pi32],

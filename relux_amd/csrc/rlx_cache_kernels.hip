@@ -2,6 +2,8 @@
 //
 // These kernels are byte movers: HBM-bound, one pass, 16-byte accesses
 // on the contiguous side of every copy.
+#include <algorithm>
+
 #include "rlx_common.h"
 
 namespace rlx {
@@ -283,6 +285,65 @@ hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t
     if (blocks > 4096) blocks = 4096;
     kv_gather_kernel<<<dim3(blocks, n_rows), 256, 0, s>>>(kpool, vpool, table, rows, k_out, v_out,
                                                           kvh, hd, hdi, P);
+    return hipGetLastError();
+}
+
+// Thread = (sequence, kv head h, token t, 8-dim octet).  chunks[c] =
+// (first token r_c, size S_c) of each append, in order.
+__global__ void ref_image_gather_kernel(const uint16_t *__restrict__ kpool,
+                                        const uint16_t *__restrict__ vpool,
+                                        const int32_t *__restrict__ table,
+                                        const RefImgSeq *__restrict__ seqs,
+                                        const int2 *__restrict__ chunks, int kvh, int hd, int P,
+                                        uint16_t *__restrict__ dk, uint16_t *__restrict__ dv,
+                                        int32_t *__restrict__ dtable, int n_pages) {
+    const RefImgSeq q = seqs[blockIdx.y];
+    if (blockIdx.y == 0)  // the scratch table: page i is entry i
+        for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_pages;
+             i += (int64_t)gridDim.x * blockDim.x)
+            dtable[i] = (int32_t)i;
+    const int oct = hd / 8;
+    const int64_t n = (int64_t)kvh * q.len * oct;
+    for (int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gid < n;
+         gid += (int64_t)gridDim.x * blockDim.x) {
+        const int o = (int)(gid % oct);
+        const int64_t ht = gid / oct;
+        const int h = (int)(ht / q.len), t = (int)(ht - (int64_t)h * q.len);
+        // flat D-row rho = h*T + t lies in append c: r_c*KVH <= rho < (r_c + S_c)*KVH
+        const int64_t rho = (int64_t)h * q.len + t;
+        int lo = 0, hi = q.n_chunks - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((int64_t)chunks[q.chunk0 + mid].x * kvh <= rho)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        const int2 ck = chunks[q.chunk0 + lo];
+        const int64_t off = rho - (int64_t)ck.x * kvh;
+        const int hs = (int)(off / ck.y);
+        const int ts = ck.x + (int)(off - (int64_t)hs * ck.y);
+        const int sp = table[q.src_tab + ts / P], ss = ts % P;
+        const int dpg = q.dst_page0 + t / P, ds = t % P;
+        const int d0 = o * 8;
+        *(u32x4 *)(dk + ((int64_t)dpg * kvh + h) * P * hd + k_page_off(ds, d0, hd)) =
+            *(const u32x4 *)(kpool + ((int64_t)sp * kvh + hs) * P * hd + k_page_off(ss, d0, hd));
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            dv[(((int64_t)dpg * kvh + h) * hd + d0 + i) * P + ds] =
+                vpool[(((int64_t)sp * kvh + hs) * hd + d0 + i) * P + ss];
+    }
+}
+
+hipError_t launch_ref_image_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                                   const int32_t *table, const RefImgSeq *seqs, int n_seqs,
+                                   int max_len, const int2 *chunks, int kvh, int hd, int P,
+                                   uint16_t *dk, uint16_t *dv, int32_t *dtable, int n_pages) {
+    if (n_seqs <= 0) return hipSuccess;
+    const int64_t work = std::max<int64_t>((int64_t)kvh * max_len * (hd / 8), n_pages);
+    const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
+    ref_image_gather_kernel<<<dim3(blocks, n_seqs), 256, 0, s>>>(kpool, vpool, table, seqs, chunks, kvh,
+                                                                 hd, P, dk, dv, dtable, n_pages);
     return hipGetLastError();
 }
 

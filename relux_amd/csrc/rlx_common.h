@@ -274,6 +274,25 @@ hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, ui
 hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
                             const int32_t *table, const AttRow *rows, int n_rows, int max_len,
                             uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int hdi, int P);
+// The reference KVCache's byte image of a GQA sequence, gathered into
+// scratch pages of the pool's layout.  Append i of a sequence put its
+// [KVH, S_i, D] block raw into rows [r_i, r_i + S_i) of a [cap][KVH * D]
+// buffer (kvcache.go:286-287, copyInto 407-423), and attention reads head h
+// at token t from flat row h * T + t (mha.go:305-310): scratch (h, t) gets
+// the logical row (kvh', r_i + s) of the D-row at flat index h * T + t =
+// r_i * KVH + kvh' * S_i + s.
+struct RefImgSeq {
+    int32_t src_tab;    // table index of the sequence's first live page
+    int32_t len;        // T
+    int32_t chunk0;     // first of its chunks in the chunk list
+    int32_t n_chunks;
+    int32_t dst_page0;  // first scratch page (scratch pages of a sequence are consecutive)
+    int32_t pad[3];
+};
+hipError_t launch_ref_image_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
+                                   const int32_t *table, const RefImgSeq *seqs, int n_seqs,
+                                   int max_len, const int2 *chunks, int kvh, int hd, int P,
+                                   uint16_t *dk, uint16_t *dv, int32_t *dtable, int n_pages);
 hipError_t launch_mla_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, int n_rows, int max_len, uint16_t *c_out,
                              uint16_t *kr_out, int dc, int dr, int P);

@@ -70,6 +70,12 @@ struct SeqState {
     int32_t first = 0;       // first live entry of the table row
     int32_t pos_offset = 0;  // absolute position of the first live token
     int32_t pages = 0;       // live pages
+    // GQA: token counts of the appends, oldest first -- the reference
+    // KVCache lays each append's [KVH, S, D] block out raw, so its byte
+    // image follows from them.  chunks_ok is cleared by a rollback that
+    // cuts an append in two.
+    std::vector<int32_t> chunks;
+    bool chunks_ok = true;
 };
 
 struct LayerState {
@@ -423,6 +429,7 @@ int32_t plan_append(Cache *c, int layer, int n_seqs, const int32_t *seq_ids, con
             toks.push_back(AppendTok{c->entry(layer, seq, k), pos % c->P, row0, n_tok[i]});
         }
         s.len += n_tok[i];
+        if (n_tok[i] > 0) s.chunks.push_back(n_tok[i]);
         row0 += n_tok[i];
     }
     return RLX_OK;
@@ -1367,6 +1374,106 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     return RLX_OK;
 }
 
+int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                 const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                                 int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                                 int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout, mask_mode,
+                                  out_dtype);
+    if (rc) return rc;
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    LayerState &ls = c->L[layer];
+    const int G = num_heads / c->kvh;
+    const int cap = gqa_rows_cap(c);
+    if (G > cap)
+        return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", G, c->hdi, cap);
+    // The byte image of each sequence, from its appends: scratch pages of
+    // the pool's layout, one run of pages per sequence.
+    std::vector<RefImgSeq> seqs(n_seqs);
+    std::vector<int2> chunks;
+    int n_pages = 0, max_len = 0, max_nq = 1;
+    for (int i = 0; i < n_seqs; i++) {
+        const SeqState &st = ls.seqs[seq_ids[i]];
+        int64_t sum = 0;
+        for (int32_t n : st.chunks) sum += n;
+        if (!st.chunks_ok || st.pos_offset != 0 || sum != st.len)
+            return fail(RLX_ERR_STATE,
+                        "sequence %d: its tokens are no longer the appends' (evicted, or a rollback cut an "
+                        "append), so the reference byte image is undefined",
+                        seq_ids[i]);
+        if (st.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
+        RefImgSeq &r = seqs[i];
+        r = RefImgSeq{};
+        r.src_tab = (int32_t)(c->row_base(layer, seq_ids[i]) + st.first);
+        r.len = st.len;
+        r.chunk0 = (int32_t)chunks.size();
+        r.n_chunks = (int32_t)st.chunks.size();
+        r.dst_page0 = n_pages;
+        int32_t t0 = 0;
+        for (int32_t n : st.chunks) {
+            chunks.push_back(int2{t0, n});
+            t0 += n;
+        }
+        n_pages += (st.len + c->P - 1) / c->P;
+        max_len = std::max(max_len, (int)st.len);
+        max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    }
+    // Rows of the decode kernel (query tiles past cap rows per kv head), each
+    // pointing at its sequence's scratch pages.
+    const int max_qr = G * max_nq;
+    const int qtile = max_qr > cap ? cap / G : 0;
+    const int nqt = std::min(max_qr, cap) > 16 ? 2 : 1;
+    int n_rows = 0;
+    if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, nullptr, 0, &n_rows))) return rc;
+    std::vector<AttRow> rows(n_rows);
+    if ((rc = gqa_decode_rows(c, layer, n_seqs, seq_ids, n_q, qtile, rows.data(), n_rows, &n_rows)))
+        return rc;
+    for (int i = 0, r = 0; i < n_seqs; i++) {  // gqa_decode_rows' order: sequences, then query tiles
+        const int nq = n_q ? n_q[i] : 1;
+        const int step = qtile > 0 ? qtile : nq;
+        for (int q0 = 0; q0 < nq; q0 += step) rows[r++].tab = seqs[i].dst_page0;
+    }
+    std::vector<int> pre(n_rows + 1), cuts(c->cus + 2);
+    std::vector<int4> ranges(c->cus + 1);
+    int total64 = 0;
+    const int n_ranges = gqa_decode_split(c, rows.data(), n_rows, pre.data(), cuts.data(), ranges.data(),
+                                          &total64);
+    ranges.resize(n_ranges);
+    const int parts = n_rows + n_ranges;
+    if ((rc = flush_patches(c))) return rc;
+    const int QRP = 16 * nqt;
+    const size_t page_bytes = (size_t)c->kvh * c->P * c->hd * 2;
+    const size_t img_bytes = ((size_t)n_pages * page_bytes + 255) & ~(size_t)255;
+    const size_t tab_bytes = ((size_t)n_pages * 4 + 255) & ~(size_t)255;
+    const size_t po_bytes = (size_t)parts * c->kvh * QRP * c->hd * sizeof(float);
+    const size_t pm_bytes = (size_t)parts * c->kvh * QRP * 2 * sizeof(float);
+    if ((rc = ensure_ws(c, 2 * img_bytes + tab_bytes + po_bytes + pm_bytes))) return rc;
+    char *ws = (char *)c->ws;
+    uint16_t *dk = (uint16_t *)ws, *dv = (uint16_t *)(ws + img_bytes);
+    int32_t *dtable = (int32_t *)(ws + 2 * img_bytes);
+    float *po = (float *)(ws + 2 * img_bytes + tab_bytes);
+    float *pm = (float *)((char *)po + po_bytes);
+    Blob b;
+    const size_t o_s = b.add(seqs), o_c = b.add(chunks), o_r = b.add(rows), o_w = b.add(ranges);
+    void *dev;
+    if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+    HIP_TRY(launch_ref_image_gather(c->stream, ls.pool0, ls.pool1, c->d_table,
+                                    (const RefImgSeq *)((char *)dev + o_s), n_seqs, max_len,
+                                    (const int2 *)((char *)dev + o_c), c->kvh, c->hd, c->P, dk, dv, dtable,
+                                    n_pages));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
+    const float qscale = scale * 1.4426950408889634f;
+    HIP_TRY(launch_gqa_decode(c->stream, nullptr, dk, dv, dtable, (const AttRow *)((char *)dev + o_r), n_rows,
+                              (const int4 *)((char *)dev + o_w), n_ranges, q, q_dtype == RLX_BF16, qo_layout,
+                              num_heads, c->kvh, c->hd, c->hdi, c->P, total64, kGqaSnap64, -1, qscale,
+                              mask_mode, nqt, po, pm, out, out_dtype == RLX_BF16, std::min(max_qr, cap),
+                              nullptr, nullptr));
+    return RLX_OK;
+}
+
 int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                                const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
                                int32_t qo_layout, float scale, int32_t mask_mode, void *out,
@@ -1697,6 +1804,14 @@ int32_t rlx_rollback(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_
             LayerState &ls = c->L[l];
             SeqState &s = ls.seqs[seq];
             s.len -= n_tokens[i];
+            for (int n = n_tokens[i]; n > 0;) {  // drop whole appends from the end
+                if (s.chunks.empty() || s.chunks.back() > n) {
+                    s.chunks_ok = false;
+                    break;
+                }
+                n -= s.chunks.back();
+                s.chunks.pop_back();
+            }
             const int keep = (s.len + c->P - 1) / c->P;
             for (int k = s.pages - 1; k >= keep; k--) {
                 ls.free_stack.push_back(c->entry(l, seq, s.first + k));

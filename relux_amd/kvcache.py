@@ -290,6 +290,27 @@ class KVCache(_PagedCache):
                                        _dev(out, "out"), _dtype_code(out)))
         return out
 
+    def AttendRefImage(self, layer_idx, q, num_heads, seq_ids=(0,), n_q=None, layout="SHD", scale=None,
+                       mask="ref", out=None, out_dtype=torch.float32):
+        """Attend over the keys and values as the reference KVCache holds
+        them (rlx_gqa_attend_ref_image): each Append's [KVH, S, D] block laid
+        out raw (kvcache.go:286-287, 407-423) and read head-major with stride
+        totalLen (mha.go:305-310) -- relux's own decode outputs, mask rule
+        RLX_MASK_REF by default.  Raises for sequences that were evicted or
+        rolled back into the middle of an append."""
+        seq_ids = list(seq_ids)
+        if n_q is None:
+            n_q = [1] * len(seq_ids)
+        if q.numel() != sum(n_q) * num_heads * self.head_dim:
+            raise ValueError("q size does not match sum(n_q) x num_heads x head_dim")
+        if out is None:
+            out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+        check(self._lib.rlx_gqa_attend_ref_image(self._h, layer_idx, len(seq_ids), i32_array(seq_ids),
+                                                 i32_array(n_q), num_heads, _dev(q, "q"), _dtype_code(q),
+                                                 _LAYOUTS[layout], float(scale or 0.0), _MASKS[mask],
+                                                 _dev(out, "out"), _dtype_code(out)))
+        return out
+
     def AttendNoAlloc(self, layer_idx, q, num_heads, out, seq_ids=(0,), n_q=None, layout="SHD",
                       scale=None, mask="causal"):
         """Attend for decode / verify calls through rlx_gqa_attend_noalloc:

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 import oracle
+from oracle import tiny_decoder as td
 
 pytestmark = pytest.mark.gpu
 
@@ -506,6 +507,72 @@ def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
     monkeypatch.setenv("RLX_MLA_EXPAND_MB", str(budget_mb))
     grouped = c.Attend(*args, seq_ids=[0, 1], n_q=nqs).cpu()
     assert torch.equal(one, grouped)
+    c.close()
+
+
+@pytest.mark.parametrize("KVH,D,chunks,nq,mask", [
+    (4, 64, [[5, 1, 3, 7, 1, 16, 2], [9, 1, 1, 30]], 1, "ref"),
+    (2, 128, [[40, 1, 1, 1], [17, 5]], 3, "causal"),
+    (8, 16, [[20], [3, 3, 3]], 20, "ref"),   # prefill row: n_q == len on sequence 0
+])
+def test_reference_byte_image_attention(gpu, KVH, D, chunks, nq, mask):
+    """rlx_gqa_attend_ref_image reads head h at token t from the D-row at
+    flat index h*T + t of the reference KVCache buffer, whose rows each
+    Append filled with its raw [KVH, S, D] block: exact f64 attention over
+    the byte image the oracle rebuilds from the same appends."""
+    from relux_amd import KVCache, ReluxError
+    rng = np.random.default_rng(KVH * 100 + D + nq)
+    H = 2 * KVH
+    S = len(chunks)
+    lens = [sum(ch) for ch in chunks]
+    c = KVCache(num_layers=1, max_len=max(lens) + 16, num_kv_heads=KVH, head_dim=D, page_tokens=16,
+                max_seqs=S, device=gpu.index)
+    logical = [[np.zeros((KVH, 0, D), np.float32)] * 2 for _ in range(S)]
+    for step in range(max(len(ch) for ch in chunks)):
+        ids = [i for i in range(S) if step < len(chunks[i])]
+        n = [chunks[i][step] for i in ids]
+        k = rng.standard_normal((sum(n), KVH, D), dtype=np.float32)
+        v = rng.standard_normal((sum(n), KVH, D), dtype=np.float32)
+        c.Append(0, torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), seq_ids=ids, n_tok=n,
+                 layout="SHD")
+        off = 0
+        for i, ni in zip(ids, n):
+            kb = oracle.round_bf16(k[off:off + ni]).transpose(1, 0, 2)
+            vb = oracle.round_bf16(v[off:off + ni]).transpose(1, 0, 2)
+            logical[i] = [np.concatenate([logical[i][0], kb], 1), np.concatenate([logical[i][1], vb], 1)]
+            off += ni
+    nqs = [min(nq, L) for L in lens]
+    q = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    out = c.AttendRefImage(0, torch.from_numpy(q).to(gpu), H, seq_ids=list(range(S)), n_q=nqs,
+                           mask=mask).cpu().numpy()
+    off = 0
+    for i, L in enumerate(lens):
+        img_k = td.ref_byte_image(logical[i][0], chunks[i], L).reshape(KVH, L, D)
+        img_v = td.ref_byte_image(logical[i][1], chunks[i], L).reshape(KVH, L, D)
+        G = H // KVH
+        qi = q[off:off + nqs[i]].transpose(1, 0, 2)
+        want = oracle.exact_attention_f64(qi, np.repeat(img_k, G, 0), np.repeat(img_v, G, 0),
+                                          _limits(mask, nqs[i], L))
+        _check(out[off:off + nqs[i]].transpose(1, 0, 2), want, TOL_EXACT, f"seq {i}")
+        off += nqs[i]
+    # a rollback of whole appends keeps the image; one that cuts an append does not
+    if len(chunks[0]) < 2:
+        c.close()
+        return
+    last = chunks[0][-1]
+    c.Rollback(0, last)
+    q1 = torch.from_numpy(q[:1].copy()).to(gpu)
+    got = c.AttendRefImage(0, q1, H, seq_ids=[0], n_q=[1], mask=mask).cpu().numpy()
+    L0 = lens[0] - last
+    img_k = td.ref_byte_image(logical[0][0][:, :L0], chunks[0][:-1], L0).reshape(KVH, L0, D)
+    img_v = td.ref_byte_image(logical[0][1][:, :L0], chunks[0][:-1], L0).reshape(KVH, L0, D)
+    want = oracle.exact_attention_f64(q[:1].transpose(1, 0, 2), np.repeat(img_k, H // KVH, 0),
+                                      np.repeat(img_v, H // KVH, 0), [L0 - 1])
+    _check(got.transpose(1, 0, 2), want, TOL_EXACT, "after rollback of the last append")
+    if chunks[0][-2] > 1:
+        c.Rollback(0, 1)
+        with pytest.raises(ReluxError):
+            c.AttendRefImage(0, q1, H, seq_ids=[0], n_q=[1])
     c.close()
 
 

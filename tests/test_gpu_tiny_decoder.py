@@ -120,3 +120,59 @@ def test_cfg1_layer0_bytes_match_fixture(run):
                                   fx["kv_bytes"][0, 0])
     np.testing.assert_array_equal(gv[0].view(torch.int16).cpu().numpy().view(np.uint16),
                                   fx["kv_bytes"][0, 1])
+
+
+class GpuRefImageCache(GpuCache):
+    """The paged GPU cache read as the reference KVCache holds its bytes
+    (rlx_gqa_attend_ref_image, the reference's mask rule)."""
+
+    def attend(self, layer, q):
+        S = q.shape[1]
+        out = self.c.AttendRefImage(layer, torch.from_numpy(np.ascontiguousarray(q)).to(self.device),
+                                    num_heads=self.H, n_q=[S], layout="HSD", mask="ref")
+        return out.cpu().numpy()
+
+
+def test_cfg1_reference_byte_image_on_gpu(gpu):
+    """KVH = 2: relux's own decode reads its cache rows scrambled (each
+    Append's [KVH, S, D] block copied raw, rows read head-major with stride
+    totalLen).  The device's ref-image attention reproduces the oracle
+    model over the reference KVCache (RefCache): logits within tolerance,
+    greedy tokens equal where the oracle's top-2 gap allows -- and they are
+    not the corrected-semantics logits."""
+    m = td.TinyDecoder(td.CFG1, seed=0)
+    prompt = td.prompt_ids(td.CFG1)
+    toks, logits, _ = m.generate(prompt, 16, GpuRefImageCache(m.cfg, gpu))
+    ref = td.RefCache(m.cfg)
+    want = [m.forward(prompt, ref)[-1]]
+    for t in toks[len(prompt):-1]:
+        want.append(m.forward([t], ref)[-1])
+    want = np.stack(want)
+    d = np.abs(logits - want)
+    print(f"cfg1 reference byte image: logits max {d.max():.3e} mean {d.mean():.3e}")
+    assert d.max() < TOL_MAX and d.mean() < TOL_MEAN
+    for i in range(16):
+        top2 = np.sort(want[i])[-2:]
+        if top2[1] - top2[0] > 2 * d[i].max():
+            assert toks[len(prompt) + i] == int(np.argmax(want[i])), i
+    logical = td.LogicalCache(m.cfg)
+    lw = [m.forward(prompt, logical)[-1]]
+    for t in toks[len(prompt):-1]:
+        lw.append(m.forward([t], logical)[-1])
+    assert np.abs(np.stack(lw)[1:] - want[1:]).max() > 1e-2  # the decode rows differ
+    # the committed reference-semantics generation (tests/golden/make_fixtures.py)
+    import os
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "cfg1_tiny_decoder.npz"))
+    assert fx["prompt"].tolist() == prompt
+    fd = np.abs(logits - fx["logits_ref"])
+    assert fd.max() < TOL_MAX and fd.mean() < TOL_MEAN
+    # free-running tokens agree step by step until a step the logit
+    # difference cannot decide (the runs may part there)
+    top2 = np.sort(fx["logits_ref"], axis=1)[:, -2:]
+    agreed = 0
+    for i in range(16):
+        if top2[i, 1] - top2[i, 0] <= 2 * fd[i].max():
+            break
+        assert toks[len(prompt) + i] == int(fx["tokens_ref"][len(prompt) + i]), i
+        agreed += 1
+    print(f"cfg1 reference byte image: {agreed} of 16 tokens checked against the fixture")
