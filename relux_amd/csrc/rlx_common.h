@@ -395,7 +395,7 @@ __device__ __forceinline__ void ring_barrier() {
 constexpr int kPrefillRows = 256;
 
 struct PrefillArgs {
-    const uint16_t *kpool;  // paged: K row pages; dense: latent pool (rope keys)
+    const uint16_t *kpool;  // paged: K pages (k-step-major 16-token blocks); dense: latent pool (rope keys)
     const uint16_t *vpool;  // paged: V dim-major pages
     const uint16_t *kc;     // dense: K_c [H][Tp][128] of the H heads expanded, sequence s at + part*H*128
     const uint16_t *vt;     // dense: V^T [H][128][Tp], same sequence offsets

@@ -21,7 +21,7 @@
 //   O^T[DV][16 rows] += V^T . P^T       MFMA 16x16x32 bf16, A = V^T rows (LDS)
 //
 // Sources (SRC):
-//   kSrcPaged : GQA paged cache, K row pages and dim-major V pages, DQK = DV = D.
+//   kSrcPaged : GQA paged cache, K pages (k-step-major 16-token blocks) and dim-major V pages, DQK = DV = D.
 //   kSrcDense : MLA, per sequence decompressed K_c [H][Tp][128] and
 //               V^T [H][128][Tp] (Tp = T rounded up to 128) plus the rope key
 //               k^R read from the paged latent rows; DQK = 192, DV = 128.

@@ -70,7 +70,7 @@ constexpr int kProjChunk = 8;   // k-steps of W held in registers at once per wa
 
 // Output layouts (features in packed order, each part a multiple of 16):
 //   kProjGQA: q (H heads x D, RoPE)    -> q_out [rows][H][D]
-//             k (KVH x D, RoPE)        -> K row pages
+//             k (KVH x D, RoPE)        -> K pages (k-step-major)
 //             v (KVH x D)              -> dim-major V pages
 //   kProjMLA: q_c (H x D)              -> q_out  [rows][H][D]
 //             q_r (H x d_r, RoPE)      -> q_out2 [rows][H][d_r]

@@ -79,7 +79,7 @@ struct SeqState {
 };
 
 struct LayerState {
-    uint16_t *pool0 = nullptr;  // GQA K row pages / MLA latent rows
+    uint16_t *pool0 = nullptr;  // GQA K pages (k-step-major blocks) / MLA latent rows
     uint16_t *pool1 = nullptr;  // GQA V dim-major pages
     std::vector<int32_t> table;       // [max_seqs * max_pages], -1 empty
     std::vector<int32_t> free_stack;  // back() is the next page handed out
