@@ -14,6 +14,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace rlx {
 
@@ -22,6 +23,35 @@ typedef __attribute__((ext_vector_type(4))) short sh4;
 typedef __attribute__((ext_vector_type(4))) float fl4;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4;
 typedef __attribute__((ext_vector_type(2))) unsigned int u32x2;
+
+// Timing of the dominant kernels (rlx_cache_timing): a pair of events per
+// launch, recorded just before and after it on the launch stream.  The
+// events are created with hipEventDisableSystemFence (timing_event_flags):
+// a default event's record performs a system-scope release -- an L2
+// write-back -- whose cost lands inside the measured interval and delays
+// the next launch.  The events are only read after a stream synchronize.
+// RLX_TIME_FENCE=system restores default events and RLX_TIME_FENCE=device
+// uses device-scope releases (comparison runs).
+inline unsigned timing_event_flags() {
+    static const unsigned f = [] {
+        const char *e = getenv("RLX_TIME_FENCE");
+        if (e && e[0] == 's') return (unsigned)hipEventDefault;
+        if (e && e[0] == 'd') return (unsigned)hipEventReleaseToDevice;
+        return (unsigned)hipEventDisableSystemFence;
+    }();
+    return f;
+}
+
+// Launch of a kernel that may be timed (e0 / e1 non-null).
+template <typename... P, typename... A>
+inline hipError_t launch_timed(void (*k)(P...), dim3 grid, dim3 block, hipStream_t s,
+                               hipEvent_t e0, hipEvent_t e1, A... args) {
+    if (e0) (void)hipEventRecord(e0, s);
+    k<<<grid, block, 0, s>>>(args...);
+    hipError_t e = hipGetLastError();
+    if (e1) (void)hipEventRecord(e1, s);
+    return e;
+}
 
 // dtype_convert.go:15-24: integer round-to-nearest-even, no NaN special case.
 __host__ __device__ __forceinline__ uint16_t bf16_rne(float x) {
@@ -246,10 +276,13 @@ struct SpecArgs {
     int32_t *n_acc, *next;
 };
 
-hipError_t launch_sample(hipStream_t s, const SampleArgs &a, int n_rows);
+// (e0, e1: optional timing events attached to the kernel's dispatch.)
+hipError_t launch_sample(hipStream_t s, const SampleArgs &a, int n_rows, hipEvent_t e0 = nullptr,
+                         hipEvent_t e1 = nullptr);
 hipError_t launch_greedy(hipStream_t s, const float *logits, int64_t stride, int V, int n_rows,
-                         int32_t *out);
-hipError_t launch_spec_accept(hipStream_t s, const SpecArgs &a, int n_rows);
+                         int32_t *out, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+hipError_t launch_spec_accept(hipStream_t s, const SpecArgs &a, int n_rows,
+                              hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 // ---- launchers (stream-ordered, return hipError_t of the launch) ----------
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);
@@ -436,7 +469,7 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
                        int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
-                       int P);
+                       int P, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 // Work-groups of the decode kernels one CU holds at once (occupancy).
 int mla_decode_wgs_per_cu(int nqt);

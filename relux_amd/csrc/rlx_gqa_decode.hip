@@ -539,13 +539,11 @@ static hipError_t launch_gqa_t(hipStream_t s, typename PlanSel<ARG>::T plan,
                                int ranges_off, float qscale,
                                int mask_mode, float *part_o, float *part_ml, void *out,
                                int out_bf16, int max_qr, hipEvent_t ev0, hipEvent_t ev1) {
-    if (ev0) (void)hipEventRecord(ev0, s);
-    gqa_decode_kernel<D, NQT, ARG><<<dim3(n_ranges * KVH), 256, 0, s>>>(
-        plan, kpool, vpool, table, rows, ranges, n_rows, q, q_bf16, layout, H, KVH, DQ, P, total64,
-        snap64, ranges_off, qscale, mask_mode, part_o, part_ml);
-    hipError_t e = hipGetLastError();
+    hipError_t e = launch_timed(gqa_decode_kernel<D, NQT, ARG>, dim3(n_ranges * KVH), dim3(256), s,
+                                ev0, ev1, plan, kpool, vpool, table, rows, ranges, n_rows, q, q_bf16,
+                                layout, H, KVH, DQ, P, total64, snap64, ranges_off, qscale,
+                                mask_mode, part_o, part_ml);
     if (e != hipSuccess) return e;
-    if (ev1) (void)hipEventRecord(ev1, s);
     gqa_combine_kernel<ARG><<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(
         plan, rows, part_o, part_ml, out, out_bf16, layout, H, KVH, D, DQ, 16 * NQT);
     return hipGetLastError();

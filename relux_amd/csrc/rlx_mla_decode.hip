@@ -670,9 +670,10 @@ template <int NQT, bool ARG>
 static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uint16_t *pool,
                          const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
                          int n_work, const uint16_t *qlat, int H, int P, int mask_mode,
-                         uint16_t *part_o, float *part_ml) {
-    mla_decode_kernel<NQT, ARG><<<n_work, 64 * MlaShape<NQT>::NW, 0, s>>>(
-        plan, pool, table, rows, work, n_rows, qlat, H, P, mask_mode, part_o, part_ml);
+                         uint16_t *part_o, float *part_ml, hipEvent_t ev0, hipEvent_t ev1) {
+    (void)launch_timed(mla_decode_kernel<NQT, ARG>, dim3(n_work), dim3(64 * MlaShape<NQT>::NW), s,
+                       ev0, ev1, plan, pool, table, rows, work, n_rows, qlat, H, P, mask_mode,
+                       part_o, part_ml);
 }
 
 template <int DMAX, bool ARG>
@@ -729,23 +730,21 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (ev0) (void)hipEventRecord(ev0, s);
     if (nqt != 1 && nqt != 2) return hipErrorInvalidValue;
     if (plan && nqt == 1)
         launch_mla_t<1, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                              mask_mode, part_o, part_ml);
+                              mask_mode, part_o, part_ml, ev0, ev1);
     else if (plan)
         launch_mla_t<2, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                              mask_mode, part_o, part_ml);
+                              mask_mode, part_o, part_ml, ev0, ev1);
     else if (nqt == 1)
         launch_mla_t<1, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                               mask_mode, part_o, part_ml);
+                               mask_mode, part_o, part_ml, ev0, ev1);
     else
         launch_mla_t<2, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
-                               mask_mode, part_o, part_ml);
+                               mask_mode, part_o, part_ml, ev0, ev1);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (ev1) (void)hipEventRecord(ev1, s);
     if (plan)
         launch_mla_out<true>(s, *plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc,
                              16 * nqt, out, out_bf16, cus);

@@ -431,18 +431,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, int n_work,
                           hipEvent_t ev0, hipEvent_t ev1) {
     if (n_work <= 0) return hipSuccess;
-    if (ev0) (void)hipEventRecord(ev0, s);
+    const dim3 g(n_work), b(64 * kWaves);
     if (src == kSrcPaged && hd == 128)
-        prefill_kernel<128, 128, kSrcPaged><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
-    else if (src == kSrcPaged && hd == 64)
-        prefill_kernel<64, 64, kSrcPaged><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
-    else if (src == kSrcDense && hd == 128)
-        prefill_kernel<192, 128, kSrcDense><<<n_work, 64 * kWaves, 0, s>>>(a, a.table);
-    else
-        return hipErrorInvalidValue;
-    hipError_t e = hipGetLastError();
-    if (ev1) (void)hipEventRecord(ev1, s);
-    return e;
+        return launch_timed(prefill_kernel<128, 128, kSrcPaged>, g, b, s, ev0, ev1, a, a.table);
+    if (src == kSrcPaged && hd == 64)
+        return launch_timed(prefill_kernel<64, 64, kSrcPaged>, g, b, s, ev0, ev1, a, a.table);
+    if (src == kSrcDense && hd == 128)
+        return launch_timed(prefill_kernel<192, 128, kSrcDense>, g, b, s, ev0, ev1, a, a.table);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace rlx

@@ -297,15 +297,16 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
                        int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
-                       int P) {
+                       int P, hipEvent_t e0, hipEvent_t e1) {
     if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
     // kProjOut: N = D (the output features), H and KVH unused.
     const int N = model == kProjGQA ? (H + 2 * KVH) * D
                                     : (model == kProjMLA ? H * (D + kMlaDr) + kMlaRow : D);
 #define RLX_PROJ_LAUNCH(ARGV, XB, MODELV, PLANV)                                                  \
-    qkv_project_kernel<ARGV, XB, MODELV><<<N / 16, 64 * kProjWaves, 0, s>>>(                      \
-        PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x, x_bf16, K, wp, H, KVH, D,  \
-        rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, table, P)
+    return launch_timed(qkv_project_kernel<ARGV, XB, MODELV>, dim3(N / 16), dim3(64 * kProjWaves), \
+                        s, e0, e1, PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x,  \
+                        x_bf16, K, wp, H, KVH, D, rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, \
+                        table, P)
 #define RLX_PROJ_MODEL(MODELV)                                                                    \
     if (plan && x_bf16)                                                                           \
         RLX_PROJ_LAUNCH(true, true, MODELV, *plan);                                               \

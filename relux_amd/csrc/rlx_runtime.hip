@@ -279,8 +279,8 @@ int32_t timing_events(Cache *c, hipEvent_t *e0, hipEvent_t *e1, int kind = RLX_T
     if (!(c->timing & kind)) return RLX_OK;
     if (c->tev_used == c->tev.size()) {
         hipEvent_t a, b;
-        HIP_TRY(hipEventCreate(&a));
-        HIP_TRY(hipEventCreate(&b));
+        HIP_TRY(hipEventCreateWithFlags(&a, timing_event_flags()));
+        HIP_TRY(hipEventCreateWithFlags(&b, timing_event_flags()));
         c->tev.emplace_back(a, b);
     }
     *e0 = c->tev[c->tev_used].first;
@@ -965,14 +965,12 @@ int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, i
         const int n = std::min(kProjRows, rows - r0);
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
-        if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
         HIP_TRY(launch_proj(c->stream, kProjModelOut, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, n,
                             (const char *)x + (size_t)r0 * k_in * xb, x_dtype == RLX_BF16, k_in,
                             (const uint16_t *)w_packed, 0, 0, n_out, nullptr, nullptr,
                             (char *)out + (size_t)r0 * n_out * ob,
                             residual ? (void *)((const char *)residual + (size_t)r0 * n_out * ob) : nullptr,
-                            out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0));
-        if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+                            out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0, e0, e1));
     }
     return RLX_OK;
 }
@@ -1061,15 +1059,13 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
         }
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
-        if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
         char *q2 = model == kProjModelMLA ? (char *)q_out2 + (size_t)r0 * num_heads * kMlaDr * qb : nullptr;
         HIP_TRY(launch_proj(c->stream, model, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
                             (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
                             x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed, num_heads,
                             c->kvh, head_dim, rope_cos, rope_sin,
                             (char *)q_out + (size_t)r0 * num_heads * head_dim * qb, q2,
-                            q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P));
-        if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+                            q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P, e0, e1));
     }
     return RLX_OK;
 }
@@ -2156,9 +2152,7 @@ int32_t rlx_greedy(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
     if (rc) return rc;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
-    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-    HIP_TRY(launch_greedy(c->stream, logits, row_stride, vocab, n_rows, (int32_t *)c->ws));
-    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    HIP_TRY(launch_greedy(c->stream, logits, row_stride, vocab, n_rows, (int32_t *)c->ws, e0, e1));
     HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     return RLX_OK;
@@ -2238,9 +2232,7 @@ int32_t rlx_sample(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
     a.out = (int32_t *)c->ws;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
-    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-    HIP_TRY(launch_sample(c->stream, a, n_rows));
-    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    HIP_TRY(launch_sample(c->stream, a, n_rows, e0, e1));
     HIP_TRY(hipMemcpyAsync(out_tokens, c->ws, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));
     return RLX_OK;
@@ -2294,9 +2286,7 @@ int32_t rlx_sample_async(void *h, const float *logits, int32_t n_rows, int32_t v
     hipEvent_t e0, e1;
     int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
     if (rc) return rc;
-    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-    HIP_TRY(launch_sample(c->stream, a, n_rows));
-    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    HIP_TRY(launch_sample(c->stream, a, n_rows, e0, e1));
     return RLX_OK;
 }
 
@@ -2330,9 +2320,7 @@ int32_t rlx_spec_accept_async(void *h, const float *draft_logits, const float *t
     hipEvent_t e0, e1;
     int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
     if (rc) return rc;
-    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-    HIP_TRY(launch_spec_accept(c->stream, a, n_rows));
-    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    HIP_TRY(launch_spec_accept(c->stream, a, n_rows, e0, e1));
     return RLX_OK;
 }
 
@@ -2384,9 +2372,7 @@ int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_
     a.next = (int32_t *)c->ws + n_rows;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
-    if (e0) HIP_TRY(hipEventRecord(e0, c->stream));
-    HIP_TRY(launch_spec_accept(c->stream, a, n_rows));
-    if (e1) HIP_TRY(hipEventRecord(e1, c->stream));
+    HIP_TRY(launch_spec_accept(c->stream, a, n_rows, e0, e1));
     HIP_TRY(hipMemcpyAsync(n_accepted, a.n_acc, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipMemcpyAsync(next_token, a.next, (size_t)n_rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIP_TRY(hipStreamSynchronize(c->stream));

@@ -1001,20 +1001,19 @@ __global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
     }
 }
 
-hipError_t launch_sample(hipStream_t st, const SampleArgs &a, int n_rows) {
-    sample_kernel<<<n_rows, kST, 0, st>>>(a);
-    return hipGetLastError();
+hipError_t launch_sample(hipStream_t st, const SampleArgs &a, int n_rows, hipEvent_t e0,
+                         hipEvent_t e1) {
+    return launch_timed(sample_kernel, dim3(n_rows), dim3(kST), st, e0, e1, a);
 }
 
 hipError_t launch_greedy(hipStream_t st, const float *logits, int64_t stride, int V, int n_rows,
-                         int32_t *out) {
-    greedy_kernel<<<n_rows, kST, 0, st>>>(logits, stride, V, out);
-    return hipGetLastError();
+                         int32_t *out, hipEvent_t e0, hipEvent_t e1) {
+    return launch_timed(greedy_kernel, dim3(n_rows), dim3(kST), st, e0, e1, logits, stride, V, out);
 }
 
-hipError_t launch_spec_accept(hipStream_t st, const SpecArgs &a, int n_rows) {
-    spec_accept_kernel<<<n_rows, kST, 0, st>>>(a);
-    return hipGetLastError();
+hipError_t launch_spec_accept(hipStream_t st, const SpecArgs &a, int n_rows, hipEvent_t e0,
+                              hipEvent_t e1) {
+    return launch_timed(spec_accept_kernel, dim3(n_rows), dim3(kST), st, e0, e1, a);
 }
 
 }  // namespace rlx
