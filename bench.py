@@ -197,9 +197,9 @@ def setup_mla(cfg, torch, dev, rng):
     ones = [1] * B
 
     def step(i):
+        # MLA.forwardCached's cache half (mla.go:308-377): append + attention
         layer = i % L
-        c.Append(layer, c1, kr1, seq_ids=seqs, n_tok=ones)
-        c.Attend(layer, qn, qr, w_uk, w_uv, H, D, seq_ids=seqs, out=out)
+        c.AppendAttend(layer, c1, kr1, qn, qr, w_uk, w_uv, H, D, seq_ids=seqs, n_tok=ones, out=out)
         c.Rollback(seqs, ones)
 
     Tatt = [T + 1 for T in lens]

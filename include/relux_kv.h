@@ -286,6 +286,20 @@ int32_t rlx_mla_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t
                        const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
                        const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
                        float scale, int32_t mask_mode, void *out, int32_t out_dtype);
+/* The cache half of MLA.forwardCached in one call: append the n_tok[i] >= 1
+ * new tokens' latent rows (c_src / kr_src as for rlx_mla_append), then the
+ * attention of those tokens (n_q = n_tok) as rlx_mla_attend.  Replaces
+ * mla.go:308-377 (MLACache.Append, View, decompress, attention).  Same
+ * cache contents and outputs as the two calls in sequence, bit for bit; on
+ * the decode path the append runs inside the attention's first launch (one
+ * launch fewer per step).  Every argument is checked before anything is
+ * appended. */
+int32_t rlx_mla_append_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                              const int32_t *n_tok, const void *c_src, const void *kr_src,
+                              int32_t src_dtype, int32_t num_heads, int32_t head_dim,
+                              const void *q_nope, const void *q_rope, int32_t q_dtype,
+                              const void *w_uk, const void *w_uv, float scale, int32_t mask_mode,
+                              void *out, int32_t out_dtype);
 
 /* ---- speculative rollback, eviction, compaction (no reference) -------- */
 /* Remove the last n_tokens[i] tokens of sequence seq_ids[i], in list order

@@ -92,6 +92,8 @@ SIGNATURES = {
                                _vp, _i32],
     "rlx_mla_attend": [_vp, _i32, _i32, _pi32, _pi32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _f32,
                        _i32, _vp, _i32],
+    "rlx_mla_append_attend": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32, _i32, _i32, _vp, _vp,
+                              _i32, _vp, _vp, _f32, _i32, _vp, _i32],
     "rlx_rollback": [_vp, _i32, _i32, _pi32, _pi32],
     "rlx_evict": [_vp, _i32, _i32, _pi32, _pi32],
     "rlx_compact": [_vp, _i32],

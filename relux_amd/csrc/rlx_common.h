@@ -180,6 +180,88 @@ __device__ __forceinline__ AppendTok plan_tok(const AppendTok *toks, int tok_off
         return toks[i];
     }
 }
+// ---- append bodies shared by the append kernels and fused launches -------
+// Load 8 consecutive source elements (f32 or bf16) and convert them to bf16
+// with the reference's integer RNE rule (dtype_convert.go:15-24).
+__device__ __forceinline__ void load8_bf16(const void *src, int64_t off, int src_bf16,
+                                           uint16_t (&o)[8]) {
+    if (src_bf16) {
+        u32x4 v = *(const u32x4 *)((const uint16_t *)src + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[2 * i] = (uint16_t)(v[i] & 0xFFFFu);
+            o[2 * i + 1] = (uint16_t)(v[i] >> 16);
+        }
+    } else {
+        const float4 *f = (const float4 *)((const float *)src + off);
+        float4 a = f[0], b = f[1];
+        o[0] = bf16_rne(a.x); o[1] = bf16_rne(a.y); o[2] = bf16_rne(a.z); o[3] = bf16_rne(a.w);
+        o[4] = bf16_rne(b.x); o[5] = bf16_rne(b.y); o[6] = bf16_rne(b.z); o[7] = bf16_rne(b.w);
+    }
+}
+
+// One source element as bf16 bits (f32 sources: BF16FromF32, dtype_convert.go:15-24).
+__device__ __forceinline__ uint16_t load1_bf16(const void *src, int64_t i, int src_bf16) {
+    return src_bf16 ? ((const uint16_t *)src)[i] : bf16_rne(((const float *)src)[i]);
+}
+
+// MLA append, thread gid: table patch gid (gid < n_patch), and chunk gid of
+// the n_tok x 72 chunks of 8 elements of the stored 576-element rows:
+// elements [0, 512) hold the latent c (the caller's d_c of them, then
+// zeros), [512, 576) the rope key (d_r, then zeros).  Chunks wholly inside
+// the caller's data take one 8-element load when the source row stride
+// allows it; the rest go element by element.
+template <bool ARG>
+__device__ __forceinline__ void mla_append_thread(int64_t gid, uint16_t *pool, int32_t *table,
+                                                  const Patch *patches, int n_patch,
+                                                  const AppendTok *toks, int tok_off, int n_tok,
+                                                  const void *c_src, const void *kr_src,
+                                                  int src_bf16, int dc, int dr, int P) {
+    if (gid < n_patch) {
+        const Patch pt = plan_patch<ARG>(patches, (int)gid);
+        table[pt.idx] = pt.val;
+    }
+    constexpr int chunks = kMlaRow / 8;  // 72
+    if (gid >= (int64_t)n_tok * chunks) return;
+    const int t = (int)(gid / chunks);
+    const int ch = (int)(gid - (int64_t)t * chunks);
+    const AppendTok tk = plan_tok<ARG>(toks, tok_off, t);
+    const bool lat = ch < kMlaDc / 8;
+    const void *src = lat ? c_src : kr_src;
+    const int width = lat ? dc : dr;                     // caller's elements per row
+    const int e0 = lat ? ch * 8 : (ch - kMlaDc / 8) * 8;  // first element of the chunk
+    uint16_t v[8];
+    if (e0 + 8 <= width && width % 8 == 0) {
+        load8_bf16(src, (int64_t)t * width + e0, src_bf16, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = (e0 + i < width) ? load1_bf16(src, (int64_t)t * width + e0 + i, src_bf16) : (uint16_t)0;
+    }
+    u32x4 pk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk[i] = (uint32_t)v[2 * i] | ((uint32_t)v[2 * i + 1] << 16);
+    *(u32x4 *)(pool + ((int64_t)tk.page * P + tk.slot) * kMlaRow + ch * 8) = pk;
+}
+
+// An MLA append carried by another launch (rlx_mla_append_attend: the
+// absorb launch of the attention that follows).  plan non-null: patches and
+// tokens in the kernel arguments (tokens at byte tok_off); else the device
+// arrays patches / toks.
+struct MlaAppendJob {
+    const PlanArg *plan;
+    int tok_off;
+    uint16_t *pool;
+    int32_t *table;
+    const Patch *patches;
+    int n_patch;
+    const AppendTok *toks;
+    int n_tok;
+    const void *c_src;
+    const void *kr_src;
+    int src_bf16, dc, dr, P;
+};
+
 // (row, split) of a decode work-group: from the device work list, or -- plan
 // in the arguments -- by binary search of the rows' first partial slots
 // (wave-uniform scalar loads).
@@ -482,6 +564,6 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              int dr, int total_q, int max_nq, int P, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
                              float *part_ml, void *out, int out_bf16, int cus,
-                             hipEvent_t ev0, hipEvent_t ev1);
+                             hipEvent_t ev0, hipEvent_t ev1, const MlaAppendJob *app = nullptr);
 
 }  // namespace rlx

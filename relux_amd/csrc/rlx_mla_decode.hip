@@ -20,6 +20,8 @@
 // registers).
 #include "rlx_common.h"
 
+#include <algorithm>
+
 namespace rlx {
 
 __device__ __forceinline__ int mla_key_limit(int mask_mode, int len, int nq, int qi) {
@@ -49,17 +51,15 @@ __device__ __forceinline__ void split_bf16(float x, uint16_t &hi, uint16_t &lo) 
 // pairs).  Every load is issued before the first product, so the kernel
 // costs one memory round trip.
 template <int KS>
-__global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
-                                                         const void *__restrict__ q_rope,
-                                                         int q_bf16,
-                                                         const uint16_t *__restrict__ w_uk,
-                                                         int H, int D, int dc, int dr, int total_q,
-                                                         float qscale, uint16_t *__restrict__ qlat) {
-    const int h = blockIdx.x;
+__device__ __forceinline__ void absorb_block(int h, int by, int bz, const void *__restrict__ q_nope,
+                                             const void *__restrict__ q_rope, int q_bf16,
+                                             const uint16_t *__restrict__ w_uk, int H, int D,
+                                             int dc, int dr, int total_q, float qscale,
+                                             uint16_t *__restrict__ qlat) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
-    const int c0 = blockIdx.y * 64 + wave * 16;
-    const int r0 = blockIdx.z * 16;
+    const int c0 = by * 64 + wave * 16;
+    const int r0 = bz * 16;
     const int row = min(r0 + col, total_q - 1);  // rows past the end load the last row
     const bool cv = c0 + col < dc;
     const uint16_t *wa = w_uk + (int64_t)(cv ? c0 + col : 0) * H * D + (int64_t)h * D + grp * 8;
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
         o[1] = (uint32_t)bf16_rne(acc[2] * qscale) | ((uint32_t)bf16_rne(acc[3] * qscale) << 16);
         *(u32x2 *)(qlat + ((int64_t)(r0 + col) * H + h) * kMlaRow + c0 + 4 * grp) = o;
     }
-    if (blockIdx.y == 0) {
+    if (by == 0) {
         for (int i = threadIdx.x; i < 16 * kMlaDr; i += blockDim.x) {
             const int r = i / kMlaDr, k = i - r * kMlaDr;
             if (r0 + r >= total_q) continue;
@@ -128,6 +128,42 @@ __global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict_
             qlat[((int64_t)(r0 + r) * H + h) * kMlaRow + kMlaDc + k] = bf16_rne(x * qscale);
         }
     }
+}
+
+template <int KS>
+__global__ __launch_bounds__(256) void mla_absorb_kernel(const void *__restrict__ q_nope,
+                                                         const void *__restrict__ q_rope,
+                                                         int q_bf16,
+                                                         const uint16_t *__restrict__ w_uk,
+                                                         int H, int D, int dc, int dr, int total_q,
+                                                         float qscale, uint16_t *__restrict__ qlat) {
+    absorb_block<KS>(blockIdx.x, blockIdx.y, blockIdx.z, q_nope, q_rope, q_bf16, w_uk, H, D, dc, dr,
+                     total_q, qscale, qlat);
+}
+
+// The absorb and the step's latent append in one launch
+// (rlx_mla_append_attend): blocks [0, H * 8 * nz) absorb (head fastest, then
+// the 64-channel block, then the 16-row tile), the rest run the append's
+// threads.  Neither part reads what the other writes: the attention that
+// reads both is the next launch.
+template <int KS, bool ARG>
+__global__ __launch_bounds__(256) void mla_absorb_append_kernel(
+    typename PlanSel<ARG>::T plan, const void *__restrict__ q_nope, const void *__restrict__ q_rope,
+    int q_bf16, const uint16_t *__restrict__ w_uk, int H, int D, int dc, int dr, int total_q,
+    float qscale, uint16_t *__restrict__ qlat, int nz, uint16_t *__restrict__ pool,
+    int32_t *__restrict__ table, const Patch *__restrict__ patches, int n_patch,
+    const AppendTok *__restrict__ toks, int tok_off, int n_tok, const void *__restrict__ c_src,
+    const void *__restrict__ kr_src, int src_bf16, int P) {
+    const int nb = H * (kMlaDc / 64) * nz;
+    const int b = blockIdx.x;
+    if (b < nb) {
+        const int rest = b / H;
+        absorb_block<KS>(b - rest * H, rest % (kMlaDc / 64), rest / (kMlaDc / 64), q_nope, q_rope,
+                         q_bf16, w_uk, H, D, dc, dr, total_q, qscale, qlat);
+        return;
+    }
+    mla_append_thread<ARG>((int64_t)(b - nb) * blockDim.x + threadIdx.x, pool, table, patches,
+                           n_patch, toks, tok_off, n_tok, c_src, kr_src, src_bf16, dc, dr, P);
 }
 
 // LDS tile layout: 16 token rows x 72 chunks of 16 B (576 bf16), no padding.
@@ -527,17 +563,9 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     __shared__ float olat[RPB][kMlaDc];
     __shared__ float red[G][RPB][DMAX];
     const int t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = t / OCT, o = t - g * OCT;
     const bool wt = g < G && o * 8 < D;  // thread takes part in the projection
-    // W_UV rows g * CPG + k (< d_c), dims h*D + 8 o .. + 8
-    const int cb = (g < G ? g : 0) * CPG;
-    const uint16_t *wp = w_uv + (int64_t)cb * H * D + (int64_t)h * D + (wt ? o * 8 : 0);
-    const int64_t wstride = (int64_t)H * D;
-    u32x4 w[WB];
-#pragma unroll
-    for (int k = 0; k < WB; k++)
-        w[k] = (wt && cb + k < dc) ? *(const u32x4 *)(wp + k * wstride) : u32x4{0u, 0u, 0u, 0u};
     // The block's query rows: row (sequence) of the call, query index, first
     // partial (query row qr of slot part), splits.
     int64_t b0[RPB];
@@ -555,6 +583,23 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
         ns[j] = R.nsplit;
         ob[j] = ((int64_t)q * H + h) * D;
     }
+    // Loads, in the order their values are needed (the memory counter
+    // retires them in issue order, so each wait covers only what it needs):
+    // (m, l) of split `lane` of row `wave` (waves < RPB), then the split
+    // partials, then the W_UV rows.  None is predicated: clamped addresses
+    // keep every load in bounds, so no load sits behind a branch.
+    int64_t bw = b0[0];
+    int nw = ns[0];
+#pragma unroll
+    for (int j = 1; j < RPB; j++)
+        if (wave == j) {
+            bw = b0[j];
+            nw = ns[j];
+        }
+    const float2 *ml = (const float2 *)(part_ml + bw * 2);
+    const int64_t st = QRP;  // float2 between split slots
+    float2 ml0 = make_float2(-INFINITY, 0.f);
+    if (wave < RPB) ml0 = ml[min(lane, nw - 1) * st];
     const int64_t sstride = (int64_t)QRP * kMlaDc;  // bf16 between split slots
     uint32_t v[RPB][SB];
 #pragma unroll
@@ -563,26 +608,30 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
 #pragma unroll
         for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(i, ns[j] - 1) * sstride);
     }
+    // W_UV rows cb + k (< d_c), dims h*D + 8 o .. + 8.  Rows past d_c read
+    // row d_c - 1 instead: their latent channels are zero in every cached
+    // row, so o_lat is exactly 0 there and the product adds nothing.
+    const int cb = (g < G ? g : 0) * CPG;
+    const uint16_t *wp = w_uv + (int64_t)h * D + (wt ? o * 8 : 0);
+    const int64_t wstride = (int64_t)H * D;
+    u32x4 w[WB];
+#pragma unroll
+    for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + (int64_t)min(cb + k, dc - 1) * wstride);
     // merge weights of row j by wave j: fac = 2^(m_s - M), inv_l = 1 / sum fac l
     if (wave < RPB) {
-        // (m, l) of split s0 = lane (+ 64 k): one 8-byte load each
         const int j = wave;
-        const float2 *ml = (const float2 *)(part_ml + b0[j] * 2);
-        const int64_t st = QRP;
-        float M = -INFINITY;
-        float2 ml0 = make_float2(-INFINITY, 0.f);
-        if (lane < ns[j]) ml0 = ml[lane * st];
-        M = ml0.x;
-        for (int s0 = lane + 64; s0 < ns[j]; s0 += 64) M = fmaxf(M, ml[s0 * st].x);
+        if (lane >= nw) ml0 = make_float2(-INFINITY, 0.f);
+        float M = ml0.x;
+        for (int s0 = lane + 64; s0 < nw; s0 += 64) M = fmaxf(M, ml[s0 * st].x);
 #pragma unroll
         for (int k = 32; k > 0; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
         float L = 0.f;
-        if (lane < ns[j]) {
+        if (lane < nw) {
             const float f = (ml0.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml0.x - M);
             fac[j][lane] = f;
             L = f * ml0.y;
         }
-        for (int s0 = lane + 64; s0 < ns[j]; s0 += 64) {
+        for (int s0 = lane + 64; s0 < nw; s0 += 64) {
             const float2 e = ml[s0 * st];
             const float f = (e.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(e.x - M);
             fac[j][s0] = f;
@@ -639,8 +688,7 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     for (int k = 0; k < WB; k++) fma8(w[k], cb + k);
     for (int k0 = WB; k0 < CPG; k0 += WB) {
 #pragma unroll
-        for (int k = 0; k < WB; k++)
-            w[k] = (wt && cb + k0 + k < dc) ? *(const u32x4 *)(wp + (k0 + k) * wstride) : u32x4{0u, 0u, 0u, 0u};
+        for (int k = 0; k < WB; k++) w[k] = *(const u32x4 *)(wp + (int64_t)min(cb + k0 + k, dc - 1) * wstride);
 #pragma unroll
         for (int k = 0; k < WB; k++) fma8(w[k], cb + k0 + k);
     }
@@ -716,17 +764,43 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
                              int dr, int total_q, int max_nq, int P, float qscale,
                              int mask_mode, int nqt, uint16_t *qlat, uint16_t *part_o,
                              float *part_ml, void *out, int out_bf16, int cus,
-                             hipEvent_t ev0, hipEvent_t ev1) {
+                             hipEvent_t ev0, hipEvent_t ev1, const MlaAppendJob *app) {
     if (n_work <= 0) return hipSuccess;
     if (hd > 256 || hd % 8 != 0 || dc > kMlaDc || dr > kMlaDr) return hipErrorInvalidValue;
-    const dim3 ag(H, kMlaDc / 64, (total_q + 15) / 16);
-    switch ((hd + 31) / 32) {
+    const int nz = (total_q + 15) / 16;
+    const dim3 ag(H, kMlaDc / 64, nz);
+    if (app && (app->n_tok > 0 || app->n_patch > 0)) {
+        // absorb + the step's append: one launch
+        const int64_t aw = std::max<int64_t>((int64_t)app->n_tok * (kMlaRow / 8), app->n_patch);
+        const dim3 fg((unsigned)(H * (kMlaDc / 64) * nz + (aw + 255) / 256));
+        switch ((hd + 31) / 32) {
+#define RLX_ABSORB_APP(KS)                                                                          \
+    case KS:                                                                                        \
+        if (app->plan)                                                                              \
+            mla_absorb_append_kernel<KS, true><<<fg, 256, 0, s>>>(                                  \
+                *app->plan, q_nope, q_rope, q_bf16, w_uk, H, hd, dc, dr, total_q, qscale, qlat, nz, \
+                app->pool, app->table, app->patches, app->n_patch, app->toks, app->tok_off,         \
+                app->n_tok, app->c_src, app->kr_src, app->src_bf16, app->P);                        \
+        else                                                                                        \
+            mla_absorb_append_kernel<KS, false><<<fg, 256, 0, s>>>(                                 \
+                NoPlan{0}, q_nope, q_rope, q_bf16, w_uk, H, hd, dc, dr, total_q, qscale, qlat, nz,  \
+                app->pool, app->table, app->patches, app->n_patch, app->toks, app->tok_off,         \
+                app->n_tok, app->c_src, app->kr_src, app->src_bf16, app->P);                        \
+        break;
+            RLX_ABSORB_APP(1) RLX_ABSORB_APP(2) RLX_ABSORB_APP(3) RLX_ABSORB_APP(4)
+            RLX_ABSORB_APP(5) RLX_ABSORB_APP(6) RLX_ABSORB_APP(7) RLX_ABSORB_APP(8)
+#undef RLX_ABSORB_APP
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch ((hd + 31) / 32) {
 #define RLX_ABSORB(KS) \
     case KS: mla_absorb_kernel<KS><<<ag, 256, 0, s>>>(q_nope, q_rope, q_bf16, w_uk, H, hd, dc, dr, total_q, qscale, qlat); break;
-        RLX_ABSORB(1) RLX_ABSORB(2) RLX_ABSORB(3) RLX_ABSORB(4)
-        RLX_ABSORB(5) RLX_ABSORB(6) RLX_ABSORB(7) RLX_ABSORB(8)
+            RLX_ABSORB(1) RLX_ABSORB(2) RLX_ABSORB(3) RLX_ABSORB(4)
+            RLX_ABSORB(5) RLX_ABSORB(6) RLX_ABSORB(7) RLX_ABSORB(8)
 #undef RLX_ABSORB
-        default: return hipErrorInvalidValue;
+            default: return hipErrorInvalidValue;
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -1539,16 +1539,12 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     return RLX_OK;
 }
 
-int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                       const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
-                       const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
-                       float scale, int32_t mask_mode, void *out, int32_t out_dtype) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_attend on a GQA cache");
-    int32_t rc = check_layer(c, layer, false);
-    if (rc) return rc;
-    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+// Argument checks of an MLA attention call that change nothing (shared by
+// rlx_mla_attend and rlx_mla_append_attend, which checks before appending).
+static int32_t mla_attend_check(Cache *c, int32_t n_seqs, const int32_t *n_q, int32_t num_heads,
+                                int32_t head_dim, const void *q_nope, const void *q_rope,
+                                int32_t q_dtype, const void *w_uk, const void *w_uv,
+                                int32_t mask_mode, void *out, int32_t out_dtype) {
     if (num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
         return fail(RLX_ERR_UNSUPPORTED,
                     "num_heads=%d head_dim=%d (head_dim a multiple of 8 up to 256)", num_heads, head_dim);
@@ -1557,15 +1553,34 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
     if (n_seqs == 0) return RLX_OK;
     if (!q_nope || !q_rope || !w_uk || !w_uv || !out) return fail(RLX_ERR_INVALID, "null operand");
-    LayerState &ls = c->L[layer];
-    std::vector<int> lens(n_seqs);
     int max_nq = 0;
-    for (int i = 0; i < n_seqs; i++) {
-        lens[i] = ls.seqs[seq_ids[i]].len;
-        max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
-    }
+    for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    const bool fa2 = num_heads * max_nq > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr;
+    if (!fa2 && num_heads * max_nq > 32 && num_heads > 32)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "MLA attention with more than 32 query rows takes head_dim 128, d_c 512 and d_r 64 "
+                    "when num_heads > 32 (got %d heads, head_dim %d, d_c %d, d_r %d)",
+                    num_heads, head_dim, c->dc, c->dr);
+    return RLX_OK;
+}
+
+// MLA attention after the checks; app: an append to run first, in the
+// attention's first launch where the path allows (rlx_mla_append_attend).
+static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               const int32_t *n_q, int32_t num_heads, int32_t head_dim,
+                               const void *q_nope, const void *q_rope, int32_t q_dtype,
+                               const void *w_uk, const void *w_uv, float scale, int32_t mask_mode,
+                               void *out, int32_t out_dtype, const MlaAppendJob *app) {
+    int32_t rc = RLX_OK;
+    LayerState &ls = c->L[layer];
+    int max_nq = 0;
+    for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     const int max_qr = num_heads * max_nq;
     if (max_qr > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr) {
+        if (app)
+            HIP_TRY(launch_mla_append(c->stream, app->plan, app->tok_off, app->pool, app->table,
+                                      app->patches, app->n_patch, app->toks, app->n_tok, app->c_src,
+                                      app->kr_src, app->src_bf16, app->dc, app->dr, app->P));
         // Chunked prefill: expand the latents into per-head K_c / V^T, then
         // FA2 tiles of kPrefillRows query tokens per head.
         std::vector<AttRow> rows;
@@ -1684,11 +1699,6 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     // (len - n_q + q0 + qn tokens, qn queries), which has the same key
     // limits; an unmasked query is a row of its own (len tokens, 1 query).
     const bool chunked = max_qr > 32;
-    if (chunked && num_heads > 32)
-        return fail(RLX_ERR_UNSUPPORTED,
-                    "MLA attention with more than 32 query rows takes head_dim 128, d_c 512 and d_r 64 "
-                    "when num_heads > 32 (got %d heads, head_dim %d, d_c %d, d_r %d)",
-                    num_heads, head_dim, c->dc, c->dr);
     const int qc = chunked ? 32 / num_heads : 0;
     std::vector<AttRow> rows;
     std::vector<int> rlen;
@@ -1766,8 +1776,69 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                               (const uint16_t *)w_uv, num_heads, head_dim, c->dc, c->dr, total_q,
                               row_nq, c->P, qscale, kmask, nqt, (uint16_t *)ws,
                               (uint16_t *)(ws + ql_bytes), (float *)(ws + ql_bytes + po_bytes), out,
-                              out_dtype == RLX_BF16, c->cus, e0, e1));
+                              out_dtype == RLX_BF16, c->cus, e0, e1, app));
     return RLX_OK;
+}
+
+int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
+                       const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
+                       float scale, int32_t mask_mode, void *out, int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_attend on a GQA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if ((rc = mla_attend_check(c, n_seqs, n_q, num_heads, head_dim, q_nope, q_rope, q_dtype, w_uk, w_uv,
+                               mask_mode, out, out_dtype)))
+        return rc;
+    if (n_seqs == 0) return RLX_OK;
+    return mla_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, head_dim, q_nope, q_rope, q_dtype,
+                           w_uk, w_uv, scale, mask_mode, out, out_dtype, nullptr);
+}
+
+int32_t rlx_mla_append_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                              const int32_t *n_tok, const void *c_src, const void *kr_src,
+                              int32_t src_dtype, int32_t num_heads, int32_t head_dim,
+                              const void *q_nope, const void *q_rope, int32_t q_dtype,
+                              const void *w_uk, const void *w_uv, float scale, int32_t mask_mode,
+                              void *out, int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_append_attend on a GQA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
+    for (int i = 0; i < n_seqs; i++)
+        if (!n_tok || n_tok[i] < 1)
+            return fail(RLX_ERR_INVALID, "rlx_mla_append_attend: every sequence appends at least one token");
+    if ((rc = mla_attend_check(c, n_seqs, n_tok, num_heads, head_dim, q_nope, q_rope, q_dtype, w_uk, w_uv,
+                               mask_mode, out, out_dtype)))
+        return rc;
+    if (n_seqs == 0) return RLX_OK;
+    if (!c_src || !kr_src) return fail(RLX_ERR_INVALID, "null latent source");
+    // The append (rlx_mla_append), then attention of the appended tokens.
+    std::vector<AppendTok> toks;
+    if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
+    std::vector<Patch> patches = take_pending(c);
+    PlanArg plan_arg;
+    MlaAppendJob job{};
+    if ((rc = append_plan(c, patches, toks, &plan_arg, &job.plan, &job.tok_off, &job.patches, &job.toks)))
+        return rc;
+    job.pool = c->L[layer].pool0;
+    job.table = c->d_table;
+    job.n_patch = (int)patches.size();
+    job.n_tok = (int)toks.size();
+    job.c_src = c_src;
+    job.kr_src = kr_src;
+    job.src_bf16 = src_dtype == RLX_BF16;
+    job.dc = c->dc;
+    job.dr = c->dr;
+    job.P = c->P;
+    return mla_attend_impl(c, layer, n_seqs, seq_ids, n_tok, num_heads, head_dim, q_nope, q_rope, q_dtype,
+                           w_uk, w_uv, scale, mask_mode, out, out_dtype, &job);
 }
 
 static int32_t layer_range(Cache *c, int layer, int *lo, int *hi) {

@@ -509,6 +509,40 @@ class MLACache(_PagedCache):
                                        _MASKS[mask], _dev(out, "out"), _dtype_code(out)))
         return out
 
+    def AppendAttend(self, layer_idx, new_c, new_kr, q_nope, q_rope, w_uk, w_uv, num_heads,
+                     head_dim, seq_ids=(0,), n_tok=None, scale=None, mask="causal", out=None,
+                     out_dtype=torch.float32):
+        """The cache half of MLA.forwardCached (mla.go:308-377): Append the
+        n_tok[i] new tokens' latent rows, then Attend with those tokens as the
+        queries (n_q = n_tok).  Same bytes and outputs as the two calls; on
+        the decode path the append rides in the attention's first launch."""
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [new_c.shape[-2]]
+        total = sum(n_tok)
+        if new_c.numel() != total * self.d_c or new_kr.numel() != total * self.d_r:
+            raise ValueError("latent / rope-key sizes do not match sum(n_tok)")
+        if new_c.dtype != new_kr.dtype:
+            raise TypeError("c and kr dtypes differ")
+        if q_nope.numel() != total * num_heads * head_dim or q_rope.numel() != total * num_heads * self.d_r:
+            raise ValueError("query sizes do not match sum(n_tok) x heads")
+        if w_uk.dtype != torch.bfloat16 or w_uv.dtype != torch.bfloat16:
+            raise TypeError("W_UK / W_UV must be bf16 (optim.Param.Data is bf16)")
+        if w_uk.numel() != self.d_c * num_heads * head_dim or w_uv.numel() != w_uk.numel():
+            raise ValueError("W_UK / W_UV must be [d_c, num_heads*head_dim]")
+        if q_nope.dtype != q_rope.dtype:
+            raise TypeError("q_nope and q_rope dtypes differ")
+        if out is None:
+            out = torch.empty((total, num_heads, head_dim), dtype=out_dtype, device=q_nope.device)
+        check(self._lib.rlx_mla_append_attend(
+            self._h, layer_idx, len(seq_ids), i32_array(seq_ids), i32_array(n_tok), _dev(new_c, "c"),
+            _dev(new_kr, "kr"), _dtype_code(new_c), num_heads, head_dim, _dev(q_nope, "q_nope"),
+            _dev(q_rope, "q_rope"), _dtype_code(q_nope), _dev(w_uk, "w_uk"), _dev(w_uv, "w_uv"),
+            float(scale or 0.0), _MASKS[mask], _dev(out, "out"), _dtype_code(out)))
+        return out
+
 
 def pack_mla_proj(w_q, w_qr, w_dkv, w_kr, num_heads, head_dim):
     """W_Q [d_model][H*D], W_QR [d_model][H*d_r], W_DKV [d_model][d_c], W_KR

@@ -510,6 +510,69 @@ def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
     c.close()
 
 
+@pytest.mark.parametrize("case", ["decode_f32", "chunked_bf16", "fa2_bf16", "staged_plans"])
+def test_mla_append_attend_equals_append_then_attend(gpu, case):
+    """rlx_mla_append_attend (the append inside the absorb launch on the
+    decode path; before the FA2 kernels on the prefill path) against
+    rlx_mla_append followed by rlx_mla_attend on a twin cache: outputs,
+    latent rows, page tables, free lists and sequence states identical, bit
+    for bit.  The twins go through a rollback that frees pages first, so the
+    fused call also carries pending page-table writes.  A call with a bad
+    argument appends nothing."""
+    from relux_amd import MLACache
+    rng = np.random.default_rng({"decode_f32": 1, "chunked_bf16": 2, "fa2_bf16": 3, "staged_plans": 4}[case])
+    P = 64
+    # chunked_bf16: 48 query rows per sequence at head_dim 64 take the
+    # decode kernels in causal chunks; fa2_bf16: 80 rows at head_dim 128 take
+    # the expansion + FA2 path; staged_plans: 140 sequences, so the append
+    # and the row plans no longer fit the kernel arguments.
+    H, D, ntok, B = {"decode_f32": (16, 128, 1, 6), "chunked_bf16": (4, 64, 12, 3),
+                     "fa2_bf16": (16, 128, 5, 2), "staged_plans": (8, 128, 1, 140)}[case]
+    dt = torch.float32 if case == "decode_f32" else torch.bfloat16
+    lens = [int(x) for x in rng.integers(100, 700, size=B)]
+    seqs = list(range(B))
+    caches = [MLACache(num_layers=2, max_len=max(lens) + 3 * P, page_tokens=P, max_seqs=B,
+                       device=gpu.index) for _ in range(2)]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    cc = t(rng.standard_normal((sum(lens), 512), dtype=np.float32))
+    kr = t(rng.standard_normal((sum(lens), 64), dtype=np.float32))
+    back = [int(x) for x in rng.integers(1, 90, size=B)]  # some cross a page boundary
+    for c in caches:
+        c.Append(1, cc, kr, seq_ids=seqs, n_tok=lens)
+        for i in seqs:
+            c.Rollback(i, back[i], layer=1)
+    w = [t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D))).view(np.int16)).view(torch.bfloat16)
+         for _ in range(2)]
+    rows = B * ntok
+    c1 = t(rng.standard_normal((rows, 512), dtype=np.float32)).to(dt)
+    k1 = t(rng.standard_normal((rows, 64), dtype=np.float32)).to(dt)
+    qn = t(rng.standard_normal((rows, H, D), dtype=np.float32)).to(dt)
+    qr = t(rng.standard_normal((rows, H, 64), dtype=np.float32)).to(dt)
+    n_tok = [ntok] * B
+    a, f = caches
+    a.Append(1, c1, k1, seq_ids=seqs, n_tok=n_tok)
+    want = a.Attend(1, qn, qr, w[0], w[1], H, D, seq_ids=seqs, n_q=n_tok).cpu()
+    from relux_amd import _lib
+    bad = f._lib.rlx_mla_append_attend(  # head_dim not a multiple of 8
+        f._h, 1, B, _lib.i32_array(seqs), _lib.i32_array(n_tok), c1.data_ptr(), k1.data_ptr(),
+        _lib.RLX_F32 if dt == torch.float32 else _lib.RLX_BF16, H, D - 4, qn.data_ptr(), qr.data_ptr(),
+        _lib.RLX_F32 if dt == torch.float32 else _lib.RLX_BF16, w[0].data_ptr(), w[1].data_ptr(), 0.0,
+        _lib.RLX_MASK_CAUSAL, torch.empty(rows, H, D, device=gpu).data_ptr(), _lib.RLX_F32)
+    assert bad == _lib.RLX_ERR_UNSUPPORTED
+    assert [f.TotalLen(1, i) for i in seqs] == [lens[i] - back[i] for i in seqs]
+    got = f.AppendAttend(1, c1, k1, qn, qr, w[0], w[1], H, D, seq_ids=seqs, n_tok=n_tok).cpu()
+    assert torch.equal(got, want)
+    for i in seqs[:8] + seqs[-2:]:
+        assert a.TotalLen(1, i) == f.TotalLen(1, i)
+        assert a.SeqState(1, i) == f.SeqState(1, i)
+        assert a.PageTable(1, i) == f.PageTable(1, i)
+        for x, y in zip(a.View(1, i), f.View(1, i)):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert a.FreeList(1) == f.FreeList(1)
+    for c in caches:
+        c.close()
+
+
 @pytest.mark.parametrize("KVH,D,chunks,nq,mask", [
     (4, 64, [[5, 1, 3, 7, 1, 16, 2], [9, 1, 1, 30]], 1, "ref"),
     (2, 128, [[40, 1, 1, 1], [17, 5]], 3, "causal"),
