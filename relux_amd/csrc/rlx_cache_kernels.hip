@@ -133,15 +133,18 @@ hipError_t launch_kv_append(hipStream_t s, const PlanArg *plan, int tok_off, uin
     int64_t work = (int64_t)n_tok * kvh * (hd / 8);
     if (work < n_patch) work = n_patch;
     if (work <= 0) return hipSuccess;
-    const unsigned grid = (unsigned)((work + 255) / 256);
+    // One-wave work-groups: a decode step's append (a few thousand threads,
+    // each one load and a few stores) then spreads over as many CUs as it has
+    // waves instead of sitting on a handful.
+    const unsigned grid = (unsigned)((work + 63) / 64);
     if (plan)
-        kv_append_kernel<true><<<grid, 256, 0, s>>>(*plan, kpool, vpool, table, patches, n_patch,
-                                                    toks, tok_off, n_tok, k_src, v_src, src_bf16,
-                                                    layout, kvh, hd, hdi, P);
+        kv_append_kernel<true><<<grid, 64, 0, s>>>(*plan, kpool, vpool, table, patches, n_patch,
+                                                   toks, tok_off, n_tok, k_src, v_src, src_bf16,
+                                                   layout, kvh, hd, hdi, P);
     else
-        kv_append_kernel<false><<<grid, 256, 0, s>>>(NoPlan{0}, kpool, vpool, table, patches,
-                                                     n_patch, toks, tok_off, n_tok, k_src, v_src,
-                                                     src_bf16, layout, kvh, hd, hdi, P);
+        kv_append_kernel<false><<<grid, 64, 0, s>>>(NoPlan{0}, kpool, vpool, table, patches,
+                                                    n_patch, toks, tok_off, n_tok, k_src, v_src,
+                                                    src_bf16, layout, kvh, hd, hdi, P);
     return hipGetLastError();
 }
 
