@@ -701,3 +701,46 @@ def test_spec_verify_stress_small(gpu):
             assert c.SeqState(0, i) == m.state(0, i)
             assert c.PageTable(0, i) == list(m.table[0][i])
         assert c.FreeList(0) == m.free[0]
+
+
+def test_kernel_timing_counts_and_leaves_results_unchanged(gpu):
+    """The timing events bench.py reads: one event pair per attention launch
+    (GQA decode, MLA decode, FA2 prefill), positive durations that add up,
+    and outputs bit-identical to untimed calls."""
+    from relux_amd import KVCache, MLACache
+    rng = np.random.default_rng(404)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    g = KVCache(num_layers=1, max_len=1024, num_kv_heads=2, head_dim=128, page_tokens=16, max_seqs=2,
+                device=gpu.index)
+    lens = [300, 700]
+    k = t(rng.standard_normal((sum(lens), 2, 128), dtype=np.float32))
+    g.Append(0, k, k * 0.5, seq_ids=[0, 1], n_tok=lens, layout="SHD")
+    q1 = t(rng.standard_normal((2, 8, 128), dtype=np.float32))
+    qp = t(rng.standard_normal((sum(lens), 8, 128), dtype=np.float32))
+    m = MLACache(num_layers=1, max_len=1024, page_tokens=64, max_seqs=2, device=gpu.index)
+    m.Append(0, t(rng.standard_normal((sum(lens), 512), dtype=np.float32)),
+             t(rng.standard_normal((sum(lens), 64), dtype=np.float32)), seq_ids=[0, 1], n_tok=lens)
+    w = [t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, 16 * 128))).view(np.int16)).view(torch.bfloat16)
+         for _ in range(2)]
+    mq = (t(rng.standard_normal((2, 16, 128), dtype=np.float32)), t(rng.standard_normal((2, 16, 64), dtype=np.float32)))
+
+    def calls():
+        return [g.Attend(0, q1, 8, seq_ids=[0, 1]).cpu(),
+                g.Attend(0, qp, 8, seq_ids=[0, 1], n_q=lens).cpu(),  # FA2 prefill
+                m.Attend(0, mq[0], mq[1], w[0], w[1], 16, 128, seq_ids=[0, 1]).cpu()]
+
+    plain = calls()
+    for c in (g, m):
+        c.Timing(True)
+    timed = calls()
+    (gms, gn), (mms, mn) = g.KernelTime(), m.KernelTime()
+    assert (gn, mn) == (2, 1)
+    assert 0.0 < gms < 100.0 and 0.0 < mms < 100.0
+    for a, b in zip(plain, timed):
+        assert torch.equal(a, b)
+    for c in (g, m):
+        c.Timing(False)
+    calls()
+    assert g.KernelTime() == (0.0, 0) and m.KernelTime() == (0.0, 0)
+    g.close()
+    m.close()
