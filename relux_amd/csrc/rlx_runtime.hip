@@ -582,6 +582,7 @@ int64_t mla_expand_budget() {
     return mb > 0 ? mb << 20 : (int64_t)4 << 30;
 }
 
+constexpr int kGqaLongRange = 4096;  // tokens per range that make a call "long"
 int gqa_wg_per_cu() {
     static const int v = [] {
         const char *e = getenv("RLX_GQA_WG_PER_CU");
@@ -595,8 +596,27 @@ int gqa_decode_split(const Cache *c, AttRow *rows, int n_rows, int *pre, int *cu
     pre[0] = 0;
     for (int i = 0; i < n_rows; i++) pre[i + 1] = pre[i] + (rows[i].len + 63) / 64;
     const int total64 = pre[n_rows];
-    const int n_ranges =
-        std::max(1, std::min({c->cus * gqa_wg_per_cu() / c->kvh, c->cus, total64}));
+    // Ranges per kv head: one work-group per CU, except for long calls
+    // (at least kGqaLongRange tokens per range), which take three quarters
+    // of the CUs, rounded down to a multiple of the 8 XCDs so that range i of
+    // every kv head runs on the same XCD (work-group b runs on XCD b mod 8).
+    // Measured on the 8k headline (16 x 8192, 8 kv heads; fraction of 8 TB/s
+    // by ranges per kv head): 16: 0.71, 20: 0.78, 22: 0.81, 23: 0.81,
+    // 24: 0.84, 25: 0.82, 26: 0.82, 28: 0.82, 30: 0.80, 32: 0.81, 48: 0.77,
+    // 64: 0.80; at 32k, 24: 0.88 against 0.85; config 2 (1 150 tokens per
+    // range at 32) keeps every CU: 0.685 against 0.655 at 24.
+    // RLX_GQA_RANGES overrides the count (tuning; at most the full count,
+    // which the callers' range arrays are sized for).
+    static const int ranges_override = [] {
+        const char *e = getenv("RLX_GQA_RANGES");
+        return e ? atoi(e) : 0;
+    }();
+    const int full = std::max(1, std::min(c->cus * gqa_wg_per_cu() / c->kvh, c->cus));
+    int want = full;
+    const int q3 = (full * 3 / 4) / 8 * 8;
+    if (q3 >= 8 && (int64_t)total64 * 64 >= (int64_t)q3 * kGqaLongRange) want = q3;
+    if (ranges_override > 0) want = std::min(ranges_override, full);
+    const int n_ranges = std::max(1, std::min(want, total64));
     gqa_range_cuts(pre, n_rows, n_ranges, kGqaSnap64, cuts);
     for (int k = 0; k < n_rows; k++) rows[k].part = -1;
     int r = 0;
