@@ -614,7 +614,9 @@ int gqa_decode_split(const Cache *c, AttRow *rows, int n_rows, int *pre, int *cu
     const int full = std::max(1, std::min(c->cus * gqa_wg_per_cu() / c->kvh, c->cus));
     int want = full;
     const int q3 = (full * 3 / 4) / 8 * 8;
-    if (q3 >= 8 && (int64_t)total64 * 64 >= (int64_t)q3 * kGqaLongRange) want = q3;
+    // (At least 2 ranges per XCD: with 16 kv heads or more the full count is
+    // kept.)
+    if (q3 >= 16 && (int64_t)total64 * 64 >= (int64_t)q3 * kGqaLongRange) want = q3;
     if (ranges_override > 0) want = std::min(ranges_override, full);
     const int n_ranges = std::max(1, std::min(want, total64));
     gqa_range_cuts(pre, n_rows, n_ranges, kGqaSnap64, cuts);
