@@ -108,9 +108,9 @@ def setup_gqa(cfg, torch, dev, rng):
     ones = [1] * B
 
     def step(i):
+        # MHA.forwardCached's cache half (mha.go:283-348): append + attention
         layer = i % L
-        c.Append(layer, k1, v1, seq_ids=seqs, n_tok=ones, layout="SHD")
-        c.Attend(layer, q, H, seq_ids=seqs, out=out)
+        c.AppendAttend(layer, k1, v1, q, H, seq_ids=seqs, n_tok=ones, kv_layout="SHD", out=out)
         c.Rollback(seqs, ones)
 
     Tatt = [T + 1 for T in lens]  # attention sees the appended token

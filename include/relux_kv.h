@@ -117,14 +117,18 @@ int32_t rlx_cache_kernel_time(void *cache, float *total_ms, int32_t *count);
  * NewKVCacheSized(numLayers, maxLen, numKVHeads, headDim, BFloat16)
  * (kvcache.go:66-93): capacity per sequence is max_pages_per_seq *
  * page_tokens tokens; pool_pages pages per layer are shared by up to
- * max_seqs sequences.  head_dim in {16, 32, 64, 128}; page_tokens a multiple of 16. */
+ * max_seqs sequences.  head_dim any multiple of 8 up to 256 (pages store 16,
+ * 32, 64, 96, 128 or 256 dims, the caller's zero padded); page_tokens a
+ * multiple of 16. */
 int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t page_tokens,
                       int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
 
 /* Paged bf16 MLA latent cache: per token the latent c^KV (d_c) and the
  * post-RoPE k^R (d_r).  Replaces NewMLACache(numLayers, maxLen, dC, dHR)
  * (mla_cache.go:38-59), whose f32 storage becomes bf16 here.
- * d_c = 512, d_r = 64 (DeepSeek-V2/V3 attention shapes). */
+ * d_c <= 512 and even d_r <= 64 (rows stored as 512 + 64 elements, zero
+ * padded; the reference's defaults 4*head_dim and head_dim/2 for head_dim
+ * <= 128, and the DeepSeek-V2/V3 shapes 512 / 64). */
 int32_t rlx_mla_create(int32_t layers, int32_t d_c, int32_t d_r, int32_t page_tokens,
                        int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
 
@@ -259,6 +263,19 @@ int32_t rlx_gqa_attend_ref_image(void *cache, int32_t layer, int32_t n_seqs, con
                                  const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
                                  int32_t qo_layout, float scale, int32_t mask_mode, void *out,
                                  int32_t out_dtype);
+/* The cache half of MHA.forwardCached in one call: append the n_tok[i] >= 1
+ * new tokens' K and V rows (k_src / v_src, src_dtype and src_layout as for
+ * rlx_kv_append), then the attention of those tokens (n_q = n_tok) as
+ * rlx_gqa_attend.  Replaces mha.go:283-348 (KVCache.Append, View, widen,
+ * expand, attention) with one call, the counterpart of
+ * rlx_mla_append_attend; it launches the append and then the attention, so
+ * cache contents and outputs are those of the two calls, bit for bit.
+ * Every argument is checked before anything is appended. */
+int32_t rlx_gqa_append_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                              const int32_t *n_tok, const void *k_src, const void *v_src,
+                              int32_t src_dtype, int32_t src_layout, int32_t num_heads,
+                              const void *q, int32_t q_dtype, int32_t qo_layout, float scale,
+                              int32_t mask_mode, void *out, int32_t out_dtype);
 /* rlx_gqa_attend for decode and verify calls, allocating nothing: no
  * reference counterpart.  For callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid

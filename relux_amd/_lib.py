@@ -90,6 +90,8 @@ SIGNATURES = {
     "rlx_gqa_attend": [_vp, _i32, _i32, _pi32, _pi32, _i32, _vp, _i32, _i32, _f32, _i32, _vp, _i32],
     "rlx_gqa_attend_noalloc": [_vp, _i32, _i32, _pi32, _pi32, _i32, _vp, _i32, _i32, _f32, _i32,
                                _vp, _i32],
+    "rlx_gqa_append_attend": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32, _i32, _i32, _vp, _i32,
+                              _i32, _f32, _i32, _vp, _i32],
     "rlx_mla_attend": [_vp, _i32, _i32, _pi32, _pi32, _i32, _i32, _vp, _vp, _i32, _vp, _vp, _f32,
                        _i32, _vp, _i32],
     "rlx_mla_append_attend": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32, _i32, _i32, _vp, _vp,

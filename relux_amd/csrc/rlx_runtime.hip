@@ -1252,21 +1252,12 @@ int32_t check_gqa_attend(Cache *c, int32_t layer, int32_t n_seqs, const int32_t 
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
     return RLX_OK;
 }
-}  // namespace
-
-extern "C" {
-
-int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
-                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
-                       int32_t out_dtype) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout,
-                                  mask_mode, out_dtype);
-    if (rc) return rc;
-    if (n_seqs == 0) return RLX_OK;
-    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+// GQA attention after the argument checks.
+int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                        const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                        int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                        int32_t out_dtype) {
+    int32_t rc = RLX_OK;
     const int G = num_heads / c->kvh;
     LayerState &ls = c->L[layer];
     std::vector<int> lens(n_seqs);
@@ -1390,6 +1381,63 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                               mask_mode, nqt, (float *)c->ws, (float *)((char *)c->ws + po_bytes),
                               out, out_dtype == RLX_BF16, std::min(max_qr, cap), e0, e1));
     return RLX_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                       const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                       int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                       int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout,
+                                  mask_mode, out_dtype);
+    if (rc) return rc;
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, q, q_dtype, qo_layout, scale,
+                           mask_mode, out, out_dtype);
+}
+
+int32_t rlx_gqa_append_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                              const int32_t *n_tok, const void *k_src, const void *v_src,
+                              int32_t src_dtype, int32_t src_layout, int32_t num_heads,
+                              const void *q, int32_t q_dtype, int32_t qo_layout, float scale,
+                              int32_t mask_mode, void *out, int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout,
+                                  mask_mode, out_dtype);
+    if (rc) return rc;
+    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
+    if (src_layout != RLX_LAYOUT_HSD && src_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "src_layout");
+    for (int i = 0; i < n_seqs; i++)
+        if (!n_tok || n_tok[i] < 1)
+            return fail(RLX_ERR_INVALID, "rlx_gqa_append_attend: every sequence appends at least one token");
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out || !k_src || !v_src) return fail(RLX_ERR_INVALID, "null q/out/k/v");
+    {
+        // the attention's shape limit, checked before anything is appended
+        int mx = 0;
+        for (int i = 0; i < n_seqs; i++) mx = std::max(mx, n_tok[i]);
+        const int Gq = num_heads / c->kvh, cap = gqa_rows_cap(c);
+        const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % Gq == 0;
+        if (Gq * mx > cap && !fa2 && Gq > cap)
+            return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", Gq,
+                        c->hdi, cap);
+    }
+    // Every argument is checked: the append, then the attention of the
+    // appended tokens.  (Carrying the append inside the decode launch --
+    // the wave that reads a block holding an appended token writing it
+    // first -- was measured and not adopted: the writing wave's wait for its
+    // stores cost the decode kernel 1.6-2.1 us, against the append launch's
+    // 4.4 us, and lowered the kernel's fraction of peak on every call.)
+    if ((rc = rlx_kv_append(h, layer, n_seqs, seq_ids, n_tok, k_src, v_src, src_dtype, src_layout)))
+        return rc;
+    return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_tok, num_heads, q, q_dtype, qo_layout, scale,
+                           mask_mode, out, out_dtype);
 }
 
 int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,

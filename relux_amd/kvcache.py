@@ -290,6 +290,38 @@ class KVCache(_PagedCache):
                                        _dev(out, "out"), _dtype_code(out)))
         return out
 
+    def AppendAttend(self, layer_idx, new_k, new_v, q, num_heads, seq_ids=(0,), n_tok=None,
+                     kv_layout="SHD", layout="SHD", scale=None, mask="causal", out=None,
+                     out_dtype=torch.float32):
+        """The cache half of MHA.forwardCached (mha.go:283-348): Append the
+        n_tok[i] new tokens' K/V rows (in `kv_layout`), then Attend with
+        those tokens as the queries (n_q = n_tok), in one library call.  Same
+        bytes and outputs as the two calls."""
+        if new_k.shape != new_v.shape:
+            raise _lib.ReluxPanic(_lib.RLX_ERR_INVALID,
+                                  f"KVCache.Append: K and V shape mismatch: {tuple(new_k.shape)} vs {tuple(new_v.shape)}")
+        if new_k.dtype != new_v.dtype:
+            raise TypeError("K and V dtypes differ")
+        seq_ids = list(seq_ids)
+        if n_tok is None:
+            if len(seq_ids) != 1:
+                raise ValueError("n_tok is required for several sequences")
+            n_tok = [new_k.shape[-2] if kv_layout == "HSD" else new_k.shape[-3]]
+        total = sum(n_tok)
+        if new_k.numel() != total * self.num_kv_heads * self.head_dim:
+            raise ValueError(f"K holds {new_k.numel()} elements, expected "
+                             f"{total}x{self.num_kv_heads}x{self.head_dim}")
+        if q.numel() != total * num_heads * self.head_dim:
+            raise ValueError("q size does not match sum(n_tok) x num_heads x head_dim")
+        if out is None:
+            out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+        check(self._lib.rlx_gqa_append_attend(
+            self._h, layer_idx, len(seq_ids), i32_array(seq_ids), i32_array(n_tok), _dev(new_k, "K"),
+            _dev(new_v, "V"), _dtype_code(new_k), _LAYOUTS[kv_layout], num_heads, _dev(q, "q"),
+            _dtype_code(q), _LAYOUTS[layout], float(scale or 0.0), _MASKS[mask], _dev(out, "out"),
+            _dtype_code(out)))
+        return out
+
     def AttendRefImage(self, layer_idx, q, num_heads, seq_ids=(0,), n_q=None, layout="SHD", scale=None,
                        mask="ref", out=None, out_dtype=torch.float32):
         """Attend over the keys and values as the reference KVCache holds

@@ -510,6 +510,72 @@ def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
     c.close()
 
 
+@pytest.mark.parametrize("case", ["decode_f32_shd", "decode_bf16_hsd_d64", "multi4_p32", "d80_two",
+                                  "d256", "nqt2", "pending_freed", "compacted", "big_plan", "fa2"])
+def test_gqa_append_attend_equals_append_then_attend(gpu, case):
+    """rlx_gqa_append_attend against rlx_kv_append followed by
+    rlx_gqa_attend on a twin cache: outputs, K/V bytes, page tables, free
+    lists and sequence states identical, bit for bit, over two steps -- for
+    both source layouts and dtypes, stored head dims 64-256, one and two
+    query tiles, table writes pending from a rollback or a compaction, a
+    call too large for the kernel-argument plan and the FA2 prefill path."""
+    from relux_amd import KVCache
+    cfg = {  # H, KVH, D, P, n_tok, B, src dtype, kv layout
+        "decode_f32_shd": (8, 2, 128, 16, 1, 6, torch.float32, "SHD"),
+        "decode_bf16_hsd_d64": (16, 4, 64, 16, 1, 5, torch.bfloat16, "HSD"),
+        "multi4_p32": (8, 2, 128, 32, 4, 7, torch.bfloat16, "SHD"),
+        "d80_two": (8, 2, 80, 16, 2, 4, torch.float32, "HSD"),
+        "d256": (8, 2, 256, 16, 1, 3, torch.bfloat16, "SHD"),
+        "nqt2": (16, 2, 128, 16, 4, 5, torch.bfloat16, "SHD"),
+        "pending_freed": (8, 2, 128, 16, 1, 6, torch.bfloat16, "SHD"),
+        "compacted": (8, 2, 128, 16, 1, 6, torch.bfloat16, "SHD"),
+        "big_plan": (8, 8, 64, 16, 1, 100, torch.bfloat16, "SHD"),
+        "fa2": (8, 2, 128, 16, 40, 2, torch.bfloat16, "SHD"),
+    }[case]
+    H, KVH, D, P, ntok, B, dt, kvl = cfg
+    rng = np.random.default_rng(sum(map(ord, case)))
+    lens = [int(x) for x in rng.integers(20, 400, size=B)]
+    seqs = list(range(B))
+    caches = [KVCache(num_layers=2, max_len=max(lens) + 4 * P + ntok, num_kv_heads=KVH, head_dim=D,
+                      page_tokens=P, max_seqs=B, device=gpu.index) for _ in range(2)]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    k0 = t(rng.standard_normal((sum(lens), KVH, D), dtype=np.float32))
+    v0 = t(rng.standard_normal((sum(lens), KVH, D), dtype=np.float32))
+    for c in caches:
+        c.Append(1, k0, v0, seq_ids=seqs, n_tok=lens, layout="SHD")
+        if case == "pending_freed":
+            for i in seqs:  # frees pages: their table writes stay pending
+                c.Rollback(i, P + 3, layer=1)
+        if case == "compacted":
+            for i in seqs:  # compaction rewrites live table entries
+                c.Evict(i, 1, layer=1)
+            c.Compact(layer=1)
+    rows = B * ntok
+    shape = (rows, KVH, D) if kvl == "SHD" else (rows * KVH, D)  # HSD: per sequence [KVH][n][D]
+    k1 = t(rng.standard_normal(shape, dtype=np.float32)).to(dt)
+    v1 = t(rng.standard_normal(shape, dtype=np.float32)).to(dt)
+    q = t(rng.standard_normal((rows, H, D), dtype=np.float32)).to(dt)
+    n_tok = [ntok] * B
+    a, f = caches
+    a.Append(1, k1, v1, seq_ids=seqs, n_tok=n_tok, layout=kvl)
+    want = a.Attend(1, q, H, seq_ids=seqs, n_q=n_tok).cpu()
+    got = f.AppendAttend(1, k1, v1, q, H, seq_ids=seqs, n_tok=n_tok, kv_layout=kvl).cpu()
+    assert torch.equal(got, want)
+    for i in seqs[:6] + seqs[-2:]:
+        assert a.SeqState(1, i) == f.SeqState(1, i)
+        assert a.PageTable(1, i) == f.PageTable(1, i)
+        for x, y in zip(a.View(1, i), f.View(1, i)):
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert a.FreeList(1) == f.FreeList(1)
+    # a second step reads the first one's new pages through the device table
+    a.Append(1, v1, k1, seq_ids=seqs, n_tok=n_tok, layout=kvl)
+    want = a.Attend(1, q, H, seq_ids=seqs, n_q=n_tok).cpu()
+    got = f.AppendAttend(1, v1, k1, q, H, seq_ids=seqs, n_tok=n_tok, kv_layout=kvl).cpu()
+    assert torch.equal(got, want)
+    for c in caches:
+        c.close()
+
+
 @pytest.mark.parametrize("case", ["decode_f32", "chunked_bf16", "fa2_bf16", "staged_plans"])
 def test_mla_append_attend_equals_append_then_attend(gpu, case):
     """rlx_mla_append_attend (the append inside the absorb launch on the
