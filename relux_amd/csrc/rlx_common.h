@@ -551,7 +551,7 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
                        int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
-                       int P, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+                       int P, int cus, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 
 // Work-groups of the decode kernels one CU holds at once (occupancy).
 int mla_decode_wgs_per_cu(int nqt);

@@ -82,6 +82,217 @@ constexpr int kProjGQA = 0;
 constexpr int kProjMLA = 1;
 constexpr int kProjOut = 2;
 
+// Output placement of one lane: feature n (lane col = n % 16) of the 4 rows
+// m*16 + grp*4 + i of lane group grp.  proj_place_plan and proj_place_rope
+// read what the plan and the RoPE tables hold for them (positions, append
+// slots, (cos, sin)), so a kernel can issue those loads before its products
+// and find them done at the output stage; proj_store then rotates and
+// writes.  Every lane of the
+// wave calls proj_store (a RoPE pair partner, feature n ^ 1, is one lane
+// away).  kProjOut: N = D output features, plus the residual; no placement.
+struct ProjPlace {
+    int part, nn, hw;      // output part, feature within it, RoPE head width (0: none)
+    int rot;               // bit i: row i rotates (position >= 0)
+    float c[4], s[4];      // RoPE (cos, sin) of each row
+    int page[4], slot[4];  // append slot of each row (k / v / latent parts)
+};
+
+// Plan reads of the placement (no load depends on another): part, RoPE
+// positions (pos < 0: no rotation), append slots.
+template <bool ARG, int MODEL>
+__device__ __forceinline__ void proj_place_plan(ProjPlace &o, int pos[4], int m, int n, int grp,
+                                                int rows, const AppendTok *__restrict__ toks,
+                                                const int32_t *__restrict__ pos_dev, int tok_off,
+                                                int pos_off, int H, int KVH, int D) {
+    if constexpr (MODEL != kProjOut) {
+        if constexpr (MODEL == kProjGQA) {
+            const int NQ = H * D, NK = KVH * D;
+            o.part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
+            o.nn = n - (o.part == 0 ? 0 : (o.part == 1 ? NQ : NQ + NK));
+            o.hw = o.part < 2 ? D : 0;
+        } else {
+            const int NQC = H * D, NQR = H * kMlaDr;
+            o.part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + kMlaDc ? 2 : 3));
+            o.nn = n - (o.part == 0 ? 0 : (o.part == 1 ? NQC : (o.part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
+            o.hw = (o.part == 1 || o.part == 3) ? kMlaDr : 0;
+        }
+        const bool to_q = (MODEL == kProjGQA) ? o.part == 0 : o.part < 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = min(m * 16 + grp * 4 + i, rows - 1);
+            pos[i] = -1;
+            if (o.hw)
+                pos[i] = ARG ? ((const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + pos_off))[r]
+                             : pos_dev[r];
+            o.page[i] = o.slot[i] = 0;
+            if (!to_q) {
+                const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
+                o.page[i] = tk.page;
+                o.slot[i] = tk.slot;
+            }
+        }
+    }
+}
+
+// RoPE (cos, sin) of the placement's rows at their positions.
+template <int MODEL>
+__device__ __forceinline__ void proj_place_rope(ProjPlace &o, const int pos[4],
+                                                const float *__restrict__ rcos,
+                                                const float *__restrict__ rsin) {
+    if constexpr (MODEL != kProjOut) {
+        const int dr = o.hw ? o.nn % o.hw : 0;  // dim within the rotated head
+        o.rot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o.c[i] = o.s[i] = 0.f;
+            if (pos[i] >= 0) {
+                o.rot |= 1 << i;
+                o.c[i] = rcos[(int64_t)pos[i] * (o.hw / 2) + (dr >> 1)];
+                o.s[i] = rsin[(int64_t)pos[i] * (o.hw / 2) + (dr >> 1)];
+            }
+        }
+    }
+}
+
+// Placement of an output wave's 16 rows when the plan is in the kernel
+// arguments: the positions are wave-uniform scalar loads (one per row), so
+// the RoPE (cos, sin) reads wait for those only.  n0 = the tile's first
+// feature (a part boundary is a multiple of 16, so the part is uniform).
+template <int MODEL>
+__device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, int col, int grp,
+                                                   int rows, int pos_off, int H, int KVH, int D,
+                                                   const float *__restrict__ rcos,
+                                                   const float *__restrict__ rsin) {
+    if constexpr (MODEL != kProjOut) {
+        typedef const __attribute__((address_space(4))) int32_t kint;
+        int part, nn0, hw;
+        if constexpr (MODEL == kProjGQA) {
+            const int NQ = H * D, NK = KVH * D;
+            part = n0 < NQ ? 0 : (n0 < NQ + NK ? 1 : 2);
+            nn0 = n0 - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
+            hw = part < 2 ? D : 0;
+        } else {
+            const int NQC = H * D, NQR = H * kMlaDr;
+            part = n0 < NQC ? 0 : (n0 < NQC + NQR ? 1 : (n0 < NQC + NQR + kMlaDc ? 2 : 3));
+            nn0 = n0 - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
+            hw = (part == 1 || part == 3) ? kMlaDr : 0;
+        }
+        o.part = part;
+        o.nn = nn0 + col;
+        o.hw = hw;
+        o.rot = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) o.c[i] = o.s[i] = 0.f;
+        if (hw && rcos) {  // tables given: row 0 exists, so every load is in bounds
+            int sp[16];
+            kint *kp = (kint *)(kernarg_plan() + pos_off);
+#pragma unroll
+            for (int j = 0; j < 16; j++)  // scalar: the lane's rows are picked below
+                sp[j] = __builtin_amdgcn_readfirstlane(kp[min(m * 16 + j, rows - 1)]);
+            const int dr = o.nn % hw;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int p = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
+                o.rot |= (p >= 0) << i;
+                // unconditional (no branch, so no wait at a join): row max(p, 0)
+                const int64_t t = (int64_t)max(p, 0) * (hw / 2) + (dr >> 1);
+                o.c[i] = rcos[t];
+                o.s[i] = rsin[t];
+            }
+        }
+    }
+}
+
+// Append slots of the lane's 4 rows from the kernel-argument plan (scalar
+// loads of the wave's 16 rows, the lane's picked by its group).
+__device__ __forceinline__ void proj_slots_kernarg(ProjPlace &o, int m, int grp, int rows, int tok_off) {
+    typedef const __attribute__((address_space(4))) int32_t kint;
+    kint *kt = (kint *)(kernarg_plan() + tok_off);
+    int sp[16], ss[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int r = min(m * 16 + j, rows - 1);
+        sp[j] = __builtin_amdgcn_readfirstlane(kt[r * 4]);
+        ss[j] = __builtin_amdgcn_readfirstlane(kt[r * 4 + 1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        o.page[i] = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
+        o.slot[i] = grp == 0 ? ss[i] : (grp == 1 ? ss[4 + i] : (grp == 2 ? ss[8 + i] : ss[12 + i]));
+    }
+}
+
+template <int MODEL>
+__device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int n, int grp,
+                                           int rows, int H, int KVH, int D,
+                                           void *__restrict__ q_out, void *__restrict__ q_out2,
+                                           int q_bf16, uint16_t *__restrict__ kpool,
+                                           uint16_t *__restrict__ vpool, int P) {
+    if constexpr (MODEL == kProjOut) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = m * 16 + grp * 4 + i;
+            if (r >= rows) continue;
+            const int64_t off = (int64_t)r * D + n;
+            float v = y[i];
+            if (q_out2)
+                v += q_bf16 ? bf16_f32(((const uint16_t *)q_out2)[off]) : ((const float *)q_out2)[off];
+            if (q_bf16)
+                ((uint16_t *)q_out)[off] = bf16_rne(v);
+            else
+                ((float *)q_out)[off] = v;
+        }
+        return;
+    } else {
+        const int part = o.part, nn = o.nn, hw = o.hw;
+        const int hdim = (MODEL == kProjGQA) ? D : (part == 1 ? kMlaDr : D);
+        const int head = nn / hdim, d = nn - head * hdim;
+        const int dr = hw ? nn % hw : 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = m * 16 + grp * 4 + i;  // C row of element i
+            float v = y[i];
+            const float partner = __shfl_xor(v, 1);
+            if (o.rot & (1 << i)) {
+                // RoPE: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), products rounded
+                // separately as in rope.go.
+                const float c = o.c[i], sn = o.s[i];
+                v = (dr & 1) ? __fadd_rn(__fmul_rn(v, c), __fmul_rn(partner, sn))
+                             : __fsub_rn(__fmul_rn(v, c), __fmul_rn(partner, sn));
+            }
+            if (r >= rows) continue;
+            const bool to_q = (MODEL == kProjGQA) ? part == 0 : part < 2;
+            if (to_q) {
+                void *dst = (MODEL == kProjMLA && part == 1) ? q_out2 : q_out;
+                const int64_t off = ((int64_t)r * H + head) * hdim + d;
+                if (q_bf16)
+                    ((uint16_t *)dst)[off] = bf16_rne(v);
+                else
+                    ((float *)dst)[off] = v;
+                continue;
+            }
+            if constexpr (MODEL == kProjGQA) {
+                if (part == 1)
+                    kpool[((int64_t)o.page[i] * KVH + head) * P * D + k_page_off(o.slot[i], d, D)] = bf16_rne(v);
+                else
+                    vpool[(((int64_t)o.page[i] * KVH + head) * D + d) * P + o.slot[i]] = bf16_rne(v);
+            } else {
+                kpool[((int64_t)o.page[i] * P + o.slot[i]) * kMlaRow + (part == 2 ? 0 : kMlaDc) + nn] = bf16_rne(v);
+            }
+        }
+    }
+}
+
+// Activations as MFMA A operands: bf16 pairs {hi, lo} of two f32 values
+// (lo = bf16(x - hi), zero where hi is not finite).
+__device__ __forceinline__ u32x2 proj_split2(float a, float b) {
+    const uint16_t ha = bf16_rne(a), hb = bf16_rne(b);
+    const float ra = bf16_f32(ha), rb = bf16_f32(hb);
+    const uint16_t la = (fabsf(ra) < INFINITY) ? bf16_rne(a - ra) : (uint16_t)0;
+    const uint16_t lb = (fabsf(rb) < INFINITY) ? bf16_rne(b - rb) : (uint16_t)0;
+    return u32x2{(uint32_t)ha | ((uint32_t)hb << 16), (uint32_t)la | ((uint32_t)lb << 16)};
+}
+
 template <bool ARG, bool XBF16, int MODEL>
 __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
@@ -124,13 +335,6 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
             wf[j] = __builtin_nontemporal_load((const u32x4 *)(wblk + (int64_t)min(base + j, ks_hi - 1) * 512));
     };
     // Activations of row tile m: bf16 as loaded, or f32 split into hi + lo.
-    auto split2 = [](float a, float b) {  // {hi pair, lo pair}
-        const uint16_t ha = bf16_rne(a), hb = bf16_rne(b);
-        const float ra = bf16_f32(ha), rb = bf16_f32(hb);
-        const uint16_t la = (fabsf(ra) < INFINITY) ? bf16_rne(a - ra) : (uint16_t)0;
-        const uint16_t lb = (fabsf(rb) < INFINITY) ? bf16_rne(b - rb) : (uint16_t)0;
-        return u32x2{(uint32_t)ha | ((uint32_t)hb << 16), (uint32_t)la | ((uint32_t)lb << 16)};
-    };
     auto load_x = [&](u32x4 (&xf)[kProjChunk], u32x4 (&xl)[kProjChunk], int base, int m) {
         const int r = min(m * 16 + col, rows - 1);
 #pragma unroll
@@ -141,8 +345,8 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
             } else {
                 const float4 f0 = *(const float4 *)((const float *)x + off);
                 const float4 f1 = *(const float4 *)((const float *)x + off + 4);
-                const u32x2 p0 = split2(f0.x, f0.y), p1 = split2(f0.z, f0.w);
-                const u32x2 p2 = split2(f1.x, f1.y), p3 = split2(f1.z, f1.w);
+                const u32x2 p0 = proj_split2(f0.x, f0.y), p1 = proj_split2(f0.z, f0.w);
+                const u32x2 p2 = proj_split2(f1.x, f1.y), p3 = proj_split2(f1.z, f1.w);
                 xf[j] = u32x4{p0[0], p1[0], p2[0], p3[0]};
                 xl[j] = u32x4{p0[1], p1[1], p2[1], p3[1]};
             }
@@ -188,95 +392,179 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     __syncthreads();
     if (wave != 0) return;
     const int n = n0 + col;
-    if constexpr (MODEL == kProjOut) {
-        // out[r][n] = x.W (+ residual[r][n]), in q_bf16's dtype.
-        const int N = gridDim.x * 16;
-#pragma unroll
-        for (int m = 0; m < kProjMaxRows / 16; m++) {
-            if (m >= MT) break;
-            fl4 y = acc[m];
-#pragma unroll
-            for (int w = 0; w < kProjWaves - 1; w++) y += red[w][m][lane];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int r = m * 16 + grp * 4 + i;
-                if (r >= rows) continue;
-                const int64_t o = (int64_t)r * N + n;
-                float v = y[i];
-                if (q_out2)
-                    v += q_bf16 ? bf16_f32(((const uint16_t *)q_out2)[o]) : ((const float *)q_out2)[o];
-                if (q_bf16)
-                    ((uint16_t *)q_out)[o] = bf16_rne(v);
-                else
-                    ((float *)q_out)[o] = v;
-            }
-        }
-        return;
-    }
-    // part of the output this work-group's 16 features belong to (uniform),
-    // feature index within the part, RoPE head width (0: no rotation)
-    int part, nn, hw;
-    if constexpr (MODEL == kProjGQA) {
-        const int NQ = H * D, NK = KVH * D;
-        part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
-        nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
-        hw = part < 2 ? D : 0;
-    } else {
-        const int NQC = H * D, NQR = H * kMlaDr;
-        part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + kMlaDc ? 2 : 3));
-        nn = n - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
-        hw = (part == 1 || part == 3) ? kMlaDr : 0;
-    }
-    const int hdim = (MODEL == kProjGQA) ? D : (part == 1 ? kMlaDr : D);
-    const int head = nn / hdim, d = nn - head * hdim;
-    const int dr = hw ? nn % hw : 0;  // dim within the rotated head
 #pragma unroll
     for (int m = 0; m < kProjMaxRows / 16; m++) {
         if (m >= MT) break;
         fl4 y = acc[m];
 #pragma unroll
         for (int w = 0; w < kProjWaves - 1; w++) y += red[w][m][lane];
+        ProjPlace pl;
+        int pos[4];
+        proj_place_plan<ARG, MODEL>(pl, pos, m, n, grp, rows, toks, pos_dev, tok_off, pos_off, H, KVH, D);
+        proj_place_rope<MODEL>(pl, pos, rcos, rsin);
+        proj_store<MODEL>(pl, y, m, n, grp, rows, H, KVH, D, q_out, q_out2, q_bf16, kpool, vpool, P);
+    }
+}
+
+// Decode-size projection (at most 32 rows, K a multiple of 256 up to 4096):
+// the weight stream is the whole cost, so every wave issues all of its loads
+// before its first product.  Work-group = K/256 waves x TPW feature tiles of
+// 16: wave w takes k-steps [8w, 8w + 8), loads the TPW x 8 weight fragments,
+// then the activations of that range (MT row tiles, used for all TPW
+// tiles), and multiplies; the waves' sums meet in LDS and are added in wave
+// order, so the result does not depend on timing.  Each work-group reads
+// all of x from L2; TPW = 2 halves that traffic when there are more tiles
+// than one round of work-groups.
+constexpr int kSkPer = 8;        // k-steps per wave
+constexpr int kSkMaxWaves = 16;  // K <= 4096
+constexpr int kSkMaxRows = 32;
+constexpr int kSkXRow = 528;                // bytes per staged activation row (512 + pad)
+constexpr int kSkXRegion = 16 * kSkXRow;    // one wave's 16 rows x 8 k-steps
+
+template <bool ARG, bool XBF16, int MODEL, int MT, int TPW>
+__global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
+    typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
+    const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
+    int pos_off, int rows, const void *__restrict__ x, int K, const uint16_t *__restrict__ wp,
+    int NT, int H, int KVH, int D, const float *__restrict__ rcos, const float *__restrict__ rsin,
+    void *__restrict__ q_out, void *__restrict__ q_out2, int q_bf16,
+    uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool, int32_t *__restrict__ table, int P) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nwave = blockDim.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    if (blockIdx.x == 0) {
+        for (int i = tid; i < n_patch; i += blockDim.x) {
+            const Patch pt = plan_patch<ARG>(patches, i);
+            table[pt.idx] = pt.val;
+        }
+    }
+    const int KS = K / 32;
+    const int ks_lo = wave * kSkPer;  // this wave's k-steps: [ks_lo, ks_lo + 8)
+    // Output waves: (t, m) = (wave / MT, wave % MT).
+    const int et = wave / MT, em = wave - (wave / MT) * MT;
+    const int etile = min((int)blockIdx.x * TPW + et, NT - 1);
+    constexpr bool kEarly = ARG && XBF16;
+    ProjPlace pl;
+    int pos[4];
+    // Per-wave LDS region (per row tile): the activations staged in MFMA
+    // order, later the wave's sums for the merge.
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kSkMaxWaves * kSkXRegion];
+    // Activations first (L2 hits).  bf16: whole 128-byte lines, instruction
+    // (pair p, half h) = rows 8h..8h+7 of row tile m x k-steps 2p, 2p+1, each
+    // lane 16 bytes (row lane / 8, chunk lane % 8); they reach the MFMA
+    // order through LDS.  f32: the A operands directly (lane = row col,
+    // group grp), split into hi/lo once the weights are issued.
+    u32x4 xf[MT][kSkPer], xl[MT][kSkPer];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = m * 16 + grp * 4 + i;  // C row of element i
-            float v = y[i];
-            const float partner = __shfl_xor(v, 1);
-            const bool live = r < rows;
-            if (hw) {
-                // RoPE: (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), products rounded
-                // separately as in rope.go.
-                const int p = live ? (ARG ? ((const __attribute__((address_space(4))) int32_t *)(kernarg_plan() + pos_off))[r]
-                                           : pos_dev[r])
-                                   : 0;
-                if (p >= 0) {
-                    const float c = rcos[(int64_t)p * (hw / 2) + (dr >> 1)];
-                    const float s = rsin[(int64_t)p * (hw / 2) + (dr >> 1)];
-                    v = (dr & 1) ? __fadd_rn(__fmul_rn(v, c), __fmul_rn(partner, s))
-                                 : __fsub_rn(__fmul_rn(v, c), __fmul_rn(partner, s));
-                }
-            }
-            if (!live) continue;
-            const bool to_q = (MODEL == kProjGQA) ? part == 0 : part < 2;
-            if (to_q) {
-                void *dst = (MODEL == kProjMLA && part == 1) ? q_out2 : q_out;
-                const int64_t o = ((int64_t)r * H + head) * hdim + d;
-                if (q_bf16)
-                    ((uint16_t *)dst)[o] = bf16_rne(v);
-                else
-                    ((float *)dst)[o] = v;
-                continue;
-            }
-            const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
-            if constexpr (MODEL == kProjGQA) {
-                if (part == 1)
-                    kpool[((int64_t)tk.page * KVH + head) * P * D + k_page_off(tk.slot, d, D)] = bf16_rne(v);
-                else
-                    vpool[(((int64_t)tk.page * KVH + head) * D + d) * P + tk.slot] = bf16_rne(v);
+    for (int m = 0; m < MT; m++) {
+#pragma unroll
+        for (int j = 0; j < kSkPer; j++) {
+            if constexpr (XBF16) {
+                const int r = min(m * 16 + (j & 1) * 8 + (lane >> 3), rows - 1);
+                const int64_t off = (int64_t)r * K + (ks_lo + (j & ~1)) * 32 + (lane & 7) * 8;
+                xf[m][j] = *(const u32x4 *)((const uint16_t *)x + off);
             } else {
-                kpool[((int64_t)tk.page * P + tk.slot) * kMlaRow + (part == 2 ? 0 : kMlaDc) + nn] = bf16_rne(v);
+                const int r = min(m * 16 + col, rows - 1);
+                const int64_t off = (int64_t)r * K + (ks_lo + j) * 32 + grp * 8;
+                xf[m][j] = __builtin_bit_cast(u32x4, *(const float4 *)((const float *)x + off));
+                xl[m][j] = __builtin_bit_cast(u32x4, *(const float4 *)((const float *)x + off + 4));
             }
         }
     }
+    // Then every weight fragment of the work-group's tiles in this k-range.
+    u32x4 wf[TPW][kSkPer];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const int tile = min((int)blockIdx.x * TPW + t, NT - 1);
+        const uint16_t *wblk = wp + (int64_t)tile * KS * 512 + (col * 32 + grp * 8);
+#pragma unroll
+        for (int j = 0; j < kSkPer; j++)
+            wf[t][j] = __builtin_nontemporal_load((const u32x4 *)(wblk + (int64_t)(ks_lo + j) * 512));
+    }
+    // Keep every load above the products (the scheduler would otherwise
+    // interleave them to save registers, leaving a few in flight).
+    __builtin_amdgcn_sched_barrier(0);
+    // RoPE table reads of the output waves behind them: they retire with the
+    // last fragment, so the output stage waits for no further load.
+    if (kEarly && wave < TPW * MT)
+        proj_place_kernarg<MODEL>(pl, em, etile * 16, col, grp, rows, pos_off, H, KVH, D, rcos, rsin);
+    if constexpr (XBF16) {
+        // Through this wave's region: rows of 512 bytes + 16 of padding, so
+        // the 16 rows of one MFMA read fall on distinct banks.  A wave's LDS
+        // accesses run in order: no barrier between its writes and reads.
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            unsigned char *reg = lds + (wave * MT + m) * kSkXRegion;
+#pragma unroll
+            for (int j = 0; j < kSkPer; j++)
+                *(u32x4 *)(reg + ((j & 1) * 8 + (lane >> 3)) * kSkXRow + (j >> 1) * 128 + (lane & 7) * 16) = xf[m][j];
+#pragma unroll
+            for (int j = 0; j < kSkPer; j++)
+                xf[m][j] = *(const u32x4 *)(reg + col * kSkXRow + j * 64 + grp * 16);
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+#pragma unroll
+            for (int j = 0; j < kSkPer; j++) {
+                const float4 f0 = __builtin_bit_cast(float4, xf[m][j]);
+                const float4 f1 = __builtin_bit_cast(float4, xl[m][j]);
+                const u32x2 p0 = proj_split2(f0.x, f0.y), p1 = proj_split2(f0.z, f0.w);
+                const u32x2 p2 = proj_split2(f1.x, f1.y), p3 = proj_split2(f1.z, f1.w);
+                xf[m][j] = u32x4{p0[0], p1[0], p2[0], p3[0]};
+                xl[m][j] = u32x4{p0[1], p1[1], p2[1], p3[1]};
+            }
+    }
+    fl4 acc[TPW][MT];
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int m = 0; m < MT; m++) acc[t][m] = fl4{0.f, 0.f, 0.f, 0.f};
+    auto mul = [&](int t, int j) {
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+            // C[m = row][n = feature]: A = x rows, B = Wp rows.
+            acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8, xf[m][j]), __builtin_bit_cast(bf16x8, wf[t][j]), acc[t][m], 0, 0, 0);
+            if constexpr (!XBF16)
+                acc[t][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8, xl[m][j]), __builtin_bit_cast(bf16x8, wf[t][j]), acc[t][m], 0, 0, 0);
+        }
+    };
+    // K is a multiple of 256 (the launcher's condition): every wave has 8
+    // k-steps and multiplies without conditions, each product waiting only
+    // for its own fragment.
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int j = 0; j < kSkPer; j++) mul(t, j);
+    // ---- k-split merge: wave (t, m) of the first TPW*MT adds the sums ------
+    // (each wave's sums go to the start of its own region, which only it
+    // has read so far)
+    fl4 *red = (fl4 *)lds;
+    const int rstride = MT * kSkXRegion / 16;  // fl4 per wave
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+#pragma unroll
+        for (int m = 0; m < MT; m++) red[wave * rstride + (t * MT + m) * 64 + lane] = acc[t][m];
+    __syncthreads();
+    if (wave >= TPW * MT) return;
+    if ((int)blockIdx.x * TPW + et >= NT || em * 16 >= rows) return;
+    if constexpr (kEarly) {
+        if constexpr (MODEL != kProjOut) {
+            const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
+            if (!to_q) proj_slots_kernarg(pl, em, grp, rows, tok_off);
+        }
+    } else {
+        proj_place_plan<ARG, MODEL>(pl, pos, em, etile * 16 + col, grp, rows, toks, pos_dev, tok_off,
+                                    pos_off, H, KVH, D);
+        proj_place_rope<MODEL>(pl, pos, rcos, rsin);
+    }
+    fl4 y = red[wave * 64 + lane];
+    for (int w = 1; w < nwave; w++) y += red[w * rstride + wave * 64 + lane];
+    proj_store<MODEL>(pl, y, em, etile * 16 + col, grp, rows, H, KVH, D, q_out, q_out2, q_bf16, kpool,
+                      vpool, P);
 }
 
 hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
@@ -297,11 +585,52 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
                        int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
-                       int P, hipEvent_t e0, hipEvent_t e1) {
+                       int P, int cus, hipEvent_t e0, hipEvent_t e1) {
     if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
     // kProjOut: N = D (the output features), H and KVH unused.
     const int N = model == kProjGQA ? (H + 2 * KVH) * D
                                     : (model == kProjMLA ? H * (D + kMlaDr) + kMlaRow : D);
+    // Decode-size calls: proj_skinny_kernel, when its operands fit 128
+    // registers per lane (activations MT x 8 fragments, twice for f32;
+    // weights TPW x 8).  TPW = 2 when one tile per work-group would take
+    // more than one round of resident work-groups (16 waves per CU).
+    const int NT = N / 16, MT = (rows + 15) / 16;
+    const int nw = K / (32 * kSkPer);
+    static const int sk_mode = [] {
+        const char *e = getenv("RLX_PROJ_TPW");  // tuning override: 0 = no skinny kernel, 1, 2
+        return e ? atoi(e) : -1;
+    }();
+    if (sk_mode != 0 && rows <= kSkMaxRows && K % (32 * kSkPer) == 0 && nw >= 1 && nw * MT <= kSkMaxWaves &&
+        (x_bf16 || MT == 1)) {
+        int tpw = sk_mode > 0 ? sk_mode : (NT > cus * (kSkMaxWaves / nw) ? 2 : 1);
+        if (!x_bf16 || MT == 2) tpw = 1;
+        const dim3 grid((NT + tpw - 1) / tpw), block(64 * nw);
+#define RLX_SK_LAUNCH(ARGV, XB, MODELV, MTV, TPWV, PLANV)                                              \
+    return launch_timed(proj_skinny_kernel<ARGV, XB, MODELV, MTV, TPWV>, grid, block, s, e0, e1, PLANV, \
+                        patches, n_patch, toks, pos, tok_off, pos_off, rows, x, K, wp, NT, H, KVH, D,   \
+                        rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, table, P)
+#define RLX_SK_SHAPE(ARGV, MODELV, PLANV)                                                              \
+    if (!x_bf16) RLX_SK_LAUNCH(ARGV, false, MODELV, 1, 1, PLANV);                                      \
+    if (MT == 2) RLX_SK_LAUNCH(ARGV, true, MODELV, 2, 1, PLANV);                                       \
+    if (tpw == 2) RLX_SK_LAUNCH(ARGV, true, MODELV, 1, 2, PLANV);                                      \
+    RLX_SK_LAUNCH(ARGV, true, MODELV, 1, 1, PLANV);
+#define RLX_SK_MODEL(MODELV)                 \
+    if (plan) {                              \
+        RLX_SK_SHAPE(true, MODELV, *plan)    \
+    } else {                                 \
+        RLX_SK_SHAPE(false, MODELV, NoPlan{0}) \
+    }
+        if (model == kProjGQA) {
+            RLX_SK_MODEL(kProjGQA)
+        } else if (model == kProjMLA) {
+            RLX_SK_MODEL(kProjMLA)
+        } else {
+            RLX_SK_MODEL(kProjOut)
+        }
+#undef RLX_SK_MODEL
+#undef RLX_SK_SHAPE
+#undef RLX_SK_LAUNCH
+    }
 #define RLX_PROJ_LAUNCH(ARGV, XB, MODELV, PLANV)                                                  \
     return launch_timed(qkv_project_kernel<ARGV, XB, MODELV>, dim3(N / 16), dim3(64 * kProjWaves), \
                         s, e0, e1, PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x,  \

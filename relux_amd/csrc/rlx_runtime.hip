@@ -992,7 +992,7 @@ int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, i
                             (const uint16_t *)w_packed, 0, 0, n_out, nullptr, nullptr,
                             (char *)out + (size_t)r0 * n_out * ob,
                             residual ? (void *)((const char *)residual + (size_t)r0 * n_out * ob) : nullptr,
-                            out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0, e0, e1));
+                            out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0, c->cus, e0, e1));
     }
     return RLX_OK;
 }
@@ -1087,7 +1087,7 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
                             x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed, num_heads,
                             c->kvh, head_dim, rope_cos, rope_sin,
                             (char *)q_out + (size_t)r0 * num_heads * head_dim * qb, q2,
-                            q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P, e0, e1));
+                            q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P, c->cus, e0, e1));
     }
     return RLX_OK;
 }
