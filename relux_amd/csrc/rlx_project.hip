@@ -203,18 +203,20 @@ __device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, 
     }
 }
 
-// Append slots of the lane's 4 rows from the kernel-argument plan (scalar
-// loads of the wave's 16 rows, the lane's picked by its group).
-__device__ __forceinline__ void proj_slots_kernarg(ProjPlace &o, int m, int grp, int rows, int tok_off) {
+// Append slots of the wave's 16 rows from the kernel-argument plan (scalar
+// loads into sp / ss), and the lane's 4 rows picked from them by its group.
+__device__ __forceinline__ void proj_slots_kernarg_load(int sp[16], int ss[16], int m, int rows,
+                                                        int tok_off) {
     typedef const __attribute__((address_space(4))) int32_t kint;
     kint *kt = (kint *)(kernarg_plan() + tok_off);
-    int sp[16], ss[16];
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const int r = min(m * 16 + j, rows - 1);
         sp[j] = __builtin_amdgcn_readfirstlane(kt[r * 4]);
         ss[j] = __builtin_amdgcn_readfirstlane(kt[r * 4 + 1]);
     }
+}
+__device__ __forceinline__ void proj_slots_pick(ProjPlace &o, const int sp[16], const int ss[16], int grp) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         o.page[i] = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
@@ -487,8 +489,14 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     __builtin_amdgcn_sched_barrier(0);
     // RoPE table reads of the output waves behind them: they retire with the
     // last fragment, so the output stage waits for no further load.
-    if (kEarly && wave < TPW * MT)
+    int sp[16], ss[16];  // append slots of the output wave's rows (scalar)
+    if (kEarly && wave < TPW * MT) {
         proj_place_kernarg<MODEL>(pl, em, etile * 16, col, grp, rows, pos_off, H, KVH, D, rcos, rsin);
+        if constexpr (MODEL != kProjOut) {
+            const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
+            if (!to_q) proj_slots_kernarg_load(sp, ss, em, rows, tok_off);
+        }
+    }
     if constexpr (XBF16) {
         // Through this wave's region: rows of 512 bytes + 16 of padding, so
         // the 16 rows of one MFMA read fall on distinct banks.  A wave's LDS
@@ -554,7 +562,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     if constexpr (kEarly) {
         if constexpr (MODEL != kProjOut) {
             const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
-            if (!to_q) proj_slots_kernarg(pl, em, grp, rows, tok_off);
+            if (!to_q) proj_slots_pick(pl, sp, ss, grp);
         }
     } else {
         proj_place_plan<ARG, MODEL>(pl, pos, em, etile * 16 + col, grp, rows, toks, pos_dev, tok_off,
