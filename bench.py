@@ -170,7 +170,7 @@ def setup_gqa_fused(cfg, torch, dev, rng):
         return c, step, B, att_bytes, step_bytes, desc, att_kname, lens
     desc["workload"] = (f"gqa_fused_step B{B} H{H} KVH{KVH} D{D} d_model{dm} P{cfg['P']} "
                         f"T{cfg['T']} (projection+RoPE+append, then decode)")
-    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel<gqa>", lens
+    return c, step, B, kernel_bytes, step_bytes, desc, "proj_skinny_kernel<gqa>", lens
 
 
 def setup_mla(cfg, torch, dev, rng):
@@ -248,7 +248,7 @@ def setup_mla_fused(cfg, torch, dev, rng):
     desc["workload"] = (f"mla_fused_step B{B} H{H} D{D} d_model{dm} P{cfg['P']} T{cfg['T']} "
                         f"(projection+RoPE+latent append, then decode)")
     desc["d_model"] = dm
-    return c, step, B, kernel_bytes, step_bytes, desc, "qkv_project_kernel<mla>", lens
+    return c, step, B, kernel_bytes, step_bytes, desc, "proj_skinny_kernel<mla>", lens
 
 
 def setup_mla_prefill(cfg, torch, dev, rng):
