@@ -601,7 +601,8 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
     // Decode-size calls: proj_skinny_kernel, when its operands fit 128
     // registers per lane (activations MT x 8 fragments, twice for f32;
     // weights TPW x 8).  TPW = 2 when one tile per work-group would take
-    // more than one round of resident work-groups (16 waves per CU).
+    // more than one round of resident work-groups (its LDS holds one
+    // work-group per CU).
     const int NT = N / 16, MT = (rows + 15) / 16;
     const int nw = K / (32 * kSkPer);
     static const int sk_mode = [] {
@@ -610,7 +611,7 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
     }();
     if (sk_mode != 0 && rows <= kSkMaxRows && K % (32 * kSkPer) == 0 && nw >= 1 && nw * MT <= kSkMaxWaves &&
         (x_bf16 || MT == 1)) {
-        int tpw = sk_mode > 0 ? sk_mode : (NT > cus * (kSkMaxWaves / nw) ? 2 : 1);
+        int tpw = sk_mode > 0 ? sk_mode : (NT > cus ? 2 : 1);
         if (!x_bf16 || MT == 2) tpw = 1;
         const dim3 grid((NT + tpw - 1) / tpw), block(64 * nw);
 #define RLX_SK_LAUNCH(ARGV, XB, MODELV, MTV, TPWV, PLANV)                                              \
