@@ -609,10 +609,12 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
         const char *e = getenv("RLX_PROJ_TPW");  // tuning override: 0 = no skinny kernel, 1, 2
         return e ? atoi(e) : -1;
     }();
-    if (sk_mode != 0 && rows <= kSkMaxRows && K % (32 * kSkPer) == 0 && nw >= 1 && nw * MT <= kSkMaxWaves &&
+    // Wave (t, m) of the work-group writes tile t's row tile m: it needs
+    // at least TPW * MT waves.
+    if (sk_mode != 0 && rows <= kSkMaxRows && K % (32 * kSkPer) == 0 && nw >= MT && nw * MT <= kSkMaxWaves &&
         (x_bf16 || MT == 1)) {
         int tpw = sk_mode > 0 ? sk_mode : (NT > cus ? 2 : 1);
-        if (!x_bf16 || MT == 2) tpw = 1;
+        if (!x_bf16 || MT == 2 || nw < 2) tpw = 1;
         const dim3 grid((NT + tpw - 1) / tpw), block(64 * nw);
 #define RLX_SK_LAUNCH(ARGV, XB, MODELV, MTV, TPWV, PLANV)                                              \
     return launch_timed(proj_skinny_kernel<ARGV, XB, MODELV, MTV, TPWV>, grid, block, s, e0, e1, PLANV, \

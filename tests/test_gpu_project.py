@@ -44,6 +44,16 @@ def _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, positions):
     # the 8k block's shapes: 16 decode rows through d_model 4096
     (4096, 32, 8, 128, [40] * 16, [1] * 16, torch.bfloat16, "offset"),
     (4096, 32, 8, 128, [40] * 16, [1] * 16, torch.float32, "offset"),
+    # decode-size kernel: 20 rows (two row tiles), d_model 2048
+    (2048, 8, 2, 128, [10] * 20, [1] * 20, torch.bfloat16, "offset"),
+    # 261 16-feature tiles (more than the CUs) at d_model 512: two tiles per
+    # work-group, the last work-group's second tile empty
+    (512, 259, 1, 16, [5, 0, 3], [1, 1, 1], torch.bfloat16, "offset"),
+    # ... and at d_model 256, whose one-wave work-groups take one tile
+    (256, 259, 1, 16, [5, 0, 3], [1, 1, 1], torch.bfloat16, "offset"),
+    # 20 rows (two row tiles) at d_model 256 (one wave per work-group): the
+    # chunked kernel
+    (256, 8, 2, 64, [3] * 20, [1] * 20, torch.bfloat16, "offset"),
 ])
 def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dtype, mode):
     from relux_amd import KVCache, pack_qkv, rope_tables
@@ -94,6 +104,43 @@ def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dt
                                        atol=1e-2, rtol=1e-2)
         off += n
     assert [c.TotalLen(0, i) for i in range(S)] == [L + n for L, n in zip(lens, ntok)]
+
+
+@pytest.mark.parametrize("x_dtype", [torch.bfloat16, torch.float32])
+def test_project_append_with_staged_plan_equals_kernel_argument_plan(gpu, x_dtype):
+    """A compaction leaves table writes pending for every moved page; the
+    next ProjectAppend carries them, and with 32 decode rows its plan no
+    longer fits the kernel arguments, so it is staged in device memory.
+    Against a twin cache that evicted the same pages without compacting
+    (plan in the kernel arguments): rotated q, every cached K/V byte and
+    the lengths identical, bit for bit."""
+    from relux_amd import KVCache, pack_qkv, rope_tables
+    rng = np.random.default_rng(11)
+    S, H, KVH, D, d_model, L = 32, 16, 4, 64, 1024, 120
+    caches = [KVCache(num_layers=1, max_len=256, num_kv_heads=KVH, head_dim=D, max_seqs=S,
+                      device=gpu.index) for _ in range(2)]
+    w = [oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, n * D)).astype(np.float32)) for n in (H, KVH, KVH)]
+    wp = pack_qkv(*[_bf16_tensor(m, gpu) for m in w], H, KVH, D)
+    rope = rope_tables(D, 10000.0, 256, gpu)
+    for i in range(S):  # interleaved fills: the pages of a sequence are scattered
+        kv = torch.from_numpy(rng.standard_normal((L, KVH, D), dtype=np.float32)).to(gpu)
+        for c in caches:
+            c.Append(0, kv, kv, seq_ids=[i], n_tok=[L], layout="SHD")
+    for c in caches:
+        c.Evict(list(range(S)), [2] * S)
+    # every sequence's table row shifts: ~8 pending writes per sequence, 256
+    # in all (2 KB of patches), past the 2 KB of kernel-argument plan
+    caches[0].Compact()
+    x = torch.from_numpy(rng.standard_normal((S, d_model), dtype=np.float32)).to(gpu).to(x_dtype)
+    qs = [c.ProjectAppend(0, x, wp, H, rope=rope, seq_ids=list(range(S)), n_tok=[1] * S).cpu()
+          for c in caches]
+    assert torch.equal(qs[0], qs[1])
+    for i in range(S):
+        assert caches[0].TotalLen(0, i) == caches[1].TotalLen(0, i)
+        k0, v0 = caches[0].View(0, i)
+        k1, v1 = caches[1].View(0, i)
+        assert torch.equal(k0.view(torch.int16), k1.view(torch.int16))
+        assert torch.equal(v0.view(torch.int16), v1.view(torch.int16))
 
 
 def test_rope_position_overflow_panics(gpu):
