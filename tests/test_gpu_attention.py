@@ -199,6 +199,27 @@ def test_gqa_balanced_ranges_many_rows(gpu, n_rows, H, KVH, nq):
         off += nq
 
 
+def test_gqa_long_call_ranges(gpu):
+    """A decode call of at least 4096 tokens per range (16 x ~6 200 tokens,
+    8 kv heads: 99k tokens) takes three quarters of the ranges, rounded to
+    the XCDs (24 per kv head on 256 CUs), as the 8k and 32k headlines do;
+    every row against exact attention."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(61)
+    H, KVH, D, P, B = 32, 8, 128, 16, 16
+    lens = [int(L) for L in rng.integers(6100, 6300, size=B)]
+    c = KVCache(num_layers=1, max_len=max(lens) + 32, num_kv_heads=KVH, head_dim=D,
+                page_tokens=P, max_seqs=B, device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=3)
+    q = rng.standard_normal((B, H, D), dtype=np.float32)
+    out = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=list(range(B))).cpu().numpy()
+    g = H // KVH
+    for i, L in enumerate(lens):
+        exact = oracle.exact_attention_f64(q[i:i + 1].transpose(1, 0, 2), np.repeat(K[i], g, 0),
+                                           np.repeat(V[i], g, 0), _limits("causal", 1, L))
+        _check(out[i:i + 1].transpose(1, 0, 2), exact, TOL_EXACT, f"row {i} len {L} vs exact")
+
+
 def test_gqa_config2_full_shape(gpu):
     """B 16, H 32, KVH 8, D 128, T ~ U[512, 4096], 16-token
     pages randomly permuted in a shared pool, one append then one query."""
