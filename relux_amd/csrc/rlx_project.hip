@@ -20,8 +20,9 @@
 // the weights with every load in flight at once (below); otherwise
 // qkv_project_kernel: work-group = 16 output features x all rows (at most
 // 64); its 4 waves take contiguous ranges of the 32-wide k-steps
-// (software-pipelined chunks of 8 weight fragments) and meet in LDS.  MFMA 16x16x32: A = x rows, B = Wp
-// rows.  bf16 activations enter as they are; f32 activations as a pair
+// (software-pipelined chunks of 8 weight fragments) and meet in LDS.
+// MFMA 16x16x32: A = x rows, B = Wp rows.  bf16 activations enter as they
+// are; f32 activations as a pair
 // hi = bf16(x), lo = bf16(x - hi) multiplied separately into the same f32
 // accumulator (bf16 products are exact in f32), which keeps the product sum
 // within ~2^-17 of the f32-activation one -- the kernel streams the weights
