@@ -425,6 +425,40 @@ def test_gqa_prefill_matches_oracle(gpu, H, KVH, D, lens, nqs, mask):
         off += nqs[i]
 
 
+@pytest.mark.parametrize("P", [48, 80])
+def test_gqa_pages_not_power_of_two(gpu, P):
+    """Pages of 48 / 80 tokens (multiples of 16, not powers of two): the
+    prefill takes its division route for page and slot, the decode and the
+    appends their generic ones; a 16-token half-block never straddles two
+    pages.  Chunked prefill, full prefill and single-query decode against
+    exact attention."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(P)
+    H, KVH, D = 16, 4, 128
+    lens, nqs = [301, 97, 160], [120, 97, 1]
+    c = KVCache(num_layers=1, max_len=max(lens) + P, num_kv_heads=KVH, head_dim=D,
+                page_tokens=P, max_seqs=len(lens), device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=3)
+    q = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    out = c.Attend(0, torch.from_numpy(q).to(gpu), H, seq_ids=list(range(len(lens))), n_q=nqs,
+                   mask="causal").cpu().numpy()
+    g = H // KVH
+    off = 0
+    for i, L in enumerate(lens):
+        qs = q[off:off + nqs[i]].transpose(1, 0, 2)
+        exact = oracle.exact_attention_f64(qs, np.repeat(K[i], g, 0), np.repeat(V[i], g, 0),
+                                           _limits("causal", nqs[i], L))
+        _check(out[off:off + nqs[i]].transpose(1, 0, 2), exact, TOL_EXACT, f"P {P} seq {i} len {L}")
+        off += nqs[i]
+    # decode of every sequence in one call
+    q1 = rng.standard_normal((len(lens), H, D), dtype=np.float32)
+    o1 = c.Attend(0, torch.from_numpy(q1).to(gpu), H, seq_ids=list(range(len(lens)))).cpu().numpy()
+    for i, L in enumerate(lens):
+        exact = oracle.exact_attention_f64(q1[i:i + 1].transpose(1, 0, 2), np.repeat(K[i], g, 0),
+                                           np.repeat(V[i], g, 0), _limits("causal", 1, L))
+        _check(o1[i:i + 1].transpose(1, 0, 2), exact, TOL_EXACT, f"P {P} decode seq {i}")
+
+
 def test_gqa_query_tiles_layouts(gpu):
     """Query-tiled attention (head_dim 16, 40 queries x 2 heads per kv head)
     gives the same rows in both q/out layouts."""
