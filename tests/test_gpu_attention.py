@@ -282,10 +282,23 @@ def _mla_exact(qc, qr, c, kr, w_uk, w_uv, limits):
     (16, [128], 1, "none"),
 ])
 def test_mla_attend_matches_oracle(gpu, H, lens, nq, mask):
+    _mla_attend_case(gpu, H, lens, nq, mask, 64)
+
+
+@pytest.mark.parametrize("P,nq", [(16, 1), (48, 1), (16, 150), (48, 150)])
+def test_mla_pages_16_and_48(gpu, P, nq):
+    """The latent cache on 16-token pages (every 16-token tile of the decode
+    ring on its own page) and on 48-token pages (not a power of two, the
+    prefill's division route), decode and FA2 prefill, against exact
+    attention."""
+    _mla_attend_case(gpu, 16, [300, 170, 40], nq, "causal", P)
+
+
+def _mla_attend_case(gpu, H, lens, nq, mask, P):
     from relux_amd import MLACache
-    rng = np.random.default_rng(31 + H + nq)
-    D, P = 128, 64
-    c = MLACache(num_layers=1, max_len=max(lens) + 64, page_tokens=P, max_seqs=len(lens),
+    rng = np.random.default_rng(31 + H + nq + P)
+    D = 128
+    c = MLACache(num_layers=1, max_len=max(lens) + P, page_tokens=P, max_seqs=len(lens),
                  device=gpu.index)
     cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
     kr = rng.standard_normal((sum(lens), 64), dtype=np.float32)
