@@ -162,6 +162,8 @@ def test_rope_position_overflow_panics(gpu):
     (17, 4096, 4096, torch.float32, torch.bfloat16, True),  # the 8k block's W_O
     (16, 4096, 4096, torch.bfloat16, torch.float32, True),  # ... with bf16 activations
     (40, 1024, 512, torch.bfloat16, torch.bfloat16, False),  # 3 row tiles
+    (20, 2048, 512, torch.bfloat16, torch.float32, True),    # decode-size kernel, two row tiles
+    (8, 512, 4608, torch.bfloat16, torch.bfloat16, True),    # 288 tiles: two per work-group
 ])
 def test_out_project_matches_oracle(gpu, rows, k_in, n_out, x_dtype, out_dtype, resid):
     """out = x . W_O (+ residual): mha.go:356-360 matmulBatched3D (bf16
