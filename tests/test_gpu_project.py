@@ -240,6 +240,8 @@ def test_cfg1_generate_with_fused_step(gpu):
     (128, 2, 64, [3, 0], [3, 4], "ref", torch.float32),
     (2048, 16, 128, [20] * 32, [1] * 32, "offset", torch.bfloat16),  # config 3's decode rows
     (512, 16, 128, [9], [66], "offset", torch.bfloat16),
+    (4096, 8, 128, [12] * 16, [1] * 16, "offset", torch.bfloat16),   # decode-size kernel, 16 waves
+    (4096, 8, 128, [12] * 20, [1] * 20, "offset", torch.bfloat16),   # 2 row tiles at 16 waves: chunked
 ])
 def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode, x_dtype):
     """mla.go:279-314: q_c = x.W_Q, q_r = RoPE(x.W_QR), c = x.W_DKV,
