@@ -310,7 +310,10 @@ int32_t rlx_mla_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t
  * cache contents and outputs as the two calls in sequence, bit for bit; on
  * the decode path the append runs inside the attention's first launch (one
  * launch fewer per step).  Every argument is checked before anything is
- * appended. */
+ * appended, including the size of a prefill's expansion.  A resource
+ * failure after that (workspace allocation, staging) still appends the
+ * tokens -- host state and device table agree, as after rlx_mla_append --
+ * and returns the error without attention outputs. */
 int32_t rlx_mla_append_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                               const int32_t *n_tok, const void *c_src, const void *kr_src,
                               int32_t src_dtype, int32_t num_heads, int32_t head_dim,

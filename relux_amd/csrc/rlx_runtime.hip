@@ -259,6 +259,13 @@ int32_t flush_patches_inline(Cache *c) {
 
 int32_t ensure_ws(Cache *c, size_t bytes) {
     if (bytes <= c->ws_cap) return RLX_OK;
+    // RLX_WS_MAX_KB caps the workspace (tests force the failure path of a
+    // call with it; unset or 0: no cap).
+    if (const char *lim = getenv("RLX_WS_MAX_KB")) {
+        const long long kb = atoll(lim);
+        if (kb > 0 && bytes > (size_t)kb << 10)
+            return fail(RLX_ERR_HIP, "workspace of %zu bytes exceeds RLX_WS_MAX_KB=%lld", bytes, kb);
+    }
     size_t cap = std::max(bytes, c->ws_cap * 2);
     cap = (cap + 65535) & ~(size_t)65535;
     HIP_TRY(hipStreamSynchronize(c->stream));
@@ -1609,6 +1616,42 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     return RLX_OK;
 }
 
+// Whether an MLA call of max_qr query rows per sequence (heads x queries)
+// runs as chunked prefill (expansion + FA2) rather than through the decode
+// kernel.
+static bool mla_use_fa2(const Cache *c, int max_qr, int head_dim) {
+    return max_qr > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr;
+}
+
+// Heads per expansion of an MLA prefill over tok_off padded tokens: the
+// expanded K_c and V^T of hg heads (2 x tok_off x hg x 128 bf16) stay within
+// the expansion budget and the kernels' 32-bit element offsets.  0: not even
+// one head fits.
+static int mla_prefill_heads(int64_t tok_off, int num_heads) {
+    const int64_t head_bytes = 2 * tok_off * 128 * 2;
+    const int64_t hg_budget = mla_expand_budget() / head_bytes;
+    const int64_t hg_index = INT32_MAX / (tok_off * 128);
+    return (int)std::max<int64_t>(0, std::min<int64_t>({(int64_t)num_heads, hg_budget, hg_index}));
+}
+
+// The prefill size check of an MLA call, before anything is appended:
+// add_tok[i] tokens are appended to sequence i first (null: none).
+static int32_t mla_prefill_check(Cache *c, int layer, int n_seqs, const int32_t *seq_ids,
+                                 const int32_t *n_q, const int32_t *add_tok, int num_heads,
+                                 int head_dim) {
+    int max_nq = 0;
+    for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
+    if (!mla_use_fa2(c, num_heads * max_nq, head_dim)) return RLX_OK;
+    int64_t tok_off = 0;
+    for (int i = 0; i < n_seqs; i++)
+        tok_off += ((int64_t)c->L[layer].seqs[seq_ids[i]].len + (add_tok ? add_tok[i] : 0) + 127) / 128 * 128;
+    if (tok_off > 0 && mla_prefill_heads(tok_off, num_heads) < 1)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "MLA prefill call too large: one head expands to %lld bytes over %lld tokens",
+                    (long long)(2 * tok_off * 128 * 2), (long long)tok_off);
+    return RLX_OK;
+}
+
 // Argument checks of an MLA attention call that change nothing (shared by
 // rlx_mla_attend and rlx_mla_append_attend, which checks before appending).
 static int32_t mla_attend_check(Cache *c, int32_t n_seqs, const int32_t *n_q, int32_t num_heads,
@@ -1625,7 +1668,7 @@ static int32_t mla_attend_check(Cache *c, int32_t n_seqs, const int32_t *n_q, in
     if (!q_nope || !q_rope || !w_uk || !w_uv || !out) return fail(RLX_ERR_INVALID, "null operand");
     int max_nq = 0;
     for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
-    const bool fa2 = num_heads * max_nq > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr;
+    const bool fa2 = mla_use_fa2(c, num_heads * max_nq, head_dim);
     if (!fa2 && num_heads * max_nq > 32 && num_heads > 32)
         return fail(RLX_ERR_UNSUPPORTED,
                     "MLA attention with more than 32 query rows takes head_dim 128, d_c 512 and d_r 64 "
@@ -1646,7 +1689,7 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     int max_nq = 0;
     for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     const int max_qr = num_heads * max_nq;
-    if (max_qr > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr) {
+    if (mla_use_fa2(c, max_qr, head_dim)) {
         if (app)
             HIP_TRY(launch_mla_append(c->stream, app->plan, app->tok_off, app->pool, app->table,
                                       app->patches, app->n_patch, app->toks, app->n_tok, app->c_src,
@@ -1678,18 +1721,11 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
             }
             tok_off += Tp;
         }
-        // Heads per expansion: the expanded K_c and V^T of hg heads (2 x
-        // tok_off x hg x 128 bf16) stay within the expansion budget and the
-        // kernels' 32-bit element offsets; larger calls run head group by
-        // head group (expansion, then FA2 over the group's heads).
-        const int64_t head_bytes = 2 * tok_off * 128 * 2;
-        const int64_t hg_budget = mla_expand_budget() / head_bytes;
-        const int64_t hg_index = INT32_MAX / (tok_off * 128);
-        const int hg = (int)std::min<int64_t>({(int64_t)num_heads, hg_budget, hg_index});
-        if (hg < 1)
-            return fail(RLX_ERR_UNSUPPORTED,
-                        "MLA prefill call too large: one head expands to %lld bytes over %lld tokens",
-                        (long long)head_bytes, (long long)tok_off);
+        // Heads per expansion (mla_prefill_heads); larger calls run head
+        // group by head group (expansion, then FA2 over the group's heads).
+        // The entry points refused a call where not one head fits.
+        const int hg = mla_prefill_heads(tok_off, num_heads);
+        if (hg < 1) return fail(RLX_ERR_UNSUPPORTED, "MLA prefill call too large");
         const int n_groups = (num_heads + hg - 1) / hg;
         // work items of the group of heads [0, hg) (the xcd order), reused by
         // every group with its heads counted from the group's first
@@ -1768,6 +1804,16 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     // [q0, q0 + qn) of n_q queries on a sequence of len tokens is the row
     // (len - n_q + q0 + qn tokens, qn queries), which has the same key
     // limits; an unmasked query is a row of its own (len tokens, 1 query).
+    // The host state of app's tokens is committed already: a failure before
+    // the launch that carries them still writes them (and their table
+    // patches) to the device, so host and device tables stay in agreement.
+    auto bail = [&](int32_t r) -> int32_t {
+        if (app)
+            (void)launch_mla_append(c->stream, app->plan, app->tok_off, app->pool, app->table,
+                                    app->patches, app->n_patch, app->toks, app->n_tok, app->c_src,
+                                    app->kr_src, app->src_bf16, app->dc, app->dr, app->P);
+        return r;
+    };
     const bool chunked = max_qr > 32;
     const int qc = chunked ? 32 / num_heads : 0;
     std::vector<AttRow> rows;
@@ -1776,8 +1822,9 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     for (int i = 0; i < n_seqs; i++) {
         const SeqState &st = ls.seqs[seq_ids[i]];
         const int nq = n_q ? n_q[i] : 1;
-        if (st.len <= 0) return fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]);
-        if (nq < 1 || nq > st.len) return fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, st.len);
+        if (st.len <= 0) return bail(fail(RLX_ERR_STATE, "sequence %d holds no tokens", seq_ids[i]));
+        if (nq < 1 || nq > st.len)
+            return bail(fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, st.len));
         const int32_t tab = (int32_t)(c->row_base(layer, seq_ids[i]) + st.first);
         auto add = [&](int len, int n, int qrow) {
             AttRow r{};
@@ -1814,12 +1861,12 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         for (int sp = 0; sp < nsplit[r]; sp++) work.push_back(int2{(int)r, sp});
         parts += nsplit[r];
     }
-    if ((rc = flush_patches(c))) return rc;
+    if ((rc = flush_patches(c))) return bail(rc);
     const int QRP = 16 * nqt;
     const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
     const size_t po_bytes = ((size_t)parts * QRP * kMlaDc * sizeof(uint16_t) + 255) & ~(size_t)255;
     const size_t pm_bytes = ((size_t)parts * QRP * 2 * sizeof(float) + 255) & ~(size_t)255;
-    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes))) return rc;
+    if ((rc = ensure_ws(c, ql_bytes + po_bytes + pm_bytes))) return bail(rc);
     PlanArg plan_arg;
     const PlanArg *plan = nullptr;
     const AttRow *d_rows = nullptr;
@@ -1831,7 +1878,7 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         Blob b;
         size_t o_r = b.add(rows), o_w = b.add(work);
         void *dev;
-        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
+        if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return bail(rc);
         d_rows = (const AttRow *)((char *)dev + o_r);
         d_work = (const int2 *)((char *)dev + o_w);
     }
@@ -1839,7 +1886,7 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     const float qscale = scale * 1.4426950408889634f;
     char *ws = (char *)c->ws;
     hipEvent_t e0, e1;
-    if ((rc = timing_events(c, &e0, &e1))) return rc;
+    if ((rc = timing_events(c, &e0, &e1))) return bail(rc);
     HIP_TRY(launch_mla_decode(c->stream, plan, ls.pool0, c->d_table, d_rows, (int)rows.size(), d_work,
                               (int)work.size(), q_nope,
                               q_rope, q_dtype == RLX_BF16, (const uint16_t *)w_uk,
@@ -1864,6 +1911,7 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                                mask_mode, out, out_dtype)))
         return rc;
     if (n_seqs == 0) return RLX_OK;
+    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_q, nullptr, num_heads, head_dim))) return rc;
     return mla_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, head_dim, q_nope, q_rope, q_dtype,
                            w_uk, w_uv, scale, mask_mode, out, out_dtype, nullptr);
 }
@@ -1889,6 +1937,7 @@ int32_t rlx_mla_append_attend(void *h, int32_t layer, int32_t n_seqs, const int3
         return rc;
     if (n_seqs == 0) return RLX_OK;
     if (!c_src || !kr_src) return fail(RLX_ERR_INVALID, "null latent source");
+    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_tok, n_tok, num_heads, head_dim))) return rc;
     // The append (rlx_mla_append), then attention of the appended tokens.
     std::vector<AppendTok> toks;
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;

@@ -707,6 +707,67 @@ def test_mla_append_attend_equals_append_then_attend(gpu, case):
         c.close()
 
 
+def test_mla_append_attend_failures_keep_host_and_device_in_step(gpu, monkeypatch):
+    """rlx_mla_append_attend on the decode path carries the append in the
+    attention's first launch.  When the call fails after the host has
+    committed the append (here the workspace, capped by RLX_WS_MAX_KB), the
+    tokens and their page-table writes still reach the device: the gather
+    through the device table returns the appended rows, the host table and
+    state equal a twin's that ran Append alone, and the next attention
+    equals the twin's bit for bit.  A prefill refused for its expansion size
+    (RLX_MLA_EXPAND_MB below one head) appends nothing."""
+    from relux_amd import MLACache, ReluxError, _lib
+    rng = np.random.default_rng(17)
+    H, D, B, P = 16, 128, 5, 64
+    lens = [130, 64, 200, 1, 77]
+    seqs = list(range(B))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    a, f = [MLACache(num_layers=1, max_len=2304, page_tokens=P, max_seqs=B, device=gpu.index)
+            for _ in range(2)]
+    cc = t(rng.standard_normal((sum(lens), 512), dtype=np.float32))
+    kr = t(rng.standard_normal((sum(lens), 64), dtype=np.float32))
+    for c in (a, f):
+        c.Append(0, cc, kr, seq_ids=seqs, n_tok=lens)
+    w = [t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D))).view(np.int16)).view(torch.bfloat16)
+         for _ in range(2)]
+    c1 = t(rng.standard_normal((B, 512), dtype=np.float32))
+    k1 = t(rng.standard_normal((B, 64), dtype=np.float32))
+    qn = t(rng.standard_normal((B, H, D), dtype=np.float32))
+    qr = t(rng.standard_normal((B, H, 64), dtype=np.float32))
+    a.Append(0, c1, k1, seq_ids=seqs, n_tok=[1] * B)  # sequence 1 opens a new page
+    monkeypatch.setenv("RLX_WS_MAX_KB", "1")
+    with pytest.raises(ReluxError):
+        f.AppendAttend(0, c1, k1, qn, qr, w[0], w[1], H, D, seq_ids=seqs, n_tok=[1] * B)
+    monkeypatch.delenv("RLX_WS_MAX_KB")
+    for i in seqs:
+        assert a.SeqState(0, i) == f.SeqState(0, i)
+        assert a.PageTable(0, i) == f.PageTable(0, i)
+        for x, y in zip(a.View(0, i), f.View(0, i)):  # through the device table
+            assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    assert a.FreeList(0) == f.FreeList(0)
+    want = a.Attend(0, qn, qr, w[0], w[1], H, D, seq_ids=seqs).cpu()
+    got = f.Attend(0, qn, qr, w[0], w[1], H, D, seq_ids=seqs).cpu()
+    assert torch.equal(got, want)
+    # prefill (80 query rows per sequence: expansion + FA2) whose single
+    # head would expand past a 1 MB budget: refused before the append
+    monkeypatch.setenv("RLX_MLA_EXPAND_MB", "1")
+    n5 = [5] * B
+    c5 = t(rng.standard_normal((5 * B, 512), dtype=np.float32))
+    k5 = t(rng.standard_normal((5 * B, 64), dtype=np.float32))
+    q5 = t(rng.standard_normal((5 * B, H, D), dtype=np.float32))
+    r5 = t(rng.standard_normal((5 * B, H, 64), dtype=np.float32))
+    f.Append(0, t(rng.standard_normal((2000, 512), dtype=np.float32)),
+             t(rng.standard_normal((2000, 64), dtype=np.float32)), seq_ids=[2], n_tok=[2000])
+    before = [f.SeqState(0, i) for i in seqs]
+    with pytest.raises(ReluxError) as e:
+        f.AppendAttend(0, c5, k5, q5, r5, w[0], w[1], H, D, seq_ids=seqs, n_tok=n5)
+    assert e.value.code == _lib.RLX_ERR_UNSUPPORTED
+    assert [f.SeqState(0, i) for i in seqs] == before
+    monkeypatch.delenv("RLX_MLA_EXPAND_MB")
+    for c in (a, f):
+        c.close()
+
+
 @pytest.mark.parametrize("KVH,D,chunks,nq,mask", [
     (4, 64, [[5, 1, 3, 7, 1, 16, 2], [9, 1, 1, 30]], 1, "ref"),
     (2, 128, [[40, 1, 1, 1], [17, 5]], 3, "causal"),

@@ -297,3 +297,160 @@ def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode,
                                        atol=1e-2, rtol=1e-2)
         off += n
     assert np.concatenate(same).mean() > 0.99
+
+
+def _check_gqa_step(c, q, x, wq, wk, wv, H, KVH, D, tables, max_seq, seqs, ntok, live_before, pos):
+    """q and the appended K/V rows of one ProjectAppend against the oracle
+    step at the given absolute RoPE positions (one per new row)."""
+    q_o, k_o, v_o = _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, pos)
+    np.testing.assert_allclose(q, q_o, atol=2e-4, rtol=1e-4)
+    off = 0
+    same = []
+    for s, n, L in zip(seqs, ntok, live_before):
+        kg, vg = c.View(0, s)
+        kg = kg[0].view(torch.int16).cpu().numpy().view(np.uint16)[:, L:, :]
+        vg = vg[0].view(torch.int16).cpu().numpy().view(np.uint16)[:, L:, :]
+        assert kg.shape[1] == n
+        for got, want in ((kg, oracle.bf16_from_f32(k_o[off:off + n].transpose(1, 0, 2))),
+                          (vg, oracle.bf16_from_f32(v_o[off:off + n].transpose(1, 0, 2)))):
+            same.append((got == want).ravel())
+            np.testing.assert_allclose(oracle.f32_from_bf16(got), oracle.f32_from_bf16(want),
+                                       atol=1e-2, rtol=1e-2)
+        off += n
+    assert np.concatenate(same).mean() > 0.99
+
+
+@pytest.mark.parametrize("tier", ["evict", "spill"])
+def test_project_append_positions_after_evict_and_spill(gpu, tier):
+    """RoPE positions of the fused step once pages have left the cache
+    (rope.go:130-180 positions a token by its place in the whole sequence):
+    after Evict + Compact, and after Spill (the same device state), the new
+    tokens are rotated at pos_offset + live_len + j -- the count of every
+    token the sequence ever held, not the live length -- and after Restore
+    the positions continue from the restored length.  Checked against
+    oracle.rope_apply at those absolute positions; a position taken from the
+    live length alone (the slip this guards against) misses it by the
+    evicted page count x page_tokens."""
+    from relux_amd import KVCache, pack_qkv, rope_tables
+    rng = np.random.default_rng(31 if tier == "evict" else 37)
+    H, KVH, D, d_model, P, max_seq = 8, 2, 64, 256, 16, 256
+    lens = [40, 70, 33, 16]
+    drop = [1, 3, 2, 1]
+    S = len(lens)
+    c = KVCache(num_layers=1, max_len=max_seq, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=S, device=gpu.index)
+    wq, wk, wv = [oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, n * D)).astype(np.float32))
+                  for n in (H, KVH, KVH)]
+    wp = pack_qkv(_bf16_tensor(wq, gpu), _bf16_tensor(wk, gpu), _bf16_tensor(wv, gpu), H, KVH, D)
+    rope = rope_tables(D, 10000.0, max_seq, gpu)
+    tables = oracle.rope_tables(D, 10000.0, max_seq)
+    for i, L in enumerate(lens):  # interleaved one-page fills scatter the pages
+        for t0 in range(0, L, P):
+            n = min(P, L - t0)
+            kv = torch.from_numpy(rng.standard_normal((n, KVH, D), dtype=np.float32)).to(gpu)
+            c.Append(0, kv, kv, seq_ids=[i], n_tok=[n], layout="SHD")
+    before = [c.View(0, i) for i in range(S)]
+    if tier == "evict":
+        c.Evict(list(range(S)), drop)
+        c.Compact()
+    else:
+        c.AttachSpill(sum(drop))
+        c.Spill(list(range(S)), drop)
+    for i in range(S):
+        st = c.SeqState(0, i)
+        assert st["pos_offset"] == drop[i] * P and st["len"] == lens[i] - drop[i] * P
+    held = list(lens)  # tokens each sequence ever held (positions of the next ones)
+    live = [L - d * P for L, d in zip(lens, drop)]
+    for ntok in ([1, 2, 1, 3], [2, 1, 1, 1]):
+        x = rng.standard_normal((sum(ntok), d_model), dtype=np.float32)
+        q = c.ProjectAppend(0, torch.from_numpy(x).to(gpu), wp, H, rope=rope, seq_ids=list(range(S)),
+                            n_tok=ntok, rope_mode="offset").cpu().numpy()
+        pos = [h + j for h, n in zip(held, ntok) for j in range(n)]
+        _check_gqa_step(c, q, x, wq, wk, wv, H, KVH, D, tables, max_seq, range(S), ntok, live, pos)
+        held = [h + n for h, n in zip(held, ntok)]
+        live = [L + n for L, n in zip(live, ntok)]
+    if tier == "spill":
+        c.Restore(list(range(S)), drop)
+        live = [L + d * P for L, d in zip(live, drop)]
+        for i in range(S):
+            st = c.SeqState(0, i)
+            assert st["pos_offset"] == 0 and st["len"] == held[i] == live[i]
+            k, v = c.View(0, i)
+            assert torch.equal(k[:, :, :lens[i]].view(torch.int16), before[i][0].view(torch.int16))
+            assert torch.equal(v[:, :, :lens[i]].view(torch.int16), before[i][1].view(torch.int16))
+        ntok = [1, 1, 2, 1]
+        x = rng.standard_normal((sum(ntok), d_model), dtype=np.float32)
+        q = c.ProjectAppend(0, torch.from_numpy(x).to(gpu), wp, H, rope=rope, seq_ids=list(range(S)),
+                            n_tok=ntok, rope_mode="offset").cpu().numpy()
+        pos = [h + j for h, n in zip(held, ntok) for j in range(n)]
+        _check_gqa_step(c, q, x, wq, wk, wv, H, KVH, D, tables, max_seq, range(S), ntok, live, pos)
+
+
+@pytest.mark.parametrize("tier", ["evict", "spill"])
+def test_mla_project_append_positions_after_evict_and_spill(gpu, tier):
+    """The MLA fused step (mla.go:279-314) after Evict + Compact / Spill /
+    Restore: q_r and the appended k^R rows rotated at the absolute position
+    pos_offset + live_len + j, against oracle.rope_apply there."""
+    from relux_amd import MLACache, pack_mla_proj, rope_tables
+    rng = np.random.default_rng(41 if tier == "evict" else 43)
+    H, D, dC, dR, d_model, P, max_seq = 4, 64, 512, 64, 256, 16, 256
+    lens = [50, 20, 35]
+    drop = [2, 1, 1]
+    S = len(lens)
+    c = MLACache(num_layers=1, max_len=max_seq, d_c=dC, d_r=dR, page_tokens=P, max_seqs=S,
+                 device=gpu.index)
+    mats = [oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, w)).astype(np.float32))
+            for w in (H * D, H * dR, dC, dR)]
+    wp = pack_mla_proj(*[_bf16_tensor(m, gpu) for m in mats], H, D)
+    rope = rope_tables(dR, 10000.0, max_seq, gpu)
+    tables = oracle.rope_tables(dR, 10000.0, max_seq)
+    for i, L in enumerate(lens):
+        for t0 in range(0, L, P):
+            n = min(P, L - t0)
+            cc = torch.from_numpy(rng.standard_normal((n, dC), dtype=np.float32)).to(gpu)
+            kr = torch.from_numpy(rng.standard_normal((n, dR), dtype=np.float32)).to(gpu)
+            c.Append(0, cc, kr, seq_ids=[i], n_tok=[n])
+    if tier == "evict":
+        c.Evict(list(range(S)), drop)
+        c.Compact()
+    else:
+        c.AttachSpill(sum(drop))
+        c.Spill(list(range(S)), drop)
+    held = list(lens)
+    live = [L - d * P for L, d in zip(lens, drop)]
+    steps = [[1, 2, 1], [1, 1, 3]]
+    for k, ntok in enumerate(steps):
+        if tier == "spill" and k == 1:
+            c.Restore(list(range(S)), drop)
+            live = [L + d * P for L, d in zip(live, drop)]
+            assert [c.SeqState(0, i)["pos_offset"] for i in range(S)] == [0] * S
+        x = rng.standard_normal((sum(ntok), d_model), dtype=np.float32)
+        qn, qr = c.ProjectAppend(0, torch.from_numpy(x).to(gpu), wp, H, D, rope=rope,
+                                 seq_ids=list(range(S)), n_tok=ntok, rope_mode="offset")
+        pos = [h + j for h, n in zip(held, ntok) for j in range(n)]
+        R = sum(ntok)
+        qc_o = oracle.matmul_bf16w(x, mats[0]).reshape(R, H, D)
+        qr_o = oracle.matmul_bf16w(x, mats[1]).reshape(R, H, dR)
+        c_o = oracle.matmul_bf16w(x, mats[2])
+        kr_o = oracle.matmul_bf16w(x, mats[3])
+        for r in range(R):
+            qr_o[r] = oracle.rope_apply(qr_o[r][:, None, :], pos[r], tables, max_seq)[:, 0, :]
+            kr_o[r] = oracle.rope_apply(kr_o[r][None, None, :], pos[r], tables, max_seq)[0, 0, :]
+        np.testing.assert_allclose(qn.cpu().numpy(), qc_o, atol=2e-4, rtol=1e-4)
+        np.testing.assert_allclose(qr.cpu().numpy(), qr_o, atol=2e-4, rtol=1e-4)
+        off = 0
+        same = []
+        for i, n in enumerate(ntok):
+            cg, krg = c.View(0, i)
+            assert cg.shape[1] == live[i] + n
+            cg = cg[0].view(torch.int16).cpu().numpy().view(np.uint16)[live[i]:]
+            krg = krg[0].view(torch.int16).cpu().numpy().view(np.uint16)[live[i]:]
+            for got, want in ((cg, oracle.bf16_from_f32(c_o[off:off + n])),
+                              (krg, oracle.bf16_from_f32(kr_o[off:off + n]))):
+                same.append((got == want).ravel())
+                np.testing.assert_allclose(oracle.f32_from_bf16(got), oracle.f32_from_bf16(want),
+                                           atol=1e-2, rtol=1e-2)
+            off += n
+        assert np.concatenate(same).mean() > 0.99
+        held = [h + n for h, n in zip(held, ntok)]
+        live = [L + n for L, n in zip(live, ntok)]
