@@ -646,9 +646,13 @@ def main():
                                  "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample",
                                  "spill8k")
                      if w != args.workload]:
-            # spec_stress: 300 timed steps after the warm-up cross one evict + compact
-            n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(50, args.steps // 2))
-            s = run_workload(name, n_steps, 2 if name == "mla_prefill" else args.warmup, torch, dev)
+            # spec_stress: 300 timed steps after the warm-up cross one evict + compact;
+            # the other secondary lines time at least 200 steps after at least 20
+            # warm-up steps, whatever the headline's K and W (a short run after a
+            # short warm-up averages in the launches of a GPU still ramping up)
+            n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(200, args.steps))
+            n_warm = {"mla_prefill": 2}.get(name, max(20, args.warmup))
+            s = run_workload(name, n_steps, n_warm, torch, dev)
             print(f"[bench] {name}: {s['tokens_per_s']:.0f} tok/s, kernel {s['kernel_avg_us']:.1f} us, "
                   f"{s['kernel_rate']:.0f} {s['rate_unit']}", file=sys.stderr, flush=True)
             entry = {"workload": s["desc"]["workload"], "tokens_per_s": round(s["tokens_per_s"], 1),
