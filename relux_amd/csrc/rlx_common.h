@@ -512,30 +512,38 @@ constexpr int kPrefillRows = 256;
 struct PrefillArgs {
     const uint16_t *kpool;  // paged: K pages (k-step-major 16-token blocks); dense: latent pool (rope keys)
     const uint16_t *vpool;  // paged: V dim-major pages
-    const uint16_t *kc;     // dense: K_c [H][Tp][128] of the H heads expanded, sequence s at + part*H*128
-    const uint16_t *vt;     // dense: V^T [H][128][Tp], same sequence offsets
+    const uint16_t *kc;     // dense: K_c [H][Tp][vd] of the H heads expanded, sequence s at + part*H*vd
+    const uint16_t *vt;     // dense: V^T [H][vd][Tp], same sequence offsets
     const int32_t *table;
     const AttRow *rows;     // dense: part = token offset of the sequence, nsplit = Tp
     const int4 *work;       // (row, head group, query tile, unused)
-    const void *q;          // paged: [rows][H][D]; dense: q_nope [rows][H][128]
-    const void *q2;         // dense: q_rope [rows][H][64]
+    const void *q;          // paged: [rows][H][qd]; dense: q_nope [rows][H][qd]
+    const void *q2;         // dense: q_rope [rows][H][qd2]
     void *out;
     int q_bf16, layout, out_bf16, mask_mode;
     int H, KVH, P;
     int HQ, h0;  // q / out rows hold HQ heads; work-item head h is the caller's head h0 + h
     int pshift;  // log2(P) when P is a power of two, else -1
     float qscale;
+    int qd;      // q (dense: q_nope) dims per head row: row stride; dims past it are zero
+    int qd2;     // dense: q_rope dims per head row (d_r)
+    int od;      // output dims per head row (row stride; dims past it are not written)
+    int vd;      // V dims per row as stored: paged, the pool's head_dim; dense, the padded
+                 // head dim of K_c / V^T (128 or 256)
+    int dv0;     // first V dim of this launch (head dims of 256 run as two 128-dim launches)
 };
 
 hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, int n_work,
                           hipEvent_t ev0, hipEvent_t ev1);
-// W_UK / W_UV [d_c][H*D] transposed to wt [H*D][d_c] (once per call).
+// W_UK / W_UV [d_c][H*D] transposed to wt [H*DP][512] (once per call): head
+// dims padded with zero rows to DP (128 or 256), channels with zero columns
+// to 512.
 hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_uv, int H, int D,
-                         uint16_t *wt_k, uint16_t *wt_v);
-// K_c / V^T of H heads from their transposed weights (wt_k, wt_v: the
-// heads' rows of the transposed matrices).
+                         int dc, int DP, uint16_t *wt_k, uint16_t *wt_v);
+// K_c [H][Tp][DP] / V^T [H][DP][Tp] of H heads from their transposed weights
+// (wt_k, wt_v: the heads' rows of the transposed matrices).
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, const int2 *work, int n_work, int H, int D, int P,
+                             const AttRow *rows, const int2 *work, int n_work, int H, int DP, int P,
                              const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,
                              int cus);
 

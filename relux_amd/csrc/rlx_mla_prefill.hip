@@ -65,7 +65,7 @@ template <int OUT_V>
 __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
     const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
     const AttRow *__restrict__ rows, const int2 *__restrict__ work, int n_work,
-    const uint16_t *__restrict__ wt, int N, int H, int P, uint16_t *__restrict__ dst) {
+    const uint16_t *__restrict__ wt, int N, int H, int P, int dps, uint16_t *__restrict__ dst) {
     __shared__ __attribute__((aligned(16))) uint16_t ring[kXS * kXStage];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar registers)
@@ -196,7 +196,8 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
         const AttRow R = rows[wk.x];
         const int tk0 = wk.y + wtk * 64;
         const int Tp = R.nsplit;
-        uint16_t *db = dst + (int64_t)R.part * H * 128;
+        const int DP = 1 << dps;  // padded head dim: feature f is dim f % DP of head f / DP
+        uint16_t *db = dst + (int64_t)R.part * H * DP;
 #pragma unroll
         for (int i = 0; i < 4; i += 2)
 #pragma unroll
@@ -221,32 +222,62 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
                     if (f < N) *(u32x4 *)(db + (int64_t)f * Tp + tk) = w;
                 } else {
                     const int f = f0 + m, tk = tk0 + n;
-                    if (f < N) *(u32x4 *)(db + ((int64_t)(f >> 7) * Tp + tk) * 128 + (f & 127)) = w;
+                    if (f < N) *(u32x4 *)(db + ((int64_t)(f >> dps) * Tp + tk) * DP + (f & (DP - 1))) = w;
                 }
             }
     }
 }
 
+// W [dc][H*D] -> WT [H*DP][512] with zeros for dims d >= D of every head and
+// for latent channels c >= dc (the expansion then writes exact zeros for
+// the padded dims, and the zero-padded channels of the latent rows meet
+// zero weights), 64x64 tiles through LDS.
+__global__ __launch_bounds__(256) void transpose_pad_kernel(const uint16_t *__restrict__ w,
+                                                            uint16_t *__restrict__ wt, int dc,
+                                                            int H, int D, int DP) {
+    __shared__ uint16_t tile[64][66];
+    const int c0 = blockIdx.y * 64;   // latent channels
+    const int f0 = blockIdx.x * 64;   // padded features h * DP + d
+    for (int i = threadIdx.x; i < 64 * 64; i += blockDim.x) {
+        const int r = i / 64, k = i % 64;  // channel c0 + r, feature f0 + k
+        const int f = f0 + k, h = f / DP, d = f - h * DP;
+        tile[r][k] = (c0 + r < dc && d < D && h < H) ? w[(int64_t)(c0 + r) * H * D + h * D + d] : 0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += blockDim.x) {
+        const int k = i / 64, r = i % 64;
+        if (f0 + k < H * DP) wt[(int64_t)(f0 + k) * kMlaDc + c0 + r] = tile[r][k];
+    }
+}
+
 hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_uv, int H, int D,
-                         uint16_t *wt_k, uint16_t *wt_v) {
-    const int N = H * D;
-    dim3 tg((N + 63) / 64, (kMlaDc + 63) / 64);
-    transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uk, wt_k, kMlaDc, N);
-    transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uv, wt_v, kMlaDc, N);
+                         int dc, int DP, uint16_t *wt_k, uint16_t *wt_v) {
+    if (D > DP || DP % 64 != 0 || dc > kMlaDc) return hipErrorInvalidValue;
+    if (D == DP && dc == kMlaDc) {
+        const int N = H * D;
+        dim3 tg((N + 63) / 64, (kMlaDc + 63) / 64);
+        transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uk, wt_k, kMlaDc, N);
+        transpose_bf16_kernel<<<tg, 256, 0, s>>>(w_uv, wt_v, kMlaDc, N);
+    } else {
+        dim3 tg(H * DP / 64, kMlaDc / 64);
+        transpose_pad_kernel<<<tg, 256, 0, s>>>(w_uk, wt_k, dc, H, D, DP);
+        transpose_pad_kernel<<<tg, 256, 0, s>>>(w_uv, wt_v, dc, H, D, DP);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
-                             const AttRow *rows, const int2 *work, int n_work, int H, int D, int P,
+                             const AttRow *rows, const int2 *work, int n_work, int H, int DP, int P,
                              const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,
                              int cus) {
-    if (D != 128) return hipErrorInvalidValue;
-    const int N = H * D;
+    if (DP != 128 && DP != 256) return hipErrorInvalidValue;
+    const int dps = DP == 128 ? 7 : 8;
+    const int N = H * DP;
     if (n_work <= 0) return hipSuccess;
     const int tiles = (N + kXM - 1) / kXM * n_work;
     const int grid = std::max(1, std::min(tiles, cus));
-    mla_expand_kernel<0><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_k, N, H, P, kc);
-    mla_expand_kernel<1><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_v, N, H, P, vt);
+    mla_expand_kernel<0><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_k, N, H, P, dps, kc);
+    mla_expand_kernel<1><<<grid, 512, 0, s>>>(pool, table, rows, work, n_work, wt_v, N, H, P, dps, vt);
     return hipGetLastError();
 }
 

@@ -79,13 +79,14 @@ template <int DQK, int DV, int SRC>
 struct PfShape {
     static constexpr int KS = DQK / 16;                              // score k-steps
     static constexpr int NKR = DQK / 64;                             // K regions
+    static constexpr int DP = SRC == kSrcDense ? DQK - 64 : DQK;     // dense: K_c row pitch
     static constexpr int ST = NKR * 512 + DV * 8;                    // chunks per stage
     static constexpr int LV = DV / 64;                               // V^T loads per wave
     static constexpr int LPW = NKR + LV;                             // ring loads per wave
-    static constexpr int S = ST * 16 * 4 <= 131072 ? 4 : 3;          // ring stages
+    static constexpr int S = ST * 16 * 4 <= 131072 ? 4 : ST * 16 * 3 <= 163840 ? 3 : 2;  // ring stages
     static constexpr int MD = DV / 32;                               // output dim tiles
     static_assert(DQK % 64 == 0 && DV % 64 == 0, "whole 64-dim regions");
-    static_assert(SRC == kSrcPaged || (DQK == 192 && DV == 128), "dense: K_c 128 + rope 64");
+    static_assert(SRC == kSrcPaged || DV == 128, "dense: 128 value dims per launch");
 };
 
 // POW2: the page size is a power of two (page index and slot by shifts).
@@ -94,6 +95,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                                                           const int32_t *__restrict__ table) {
     using SH = PfShape<DQK, DV, SRC>;
     constexpr int KS = SH::KS, NKR = SH::NKR, S = SH::S, MD = SH::MD, LV = SH::LV, LPW = SH::LPW;
+    constexpr int DP = SH::DP;
     __shared__ __attribute__((aligned(16))) uint16_t ring[S * SH::ST * 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hh = lane >> 5;
@@ -123,8 +125,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     for (int q = 0; q < NKR; q++) {
         if (SRC == kSrcPaged)
             ko[q] = (uint32_t)k_page_off(kr & 15, 64 * q + klc * 8, DQK) * 2;
-        else if (q < 2)
-            ko[q] = (uint32_t)(kr * 128 + 64 * q + klc * 8) * 2;
+        else if (q < NKR - 1)
+            ko[q] = (uint32_t)(kr * DP + 64 * q + klc * 8) * 2;
         else
             ko[q] = (uint32_t)((kr & 15) * kMlaRow + kMlaDc + klc * 8) * 2;
     }
@@ -136,14 +138,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const int p = (8 * i + wave) * 64 + lane;
         vd[i] = p >> 3;
         vlc[i] = (p & 7) ^ pf_swz(vd[i]);
-        ov[i] = (SRC == kSrcDense) ? (uint32_t)((int64_t)vd[i] * R.nsplit + vlc[i] * 8) * 2 : 0u;
+        ov[i] = (SRC == kSrcDense) ? (uint32_t)((int64_t)(a.dv0 + vd[i]) * R.nsplit + vlc[i] * 8) * 2 : 0u;
     }
     auto pdiv = [&](int t) { return POW2 ? t >> a.pshift : t / a.P; };
     auto pmod = [&](int t) { return POW2 ? t & (a.P - 1) : t % a.P; };
     const uint16_t *kc_seq = nullptr, *vt_seq = nullptr;
     if (SRC == kSrcDense) {
-        kc_seq = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit) * 128;
-        vt_seq = a.vt + (int64_t)R.part * a.H * 128 + (int64_t)hg * 128 * R.nsplit;
+        kc_seq = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit) * DP;
+        vt_seq = a.vt + (int64_t)R.part * a.H * DP + (int64_t)hg * DP * R.nsplit;
     }
     // Blocks are issued in order, one per call: running K_c / V^T pointers
     // and stage offset of the next block to issue.
@@ -170,7 +172,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const uint16_t *kc_blk = kc_next, *vt_blk = vt_next;
         st_next = (st_next + kStageBytes == S * kStageBytes) ? 0u : st_next + kStageBytes;
         if (SRC == kSrcDense) {
-            kc_next += kKeyBlock * 128;
+            kc_next += kKeyBlock * DP;
             vt_next += kKeyBlock;
         }
         if (k0 + kKeyBlock <= R.len) {
@@ -182,10 +184,10 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 #pragma unroll
                 for (int q = 0; q < NKR; q++) lds_dma16(b, ko[q], kdst + q * 8192);
             } else {
-                lds_dma16(kc_blk, ko[0], kdst);
-                lds_dma16(kc_blk, ko[1], kdst + 8192);
+#pragma unroll
+                for (int q = 0; q < NKR - 1; q++) lds_dma16(kc_blk, ko[q], kdst + q * 8192);
                 const uint16_t *r = a.kpool + ((int64_t)page_of(tg) * a.P + pmod(tg)) * kMlaRow;
-                lds_dma16(r, ko[2], kdst + 2 * 8192);
+                lds_dma16(r, ko[NKR - 1], kdst + (NKR - 1) * 8192);
             }
             if (SRC == kSrcPaged) {
                 int pg[4];
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                 for (int i = 0; i < LV; i++) {
                     const uint32_t dst = stage + (uint32_t)(NKR * 512 + (8 * i + wave) * 64) * 16;
                     const int pgl = vg1[i] ? pg[1] : vg2[i] ? pg[2] : vg3[i] ? pg[3] : pg[0];
-                    const uint16_t *gp = a.vpool + (((int64_t)pgl * a.KVH + hg) * DV + vd[i]) * a.P +
+                    const uint16_t *gp = a.vpool + (((int64_t)pgl * a.KVH + hg) * a.vd + a.dv0 + vd[i]) * a.P +
                                          pmod(k0 + 8 * vlc[i]);
                     lds_dma16(gp, dst);
                 }
@@ -211,14 +213,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         // chunk (their entries are zeroed in LDS before use).
         {
             const int t = min(k0 + kr, R.len - 1);
-            const int pgt = (SRC == kSrcPaged || NKR > 2) ? table[R.tab + pdiv(t)] : 0;
+            const int pgt = table[R.tab + pdiv(t)];
 #pragma unroll
             for (int q = 0; q < NKR; q++) {
                 const uint16_t *gp;
                 if (SRC == kSrcPaged)
                     gp = a.kpool + ((int64_t)pgt * a.KVH + hg) * a.P * DQK + k_page_off(pmod(t), 64 * q + klc * 8, DQK);
-                else if (q < 2)
-                    gp = kc_seq + (int64_t)t * 128 + 64 * q + klc * 8;
+                else if (q < NKR - 1)
+                    gp = kc_seq + (int64_t)t * DP + 64 * q + klc * 8;
                 else
                     gp = a.kpool + ((int64_t)pgt * a.P + pmod(t)) * kMlaRow + kMlaDc + klc * 8;
                 lds_dma16(gp, __builtin_amdgcn_readfirstlane(kdst + q * 8192));
@@ -233,9 +235,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             const uint16_t *gp;
             if (SRC == kSrcPaged) {
                 const int pgt = table[R.tab + pdiv(t)];
-                gp = a.vpool + (((int64_t)pgt * a.KVH + hg) * DV + vd[i]) * a.P + pmod(t);
+                gp = a.vpool + (((int64_t)pgt * a.KVH + hg) * a.vd + a.dv0 + vd[i]) * a.P + pmod(t);
             } else {
-                gp = vt_seq + (int64_t)vd[i] * R.nsplit + t;
+                gp = vt_seq + (int64_t)(a.dv0 + vd[i]) * R.nsplit + t;
             }
             lds_dma16(gp, dst);
         }
@@ -267,32 +269,45 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const float zs = rvalid ? a.qscale : 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ks++) {
+            // q dims d .. d + 7 of a row of nd dims (zeros past nd: the K and V
+            // rows hold zeros there too)
             const int d0 = ks * 16 + hh * 8;
             const void *src;
             int64_t off;
-            if (SRC == kSrcPaged || d0 < 128) {
-                const int D = (SRC == kSrcPaged) ? DQK : 128;
+            int d, nd;
+            if (SRC == kSrcPaged || d0 < DP) {
                 src = a.q;
+                d = d0;
+                nd = a.qd;
                 off = (a.layout == kLayoutSHD || SRC == kSrcDense)
-                          ? ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + qh) * D + d0
-                          : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + qh) * R.nq + jc) * D + d0;
+                          ? ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + qh) * nd + d
+                          : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + qh) * R.nq + jc) * nd + d;
             } else {
                 src = a.q2;
-                off = ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + qh) * kMlaDr + (d0 - 128);
+                d = d0 - DP;
+                nd = a.qd2;
+                off = ((int64_t)(R.qrow + jc) * a.HQ + a.h0 + qh) * nd + d;
             }
-            float v[8];
-            if (a.q_bf16) {
-                const u32x4 raw = *(const u32x4 *)((const uint16_t *)src + off);
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (d + 8 <= nd && (nd & 7) == 0) {  // whole aligned chunk
+                if (a.q_bf16) {
+                    const u32x4 raw = *(const u32x4 *)((const uint16_t *)src + off);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    v[2 * i] = bf16_f32((uint16_t)(raw[i] & 0xFFFFu));
-                    v[2 * i + 1] = bf16_f32((uint16_t)(raw[i] >> 16));
+                    for (int i = 0; i < 4; i++) {
+                        v[2 * i] = bf16_f32((uint16_t)(raw[i] & 0xFFFFu));
+                        v[2 * i + 1] = bf16_f32((uint16_t)(raw[i] >> 16));
+                    }
+                } else {
+                    const float4 *f = (const float4 *)((const float *)src + off);
+                    const float4 x = f[0], y = f[1];
+                    v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+                    v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
                 }
             } else {
-                const float4 *f = (const float4 *)((const float *)src + off);
-                const float4 x = f[0], y = f[1];
-                v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-                v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (d + i < nd)
+                        v[i] = a.q_bf16 ? bf16_f32(((const uint16_t *)src)[off + i]) : ((const float *)src)[off + i];
             }
             u32x4 w;
 #pragma unroll
@@ -473,13 +488,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     }
     if (!rvalid) return;
     const float inv = (l_part > 0.f) ? 1.f / l_part : 0.f;
-    const int64_t obase = (a.layout == kLayoutSHD || SRC == kSrcDense)
-                              ? ((int64_t)(R.qrow + qj) * a.HQ + a.h0 + qh) * DV
-                              : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + qh) * R.nq + qj) * DV;
+    const int64_t obase = ((a.layout == kLayoutSHD || SRC == kSrcDense)
+                               ? ((int64_t)(R.qrow + qj) * a.HQ + a.h0 + qh) * a.od
+                               : ((int64_t)R.qrow * a.HQ + (int64_t)(a.h0 + qh) * R.nq + qj) * a.od) + a.dv0;
 #pragma unroll
     for (int md = 0; md < MD; md++)
 #pragma unroll
         for (int g4 = 0; g4 < 4; g4++) {
+            if (a.dv0 + md * 32 + 8 * g4 + 4 * hh >= a.od) continue;  // (od is a multiple of 8)
             const int64_t off = obase + md * 32 + 8 * g4 + 4 * hh;
             const fl4 o = fl4{acc[md][4 * g4], acc[md][4 * g4 + 1], acc[md][4 * g4 + 2], acc[md][4 * g4 + 3]} * inv;
             if (a.out_bf16) {
@@ -498,15 +514,23 @@ hipError_t launch_prefill(hipStream_t s, int src, int hd, const PrefillArgs &a, 
     if (n_work <= 0) return hipSuccess;
     const dim3 g(n_work), b(64 * kWaves);
     const bool p2 = a.pshift >= 0;
-    if (src == kSrcPaged && hd == 128)
-        return p2 ? launch_timed(prefill_kernel<128, 128, kSrcPaged, true>, g, b, s, ev0, ev1, a, a.table)
-                  : launch_timed(prefill_kernel<128, 128, kSrcPaged, false>, g, b, s, ev0, ev1, a, a.table);
-    if (src == kSrcPaged && hd == 64)
-        return p2 ? launch_timed(prefill_kernel<64, 64, kSrcPaged, true>, g, b, s, ev0, ev1, a, a.table)
-                  : launch_timed(prefill_kernel<64, 64, kSrcPaged, false>, g, b, s, ev0, ev1, a, a.table);
-    if (src == kSrcDense && hd == 128)
-        return p2 ? launch_timed(prefill_kernel<192, 128, kSrcDense, true>, g, b, s, ev0, ev1, a, a.table)
-                  : launch_timed(prefill_kernel<192, 128, kSrcDense, false>, g, b, s, ev0, ev1, a, a.table);
+#define RLX_PF(DQK, DV, SRC, A, E0, E1)                                                              \
+    (p2 ? launch_timed(prefill_kernel<DQK, DV, SRC, true>, g, b, s, E0, E1, A, A.table)            \
+        : launch_timed(prefill_kernel<DQK, DV, SRC, false>, g, b, s, E0, E1, A, A.table))
+    if (src == kSrcPaged && hd == 128) return RLX_PF(128, 128, kSrcPaged, a, ev0, ev1);
+    if (src == kSrcPaged && hd == 64) return RLX_PF(64, 64, kSrcPaged, a, ev0, ev1);
+    if (src == kSrcDense && hd == 128) return RLX_PF(192, 128, kSrcDense, a, ev0, ev1);
+    if (hd == 256) {  // two launches, one per 128 value dims (the scores are computed in each)
+        PrefillArgs a0 = a, a1 = a;
+        a0.dv0 = 0;
+        a1.dv0 = 128;
+        hipError_t e = src == kSrcPaged ? RLX_PF(256, 128, kSrcPaged, a0, ev0, nullptr)
+                                        : RLX_PF(320, 128, kSrcDense, a0, ev0, nullptr);
+        if (e != hipSuccess) return e;
+        return src == kSrcPaged ? RLX_PF(256, 128, kSrcPaged, a1, nullptr, ev1)
+                                : RLX_PF(320, 128, kSrcDense, a1, nullptr, ev1);
+    }
+#undef RLX_PF
     return hipErrorInvalidValue;
 }
 

@@ -1274,10 +1274,11 @@ int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = G * max_nq;
-    // The FA2 prefill kernel covers head_dim 64/128 with G dividing 128;
-    // other shapes tile their queries through the decode kernel, whose
-    // work-group holds at most cap query rows of one kv head.
-    const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
+    // The FA2 prefill kernel covers stored head dims 64, 128 and 256 (any
+    // caller head_dim they hold) with G dividing 256; other shapes tile their
+    // queries through the decode kernel, whose work-group holds at most cap
+    // query rows of one kv head.
+    const bool fa2 = (c->hd == 64 || c->hd == 128 || c->hd == 256) && kPrefillRows % G == 0;
     const int cap = gqa_rows_cap(c);
     if (max_qr > cap && !fa2 && G > cap)
         return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", G,
@@ -1329,6 +1330,10 @@ int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *
         a.P = c->P;
         a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
         a.qscale = scale * 1.4426950408889634f;
+        a.qd = c->hdi;
+        a.od = c->hdi;
+        a.vd = c->hd;
+        a.dv0 = 0;
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
         HIP_TRY(launch_prefill(c->stream, kSrcPaged, c->hd, a, (int)work.size(), e0, e1));
@@ -1620,17 +1625,21 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
 // runs as chunked prefill (expansion + FA2) rather than through the decode
 // kernel.
 static bool mla_use_fa2(const Cache *c, int max_qr, int head_dim) {
-    return max_qr > 32 && head_dim == 128 && c->dc == kMlaDc && c->dr == kMlaDr;
+    (void)c;
+    return max_qr > 32 && head_dim <= 256;
 }
 
+// Padded head dim of the expanded K_c / V^T rows of an MLA prefill.
+static int mla_prefill_dp(int head_dim) { return head_dim <= 128 ? 128 : 256; }
+
 // Heads per expansion of an MLA prefill over tok_off padded tokens: the
-// expanded K_c and V^T of hg heads (2 x tok_off x hg x 128 bf16) stay within
+// expanded K_c and V^T of hg heads (2 x tok_off x hg x DP bf16) stay within
 // the expansion budget and the kernels' 32-bit element offsets.  0: not even
 // one head fits.
-static int mla_prefill_heads(int64_t tok_off, int num_heads) {
-    const int64_t head_bytes = 2 * tok_off * 128 * 2;
+static int mla_prefill_heads(int64_t tok_off, int num_heads, int dp) {
+    const int64_t head_bytes = 2 * tok_off * dp * 2;
     const int64_t hg_budget = mla_expand_budget() / head_bytes;
-    const int64_t hg_index = INT32_MAX / (tok_off * 128);
+    const int64_t hg_index = INT32_MAX / (tok_off * dp);
     return (int)std::max<int64_t>(0, std::min<int64_t>({(int64_t)num_heads, hg_budget, hg_index}));
 }
 
@@ -1645,10 +1654,11 @@ static int32_t mla_prefill_check(Cache *c, int layer, int n_seqs, const int32_t 
     int64_t tok_off = 0;
     for (int i = 0; i < n_seqs; i++)
         tok_off += ((int64_t)c->L[layer].seqs[seq_ids[i]].len + (add_tok ? add_tok[i] : 0) + 127) / 128 * 128;
-    if (tok_off > 0 && mla_prefill_heads(tok_off, num_heads) < 1)
+    const int dp = mla_prefill_dp(head_dim);
+    if (tok_off > 0 && mla_prefill_heads(tok_off, num_heads, dp) < 1)
         return fail(RLX_ERR_UNSUPPORTED,
                     "MLA prefill call too large: one head expands to %lld bytes over %lld tokens",
-                    (long long)(2 * tok_off * 128 * 2), (long long)tok_off);
+                    (long long)(2 * tok_off * dp * 2), (long long)tok_off);
     return RLX_OK;
 }
 
@@ -1666,14 +1676,8 @@ static int32_t mla_attend_check(Cache *c, int32_t n_seqs, const int32_t *n_q, in
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
     if (n_seqs == 0) return RLX_OK;
     if (!q_nope || !q_rope || !w_uk || !w_uv || !out) return fail(RLX_ERR_INVALID, "null operand");
-    int max_nq = 0;
-    for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
-    const bool fa2 = mla_use_fa2(c, num_heads * max_nq, head_dim);
-    if (!fa2 && num_heads * max_nq > 32 && num_heads > 32)
-        return fail(RLX_ERR_UNSUPPORTED,
-                    "MLA attention with more than 32 query rows takes head_dim 128, d_c 512 and d_r 64 "
-                    "when num_heads > 32 (got %d heads, head_dim %d, d_c %d, d_r %d)",
-                    num_heads, head_dim, c->dc, c->dr);
+    // (Calls of more than 32 query rows per sequence take the FA2 path, which
+    // covers every head_dim accepted above.)
     return RLX_OK;
 }
 
@@ -1724,7 +1728,8 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         // Heads per expansion (mla_prefill_heads); larger calls run head
         // group by head group (expansion, then FA2 over the group's heads).
         // The entry points refused a call where not one head fits.
-        const int hg = mla_prefill_heads(tok_off, num_heads);
+        const int dp = mla_prefill_dp(head_dim);
+        const int hg = mla_prefill_heads(tok_off, num_heads, dp);
         if (hg < 1) return fail(RLX_ERR_UNSUPPORTED, "MLA prefill call too large");
         const int n_groups = (num_heads + hg - 1) / hg;
         // work items of the group of heads [0, hg) (the xcd order), reused by
@@ -1738,8 +1743,8 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
             }
         const std::vector<int4> pwork = xcd_order(pg_grp, pc_grp);
         if ((rc = flush_patches(c))) return rc;
-        const size_t w_bytes = (size_t)num_heads * 128 * kMlaDc * 2;
-        const size_t e_bytes = (size_t)tok_off * hg * 128 * 2;
+        const size_t w_bytes = (size_t)num_heads * dp * kMlaDc * 2;
+        const size_t e_bytes = (size_t)tok_off * hg * dp * 2;
         if ((rc = ensure_ws(c, 2 * w_bytes + 2 * e_bytes))) return rc;
         Blob b;
         size_t o_r = b.add(rows), o_d = b.add(dwork), o_p = b.add(pwork);
@@ -1750,16 +1755,16 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         uint16_t *kc = (uint16_t *)(ws + 2 * w_bytes), *vt = (uint16_t *)(ws + 2 * w_bytes + e_bytes);
         const AttRow *drows = (const AttRow *)((char *)dev + o_r);
         HIP_TRY(launch_mla_wt(c->stream, (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
-                              wt_k, wt_v));
-        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + kMlaDr)));
+                              c->dc, dp, wt_k, wt_v));
+        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + c->dr)));
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
         for (int g = 0; g < n_groups; g++) {
             const int h0 = g * hg, nh = std::min(hg, num_heads - h0);
             HIP_TRY(launch_mla_expand(c->stream, ls.pool0, c->d_table, drows,
-                                      (const int2 *)((char *)dev + o_d), (int)dwork.size(), nh, head_dim,
-                                      c->P, wt_k + (size_t)h0 * 128 * kMlaDc,
-                                      wt_v + (size_t)h0 * 128 * kMlaDc, kc, vt, c->cus));
+                                      (const int2 *)((char *)dev + o_d), (int)dwork.size(), nh, dp,
+                                      c->P, wt_k + (size_t)h0 * dp * kMlaDc,
+                                      wt_v + (size_t)h0 * dp * kMlaDc, kc, vt, c->cus));
             PrefillArgs a{};
             a.kpool = ls.pool0;
             a.kc = kc;
@@ -1781,18 +1786,23 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
             a.P = c->P;
             a.pshift = (c->P & (c->P - 1)) == 0 ? __builtin_ctz((unsigned)c->P) : -1;
             a.qscale = scale * 1.4426950408889634f;
+            a.qd = head_dim;
+            a.qd2 = c->dr;
+            a.od = head_dim;
+            a.vd = dp;
+            a.dv0 = 0;
             // work items of heads >= nh (a last, smaller group) are dropped
             int n_work = (int)pwork.size();
             if (nh < hg) {
                 std::vector<int4> part_w;
                 for (const int4 &w : pwork)
                     if (w.y < nh) part_w.push_back(w);
-                void *dp;
-                if ((rc = stage(c, part_w.data(), part_w.size() * sizeof(int4), &dp))) return rc;
-                a.work = (const int4 *)dp;
+                void *dw;
+                if ((rc = stage(c, part_w.data(), part_w.size() * sizeof(int4), &dw))) return rc;
+                a.work = (const int4 *)dw;
                 n_work = (int)part_w.size();
             }
-            HIP_TRY(launch_prefill(c->stream, kSrcDense, head_dim, a, n_work, g == 0 ? e0 : nullptr,
+            HIP_TRY(launch_prefill(c->stream, kSrcDense, dp, a, n_work, g == 0 ? e0 : nullptr,
                                    g == n_groups - 1 ? e1 : nullptr));
         }
         return RLX_OK;

@@ -343,6 +343,13 @@ def _mla_attend_case(gpu, H, lens, nq, mask, P):
     (16, 128, 512, 64, [300, 65], 1, "causal"),    # default DeepSeek dims, generic absorb / out
     (16, 96, 384, 48, [260], 2, "causal"),
     (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128 prefill through FA2 (240 rows)
+    # FA2 at the reference's default dims (K_c / V^T expanded with zero rows
+    # to a 128-dim pitch, W_UK / W_UV columns past d_c zero): 64 heads at
+    # headDim 32 (dC 128, dR 16), and 40 heads decoding one query each
+    (64, 32, 128, 16, [300, 90], 3, "causal"),
+    (40, 64, 256, 32, [280, 50], 1, "causal"),
+    # head_dim 160: 256-dim pitch, two FA2 launches of 128 value dims
+    (48, 160, 512, 64, [270], 2, "causal"),
 ])
 def test_mla_other_dims_match_oracle(gpu, H, D, dC, dR, lens, nq, mask):
     """MLA at the reference's default dims (dC = 4 headDim, dHR = headDim/2,
@@ -406,8 +413,13 @@ def test_mla_other_dims_match_oracle(gpu, H, D, dC, dR, lens, nq, mask):
     (12, 4, 64, [290, 50], [60, 50], "causal"),            # G = 3 does not divide 128
     (6, 2, 128, [260], [260], "none"),
     (16, 4, 80, [300, 40], [70, 40], "causal"),            # padded head_dim: query tiles
-    (8, 2, 256, [290, 50], [60, 50], "causal"),            # head_dim 256: 16-row tiles
     (8, 8, 96, [270], [40], "ref"),
+    # FA2 at head_dim 256: two launches of 128 value dims each
+    (8, 2, 256, [290, 50], [60, 50], "causal"),
+    (32, 8, 256, [400, 100], [150, 100], "causal"),
+    (16, 2, 256, [300], [300], "none"),
+    # FA2 at a head_dim below the stored one (120 in 128-dim pages)
+    (16, 4, 120, [300, 70], [100, 70], "causal"),
 ])
 def test_gqa_prefill_matches_oracle(gpu, H, KVH, D, lens, nqs, mask):
     from relux_amd import KVCache
