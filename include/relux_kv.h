@@ -172,7 +172,10 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
  * caller's tables rope_cos/rope_sin [rope_rows][head_dim/2] (f32, device) at
  * the positions rope_mode selects, then the paged append of k and v (bf16
  * round-to-nearest-even); q_out [sum n][num_heads][head_dim] receives the
- * rotated queries for rlx_gqa_attend.  Replaces mha.go:250-289
+ * rotated queries for rlx_gqa_attend.  head_dim is the cache's (its pages
+ * may store it padded: the padding of the new rows is written with zeros);
+ * num_heads x head_dim and kv_heads x head_dim must be multiples of 16
+ * (RLX_ERR_UNSUPPORTED otherwise).  Replaces mha.go:250-289
  * (matmulBatched3D x3, rearrange, RotaryEmbedding.Apply, KVCache.Append).
  * Projections run on MFMA (bf16 operands, f32 sums): results match the
  * reference's f32 loops within tolerance, not bit for bit.  A position at
@@ -185,16 +188,19 @@ int32_t rlx_gqa_project_append(void *cache, int32_t layer, int32_t n_seqs, const
 
 /* MLA layer: pack W_Q [d_model][H*D], W_QR [d_model][H*d_r], W_DKV
  * [d_model][d_c] and W_KR [d_model][d_r] (mla.go:39-44, bf16 or f32) into
- * out (N = H*(D + d_r) + d_c + d_r features, the same fragment layout as
- * rlx_pack_qkv) for rlx_mla_project_append.  Null stream.  No reference
+ * out (N = H*(D + d_r') + d_c' + d_r' features, d_r' and d_c' = d_r and
+ * d_c rounded up to 16 with zero columns, the same fragment layout as
+ * rlx_pack_qkv) for rlx_mla_project_append on a cache of these d_c / d_r.
+ * head_dim must be a multiple of 16.  Null stream.  No reference
  * counterpart: a one-time weight preparation. */
 int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
                           int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,
-                          void *out);
+                          int32_t d_c, int32_t d_r, void *out);
 /* q_c = x.W_Q -> q_nope_out [sum n][H][head_dim]; q_r = RoPE(x.W_QR) ->
  * q_rope_out [sum n][H][d_r]; c = x.W_DKV and k^R = RoPE(x.W_KR) appended
- * as the tokens' latent rows (bf16).  Tables [rope_rows][d_r/2] (f32,
- * device), positions as for rlx_gqa_project_append.  The q outputs are the
+ * as the tokens' latent rows (bf16), zero padded past the cache's d_c and
+ * d_r.  Tables [rope_rows][d_r/2] (f32, device), positions as for
+ * rlx_gqa_project_append.  The q outputs are the
  * inputs of rlx_mla_attend.  Replaces mla.go:279-314 (four
  * matmulBatched3D, RotaryEmbedding.Apply of q^R and k^R, MLACache.Append);
  * within tolerance of the reference's f32 loops, not bit for bit. */

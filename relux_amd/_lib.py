@@ -79,7 +79,7 @@ SIGNATURES = {
     "rlx_pack_qkv": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],
     "rlx_gqa_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _vp, _vp,
                                _i32, _i32, _vp, _i32],
-    "rlx_pack_mla_proj": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp],
+    "rlx_pack_mla_proj": [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
     "rlx_mla_project_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _i32, _i32, _vp, _i32, _i32, _vp,
                                _vp, _i32, _i32, _vp, _vp, _i32],
     "rlx_pack_out": [_vp, _i32, _i32, _i32, _vp],

@@ -552,12 +552,33 @@ constexpr int kProjRows = 64;
 constexpr int kProjModelGQA = 0;
 constexpr int kProjModelMLA = 1;
 constexpr int kProjModelOut = 2;  // out = x.W (+ residual): D = output features
-hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
-                            int w_bf16, int K, uint16_t *out);
+// Matrices packed by launch_pack_proj: matrix i holds nh[i] heads of tw[i]
+// columns, each padded to pw[i] features with zero columns (unused entries:
+// nh = 0).
+struct PackSrc {
+    const void *m[4];
+    int nh[4], tw[4], pw[4];
+};
+hipError_t launch_pack_proj(hipStream_t s, const PackSrc &src, int w_bf16, int K, uint16_t *out);
+// Shapes of a projection: GQA (H, KVH, D = the caller's head dim, DS = the
+// pool's); MLA (H, D = q_c dims per head, DR / DC = d_r / d_c and DRP / DCP =
+// the same rounded up to 16, the packed widths of the rope heads and of the
+// latent); kProjOut (D = output features).
+struct ProjDims {
+    int H, KVH, D, DS, DR, DRP, DC, DCP;
+};
+__host__ __device__ inline int proj_features(int model, const ProjDims &pd) {
+    return model == kProjModelGQA ? (pd.H + 2 * pd.KVH) * pd.D
+         : model == kProjModelMLA ? pd.H * (pd.D + pd.DRP) + pd.DCP + pd.DRP
+                                  : pd.D;
+}
+hipError_t launch_proj_pad_zero(hipStream_t s, int model, const PlanArg *plan, const AppendTok *toks,
+                                int tok_off, int rows, const ProjDims &pd, uint16_t *kpool,
+                                uint16_t *vpool, int P);
 hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patch *patches,
                        int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
-                       int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
+                       const ProjDims &pd, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
                        int P, int cus, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 

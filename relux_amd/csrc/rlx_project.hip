@@ -35,15 +35,12 @@ namespace rlx {
 
 constexpr int kProjMaxRows = 64;
 
-// Packed weights: the output features of up to 4 matrices m[k][n] (widths
-// wd[i], the reference's in-row/out-col layout), concatenated, in
-// MFMA-fragment blocks: element (n, k) at ((n/16 * K/32 + k/32) * 16 + n%16)
-// * 32 + k%32, so the B fragment of one (16-feature, 32-k) step is 1 KB of
-// contiguous memory.
-struct PackSrc {
-    const void *m[4];
-    int wd[4];
-};
+// Packed weights: the output features of up to 4 matrices m[k][n] (the
+// reference's in-row/out-col layout; matrix i holds nh[i] heads of tw[i]
+// columns), concatenated with each head padded to pw[i] features by zero
+// columns, in MFMA-fragment blocks: element (n, k) at ((n/16 * K/32 + k/32)
+// * 16 + n%16) * 32 + k%32, so the B fragment of one (16-feature, 32-k) step
+// is 1 KB of contiguous memory.
 __global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int N, uint16_t *__restrict__ out) {
     __shared__ uint16_t tile[32][33];
     const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
@@ -53,9 +50,12 @@ __global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int N, uint16_t
         uint16_t v = 0;
         if (k < K && n < N) {
             int i = 0, nn = n;
-            while (i < 3 && nn >= src.wd[i]) nn -= src.wd[i++];
-            const int64_t off = (int64_t)k * src.wd[i] + nn;
-            v = w_bf16 ? ((const uint16_t *)src.m[i])[off] : bf16_rne(((const float *)src.m[i])[off]);
+            while (i < 3 && nn >= src.nh[i] * src.pw[i]) nn -= src.nh[i] * src.pw[i++];
+            const int head = nn / src.pw[i], d = nn - head * src.pw[i];
+            if (d < src.tw[i]) {
+                const int64_t off = (int64_t)k * src.nh[i] * src.tw[i] + head * src.tw[i] + d;
+                v = w_bf16 ? ((const uint16_t *)src.m[i])[off] : bf16_rne(((const float *)src.m[i])[off]);
+            }
         }
         tile[r][tx] = v;
     }
@@ -94,11 +94,33 @@ constexpr int kProjOut = 2;
 // wave calls proj_store (a RoPE pair partner, feature n ^ 1, is one lane
 // away).  kProjOut: N = D output features, plus the residual; no placement.
 struct ProjPlace {
-    int part, nn, hw;      // output part, feature within it, RoPE head width (0: none)
+    int part, nn, hw;      // output part, feature within it, features per RoPE head (0: none)
+    int tw;                // rotated dims per RoPE head (the RoPE tables' width)
     int rot;               // bit i: row i rotates (position >= 0)
     float c[4], s[4];      // RoPE (cos, sin) of each row
     int page[4], slot[4];  // append slot of each row (k / v / latent parts)
 };
+
+// Part of packed feature n: output part, feature within it, features per
+// RoPE head and rotated dims per head (0, 0: no RoPE).
+template <int MODEL>
+__device__ __forceinline__ void proj_part(const ProjDims &pd, int n, int &part, int &nn, int &hw, int &tw) {
+    part = 0;
+    nn = n;
+    hw = tw = 0;
+    if constexpr (MODEL == kProjGQA) {
+        const int NQ = pd.H * pd.D, NK = pd.KVH * pd.D;
+        part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
+        nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
+        hw = tw = part < 2 ? pd.D : 0;
+    } else if constexpr (MODEL == kProjMLA) {
+        const int NQC = pd.H * pd.D, NQR = pd.H * pd.DRP;
+        part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + pd.DCP ? 2 : 3));
+        nn = n - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + pd.DCP)));
+        hw = (part == 1 || part == 3) ? pd.DRP : 0;
+        tw = hw ? pd.DR : 0;
+    }
+}
 
 // Plan reads of the placement (no load depends on another): part, RoPE
 // positions (pos < 0: no rotation), append slots.
@@ -106,19 +128,9 @@ template <bool ARG, int MODEL>
 __device__ __forceinline__ void proj_place_plan(ProjPlace &o, int pos[4], int m, int n, int grp,
                                                 int rows, const AppendTok *__restrict__ toks,
                                                 const int32_t *__restrict__ pos_dev, int tok_off,
-                                                int pos_off, int H, int KVH, int D) {
+                                                int pos_off, const ProjDims &pd) {
     if constexpr (MODEL != kProjOut) {
-        if constexpr (MODEL == kProjGQA) {
-            const int NQ = H * D, NK = KVH * D;
-            o.part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
-            o.nn = n - (o.part == 0 ? 0 : (o.part == 1 ? NQ : NQ + NK));
-            o.hw = o.part < 2 ? D : 0;
-        } else {
-            const int NQC = H * D, NQR = H * kMlaDr;
-            o.part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + kMlaDc ? 2 : 3));
-            o.nn = n - (o.part == 0 ? 0 : (o.part == 1 ? NQC : (o.part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
-            o.hw = (o.part == 1 || o.part == 3) ? kMlaDr : 0;
-        }
+        proj_part<MODEL>(pd, n, o.part, o.nn, o.hw, o.tw);
         const bool to_q = (MODEL == kProjGQA) ? o.part == 0 : o.part < 2;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -148,10 +160,10 @@ __device__ __forceinline__ void proj_place_rope(ProjPlace &o, const int pos[4],
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             o.c[i] = o.s[i] = 0.f;
-            if (pos[i] >= 0) {
+            if (pos[i] >= 0 && dr < o.tw) {  // (padding dims past tw: zero weights, no rotation)
                 o.rot |= 1 << i;
-                o.c[i] = rcos[(int64_t)pos[i] * (o.hw / 2) + (dr >> 1)];
-                o.s[i] = rsin[(int64_t)pos[i] * (o.hw / 2) + (dr >> 1)];
+                o.c[i] = rcos[(int64_t)pos[i] * (o.tw / 2) + (dr >> 1)];
+                o.s[i] = rsin[(int64_t)pos[i] * (o.tw / 2) + (dr >> 1)];
             }
         }
     }
@@ -163,26 +175,17 @@ __device__ __forceinline__ void proj_place_rope(ProjPlace &o, const int pos[4],
 // feature (a part boundary is a multiple of 16, so the part is uniform).
 template <int MODEL>
 __device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, int col, int grp,
-                                                   int rows, int pos_off, int H, int KVH, int D,
+                                                   int rows, int pos_off, const ProjDims &pd,
                                                    const float *__restrict__ rcos,
                                                    const float *__restrict__ rsin) {
     if constexpr (MODEL != kProjOut) {
         typedef const __attribute__((address_space(4))) int32_t kint;
-        int part, nn0, hw;
-        if constexpr (MODEL == kProjGQA) {
-            const int NQ = H * D, NK = KVH * D;
-            part = n0 < NQ ? 0 : (n0 < NQ + NK ? 1 : 2);
-            nn0 = n0 - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
-            hw = part < 2 ? D : 0;
-        } else {
-            const int NQC = H * D, NQR = H * kMlaDr;
-            part = n0 < NQC ? 0 : (n0 < NQC + NQR ? 1 : (n0 < NQC + NQR + kMlaDc ? 2 : 3));
-            nn0 = n0 - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + kMlaDc)));
-            hw = (part == 1 || part == 3) ? kMlaDr : 0;
-        }
+        int part, nn0, hw, tw;
+        proj_part<MODEL>(pd, n0, part, nn0, hw, tw);
         o.part = part;
         o.nn = nn0 + col;
         o.hw = hw;
+        o.tw = tw;
         o.rot = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) o.c[i] = o.s[i] = 0.f;
@@ -196,9 +199,10 @@ __device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int p = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
-                o.rot |= (p >= 0) << i;
-                // unconditional (no branch, so no wait at a join): row max(p, 0)
-                const int64_t t = (int64_t)max(p, 0) * (hw / 2) + (dr >> 1);
+                o.rot |= (p >= 0 && dr < tw) << i;
+                // unconditional (no branch, so no wait at a join): row max(p, 0),
+                // pair min(dr, tw - 1) / 2 (padding dims past tw do not rotate)
+                const int64_t t = (int64_t)max(p, 0) * (tw / 2) + (min(dr, tw - 1) >> 1);
                 o.c[i] = rcos[t];
                 o.s[i] = rsin[t];
             }
@@ -229,7 +233,7 @@ __device__ __forceinline__ void proj_slots_pick(ProjPlace &o, const int sp[16], 
 
 template <int MODEL>
 __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int n, int grp,
-                                           int rows, int H, int KVH, int D,
+                                           int rows, const ProjDims &pd,
                                            void *__restrict__ q_out, void *__restrict__ q_out2,
                                            int q_bf16, uint16_t *__restrict__ kpool,
                                            uint16_t *__restrict__ vpool, int P) {
@@ -238,7 +242,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
         for (int i = 0; i < 4; i++) {
             const int r = m * 16 + grp * 4 + i;
             if (r >= rows) continue;
-            const int64_t off = (int64_t)r * D + n;
+            const int64_t off = (int64_t)r * pd.D + n;
             float v = y[i];
             if (q_out2)
                 v += q_bf16 ? bf16_f32(((const uint16_t *)q_out2)[off]) : ((const float *)q_out2)[off];
@@ -250,7 +254,8 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
         return;
     } else {
         const int part = o.part, nn = o.nn, hw = o.hw;
-        const int hdim = (MODEL == kProjGQA) ? D : (part == 1 ? kMlaDr : D);
+        const int H = pd.H, KVH = pd.KVH;
+        const int hdim = (MODEL == kProjGQA) ? pd.D : (part == 1 ? pd.DRP : pd.D);
         const int head = nn / hdim, d = nn - head * hdim;
         const int dr = hw ? nn % hw : 0;
 #pragma unroll
@@ -268,8 +273,11 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
             if (r >= rows) continue;
             const bool to_q = (MODEL == kProjGQA) ? part == 0 : part < 2;
             if (to_q) {
+                // (q_r heads are DRP features wide, of which DR are stored)
                 void *dst = (MODEL == kProjMLA && part == 1) ? q_out2 : q_out;
-                const int64_t off = ((int64_t)r * H + head) * hdim + d;
+                const int qw = (MODEL == kProjMLA && part == 1) ? pd.DR : hdim;
+                if (d >= qw) continue;
+                const int64_t off = ((int64_t)r * H + head) * qw + d;
                 if (q_bf16)
                     ((uint16_t *)dst)[off] = bf16_rne(v);
                 else
@@ -277,11 +285,14 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
                 continue;
             }
             if constexpr (MODEL == kProjGQA) {
+                const int DS = pd.DS;  // the pool's dims per head (DS - D padding dims: zeroed apart)
                 if (part == 1)
-                    kpool[((int64_t)o.page[i] * KVH + head) * P * D + k_page_off(o.slot[i], d, D)] = bf16_rne(v);
+                    kpool[((int64_t)o.page[i] * KVH + head) * P * DS + k_page_off(o.slot[i], d, DS)] = bf16_rne(v);
                 else
-                    vpool[(((int64_t)o.page[i] * KVH + head) * D + d) * P + o.slot[i]] = bf16_rne(v);
+                    vpool[(((int64_t)o.page[i] * KVH + head) * DS + d) * P + o.slot[i]] = bf16_rne(v);
             } else {
+                // latent c^KV dims < DC, k^R dims < DR (the row's padding is zeroed apart)
+                if (part == 2 ? nn >= pd.DC : nn >= pd.DR) continue;
                 kpool[((int64_t)o.page[i] * P + o.slot[i]) * kMlaRow + (part == 2 ? 0 : kMlaDc) + nn] = bf16_rne(v);
             }
         }
@@ -303,7 +314,7 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
     typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
     const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
     int pos_off, int rows, const void *__restrict__ x, int x_bf16, int K,
-    const uint16_t *__restrict__ wp, int H, int KVH, int D, const float *__restrict__ rcos,
+    const uint16_t *__restrict__ wp, const ProjDims pd, const float *__restrict__ rcos,
     const float *__restrict__ rsin, void *__restrict__ q_out, void *__restrict__ q_out2,
     int q_bf16, uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool,
     int32_t *__restrict__ table, int P) {
@@ -405,9 +416,9 @@ __global__ __launch_bounds__(64 * kProjWaves) void qkv_project_kernel(
         for (int w = 0; w < kProjWaves - 1; w++) y += red[w][m][lane];
         ProjPlace pl;
         int pos[4];
-        proj_place_plan<ARG, MODEL>(pl, pos, m, n, grp, rows, toks, pos_dev, tok_off, pos_off, H, KVH, D);
+        proj_place_plan<ARG, MODEL>(pl, pos, m, n, grp, rows, toks, pos_dev, tok_off, pos_off, pd);
         proj_place_rope<MODEL>(pl, pos, rcos, rsin);
-        proj_store<MODEL>(pl, y, m, n, grp, rows, H, KVH, D, q_out, q_out2, q_bf16, kpool, vpool, P);
+        proj_store<MODEL>(pl, y, m, n, grp, rows, pd, q_out, q_out2, q_bf16, kpool, vpool, P);
     }
 }
 
@@ -431,7 +442,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     typename PlanSel<ARG>::T plan, const Patch *__restrict__ patches, int n_patch,
     const AppendTok *__restrict__ toks, const int32_t *__restrict__ pos_dev, int tok_off,
     int pos_off, int rows, const void *__restrict__ x, int K, const uint16_t *__restrict__ wp,
-    int NT, int H, int KVH, int D, const float *__restrict__ rcos, const float *__restrict__ rsin,
+    int NT, const ProjDims pd, const float *__restrict__ rcos, const float *__restrict__ rsin,
     void *__restrict__ q_out, void *__restrict__ q_out2, int q_bf16,
     uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool, int32_t *__restrict__ table, int P) {
     const int tid = threadIdx.x, lane = tid & 63;
@@ -494,7 +505,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     // last fragment, so the output stage waits for no further load.
     int sp[16], ss[16];  // append slots of the output wave's rows (scalar)
     if (kEarly && wave < TPW * MT) {
-        proj_place_kernarg<MODEL>(pl, em, etile * 16, col, grp, rows, pos_off, H, KVH, D, rcos, rsin);
+        proj_place_kernarg<MODEL>(pl, em, etile * 16, col, grp, rows, pos_off, pd, rcos, rsin);
         if constexpr (MODEL != kProjOut) {
             const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
             if (!to_q) proj_slots_kernarg_load(sp, ss, em, rows, tok_off);
@@ -569,24 +580,57 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
         }
     } else {
         proj_place_plan<ARG, MODEL>(pl, pos, em, etile * 16 + col, grp, rows, toks, pos_dev, tok_off,
-                                    pos_off, H, KVH, D);
+                                    pos_off, pd);
         proj_place_rope<MODEL>(pl, pos, rcos, rsin);
     }
     fl4 y = red[wave * 64 + lane];
     for (int w = 1; w < nwave; w++) y += red[w * rstride + wave * 64 + lane];
-    proj_store<MODEL>(pl, y, em, etile * 16 + col, grp, rows, H, KVH, D, q_out, q_out2, q_bf16, kpool,
+    proj_store<MODEL>(pl, y, em, etile * 16 + col, grp, rows, pd, q_out, q_out2, q_bf16, kpool,
                       vpool, P);
 }
 
-hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, const int *widths,
-                            int w_bf16, int K, uint16_t *out) {
-    PackSrc src{};
-    int N = 0;
-    for (int i = 0; i < 4; i++) {
-        src.m[i] = i < n_mats ? mats[i] : mats[0];
-        src.wd[i] = i < n_mats ? widths[i] : 0;
-        N += src.wd[i];
+// Zeros in the stored dims past the caller's of the appended rows (recycled
+// pages hold earlier tokens' bytes there): GQA K and V dims [D, DS) of
+// every kv head; MLA latent dims [DC, 512) and rope dims [512 + DR, 576).
+// Thread i of the launch takes element i of the flattened (row, dim) list.
+template <bool ARG>
+__global__ void proj_pad_zero_kernel(typename PlanSel<ARG>::T plan, const AppendTok *__restrict__ toks,
+                                     int tok_off, int rows, int model, const ProjDims pd,
+                                     uint16_t *__restrict__ kpool, uint16_t *__restrict__ vpool, int P) {
+    const int per = model == kProjGQA ? 2 * pd.KVH * (pd.DS - pd.D) : (kMlaDc - pd.DC) + (kMlaDr - pd.DR);
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (per <= 0 || i >= (int64_t)rows * per) return;
+    const int r = (int)(i / per), e = (int)(i - (int64_t)r * per);
+    const AppendTok tk = plan_tok<ARG>(toks, tok_off, r);
+    if (model == kProjGQA) {
+        const int pad = pd.DS - pd.D, kv = e / pad % pd.KVH, d = pd.D + e % pad;
+        if (e < pd.KVH * pad)
+            kpool[((int64_t)tk.page * pd.KVH + kv) * P * pd.DS + k_page_off(tk.slot, d, pd.DS)] = 0;
+        else
+            vpool[(((int64_t)tk.page * pd.KVH + kv) * pd.DS + d) * P + tk.slot] = 0;
+    } else {
+        const int d = e < kMlaDc - pd.DC ? pd.DC + e : kMlaDc + pd.DR + (e - (kMlaDc - pd.DC));
+        kpool[((int64_t)tk.page * P + tk.slot) * kMlaRow + d] = 0;
     }
+}
+
+hipError_t launch_proj_pad_zero(hipStream_t s, int model, const PlanArg *plan, const AppendTok *toks,
+                                int tok_off, int rows, const ProjDims &pd, uint16_t *kpool,
+                                uint16_t *vpool, int P) {
+    const int per = model == kProjGQA ? 2 * pd.KVH * (pd.DS - pd.D) : (kMlaDc - pd.DC) + (kMlaDr - pd.DR);
+    if (per <= 0 || rows <= 0) return hipSuccess;
+    const int64_t n = (int64_t)rows * per;
+    const dim3 g((unsigned)((n + 255) / 256));
+    if (plan)
+        proj_pad_zero_kernel<true><<<g, 256, 0, s>>>(*plan, toks, tok_off, rows, model, pd, kpool, vpool, P);
+    else
+        proj_pad_zero_kernel<false><<<g, 256, 0, s>>>(NoPlan{0}, toks, tok_off, rows, model, pd, kpool, vpool, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_proj(hipStream_t s, const PackSrc &src, int w_bf16, int K, uint16_t *out) {
+    int N = 0;
+    for (int i = 0; i < 4; i++) N += src.nh[i] * src.pw[i];
     pack_proj_kernel<<<dim3((N + 31) / 32, (K + 31) / 32), 256, 0, s>>>(src, w_bf16, K, N, out);
     return hipGetLastError();
 }
@@ -594,13 +638,12 @@ hipError_t launch_pack_proj(hipStream_t s, int n_mats, const void *const *mats, 
 hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patch *patches,
                        int n_patch, const AppendTok *toks, const int32_t *pos, int tok_off,
                        int pos_off, int rows, const void *x, int x_bf16, int K, const uint16_t *wp,
-                       int H, int KVH, int D, const float *rcos, const float *rsin, void *q_out,
+                       const ProjDims &pd, const float *rcos, const float *rsin, void *q_out,
                        void *q_out2, int q_bf16, uint16_t *kpool, uint16_t *vpool, int32_t *table,
                        int P, int cus, hipEvent_t e0, hipEvent_t e1) {
-    if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || D % 16 != 0) return hipErrorInvalidValue;
     // kProjOut: N = D (the output features), H and KVH unused.
-    const int N = model == kProjGQA ? (H + 2 * KVH) * D
-                                    : (model == kProjMLA ? H * (D + kMlaDr) + kMlaRow : D);
+    const int N = proj_features(model, pd);
+    if (rows <= 0 || rows > kProjMaxRows || K % 32 != 0 || N % 16 != 0) return hipErrorInvalidValue;
     // Decode-size calls: proj_skinny_kernel, when its operands fit 128
     // registers per lane (activations MT x 8 fragments, twice for f32;
     // weights TPW x 8).  TPW = 2 when one tile per work-group would take
@@ -621,7 +664,7 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
         const dim3 grid((NT + tpw - 1) / tpw), block(64 * nw);
 #define RLX_SK_LAUNCH(ARGV, XB, MODELV, MTV, TPWV, PLANV)                                              \
     return launch_timed(proj_skinny_kernel<ARGV, XB, MODELV, MTV, TPWV>, grid, block, s, e0, e1, PLANV, \
-                        patches, n_patch, toks, pos, tok_off, pos_off, rows, x, K, wp, NT, H, KVH, D,   \
+                        patches, n_patch, toks, pos, tok_off, pos_off, rows, x, K, wp, NT, pd,          \
                         rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, table, P)
 #define RLX_SK_SHAPE(ARGV, MODELV, PLANV)                                                              \
     if (!x_bf16) RLX_SK_LAUNCH(ARGV, false, MODELV, 1, 1, PLANV);                                      \
@@ -648,7 +691,7 @@ hipError_t launch_proj(hipStream_t s, int model, const PlanArg *plan, const Patc
 #define RLX_PROJ_LAUNCH(ARGV, XB, MODELV, PLANV)                                                  \
     return launch_timed(qkv_project_kernel<ARGV, XB, MODELV>, dim3(N / 16), dim3(64 * kProjWaves), \
                         s, e0, e1, PLANV, patches, n_patch, toks, pos, tok_off, pos_off, rows, x,  \
-                        x_bf16, K, wp, H, KVH, D, rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool, \
+                        x_bf16, K, wp, pd, rcos, rsin, q_out, q_out2, q_bf16, kpool, vpool,        \
                         table, P)
 #define RLX_PROJ_MODEL(MODELV)                                                                    \
     if (plan && x_bf16)                                                                           \

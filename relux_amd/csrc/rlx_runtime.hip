@@ -957,9 +957,11 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
     if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
     if (d_model <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0)
         return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
-    const void *mats[3] = {w_q, w_k, w_v};
-    const int wd[3] = {num_heads * head_dim, kv_heads * head_dim, kv_heads * head_dim};
-    HIP_TRY(launch_pack_proj(nullptr, 3, mats, wd, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
+    const PackSrc src{{w_q, w_k, w_v, w_q},
+                      {num_heads, kv_heads, kv_heads, 0},
+                      {head_dim, head_dim, head_dim, 0},
+                      {head_dim, head_dim, head_dim, 0}};
+    HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
     return RLX_OK;
 }
 
@@ -970,9 +972,8 @@ int32_t rlx_pack_out(const void *w, int32_t w_dtype, int32_t k_in, int32_t n_out
     if (k_in % 32 != 0 || n_out % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "rlx_pack_out: k_in %% 32 and n_out %% 16 must be 0 (k_in=%d n_out=%d)",
                     k_in, n_out);
-    const void *mats[1] = {w};
-    const int wd[1] = {n_out};
-    HIP_TRY(launch_pack_proj(nullptr, 1, mats, wd, w_dtype == RLX_BF16, k_in, (uint16_t *)out));
+    const PackSrc src{{w, w, w, w}, {1, 0, 0, 0}, {n_out, 0, 0, 0}, {n_out, 0, 0, 0}};
+    HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, k_in, (uint16_t *)out));
     return RLX_OK;
 }
 
@@ -994,9 +995,11 @@ int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, i
         const int n = std::min(kProjRows, rows - r0);
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
+        ProjDims pd{};
+        pd.D = n_out;
         HIP_TRY(launch_proj(c->stream, kProjModelOut, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, n,
                             (const char *)x + (size_t)r0 * k_in * xb, x_dtype == RLX_BF16, k_in,
-                            (const uint16_t *)w_packed, 0, 0, n_out, nullptr, nullptr,
+                            (const uint16_t *)w_packed, pd, nullptr, nullptr,
                             (char *)out + (size_t)r0 * n_out * ob,
                             residual ? (void *)((const char *)residual + (size_t)r0 * n_out * ob) : nullptr,
                             out_dtype == RLX_BF16, nullptr, nullptr, nullptr, 0, c->cus, e0, e1));
@@ -1006,14 +1009,17 @@ int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, i
 
 int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
                           int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,
-                          void *out) {
+                          int32_t d_c, int32_t d_r, void *out) {
     if (!w_q || !w_qr || !w_dkv || !w_kr || !out) return fail(RLX_ERR_INVALID, "null weight pointer");
     if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
-    if (d_model <= 0 || num_heads <= 0 || head_dim <= 0)
-        return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
-    const void *mats[4] = {w_q, w_qr, w_dkv, w_kr};
-    const int wd[4] = {num_heads * head_dim, num_heads * kMlaDr, kMlaDc, kMlaDr};
-    HIP_TRY(launch_pack_proj(nullptr, 4, mats, wd, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
+    if (d_model <= 0 || num_heads <= 0 || head_dim <= 0 || d_c <= 0 || d_r <= 0)
+        return fail(RLX_ERR_INVALID, "d_model, heads, head_dim, d_c and d_r must be > 0");
+    const int drp = (d_r + 15) & ~15, dcp = (d_c + 15) & ~15;
+    const PackSrc src{{w_q, w_qr, w_dkv, w_kr},
+                      {num_heads, num_heads, 1, 1},
+                      {head_dim, d_r, d_c, d_r},
+                      {head_dim, drp, dcp, drp}};
+    HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
     return RLX_OK;
 }
 
@@ -1024,9 +1030,9 @@ namespace {
 // Shared body of the fused projection + RoPE + append entry points.
 int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                        const int32_t *n_tok, const void *x, int32_t x_dtype, int32_t d_model,
-                       const void *w_packed, int32_t num_heads, int32_t head_dim,
-                       const float *rope_cos, const float *rope_sin, int32_t rope_rows,
-                       int32_t rope_mode, void *q_out, void *q_out2, int32_t q_dtype) {
+                       const void *w_packed, const ProjDims &pd, const float *rope_cos,
+                       const float *rope_sin, int32_t rope_rows, int32_t rope_mode, void *q_out,
+                       void *q_out2, int32_t q_dtype) {
     int32_t rc = check_layer(c, layer, false);
     if (rc) return rc;
     if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
@@ -1086,14 +1092,16 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
             d_t = (const AppendTok *)((char *)dev + toff);
             d_pos = (const int32_t *)((char *)dev + poff);
         }
+        // zeros in the stored dims past the caller's (none at the stored shapes)
+        HIP_TRY(launch_proj_pad_zero(c->stream, model, plan, d_t, (int)toff, rows, pd, ls.pool0, ls.pool1,
+                                     c->P));
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
-        char *q2 = model == kProjModelMLA ? (char *)q_out2 + (size_t)r0 * num_heads * kMlaDr * qb : nullptr;
+        char *q2 = model == kProjModelMLA ? (char *)q_out2 + (size_t)r0 * pd.H * pd.DR * qb : nullptr;
         HIP_TRY(launch_proj(c->stream, model, plan, d_p, (int)pt.size(), d_t, d_pos, (int)toff,
                             (int)poff, rows, (const char *)x + (size_t)r0 * d_model * xb,
-                            x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed, num_heads,
-                            c->kvh, head_dim, rope_cos, rope_sin,
-                            (char *)q_out + (size_t)r0 * num_heads * head_dim * qb, q2,
+                            x_dtype == RLX_BF16, d_model, (const uint16_t *)w_packed, pd, rope_cos,
+                            rope_sin, (char *)q_out + (size_t)r0 * pd.H * pd.D * qb, q2,
                             q_dtype == RLX_BF16, ls.pool0, ls.pool1, c->d_table, c->P, c->cus, e0, e1));
     }
     return RLX_OK;
@@ -1111,14 +1119,22 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
-    if (c->hd != c->hdi)
-        return fail(RLX_ERR_UNSUPPORTED, "rlx_gqa_project_append: head_dim %d is stored padded to %d",
-                    c->hdi, c->hd);
     if (num_heads <= 0 || num_heads % c->kvh != 0)
         return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
+    // The packed features come in 16-feature tiles, each within one of the
+    // q / k / v parts.
+    if ((num_heads * c->hdi) % 16 != 0 || (c->kvh * c->hdi) % 16 != 0)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_project_append: heads x head_dim must be multiples of 16 (%d x %d, %d x %d)",
+                    num_heads, c->hdi, c->kvh, c->hdi);
+    ProjDims pd{};
+    pd.H = num_heads;
+    pd.KVH = c->kvh;
+    pd.D = c->hdi;
+    pd.DS = c->hd;
     return project_append(c, kProjModelGQA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
-                          w_packed, num_heads, c->hd, rope_cos, rope_sin, rope_rows, rope_mode,
-                          q_out, nullptr, q_dtype);
+                          w_packed, pd, rope_cos, rope_sin, rope_rows, rope_mode, q_out, nullptr,
+                          q_dtype);
 }
 
 int32_t rlx_mla_project_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
@@ -1130,15 +1146,19 @@ int32_t rlx_mla_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_project_append on a GQA cache");
-    if (c->dc != kMlaDc || c->dr != kMlaDr)
-        return fail(RLX_ERR_UNSUPPORTED, "rlx_mla_project_append takes d_c %d and d_r %d (cache: %d, %d)",
-                    kMlaDc, kMlaDr, c->dc, c->dr);
     if (num_heads <= 0 || head_dim <= 0 || head_dim % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim a multiple of 16)",
                     num_heads, head_dim);
+    ProjDims pd{};
+    pd.H = num_heads;
+    pd.D = head_dim;
+    pd.DR = c->dr;
+    pd.DRP = (c->dr + 15) & ~15;
+    pd.DC = c->dc;
+    pd.DCP = (c->dc + 15) & ~15;
     return project_append(c, kProjModelMLA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
-                          w_packed, num_heads, head_dim, rope_cos, rope_sin, rope_rows, rope_mode,
-                          q_nope_out, q_rope_out, q_dtype);
+                          w_packed, pd, rope_cos, rope_sin, rope_rows, rope_mode, q_nope_out,
+                          q_rope_out, q_dtype);
 }
 
 int32_t rlx_mla_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,

@@ -54,6 +54,10 @@ def _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, positions):
     # 20 rows (two row tiles) at d_model 256 (one wave per work-group): the
     # chunked kernel
     (256, 8, 2, 64, [3] * 20, [1] * 20, torch.bfloat16, "offset"),
+    # head_dim 80 stored in 96-dim pages (the new rows' padding is zeroed),
+    # decode-size and chunked kernels
+    (512, 8, 2, 80, [7, 30], [1, 1], torch.bfloat16, "offset"),
+    (256, 4, 2, 80, [0, 12], [40, 30], torch.float32, "offset"),
 ])
 def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dtype, mode):
     from relux_amd import KVCache, pack_qkv, rope_tables
@@ -234,23 +238,28 @@ def test_cfg1_generate_with_fused_step(gpu):
     assert m.cache.TotalLen(0) == len(toks) - 1
 
 
-@pytest.mark.parametrize("d_model,H,D,lens,ntok,mode,x_dtype", [
-    (256, 4, 128, [0, 70], [5, 2], "offset", torch.float32),
-    (512, 16, 128, [9], [66], "offset", torch.float32),     # > 64 rows: two launches
-    (128, 2, 64, [3, 0], [3, 4], "ref", torch.float32),
-    (2048, 16, 128, [20] * 32, [1] * 32, "offset", torch.bfloat16),  # config 3's decode rows
-    (512, 16, 128, [9], [66], "offset", torch.bfloat16),
-    (4096, 8, 128, [12] * 16, [1] * 16, "offset", torch.bfloat16),   # decode-size kernel, 16 waves
-    (4096, 8, 128, [12] * 20, [1] * 20, "offset", torch.bfloat16),   # 2 row tiles at 16 waves: chunked
+@pytest.mark.parametrize("d_model,H,D,lens,ntok,mode,x_dtype,dC,dR", [
+    (256, 4, 128, [0, 70], [5, 2], "offset", torch.float32, 512, 64),
+    (512, 16, 128, [9], [66], "offset", torch.float32, 512, 64),     # > 64 rows: two launches
+    (128, 2, 64, [3, 0], [3, 4], "ref", torch.float32, 512, 64),
+    (2048, 16, 128, [20] * 32, [1] * 32, "offset", torch.bfloat16, 512, 64),  # config 3's decode rows
+    (512, 16, 128, [9], [66], "offset", torch.bfloat16, 512, 64),
+    (4096, 8, 128, [12] * 16, [1] * 16, "offset", torch.bfloat16, 512, 64),   # decode-size kernel, 16 waves
+    (4096, 8, 128, [12] * 20, [1] * 20, "offset", torch.bfloat16, 512, 64),   # 2 row tiles at 16 waves: chunked
+    # the reference's default latent dims (dC = 4 headDim, dHR = headDim/2,
+    # transformer.go:223-233): packed widths rounded up to 16, zero padded
+    (512, 8, 32, [5, 40], [1, 1], "offset", torch.bfloat16, 128, 16),
+    (256, 4, 64, [0, 20], [9, 3], "offset", torch.float32, 256, 32),
+    (256, 4, 16, [3, 0], [2, 5], "ref", torch.float32, 64, 8),      # config-1-sized MLA layer
 ])
-def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode, x_dtype):
+def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode, x_dtype, dC, dR):
     """mla.go:279-314: q_c = x.W_Q, q_r = RoPE(x.W_QR), c = x.W_DKV,
     k^R = RoPE(x.W_KR) appended as latent rows."""
     from relux_amd import MLACache, pack_mla_proj, rope_tables
-    rng = np.random.default_rng(7 + d_model + H)
-    S, dC, dR = len(lens), 512, 64
+    rng = np.random.default_rng(7 + d_model + H + dC)
+    S = len(lens)
     max_seq = 256
-    c = MLACache(num_layers=1, max_len=max_seq, max_seqs=S, device=gpu.index)
+    c = MLACache(num_layers=1, max_len=max_seq, d_c=dC, d_r=dR, max_seqs=S, device=gpu.index)
     mats = [oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, w)).astype(np.float32))
             for w in (H * D, H * dR, dC, dR)]
     wp = pack_mla_proj(*[_bf16_tensor(m, gpu) for m in mats], H, D)
