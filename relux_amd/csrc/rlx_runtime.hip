@@ -1279,6 +1279,14 @@ int32_t check_gqa_attend(Cache *c, int32_t layer, int32_t n_seqs, const int32_t 
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
     return RLX_OK;
 }
+// Whether GQA calls with more query rows per kv head than the decode kernel
+// holds run as FA2 chunked prefill: stored head dims 64, 128 and 256 (any
+// caller head_dim they hold) with G = heads per kv head dividing 256; other
+// shapes tile their queries through the decode kernel.
+bool gqa_use_fa2(const Cache *c, int G) {
+    return (c->hd == 64 || c->hd == 128 || c->hd == 256) && kPrefillRows % G == 0;
+}
+
 // GQA attention after the argument checks.
 int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                         const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
@@ -1294,11 +1302,9 @@ int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *
         max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     }
     const int max_qr = G * max_nq;
-    // The FA2 prefill kernel covers stored head dims 64, 128 and 256 (any
-    // caller head_dim they hold) with G dividing 256; other shapes tile their
-    // queries through the decode kernel, whose work-group holds at most cap
-    // query rows of one kv head.
-    const bool fa2 = (c->hd == 64 || c->hd == 128 || c->hd == 256) && kPrefillRows % G == 0;
+    // Query rows past cap (the decode kernel's per kv head) take FA2 or query
+    // tiles (gqa_use_fa2).
+    const bool fa2 = gqa_use_fa2(c, G);
     const int cap = gqa_rows_cap(c);
     if (max_qr > cap && !fa2 && G > cap)
         return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", G,
@@ -1455,7 +1461,7 @@ int32_t rlx_gqa_append_attend(void *h, int32_t layer, int32_t n_seqs, const int3
         int mx = 0;
         for (int i = 0; i < n_seqs; i++) mx = std::max(mx, n_tok[i]);
         const int Gq = num_heads / c->kvh, cap = gqa_rows_cap(c);
-        const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % Gq == 0;
+        const bool fa2 = gqa_use_fa2(c, Gq);
         if (Gq * mx > cap && !fa2 && Gq > cap)
             return fail(RLX_ERR_UNSUPPORTED, "heads per kv head = %d with head_dim %d (at most %d)", Gq,
                         c->hdi, cap);
@@ -1590,7 +1596,7 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     for (int i = 0; i < n_seqs; i++) max_nq = std::max(max_nq, n_q ? n_q[i] : 1);
     const int max_qr = G * max_nq;
     // Decode and verify calls only: the FA2 path's work lists are staged.
-    const bool fa2 = c->hd == c->hdi && (c->hd == 64 || c->hd == 128) && kPrefillRows % G == 0;
+    const bool fa2 = gqa_use_fa2(c, G);
     const int cap = gqa_rows_cap(c);
     if (max_qr > cap && (fa2 || G > cap))
         return fail(RLX_ERR_UNSUPPORTED,
