@@ -343,6 +343,13 @@ struct SampleArgs {
     int window;                // repeat_window; <= 0: the whole history
     const float *u;            // one draw per row
     int32_t *out;
+    // vocabulary split (nch > 0, set by plan_sample_split): row b's chunk c
+    // covers entries [c * pch, min(V, (c + 1) * pch)) and leaves its top-k
+    // candidates at part_v / part_i[(b * nch + c) * pcap ..] with their
+    // count (-1: overflow) at part_n[b * nch + c]
+    int nch, pch, pcap;
+    float *part_v;
+    int32_t *part_i, *part_n;
 };
 
 struct SpecArgs {
@@ -356,6 +363,17 @@ struct SpecArgs {
     int top_k;
     float top_p, min_p;
     int32_t *n_acc, *next;
+    // per (row, position, side) figures (set by plan_spec_split):
+    // rec[((b * max_k + i) * 2 + side) * 4 + {0, 1, 2}]: the row's max, its
+    // fastexp32 sum, the draft token's probability (side 0 draft, 1 target);
+    // st_mass[(b * sch + c) * 2 + {0, 1}]: the first rejection's chunk c
+    // sums of max(0, p_t - p_d) and of p_t
+    float *rec, *st_mass;
+    int sch;
+    // the next target row's top-k chunk lists, as SampleArgs
+    int nch, pch, pcap;
+    float *part_v;
+    int32_t *part_i, *part_n;
 };
 
 // (e0, e1: optional timing events attached to the kernel's dispatch.)
@@ -365,6 +383,12 @@ hipError_t launch_greedy(hipStream_t s, const float *logits, int64_t stride, int
                          int32_t *out, hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 hipError_t launch_spec_accept(hipStream_t s, const SpecArgs &a, int n_rows,
                               hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// Chunking and device scratch of the split token selection, from the
+// arguments' vocabulary and sampler: returns the scratch bytes the call
+// needs and, with `base` non-null, points the arguments into it (base: 256-B
+// aligned).  Fails (-1) when a launch would exceed the grid's limits.
+int64_t plan_sample_split(SampleArgs &a, int n_rows, char *base);
+int64_t plan_spec_split(SpecArgs &a, int n_rows, char *base);
 
 // ---- launchers (stream-ordered, return hipError_t of the launch) ----------
 hipError_t launch_patch(hipStream_t s, int32_t *table, const Patch *p, int n);

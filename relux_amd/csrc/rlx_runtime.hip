@@ -2436,11 +2436,15 @@ int32_t rlx_sample(void *h, const float *logits, int32_t n_rows, int32_t vocab, 
         o_o = b.add(so);
     }
     void *dev;
-    int32_t rc = ensure_ws(c, (size_t)n_rows * 4);
+    SampleArgs a{};
+    a.V = vocab;
+    a.top_k = p->top_k;
+    const size_t o_split = ((size_t)n_rows * 4 + 255) & ~(size_t)255;
+    int32_t rc = ensure_ws(c, o_split + (size_t)plan_sample_split(a, n_rows, nullptr));
     if (rc) return rc;
+    plan_sample_split(a, n_rows, (char *)c->ws + o_split);
     if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
     char *d = (char *)dev;
-    SampleArgs a{};
     a.logits = logits;
     a.stride = row_stride;
     a.V = vocab;
@@ -2509,9 +2513,11 @@ int32_t rlx_sample_async(void *h, const float *logits, int32_t n_rows, int32_t v
     a.window = p->repeat_window;
     a.u = uniforms;
     a.out = out_tokens;
-    hipEvent_t e0, e1;
-    int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
+    int32_t rc = ensure_ws(c, (size_t)plan_sample_split(a, n_rows, nullptr));
     if (rc) return rc;
+    plan_sample_split(a, n_rows, (char *)c->ws);
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
     HIP_TRY(launch_sample(c->stream, a, n_rows, e0, e1));
     return RLX_OK;
 }
@@ -2543,9 +2549,15 @@ int32_t rlx_spec_accept_async(void *h, const float *draft_logits, const float *t
     a.min_p = p->min_p;
     a.n_acc = n_accepted;
     a.next = next_token;
-    hipEvent_t e0, e1;
-    int32_t rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT);
+    const int64_t ws_bytes = plan_spec_split(a, n_rows, nullptr);
+    if (ws_bytes < 0)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_spec_accept_async: max_k=%d at vocab %d exceeds the grid", max_k,
+                    vocab);
+    int32_t rc = ensure_ws(c, (size_t)ws_bytes);
     if (rc) return rc;
+    plan_spec_split(a, n_rows, (char *)c->ws);
+    hipEvent_t e0, e1;
+    if ((rc = timing_events(c, &e0, &e1, RLX_TIME_SELECT))) return rc;
     HIP_TRY(launch_spec_accept(c->stream, a, n_rows, e0, e1));
     return RLX_OK;
 }
@@ -2578,11 +2590,19 @@ int32_t rlx_spec_accept(void *h, const float *draft_logits, const float *target_
     const size_t o_n = bl.add(std::vector<int32_t>(n_draft, n_draft + n_rows));
     const size_t o_u = bl.add(std::vector<float>(uniforms, uniforms + (size_t)n_rows * (max_k + 1)));
     void *dev;
-    int32_t rc = ensure_ws(c, (size_t)n_rows * 8);
+    SpecArgs a{};
+    a.max_k = max_k;
+    a.V = vocab;
+    a.top_k = p->top_k;
+    const size_t o_split = ((size_t)n_rows * 8 + 255) & ~(size_t)255;
+    const int64_t split_bytes = plan_spec_split(a, n_rows, nullptr);
+    if (split_bytes < 0)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_spec_accept: max_k=%d at vocab %d exceeds the grid", max_k, vocab);
+    int32_t rc = ensure_ws(c, o_split + (size_t)split_bytes);
     if (rc) return rc;
+    plan_spec_split(a, n_rows, (char *)c->ws + o_split);
     if ((rc = stage(c, bl.bytes.data(), bl.bytes.size(), &dev))) return rc;
     char *d = (char *)dev;
-    SpecArgs a{};
     a.d_logits = draft_logits;
     a.t_logits = target_logits;
     a.d_tok = (const int32_t *)(d + o_d);

@@ -130,7 +130,8 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, RLX_DPP(v, 0x143, 0xC, -INFINITY));
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
-__device__ __forceinline__ void blk_sum2(float &a, float &b, SampLds &s) {
+template <class L>
+__device__ __forceinline__ void blk_sum2(float &a, float &b, L &s) {
     a = wave_sum_dpp(a);
     b = wave_sum_dpp(b);
     __syncthreads();
@@ -147,7 +148,8 @@ __device__ __forceinline__ void blk_sum2(float &a, float &b, SampLds &s) {
         b += s.red[1][w];
     }
 }
-__device__ __forceinline__ void blk_max2(float &a, float &b, SampLds &s) {
+template <class L>
+__device__ __forceinline__ void blk_max2(float &a, float &b, L &s) {
     a = wave_max_dpp(a);
     b = wave_max_dpp(b);
     __syncthreads();
@@ -164,12 +166,14 @@ __device__ __forceinline__ void blk_max2(float &a, float &b, SampLds &s) {
         b = fmaxf(b, s.red[1][w]);
     }
 }
-__device__ __forceinline__ float blk_sum(float v, SampLds &s) {
+template <class L>
+__device__ __forceinline__ float blk_sum(float v, L &s) {
     float z = 0.f;
     blk_sum2(v, z, s);
     return v;
 }
-__device__ __forceinline__ float blk_max(float v, SampLds &s) {
+template <class L>
+__device__ __forceinline__ float blk_max(float v, L &s) {
     float z = -INFINITY;
     blk_max2(v, z, s);
     return v;
@@ -194,7 +198,8 @@ __device__ __forceinline__ int wave_iscan_dpp(int v) {
     v += RLX_DPPI(v, 0x143, 0xC);
     return v;
 }
-__device__ __forceinline__ float blk_scan_excl(float v, SampLds &s, float *total) {
+template <class L>
+__device__ __forceinline__ float blk_scan_excl(float v, L &s, float *total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const float inc = wave_scan_dpp(v);
     const float exc = RLX_DPP(inc, 0x138, 0xF, 0.f);  // wave_shr:1, lane 0 gets 0
@@ -209,7 +214,8 @@ __device__ __forceinline__ float blk_scan_excl(float v, SampLds &s, float *total
     *total = tot;
     return base + exc;
 }
-__device__ __forceinline__ int blk_iscan_excl(int v, SampLds &s, int *total) {
+template <class L>
+__device__ __forceinline__ int blk_iscan_excl(int v, L &s, int *total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int inc = wave_iscan_dpp(v);
     __syncthreads();
@@ -224,7 +230,8 @@ __device__ __forceinline__ int blk_iscan_excl(int v, SampLds &s, int *total) {
     *total = tot;
     return base + inc - v;
 }
-__device__ __forceinline__ int blk_isum(int v, SampLds &s) {
+template <class L>
+__device__ __forceinline__ int blk_isum(int v, L &s) {
     int t;
     blk_iscan_excl(v, s, &t);
     return t;
@@ -332,8 +339,8 @@ __device__ __forceinline__ void with_groups(int n, F f) {
 
 // With lo_bit > 0 only the key bits above lo_bit are searched: the result
 // is then a lower bound of the k-th largest key (its low bits zero).
-template <class K>
-__device__ uint32_t kth_key_w0(int n, int k, SampLds &s, K key, int lo_bit = 0) {
+template <class L, class K>
+__device__ uint32_t kth_key_w0(int n, int k, L &s, K key, int lo_bit = 0) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
         with_groups<kCandCap / 64>(n, [&](auto gc) {
@@ -358,8 +365,8 @@ __device__ uint32_t kth_key_w0(int n, int k, SampLds &s, K key, int lo_bit = 0) 
     return r;
 }
 // The same over the whole working set with every thread (n entries).
-template <class K>
-__device__ uint32_t kth_key_blk(int n, int k, SampLds &s, K key) {
+template <class L, class K>
+__device__ uint32_t kth_key_blk(int n, int k, L &s, K key) {
     uint32_t res = 0;
     for (int bit = 31; bit >= 0; bit--) {
         const uint32_t cand = res | (1u << bit);
@@ -375,8 +382,8 @@ __device__ uint32_t kth_key_blk(int n, int k, SampLds &s, K key) {
 // it exceeds kCandCap.  64-entry tiles: a ballot per tile, an ordered scan
 // of the tile counts, then each kept entry's slot is its tile's offset plus
 // the kept lanes below it.
-template <class P, class Vf, class If>
-__device__ int compact_blk(int n, int *tc, SampLds &s, P keep, Vf val, If idx) {
+template <class L, class P, class Vf, class If>
+__device__ int compact_blk(int n, int *tc, L &s, P keep, Vf val, If idx) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int T = (n + 63) / 64;
 #pragma unroll 8
@@ -420,8 +427,8 @@ __device__ int compact_blk(int n, int *tc, SampLds &s, P keep, Vf val, If idx) {
 // its first slot.  One pass over the entries; index order is kept.  (With C
 // odd the lanes of a wave read distinct banks; C = 64, a 32768 row, reads
 // one bank per step.)
-template <class P, class Vf>
-__device__ int compact_chunks(int n, SampLds &s, P keep, Vf val) {
+template <class L, class P, class Vf>
+__device__ int compact_chunks(int n, L &s, P keep, Vf val) {
     const int tid = threadIdx.x;
     const int C = (n + kST - 1) / kST;
     const int i0 = tid * C;
@@ -446,8 +453,8 @@ __device__ int compact_chunks(int n, SampLds &s, P keep, Vf val) {
 
 // Filter the candidate list in place, in order (wave 0, one 64-entry tile
 // after another: a tile is read before any slot at or below it is written).
-template <class P>
-__device__ int filter_w0(int n, SampLds &s, P keep) {
+template <class L, class P>
+__device__ int filter_w0(int n, L &s, P keep) {
     const int lane = threadIdx.x & 63;
     if (threadIdx.x < 64) {
         int out = 0;
@@ -472,21 +479,20 @@ __device__ int filter_w0(int n, SampLds &s, P keep) {
     return r;
 }
 
-// First entry (in order) at which the running sum of w exceeds r, mapped
-// through idx; `dflt` when none does.  Chunk sums per thread (contiguous
-// chunks), an ordered exclusive scan, then only the thread whose chunk
-// holds r walks it; should rounding leave that walk without a hit, every
-// later chunk is walked.
-template <class W, class I>
-__device__ int samp_draw(int n, float r, int dflt, SampLds &s, W w, I idx) {
+// First entry (in order) at which the running sum of w, started at `base`,
+// exceeds r, or -1 when none does; *tot: the sum of the n weights.  Chunk
+// sums per thread (contiguous chunks), an ordered exclusive scan, then only
+// the thread whose chunk holds r walks it; should rounding leave that walk
+// without a hit, every later chunk is walked.
+template <class L, class W>
+__device__ int samp_draw_from(int n, float r, float base, L &s, W w, float *tot) {
     const int tid = threadIdx.x;
     const int C = (n + kST - 1) / kST;
     const int i0 = min(n, tid * C), i1 = min(n, i0 + C);
     float cs = 0.f;
 #pragma unroll 8
     for (int i = i0; i < i1; i++) cs += w(i);
-    float tot;
-    const float start = blk_scan_excl(cs, s, &tot);
+    const float start = base + blk_scan_excl(cs, s, tot);
     if (tid == 0) s.best = INT_MAX;
     __syncthreads();
     auto walk = [&]() {
@@ -506,7 +512,16 @@ __device__ int samp_draw(int n, float r, int dflt, SampLds &s, W w, I idx) {
         __syncthreads();
     }
     const int b = s.best;
-    return b == INT_MAX ? dflt : idx(b);
+    __syncthreads();
+    return b == INT_MAX ? -1 : b;
+}
+// The same over a whole set: the hit mapped through idx, `dflt` when r is
+// never reached.
+template <class L, class W, class I>
+__device__ int samp_draw(int n, float r, int dflt, L &s, W w, I idx) {
+    float tot;
+    const int b = samp_draw_from(n, r, 0.f, s, w, &tot);
+    return b < 0 ? dflt : idx(b);
 }
 
 // ---- Sampler.Sample ---------------------------------------------------------
@@ -688,6 +703,15 @@ __device__ __forceinline__ int sample_set(Src &c, int top_k, float top_p, float 
     return sample_finish<2>(c, top_p, min_p, r, s);
 }
 
+// Penalties of a window token seen f times (sampler.go:213-262): repeat
+// (divide a positive logit, multiply a negative one), frequency, presence.
+__device__ __forceinline__ float pen_value(float x, int f, float rp, float fp, float pp) {
+    if (rp != 1.f && rp != 0.f) x = (x > 0.f) ? __fdiv_rn(x, rp) : __fmul_rn(x, rp);
+    if (fp != 0.f) x = __fsub_rn(x, __fmul_rn(fp, (float)f));
+    if (pp != 0.f) x = __fsub_rn(x, pp);
+    return x;
+}
+
 // Bring a row into the working set: LDS values (penalties applied in place,
 // then divided by the temperature) when it fits, else memory reads with the
 // penalised tokens in an LDS bitmap and list.  seen(i) / freq(i): the row's
@@ -706,12 +730,7 @@ __device__ __forceinline__ void load_row(Src &c, SampLds &s, const float *row, i
     c.div = (t != 1.f);
     c.topk = c.topp = c.minp = false;
     c.n1 = c.n2 = c.n3 = false;
-    auto pen = [&](float x, int f) {
-        if (rp != 1.f && rp != 0.f) x = (x > 0.f) ? __fdiv_rn(x, rp) : __fmul_rn(x, rp);
-        if (fp != 0.f) x = __fsub_rn(x, __fmul_rn(fp, (float)f));
-        if (pp != 0.f) x = __fsub_rn(x, pp);
-        return x;
-    };
+    auto pen = [&](float x, int f) { return pen_value(x, f, rp, fp, pp); };
     if (V <= kRowCap) {
         // scratch value = pen(x) / temperature (sampler.go:80-97), the
         // division applied as the row is stored; the penalised entries are
@@ -828,10 +847,519 @@ __device__ __forceinline__ int count_window(const SampleArgs &a, int b, SampLds 
     return nd;
 }
 
+// ---- the vocabulary split ----------------------------------------------------
+// One work-group per row leaves most of the chip idle for a decode batch, so
+// rows are cut into vocabulary chunks of at most kPartChunk entries, one
+// work-group each.  For top-k sampling a chunk keeps its own candidates: the
+// entries at or above its k-th largest value.  The row's k-th largest is at
+// least any chunk's (that chunk holds k entries at or above its own), so
+// every entry the row keeps is among them, and the k-th largest of the
+// merged lists is the row's.  The row's work-group merges the lists in
+// chunk order, which is index order, and continues at Sample's
+// candidate-list stage (the exact k-th largest, softmax, top-p, min-p, the
+// draw), as a whole-row work-group does after its own compaction.  A chunk
+// list past its slots (ties) or a merge past kCandCap sends the row down the
+// whole-row path instead.
+constexpr int kPartChunk = 8192;  // entries of a top-k chunk
+constexpr int kPartMaxK = 256;    // largest top-k the split serves
+constexpr int kRegRow = 16;       // float4 rounds a thread holds: rows of up to 32768 entries
+
+struct PartLds {
+    float red[2][kSW];
+    int cnt[kST];
+    uint32_t key[kST];
+    int sel_i[2];
+    float sel_f;
+    int best;
+    union {
+        struct {
+            float cv[kCandCap];
+            int ci[kCandCap];
+        };
+        // one 16-bit slot per chunk entry until the penalties are applied:
+        // its window count, or its position + 1 in a host-counted list
+        uint32_t pcw[kPartChunk / 2];
+    };
+};
+static_assert(kPartChunk / 2 <= 2 * kCandCap, "window slots alias the candidate arrays");
+static_assert(kSampMaxSeen < (1 << 16), "a window count or list position fits 16 bits");
+static_assert(kRegRow * kSW <= 128, "reg_topk scans the tile totals 2 per lane of a wave");
+
+struct RedLds {
+    float red[2][kSW];
+};
+
+// ---- rows held in registers ---------------------------------------------------
+// Entry e of a segment [0, n) sits in thread (e / 4) % kST, float4 round
+// e / (4 kST), component e % 4 (x[4 round + component]): the loads
+// coalesce, and (round, thread, component) is index order.  Entries past n
+// read as -inf.
+template <int R>
+__device__ __forceinline__ void reg_load(const float *src, int n, float (&x)[4 * R]) {
+    const int tid = threadIdx.x;
+    const bool vec = (((uintptr_t)src) & 15) == 0;
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const int e = 4 * (tid + kST * j);
+        if (vec && e + 3 < n) {
+            const float4 v = *(const float4 *)(src + e);
+            x[4 * j] = v.x;
+            x[4 * j + 1] = v.y;
+            x[4 * j + 2] = v.z;
+            x[4 * j + 3] = v.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; q++) x[4 * j + q] = (e + q < n) ? src[e + q] : -INFINITY;
+        }
+    }
+}
+__device__ __forceinline__ int reg_idx(int j, int q) { return 4 * ((int)threadIdx.x + kST * j) + q; }
+
+// Calls f(std::integral_constant<int, R>) with the fewest float4 rounds R
+// (2, 4, 8 or 16) that hold n <= 4 kST kRegRow entries.
+template <class F>
+__device__ __forceinline__ void with_rounds(int n, F f) {
+    if (n <= 8 * kST) f(std::integral_constant<int, 2>{});
+    else if (n <= 16 * kST) f(std::integral_constant<int, 4>{});
+    else if (n <= 32 * kST) f(std::integral_constant<int, 8>{});
+    else f(std::integral_constant<int, kRegRow>{});
+}
+
+// A row's window tokens for the penalties (sampler.go:213-262), loaded with
+// the chunk's logits: rlx_sample_async's device history (the last `window`
+// ids of the row's history; the caller bounds it by kSampMaxSeen) or
+// rlx_sample's host-counted distinct tokens.  ids[r] is entry tid + kST r,
+// -1 past the end.
+struct WinIds {
+    int ids[kSampMaxSeen / kST];
+    int n0;  // host lists: the row's first list position
+};
+__device__ __forceinline__ void win_load(const SampleArgs &a, int b, WinIds &w) {
+    const int tid = threadIdx.x;
+    int nw = 0;
+    const int32_t *h = nullptr;
+    w.n0 = 0;
+    if (a.hist) {
+        const int hn = (int)max((int64_t)0, min((int64_t)a.hist_len[b], a.hist_stride));
+        const int h0 = (a.window > 0 && hn > a.window) ? hn - a.window : 0;
+        nw = hn - h0;
+        h = a.hist + (int64_t)b * a.hist_stride + h0;
+    } else if (a.seen_off) {
+        w.n0 = a.seen_off[b];
+        nw = a.seen_off[b + 1] - w.n0;
+        h = a.seen_tok + w.n0;
+    }
+#pragma unroll
+    for (int r = 0; r < kSampMaxSeen / kST; r++) {
+        const int i = tid + kST * r;
+        w.ids[r] = i < nw ? h[i] : -1;
+    }
+}
+
+// The penalties applied to the chunk's raw logits in registers: each window
+// token in [lo, lo + n) marks its entry's 16-bit LDS slot -- with its
+// occurrence count (device history; ids outside [0, V) fall in no chunk) or
+// its list position + 1 (host lists, whose counts are read back).
+template <int R>
+__device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds &w, int lo, int n,
+                                              float (&x)[4 * R], PartLds &s) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < (n + 1) >> 1; i += kST) s.pcw[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kSampMaxSeen / kST; r++) {
+        const int id = w.ids[r];
+        if (id >= lo && id < lo + n) {
+            const uint32_t sh = 16 * ((id - lo) & 1);
+            if (a.hist)
+                atomicAdd(&s.pcw[(id - lo) >> 1], 1u << sh);
+            else
+                atomicOr(&s.pcw[(id - lo) >> 1], (uint32_t)(tid + kST * r + 1) << sh);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const int e = reg_idx(j, 0);
+        if (e >= n) continue;
+        const uint2 v = *(const uint2 *)&s.pcw[e >> 1];  // the round's 4 slots
+        const uint32_t sl[4] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16};
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (sl[q] != 0u && e + q < n) {
+                const int f = a.hist ? (int)sl[q] : a.seen_freq[w.n0 + (int)sl[q] - 1];
+                x[4 * j + q] = pen_value(x[4 * j + q], f, a.rp, a.fp, a.pp);
+            }
+    }
+    __syncthreads();  // the slots alias the candidate list
+}
+
+// Top-k candidates of n register-held values (0 < k), in index order, into
+// s.cv / s.ci (indices relative to the segment): the entries at or above a
+// lower bound of their k-th largest, or, when those pass cap, the entries
+// at or above the exact k-th largest; returns their count, -1 when the
+// first compaction passes kCandCap.
+//   1. lower bound: each wave's ceil(k / kSW)-th largest lane maximum, to 16
+//      key bits; the smallest over the waves (every wave holds that many
+//      entries at or above it: kSW ceil(k / kSW) >= k in all);
+//   2. the entries at or above it compacted in index order: per (round,
+//      wave) tile a ballot-free lane scan, then an ordered scan of the tile
+//      totals;
+//   3. past cap only: the exact k-th largest of that list (wave 0, one key
+//      bit per step) and the list filtered to it.
+template <int R>
+__device__ __forceinline__ int reg_topk(const float (&x)[4 * R], int n, int k, int cap, PartLds &s) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t mk = 0;
+#pragma unroll
+    for (int j = 0; j < 4 * R; j++)
+        if (reg_idx(j >> 2, j & 3) < n) mk = max(mk, fkey(x[j]));
+    const int kw = (k + kSW - 1) / kSW;
+    uint32_t lbw = 0;
+    for (int bit = 31; bit >= 16; bit--) {
+        const uint32_t cand = lbw | (1u << bit);
+        if ((int)__popcll(__ballot(mk >= cand)) >= kw) lbw = cand;
+    }
+    if (lane == 0) s.key[wave] = lbw;
+    __syncthreads();
+    uint32_t lb = s.key[0];
+#pragma unroll
+    for (int w = 1; w < kSW; w++) lb = min(lb, s.key[w]);
+    uint32_t keep[R];
+    int off[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        keep[j] = 0u;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (reg_idx(j, q) < n && fkey(x[4 * j + q]) >= lb) keep[j] |= 1u << q;
+        const int c = __popc(keep[j]);
+        const int inc = wave_iscan_dpp(c);
+        off[j] = inc - c;
+        if (lane == 63) s.cnt[j * kSW + wave] = inc;
+    }
+    __syncthreads();
+    if (tid < 64) {  // ordered exclusive scan of the R kSW tile totals, 2 per lane
+        const int t0 = 2 * lane, t1 = 2 * lane + 1;
+        const int c0 = t0 < R * kSW ? s.cnt[t0] : 0, c1 = t1 < R * kSW ? s.cnt[t1] : 0;
+        const int inc = wave_iscan_dpp(c0 + c1);
+        if (t0 < R * kSW) s.cnt[t0] = inc - c0 - c1;
+        if (t1 < R * kSW) s.cnt[t1] = inc - c1;
+        if (lane == 63) s.sel_i[0] = inc;
+    }
+    __syncthreads();
+    const int total = s.sel_i[0];
+    if (total > kCandCap) {
+        __syncthreads();
+        return -1;
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        int o = s.cnt[j * kSW + wave] + off[j];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (keep[j] & (1u << q)) {
+                s.cv[o] = x[4 * j + q];
+                s.ci[o] = reg_idx(j, q);
+                o++;
+            }
+    }
+    __syncthreads();
+    if (total <= cap) return total;
+    const uint32_t tk = kth_key_w0(total, k, s, [&](int i) { return fkey(s.cv[i]); });
+    return filter_w0(total, s, [&](float v) { return fkey(v) >= tk; });
+}
+
+// The list of reg_topk written out: values, indices + lo, and its count
+// (-1: overflow, or more than cap entries).
+__device__ __forceinline__ void part_write(int m, int lo, int cap, PartLds &s, float *ov, int32_t *oi,
+                                           int32_t *on) {
+    if (m > cap) m = -1;
+    for (int j = threadIdx.x; j < m; j += kST) {
+        ov[j] = s.cv[j];
+        oi[j] = lo + s.ci[j];
+    }
+    if (threadIdx.x == 0) *on = m;
+}
+
+// k-th largest of n keys (0 when n < k), 8 key bits per step: an LDS
+// histogram of the next digit over the keys matching the digits so far,
+// then wave 0 finds the digit from the top (lane l holds digits 255 - 4l
+// down to 252 - 4l; an ordered scan of the lanes' totals).
+template <class L, class K>
+__device__ uint32_t kth_key_radix(int n, int k, L &s, K key) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (n < k) return 0u;
+    uint32_t prefix = 0;
+    int kk = k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        const uint32_t hi = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
+        if (tid < 256) s.cnt[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += kST) {
+            const uint32_t kv = key(i);
+            if ((kv & hi) == prefix) atomicAdd(&s.cnt[(kv >> shift) & 255u], 1);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            int h[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) h[q] = s.cnt[255 - 4 * lane - q];
+            const int loc = h[0] + h[1] + h[2] + h[3];
+            const int inc = wave_iscan_dpp(loc);
+            const uint64_t hit = __ballot(inc >= kk);  // the last lane's total is >= kk
+            if (lane == (int)__builtin_ctzll(hit)) {
+                int before = inc - loc, d = 255 - 4 * lane;
+                bool found = false;
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (!found) {
+                        if (before + h[q] >= kk) {
+                            found = true;
+                            d = 255 - 4 * lane - q;
+                        } else {
+                            before += h[q];
+                        }
+                    }
+                s.sel_i[0] = d;
+                s.sel_i[1] = kk - before;
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)s.sel_i[0] << shift;
+        kk = s.sel_i[1];
+    }
+    __syncthreads();
+    return prefix;
+}
+
+// Keep the candidate-list entries with keep(v), in order, in place: each
+// thread reads its contiguous run (at most 4 entries: n <= kCandCap), an
+// ordered scan gives its first slot, the writes follow every read.
+template <class P>
+__device__ __forceinline__ int filter_blk(int n, SampLds &s, P keep) {
+    static_assert(kCandCap <= 4 * kST, "at most 4 entries per thread");
+    const int C = (n + kST - 1) / kST;
+    const int i0 = min(n, (int)threadIdx.x * C);
+    float v[4];
+    int ix[4];
+    uint32_t m = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (q < C && i0 + q < n) {
+            v[q] = s.cv[i0 + q];
+            ix[q] = s.ci[i0 + q];
+            if (keep(v[q])) m |= 1u << q;
+        }
+    int total;
+    int o = blk_iscan_excl(__popc(m), s, &total);  // (its barriers follow every read)
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (m & (1u << q)) {
+            s.cv[o] = v[q];
+            s.ci[o] = ix[q];
+            o++;
+        }
+    __syncthreads();
+    return total;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x111, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x112, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x114, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x118, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x142, 0xA));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x143, 0xC));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Softmax, top-p, min-p and the draw (sampler.go:117-206) over a candidate
+// list of n <= 64 entries, one per lane of wave 0 (lane order = list order
+// = index order), with wave-level sums: the arithmetic of sample_finish.
+// The top-p cutoff is the largest key whose tail sum reaches p; every
+// entry's tail is summed by the 8 waves at once, over 8 entries each, then
+// the 8 partials in order.
+__device__ __forceinline__ int finish_list64(int n, int V, float top_p, float min_p, float r, SampLds &s) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const bool in = lane < n;
+    float p = 0.f;
+    uint32_t kp = 0u;
+    if (tid < 64) {
+        const float x = in ? s.cv[lane] : -INFINITY;
+        const float m = wave_max_dpp(x);
+        p = (x == -INFINITY) ? 0.f : fastexp32_dev(__fsub_rn(x, m));
+        const float S1 = wave_sum_dpp(p);
+        if (S1 > 0.f) p = __fmul_rn(p, __fdiv_rn(1.f, S1));
+        kp = fkey(p);
+    }
+    if (top_p > 0.f && top_p < 1.f) {
+        if (tid < 64) {
+            s.cv[lane] = p;  // the values are no longer needed
+            s.key[lane] = kp;
+        }
+        __syncthreads();
+        const uint32_t kj = s.key[lane];
+        float part = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const int i = 8 * wave + q;
+            if (i < n && s.key[i] >= kj) part += s.cv[i];
+        }
+        s.cnt[tid] = __float_as_int(part);
+        __syncthreads();
+        if (tid < 64) {
+            float T = 0.f;
+#pragma unroll
+            for (int w = 0; w < kSW; w++) T += __int_as_float(s.cnt[64 * w + lane]);
+            const uint32_t tau = wave_max_u32((in && T >= top_p) ? kp : 0u);  // 0: keep all
+            p = (kp >= tau) ? p : 0.f;
+            const float S2 = wave_sum_dpp(p);
+            if (S2 > 0.f) p = __fmul_rn(p, __fdiv_rn(1.f, S2));
+        }
+    }
+    if (tid < 64) {
+        if (min_p > 0.f) {
+            const float thr = __fmul_rn(wave_max_dpp(p), min_p);
+            p = (p < thr) ? 0.f : p;
+            const float S3 = wave_sum_dpp(p);
+            if (S3 > 0.f) p = __fmul_rn(p, __fdiv_rn(1.f, S3));
+        }
+        const float cum = wave_scan_dpp(p);
+        const uint64_t hit = __ballot(in && r < cum);
+        if (lane == 0) s.sel_i[0] = hit ? s.ci[__builtin_ctzll(hit)] : V - 1;
+    }
+    __syncthreads();
+    const int res = s.sel_i[0];
+    __syncthreads();
+    return res;
+}
+
+// Row b's chunk lists merged, in chunk order, into the working set's
+// candidate list (mode 1): every thread loads its slots while wave 0 scans
+// the counts; false, for the whole work-group, when a chunk overflowed or
+// the lists pass kCandCap.
+__device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, const int32_t *pn, int nch,
+                                           int cap, int V, Src &c, SampLds &s) {
+    constexpr int kSlots = 8;  // nch * cap <= kSlots * kST
+    const int tid = threadIdx.x;
+    const int ns = nch * cap;
+    float v[kSlots];
+    int ix[kSlots];
+#pragma unroll
+    for (int r = 0; r < kSlots; r++) {
+        const int j = tid + kST * r;
+        if (j < ns) {
+            v[r] = pv[j];
+            ix[r] = pi[j];
+        }
+    }
+    if (tid < 64) {  // nch <= 64
+        const int m = tid < nch ? pn[tid] : 0;
+        const bool bad = __ballot(m < 0) != 0;
+        const int m0 = max(m, 0);
+        const int inc = wave_iscan_dpp(m0);
+        s.key[tid] = (uint32_t)(inc - m0);
+        s.cnt[tid] = m0;
+        if (tid == 63) s.sel_i[0] = bad ? -1 : inc;
+    }
+    __syncthreads();
+    const int total = s.sel_i[0];
+    if (total < 0 || total > kCandCap) {
+        __syncthreads();
+        return false;
+    }
+#pragma unroll
+    for (int r = 0; r < kSlots; r++) {
+        const int j = tid + kST * r;
+        if (j < ns) {
+            const int ch = j / cap, e = j - ch * cap;
+            if (e < s.cnt[ch]) {
+                s.cv[(int)s.key[ch] + e] = v[r];
+                s.ci[(int)s.key[ch] + e] = ix[r];
+            }
+        }
+    }
+    __syncthreads();
+    c.mode = 1;
+    c.n = total;
+    c.row = nullptr;
+    c.V = V;
+    c.nseen = 0;
+    c.temp = 1.f;
+    c.div = false;
+    c.topk = c.topp = c.minp = false;
+    c.n1 = c.n2 = c.n3 = false;
+    return true;
+}
+
+// Top-k completed on the merged list (the row's exact k-th largest, then
+// the entries at or above it), then Sample's remaining stages.
+__device__ __forceinline__ int part_finish(Src &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
+    const uint32_t tk = kth_key_radix(c.n, top_k, s, [&](int i) { return fkey(s.cv[i]); });
+    c.n = filter_blk(c.n, s, [&](float v) { return fkey(v) >= tk; });
+    if (c.n <= 64) return finish_list64(c.n, c.V, top_p, min_p, r, s);
+    return sample_finish<1>(c, top_p, min_p, r, s);
+}
+
+// One chunk [lo, lo + n) of a row: its values (the penalties of Sample's
+// arguments a when PEN, then the temperature t), its candidates written out.
+template <int R, bool PEN, class A>
+__device__ __forceinline__ void part_chunk(const A &a, const float *row, int lo, int n, float t, int k, int cap,
+                                           PartLds &s, float *ov, int32_t *oi, int32_t *on) {
+    float x[4 * R];
+    reg_load<R>(row + lo, n, x);
+    if constexpr (PEN) {
+        WinIds w;
+        win_load(a, blockIdx.x, w);
+        reg_penalties<R>(a, w, lo, n, x, s);
+    }
+    if (t != 1.f)
+#pragma unroll
+        for (int j = 0; j < 4 * R; j++) x[j] = __fdiv_rn(x[j], t);
+    part_write(reg_topk<R>(x, n, k, cap, s), lo, cap, s, ov, oi, on);
+}
+
+// Phase one of the split Sample: chunk blockIdx.y of row blockIdx.x.
+__global__ __launch_bounds__(kST) void sample_part_kernel(const SampleArgs a) {
+    __shared__ PartLds s;
+    const int b = blockIdx.x, ch = blockIdx.y;
+    const int lo = ch * a.pch, n = min(a.V - lo, a.pch);
+    float t = a.temperature;
+    if (t <= 0.f) t = 1e-5f;
+    const int64_t q = (int64_t)b * a.nch + ch;
+    const float *row = a.logits + (int64_t)b * a.stride;
+    float *ov = a.part_v + q * a.pcap;
+    int32_t *oi = a.part_i + q * a.pcap;
+    const int k = clamp_topk(a.top_k, a.V);
+    const bool pen = a.hist || a.seen_off;
+    if (n <= 8 * kST) {
+        if (pen)
+            part_chunk<2, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+        else
+            part_chunk<2, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+    } else {
+        if (pen)
+            part_chunk<4, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+        else
+            part_chunk<4, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+    }
+}
+
+// Sample, one work-group per row: phase two of the split path when the
+// chunk lists are there, else the whole row.
 __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs a) {
     __shared__ SampLds s;
     const int b = blockIdx.x;
     Src c;
+    if (a.nch > 0) {
+        const int64_t q = (int64_t)b * a.nch;
+        if (part_merge(a.part_v + q * a.pcap, a.part_i + q * a.pcap, a.part_n + q, a.nch, a.pcap, a.V, c, s)) {
+            const int t = part_finish(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
+            if (threadIdx.x == 0) a.out[b] = t;
+            return;
+        }
+    }
     const float *row = a.logits + (int64_t)b * a.stride;
     if (a.hist) {
         const int ns = count_window(a, b, s);
@@ -883,118 +1411,244 @@ __global__ __launch_bounds__(kST) void greedy_kernel(const float *__restrict__ l
     if (tid == 0) out[blockIdx.x] = bi[0];
 }
 
-// ---- speculative acceptance ---------------------------------------------------
-__device__ __forceinline__ float spec_p(const float *row, int v, float m, bool norm, float inv) {
-    const float e = fastexp32_dev(__fsub_rn(row[v], m));
+// ---- speculative acceptance -------------------------------------------------
+// acceptPhase for a batch of sequences (speculative.go:203-244): accept
+// draft i while u_i < min(1, p_t/max(p_d, 1e-10)); on the first rejection
+// draw the replacement from norm(max(0, p_t - p_d)) (resampleRejected
+// 247-290; the target distribution if that is empty); all accepted: Sample
+// the target's next row without penalties.  Three launches:
+//   1. spec_stat_kernel: one work-group per (row, position, side) holds the
+//      draft or target row in registers (up to 4 kST kRegRow entries, else
+//      it reads the row twice) and gives softmaxAlloc's figures
+//      (speculative.go:344-368: the max, the sum of fastexp32 weights
+//      against it) and the draft token's probability, for every draft at
+//      once; further work-groups cut the next target row into top-k chunk
+//      lists (as the split Sample);
+//   2. spec_mass_kernel, per (row, chunk of kStatChunk entries): the first
+//      rejection from those figures (all drafts at once, by ballot), then
+//      that position's chunk sums of the resample weights max(0, p_t - p_d)
+//      and of p_t;
+//   3. spec_final_kernel, one work-group per row: the chunk whose running
+//      mass passes the draw, then the draw within it; or, all accepted, the
+//      next row's Sample from the merged lists.
+constexpr int kStatChunk = 8 * kST;  // entries of a resample chunk (2 float4 rounds)
+
+struct SpecLds {
+    float red[2][kSW];
+    int cnt[kST];
+    int sel_i[2];
+};
+
+__device__ __forceinline__ float spec_pv(float x, float m, bool norm, float inv) {
+    const float e = fastexp32_dev(__fsub_rn(x, m));
     return norm ? __fmul_rn(e, inv) : e;
 }
 
-// acceptPhase for one sequence (speculative.go:203-244): accept draft i
-// while u_i < min(1, p_t/max(p_d, 1e-10)); on the first rejection draw the
-// replacement from norm(max(0, p_t - p_d)) (resampleRejected 247-290, the
-// target distribution if that is empty); all accepted: Sample the target's
-// next row without penalties.  The draft and target rows of a position are
-// reduced together (softmaxAlloc, speculative.go:344-368: max, then the sum
-// of fastexp32 weights) with 16-byte loads; the resample weights are staged
-// in LDS for the draw when the vocabulary fits.
-__global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
+// Draft count of row b: clamped to [0, max_k] (rlx_spec_accept_async takes
+// it from the device; rlx_spec_accept checks it on the host).
+__device__ __forceinline__ int spec_count(const SpecArgs &a, int b) { return min(max(a.n_draft[b], 0), a.max_k); }
+
+// The first rejected draft of row b (k: none), every thread of the
+// work-group getting it: wave 0 tests 64 drafts per ballot; an id outside
+// [0, V) is a rejection.
+template <class L>
+__device__ __forceinline__ int spec_first_reject(const SpecArgs &a, int b, int k, L &s) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < 64) {
+        const float4 *rec = (const float4 *)a.rec + (int64_t)b * a.max_k * 2;
+        const float *u = a.u + (int64_t)b * (a.max_k + 1);
+        int first = k;
+        for (int i0 = 0; i0 < k; i0 += 64) {
+            const int i = i0 + lane;
+            bool rej = false;
+            if (i < k) {
+                const int tok = a.d_tok[(int64_t)b * a.max_k + i];
+                rej = true;
+                if (tok >= 0 && tok < a.V) {
+                    const float dP = rec[2 * i].z, tP = rec[2 * i + 1].z;
+                    float q = __fdiv_rn(tP, dP > 1e-10f ? dP : 1e-10f);
+                    if (q > 1.f) q = 1.f;
+                    rej = !(u[i] < q);
+                }
+            }
+            const uint64_t m = __ballot(rej);
+            if (m) {
+                first = i0 + (int)__builtin_ctzll(m);
+                break;
+            }
+        }
+        if (tid == 0) s.sel_i[0] = first;
+    }
+    __syncthreads();
+    const int i = s.sel_i[0];
+    __syncthreads();
+    return i;
+}
+
+// Position i's figures: maxima, whether each sum is positive, and 1/sum.
+struct SpecFig {
+    float dm, tm, di, ti;
+    bool dn, tn;
+};
+__device__ __forceinline__ SpecFig spec_fig(const SpecArgs &a, int b, int i) {
+    const float4 *rec = (const float4 *)a.rec + ((int64_t)b * a.max_k + i) * 2;
+    const float4 d = rec[0], t = rec[1];
+    SpecFig f;
+    f.dm = d.x;
+    f.tm = t.x;
+    f.dn = d.y > 0.f;
+    f.tn = t.y > 0.f;
+    f.di = f.dn ? __fdiv_rn(1.f, d.y) : 1.f;
+    f.ti = f.tn ? __fdiv_rn(1.f, t.y) : 1.f;
+    return f;
+}
+// max(0, p_t - p_d) of one entry (resampleRejected, speculative.go:256-262)
+__device__ __forceinline__ float spec_resid(const SpecFig &f, float d, float t) {
+    const float x = __fsub_rn(spec_pv(t, f.tm, f.tn, f.ti), spec_pv(d, f.dm, f.dn, f.di));
+    return x < 0.f ? 0.f : x;
+}
+
+__global__ __launch_bounds__(kST) void spec_stat_kernel(const SpecArgs a) {
+    __shared__ PartLds s;
+    const int b = blockIdx.x, y = blockIdx.y;
+    const int V = a.V, k = spec_count(a, b);
+    if (y >= 2 * a.max_k) {  // chunk y - 2 max_k of the target's row k
+        const int ch = y - 2 * a.max_k;
+        const int lo = ch * a.pch, n = min(V - lo, a.pch);
+        const float *row = a.t_logits + ((int64_t)b * (a.max_k + 1) + k) * V;
+        float t = a.temperature;
+        if (t <= 0.f) t = 1e-5f;
+        const int64_t q = (int64_t)b * a.nch + ch;
+        const int kk = clamp_topk(a.top_k, V);
+        if (n <= 8 * kST)
+            part_chunk<2, false>(a, row, lo, n, t, kk, a.pcap, s, a.part_v + q * a.pcap, a.part_i + q * a.pcap,
+                                 a.part_n + q);
+        else
+            part_chunk<4, false>(a, row, lo, n, t, kk, a.pcap, s, a.part_v + q * a.pcap, a.part_i + q * a.pcap,
+                                 a.part_n + q);
+        return;
+    }
+    const int i = y >> 1, side = y & 1;
+    if (i >= k) return;
+    const float *row = side ? a.t_logits + ((int64_t)b * (a.max_k + 1) + i) * V
+                            : a.d_logits + ((int64_t)b * a.max_k + i) * V;
+    float m, S;
+    if (V <= 4 * kST * kRegRow) {
+        with_rounds(V, [&](auto rc) {
+            constexpr int R = decltype(rc)::value;
+            float x[4 * R];
+            reg_load<R>(row, V, x);  // entries past V read as -inf
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4 * R; j++) mx = fmaxf(mx, x[j]);
+            m = blk_max(mx, s);
+            float sm = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4 * R; j++)
+                if (reg_idx(j >> 2, j & 3) < V) sm += fastexp32_dev(__fsub_rn(x[j], m));
+            S = blk_sum(sm, s);
+        });
+    } else {
+        float mx = -INFINITY;
+#pragma unroll 8
+        for (int v = threadIdx.x; v < V; v += kST) mx = fmaxf(mx, row[v]);
+        m = blk_max(mx, s);
+        float sm = 0.f;
+#pragma unroll 8
+        for (int v = threadIdx.x; v < V; v += kST) sm += fastexp32_dev(__fsub_rn(row[v], m));
+        S = blk_sum(sm, s);
+    }
+    const int tok = a.d_tok[(int64_t)b * a.max_k + i];
+    const bool norm = S > 0.f;
+    const float p = (tok >= 0 && tok < V) ? spec_pv(row[tok], m, norm, norm ? __fdiv_rn(1.f, S) : 1.f) : 0.f;
+    if (threadIdx.x == 0) ((float4 *)a.rec)[((int64_t)b * a.max_k + i) * 2 + side] = make_float4(m, S, p, 0.f);
+}
+
+__global__ __launch_bounds__(kST) void spec_mass_kernel(const SpecArgs a) {
+    __shared__ SpecLds s;
+    const int b = blockIdx.x, c = blockIdx.y;
+    const int V = a.V, k = spec_count(a, b);
+    const int i = spec_first_reject(a, b, k, s);
+    if (i >= k) return;
+    const SpecFig f = spec_fig(a, b, i);
+    const int lo = c * kStatChunk, n = min(V - lo, kStatChunk);
+    float xd[8], xt[8];
+    reg_load<2>(a.d_logits + ((int64_t)b * a.max_k + i) * V + lo, n, xd);
+    reg_load<2>(a.t_logits + ((int64_t)b * (a.max_k + 1) + i) * V + lo, n, xt);
+    float sa = 0.f, st = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (reg_idx(j >> 2, j & 3) < n) {
+            sa += spec_resid(f, xd[j], xt[j]);
+            st += spec_pv(xt[j], f.tm, f.tn, f.ti);
+        }
+    blk_sum2(sa, st, s);
+    if (threadIdx.x == 0) ((float2 *)a.st_mass)[(int64_t)b * a.sch + c] = make_float2(sa, st);
+}
+
+__global__ __launch_bounds__(kST) void spec_final_kernel(const SpecArgs a) {
     __shared__ SampLds s;
     const int b = blockIdx.x, tid = threadIdx.x;
-    // draft counts and ids come from the device in rlx_spec_accept_async:
-    // the count is clamped to [0, max_k], an id outside [0, V) is rejected
-    // (rlx_spec_accept checks both on the host)
-    const int V = a.V;
-    const int k = min(max(a.n_draft[b], 0), a.max_k);
+    const int V = a.V, k = spec_count(a, b);
     const float *u = a.u + (int64_t)b * (a.max_k + 1);
-    const float *dl = a.d_logits + (int64_t)b * a.max_k * V;
     const float *tl = a.t_logits + (int64_t)b * (a.max_k + 1) * V;
-    for (int i = 0; i < k; i++) {
-        const float *dr = dl + (int64_t)i * V, *tr = tl + (int64_t)i * V;
-        const bool vec = ((((uintptr_t)dr) | ((uintptr_t)tr)) & 15) == 0 && (V & 3) == 0;
-        float dm = -INFINITY, tm = -INFINITY;
-        if (vec) {
-            const float4 *d4 = (const float4 *)dr, *t4 = (const float4 *)tr;
-#pragma unroll 8
-            for (int v = tid; v < V / 4; v += kST) {
-                const float4 x = d4[v], y = t4[v];
-                dm = fmaxf(dm, fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)));
-                tm = fmaxf(tm, fmaxf(fmaxf(y.x, y.y), fmaxf(y.z, y.w)));
-            }
-        } else {
-#pragma unroll 8
-            for (int v = tid; v < V; v += kST) {
-                dm = fmaxf(dm, dr[v]);
-                tm = fmaxf(tm, tr[v]);
-            }
+    const int i = spec_first_reject(a, b, k, s);
+    if (i < k) {
+        const SpecFig f = spec_fig(a, b, i);
+        const float *dr = a.d_logits + ((int64_t)b * a.max_k + i) * V, *tr = tl + (int64_t)i * V;
+        const float2 *ms = (const float2 *)a.st_mass + (int64_t)b * a.sch;
+        float SA = 0.f;
+        for (int c = 0; c < a.sch; c++) SA += ms[c].x;
+        // norm(max(0, p_t - p_d)), or p_t when that is empty
+        const bool resid = SA > 0.f;
+        const float inv = resid ? __fdiv_rn(1.f, SA) : 1.f;
+        const float rr = u[i + 1];
+        // the chunk whose running mass passes the draw, then the draw within
+        // it (on through later chunks should rounding leave it no hit)
+        int c0 = 0;
+        float base = 0.f;
+        for (; c0 < a.sch - 1; c0++) {
+            const float m = resid ? __fmul_rn(ms[c0].x, inv) : ms[c0].y;
+            if (rr < base + m) break;
+            base += m;
         }
-        blk_max2(dm, tm, s);
-        float ds = 0.f, ts = 0.f;
-        if (vec) {
-            const float4 *d4 = (const float4 *)dr, *t4 = (const float4 *)tr;
-#pragma unroll 8
-            for (int v = tid; v < V / 4; v += kST) {
-                const float4 x = d4[v], y = t4[v];
-                ds += fastexp32_dev(__fsub_rn(x.x, dm));
-                ds += fastexp32_dev(__fsub_rn(x.y, dm));
-                ds += fastexp32_dev(__fsub_rn(x.z, dm));
-                ds += fastexp32_dev(__fsub_rn(x.w, dm));
-                ts += fastexp32_dev(__fsub_rn(y.x, tm));
-                ts += fastexp32_dev(__fsub_rn(y.y, tm));
-                ts += fastexp32_dev(__fsub_rn(y.z, tm));
-                ts += fastexp32_dev(__fsub_rn(y.w, tm));
+        int res = -1;
+        for (int c = c0; c < a.sch && res < 0; c++) {
+            const int lo = c * kStatChunk, n = min(V - lo, kStatChunk);
+            float xd[8], xt[8];
+            reg_load<2>(dr + lo, n, xd);
+            reg_load<2>(tr + lo, n, xt);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int e = reg_idx(j >> 2, j & 3);
+                if (e < n)
+                    s.region[e] = resid ? __fmul_rn(spec_resid(f, xd[j], xt[j]), inv)
+                                        : spec_pv(xt[j], f.tm, f.tn, f.ti);
             }
-        } else {
-#pragma unroll 8
-            for (int v = tid; v < V; v += kST) {
-                ds += fastexp32_dev(__fsub_rn(dr[v], dm));
-                ts += fastexp32_dev(__fsub_rn(tr[v], tm));
-            }
-        }
-        blk_sum2(ds, ts, s);
-        const bool dn = ds > 0.f, tn = ts > 0.f;
-        const float di = dn ? __fdiv_rn(1.f, ds) : 1.f, ti = tn ? __fdiv_rn(1.f, ts) : 1.f;
-        const int tok = a.d_tok[(int64_t)b * a.max_k + i];
-        if (tok >= 0 && tok < V) {
-            const float dP = spec_p(dr, tok, dm, dn, di), tP = spec_p(tr, tok, tm, tn, ti);
-            float acc = __fdiv_rn(tP, dP > 1e-10f ? dP : 1e-10f);
-            if (acc > 1.f) acc = 1.f;
-            if (u[i] < acc) continue;
-        }
-        auto adj = [&](int v) {
-            const float d = __fsub_rn(spec_p(tr, v, tm, tn, ti), spec_p(dr, v, dm, dn, di));
-            return d < 0.f ? 0.f : d;
-        };
-        const bool lds = V <= kRowCap;
-        float sa = 0.f;
-#pragma unroll 4
-        for (int v = tid; v < V; v += kST) {
-            const float x = adj(v);
-            if (lds) s.region[v] = x;
-            sa += x;
-        }
-        const float SA = blk_sum(sa, s);  // (its barriers also publish the region)
-        auto ident = [](int v) { return v; };
-        int res;
-        if (SA > 0.f) {
-            const float inv = __fdiv_rn(1.f, SA);
-            if (lds)
-                res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return __fmul_rn(s.region[v], inv); }, ident);
-            else
-                res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return __fmul_rn(adj(v), inv); }, ident);
-        } else {
-            res = samp_draw(V, u[i + 1], 0, s, [&](int v) { return spec_p(tr, v, tm, tn, ti); }, ident);
+            __syncthreads();
+            float tot;
+            const int hit = samp_draw_from(n, rr, base, s, [&](int v) { return s.region[v]; }, &tot);
+            if (hit >= 0) res = lo + hit;
+            base += tot;
         }
         if (tid == 0) {
             a.n_acc[b] = i;
-            a.next[b] = res;
+            a.next[b] = res < 0 ? 0 : res;
         }
         return;
     }
+    int t;
     Src c;
-    load_row(
-        c, s, tl + (int64_t)k * V, V, a.temperature, [](int) { return 0; }, [](int) { return 0; }, 0, 0.f,
-        0.f, 0.f);
-    const int t = sample_set(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
+    if (a.nch > 0 &&
+        part_merge(a.part_v + (int64_t)b * a.nch * a.pcap, a.part_i + (int64_t)b * a.nch * a.pcap,
+                   a.part_n + (int64_t)b * a.nch, a.nch, a.pcap, V, c, s)) {
+        t = part_finish(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
+    } else {
+        load_row(
+            c, s, tl + (int64_t)k * V, V, a.temperature, [](int) { return 0; }, [](int) { return 0; }, 0, 0.f,
+            0.f, 0.f);
+        t = sample_set(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
+    }
     if (tid == 0) {
         a.n_acc[b] = k;
         a.next[b] = t;
@@ -1003,7 +1657,16 @@ __global__ __launch_bounds__(kST) void spec_accept_kernel(const SpecArgs a) {
 
 hipError_t launch_sample(hipStream_t st, const SampleArgs &a, int n_rows, hipEvent_t e0,
                          hipEvent_t e1) {
-    return launch_timed(sample_kernel, dim3(n_rows), dim3(kST), st, e0, e1, a);
+    if (e0) (void)hipEventRecord(e0, st);
+    if (a.nch > 0) {
+        sample_part_kernel<<<dim3(n_rows, a.nch), dim3(kST), 0, st>>>(a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    sample_kernel<<<dim3(n_rows), dim3(kST), 0, st>>>(a);
+    const hipError_t e = hipGetLastError();
+    if (e1) (void)hipEventRecord(e1, st);
+    return e;
 }
 
 hipError_t launch_greedy(hipStream_t st, const float *logits, int64_t stride, int V, int n_rows,
@@ -1013,7 +1676,98 @@ hipError_t launch_greedy(hipStream_t st, const float *logits, int64_t stride, in
 
 hipError_t launch_spec_accept(hipStream_t st, const SpecArgs &a, int n_rows, hipEvent_t e0,
                               hipEvent_t e1) {
-    return launch_timed(spec_accept_kernel, dim3(n_rows), dim3(kST), st, e0, e1, a);
+    if (e0) (void)hipEventRecord(e0, st);
+    hipError_t e = hipSuccess;
+    const int ny = 2 * a.max_k + a.nch;
+    if (ny > 0) {
+        spec_stat_kernel<<<dim3(n_rows, ny), dim3(kST), 0, st>>>(a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    if (a.max_k > 0) {
+        spec_mass_kernel<<<dim3(n_rows, a.sch), dim3(kST), 0, st>>>(a);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    spec_final_kernel<<<dim3(n_rows), dim3(kST), 0, st>>>(a);
+    e = hipGetLastError();
+    if (e1) (void)hipEventRecord(e1, st);
+    return e;
+}
+
+namespace {
+constexpr int kGridY = 65535;  // grid y extent limit
+
+// Top-k chunking of a vocabulary V for top-k k (clamped as Sample does):
+// chunks of about 4096 entries, fewer when their lists could pass
+// kCandCap (and their slots past 8 per thread of the merge), at most
+// kPartChunk entries and 64 chunks; none (nch 0) when top-k is off, larger
+// than kPartMaxK, or a single chunk would do.
+void topk_split(int V, int top_k, int &nch, int &pch, int &pcap) {
+    nch = pch = pcap = 0;
+    const int k = (top_k < 0 || top_k >= V) ? 0 : top_k;
+    if (k <= 0 || k > kPartMaxK) return;
+    int n = (V + 4095) / 4096;
+    if (n * k > kCandCap) n = kCandCap / k;
+    if (n < 2) return;
+    const int len = ((V + n - 1) / n + 3) & ~3;
+    const int nc = (V + len - 1) / len;
+    if (len > kPartChunk || nc > 64 || nc < 2) return;
+    // slots for a chunk's lower-bound list (about 2k entries on typical
+    // rows), within the merge's 8 slots per thread
+    const int cap = min(min(kCandCap, max(128, 4 * k)), 8 * kST / nc);
+    if (cap < k) return;
+    nch = nc;
+    pch = len;
+    pcap = cap;
+}
+
+int64_t carve(int64_t &off, int64_t bytes) {
+    const int64_t at = off;
+    off += (bytes + 255) & ~(int64_t)255;
+    return at;
+}
+}  // namespace
+
+int64_t plan_sample_split(SampleArgs &a, int n_rows, char *base) {
+    topk_split(a.V, a.top_k, a.nch, a.pch, a.pcap);
+    a.part_v = nullptr;
+    a.part_i = a.part_n = nullptr;
+    if (a.nch == 0) return 0;
+    int64_t off = 0;
+    const int64_t slots = (int64_t)n_rows * a.nch * a.pcap;
+    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 4);
+    const int64_t o_v = carve(off, slots * 4);
+    const int64_t o_i = carve(off, slots * 4);
+    if (base) {
+        a.part_n = (int32_t *)(base + o_n);
+        a.part_v = (float *)(base + o_v);
+        a.part_i = (int32_t *)(base + o_i);
+    }
+    return off;
+}
+
+int64_t plan_spec_split(SpecArgs &a, int n_rows, char *base) {
+    topk_split(a.V, a.top_k, a.nch, a.pch, a.pcap);
+    a.sch = (a.V + kStatChunk - 1) / kStatChunk;
+    if ((int64_t)2 * a.max_k + a.nch > kGridY || a.sch > kGridY) return -1;
+    a.rec = a.st_mass = a.part_v = nullptr;
+    a.part_i = a.part_n = nullptr;
+    int64_t off = 0;
+    const int64_t o_r = carve(off, (int64_t)n_rows * a.max_k * 2 * 16);
+    const int64_t o_m = carve(off, (int64_t)n_rows * a.sch * 8);
+    const int64_t slots = (int64_t)n_rows * a.nch * a.pcap;
+    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 4);
+    const int64_t o_v = carve(off, slots * 4);
+    const int64_t o_i = carve(off, slots * 4);
+    if (base) {
+        a.rec = (float *)(base + o_r);
+        a.st_mass = (float *)(base + o_m);
+        if (a.nch) {
+            a.part_n = (int32_t *)(base + o_n);
+            a.part_v = (float *)(base + o_v);
+            a.part_i = (int32_t *)(base + o_i);
+        }
+    }
+    return off;
 }
 
 }  // namespace rlx

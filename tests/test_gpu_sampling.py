@@ -68,8 +68,11 @@ PARAMS = {
 
 
 # V 50000 is past the LDS row (32768 entries): the memory-read path, with
-# the penalised tokens in the LDS bitmap and top-k compaction.
+# the penalised tokens in the LDS bitmap and top-k compaction.  With top-k on
+# and V past 4096 the vocabulary is split over work-groups (V 32000: 8
+# chunks; V 50000: 13), each keeping its own candidates.
 CASES = [(n, V) for V in (100, 4096) for n in sorted(PARAMS)] + \
+    [(n, 32000) for n in ("topk5", "topk50_t1.3", "all")] + \
     [(n, 50000) for n in ("plain", "temp0.7", "topk5", "all", "penalties")]
 
 
@@ -92,6 +95,36 @@ def test_sample(gpu, handle, name, V):
         assert got[i] == want, (name, V, i, got[i], want)
     print(f"sample {name} V{V}: {kept}/{rows} robust rows compared")
     assert kept >= rows // 2
+
+
+def test_sample_split_ties(gpu, handle):
+    """Ties at a chunk's k-th largest value: a chunk list past its slots (or a
+    merge past the candidate capacity) sends the row down the whole-row
+    path, smaller ties stay on the split path; every row agrees with the
+    oracle, which keeps all entries tied with the k-th largest."""
+    rng = np.random.default_rng(77)
+    V, rows = 32000, 8
+    x = rng.normal(0, 2.5, (rows, V)).astype(np.float32)
+    x[0, :] = 0.0                    # ties at every chunk's k-th largest: all lists overflow;
+    x[0, [5, 17000, 31000]] = 12.0   # three entries hold most of the mass (a flat row's
+    #                                  sequential f32 sums drift by 1e-4 over 32000 entries)
+    x[1, 100:400] = 12.0             # 300 tied maxima in one chunk (past its 100 slots)
+    x[2, ::500] = 12.0               # 64 tied maxima spread over the 8 chunks
+    x[3, 3990:4010] = 12.0           # ties across a chunk boundary
+    x[4, :] = np.round(x[4, :])      # a few thousand entries on each integer
+    x[5, 31990:] = 12.0              # ties in the last chunk
+    x[6, :60] = np.float32(-np.inf)  # masked entries in the first chunk
+    u = rng.random(rows, dtype=np.float32)
+    for p in (S.SamplerParams(top_k=50, temperature=0.9), S.SamplerParams(top_k=5, min_p=0.05)):
+        got = make_sampler(p, S.Draws(u)).Sample(dev(x, gpu), None, handle)
+        kept = 0
+        for i in range(rows):
+            want = S.sample(x[i], p, u[i])
+            if S.sample(x[i], p, u[i] - DELTA) != want or S.sample(x[i], p, u[i] + DELTA) != want:
+                continue
+            kept += 1
+            assert got[i] == want, (p, i, got[i], want)
+        assert kept >= rows // 2
 
 
 WINDOW_CASES = [
@@ -167,7 +200,9 @@ def test_sample_async_no_history_and_limits(gpu, handle):
         smp.SampleAsync(x, None, None, torch.from_numpy(u), handle)
 
 
-@pytest.mark.parametrize("V", [100, 4096, 50000])
+# V 32000 and 50000: the next-row Sample of all-accepted rows runs split
+# (top-k 30); every V reduces its softmax statistics over 4096-entry chunks.
+@pytest.mark.parametrize("V", [100, 4096, 32000, 50000])
 def test_spec_accept(gpu, handle, V):
     from relux_amd import spec_accept
     rng = np.random.default_rng(V)
