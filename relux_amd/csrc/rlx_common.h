@@ -345,8 +345,9 @@ struct SampleArgs {
     int32_t *out;
     // vocabulary split (nch > 0, set by plan_sample_split): row b's chunk c
     // covers entries [c * pch, min(V, (c + 1) * pch)) and leaves its top-k
-    // candidates at part_v / part_i[(b * nch + c) * pcap ..] with their
-    // count (-1: overflow) at part_n[b * nch + c]
+    // candidates at part_v / part_i[(b * nch + c) * pcap ..] with its record
+    // part_n[(b * nch + c) * 4 ..] = {count (-1: overflow), lower bound key
+    // of its k-th largest, largest key, 0}
     int nch, pch, pcap;
     float *part_v;
     int32_t *part_i, *part_n;

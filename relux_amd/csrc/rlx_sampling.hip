@@ -198,6 +198,15 @@ __device__ __forceinline__ int wave_iscan_dpp(int v) {
     v += RLX_DPPI(v, 0x143, 0xC);
     return v;
 }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x111, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x112, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x114, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x118, 0xF));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x142, 0xA));
+    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x143, 0xC));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 template <class L>
 __device__ __forceinline__ float blk_scan_excl(float v, L &s, float *total) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -939,6 +948,25 @@ __device__ __forceinline__ void win_load(const SampleArgs &a, int b, WinIds &w) 
     int nw = 0;
     const int32_t *h = nullptr;
     w.n0 = 0;
+    if (a.hist && a.hist_stride <= kSampMaxSeen) {
+        // a short history row is read whole, with its length, then cut to
+        // the window
+        const int32_t *row = a.hist + (int64_t)b * a.hist_stride;
+        const int S = (int)a.hist_stride;
+#pragma unroll
+        for (int r = 0; r < kSampMaxSeen / kST; r++) {
+            const int i = tid + kST * r;
+            w.ids[r] = i < S ? row[i] : -1;
+        }
+        const int hn = (int)max((int64_t)0, min((int64_t)a.hist_len[b], a.hist_stride));
+        const int h0 = (a.window > 0 && hn > a.window) ? hn - a.window : 0;
+#pragma unroll
+        for (int r = 0; r < kSampMaxSeen / kST; r++) {
+            const int i = tid + kST * r;
+            if (i < h0 || i >= hn) w.ids[r] = -1;
+        }
+        return;
+    }
     if (a.hist) {
         const int hn = (int)max((int64_t)0, min((int64_t)a.hist_len[b], a.hist_stride));
         const int h0 = (a.window > 0 && hn > a.window) ? hn - a.window : 0;
@@ -962,9 +990,9 @@ __device__ __forceinline__ void win_load(const SampleArgs &a, int b, WinIds &w) 
 // its list position + 1 (host lists, whose counts are read back).
 template <int R>
 __device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds &w, int lo, int n,
-                                              float (&x)[4 * R], PartLds &s) {
+                                              float (&x)[4 * R], uint32_t *slots) {
     const int tid = threadIdx.x;
-    for (int i = tid; i < (n + 1) >> 1; i += kST) s.pcw[i] = 0u;
+    for (int i = tid; i < (n + 1) >> 1; i += kST) slots[i] = 0u;
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < kSampMaxSeen / kST; r++) {
@@ -972,9 +1000,9 @@ __device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds 
         if (id >= lo && id < lo + n) {
             const uint32_t sh = 16 * ((id - lo) & 1);
             if (a.hist)
-                atomicAdd(&s.pcw[(id - lo) >> 1], 1u << sh);
+                atomicAdd(&slots[(id - lo) >> 1], 1u << sh);
             else
-                atomicOr(&s.pcw[(id - lo) >> 1], (uint32_t)(tid + kST * r + 1) << sh);
+                atomicOr(&slots[(id - lo) >> 1], (uint32_t)(tid + kST * r + 1) << sh);
         }
     }
     __syncthreads();
@@ -982,7 +1010,7 @@ __device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds 
     for (int j = 0; j < R; j++) {
         const int e = reg_idx(j, 0);
         if (e >= n) continue;
-        const uint2 v = *(const uint2 *)&s.pcw[e >> 1];  // the round's 4 slots
+        const uint2 v = *(const uint2 *)&slots[e >> 1];  // the round's 4 slots
         const uint32_t sl[4] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16};
 #pragma unroll
         for (int q = 0; q < 4; q++)
@@ -991,24 +1019,21 @@ __device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds 
                 x[4 * j + q] = pen_value(x[4 * j + q], f, a.rp, a.fp, a.pp);
             }
     }
-    __syncthreads();  // the slots alias the candidate list
+    __syncthreads();  // the slots alias the candidate list or the row region
 }
 
-// Top-k candidates of n register-held values (0 < k), in index order, into
-// s.cv / s.ci (indices relative to the segment): the entries at or above a
-// lower bound of their k-th largest, or, when those pass cap, the entries
-// at or above the exact k-th largest; returns their count, -1 when the
-// first compaction passes kCandCap.
-//   1. lower bound: each wave's ceil(k / kSW)-th largest lane maximum, to 16
-//      key bits; the smallest over the waves (every wave holds that many
-//      entries at or above it: kSW ceil(k / kSW) >= k in all);
-//   2. the entries at or above it compacted in index order: per (round,
-//      wave) tile a ballot-free lane scan, then an ordered scan of the tile
-//      totals;
-//   3. past cap only: the exact k-th largest of that list (wave 0, one key
-//      bit per step) and the list filtered to it.
-template <int R>
-__device__ __forceinline__ int reg_topk(const float (&x)[4 * R], int n, int k, int cap, PartLds &s) {
+// Candidates from n register-held values (0 < k): the entries at or above a
+// lower bound of their k-th largest, placed in index order.
+//   reg_bound: lb = each wave's ceil(k / kSW)-th largest lane maximum, to 16
+//     key bits, the smallest over the waves (every wave holds that many
+//     entries at or above it: kSW ceil(k / kSW) >= k in all); ub = the
+//     largest key; the kept entries' lane offsets within their (round,
+//     wave) tile and, in s.cnt, the tiles' first slots (an ordered scan);
+//     returns their count (every thread).
+//   reg_place: the kept entries written to dv / di (indices + ioff).
+template <int R, class L>
+__device__ __forceinline__ int reg_bound(const float (&x)[4 * R], int n, int k, L &s, uint32_t (&keep)[R],
+                                         int (&off)[R], uint32_t &lb, uint32_t &ub) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t mk = 0;
 #pragma unroll
@@ -1020,13 +1045,19 @@ __device__ __forceinline__ int reg_topk(const float (&x)[4 * R], int n, int k, i
         const uint32_t cand = lbw | (1u << bit);
         if ((int)__popcll(__ballot(mk >= cand)) >= kw) lbw = cand;
     }
-    if (lane == 0) s.key[wave] = lbw;
+    const uint32_t ubw = wave_max_u32(mk);
+    if (lane == 0) {
+        s.key[wave] = lbw;
+        s.key[kSW + wave] = ubw;
+    }
     __syncthreads();
-    uint32_t lb = s.key[0];
+    lb = s.key[0];
+    ub = s.key[kSW];
 #pragma unroll
-    for (int w = 1; w < kSW; w++) lb = min(lb, s.key[w]);
-    uint32_t keep[R];
-    int off[R];
+    for (int w = 1; w < kSW; w++) {
+        lb = min(lb, s.key[w]);
+        ub = max(ub, s.key[kSW + w]);
+    }
 #pragma unroll
     for (int j = 0; j < R; j++) {
         keep[j] = 0u;
@@ -1048,57 +1079,85 @@ __device__ __forceinline__ int reg_topk(const float (&x)[4 * R], int n, int k, i
         if (lane == 63) s.sel_i[0] = inc;
     }
     __syncthreads();
-    const int total = s.sel_i[0];
-    if (total > kCandCap) {
-        __syncthreads();
-        return -1;
-    }
+    return s.sel_i[0];
+}
+template <int R>
+__device__ __forceinline__ void reg_place(const float (&x)[4 * R], const uint32_t (&keep)[R], const int (&off)[R],
+                                          const int *base, float *dv, int32_t *di, int ioff) {
+    const int wave = threadIdx.x >> 6;
 #pragma unroll
     for (int j = 0; j < R; j++) {
-        int o = s.cnt[j * kSW + wave] + off[j];
+        int o = base[j * kSW + wave] + off[j];
 #pragma unroll
         for (int q = 0; q < 4; q++)
             if (keep[j] & (1u << q)) {
-                s.cv[o] = x[4 * j + q];
-                s.ci[o] = reg_idx(j, q);
+                dv[o] = x[4 * j + q];
+                di[o] = ioff + reg_idx(j, q);
                 o++;
             }
     }
-    __syncthreads();
-    if (total <= cap) return total;
-    const uint32_t tk = kth_key_w0(total, k, s, [&](int i) { return fkey(s.cv[i]); });
-    return filter_w0(total, s, [&](float v) { return fkey(v) >= tk; });
 }
 
-// The list of reg_topk written out: values, indices + lo, and its count
-// (-1: overflow, or more than cap entries).
-__device__ __forceinline__ void part_write(int m, int lo, int cap, PartLds &s, float *ov, int32_t *oi,
-                                           int32_t *on) {
-    if (m > cap) m = -1;
-    for (int j = threadIdx.x; j < m; j += kST) {
-        ov[j] = s.cv[j];
-        oi[j] = lo + s.ci[j];
+// A chunk's top-k candidates written out in index order (indices offset by
+// lo) with the chunk record on = {count, lower bound key, largest key}
+// (count -1: overflow): the reg_bound entries straight from registers when
+// they fit the cap slots; otherwise compacted in LDS, cut to the exact k-th
+// largest (wave 0, one key bit per step; it becomes the lower bound) and
+// written from there.
+template <int R>
+__device__ __forceinline__ void reg_topk(const float (&x)[4 * R], int n, int k, int lo, int cap, PartLds &s,
+                                         float *ov, int32_t *oi, int32_t *on) {
+    const int tid = threadIdx.x;
+    uint32_t keep[R], lb, ub;
+    int off[R];
+    const int total = reg_bound<R>(x, n, k, s, keep, off, lb, ub);
+    if (total <= cap) {
+        reg_place<R>(x, keep, off, s.cnt, ov, oi, lo);
+        if (tid == 0) *(int4 *)on = make_int4(total, (int)lb, (int)ub, 0);
+        return;
     }
-    if (threadIdx.x == 0) *on = m;
+    int m = -1;
+    uint32_t tk = 0;
+    if (total <= kCandCap) {
+        reg_place<R>(x, keep, off, s.cnt, s.cv, s.ci, 0);
+        __syncthreads();
+        tk = kth_key_w0(total, k, s, [&](int i) { return fkey(s.cv[i]); });
+        m = filter_w0(total, s, [&](float v) { return fkey(v) >= tk; });
+        if (m > cap) m = -1;
+        for (int j = tid; j < m; j += kST) {
+            ov[j] = s.cv[j];
+            oi[j] = lo + s.ci[j];
+        }
+    }
+    if (tid == 0) *(int4 *)on = make_int4(m, (int)tk, (int)ub, 0);
 }
 
-// k-th largest of n keys (0 when n < k), 8 key bits per step: an LDS
-// histogram of the next digit over the keys matching the digits so far,
-// then wave 0 finds the digit from the top (lane l holds digits 255 - 4l
-// down to 252 - 4l; an ordered scan of the lanes' totals).
+// k-th largest of n keys (0 when n < k), given that it lies in [lo, hi]
+// and no key exceeds hi: the bits above the highest one in which lo and hi
+// differ are known; the rest is found 8 bits per step (the first step
+// takes the odd bits), by an LDS histogram of the next digit over the keys
+// matching the digits so far, then wave 0 finds the digit from the top
+// (lane l holds digits 255 - 4l down to 252 - 4l; an ordered scan of the
+// lanes' totals).  Keys below lo that match the known bits only add to the
+// counts below the answer.
 template <class L, class K>
-__device__ uint32_t kth_key_radix(int n, int k, L &s, K key) {
+__device__ uint32_t kth_key_radix(int n, int k, uint32_t lo, uint32_t hi, L &s, K key) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (n < k) return 0u;
-    uint32_t prefix = 0;
+    if (lo >= hi) return hi;
+    const int top = 31 - __builtin_clz(lo ^ hi);  // highest differing bit
+    const int steps = (top + 8) / 8;
+    const uint32_t known = top == 31 ? 0u : (0xFFFFFFFFu << (top + 1));
+    uint32_t prefix = lo & known;
     int kk = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        const uint32_t hi = shift == 24 ? 0u : (0xFFFFFFFFu << (shift + 8));
+    for (int st = 0; st < steps; st++) {
+        const int shift = 8 * (steps - 1 - st);
+        const uint32_t fixed = st == 0 ? known : (0xFFFFFFFFu << (shift + 8));
         if (tid < 256) s.cnt[tid] = 0;
         __syncthreads();
         for (int i = tid; i < n; i += kST) {
             const uint32_t kv = key(i);
-            if ((kv & hi) == prefix) atomicAdd(&s.cnt[(kv >> shift) & 255u], 1);
+            if ((kv & fixed) == prefix) atomicAdd(&s.cnt[(kv >> shift) & 255u], 1);
         }
         __syncthreads();
         if (tid < 64) {
@@ -1164,15 +1223,6 @@ __device__ __forceinline__ int filter_blk(int n, SampLds &s, P keep) {
     return total;
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x111, 0xF));
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x112, 0xF));
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x114, 0xF));
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x118, 0xF));
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x142, 0xA));
-    v = max(v, (uint32_t)RLX_DPPI((int)v, 0x143, 0xC));
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
 
 // Softmax, top-p, min-p and the draw (sampler.go:117-206) over a candidate
 // list of n <= 64 entries, one per lane of wave 0 (lane order = list order
@@ -1237,10 +1287,12 @@ __device__ __forceinline__ int finish_list64(int n, int V, float top_p, float mi
 
 // Row b's chunk lists merged, in chunk order, into the working set's
 // candidate list (mode 1): every thread loads its slots while wave 0 scans
-// the counts; false, for the whole work-group, when a chunk overflowed or
-// the lists pass kCandCap.
+// the chunk records {count, lower bound key, largest key}; lb / ub: the
+// largest lower bound and the largest key (the row's k-th largest lies
+// between them); false, for the whole work-group, when a chunk overflowed
+// or the lists pass kCandCap.
 __device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, const int32_t *pn, int nch,
-                                           int cap, int V, Src &c, SampLds &s) {
+                                           int cap, int V, Src &c, uint32_t &lb, uint32_t &ub, SampLds &s) {
     constexpr int kSlots = 8;  // nch * cap <= kSlots * kST
     const int tid = threadIdx.x;
     const int ns = nch * cap;
@@ -1255,16 +1307,23 @@ __device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, c
         }
     }
     if (tid < 64) {  // nch <= 64
-        const int m = tid < nch ? pn[tid] : 0;
-        const bool bad = __ballot(m < 0) != 0;
-        const int m0 = max(m, 0);
+        const int4 r = tid < nch ? ((const int4 *)pn)[tid] : make_int4(0, 0, 0, 0);
+        const bool bad = __ballot(r.x < 0) != 0;
+        const int m0 = max(r.x, 0);
         const int inc = wave_iscan_dpp(m0);
         s.key[tid] = (uint32_t)(inc - m0);
         s.cnt[tid] = m0;
-        if (tid == 63) s.sel_i[0] = bad ? -1 : inc;
+        const uint32_t l = wave_max_u32((uint32_t)r.y), u = wave_max_u32((uint32_t)r.z);
+        if (tid == 63) {
+            s.sel_i[0] = bad ? -1 : inc;
+            s.key[64] = l;
+            s.key[65] = u;
+        }
     }
     __syncthreads();
     const int total = s.sel_i[0];
+    lb = s.key[64];
+    ub = s.key[65];
     if (total < 0 || total > kCandCap) {
         __syncthreads();
         return false;
@@ -1295,8 +1354,9 @@ __device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, c
 
 // Top-k completed on the merged list (the row's exact k-th largest, then
 // the entries at or above it), then Sample's remaining stages.
-__device__ __forceinline__ int part_finish(Src &c, int top_k, float top_p, float min_p, float r, SampLds &s) {
-    const uint32_t tk = kth_key_radix(c.n, top_k, s, [&](int i) { return fkey(s.cv[i]); });
+__device__ __forceinline__ int part_finish(Src &c, uint32_t lb, uint32_t ub, int top_k, float top_p, float min_p,
+                                           float r, SampLds &s) {
+    const uint32_t tk = kth_key_radix(c.n, top_k, lb, ub, s, [&](int i) { return fkey(s.cv[i]); });
     c.n = filter_blk(c.n, s, [&](float v) { return fkey(v) >= tk; });
     if (c.n <= 64) return finish_list64(c.n, c.V, top_p, min_p, r, s);
     return sample_finish<1>(c, top_p, min_p, r, s);
@@ -1312,12 +1372,12 @@ __device__ __forceinline__ void part_chunk(const A &a, const float *row, int lo,
     if constexpr (PEN) {
         WinIds w;
         win_load(a, blockIdx.x, w);
-        reg_penalties<R>(a, w, lo, n, x, s);
+        reg_penalties<R>(a, w, lo, n, x, s.pcw);
     }
     if (t != 1.f)
 #pragma unroll
         for (int j = 0; j < 4 * R; j++) x[j] = __fdiv_rn(x[j], t);
-    part_write(reg_topk<R>(x, n, k, cap, s), lo, cap, s, ov, oi, on);
+    reg_topk<R>(x, n, k, lo, cap, s, ov, oi, on);
 }
 
 // Phase one of the split Sample: chunk blockIdx.y of row blockIdx.x.
@@ -1335,14 +1395,14 @@ __global__ __launch_bounds__(kST) void sample_part_kernel(const SampleArgs a) {
     const bool pen = a.hist || a.seen_off;
     if (n <= 8 * kST) {
         if (pen)
-            part_chunk<2, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+            part_chunk<2, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + 4 * q);
         else
-            part_chunk<2, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+            part_chunk<2, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + 4 * q);
     } else {
         if (pen)
-            part_chunk<4, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+            part_chunk<4, true>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + 4 * q);
         else
-            part_chunk<4, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + q);
+            part_chunk<4, false>(a, row, lo, n, t, k, a.pcap, s, ov, oi, a.part_n + 4 * q);
     }
 }
 
@@ -1354,8 +1414,11 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs a) {
     Src c;
     if (a.nch > 0) {
         const int64_t q = (int64_t)b * a.nch;
-        if (part_merge(a.part_v + q * a.pcap, a.part_i + q * a.pcap, a.part_n + q, a.nch, a.pcap, a.V, c, s)) {
-            const int t = part_finish(c, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
+        uint32_t lb, ub;
+        if (part_merge(a.part_v + q * a.pcap, a.part_i + q * a.pcap, a.part_n + 4 * q, a.nch, a.pcap, a.V, c, lb,
+                       ub, s)) {
+            const int t =
+                part_finish(c, lb, ub, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
             if (threadIdx.x == 0) a.out[b] = t;
             return;
         }
@@ -1522,10 +1585,10 @@ __global__ __launch_bounds__(kST) void spec_stat_kernel(const SpecArgs a) {
         const int kk = clamp_topk(a.top_k, V);
         if (n <= 8 * kST)
             part_chunk<2, false>(a, row, lo, n, t, kk, a.pcap, s, a.part_v + q * a.pcap, a.part_i + q * a.pcap,
-                                 a.part_n + q);
+                                 a.part_n + 4 * q);
         else
             part_chunk<4, false>(a, row, lo, n, t, kk, a.pcap, s, a.part_v + q * a.pcap, a.part_i + q * a.pcap,
-                                 a.part_n + q);
+                                 a.part_n + 4 * q);
         return;
     }
     const int i = y >> 1, side = y & 1;
@@ -1639,10 +1702,11 @@ __global__ __launch_bounds__(kST) void spec_final_kernel(const SpecArgs a) {
     }
     int t;
     Src c;
+    uint32_t lb, ub;
     if (a.nch > 0 &&
         part_merge(a.part_v + (int64_t)b * a.nch * a.pcap, a.part_i + (int64_t)b * a.nch * a.pcap,
-                   a.part_n + (int64_t)b * a.nch, a.nch, a.pcap, V, c, s)) {
-        t = part_finish(c, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
+                   a.part_n + (int64_t)b * a.nch * 4, a.nch, a.pcap, V, c, lb, ub, s)) {
+        t = part_finish(c, lb, ub, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
     } else {
         load_row(
             c, s, tl + (int64_t)k * V, V, a.temperature, [](int) { return 0; }, [](int) { return 0; }, 0, 0.f,
@@ -1697,15 +1761,15 @@ namespace {
 constexpr int kGridY = 65535;  // grid y extent limit
 
 // Top-k chunking of a vocabulary V for top-k k (clamped as Sample does):
-// chunks of about 4096 entries, fewer when their lists could pass
-// kCandCap (and their slots past 8 per thread of the merge), at most
-// kPartChunk entries and 64 chunks; none (nch 0) when top-k is off, larger
-// than kPartMaxK, or a single chunk would do.
+// chunks of up to kPartChunk entries (measured faster than 4096 or 16384:
+// fewer, larger chunks shorten the merge), fewer when their lists could
+// pass kCandCap (or their slots the merge's 8 per thread); none (nch 0)
+// when top-k is off, larger than kPartMaxK, or a single chunk would do.
 void topk_split(int V, int top_k, int &nch, int &pch, int &pcap) {
     nch = pch = pcap = 0;
     const int k = (top_k < 0 || top_k >= V) ? 0 : top_k;
     if (k <= 0 || k > kPartMaxK) return;
-    int n = (V + 4095) / 4096;
+    int n = (V + kPartChunk - 1) / kPartChunk;
     if (n * k > kCandCap) n = kCandCap / k;
     if (n < 2) return;
     const int len = ((V + n - 1) / n + 3) & ~3;
@@ -1734,7 +1798,7 @@ int64_t plan_sample_split(SampleArgs &a, int n_rows, char *base) {
     if (a.nch == 0) return 0;
     int64_t off = 0;
     const int64_t slots = (int64_t)n_rows * a.nch * a.pcap;
-    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 4);
+    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 16);
     const int64_t o_v = carve(off, slots * 4);
     const int64_t o_i = carve(off, slots * 4);
     if (base) {
@@ -1755,7 +1819,7 @@ int64_t plan_spec_split(SpecArgs &a, int n_rows, char *base) {
     const int64_t o_r = carve(off, (int64_t)n_rows * a.max_k * 2 * 16);
     const int64_t o_m = carve(off, (int64_t)n_rows * a.sch * 8);
     const int64_t slots = (int64_t)n_rows * a.nch * a.pcap;
-    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 4);
+    const int64_t o_n = carve(off, (int64_t)n_rows * a.nch * 16);
     const int64_t o_v = carve(off, slots * 4);
     const int64_t o_i = carve(off, slots * 4);
     if (base) {
