@@ -1022,17 +1022,37 @@ __device__ __forceinline__ void reg_penalties(const SampleArgs &a, const WinIds 
     __syncthreads();  // the slots alias the candidate list or the row region
 }
 
+// Chunks select on the logits before their division by the temperature t
+// (> 0): fl(x / t) does not decrease as x grows, so the order is the same,
+// and only the candidates are divided.  Entries whose quotient rounds to a
+// bound's quotient lie within a few floats of the bound (in the normal
+// range dividing scales the float spacing by 1/t up to a factor 2 either
+// way, so at most about 6 consecutive floats share a quotient): selecting
+// 16 keys below the raw bound keeps every entry whose quotient reaches the
+// bound's.  Near zero, overflow or underflow every entry is kept instead.
+__device__ __forceinline__ uint32_t div_margin(uint32_t lb, float t) {
+    if (t == 1.f || lb == 0u) return 0u;
+    const float f = fabsf(funkey(lb)), q = fabsf(__fdiv_rn(funkey(lb), t));
+    if (!(f >= 0x1p-60f && f <= 0x1p100f && q >= 0x1p-100f && q <= 0x1p100f)) return lb;
+    return 16u;
+}
+// The key of fl(funkey(k) / t) (k = 0, no bound, stays 0).
+__device__ __forceinline__ uint32_t div_key(uint32_t k, float t) {
+    return (t == 1.f || k == 0u) ? k : fkey(__fdiv_rn(funkey(k), t));
+}
+
 // Candidates from n register-held values (0 < k): the entries at or above a
 // lower bound of their k-th largest, placed in index order.
 //   reg_bound: lb = each wave's ceil(k / kSW)-th largest lane maximum, to 16
 //     key bits, the smallest over the waves (every wave holds that many
 //     entries at or above it: kSW ceil(k / kSW) >= k in all); ub = the
-//     largest key; the kept entries' lane offsets within their (round,
-//     wave) tile and, in s.cnt, the tiles' first slots (an ordered scan);
-//     returns their count (every thread).
+//     largest key; the entries kept (at or above lb, less div_margin for
+//     the division by t still to come); their lane offsets within their
+//     (round, wave) tile and, in s.cnt, the tiles' first slots (an ordered
+//     scan); returns their count (every thread).
 //   reg_place: the kept entries written to dv / di (indices + ioff).
 template <int R, class L>
-__device__ __forceinline__ int reg_bound(const float (&x)[4 * R], int n, int k, L &s, uint32_t (&keep)[R],
+__device__ __forceinline__ int reg_bound(const float (&x)[4 * R], int n, int k, float t, L &s, uint32_t (&keep)[R],
                                          int (&off)[R], uint32_t &lb, uint32_t &ub) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint32_t mk = 0;
@@ -1058,12 +1078,13 @@ __device__ __forceinline__ int reg_bound(const float (&x)[4 * R], int n, int k, 
         lb = min(lb, s.key[w]);
         ub = max(ub, s.key[kSW + w]);
     }
+    const uint32_t th = lb - div_margin(lb, t);
 #pragma unroll
     for (int j = 0; j < R; j++) {
         keep[j] = 0u;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (reg_idx(j, q) < n && fkey(x[4 * j + q]) >= lb) keep[j] |= 1u << q;
+            if (reg_idx(j, q) < n && fkey(x[4 * j + q]) >= th) keep[j] |= 1u << q;
         const int c = __popc(keep[j]);
         const int inc = wave_iscan_dpp(c);
         off[j] = inc - c;
@@ -1098,22 +1119,23 @@ __device__ __forceinline__ void reg_place(const float (&x)[4 * R], const uint32_
     }
 }
 
-// A chunk's top-k candidates written out in index order (indices offset by
-// lo) with the chunk record on = {count, lower bound key, largest key}
-// (count -1: overflow): the reg_bound entries straight from registers when
-// they fit the cap slots; otherwise compacted in LDS, cut to the exact k-th
-// largest (wave 0, one key bit per step; it becomes the lower bound) and
-// written from there.
+// A chunk's top-k candidates (logits not yet divided by t) written out in
+// index order (indices offset by lo) with the chunk record on = {count,
+// lower bound key, largest key} (count -1: overflow; keys of the divided
+// values): the reg_bound entries straight from registers when they fit the
+// cap slots; otherwise compacted in LDS, cut to the exact k-th largest
+// (wave 0, one key bit per step; it becomes the lower bound) and written
+// from there.
 template <int R>
-__device__ __forceinline__ void reg_topk(const float (&x)[4 * R], int n, int k, int lo, int cap, PartLds &s,
-                                         float *ov, int32_t *oi, int32_t *on) {
+__device__ __forceinline__ void reg_topk(const float (&x)[4 * R], int n, int k, float t, int lo, int cap,
+                                         PartLds &s, float *ov, int32_t *oi, int32_t *on) {
     const int tid = threadIdx.x;
     uint32_t keep[R], lb, ub;
     int off[R];
-    const int total = reg_bound<R>(x, n, k, s, keep, off, lb, ub);
+    const int total = reg_bound<R>(x, n, k, t, s, keep, off, lb, ub);
     if (total <= cap) {
         reg_place<R>(x, keep, off, s.cnt, ov, oi, lo);
-        if (tid == 0) *(int4 *)on = make_int4(total, (int)lb, (int)ub, 0);
+        if (tid == 0) *(int4 *)on = make_int4(total, (int)div_key(lb, t), (int)div_key(ub, t), 0);
         return;
     }
     int m = -1;
@@ -1122,14 +1144,15 @@ __device__ __forceinline__ void reg_topk(const float (&x)[4 * R], int n, int k, 
         reg_place<R>(x, keep, off, s.cnt, s.cv, s.ci, 0);
         __syncthreads();
         tk = kth_key_w0(total, k, s, [&](int i) { return fkey(s.cv[i]); });
-        m = filter_w0(total, s, [&](float v) { return fkey(v) >= tk; });
+        const uint32_t th = tk - div_margin(tk, t);
+        m = filter_w0(total, s, [&](float v) { return fkey(v) >= th; });
         if (m > cap) m = -1;
         for (int j = tid; j < m; j += kST) {
             ov[j] = s.cv[j];
             oi[j] = lo + s.ci[j];
         }
     }
-    if (tid == 0) *(int4 *)on = make_int4(m, (int)tk, (int)ub, 0);
+    if (tid == 0) *(int4 *)on = make_int4(m, (int)div_key(tk, t), (int)div_key(ub, t), 0);
 }
 
 // k-th largest of n keys (0 when n < k), given that it lies in [lo, hi]
@@ -1286,13 +1309,15 @@ __device__ __forceinline__ int finish_list64(int n, int V, float top_p, float mi
 }
 
 // Row b's chunk lists merged, in chunk order, into the working set's
-// candidate list (mode 1): every thread loads its slots while wave 0 scans
-// the chunk records {count, lower bound key, largest key}; lb / ub: the
-// largest lower bound and the largest key (the row's k-th largest lies
-// between them); false, for the whole work-group, when a chunk overflowed
-// or the lists pass kCandCap.
+// candidate list (mode 1), each value divided by the temperature t here
+// (sampler.go:94-97): every thread loads its slots while wave 0 scans the
+// chunk records {count, lower bound key, largest key}; lb / ub: the largest
+// lower bound and the largest key (the row's k-th largest lies between
+// them); false, for the whole work-group, when a chunk overflowed or the
+// lists pass kCandCap.
 __device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, const int32_t *pn, int nch,
-                                           int cap, int V, Src &c, uint32_t &lb, uint32_t &ub, SampLds &s) {
+                                           int cap, int V, float t, Src &c, uint32_t &lb, uint32_t &ub,
+                                           SampLds &s) {
     constexpr int kSlots = 8;  // nch * cap <= kSlots * kST
     const int tid = threadIdx.x;
     const int ns = nch * cap;
@@ -1334,7 +1359,7 @@ __device__ __forceinline__ bool part_merge(const float *pv, const int32_t *pi, c
         if (j < ns) {
             const int ch = j / cap, e = j - ch * cap;
             if (e < s.cnt[ch]) {
-                s.cv[(int)s.key[ch] + e] = v[r];
+                s.cv[(int)s.key[ch] + e] = t == 1.f ? v[r] : __fdiv_rn(v[r], t);
                 s.ci[(int)s.key[ch] + e] = ix[r];
             }
         }
@@ -1362,8 +1387,9 @@ __device__ __forceinline__ int part_finish(Src &c, uint32_t lb, uint32_t ub, int
     return sample_finish<1>(c, top_p, min_p, r, s);
 }
 
-// One chunk [lo, lo + n) of a row: its values (the penalties of Sample's
-// arguments a when PEN, then the temperature t), its candidates written out.
+// One chunk [lo, lo + n) of a row: its logits (with the penalties of
+// Sample's arguments a when PEN), its candidates written out; the merge
+// divides them by the temperature t.
 template <int R, bool PEN, class A>
 __device__ __forceinline__ void part_chunk(const A &a, const float *row, int lo, int n, float t, int k, int cap,
                                            PartLds &s, float *ov, int32_t *oi, int32_t *on) {
@@ -1374,10 +1400,7 @@ __device__ __forceinline__ void part_chunk(const A &a, const float *row, int lo,
         win_load(a, blockIdx.x, w);
         reg_penalties<R>(a, w, lo, n, x, s.pcw);
     }
-    if (t != 1.f)
-#pragma unroll
-        for (int j = 0; j < 4 * R; j++) x[j] = __fdiv_rn(x[j], t);
-    reg_topk<R>(x, n, k, lo, cap, s, ov, oi, on);
+    reg_topk<R>(x, n, k, t, lo, cap, s, ov, oi, on);
 }
 
 // Phase one of the split Sample: chunk blockIdx.y of row blockIdx.x.
@@ -1415,8 +1438,10 @@ __global__ __launch_bounds__(kST) void sample_kernel(const SampleArgs a) {
     if (a.nch > 0) {
         const int64_t q = (int64_t)b * a.nch;
         uint32_t lb, ub;
-        if (part_merge(a.part_v + q * a.pcap, a.part_i + q * a.pcap, a.part_n + 4 * q, a.nch, a.pcap, a.V, c, lb,
-                       ub, s)) {
+        float t = a.temperature;
+        if (t <= 0.f) t = 1e-5f;
+        if (part_merge(a.part_v + q * a.pcap, a.part_i + q * a.pcap, a.part_n + 4 * q, a.nch, a.pcap, a.V, t, c,
+                       lb, ub, s)) {
             const int t =
                 part_finish(c, lb, ub, clamp_topk(a.top_k, a.V), clamp_topp(a.top_p), a.min_p, a.u[b], s);
             if (threadIdx.x == 0) a.out[b] = t;
@@ -1703,9 +1728,11 @@ __global__ __launch_bounds__(kST) void spec_final_kernel(const SpecArgs a) {
     int t;
     Src c;
     uint32_t lb, ub;
+    float tt = a.temperature;
+    if (tt <= 0.f) tt = 1e-5f;
     if (a.nch > 0 &&
         part_merge(a.part_v + (int64_t)b * a.nch * a.pcap, a.part_i + (int64_t)b * a.nch * a.pcap,
-                   a.part_n + (int64_t)b * a.nch * 4, a.nch, a.pcap, V, c, lb, ub, s)) {
+                   a.part_n + (int64_t)b * a.nch * 4, a.nch, a.pcap, V, tt, c, lb, ub, s)) {
         t = part_finish(c, lb, ub, clamp_topk(a.top_k, V), clamp_topp(a.top_p), a.min_p, u[k], s);
     } else {
         load_row(

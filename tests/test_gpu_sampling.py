@@ -62,6 +62,9 @@ PARAMS = {
     "topp0.9": S.SamplerParams(top_p=0.9),
     "minp0.05": S.SamplerParams(min_p=0.05),
     "all": S.SamplerParams(temperature=0.8, top_k=40, top_p=0.95, min_p=0.02),
+    # top-k chunks select before the division by the temperature
+    "topk5_t0": S.SamplerParams(top_k=5, temperature=0.0),
+    "topk40_t25": S.SamplerParams(top_k=40, temperature=25.0, top_p=0.9),
     "penalties": S.SamplerParams(repeat_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.3,
                                  repeat_window=16),
 }
@@ -72,7 +75,7 @@ PARAMS = {
 # and V past 4096 the vocabulary is split over work-groups (V 32000: 8
 # chunks; V 50000: 13), each keeping its own candidates.
 CASES = [(n, V) for V in (100, 4096) for n in sorted(PARAMS)] + \
-    [(n, 32000) for n in ("topk5", "topk50_t1.3", "all")] + \
+    [(n, 32000) for n in ("topk5", "topk50_t1.3", "all", "topk5_t0", "topk40_t25")] + \
     [(n, 50000) for n in ("plain", "temp0.7", "topk5", "all", "penalties")]
 
 
