@@ -190,15 +190,20 @@ __device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, 
 #pragma unroll
         for (int i = 0; i < 4; i++) o.c[i] = o.s[i] = 0.f;
         if (hw && rcos) {  // tables given: row 0 exists, so every load is in bounds
-            int sp[16];
+            // the wave's 16 row positions (scalar loads), the lane's 4 rows
+            // (group grp) picked as they arrive: constant indices only, so
+            // nothing goes through a private array
+            int mine[4] = {0, 0, 0, 0};
             kint *kp = (kint *)(kernarg_plan() + pos_off);
 #pragma unroll
-            for (int j = 0; j < 16; j++)  // scalar: the lane's rows are picked below
-                sp[j] = __builtin_amdgcn_readfirstlane(kp[min(m * 16 + j, rows - 1)]);
+            for (int j = 0; j < 16; j++) {
+                const int v = __builtin_amdgcn_readfirstlane(kp[min(m * 16 + j, rows - 1)]);
+                if ((j >> 2) == grp) mine[j & 3] = v;
+            }
             const int dr = o.nn % hw;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int p = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
+                const int p = mine[i];
                 o.rot |= (p >= 0 && dr < tw) << i;
                 // unconditional (no branch, so no wait at a join): row max(p, 0),
                 // pair min(dr, tw - 1) / 2 (padding dims past tw do not rotate)
@@ -211,23 +216,28 @@ __device__ __forceinline__ void proj_place_kernarg(ProjPlace &o, int m, int n0, 
 }
 
 // Append slots of the wave's 16 rows from the kernel-argument plan (scalar
-// loads into sp / ss), and the lane's 4 rows picked from them by its group.
-__device__ __forceinline__ void proj_slots_kernarg_load(int sp[16], int ss[16], int m, int rows,
-                                                        int tok_off) {
+// loads), the lane's 4 rows (group grp) picked as they arrive into
+// sp / ss[4] (constant indices only: no private array).
+__device__ __forceinline__ void proj_slots_kernarg_load(int sp[4], int ss[4], int m, int rows, int tok_off,
+                                                        int grp) {
     typedef const __attribute__((address_space(4))) int32_t kint;
     kint *kt = (kint *)(kernarg_plan() + tok_off);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
         const int r = min(m * 16 + j, rows - 1);
-        sp[j] = __builtin_amdgcn_readfirstlane(kt[r * 4]);
-        ss[j] = __builtin_amdgcn_readfirstlane(kt[r * 4 + 1]);
+        const int pg = __builtin_amdgcn_readfirstlane(kt[r * 4]);
+        const int sl = __builtin_amdgcn_readfirstlane(kt[r * 4 + 1]);
+        if ((j >> 2) == grp) {
+            sp[j & 3] = pg;
+            ss[j & 3] = sl;
+        }
     }
 }
-__device__ __forceinline__ void proj_slots_pick(ProjPlace &o, const int sp[16], const int ss[16], int grp) {
+__device__ __forceinline__ void proj_slots_pick(ProjPlace &o, const int sp[4], const int ss[4]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        o.page[i] = grp == 0 ? sp[i] : (grp == 1 ? sp[4 + i] : (grp == 2 ? sp[8 + i] : sp[12 + i]));
-        o.slot[i] = grp == 0 ? ss[i] : (grp == 1 ? ss[4 + i] : (grp == 2 ? ss[8 + i] : ss[12 + i]));
+        o.page[i] = sp[i];
+        o.slot[i] = ss[i];
     }
 }
 
@@ -503,12 +513,12 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     __builtin_amdgcn_sched_barrier(0);
     // RoPE table reads of the output waves behind them: they retire with the
     // last fragment, so the output stage waits for no further load.
-    int sp[16], ss[16];  // append slots of the output wave's rows (scalar)
+    int sp[4] = {0, 0, 0, 0}, ss[4] = {0, 0, 0, 0};  // append slots of the lane's rows
     if (kEarly && wave < TPW * MT) {
         proj_place_kernarg<MODEL>(pl, em, etile * 16, col, grp, rows, pos_off, pd, rcos, rsin);
         if constexpr (MODEL != kProjOut) {
             const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
-            if (!to_q) proj_slots_kernarg_load(sp, ss, em, rows, tok_off);
+            if (!to_q) proj_slots_kernarg_load(sp, ss, em, rows, tok_off, grp);
         }
     }
     if constexpr (XBF16) {
@@ -576,7 +586,7 @@ __global__ __launch_bounds__(64 * kSkMaxWaves) void proj_skinny_kernel(
     if constexpr (kEarly) {
         if constexpr (MODEL != kProjOut) {
             const bool to_q = (MODEL == kProjGQA) ? pl.part == 0 : pl.part < 2;
-            if (!to_q) proj_slots_pick(pl, sp, ss, grp);
+            if (!to_q) proj_slots_pick(pl, sp, ss);
         }
     } else {
         proj_place_plan<ARG, MODEL>(pl, pos, em, etile * 16 + col, grp, rows, toks, pos_dev, tok_off,
