@@ -359,7 +359,8 @@ def setup_accept(cfg, torch, dev, rng):
     reference's acceptPhase examines (draft and target row of each tested
     draft, plus the next target row when all are accepted), counted after
     the run from each timed call's accepted counts (kept on the device, one
-    row per call)."""
+    row per call).  The kernel time spans the call's three launches (HIP
+    events before the first and after the last)."""
     import numpy as np
     from relux_amd import Sampler, spec_accept_async
     B, K, V = cfg["B"], cfg["K"], cfg["V"]
@@ -392,7 +393,7 @@ def setup_accept(cfg, torch, dev, rng):
     desc = {"workload": f"spec_accept B{B} drafts{K} V{V} (acceptPhase + resample, T0.8 top-k50 top-p0.9; "
                         f"device-resident, no host sync per step)",
             "batch": B, "drafts": K, "vocab": V, "state": state, "finish": finish}
-    return c, step, B, 0, 0, desc, "spec_accept_kernel", None
+    return c, step, B, 0, 0, desc, "spec_stat_kernel+spec_mass_kernel+spec_final_kernel", None
 
 
 def setup_sample(cfg, torch, dev, rng):
@@ -401,7 +402,8 @@ def setup_sample(cfg, torch, dev, rng):
     decode loop's form (rlx_sample_async): logits, each row's token history
     (256 entries, the last 64 counted), the draws and the chosen tokens all
     stay on the device, and the windows are counted in the kernel.
-    Algorithmic bytes: each logit row once plus the window ids."""
+    Algorithmic bytes: each logit row once plus the window ids.  The kernel
+    time spans the call's two launches (vocabulary chunks, then the rows)."""
     from relux_amd import Sampler
     B, V, S = cfg["B"], cfg["V"], 256
     c = _select_handle(dev)
@@ -421,7 +423,7 @@ def setup_sample(cfg, torch, dev, rng):
     desc = {"workload": f"sample B{B} V{V} (penalties/64 of a 256-token device history, T0.8, "
                         f"top-k50, top-p0.9, min-p0.02; device-resident, no host sync per step)",
             "batch": B, "vocab": V}
-    return c, step, B, b, b, desc, "sample_kernel", None
+    return c, step, B, b, b, desc, "sample_part_kernel+sample_kernel", None
 
 
 def setup_spill(cfg, torch, dev, rng):
