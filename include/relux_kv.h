@@ -433,8 +433,11 @@ int32_t rlx_sample(void *cache, const float *logits, int32_t n_rows, int32_t voc
  * (RLX_ERR_UNSUPPORTED otherwise).  history NULL: no penalties.  uniforms
  * (the rng.Float32() draws) are device f32 [n_rows]; out_tokens device
  * int32 [n_rows].  Enqueued on the cache's stream: nothing is copied to or
- * from the host and the call does not wait.  Same tokens as rlx_sample
- * given the same windows and draws. */
+ * from the host and the call does not wait -- except the first call that
+ * needs a larger cache workspace (the split path's chunk lists, top-k in
+ * (0, 256] past 8192 entries), which synchronises the stream and
+ * allocates it once.  Same tokens as rlx_sample given the same windows
+ * and draws. */
 int32_t rlx_sample_async(void *cache, const float *logits, int32_t n_rows, int32_t vocab,
                          int64_t row_stride, const rlx_sampler_t *params, const int32_t *history,
                          int64_t hist_stride, const int32_t *hist_len, const float *uniforms,
@@ -460,7 +463,9 @@ int32_t rlx_spec_accept(void *cache, const float *draft_logits, const float *tar
  * and ids are not seen by the host: a count is clamped to [0, max_k] and
  * an id outside [0, vocab) is treated as a rejection at its position.
  * Enqueued on the cache's stream; nothing is copied and the call does not
- * wait.  Same results as rlx_spec_accept on valid inputs. */
+ * wait -- except the first call that needs a larger cache workspace (the
+ * per-draft figures and chunk sums), which synchronises the stream and
+ * allocates it once.  Same results as rlx_spec_accept on valid inputs. */
 int32_t rlx_spec_accept_async(void *cache, const float *draft_logits, const float *target_logits,
                               const int32_t *draft_tokens, const int32_t *n_draft, int32_t n_rows,
                               int32_t max_k, int32_t vocab, const float *uniforms,
