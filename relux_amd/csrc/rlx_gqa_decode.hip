@@ -451,14 +451,17 @@ __global__ __launch_bounds__(256, (gqa_min_waves<D, NQT>())) void gqa_decode_ker
     }
 }
 
-// Merge the partials (one per segment of the row) of one (row, kv head,
-// query row): O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s, written in the
-// caller's layout and dtype.  One block of max(D, 64) threads per query row,
-// thread d owning dim d.  With at most kFewParts partials (the usual case)
-// every thread loads all (m, l) pairs and its dim of every partial at once
-// and computes the weights itself (no LDS); with more, wave 0 computes the
-// weights once in LDS and every thread streams its dim across the partials.
-constexpr int kFewParts = 8;  // partials merged without LDS (one round trip)
+// Merge the partials (one per segment of the row) of a (row, kv head) for
+// some of its query rows: O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s,
+// written in the caller's layout and dtype.  Work-group = 256 threads over
+// TQ = 256 / (D/4) consecutive query rows (blockIdx.z), thread (row j,
+// quad d4) owning dims 4 d4 .. 4 d4 + 3 of query row j: one float4 of each
+// partial, so a verify call's 32 query rows take 4-8 work-groups instead of
+// one each.  With at most kFewParts partials (the usual case) every load is
+// issued at once -- one memory round trip -- and each thread computes its
+// row's weights itself; with more, the partials are walked in batches of
+// kFewParts after a first pass for the maximum.
+constexpr int kFewParts = 8;  // partials merged in one round trip
 
 template <bool ARG>
 __global__ __launch_bounds__(256) void gqa_combine_kernel(
@@ -467,66 +470,87 @@ __global__ __launch_bounds__(256) void gqa_combine_kernel(
     int out_bf16, int layout, int H, int KVH, int D, int DQ, int QRP) {
     const AttRow R = plan_row<ARG>(rows, blockIdx.x);
     const int kvh = blockIdx.y;
-    const int qr = blockIdx.z;
+    const int Q4 = D >> 2;              // quads per query row
+    const int TQ = 256 / Q4;            // query rows per work-group
+    const int t = threadIdx.x;
+    const int qr = blockIdx.z * TQ + t / Q4;
+    const int d0 = (t - (t / Q4) * Q4) * 4;
     const int G = H / KVH;
-    if (qr >= G * R.qn) return;
-    __shared__ float fac[kMaxSplits];
-    __shared__ float inv_l;
+    if (t >= TQ * Q4 || qr >= G * R.qn) return;
     const int64_t b0 = ((int64_t)R.part * KVH + kvh) * QRP + qr;  // first partial
     const int64_t sstride = (int64_t)KVH * QRP;                    // between partials
-    const int ql = qr / G;
-    const int h = kvh * G + (qr - ql * G);
-    const int qi = R.q0 + ql;
     const int n = R.nsplit;
+    float M = -INFINITY, L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto add = [&](float m, float l, const float4 &o) {
+        const float f = (m == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m - M);
+        L += f * l;
+        O.x += f * o.x;
+        O.y += f * o.y;
+        O.z += f * o.z;
+        O.w += f * o.w;
+    };
     if (n <= kFewParts) {
-        // Few partials (the usual case): every thread loads all (m, l) pairs
-        // and its dim of every partial at once -- one memory round trip, no
-        // LDS; partials past n re-read the last one and get weight 0.
-        const int d = threadIdx.x;
-        float mv[kFewParts], lv[kFewParts], ov[kFewParts];
+        // partials past n re-read the last one and get weight 0
+        float2 ml[kFewParts];
+        float4 ov[kFewParts];
 #pragma unroll
         for (int s = 0; s < kFewParts; s++) {
             const int64_t bs = b0 + (int64_t)min(s, n - 1) * sstride;
-            mv[s] = part_ml[bs * 2];
-            lv[s] = part_ml[bs * 2 + 1];
-            ov[s] = d < D ? part_o[bs * D + d] : 0.f;
+            ml[s] = *(const float2 *)(part_ml + bs * 2);
+            ov[s] = *(const float4 *)(part_o + bs * D + d0);
         }
-        float M = -INFINITY;
 #pragma unroll
         for (int s = 0; s < kFewParts; s++)
-            if (s < n) M = fmaxf(M, mv[s]);
-        float L = 0.f, O = 0.f;
+            if (s < n) M = fmaxf(M, ml[s].x);
 #pragma unroll
-        for (int s = 0; s < kFewParts; s++) {
-            const float f = (s < n && mv[s] != -INFINITY) ? __builtin_amdgcn_exp2f(mv[s] - M) : 0.f;
-            L += f * lv[s];
-            O += f * ov[s];
+        for (int s = 0; s < kFewParts; s++)
+            if (s < n) add(ml[s].x, ml[s].y, ov[s]);
+    } else {
+        for (int s = 0; s < n; s++) M = fmaxf(M, part_ml[(b0 + (int64_t)s * sstride) * 2]);
+        for (int s0 = 0; s0 < n; s0 += kFewParts) {
+            float2 ml[kFewParts];
+            float4 ov[kFewParts];
+#pragma unroll
+            for (int s = 0; s < kFewParts; s++) {
+                const int64_t bs = b0 + (int64_t)min(s0 + s, n - 1) * sstride;
+                ml[s] = *(const float2 *)(part_ml + bs * 2);
+                ov[s] = *(const float4 *)(part_o + bs * D + d0);
+            }
+#pragma unroll
+            for (int s = 0; s < kFewParts; s++)
+                if (s0 + s < n) add(ml[s].x, ml[s].y, ov[s]);
         }
-        if (d < DQ) {
-            const float v = O * (L > 0.f ? 1.f / L : 0.f);
-            const int64_t o = (layout == kLayoutSHD)
-                                  ? ((int64_t)(R.qrow + qi) * H + h) * DQ + d
-                                  : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ + d;
-            if (out_bf16)
-                ((uint16_t *)out)[o] = bf16_rne(v);
-            else
-                ((float *)out)[o] = v;
-        }
-        return;
     }
-    merge_weights(part_ml + b0 * 2, sstride, n, fac, &inv_l);
-    __syncthreads();
-    for (int d = threadIdx.x; d < DQ; d += blockDim.x) {
-        float O = 0.f;
-        for (int s = 0; s < R.nsplit; s++) O += fac[s] * part_o[(b0 + s * sstride) * D + d];
-        const float v = O * inv_l;
-        const int64_t o = (layout == kLayoutSHD)
-                              ? ((int64_t)(R.qrow + qi) * H + h) * DQ + d
-                              : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ + d;
-        if (out_bf16)
-            ((uint16_t *)out)[o] = bf16_rne(v);
-        else
-            ((float *)out)[o] = v;
+    if (d0 >= DQ) return;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float v[4] = {O.x * inv, O.y * inv, O.z * inv, O.w * inv};
+    const int ql = qr / G;
+    const int h = kvh * G + (qr - ql * G);
+    const int qi = R.q0 + ql;
+    const int64_t o = (layout == kLayoutSHD) ? ((int64_t)(R.qrow + qi) * H + h) * DQ + d0
+                                             : ((int64_t)R.qrow * H + (int64_t)h * R.nq + qi) * DQ + d0;
+    // DQ is a multiple of 8: the 4 dims are all in or all out; one store
+    // when the caller's buffer is aligned for it
+    const bool vec = (((uintptr_t)out) & (out_bf16 ? 7 : 15)) == 0;
+    if (out_bf16) {
+        uint16_t *dst = (uint16_t *)out + o;
+        if (vec) {
+            const uint32_t lo = bf16_rne(v[0]) | ((uint32_t)bf16_rne(v[1]) << 16);
+            const uint32_t hi = bf16_rne(v[2]) | ((uint32_t)bf16_rne(v[3]) << 16);
+            *(uint2 *)dst = make_uint2(lo, hi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[i] = bf16_rne(v[i]);
+        }
+    } else {
+        float *dst = (float *)out + o;
+        if (vec) {
+            *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[i] = v[i];
+        }
     }
 }
 
@@ -544,7 +568,8 @@ static hipError_t launch_gqa_t(hipStream_t s, typename PlanSel<ARG>::T plan,
                                 layout, H, KVH, DQ, P, total64, snap64, ranges_off, qscale,
                                 mask_mode, part_o, part_ml);
     if (e != hipSuccess) return e;
-    gqa_combine_kernel<ARG><<<dim3(n_rows, KVH, max_qr), (D < 64 ? 64 : D), 0, s>>>(
+    constexpr int TQ = 256 / (D / 4);  // query rows per combine work-group
+    gqa_combine_kernel<ARG><<<dim3(n_rows, KVH, (max_qr + TQ - 1) / TQ), 256, 0, s>>>(
         plan, rows, part_o, part_ml, out, out_bf16, layout, H, KVH, D, DQ, 16 * NQT);
     return hipGetLastError();
 }
