@@ -535,10 +535,11 @@ __device__ __forceinline__ void ring_barrier() {
 constexpr int kPrefillRows = 256;
 
 struct PrefillArgs {
-    const uint16_t *kpool;  // paged: K pages (k-step-major 16-token blocks); dense: latent pool (rope keys)
+    const uint16_t *kpool;  // paged: K pages (k-step-major 16-token blocks)
     const uint16_t *vpool;  // paged: V dim-major pages
     const uint16_t *kc;     // dense: K_c [H][Tp][vd] of the H heads expanded, sequence s at + part*H*vd
     const uint16_t *vt;     // dense: V^T [H][vd][Tp], same sequence offsets
+    const uint16_t *kr;     // dense: rope keys [Tp][64] per sequence, sequence s at row part
     const int32_t *table;
     const AttRow *rows;     // dense: part = token offset of the sequence, nsplit = Tp
     const int4 *work;       // (row, head group, query tile, unused)
@@ -567,6 +568,9 @@ hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_
                          int dc, int DP, uint16_t *wt_k, uint16_t *wt_v);
 // K_c [H][Tp][DP] / V^T [H][DP][Tp] of H heads from their transposed weights
 // (wt_k, wt_v: the heads' rows of the transposed matrices).
+hipError_t launch_mla_rope_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                                  const AttRow *rows, const int2 *work, int n_work, int P,
+                                  uint16_t *kr);
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, const int2 *work, int n_work, int H, int DP, int P,
                              const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,

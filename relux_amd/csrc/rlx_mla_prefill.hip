@@ -266,6 +266,37 @@ hipError_t launch_mla_wt(hipStream_t s, const uint16_t *w_uk, const uint16_t *w_
     return hipGetLastError();
 }
 
+// Rope keys of the call, kr[part + t][0 .. 64) = latent row t's k^R (the
+// last 64 entries of the stored row), zero for padding rows t >= len.  One
+// block per expansion work item (sequence, 128 tokens); 16-byte chunks.  The
+// FA2 kernel then reads each 64-key block's rope keys as one contiguous 8 KB
+// region through a running pointer, like K_c.
+__global__ __launch_bounds__(256) void mla_rope_gather_kernel(const uint16_t *__restrict__ pool,
+                                                              const int32_t *__restrict__ table,
+                                                              const AttRow *__restrict__ rows,
+                                                              const int2 *__restrict__ work, int P,
+                                                              uint16_t *__restrict__ kr) {
+    const int2 wk = work[blockIdx.x];
+    const AttRow R = rows[wk.x];
+    for (int e = threadIdx.x; e < 128 * (kMlaDr / 8); e += blockDim.x) {
+        const int t = wk.y + e / (kMlaDr / 8), ch = e % (kMlaDr / 8);
+        u32x4 v = u32x4{0, 0, 0, 0};
+        if (t < R.len) {
+            const int page = table[R.tab + t / P];
+            v = *(const u32x4 *)(pool + ((int64_t)page * P + t % P) * kMlaRow + kMlaDc + ch * 8);
+        }
+        *(u32x4 *)(kr + ((int64_t)R.part + t) * kMlaDr + ch * 8) = v;
+    }
+}
+
+hipError_t launch_mla_rope_gather(hipStream_t s, const uint16_t *pool, const int32_t *table,
+                                  const AttRow *rows, const int2 *work, int n_work, int P,
+                                  uint16_t *kr) {
+    if (n_work <= 0) return hipSuccess;
+    mla_rope_gather_kernel<<<n_work, 256, 0, s>>>(pool, table, rows, work, P, kr);
+    return hipGetLastError();
+}
+
 hipError_t launch_mla_expand(hipStream_t s, const uint16_t *pool, const int32_t *table,
                              const AttRow *rows, const int2 *work, int n_work, int H, int DP, int P,
                              const uint16_t *wt_k, const uint16_t *wt_v, uint16_t *kc, uint16_t *vt,

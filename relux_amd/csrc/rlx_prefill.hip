@@ -23,8 +23,10 @@
 //   kSrcPaged : GQA paged cache, K pages (k-step-major 16-token blocks) and
 //               dim-major V pages, DQK = DV = D.
 //   kSrcDense : MLA, per sequence decompressed K_c [H][Tp][128] and
-//               V^T [H][128][Tp] (Tp = T rounded up to 128) plus the rope key
-//               k^R read from the paged latent rows; DQK = 192, DV = 128.
+//               V^T [H][128][Tp] (Tp = T rounded up to 128) plus the rope keys
+//               k^R [Tp][64] gathered from the latent rows once per call
+//               (shared by every head, addressed like K_c: no page-table
+//               reads in the key loop); DQK = 192, DV = 128.
 // Keys at or past the live length are masked; the K rows staged for them
 // repeat the last live key and their V^T entries are zeroed in LDS, so
 // nothing past the live length can reach the output.
@@ -55,8 +57,8 @@ __device__ __forceinline__ int pf_limit(int mask_mode, int len, int nq, int qi) 
 // output is unchanged.
 //
 // LDS stage: K regions of [64 keys][8 chunks] (64 dims each: the paged K
-// row split in DQK/64 regions; dense: K_c in two, then the rope keys from
-// the latent pages) and the V^T region [DV][8 chunks].  Every region has a
+// row split in DQK/64 regions; dense: K_c in two, then the rope keys) and
+// the V^T region [DV][8 chunks].  Every region has a
 // 128-byte row pitch and the same swizzle, chunk c of row r at c ^ ((r/2) & 7):
 // the LDS serves a 16-byte read for 16 lanes per cycle from 64 banks, and
 // any 16 consecutive rows -- two per 256-byte bank row -- then fill 16
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         else if (q < NKR - 1)
             ko[q] = (uint32_t)(kr * DP + 64 * q + klc * 8) * 2;
         else
-            ko[q] = (uint32_t)((kr & 15) * kMlaRow + kMlaDc + klc * 8) * 2;
+            ko[q] = (uint32_t)(kr * kMlaDr + klc * 8) * 2;
     }
     // V^T load i: row vd, logical chunk vlc (keys 8 vlc .. 8 vlc + 7).
     int vd[LV], vlc[LV];
@@ -142,14 +144,15 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     }
     auto pdiv = [&](int t) { return POW2 ? t >> a.pshift : t / a.P; };
     auto pmod = [&](int t) { return POW2 ? t & (a.P - 1) : t % a.P; };
-    const uint16_t *kc_seq = nullptr, *vt_seq = nullptr;
+    const uint16_t *kc_seq = nullptr, *vt_seq = nullptr, *kr_seq = nullptr;
     if (SRC == kSrcDense) {
         kc_seq = a.kc + ((int64_t)R.part * a.H + (int64_t)hg * R.nsplit) * DP;
         vt_seq = a.vt + (int64_t)R.part * a.H * DP + (int64_t)hg * DP * R.nsplit;
+        kr_seq = a.kr + (int64_t)R.part * kMlaDr;
     }
-    // Blocks are issued in order, one per call: running K_c / V^T pointers
-    // and stage offset of the next block to issue.
-    const uint16_t *kc_next = kc_seq, *vt_next = vt_seq;
+    // Blocks are issued in order, one per call: running K_c / V^T / rope-key
+    // pointers and stage offset of the next block to issue.
+    const uint16_t *kc_next = kc_seq, *vt_next = vt_seq, *kr_next = kr_seq;
     uint32_t st_next = 0;
     constexpr uint32_t kStageBytes = SH::ST * 16;
 
@@ -169,25 +172,25 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const int k0 = j * kKeyBlock;
         const uint32_t stage = ring_lds + st_next;
         const uint32_t kdst = stage + (uint32_t)(wave * 64) * 16;  // + region q: q * 8 KB
-        const uint16_t *kc_blk = kc_next, *vt_blk = vt_next;
+        const uint16_t *kc_blk = kc_next, *vt_blk = vt_next, *kr_blk = kr_next;
         st_next = (st_next + kStageBytes == S * kStageBytes) ? 0u : st_next + kStageBytes;
         if (SRC == kSrcDense) {
             kc_next += kKeyBlock * DP;
             vt_next += kKeyBlock;
+            kr_next += kKeyBlock * kMlaDr;
         }
         if (k0 + kKeyBlock <= R.len) {
             // Every key of the block is live.  K: the wave's 8 rows lie in
             // 16-key group wave / 2.
-            const int tg = k0 + 16 * (wave >> 1);
             if (SRC == kSrcPaged) {
+                const int tg = k0 + 16 * (wave >> 1);
                 const uint16_t *b = a.kpool + (((int64_t)page_of(tg) * a.KVH + hg) * a.P + pmod(tg)) * DQK;
 #pragma unroll
                 for (int q = 0; q < NKR; q++) lds_dma16(b, ko[q], kdst + q * 8192);
             } else {
 #pragma unroll
                 for (int q = 0; q < NKR - 1; q++) lds_dma16(kc_blk, ko[q], kdst + q * 8192);
-                const uint16_t *r = a.kpool + ((int64_t)page_of(tg) * a.P + pmod(tg)) * kMlaRow;
-                lds_dma16(r, ko[NKR - 1], kdst + (NKR - 1) * 8192);
+                lds_dma16(kr_blk, ko[NKR - 1], kdst + (NKR - 1) * 8192);
             }
             if (SRC == kSrcPaged) {
                 int pg[4];
@@ -213,7 +216,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         // chunk (their entries are zeroed in LDS before use).
         {
             const int t = min(k0 + kr, R.len - 1);
-            const int pgt = table[R.tab + pdiv(t)];
+            const int pgt = SRC == kSrcPaged ? table[R.tab + pdiv(t)] : 0;
 #pragma unroll
             for (int q = 0; q < NKR; q++) {
                 const uint16_t *gp;
@@ -222,7 +225,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                 else if (q < NKR - 1)
                     gp = kc_seq + (int64_t)t * DP + 64 * q + klc * 8;
                 else
-                    gp = a.kpool + ((int64_t)pgt * a.P + pmod(t)) * kMlaRow + kMlaDc + klc * 8;
+                    gp = kr_seq + (int64_t)t * kMlaDr + klc * 8;
                 lds_dma16(gp, __builtin_amdgcn_readfirstlane(kdst + q * 8192));
             }
         }
@@ -349,7 +352,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     for (int j = 0, st_read = 0; j < nblk; j++, st_read = (st_read + SH::ST * 8 == S * SH::ST * 8) ? 0 : st_read + SH::ST * 8) {
         wait_block(j);
         ring_barrier();
-        if (j + S - 1 < nblk) issue_block(j + S - 1);
+        if (SRC == kSrcPaged && j + S - 1 < nblk) issue_block(j + S - 1);
         const int k0 = j * kKeyBlock;
         const uint16_t *st = ring + st_read;
         if (k0 + kKeyBlock > R.len) {
@@ -451,6 +454,12 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         }
 #pragma unroll
         for (int k = KS - 2; k < 8; k++) pword(0, k);  // (what did not fit)
+        // Dense sources refill the stage the barrier released with block
+        // j + S - 1 here, between the score and the P.V products, so that a
+        // load stalled by memory back-pressure does not hold up this block's
+        // score reads (config 4: -0.5 %).  (The paged source issues right
+        // after the barrier: its block loads wait on page-table reads.)
+        if (SRC == kSrcDense && j + S - 1 < nblk) issue_block(j + S - 1);
         if (need_mask) mask(1);
         fixup(0);
         // P.V with the V^T operands kPfD steps ahead; tile 1's weights during

@@ -1771,7 +1771,8 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         if ((rc = flush_patches(c))) return rc;
         const size_t w_bytes = (size_t)num_heads * dp * kMlaDc * 2;
         const size_t e_bytes = (size_t)tok_off * hg * dp * 2;
-        if ((rc = ensure_ws(c, 2 * w_bytes + 2 * e_bytes))) return rc;
+        const size_t r_bytes = (size_t)tok_off * kMlaDr * 2;  // rope keys of the call
+        if ((rc = ensure_ws(c, 2 * w_bytes + 2 * e_bytes + r_bytes))) return rc;
         Blob b;
         size_t o_r = b.add(rows), o_d = b.add(dwork), o_p = b.add(pwork);
         void *dev;
@@ -1779,9 +1780,12 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         char *ws = (char *)c->ws;
         uint16_t *wt_k = (uint16_t *)ws, *wt_v = (uint16_t *)(ws + w_bytes);
         uint16_t *kc = (uint16_t *)(ws + 2 * w_bytes), *vt = (uint16_t *)(ws + 2 * w_bytes + e_bytes);
+        uint16_t *kr = (uint16_t *)(ws + 2 * w_bytes + 2 * e_bytes);
         const AttRow *drows = (const AttRow *)((char *)dev + o_r);
         HIP_TRY(launch_mla_wt(c->stream, (const uint16_t *)w_uk, (const uint16_t *)w_uv, num_heads, head_dim,
                               c->dc, dp, wt_k, wt_v));
+        HIP_TRY(launch_mla_rope_gather(c->stream, ls.pool0, c->d_table, drows,
+                                       (const int2 *)((char *)dev + o_d), (int)dwork.size(), c->P, kr));
         if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + c->dr)));
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1))) return rc;
@@ -1792,9 +1796,9 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
                                       c->P, wt_k + (size_t)h0 * dp * kMlaDc,
                                       wt_v + (size_t)h0 * dp * kMlaDc, kc, vt, c->cus));
             PrefillArgs a{};
-            a.kpool = ls.pool0;
             a.kc = kc;
             a.vt = vt;
+            a.kr = kr;
             a.table = c->d_table;
             a.rows = drows;
             a.work = (const int4 *)((char *)dev + o_p);
