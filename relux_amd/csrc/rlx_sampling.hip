@@ -1,6 +1,28 @@
 // Token selection on the device: Sampler.Greedy, Sampler.Sample and the
-// speculative decoder's acceptPhase / resampleRejected, one 512-thread
-// work-group per row of logits.
+// speculative decoder's acceptPhase / resampleRejected, with 512-thread
+// work-groups.
+//
+// Launch shapes:
+//   * Greedy, and Sample without top-k, with top-k above kPartMaxK, or on a
+//     vocabulary of at most kPartChunk entries: one work-group per row
+//     (the whole-row path below).
+//   * Sample with top-k on a larger vocabulary (the split path):
+//     sample_part_kernel, one work-group per (row, chunk of at most
+//     kPartChunk entries), holds its chunk in registers, applies the
+//     penalties and writes, in index order, the entries at or above a
+//     lower bound of the chunk's k-th largest undivided logit (with a
+//     16-key margin for the temperature division still to come) plus a
+//     record {count, lower bound, largest key}; sample_kernel then merges a
+//     row's lists in one load round trip, divides by the temperature, finds
+//     the exact k-th largest by radix select over the key range the records
+//     leave open, and finishes the short list.  A list past its slots or a
+//     merge past kCandCap sends the row down the whole-row path.
+//   * acceptPhase + resampleRejected: spec_stat_kernel (per row, draft
+//     position and side: softmaxAlloc's max, sum and the draft token's
+//     probability, all drafts at once; further work-groups cut the next
+//     target row into the split path's chunk lists), spec_mass_kernel (per
+//     row and chunk: the first rejection, then that position's chunk sums
+//     of max(0, p_t - p_d) and of p_t) and spec_final_kernel (the draw).
 //
 // Reference: sampler.go:56-68 (Greedy), 73-210 (Sample: penalties ->
 // temperature -> top-k -> fastexp32 softmax -> top-p -> min-p -> categorical
@@ -8,7 +30,7 @@
 // r < min(1, p_t/p_d), resample from norm(max(0, p_t - p_d))), 344-368
 // (softmaxAlloc).  Each rng.Float32() draw is an input.
 //
-// Working set.  Sample first brings the row's scratch values (logits after
+// Whole-row working set.  Sample first brings the row's scratch values (logits after
 // penalties and temperature, sampler.go:80-97) into LDS when the vocabulary
 // fits (<= 32768 entries: 128 KB), applying the penalties in place on the
 // row's distinct window tokens; larger vocabularies are re-read from memory

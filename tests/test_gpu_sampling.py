@@ -70,13 +70,16 @@ PARAMS = {
 }
 
 
-# V 50000 is past the LDS row (32768 entries): the memory-read path, with
-# the penalised tokens in the LDS bitmap and top-k compaction.  With top-k on
-# and V past 4096 the vocabulary is split over work-groups (V 32000: 8
-# chunks; V 50000: 13), each keeping its own candidates.
+# V 50000 is past the LDS row (32768 entries): the whole-row path's
+# memory-read form, with the penalised tokens in the LDS bitmap.  With top-k
+# on and V past 8192 the vocabulary is split over work-groups (V 32000: 4
+# chunks of 8000; V 50000: 7), each keeping its own candidates; V 50257 and
+# 32003 put every row but the first off 16-byte alignment (the chunks' loads
+# fall back to single floats).
 CASES = [(n, V) for V in (100, 4096) for n in sorted(PARAMS)] + \
     [(n, 32000) for n in ("topk5", "topk50_t1.3", "all", "topk5_t0", "topk40_t25")] + \
-    [(n, 50000) for n in ("plain", "temp0.7", "topk5", "all", "penalties")]
+    [(n, 50000) for n in ("plain", "temp0.7", "topk5", "all", "penalties")] + \
+    [("all", 50257), ("topk50_t1.3", 32003)]
 
 
 @pytest.mark.parametrize("name,V", CASES)
@@ -204,8 +207,9 @@ def test_sample_async_no_history_and_limits(gpu, handle):
 
 
 # V 32000 and 50000: the next-row Sample of all-accepted rows runs split
-# (top-k 30); every V reduces its softmax statistics over 4096-entry chunks.
-@pytest.mark.parametrize("V", [100, 4096, 32000, 50000])
+# (top-k 30); every V reduces its softmax statistics over 4096-entry chunks;
+# V 32003 leaves every row but the first off 16-byte alignment.
+@pytest.mark.parametrize("V", [100, 4096, 32000, 50000, 32003])
 def test_spec_accept(gpu, handle, V):
     from relux_amd import spec_accept
     rng = np.random.default_rng(V)
