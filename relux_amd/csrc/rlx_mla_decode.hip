@@ -174,12 +174,15 @@ __global__ __launch_bounds__(256) void mla_absorb_append_kernel(
 // = 4 rows x one 32-B chunk pair) see 4 distinct chunk pairs.
 __device__ __forceinline__ int mla_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
-// Token bounds of a row's splits: split s of n covers [b(s), b(s + 1)) with
-// b(s) = floor(s * len / n) rounded down to a 16-token tile (b(n) = len), so
-// a row's splits differ by at most one tile.  The host keeps n <= len / 64,
-// so no split is empty.
+// Token bounds of a row's splits: the row's ceil(len / 16) tiles are dealt
+// out evenly, split s of n covering [b(s), b(s + 1)) with b(s) = 16 *
+// floor(s * tiles / n) (b(n) = len), so a row's splits differ by at most one
+// tile, the partial last tile included (rounding token bounds down to a
+// tile gave an 8193-token row's last split 36 tiles against 34).  The host
+// keeps n <= len / 64, so no split is empty.
 __device__ __forceinline__ int mla_split_bound(int len, int n, int s) {
-    return s >= n ? len : (int)(((int64_t)s * len / n) & ~(int64_t)15);
+    const int tiles = (len + 15) >> 4;
+    return s >= n ? len : (int)(((int64_t)s * tiles / n) << 4);
 }
 
 // Shape per query-row tile count: 4 waves and two work-groups per CU (80 KB
