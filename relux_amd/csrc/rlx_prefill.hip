@@ -348,6 +348,15 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     for (int md = 0; md < MD; md++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[md][i] = 0.f;
+    // -m_use in every entry: the first score product of a key tile starts
+    // its accumulation from it, so the scores come out as s - m_use and the
+    // weights need no subtraction (rebuilt only when the running max moves).
+    // The widest shape (<320,128>) keeps the subtraction: its 16 registers
+    // would spill there.
+    constexpr bool FOLD = DQK + DV <= 384;
+    fl16 negm;
+#pragma unroll
+    for (int i = 0; i < 16; i++) negm[i] = 0.f;
 
     for (int j = 0, st_read = 0; j < nblk; j++, st_read = (st_read + SH::ST * 8 == S * SH::ST * 8) ? 0 : st_read + SH::ST * 8) {
         wait_block(j);
@@ -384,6 +393,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         fl16 sc[2];
         u32x4 pw[4];
         float lt[2] = {0.f, 0.f};
+        // With FOLD, sc holds s - m_use (m_use = the running max, 0 before a
+        // row's first unmasked key); a rescale moves m_use and shifts the
+        // tiles still to be weighed by the same amount.
         float m_use = (m_run == -INFINITY) ? 0.f : m_run;
         // P^T operands: word k (0..7) of key tile kt packs values 2k, 2k+1
         // (the B operand of k-step 2kt + k/4 is words 4(k/4) .. +3).
@@ -391,8 +403,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         // compiler sinks the work to its first use, out of the products it
         // is meant to overlap.)
         auto pword = [&](int kt, int k) {
-            const float p0 = __builtin_amdgcn_exp2f(sc[kt][2 * k] - m_use);
-            const float p1 = __builtin_amdgcn_exp2f(sc[kt][2 * k + 1] - m_use);
+            const float p0 = __builtin_amdgcn_exp2f(FOLD ? sc[kt][2 * k] : sc[kt][2 * k] - m_use);
+            const float p1 = __builtin_amdgcn_exp2f(FOLD ? sc[kt][2 * k + 1] : sc[kt][2 * k + 1] - m_use);
             const uint32_t w = pack_bf16x2(p0, p1);
             pw[2 * kt + (k >> 2)][k & 3] = w;
             lt[kt] = add_bf16x2(w, lt[kt]);
@@ -414,7 +426,8 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 #pragma unroll
                 for (int i = 1; i < 16; i++) mx = fmaxf(mx, sc[kt][i]);
                 const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-                const float m_new = fmaxf(m_run, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])));
+                // (-inf + m_use stays -inf: a row with only masked keys)
+                const float m_new = fmaxf(m_run, fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) + (FOLD ? m_use : 0.f));
                 // A row that has seen only masked keys keeps m = -inf (factor
                 // 1: its accumulators are zero).
                 const float c = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -422,7 +435,17 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 #pragma unroll
                 for (int md = 0; md < MD; md++) acc[md] *= c;
                 m_run = m_new;
-                m_use = (m_run == -INFINITY) ? 0.f : m_run;
+                const float m_use_new = (m_run == -INFINITY) ? 0.f : m_run;
+                const float dlt = m_use_new - m_use;
+                m_use = m_use_new;
+                if constexpr (FOLD) {
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        negm[i] = -m_use;
+                        sc[kt][i] -= dlt;
+                        if (kt == 0) sc[1][i] -= dlt;  // tile 1 is weighed after this
+                    }
+                }
                 lt[kt] = 0.f;
 #pragma unroll
                 for (int k = 0; k < 8; k++) pword(kt, k);
@@ -443,7 +466,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                 const int kt = n / KS, ks = n % KS;
                 const bf16x8 A = __builtin_bit_cast(bf16x8, ka[n % (kPfD + 1)]);
                 if (ks == 0)
-                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, qb[ks], fl16{}, 0, 0, 0);
+                    sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, qb[ks], FOLD ? negm : fl16{}, 0, 0, 0);
                 else
                     sc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, qb[ks], sc[kt], 0, 0, 0);
                 if (n == KS + 1 && need_mask) mask(0);
