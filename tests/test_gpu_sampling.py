@@ -114,9 +114,9 @@ def test_sample_split_ties(gpu, handle):
     x[0, :] = 0.0                    # ties at every chunk's k-th largest: all lists overflow;
     x[0, [5, 17000, 31000]] = 12.0   # three entries hold most of the mass (a flat row's
     #                                  sequential f32 sums drift by 1e-4 over 32000 entries)
-    x[1, 100:400] = 12.0             # 300 tied maxima in one chunk (past its 100 slots)
-    x[2, ::500] = 12.0               # 64 tied maxima spread over the 8 chunks
-    x[3, 3990:4010] = 12.0           # ties across a chunk boundary
+    x[1, 100:400] = 12.0             # 300 tied maxima in one chunk (past its slots)
+    x[2, ::500] = 12.0               # 64 tied maxima spread over the 4 chunks
+    x[3, 7990:8010] = 12.0           # ties across a chunk boundary (chunks of 8000)
     x[4, :] = np.round(x[4, :])      # a few thousand entries on each integer
     x[5, 31990:] = 12.0              # ties in the last chunk
     x[6, :60] = np.float32(-np.inf)  # masked entries in the first chunk
@@ -131,6 +131,36 @@ def test_sample_split_ties(gpu, handle):
             kept += 1
             assert got[i] == want, (p, i, got[i], want)
         assert kept >= rows // 2
+
+
+# Split-path boundaries: the smallest split (V 8193: two chunks), top-k at
+# both ends of the split path (1 and 256, the largest it takes), many
+# chunks (V 65537: nine), and top-p / min-p filtering after the merge.
+SPLIT_EDGES = [
+    (8193, S.SamplerParams(top_k=1)),
+    (8193, S.SamplerParams(top_k=256, temperature=1.1)),
+    (65537, S.SamplerParams(top_k=256, top_p=0.8, min_p=0.01)),
+    (65537, S.SamplerParams(top_k=7, temperature=0.5)),
+    (20000, S.SamplerParams(top_k=100, top_p=0.5, min_p=0.1, temperature=1.7)),
+]
+
+
+@pytest.mark.parametrize("V,p", SPLIT_EDGES)
+def test_sample_split_edges(gpu, handle, V, p):
+    rng = np.random.default_rng(V + p.top_k)
+    rows = 16
+    x = rng.normal(0, 2.5, (rows, V)).astype(np.float32)
+    u = rng.random(rows, dtype=np.float32)
+    got = make_sampler(p, S.Draws(u)).Sample(dev(x, gpu), None, handle)
+    kept = 0
+    for i in range(rows):
+        want = S.sample(x[i], p, u[i])
+        if S.sample(x[i], p, u[i] - DELTA) != want or S.sample(x[i], p, u[i] + DELTA) != want:
+            continue
+        kept += 1
+        assert got[i] == want, (V, p, i, got[i], want)
+    print(f"split edge V{V} k{p.top_k}: {kept}/{rows} robust rows compared")
+    assert kept >= rows // 2
 
 
 WINDOW_CASES = [
