@@ -272,6 +272,39 @@ def test_spec_accept(gpu, handle, V):
     assert outcomes == {True, False}  # both the rejection and the all-accepted paths ran
 
 
+@pytest.mark.parametrize("K,V", [(1, 32000), (8, 32000), (8, 4096)])
+def test_spec_accept_draft_counts(gpu, handle, K, V):
+    """One and eight drafts per row (the statistics launch holds 2K row
+    sides per row), counts from 0 to K."""
+    from relux_amd import spec_accept
+    rng = np.random.default_rng(1000 * K + V)
+    B = 12
+    d = rng.normal(0, 1.5, (B, K, V)).astype(np.float32)
+    t = np.concatenate([d + rng.normal(0, 0.6, (B, K, V)).astype(np.float32),
+                        rng.normal(0, 1.5, (B, 1, V)).astype(np.float32)], axis=1)
+    nd = rng.integers(0, K + 1, B).astype(np.int32)
+    nd[:4] = K
+    tok = np.zeros((B, K), np.int32)
+    for b in range(B):
+        for i in range(K):
+            tok[b, i] = S.sample(d[b, i], S.SamplerParams(), float(rng.random()))
+    u = rng.random((B, K + 1), dtype=np.float32)
+    params = S.SamplerParams(temperature=0.8, top_k=40, top_p=0.9)
+    acc, nxt = spec_accept(handle, dev(d, gpu), dev(t, gpu), tok, nd, u, make_sampler(params))
+    kept = 0
+    for b in range(B):
+        k = nd[b]
+        want = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1], params)
+        lo = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1] - DELTA, params)
+        hi = S.spec_accept(d[b, :k], t[b, :k + 1], tok[b, :k], u[b, :k + 1] + DELTA, params)
+        if lo != want or hi != want:
+            continue
+        kept += 1
+        assert (acc[b], nxt[b]) == want, (K, V, b, acc[b], nxt[b], want)
+    print(f"spec_accept K{K} V{V}: {kept}/{B} robust rows compared")
+    assert kept >= B // 2
+
+
 @pytest.mark.parametrize("V", [4096, 50000])
 def test_spec_accept_async_equals_sync(gpu, handle, V):
     """rlx_spec_accept_async (draft ids, counts and draws on the device)
