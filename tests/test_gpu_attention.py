@@ -562,6 +562,44 @@ def test_mla_prefill_matches_oracle(gpu, H, lens, nqs, mask):
         toff += L
 
 
+def test_mla_prefill_after_evict_equals_survivors(gpu):
+    """A chunked MLA prefill (the expansion path: the call's rope keys
+    gathered through the page table from the first live entry) over
+    sequences whose oldest pages were evicted == exact attention over the
+    surviving tokens, before and after compaction (row A17)."""
+    from relux_amd import MLACache
+    rng = np.random.default_rng(61)
+    H, D, P = 16, 128, 16
+    lens, ev, nqs = [300, 200], [3, 2], [64, 40]
+    c = MLACache(num_layers=1, max_len=max(lens) + P, page_tokens=P, max_seqs=2, device=gpu.index)
+    cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
+    kr = rng.standard_normal((sum(lens), 64), dtype=np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    c.Append(0, t(cc), t(kr), seq_ids=[0, 1], n_tok=lens)
+    c.Evict([0, 1], ev)
+    w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+    qn = rng.standard_normal((sum(nqs), H, D), dtype=np.float32)
+    qr = rng.standard_normal((sum(nqs), H, 64), dtype=np.float32)
+    args = (t(qn), t(qr), t(w_uk.view(np.int16)).view(torch.bfloat16),
+            t(w_uv.view(np.int16)).view(torch.bfloat16), H, D)
+    before = c.Attend(0, *args, seq_ids=[0, 1], n_q=nqs).cpu().numpy()
+    c.Compact()
+    after = c.Attend(0, *args, seq_ids=[0, 1], n_q=nqs).cpu().numpy()
+    assert np.array_equal(before, after)
+    off = toff = 0
+    for i, L in enumerate(lens):
+        s0 = toff + ev[i] * P  # first surviving token
+        T = L - ev[i] * P
+        cs = oracle.round_bf16(cc[s0:toff + L])
+        ks = oracle.round_bf16(kr[s0:toff + L])
+        exact = _mla_exact(qn[off:off + nqs[i]].transpose(1, 0, 2), qr[off:off + nqs[i]].transpose(1, 0, 2),
+                           cs, ks, w_uk, w_uv, _limits("causal", nqs[i], T))
+        _check(after[off:off + nqs[i]].transpose(1, 0, 2), exact, (1e-2, 1e-3), f"seq {i} survivors")
+        off += nqs[i]
+        toff += L
+
+
 @pytest.mark.parametrize("H,budget_mb", [(24, 2), (16, 3)])
 def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
     """A chunked-prefill call whose expanded K_c / V^T exceed the expansion
