@@ -150,6 +150,36 @@ def test_gqa_attention_after_evict_equals_dense_survivors(gpu):
         _check(after[s:s + 1].transpose(1, 0, 2), exact, TOL_EXACT, f"seq {s} survivors")
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_gqa_prefill_after_evict_equals_survivors(gpu, D):
+    """A chunked GQA prefill (the FA2 kernel, pages through the table from
+    the first live entry) over sequences whose oldest pages were evicted ==
+    exact attention over the surviving tokens, before and after compaction."""
+    from relux_amd import KVCache
+    rng = np.random.default_rng(23 + D)
+    H, KVH, P = 16, 4, 16
+    lens, ev, nqs = [520, 300], [5, 3], [96, 64]
+    c = KVCache(num_layers=1, max_len=1024, num_kv_heads=KVH, head_dim=D, page_tokens=P,
+                max_seqs=2, device=gpu.index)
+    K, V = _fill_gqa(c, rng, gpu, lens, KVH, D)
+    for s, e in enumerate(ev):
+        c.Evict(s, e)
+    q = torch.from_numpy(rng.standard_normal((sum(nqs), H, D), dtype=np.float32)).to(gpu)
+    before = c.Attend(0, q, H, seq_ids=[0, 1], n_q=nqs).cpu().numpy()
+    c.Compact()
+    after = c.Attend(0, q, H, seq_ids=[0, 1], n_q=nqs).cpu().numpy()
+    assert np.array_equal(before, after)
+    off = 0
+    for s in range(2):
+        Ks, Vs = K[s][:, ev[s] * P:], V[s][:, ev[s] * P:]
+        T = Ks.shape[1]
+        exact = oracle.exact_attention_f64(q[off:off + nqs[s]].cpu().numpy().transpose(1, 0, 2),
+                                           np.repeat(Ks, H // KVH, 0), np.repeat(Vs, H // KVH, 0),
+                                           _limits("causal", nqs[s], T))
+        _check(after[off:off + nqs[s]].transpose(1, 0, 2), exact, TOL_EXACT, f"seq {s} survivors")
+        off += nqs[s]
+
+
 def _torch_gqa_ref(k_list, v_list, q, H, KVH):
     """f32 exact attention in torch over dense K/V (full-size property check)."""
     outs = []
