@@ -649,11 +649,13 @@ def main():
                                  "spill8k")
                      if w != args.workload]:
             # spec_stress: 300 timed steps after the warm-up cross one evict + compact;
-            # the other secondary lines time at least 200 steps after at least 20
-            # warm-up steps, whatever the headline's K and W (a short run after a
-            # short warm-up averages in the launches of a GPU still ramping up)
-            n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(200, args.steps))
-            n_warm = {"mla_prefill": 2}.get(name, max(20, args.warmup))
+            # the other secondary lines time at least 400 steps after at least 40
+            # warm-up steps (the default run's K and W), whatever the headline's: a
+            # decode kernel settles over the first few hundred steps after a cache
+            # fill (8k GQA, per 20-step window: 82-83 us at first, 80 us by step
+            # 250, 79 us by step 500), so a short run reads the GPU still ramping up
+            n_steps = {"mla_prefill": 8, "spec_stress": 300}.get(name, max(400, args.steps))
+            n_warm = {"mla_prefill": 2}.get(name, max(40, args.warmup))
             s = run_workload(name, n_steps, n_warm, torch, dev)
             print(f"[bench] {name}: {s['tokens_per_s']:.0f} tok/s, kernel {s['kernel_avg_us']:.1f} us, "
                   f"{s['kernel_rate']:.0f} {s['rate_unit']}", file=sys.stderr, flush=True)
