@@ -722,6 +722,205 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
     }
 }
 
+// The same step for head dim 128 with the projection on the matrix cores.
+// Block = (head h, RPB query rows), 4 waves; wave w produces output dims
+// [32w, 32w + 32) of the block's rows:
+//   out[r][d] = sum_c o_lat[r][c] W_UV[c][h*128 + d]
+// as MFMA 16x16x16 bf16 tiles D[16][16 dims] over the 512 channels.  A rows
+// hold the merged latent as an exact-sum bf16 pair: row 2r = hi(o_lat[r]),
+// row 2r + 1 = lo = bf16(o_lat[r] - hi), so one product covers both halves
+// and out[r] = D[2r] + D[2r + 1] keeps the f32 latent to ~2^-17 relative
+// (bf16 products are exact in f32).  The B operand needs 4 consecutive
+// channels of one dim per lane while W_UV rows are dim-contiguous: each
+// wave copies its [512 ch][32 dims] slice into its own LDS region (64-byte
+// rows, the two 32-byte halves swapped on rows with bit 2 set, so a
+// transpose read of 32 lanes touches every bank once) and reads operands
+// with the LDS transpose read.  Loads are issued as in mla_out_kernel:
+// (m, l) pairs, the split partials, then the W_UV slice (into registers);
+// the slice goes to LDS after the merge, so the merge waits only for the
+// partials.
+template <int RPB, bool ARG>
+__global__ __launch_bounds__(256) void mla_out_mfma_kernel(
+    typename PlanSel<ARG>::T plan, const AttRow *__restrict__ rows, int n_rows, int total_q, int one_q,
+    const uint16_t *__restrict__ part_o, const float *__restrict__ part_ml,
+    const uint16_t *__restrict__ w_uv, int H, int dc, int QRP, void *__restrict__ out, int out_bf16) {
+    constexpr int D = 128;                     // head dim
+    constexpr int WD = D / 4;                  // output dims per wave
+    constexpr int WL = kMlaDc * WD / 8 / 64;   // 16-byte slice loads per lane (32)
+    constexpr int SB = 16;                     // splits per batch of loads
+    constexpr int OP = kMlaDc / 2 + 8;         // o_lat row pitch in bf16 pairs (32 B pad)
+    static_assert(2 * RPB <= 16, "the hi and lo rows fill at most one MFMA tile");
+    static_assert(RPB <= 4, "one wave computes each row's merge weights");
+    const int h = blockIdx.x;
+    const int q0 = blockIdx.y * RPB;
+    __shared__ __attribute__((aligned(16))) uint16_t wsl[4][kMlaDc * WD];
+    __shared__ __attribute__((aligned(16))) float fac[RPB][kMaxSplits];
+    __shared__ float inv_l[RPB];
+    __shared__ __attribute__((aligned(16))) uint32_t olat[2 * RPB][OP];  // row 2r + s: s = 0 hi, 1 lo
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    int64_t b0[RPB];
+    int ns[RPB];
+    int64_t ob[RPB];
+    bool live[RPB];
+#pragma unroll
+    for (int j = 0; j < RPB; j++) {
+        const int q = min(q0 + j, total_q - 1);
+        live[j] = q0 + j < total_q;
+        const AttRow R = plan_row<ARG>(rows, one_q ? q : plan_qrow_row<ARG>(rows, n_rows, q));
+        const int qi = q - R.qrow;
+        b0[j] = (int64_t)R.part * QRP + qi * H + h;
+        ns[j] = R.nsplit;
+        ob[j] = ((int64_t)q * H + h) * D;
+    }
+    int64_t bw = b0[0];
+    int nw = ns[0];
+#pragma unroll
+    for (int j = 1; j < RPB; j++)
+        if (wave == j) {
+            bw = b0[j];
+            nw = ns[j];
+        }
+    const float2 *ml = (const float2 *)(part_ml + bw * 2);
+    const int64_t st = QRP;
+    float2 ml0 = make_float2(-INFINITY, 0.f);
+    if (wave < RPB) ml0 = ml[min(lane, nw - 1) * st];
+    const int64_t sstride = (int64_t)QRP * kMlaDc;
+    uint32_t v[RPB][SB];
+#pragma unroll
+    for (int j = 0; j < RPB; j++) {
+        const uint16_t *src = part_o + b0[j] * kMlaDc + 2 * t;
+#pragma unroll
+        for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(i, ns[j] - 1) * sstride);
+    }
+    // Slice load k of this lane: channel 16k + lane / 4, 16-byte chunk
+    // lane % 4 of the wave's 32 dims.  Channels past d_c read channel
+    // d_c - 1: o_lat is exactly 0 there, so they add nothing.
+    const uint16_t *wp = w_uv + (int64_t)h * D + wave * WD + (lane & 3) * 8;
+    const int64_t wstride = (int64_t)H * D;
+    u32x4 w[WL];
+#pragma unroll
+    for (int k = 0; k < WL; k++) w[k] = *(const u32x4 *)(wp + (int64_t)min(16 * k + (lane >> 2), dc - 1) * wstride);
+    // Merge weights of row j by wave j, as in mla_out_kernel, except that
+    // fac is written as 0 past the row's splits up to a multiple of SB: the
+    // merge then reads whole float4s of weights with no per-split test
+    // (the partials it pairs them with are finite clamped loads).
+    if (wave < RPB) {
+        const int j = wave;
+        const int nz = (nw + SB - 1) / SB * SB;
+        if (lane >= nw) ml0 = make_float2(-INFINITY, 0.f);
+        float M = ml0.x;
+        for (int s0 = lane + 64; s0 < nw; s0 += 64) M = fmaxf(M, ml[s0 * st].x);
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) M = fmaxf(M, __shfl_xor(M, k));
+        float L = 0.f;
+        {
+            const float f = (ml0.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml0.x - M);
+            fac[j][lane] = f;
+            L = f * ml0.y;
+        }
+        for (int s0 = lane + 64; s0 < nz; s0 += 64) {
+            float f = 0.f;
+            if (s0 < nw) {
+                const float2 e = ml[s0 * st];
+                f = (e.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(e.x - M);
+                L += f * e.y;
+            }
+            fac[j][s0] = f;
+        }
+#pragma unroll
+        for (int k = 32; k > 0; k >>= 1) L += __shfl_xor(L, k);
+        if (lane == 0) inv_l[j] = (L > 0.f) ? 1.f / L : 0.f;
+    }
+    ring_barrier();  // fac, inv_l (the slice loads stay in flight)
+    auto merge_batch = [&](int j, int s0, float &o0, float &o1) {
+        const float4 *fp = (const float4 *)&fac[j][s0];
+        float4 f4[SB / 4];
+#pragma unroll
+        for (int u = 0; u < SB / 4; u++) f4[u] = fp[u];
+#pragma unroll
+        for (int i = 0; i < SB; i++) {
+            const float f = f4[i / 4][i % 4];
+            o0 += f * bf16_lo(v[j][i]);
+            o1 += f * bf16_hi(v[j][i]);
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < RPB; j++) {
+        const uint16_t *src = part_o + b0[j] * kMlaDc + 2 * t;
+        float o0 = 0.f, o1 = 0.f;
+        merge_batch(j, 0, o0, o1);
+        for (int s0 = SB; s0 < ns[j]; s0 += SB) {
+#pragma unroll
+            for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(s0 + i, ns[j] - 1) * sstride);
+            merge_batch(j, s0, o0, o1);
+        }
+        uint16_t h0, l0, h1, l1;
+        split_bf16(o0 * inv_l[j], h0, l0);
+        split_bf16(o1 * inv_l[j], h1, l1);
+        olat[2 * j][t] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        olat[2 * j + 1][t] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+    // The slice goes to LDS only now (the compiler would otherwise hoist
+    // these stores, and their waits for the slice loads, above the merge).
+    asm volatile("" ::: "memory");
+    uint16_t *my = wsl[wave];
+    const int sw16 = ((lane >> 4) & 1) << 1;  // channel 16k + lane/4 has bit 2 = bit 4 of lane
+#pragma unroll
+    for (int k = 0; k < WL; k++)
+        *(u32x4 *)(my + (16 * k + (lane >> 2)) * WD + (((lane & 3) ^ sw16) << 3)) = w[k];
+    ring_barrier();  // o_lat of every row; this wave's slice
+    // A: row m = lane % 16 (2r + s), channels 16 ks + 4 g .. + 4 (g = lane / 16).
+    // B (transpose read): lane i of group g fetches dims 4 (i % 4) .. + 4 of
+    // channel 16 ks + 4 g + i / 4; lane j ends up with dim j of the group's
+    // 4 channels.  Channel 16 ks + 4 g + x has bit 2 = g & 1.
+    const int m = lane & 15, g = lane >> 4;
+    const bool arow = m < 2 * RPB;
+    const uint32_t *ap = &olat[arow ? m : 0][2 * g];
+    const uint16_t *bp = my + (4 * g + (m >> 2)) * WD + 4 * (m & 3);
+    // Operands of KB k-steps are read before their products, so the LDS
+    // round trips overlap instead of one per k-step.
+    constexpr int KB = 8;
+    fl4 acc[2] = {fl4{0.f, 0.f, 0.f, 0.f}, fl4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int k0 = 0; k0 < kMlaDc / 16; k0 += KB) {
+        sh4 av[KB], bv[KB][2];
+#pragma unroll
+        for (int u = 0; u < KB; u++) {
+            u32x2 a2 = u32x2{0u, 0u};
+            if (arow) a2 = *(const u32x2 *)(ap + 8 * (k0 + u));
+            av[u] = __builtin_bit_cast(sh4, a2);
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+                bv[u][nt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) sh4 *)(bp + (k0 + u) * 16 * WD + ((nt ^ (g & 1)) << 4)));
+        }
+#pragma unroll
+        for (int u = 0; u < KB; u++)
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++)
+                acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av[u], bv[u][nt], acc[nt], 0, 0, 0);
+    }
+    // acc[nt][i] = D[4g + i][dim 16 nt + m]: rows 2g (i = 0, 1) and 2g + 1 (i = 2, 3).
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const int d = wave * WD + nt * 16 + m;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int r = 2 * g + u;
+#pragma unroll
+            for (int j = 0; j < RPB; j++) {
+                if (j != r || !live[j]) continue;
+                const float val = acc[nt][2 * u] + acc[nt][2 * u + 1];
+                if (out_bf16)
+                    ((uint16_t *)out)[ob[j] + d] = bf16_rne(val);
+                else
+                    ((float *)out)[ob[j] + d] = val;
+            }
+        }
+    }
+}
+
 template <int NQT, bool ARG>
 static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uint16_t *pool,
                          const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
@@ -754,7 +953,16 @@ static void launch_mla_out(hipStream_t s, typename PlanSel<ARG>::T plan, const A
                            int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
                            const uint16_t *w_uv, int H, int hd, int dc, int QRP, void *out,
                            int out_bf16, int cus) {
-    if (hd <= 32)
+    if (hd == 128) {
+        if ((int64_t)H * ((total_q + 1) / 2) >= cus)
+            mla_out_mfma_kernel<2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
+                plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, dc, QRP,
+                out, out_bf16);
+        else
+            mla_out_mfma_kernel<1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
+                plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, dc, QRP,
+                out, out_bf16);
+    } else if (hd <= 32)
         launch_mla_out_d<32, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
     else if (hd <= 64)
         launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);

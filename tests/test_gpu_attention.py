@@ -363,6 +363,45 @@ def _mla_attend_case(gpu, H, lens, nq, mask, P):
         toff += L
 
 
+def test_mla_decode_many_splits(gpu):
+    """Decode rows cut into more than 16 context splits (the merge reloads
+    the split partials in batches of 16) and more than 64 (merge weights
+    past split 64 in a second pass): a 12 000-token row alone takes 94
+    splits, 2 100 tokens 17.  f32 outputs against exact attention; bf16
+    outputs equal the f32 outputs rounded to nearest even, bit for bit."""
+    from relux_amd import MLACache
+    rng = np.random.default_rng(97)
+    H, D, P = 16, 128, 64
+    for lens in ([12000], [12000, 2100, 300, 40]):
+        c = MLACache(num_layers=1, max_len=max(lens) + P, page_tokens=P, max_seqs=len(lens),
+                     device=gpu.index)
+        cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
+        kr = rng.standard_normal((sum(lens), 64), dtype=np.float32)
+        c.Append(0, torch.from_numpy(cc).to(gpu), torch.from_numpy(kr).to(gpu),
+                 seq_ids=list(range(len(lens))), n_tok=lens)
+        w_uk = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+        w_uv = oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D)))
+        qn = rng.standard_normal((len(lens), H, D), dtype=np.float32)
+        qr = rng.standard_normal((len(lens), H, 64), dtype=np.float32)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+        args = (t(qn), t(qr), t(w_uk.view(np.int16)).view(torch.bfloat16),
+                t(w_uv.view(np.int16)).view(torch.bfloat16), H, D)
+        ids = list(range(len(lens)))
+        out = c.Attend(0, *args, seq_ids=ids).cpu().numpy()
+        out16 = c.Attend(0, *args, seq_ids=ids, out_dtype=torch.bfloat16).cpu()
+        assert np.array_equal(out16.view(torch.int16).numpy().view(np.uint16),
+                              oracle.bf16_from_f32(out)), lens
+        toff = 0
+        for i, L in enumerate(lens):
+            cs = oracle.round_bf16(cc[toff:toff + L])
+            ks = oracle.round_bf16(kr[toff:toff + L])
+            exact = _mla_exact(qn[i:i + 1].transpose(1, 0, 2), qr[i:i + 1].transpose(1, 0, 2), cs, ks,
+                               w_uk, w_uv, [L - 1])
+            _check(out[i:i + 1].transpose(1, 0, 2), exact, TOL_MLA_EXACT, f"len {L} of {lens} vs exact")
+            toff += L
+        c.close()
+
+
 @pytest.mark.parametrize("H,D,dC,dR,lens,nq,mask", [
     (4, 8, 32, 4, [8, 23, 300], 1, "causal"),      # TestTransformer_MLA's dims (transformer_test.go:1012-1027)
     (4, 16, 64, 8, [9, 100, 260], 4, "causal"),    # config-1-sized layer, 4-query verify
@@ -371,6 +410,7 @@ def _mla_attend_case(gpu, H, lens, nq, mask, P):
     (4, 16, 64, 8, [70, 40], 40, "none"),          # unmasked: a row per query
     (2, 8, 32, 4, [50], 50, "ref"),                # reference rule with n_q == len: causal
     (16, 128, 512, 64, [300, 65], 1, "causal"),    # default DeepSeek dims, generic absorb / out
+    (8, 128, 256, 32, [2100, 70], 1, "causal"),    # head_dim 128 with d_c < 512: latent channels past d_c
     (16, 96, 384, 48, [260], 2, "causal"),
     (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128 prefill through FA2 (240 rows)
     # FA2 at the reference's default dims (K_c / V^T expanded with zero rows
