@@ -731,11 +731,12 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
 // row 2r + 1 = lo = bf16(o_lat[r] - hi), so one product covers both halves
 // and out[r] = D[2r] + D[2r + 1] keeps the f32 latent to ~2^-17 relative
 // (bf16 products are exact in f32).  The B operand needs 4 consecutive
-// channels of one dim per lane while W_UV rows are dim-contiguous: each
-// wave copies its [512 ch][32 dims] slice into its own LDS region (64-byte
-// rows, the two 32-byte halves swapped on rows with bit 2 set, so a
-// transpose read of 32 lanes touches every bank once) and reads operands
-// with the LDS transpose read.  Loads are issued as in mla_out_kernel:
+// channels of one dim per lane while W_UV rows are dim-contiguous: the
+// block copies the head's [512 ch][128 dims] slice into LDS (whole 256-byte
+// rows per 16 lanes, so every 128-byte line is requested once; 32-byte
+// chunk c of channel r at slot c ^ (r & 7), so a transpose read of 32
+// lanes touches every bank once) and each wave reads its operands with the
+// LDS transpose read.  Loads are issued as in mla_out_kernel:
 // (m, l) pairs, the split partials, then the W_UV slice (into registers);
 // the slice goes to LDS after the merge, so the merge waits only for the
 // partials.
@@ -746,14 +747,14 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
     const uint16_t *__restrict__ w_uv, int H, int dc, int QRP, void *__restrict__ out, int out_bf16) {
     constexpr int D = 128;                     // head dim
     constexpr int WD = D / 4;                  // output dims per wave
-    constexpr int WL = kMlaDc * WD / 8 / 64;   // 16-byte slice loads per lane (32)
+    constexpr int WL = kMlaDc * D / 8 / 256;   // 16-byte slice loads per lane (32)
     constexpr int SB = 16;                     // splits per batch of loads
     constexpr int OP = kMlaDc / 2 + 8;         // o_lat row pitch in bf16 pairs (32 B pad)
     static_assert(2 * RPB <= 16, "the hi and lo rows fill at most one MFMA tile");
     static_assert(RPB <= 4, "one wave computes each row's merge weights");
     const int h = blockIdx.x;
     const int q0 = blockIdx.y * RPB;
-    __shared__ __attribute__((aligned(16))) uint16_t wsl[4][kMlaDc * WD];
+    __shared__ __attribute__((aligned(16))) uint16_t wsl[kMlaDc * D];
     __shared__ __attribute__((aligned(16))) float fac[RPB][kMaxSplits];
     __shared__ float inv_l[RPB];
     __shared__ __attribute__((aligned(16))) uint32_t olat[2 * RPB][OP];  // row 2r + s: s = 0 hi, 1 lo
@@ -793,14 +794,15 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
 #pragma unroll
         for (int i = 0; i < SB; i++) v[j][i] = *(const uint32_t *)(src + (int64_t)min(i, ns[j] - 1) * sstride);
     }
-    // Slice load k of this lane: channel 16k + lane / 4, 16-byte chunk
-    // lane % 4 of the wave's 32 dims.  Channels past d_c read channel
-    // d_c - 1: o_lat is exactly 0 there, so they add nothing.
-    const uint16_t *wp = w_uv + (int64_t)h * D + wave * WD + (lane & 3) * 8;
+    // Slice load k of this lane: channel 128 wave + 4k + lane / 16,
+    // 16-byte chunk lane % 16 of the head's 128 dims.  Channels past d_c
+    // read channel d_c - 1: o_lat is exactly 0 there, so they add nothing.
+    const int wc0 = 128 * wave + (lane >> 4);
+    const uint16_t *wp = w_uv + (int64_t)h * D + (lane & 15) * 8;
     const int64_t wstride = (int64_t)H * D;
     u32x4 w[WL];
 #pragma unroll
-    for (int k = 0; k < WL; k++) w[k] = *(const u32x4 *)(wp + (int64_t)min(16 * k + (lane >> 2), dc - 1) * wstride);
+    for (int k = 0; k < WL; k++) w[k] = *(const u32x4 *)(wp + (int64_t)min(wc0 + 4 * k, dc - 1) * wstride);
     // Merge weights of row j by wave j, as in mla_out_kernel, except that
     // fac is written as 0 past the row's splits up to a multiple of SB: the
     // merge then reads whole float4s of weights with no per-split test
@@ -864,20 +866,22 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
     // The slice goes to LDS only now (the compiler would otherwise hoist
     // these stores, and their waits for the slice loads, above the merge).
     asm volatile("" ::: "memory");
-    uint16_t *my = wsl[wave];
-    const int sw16 = ((lane >> 4) & 1) << 1;  // channel 16k + lane/4 has bit 2 = bit 4 of lane
+    // channel wc0 + 4k: (r & 7) = 4 (k & 1) + lane / 16
 #pragma unroll
-    for (int k = 0; k < WL; k++)
-        *(u32x4 *)(my + (16 * k + (lane >> 2)) * WD + (((lane & 3) ^ sw16) << 3)) = w[k];
-    ring_barrier();  // o_lat of every row; this wave's slice
+    for (int k = 0; k < WL; k++) {
+        const int q = lane & 15, sw = ((k & 1) << 2) | (lane >> 4);
+        *(u32x4 *)(wsl + (wc0 + 4 * k) * D + ((((q >> 1) ^ sw) << 1 | (q & 1)) << 3)) = w[k];
+    }
+    ring_barrier();  // o_lat of every row; the slice
     // A: row m = lane % 16 (2r + s), channels 16 ks + 4 g .. + 4 (g = lane / 16).
     // B (transpose read): lane i of group g fetches dims 4 (i % 4) .. + 4 of
-    // channel 16 ks + 4 g + i / 4; lane j ends up with dim j of the group's
-    // 4 channels.  Channel 16 ks + 4 g + x has bit 2 = g & 1.
+    // the 16-dim tile, channel 16 ks + 4 g + i / 4; lane j ends up with dim
+    // j of the group's 4 channels.  That channel has (r & 7) = 4 (g & 1) + i / 4.
     const int m = lane & 15, g = lane >> 4;
     const bool arow = m < 2 * RPB;
     const uint32_t *ap = &olat[arow ? m : 0][2 * g];
-    const uint16_t *bp = my + (4 * g + (m >> 2)) * WD + 4 * (m & 3);
+    const int rsw = ((g & 1) << 2) | (m >> 2);
+    const uint16_t *bp = wsl + (4 * g + (m >> 2)) * D + 4 * (m & 3);
     // Operands of KB k-steps are read before their products, so the LDS
     // round trips overlap instead of one per k-step.
     constexpr int KB = 8;
@@ -893,7 +897,7 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
 #pragma unroll
             for (int nt = 0; nt < 2; nt++)
                 bv[u][nt] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (__attribute__((address_space(3))) sh4 *)(bp + (k0 + u) * 16 * WD + ((nt ^ (g & 1)) << 4)));
+                    (__attribute__((address_space(3))) sh4 *)(bp + (k0 + u) * 16 * D + (((2 * wave + nt) ^ rsw) << 4)));
         }
 #pragma unroll
         for (int u = 0; u < KB; u++)
