@@ -128,6 +128,8 @@ struct Cache {
     int next_slot = 0;
     void *ws = nullptr;
     size_t ws_cap = 0;
+    size_t ws_peak = 0;     // largest workspace a call asked for
+    size_t stage_peak = 0;  // largest plan a call staged
     SpillTier spill;
     // Attention-kernel timing: event pairs, reused across reports.
     int timing = 0;  // RLX_TIME_* mask
@@ -152,6 +154,7 @@ struct Cache {
 int32_t stage(Cache *c, const void *data, size_t bytes, void **dev_out) {
     Slot &s = c->slots[c->next_slot];
     c->next_slot = (c->next_slot + 1) % kSlots;
+    c->stage_peak = std::max(c->stage_peak, bytes);
     if (s.pending) {
         HIP_TRY(hipEventSynchronize(s.ev));
         s.pending = false;
@@ -258,6 +261,7 @@ int32_t flush_patches_inline(Cache *c) {
 }
 
 int32_t ensure_ws(Cache *c, size_t bytes) {
+    c->ws_peak = std::max(c->ws_peak, bytes);
     if (bytes <= c->ws_cap) return RLX_OK;
     // RLX_WS_MAX_KB caps the workspace (tests force the failure path of a
     // call with it; unset or 0: no cap).
@@ -893,6 +897,48 @@ int32_t rlx_cache_set_stream(void *h, void *stream) {
     HIP_TRY(hipStreamSynchronize(c->stream));
     // NULL is the device's null stream (torch's default stream reports 0).
     c->stream = (hipStream_t)stream;
+    return RLX_OK;
+}
+
+int32_t rlx_cache_reserve(void *h, uint64_t ws_bytes, uint64_t stage_bytes) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    if (ws_bytes > c->ws_cap) {
+        const size_t cap = ((size_t)ws_bytes + 65535) & ~(size_t)65535;
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (c->ws) HIP_TRY(hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_cap = 0;
+        HIP_TRY(hipMalloc(&c->ws, cap));
+        c->ws_cap = cap;
+    }
+    for (Slot &s : c->slots) {
+        if (stage_bytes <= s.cap) continue;
+        const size_t cap = ((size_t)stage_bytes + 4095) & ~(size_t)4095;
+        // The slot's device copy may still be read by queued kernels.
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        s.pending = false;
+        if (s.host) HIP_TRY(hipHostFree(s.host));
+        if (s.dev) HIP_TRY(hipFree(s.dev));
+        s.host = nullptr;
+        s.dev = nullptr;
+        s.cap = 0;
+        HIP_TRY(hipHostMalloc(&s.host, cap, hipHostMallocDefault));
+        HIP_TRY(hipMalloc(&s.dev, cap));
+        s.cap = cap;
+    }
+    return RLX_OK;
+}
+
+int32_t rlx_cache_memory(void *h, uint64_t *out) {
+    if (!h || !out) return fail(RLX_ERR_INVALID, "null argument");
+    const Cache *c = as_cache(h);
+    size_t smin = c->slots[0].cap;
+    for (const Slot &s : c->slots) smin = std::min(smin, s.cap);
+    out[0] = c->ws_cap;
+    out[1] = c->ws_peak;
+    out[2] = smin;
+    out[3] = c->stage_peak;
     return RLX_OK;
 }
 

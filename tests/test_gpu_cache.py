@@ -459,3 +459,55 @@ def test_mla_spill_restore_roundtrip(gpu, tmp_path):
     after = [[t.clone() for t in c.View(l, s)] for l in range(2) for s in range(2)]
     for a, b in zip(views, after):
         assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_reserve_keeps_calls_from_allocating(gpu):
+    """rlx_cache_reserve / rlx_cache_memory: a trial handle runs an MLA
+    prefill (expanded latents in the workspace) and an 80-sequence GQA
+    decode (its plan staged, past what the kernel arguments hold); a second
+    handle reserves the peaks the first reported, and the same calls then
+    grow neither its workspace nor its staging slots, with outputs
+    bit-identical to the trial handle's."""
+    rng = np.random.default_rng(404)
+    H, D, lens = 16, 128, [700, 300]
+    cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
+    kr = rng.standard_normal((sum(lens), 64), dtype=np.float32)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+    w_uk = t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D))).view(np.int16)).view(torch.bfloat16)
+    w_uv = t(oracle.bf16_from_f32(rng.normal(0, 0.02, size=(512, H * D))).view(np.int16)).view(torch.bfloat16)
+    qn = t(rng.standard_normal((sum(lens), H, D), dtype=np.float32))
+    qr = t(rng.standard_normal((sum(lens), H, 64), dtype=np.float32))
+    B, KVH = 80, 8
+    glens = rng.integers(20, 200, B).tolist()
+    gk = t(rng.standard_normal((sum(glens), KVH, D), dtype=np.float32))
+    gv = t(rng.standard_normal((sum(glens), KVH, D), dtype=np.float32))
+    gq = t(rng.standard_normal((B, 32, D), dtype=np.float32))
+
+    def run(reserve=None):
+        m = _mla(gpu, num_layers=1, max_len=1024, page_tokens=64, max_seqs=2)
+        g = _kv(gpu, num_layers=1, max_len=256, num_kv_heads=KVH, head_dim=D, page_tokens=16,
+                max_seqs=B)
+        if reserve:
+            m.Reserve(*reserve[0])
+            g.Reserve(*reserve[1])
+        before = (m.MemoryStats(), g.MemoryStats())
+        m.Append(0, t(cc), t(kr), seq_ids=[0, 1], n_tok=lens)
+        mo = m.Attend(0, qn, qr, w_uk, w_uv, H, D, seq_ids=[0, 1], n_q=lens)
+        g.Append(0, gk, gv, seq_ids=list(range(B)), n_tok=glens, layout="SHD")
+        go = g.Attend(0, gq, 32, seq_ids=list(range(B)))
+        after = (m.MemoryStats(), g.MemoryStats())
+        out = (mo.cpu(), go.cpu())
+        m.close()
+        g.close()
+        return before, after, out
+
+    _, (ms, gs), ref = run()
+    assert ms["workspace_peak"] > 0 and gs["workspace_peak"] > 0 and gs["staging_peak"] > 0
+    assert ms["workspace"] >= ms["workspace_peak"]  # (staging: slots unused so far stay empty)
+    want = ((ms["workspace_peak"], ms["staging_peak"]), (gs["workspace_peak"], gs["staging_peak"]))
+    before, after, got = run(want)
+    for b, a, (wsb, stb) in zip(before, after, want):
+        assert b["workspace"] >= wsb and b["staging"] >= stb
+        assert a["workspace"] == b["workspace"] and a["staging"] == b["staging"], (b, a)
+    for x, y in zip(got, ref):
+        assert torch.equal(x, y)
