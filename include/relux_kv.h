@@ -117,9 +117,12 @@ int32_t rlx_cache_kernel_time(void *cache, float *total_ms, int32_t *count);
  * NewKVCacheSized(numLayers, maxLen, numKVHeads, headDim, BFloat16)
  * (kvcache.go:66-93): capacity per sequence is max_pages_per_seq *
  * page_tokens tokens; pool_pages pages per layer are shared by up to
- * max_seqs sequences.  head_dim any multiple of 8 up to 256 (pages store 16,
- * 32, 64, 96, 128 or 256 dims, the caller's zero padded); page_tokens a
- * multiple of 16. */
+ * max_seqs sequences.  head_dim 1 to 256 (pages store 16, 32, 64, 96, 128
+ * or 256 dims, the caller's zero padded; a head_dim that is not a multiple
+ * of 8 -- the reference's tests use 2 and 4 -- crosses every call padded
+ * to the next multiple of 8 through a per-handle adapter buffer, and
+ * rlx_gqa_attend_noalloc / rlx_gqa_project_append refuse it with
+ * RLX_ERR_UNSUPPORTED); page_tokens a multiple of 16. */
 int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_t page_tokens,
                       int32_t pool_pages, int32_t max_seqs, int32_t max_pages_per_seq, void **out);
 
@@ -308,7 +311,8 @@ int32_t rlx_gqa_append_attend(void *cache, int32_t layer, int32_t n_seqs, const 
  * writes travel in kernel arguments, and no staging buffer is used.  Limits
  * (RLX_ERR_UNSUPPORTED beyond them, nothing launched): at most 32 query rows
  * per kv head, at most 64 rows (sequences, or query tiles of head_dim 16/32
- * calls), partials within the scratch.  rlx_init(device) must have run.
+ * calls), partials within the scratch, a head_dim that is a multiple of 8
+ * (others would need adapter memory).  rlx_init(device) must have run.
  * Every call on a device shares its scratch: calls that overlap on one
  * device (different streams) race. */
 int32_t rlx_gqa_attend_noalloc(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
@@ -321,7 +325,10 @@ int32_t rlx_gqa_attend_noalloc(void *cache, int32_t layer, int32_t n_seqs, const
  * [d_c][num_heads*head_dim] exactly as MLA.W_UK/W_UV are stored (mla.go:42-43),
  * out [rows][num_heads][head_dim].  Computes the same attention as
  * mla.go:316-377 (decompress-all) by absorbing W_UK into the query and
- * W_UV into the output.  scale <= 0 selects 1/sqrt(head_dim + d_r). */
+ * W_UV into the output.  scale <= 0 selects 1/sqrt(head_dim + d_r).
+ * head_dim 1 to 256; one that is not a multiple of 8 crosses padded with
+ * zero dims (q_nope, w_uk, w_uv copied into the handle's adapter buffer,
+ * out copied back). */
 int32_t rlx_mla_attend(void *cache, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                        const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
                        const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,

@@ -240,6 +240,30 @@ hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t
     return hipGetLastError();
 }
 
+// Caller rows whose head width is not a multiple of 8 cross the C boundary
+// through this copy: `rows` rows of sw 16-bit units to rows of dw units,
+// the first min(sw, dw) units copied and the rest of a wider row zeroed
+// (f32 rows count two units per element).  Thread = one destination unit.
+__global__ void repack_rows_kernel(const uint16_t *__restrict__ src, int sw, uint16_t *__restrict__ dst,
+                                   int dw, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / dw;
+        const int k = (int)(i - r * dw);
+        dst[i] = k < sw ? src[r * sw + k] : (uint16_t)0;
+    }
+}
+
+hipError_t launch_repack_rows(hipStream_t s, const void *src, int sw, void *dst, int dw,
+                              int64_t rows, int esz) {
+    const int u = esz / 2;
+    const int64_t n = rows * dw * u;
+    if (n <= 0) return hipSuccess;
+    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    repack_rows_kernel<<<blocks, 256, 0, s>>>((const uint16_t *)src, sw * u, (uint16_t *)dst, dw * u, n);
+    return hipGetLastError();
+}
+
 // Thread = (sequence, kv head h, token t, 8-dim octet).  chunks[c] =
 // (first token r_c, size S_c) of each append, in order.
 __global__ void ref_image_gather_kernel(const uint16_t *__restrict__ kpool,

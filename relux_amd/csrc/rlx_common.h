@@ -411,6 +411,9 @@ hipError_t launch_mla_append(hipStream_t s, const PlanArg *plan, int tok_off, ui
                              int n_patch, const AppendTok *toks, int n_tok, const void *c_src,
                              const void *kr_src, int src_bf16, int dc, int dr, int P);
 
+// rows of sw elements (esz = 2 or 4 bytes) to rows of dw: copied, then zeros.
+hipError_t launch_repack_rows(hipStream_t s, const void *src, int sw, void *dst, int dw,
+                              int64_t rows, int esz);
 hipError_t launch_kv_gather(hipStream_t s, const uint16_t *kpool, const uint16_t *vpool,
                             const int32_t *table, const AttRow *rows, int n_rows, int max_len,
                             uint16_t *k_out, uint16_t *v_out, int kvh, int hd, int hdi, int P);

@@ -116,7 +116,8 @@ struct SpillTier {
 struct Cache {
     int kind = kGQA;
     int layers = 0, kvh = 0, hd = 0, P = 0, pool_pages = 0, max_seqs = 0, max_pages = 0;
-    int hdi = 0;  // GQA: the caller's head dim (hd, the stored one, may be larger: zero padding)
+    int hdi = 0;  // GQA: the kernels' caller head dim (hd, the stored one, may be larger: zero padding)
+    int hdu = 0;  // GQA: the caller's head dim as given (hdi = hdu rounded up to a multiple of 8)
     int dc = 0, dr = 0;
     int device = 0;
     int cus = 256;  // compute units of the device
@@ -129,6 +130,8 @@ struct Cache {
     void *ws = nullptr;
     size_t ws_cap = 0;
     size_t ws_peak = 0;     // largest workspace a call asked for
+    void *ad = nullptr;     // adapter rows of head dims that are not multiples of 8
+    size_t ad_cap = 0;
     size_t stage_peak = 0;  // largest plan a call staged
     SpillTier spill;
     // Attention-kernel timing: event pairs, reused across reports.
@@ -281,6 +284,32 @@ int32_t ensure_ws(Cache *c, size_t bytes) {
     return RLX_OK;
 }
 
+// Caller rows of a head dim that is not a multiple of 8 cross the boundary
+// through the handle's adapter buffer: inputs are copied to rows of the next
+// multiple of 8 (zero filled: zero dims add nothing to a dot product and
+// RoPE pairs (2i, 2i + 1) stay within the caller's dims), the kernels run on
+// those, and outputs are copied back at the caller's width.  Regions of
+// `bytes[i]` each, 256-byte aligned; growing the buffer waits for the stream
+// first (queued kernels may still read the old one).
+int32_t adapter_regions(Cache *c, const size_t *bytes, int n, char **out) {
+    size_t off[8], total = 0;
+    for (int i = 0; i < n; i++) {
+        off[i] = total;
+        total += (bytes[i] + 255) & ~(size_t)255;
+    }
+    if (total > c->ad_cap) {
+        const size_t cap = (std::max(total, c->ad_cap * 2) + 65535) & ~(size_t)65535;
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (c->ad) HIP_TRY(hipFree(c->ad));
+        c->ad = nullptr;
+        c->ad_cap = 0;
+        HIP_TRY(hipMalloc(&c->ad, cap));
+        c->ad_cap = cap;
+    }
+    for (int i = 0; i < n; i++) out[i] = (char *)c->ad + off[i];
+    return RLX_OK;
+}
+
 Cache *as_cache(void *h) { return static_cast<Cache *>(h); }
 
 // Next event pair bracketing a kernel of the given kind (RLX_TIME_*), or
@@ -362,6 +391,7 @@ void destroy_cache(Cache *c) {
     }
     if (c->d_table) (void)hipFree(c->d_table);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->ad) (void)hipFree(c->ad);
     for (auto &p : c->tev) {
         (void)hipEventDestroy(p.first);
         (void)hipEventDestroy(p.second);
@@ -804,8 +834,8 @@ int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_
     if (layers <= 0) return fail(RLX_ERR_INVALID, "NewKVCacheSized: numLayers=%d, must be > 0", layers);
     if (kv_heads <= 0 || pool_pages <= 0 || max_seqs <= 0 || max_pages_per_seq <= 0)
         return fail(RLX_ERR_INVALID, "kv_heads, pool_pages, max_seqs, max_pages must be > 0");
-    if (head_dim <= 0 || head_dim > 256 || head_dim % 8 != 0)
-        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: multiples of 8 up to 256)", head_dim);
+    if (head_dim <= 0 || head_dim > 256)
+        return fail(RLX_ERR_UNSUPPORTED, "head_dim=%d (supported: 1 to 256)", head_dim);
     if (page_tokens <= 0 || page_tokens % 16 != 0)
         return fail(RLX_ERR_UNSUPPORTED, "page_tokens=%d must be a positive multiple of 16", page_tokens);
     Cache *c = new Cache;
@@ -813,14 +843,16 @@ int32_t rlx_kv_create(int32_t layers, int32_t kv_heads, int32_t head_dim, int32_
     c->layers = layers;
     c->kvh = kv_heads;
     // Pages store the smallest supported head dim >= head_dim; the dims past
-    // head_dim hold zeros (written by every append).
+    // head_dim hold zeros (written by every append).  The kernels take caller
+    // rows of a multiple of 8 dims: other widths are padded at the boundary.
+    c->hdu = head_dim;
+    c->hdi = (head_dim + 7) & ~7;
     static const int kStoredDims[] = {16, 32, 64, 96, 128, 256};
     for (int d : kStoredDims)
-        if (d >= head_dim) {
+        if (d >= c->hdi) {
             c->hd = d;
             break;
         }
-    c->hdi = head_dim;
     c->P = page_tokens;
     c->pool_pages = pool_pages;
     c->max_seqs = max_seqs;
@@ -967,20 +999,32 @@ int32_t rlx_cache_kernel_time(void *h, float *total_ms, int32_t *count) {
     return RLX_OK;
 }
 
-int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                      const int32_t *n_tok, const void *k_src, const void *v_src,
-                      int32_t src_dtype, int32_t src_layout) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_kv_append on an MLA cache");
-    int32_t rc = check_layer(c, layer, false);
-    if (rc) return rc;
-    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
-    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
-    if (src_layout != RLX_LAYOUT_HSD && src_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "src_layout");
+// Rows (tokens x kv heads) an append of n_tok tokens per sequence carries.
+static int64_t append_rows(const Cache *c, int n_seqs, const int32_t *n_tok) {
+    int64_t n = 0;
+    for (int i = 0; n_tok && i < n_seqs; i++) n += std::max(0, n_tok[i]);
+    return n * c->kvh;
+}
+
+// rlx_kv_append after its argument checks.  pad: two adapter regions for
+// the K and V rows of a padded head dim, carved by the caller before
+// anything changes (so that a failed allocation leaves the cache as it
+// was), or null.
+static int32_t kv_append_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                              const int32_t *n_tok, const void *k_src, const void *v_src,
+                              int32_t src_dtype, int32_t src_layout, char *const *pad) {
+    int32_t rc;
     std::vector<AppendTok> toks;
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     if (!toks.empty() && (!k_src || !v_src)) return fail(RLX_ERR_INVALID, "null K/V source");
+    if (pad && !toks.empty()) {
+        const int esz = src_dtype == RLX_BF16 ? 2 : 4;
+        const int64_t rows = append_rows(c, n_seqs, n_tok);
+        HIP_TRY(launch_repack_rows(c->stream, k_src, c->hdu, pad[0], c->hdi, rows, esz));
+        HIP_TRY(launch_repack_rows(c->stream, v_src, c->hdu, pad[1], c->hdi, rows, esz));
+        k_src = pad[0];
+        v_src = pad[1];
+    }
     std::vector<Patch> patches = take_pending(c);
     PlanArg plan_arg;
     const PlanArg *plan;
@@ -994,6 +1038,36 @@ int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
                              (int)patches.size(), d_toks, (int)toks.size(), k_src, v_src,
                              src_dtype == RLX_BF16, src_layout, c->kvh, c->hd, c->hdi, c->P));
     return RLX_OK;
+}
+
+static int32_t kv_append_check(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                               int32_t src_dtype, int32_t src_layout) {
+    if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_kv_append on an MLA cache");
+    int32_t rc = check_layer(c, layer, false);
+    if (rc) return rc;
+    if ((rc = check_seqs(c, n_seqs, seq_ids))) return rc;
+    if (src_dtype != RLX_F32 && src_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "src_dtype");
+    if (src_layout != RLX_LAYOUT_HSD && src_layout != RLX_LAYOUT_SHD) return fail(RLX_ERR_INVALID, "src_layout");
+    return RLX_OK;
+}
+
+int32_t rlx_kv_append(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                      const int32_t *n_tok, const void *k_src, const void *v_src,
+                      int32_t src_dtype, int32_t src_layout) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = kv_append_check(c, layer, n_seqs, seq_ids, src_dtype, src_layout);
+    if (rc) return rc;
+    char *pad[2] = {nullptr, nullptr};
+    const int64_t rows = append_rows(c, n_seqs, n_tok);
+    const bool padded = c->hdu != c->hdi && rows > 0;
+    if (padded) {
+        const size_t b = (size_t)rows * c->hdi * (src_dtype == RLX_BF16 ? 2 : 4);
+        const size_t sz[2] = {b, b};
+        if ((rc = adapter_regions(c, sz, 2, pad))) return rc;
+    }
+    return kv_append_impl(c, layer, n_seqs, seq_ids, n_tok, k_src, v_src, src_dtype, src_layout,
+                          padded ? pad : nullptr);
 }
 
 int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t w_dtype,
@@ -1165,6 +1239,9 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
+    if (c->hdu != c->hdi)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_project_append: head_dim %d is not a multiple of 8", c->hdu);
     if (num_heads <= 0 || num_heads % c->kvh != 0)
         return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
     // The packed features come in 16-feature tiles, each within one of the
@@ -1266,6 +1343,17 @@ int32_t rlx_kv_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     gather_rows(c, layer, n_seqs, seq_ids, rows, &max_len);
     if (max_len == 0) return RLX_OK;
     if (!k_out || !v_out) return fail(RLX_ERR_INVALID, "null gather output");
+    void *ko = k_out, *vo = v_out;
+    int64_t pad_rows = 0;
+    if (c->hdu != c->hdi) {  // gathered at the padded width, then narrowed
+        for (const AttRow &r : rows) pad_rows += r.len;
+        pad_rows *= c->kvh;
+        const size_t sz[2] = {(size_t)pad_rows * c->hdi * 2, (size_t)pad_rows * c->hdi * 2};
+        char *pad[2];
+        if ((rc = adapter_regions(c, sz, 2, pad))) return rc;
+        ko = pad[0];
+        vo = pad[1];
+    }
     Blob b;
     size_t o_r = b.add(rows);
     void *dev;
@@ -1273,7 +1361,11 @@ int32_t rlx_kv_gather(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq
     LayerState &ls = c->L[layer];
     HIP_TRY(launch_kv_gather(c->stream, ls.pool0, ls.pool1, c->d_table,
                              (const AttRow *)((char *)dev + o_r), n_seqs, max_len,
-                             (uint16_t *)k_out, (uint16_t *)v_out, c->kvh, c->hd, c->hdi, c->P));
+                             (uint16_t *)ko, (uint16_t *)vo, c->kvh, c->hd, c->hdi, c->P));
+    if (pad_rows > 0) {
+        HIP_TRY(launch_repack_rows(c->stream, ko, c->hdi, k_out, c->hdu, pad_rows, 2));
+        HIP_TRY(launch_repack_rows(c->stream, vo, c->hdi, v_out, c->hdu, pad_rows, 2));
+    }
     return RLX_OK;
 }
 
@@ -1333,6 +1425,37 @@ bool gqa_use_fa2(const Cache *c, int G) {
     return (c->hd == 64 || c->hd == 128 || c->hd == 256) && kPrefillRows % G == 0;
 }
 
+// Query / output rows of a GQA call: sum of n_q (1 per sequence if null)
+// times the query heads.
+int64_t gqa_qo_rows(int n_seqs, const int32_t *n_q, int num_heads) {
+    int64_t n = 0;
+    for (int i = 0; i < n_seqs; i++) n += n_q ? std::max(0, n_q[i]) : 1;
+    return n * num_heads;
+}
+
+// A GQA attention call on (q, out), through adapter rows of the padded head
+// dim when the caller's is not a multiple of 8.  extra / pad: further
+// regions to carve in the same adapter allocation (the K / V rows of
+// rlx_gqa_append_attend), returned in pad.
+template <class F>
+int32_t gqa_call_padded(Cache *c, int64_t rows, const void *q, int32_t q_dtype, void *out,
+                        int32_t out_dtype, F call, size_t extra = 0, char **pad = nullptr) {
+    if (c->hdu == c->hdi || rows <= 0) return call(q, out);
+    const int qe = q_dtype == RLX_BF16 ? 2 : 4, oe = out_dtype == RLX_BF16 ? 2 : 4;
+    const size_t sz[4] = {(size_t)rows * c->hdi * qe, (size_t)rows * c->hdi * oe, extra, extra};
+    char *p[4];
+    int32_t rc = adapter_regions(c, sz, extra ? 4 : 2, p);
+    if (rc) return rc;
+    if (pad) {
+        pad[0] = p[2];
+        pad[1] = p[3];
+    }
+    HIP_TRY(launch_repack_rows(c->stream, q, c->hdu, p[0], c->hdi, rows, qe));
+    if ((rc = call((const void *)p[0], (void *)p[1]))) return rc;
+    HIP_TRY(launch_repack_rows(c->stream, p[1], c->hdi, out, c->hdu, rows, oe));
+    return RLX_OK;
+}
+
 // GQA attention after the argument checks.
 int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                         const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
@@ -1382,7 +1505,7 @@ int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *
         size_t o_r = b.add(rows), o_w = b.add(work);
         void *dev;
         if ((rc = stage(c, b.bytes.data(), b.bytes.size(), &dev))) return rc;
-        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
+        if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdu));
         PrefillArgs a{};
         a.kpool = ls.pool0;
         a.vpool = ls.pool1;
@@ -1455,7 +1578,7 @@ int32_t gqa_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *
         d_rows = (const AttRow *)((char *)dev + o_r);
         d_ranges = (const int4 *)((char *)dev + o_w);
     }
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdu));
     const float qscale = scale * 1.4426950408889634f;
     hipEvent_t e0, e1;
     if ((rc = timing_events(c, &e0, &e1))) return rc;
@@ -1481,8 +1604,11 @@ int32_t rlx_gqa_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
     if (rc) return rc;
     if (n_seqs == 0) return RLX_OK;
     if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
-    return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, q, q_dtype, qo_layout, scale,
-                           mask_mode, out, out_dtype);
+    return gqa_call_padded(c, gqa_qo_rows(n_seqs, n_q, num_heads), q, q_dtype, out, out_dtype,
+                           [&](const void *qk, void *ok) {
+                               return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, qk,
+                                                      q_dtype, qo_layout, scale, mask_mode, ok, out_dtype);
+                           });
 }
 
 int32_t rlx_gqa_append_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
@@ -1518,23 +1644,29 @@ int32_t rlx_gqa_append_attend(void *h, int32_t layer, int32_t n_seqs, const int3
     // first -- was measured and not adopted: the writing wave's wait for its
     // stores cost the decode kernel 1.6-2.1 us, against the append launch's
     // 4.4 us, and lowered the kernel's fraction of peak on every call.)
-    if ((rc = rlx_kv_append(h, layer, n_seqs, seq_ids, n_tok, k_src, v_src, src_dtype, src_layout)))
-        return rc;
-    return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_tok, num_heads, q, q_dtype, qo_layout, scale,
-                           mask_mode, out, out_dtype);
+    // (A padded head dim carves the K / V adapter rows with q's and out's,
+    // before anything is appended.)
+    if ((rc = kv_append_check(c, layer, n_seqs, seq_ids, src_dtype, src_layout))) return rc;
+    const int64_t kv_rows = append_rows(c, n_seqs, n_tok);
+    const size_t kv_bytes = (size_t)kv_rows * c->hdi * (src_dtype == RLX_BF16 ? 2 : 4);
+    char *pad[2] = {nullptr, nullptr};
+    return gqa_call_padded(
+        c, gqa_qo_rows(n_seqs, n_tok, num_heads), q, q_dtype, out, out_dtype,
+        [&](const void *qk, void *ok) {
+            int32_t r = kv_append_impl(c, layer, n_seqs, seq_ids, n_tok, k_src, v_src, src_dtype,
+                                       src_layout, pad[0] ? pad : nullptr);
+            if (r) return r;
+            return gqa_attend_impl(c, layer, n_seqs, seq_ids, n_tok, num_heads, qk, q_dtype, qo_layout,
+                                   scale, mask_mode, ok, out_dtype);
+        },
+        c->hdu != c->hdi ? kv_bytes : 0, pad);
 }
 
-int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
-                                 const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
-                                 int32_t qo_layout, float scale, int32_t mask_mode, void *out,
-                                 int32_t out_dtype) {
-    if (!h) return fail(RLX_ERR_INVALID, "null cache");
-    Cache *c = as_cache(h);
-    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout, mask_mode,
-                                  out_dtype);
-    if (rc) return rc;
-    if (n_seqs == 0) return RLX_OK;
-    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+static int32_t gqa_ref_image_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                  const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                                  int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                                  int32_t out_dtype) {
+    int32_t rc;
     LayerState &ls = c->L[layer];
     const int G = num_heads / c->kvh;
     const int cap = gqa_rows_cap(c);
@@ -1614,7 +1746,7 @@ int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const i
                                     (const RefImgSeq *)((char *)dev + o_s), n_seqs, max_len,
                                     (const int2 *)((char *)dev + o_c), c->kvh, c->hd, c->P, dk, dv, dtable,
                                     n_pages));
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdu));
     const float qscale = scale * 1.4426950408889634f;
     HIP_TRY(launch_gqa_decode(c->stream, nullptr, dk, dv, dtable, (const AttRow *)((char *)dev + o_r), n_rows,
                               (const int4 *)((char *)dev + o_w), n_ranges, q, q_dtype == RLX_BF16, qo_layout,
@@ -1622,6 +1754,25 @@ int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const i
                               mask_mode, nqt, po, pm, out, out_dtype == RLX_BF16, std::min(max_qr, cap),
                               nullptr, nullptr));
     return RLX_OK;
+}
+
+int32_t rlx_gqa_attend_ref_image(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                 const int32_t *n_q, int32_t num_heads, const void *q, int32_t q_dtype,
+                                 int32_t qo_layout, float scale, int32_t mask_mode, void *out,
+                                 int32_t out_dtype) {
+    if (!h) return fail(RLX_ERR_INVALID, "null cache");
+    Cache *c = as_cache(h);
+    int32_t rc = check_gqa_attend(c, layer, n_seqs, seq_ids, num_heads, q_dtype, qo_layout, mask_mode,
+                                  out_dtype);
+    if (rc) return rc;
+    if (n_seqs == 0) return RLX_OK;
+    if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    return gqa_call_padded(c, gqa_qo_rows(n_seqs, n_q, num_heads), q, q_dtype, out, out_dtype,
+                           [&](const void *qk, void *ok) {
+                               return gqa_ref_image_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, qk,
+                                                         q_dtype, qo_layout, scale, mask_mode, ok,
+                                                         out_dtype);
+                           });
 }
 
 int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
@@ -1635,6 +1786,10 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     if (rc) return rc;
     if (n_seqs == 0) return RLX_OK;
     if (!q || !out) return fail(RLX_ERR_INVALID, "null q/out");
+    if (c->hdu != c->hdi)
+        return fail(RLX_ERR_UNSUPPORTED,
+                    "rlx_gqa_attend_noalloc: head_dim %d is not a multiple of 8 (its rows would cross "
+                    "through adapter memory)", c->hdu);
     void *scr = (c->device >= 0 && c->device < kMaxDevices) ? g_scratch[c->device] : nullptr;
     if (!scr) return fail(RLX_ERR_STATE, "no scratch address for device %d (rlx_init not run)", c->device);
     const int G = num_heads / c->kvh;
@@ -1683,7 +1838,7 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
         memcpy(plan.b + rows_bytes, ranges, (size_t)n_ranges * sizeof(int4));
         ranges_off = (int)rows_bytes;
     }
-    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdi));
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)c->hdu));
     HIP_TRY(launch_gqa_decode(c->stream, &plan, c->L[layer].pool0, c->L[layer].pool1, c->d_table,
                               nullptr, n_rows, nullptr, n_ranges, q, q_dtype == RLX_BF16, qo_layout,
                               num_heads, c->kvh, c->hd, c->hdi, c->P, total64, kGqaSnap64, ranges_off,
@@ -1740,9 +1895,8 @@ static int32_t mla_attend_check(Cache *c, int32_t n_seqs, const int32_t *n_q, in
                                 int32_t head_dim, const void *q_nope, const void *q_rope,
                                 int32_t q_dtype, const void *w_uk, const void *w_uv,
                                 int32_t mask_mode, void *out, int32_t out_dtype) {
-    if (num_heads <= 0 || head_dim <= 0 || head_dim % 8 != 0 || head_dim > 256)
-        return fail(RLX_ERR_UNSUPPORTED,
-                    "num_heads=%d head_dim=%d (head_dim a multiple of 8 up to 256)", num_heads, head_dim);
+    if (num_heads <= 0 || head_dim <= 0 || head_dim > 256)
+        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim 1 to 256)", num_heads, head_dim);
     if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
     if (out_dtype != RLX_F32 && out_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "out_dtype");
     if (mask_mode < RLX_MASK_CAUSAL || mask_mode > RLX_MASK_NONE) return fail(RLX_ERR_INVALID, "mask_mode");
@@ -1983,6 +2137,47 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     return RLX_OK;
 }
 
+static int32_t mla_append_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                      const int32_t *n_tok, const void *c_src, const void *kr_src,
+                                      int32_t src_dtype, int32_t num_heads, int32_t head_dim,
+                                      const void *q_nope, const void *q_rope, int32_t q_dtype,
+                                      const void *w_uk, const void *w_uv, float scale, int32_t mask_mode,
+                                      void *out, int32_t out_dtype);
+
+}  // extern "C"
+
+// An MLA attention call through adapter rows when head_dim is not a
+// multiple of 8: q_nope [rows][H][D], W_UK and W_UV [d_c][H][D] and out
+// cross at the next multiple of 8 (zero dims), with the default scale of
+// the caller's head dim.  call(head_dim, q_nope, w_uk, w_uv, out, scale).
+template <class F>
+static int32_t mla_call_padded(Cache *c, int n_seqs, const int32_t *n_q, int num_heads, int head_dim,
+                               const void *q_nope, int32_t q_dtype, const void *w_uk, const void *w_uv,
+                               void *out, int32_t out_dtype, float scale, F call) {
+    if (head_dim % 8 == 0) return call(head_dim, q_nope, w_uk, w_uv, out, scale);
+    const int hp = (head_dim + 7) & ~7;
+    if (scale <= 0.f) scale = (float)(1.0 / std::sqrt((double)(head_dim + c->dr)));
+    int64_t rows = 0;
+    for (int i = 0; i < n_seqs; i++) rows += n_q ? std::max(0, n_q[i]) : 1;
+    rows *= num_heads;
+    const int64_t wrows = (int64_t)c->dc * num_heads;
+    const int qe = q_dtype == RLX_BF16 ? 2 : 4, oe = out_dtype == RLX_BF16 ? 2 : 4;
+    const size_t sz[4] = {(size_t)rows * hp * qe, (size_t)wrows * hp * 2, (size_t)wrows * hp * 2,
+                          (size_t)rows * hp * oe};
+    char *p[4];
+    int32_t rc = adapter_regions(c, sz, 4, p);
+    if (rc) return rc;
+    HIP_TRY(launch_repack_rows(c->stream, q_nope, head_dim, p[0], hp, rows, qe));
+    HIP_TRY(launch_repack_rows(c->stream, w_uk, head_dim, p[1], hp, wrows, 2));
+    HIP_TRY(launch_repack_rows(c->stream, w_uv, head_dim, p[2], hp, wrows, 2));
+    if ((rc = call(hp, (const void *)p[0], (const void *)p[1], (const void *)p[2], (void *)p[3], scale)))
+        return rc;
+    HIP_TRY(launch_repack_rows(c->stream, p[3], hp, out, head_dim, rows, oe));
+    return RLX_OK;
+}
+
+extern "C" {
+
 int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
                        const int32_t *n_q, int32_t num_heads, int32_t head_dim, const void *q_nope,
                        const void *q_rope, int32_t q_dtype, const void *w_uk, const void *w_uv,
@@ -1997,9 +2192,14 @@ int32_t rlx_mla_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *se
                                mask_mode, out, out_dtype)))
         return rc;
     if (n_seqs == 0) return RLX_OK;
-    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_q, nullptr, num_heads, head_dim))) return rc;
-    return mla_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, head_dim, q_nope, q_rope, q_dtype,
-                           w_uk, w_uv, scale, mask_mode, out, out_dtype, nullptr);
+    const int hk = (head_dim + 7) & ~7;  // the kernels' head dim
+    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_q, nullptr, num_heads, hk))) return rc;
+    return mla_call_padded(c, n_seqs, n_q, num_heads, head_dim, q_nope, q_dtype, w_uk, w_uv, out, out_dtype,
+                           scale, [&](int hd, const void *qn, const void *wk, const void *wv, void *o, float sc) {
+                               return mla_attend_impl(c, layer, n_seqs, seq_ids, n_q, num_heads, hd, qn,
+                                                      q_rope, q_dtype, wk, wv, sc, mask_mode, o, out_dtype,
+                                                      nullptr);
+                           });
 }
 
 int32_t rlx_mla_append_attend(void *h, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
@@ -2023,8 +2223,26 @@ int32_t rlx_mla_append_attend(void *h, int32_t layer, int32_t n_seqs, const int3
         return rc;
     if (n_seqs == 0) return RLX_OK;
     if (!c_src || !kr_src) return fail(RLX_ERR_INVALID, "null latent source");
-    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_tok, n_tok, num_heads, head_dim))) return rc;
-    // The append (rlx_mla_append), then attention of the appended tokens.
+    const int hk = (head_dim + 7) & ~7;  // the kernels' head dim
+    if ((rc = mla_prefill_check(c, layer, n_seqs, seq_ids, n_tok, n_tok, num_heads, hk))) return rc;
+    return mla_call_padded(c, n_seqs, n_tok, num_heads, head_dim, q_nope, q_dtype, w_uk, w_uv, out,
+                           out_dtype, scale,
+                           [&](int hd, const void *qn, const void *wk, const void *wv, void *o, float sc) {
+                               return mla_append_attend_impl(c, layer, n_seqs, seq_ids, n_tok, c_src, kr_src,
+                                                             src_dtype, num_heads, hd, qn, q_rope, q_dtype,
+                                                             wk, wv, sc, mask_mode, o, out_dtype);
+                           });
+}
+
+// rlx_mla_append_attend after its checks: the append (rlx_mla_append), then
+// attention of the appended tokens.
+static int32_t mla_append_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const int32_t *seq_ids,
+                                      const int32_t *n_tok, const void *c_src, const void *kr_src,
+                                      int32_t src_dtype, int32_t num_heads, int32_t head_dim,
+                                      const void *q_nope, const void *q_rope, int32_t q_dtype,
+                                      const void *w_uk, const void *w_uv, float scale, int32_t mask_mode,
+                                      void *out, int32_t out_dtype) {
+    int32_t rc;
     std::vector<AppendTok> toks;
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     std::vector<Patch> patches = take_pending(c);

@@ -78,6 +78,14 @@ def _fill_gqa(c, rng, gpu, lens, KVH, D, chunks=2):
     (16, 2, 256, [400, 65], 2, "causal"),                            # 256: 16-row tiles
     (4, 2, 8, [8, 23, 300], 1, "causal"),                            # 8: stored as 16
     (8, 2, 48, [260, 9], 3, "ref"),                                  # 48: stored as 64
+    # head dims that are not multiples of 8 (rows padded at the C boundary):
+    # the reference tests' own shapes, then wider ones on every path
+    (2, 1, 2, [3, 40, 300], 1, "causal"),                            # mha_test.go:86 (dModel 4, 2 heads)
+    (4, 2, 2, [9, 300], 4, "causal"),                                # NewMHA(8, 4, 2): head_dim 2
+    (1, 1, 4, [5, 260], 1, "causal"),                                # NewMHA(4, 1, 1): head_dim 4
+    (4, 1, 20, [70, 300], 40, "causal"),                             # 160 rows per kv head: query chunks
+    (8, 2, 100, [300, 77], 50, "causal"),                            # 100 (stored 128): FA2 prefill
+    (16, 4, 250, [290], 2, "causal"),                                # 250 (stored 256)
 ])
 def test_gqa_attend_matches_oracle(gpu, H, KVH, D, lens, nq, mask):
     from relux_amd import KVCache
@@ -412,6 +420,12 @@ def test_mla_decode_many_splits(gpu):
     (16, 128, 512, 64, [300, 65], 1, "causal"),    # default DeepSeek dims, generic absorb / out
     (8, 128, 256, 32, [2100, 70], 1, "causal"),    # head_dim 128 with d_c < 512: latent channels past d_c
     (16, 96, 384, 48, [260], 2, "causal"),
+    # head dims that are not multiples of 8 (q_nope, W_UK, W_UV and the
+    # output padded at the boundary): mla_test.go's dims (dModel 8, 2 heads:
+    # headDim 4, dC 16, dHR 2), decode and FA2 prefill, and head_dim 20
+    (2, 4, 16, 2, [9, 70], 1, "causal"),
+    (2, 4, 16, 2, [60, 30], 40, "causal"),
+    (3, 20, 80, 10, [300, 20], 2, "causal"),
     (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128 prefill through FA2 (240 rows)
     # FA2 at the reference's default dims (K_c / V^T expanded with zero rows
     # to a 128-dim pitch, W_UK / W_UV columns past d_c zero): 64 heads at
@@ -424,7 +438,8 @@ def test_mla_decode_many_splits(gpu):
 def test_mla_other_dims_match_oracle(gpu, H, D, dC, dR, lens, nq, mask):
     """MLA at the reference's default dims (dC = 4 headDim, dHR = headDim/2,
     transformer.go:223-233) and others: latent rows stored zero padded,
-    absorb and W_UV projection at any head_dim multiple of 8, and calls with
+    absorb and W_UV projection at head_dims that are multiples of 8 (other
+    widths padded to one at the C boundary), and calls with
     more than 32 query rows cut into causal query chunks (or single-query
     rows when unmasked) through the decode kernel."""
     from relux_amd import MLACache
@@ -699,7 +714,8 @@ def test_mla_prefill_head_groups_identical(gpu, monkeypatch, H, budget_mb):
 
 
 @pytest.mark.parametrize("case", ["decode_f32_shd", "decode_bf16_hsd_d64", "multi4_p32", "d80_two",
-                                  "d256", "nqt2", "pending_freed", "compacted", "big_plan", "fa2"])
+                                  "d256", "nqt2", "pending_freed", "compacted", "big_plan", "fa2",
+                                  "d12_padded", "d100_padded_fa2"])
 def test_gqa_append_attend_equals_append_then_attend(gpu, case):
     """rlx_gqa_append_attend against rlx_kv_append followed by
     rlx_gqa_attend on a twin cache: outputs, K/V bytes, page tables, free
@@ -719,6 +735,9 @@ def test_gqa_append_attend_equals_append_then_attend(gpu, case):
         "compacted": (8, 2, 128, 16, 1, 6, torch.bfloat16, "SHD"),
         "big_plan": (8, 8, 64, 16, 1, 100, torch.bfloat16, "SHD"),
         "fa2": (8, 2, 128, 16, 40, 2, torch.bfloat16, "SHD"),
+        # head dims padded to a multiple of 8 at the boundary (K, V, q, out)
+        "d12_padded": (4, 2, 12, 16, 2, 4, torch.float32, "HSD"),
+        "d100_padded_fa2": (8, 2, 100, 16, 40, 2, torch.bfloat16, "SHD"),
     }[case]
     H, KVH, D, P, ntok, B, dt, kvl = cfg
     rng = np.random.default_rng(sum(map(ord, case)))
@@ -807,9 +826,9 @@ def test_mla_append_attend_equals_append_then_attend(gpu, case):
     a.Append(1, c1, k1, seq_ids=seqs, n_tok=n_tok)
     want = a.Attend(1, qn, qr, w[0], w[1], H, D, seq_ids=seqs, n_q=n_tok).cpu()
     from relux_amd import _lib
-    bad = f._lib.rlx_mla_append_attend(  # head_dim not a multiple of 8
+    bad = f._lib.rlx_mla_append_attend(  # head_dim past 256
         f._h, 1, B, _lib.i32_array(seqs), _lib.i32_array(n_tok), c1.data_ptr(), k1.data_ptr(),
-        _lib.RLX_F32 if dt == torch.float32 else _lib.RLX_BF16, H, D - 4, qn.data_ptr(), qr.data_ptr(),
+        _lib.RLX_F32 if dt == torch.float32 else _lib.RLX_BF16, H, 300, qn.data_ptr(), qr.data_ptr(),
         _lib.RLX_F32 if dt == torch.float32 else _lib.RLX_BF16, w[0].data_ptr(), w[1].data_ptr(), 0.0,
         _lib.RLX_MASK_CAUSAL, torch.empty(rows, H, D, device=gpu).data_ptr(), _lib.RLX_F32)
     assert bad == _lib.RLX_ERR_UNSUPPORTED

@@ -113,8 +113,8 @@ def test_multi_sequence_append_gather_bit_exact(gpu, src_dtype, layout, D):
 
 @pytest.mark.parametrize("D", [8, 48, 96, 256])
 def test_append_gather_other_head_dims(gpu, D):
-    """head_dim any multiple of 8 up to 256 (NewKVCacheSized takes any,
-    kvcache.go:66-93): stored as 16/32/64/96/128/256 dims, zero padded;
+    """head_dims that are multiples of 8 up to 256 (NewKVCacheSized takes any,
+    kvcache.go:66-93; other widths below): stored as 16/32/64/96/128/256 dims, zero padded;
     View returns exactly the appended rows, across pages and two calls."""
     rng = np.random.default_rng(D)
     KVH, P = 2, 16
@@ -137,7 +137,7 @@ def test_append_gather_other_head_dims(gpu, D):
         assert np.array_equal(cv.view(torch.int16).cpu().numpy().view(np.uint16)[0], want_v)
     c.close()
     from relux_amd import _lib
-    for bad in (12, 264, 0):
+    for bad in (264, 0):
         with pytest.raises(_lib.ReluxError) as e:
             _kv(gpu, num_layers=1, max_len=16, num_kv_heads=1, head_dim=bad)
         assert e.value.code in (_lib.RLX_ERR_UNSUPPORTED, _lib.RLX_ERR_INVALID)
@@ -511,3 +511,39 @@ def test_reserve_keeps_calls_from_allocating(gpu):
         assert a["workspace"] == b["workspace"] and a["staging"] == b["staging"], (b, a)
     for x, y in zip(got, ref):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("D", [2, 4, 12, 100])
+def test_odd_head_dims_append_and_gather_bit_exact(gpu, D):
+    """head_dim not a multiple of 8 (the reference tests' 2 and 4, and wider):
+    appended rows cross the C boundary padded with zero dims, the gather
+    narrows them back; f32 and bf16 sources, both layouts, bit-exact against
+    BF16FromF32.  The no-allocation attention refuses such head dims (its
+    rows would need adapter memory)."""
+    from relux_amd import _lib
+    rng = np.random.default_rng(500 + D)
+    KVH, lens = 2, [5, 40, 17]
+    c = _kv(gpu, num_layers=1, max_len=64, num_kv_heads=KVH, head_dim=D, max_seqs=3)
+    want = [[] for _ in lens]
+    for step, (dt, layout) in enumerate([(torch.float32, "SHD"), (torch.bfloat16, "HSD")]):
+        n = [L // 2 if step == 0 else L - L // 2 for L in lens]
+        rows = [rng.standard_normal((KVH, m, D), dtype=np.float32) for m in n]  # logical [KVH][n][D]
+        if layout == "SHD":
+            src = np.concatenate([r.transpose(1, 0, 2) for r in rows])
+        else:
+            src = np.concatenate([r.reshape(-1, D) for r in rows])
+        t = torch.from_numpy(np.ascontiguousarray(src)).to(gpu).to(dt)
+        c.Append(0, t, t * 2, seq_ids=[0, 1, 2], n_tok=n, layout=layout)
+        for i, r in enumerate(rows):
+            want[i].append(oracle.round_bf16(torch.from_numpy(r).to(dt).float().numpy()))
+    for i in range(len(lens)):
+        k, v = c.View(0, i)
+        w = np.concatenate(want[i], axis=1)[None]
+        assert np.array_equal(k.float().cpu().numpy(), w), (D, i)
+        assert np.array_equal(v.float().cpu().numpy(), oracle.round_bf16(w * 2)), (D, i)
+    q = torch.zeros((3, 4, D), device=gpu)
+    out = torch.empty_like(q)
+    if D % 8:
+        with pytest.raises(_lib.ReluxError) as e:
+            c.AttendNoAlloc(0, q, 4, out, seq_ids=[0, 1, 2])
+        assert e.value.code == _lib.RLX_ERR_UNSUPPORTED
