@@ -85,7 +85,14 @@ struct PfShape {
     static constexpr int ST = NKR * 512 + DV * 8;                    // chunks per stage
     static constexpr int LV = DV / 64;                               // V^T loads per wave
     static constexpr int LPW = NKR + LV;                             // ring loads per wave
-    static constexpr int S = ST * 16 * 4 <= 131072 ? 4 : ST * 16 * 3 <= 163840 ? 3 : 2;  // ring stages
+    static constexpr int S = ST * 16 * 4 <= 131072 ? 4 : ST * 16 * 3 <= 163840 ? 3 : 2;  // blocks in flight + 1
+    // Staggered waves (waves 4-7 run their P.V of block j - 1 in iteration
+    // j) keep one more stage resident: the dense (MLA) shape, where it fits
+    // the 160 KB and measured faster (config 4: 4.45-4.48 -> 4.36-4.39 ms;
+    // the paged GQA shapes at D 64 / 128 were unchanged, so they keep the
+    // plain schedule).
+    static constexpr bool STAG = SRC == kSrcDense && ST * 16 * (S + 1) <= 163840;
+    static constexpr int SR = S + (STAG ? 1 : 0);                    // ring stages
     static constexpr int MD = DV / 32;                               // output dim tiles
     static_assert(DQK % 64 == 0 && DV % 64 == 0, "whole 64-dim regions");
     static_assert(SRC == kSrcPaged || DV == 128, "dense: 128 value dims per launch");
@@ -97,8 +104,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                                                           const int32_t *__restrict__ table) {
     using SH = PfShape<DQK, DV, SRC>;
     constexpr int KS = SH::KS, NKR = SH::NKR, S = SH::S, MD = SH::MD, LV = SH::LV, LPW = SH::LPW;
-    constexpr int DP = SH::DP;
-    __shared__ __attribute__((aligned(16))) uint16_t ring[S * SH::ST * 8];
+    constexpr int DP = SH::DP, SR = SH::SR;
+    constexpr bool STAG = SH::STAG;
+    __shared__ __attribute__((aligned(16))) uint16_t ring[SR * SH::ST * 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31, hh = lane >> 5;
     const int4 wk = a.work[blockIdx.x];
@@ -173,7 +181,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         const uint32_t stage = ring_lds + st_next;
         const uint32_t kdst = stage + (uint32_t)(wave * 64) * 16;  // + region q: q * 8 KB
         const uint16_t *kc_blk = kc_next, *vt_blk = vt_next, *kr_blk = kr_next;
-        st_next = (st_next + kStageBytes == S * kStageBytes) ? 0u : st_next + kStageBytes;
+        st_next = (st_next + kStageBytes == SR * kStageBytes) ? 0u : st_next + kStageBytes;
         if (SRC == kSrcDense) {
             kc_next += kKeyBlock * DP;
             vt_next += kKeyBlock;
@@ -357,8 +365,45 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     fl16 negm;
 #pragma unroll
     for (int i = 0; i < 16; i++) negm[i] = 0.f;
+    // P^T operands of the current block (the lagging waves keep them into
+    // the next iteration).
+    u32x4 pw[4];
+    // P.V of the weights in pw over the V^T region of stage sv, operand
+    // reads kPfD steps ahead (the lagging waves' form: no softmax work to
+    // interleave).
+    auto pv_plain = [&](const uint16_t *sv) {
+        constexpr int NV = 4 * MD;
+        auto vr = [&](int n) { return *(const u32x4 *)&sv[vrd[n / MD] + (n % MD) * 32 * 64]; };
+        u32x4 va[kPfD + 1];
+#pragma unroll
+        for (int n = 0; n < kPfD; n++) va[n] = vr(n);
+#pragma unroll
+        for (int n = 0; n < NV; n++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (n + kPfD < NV) va[(n + kPfD) % (kPfD + 1)] = vr(n + kPfD);
+            const int md = n % MD;
+            acc[md] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8, va[n % (kPfD + 1)]), __builtin_bit_cast(bf16x8, pw[n / MD]),
+                acc[md], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
-    for (int j = 0, st_read = 0; j < nblk; j++, st_read = (st_read + SH::ST * 8 == S * SH::ST * 8) ? 0 : st_read + SH::ST * 8) {
+    // Staggered schedule: waves w and w + 4 share a SIMD.  Waves 0-3 run
+    // block j's scores, softmax and P.V in iteration j; waves 4-7 first run
+    // the P.V of block j - 1 (its weights kept in registers), then block j's
+    // scores and softmax, so that one wave's softmax meets the other's
+    // products instead of both waiting on the matrix unit's neighbour at
+    // once.  Block j - 1 stays resident through iteration j: the refill of
+    // iteration j goes to block j - 2's stage (SR = S + 1 stages).
+    // The two schedules are separate loops (a compile-time flag each), so
+    // that each gets its own register allocation; both pass the same
+    // barriers.
+    auto run = [&](auto lagc) {
+    constexpr bool lag = decltype(lagc)::value;
+    int st_prev = 0;
+    for (int j = 0, st_read = 0; j < nblk;
+         j++, st_prev = st_read, st_read = (st_read + SH::ST * 8 == SR * SH::ST * 8) ? 0 : st_read + SH::ST * 8) {
         wait_block(j);
         ring_barrier();
         if (SRC == kSrcPaged && j + S - 1 < nblk) issue_block(j + S - 1);
@@ -390,8 +435,11 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             return *(const u32x4 *)&st[(ks >> 2) * 4096 + krd[kt][ks & 3]];
         };
         auto vread = [&](int n) { return *(const u32x4 *)&st[vrd[n / MD] + (n % MD) * 32 * 64]; };
+        // The lagging waves' P.V of the previous block (its stage stays
+        // resident through this iteration).
+        if constexpr (lag)
+            if (j > 0) pv_plain(ring + st_prev);
         fl16 sc[2];
-        u32x4 pw[4];
         float lt[2] = {0.f, 0.f};
         // With FOLD, sc holds s - m_use (m_use = the running max, 0 before a
         // row's first unmasked key); a rescale moves m_use and shifts the
@@ -420,7 +468,10 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             for (int i = 0; i < 16; i++)
                 if (32 * kt + 16 * (i >> 3) + (i & 7) > t) sc[kt][i] = -INFINITY;
         };
-        auto fixup = [&](int kt) {
+        // redo0 (the lagging waves at tile 1): tile 0's weights are not in
+        // the accumulators yet, so a rescale recomputes them at the new max,
+        // and l_part takes their new sum in place of the old one scaled.
+        auto fixup = [&](int kt, bool redo0 = false) {
             if (__builtin_amdgcn_ballot_w64(!(lt[kt] <= kLazySum) || (m_run == -INFINITY && lt[kt] > 0.f))) {
                 float mx = sc[kt][0];
 #pragma unroll
@@ -443,8 +494,15 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
                     for (int i = 0; i < 16; i++) {
                         negm[i] = -m_use;
                         sc[kt][i] -= dlt;
-                        if (kt == 0) sc[1][i] -= dlt;  // tile 1 is weighed after this
+                        if (kt == 0 || redo0) sc[1 - kt][i] -= dlt;  // tile 1 is weighed after this
                     }
+                }
+                if (redo0) {
+                    const float old0 = lt[0] * c;
+                    lt[0] = 0.f;
+#pragma unroll
+                    for (int k = 0; k < 8; k++) pword(0, k);
+                    l_part += lt[0] - old0;
                 }
                 lt[kt] = 0.f;
 #pragma unroll
@@ -485,6 +543,13 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
         if (SRC == kSrcDense && j + S - 1 < nblk) issue_block(j + S - 1);
         if (need_mask) mask(1);
         fixup(0);
+        if constexpr (lag) {
+            // tile 1's weights now; the products follow next iteration
+#pragma unroll
+            for (int k = 0; k < 8; k++) pword(1, k);
+            fixup(1, true);
+            continue;
+        }
         // P.V with the V^T operands kPfD steps ahead; tile 1's weights during
         // tile 0's products.
         {
@@ -512,6 +577,14 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+
+    if constexpr (lag)
+        if (nblk > 0) pv_plain(ring + st_prev);  // the last block's P.V
+    };
+    if (STAG && wave >= kWaves / 2)
+        run(std::true_type{});
+    else
+        run(std::false_type{});
 
     // ---- normalise and write ----------------------------------------------
     {
