@@ -179,10 +179,14 @@ int32_t rlx_kv_append(void *cache, int32_t layer, int32_t n_seqs, const int32_t 
 /* ---- fused pre-attention step (projection + RoPE + append) ------------- */
 /* Pack a GQA layer's W_q [d_model][H*D], W_k and W_v [d_model][KVH*D] (the
  * reference's in-row/out-col layout, mha.go:84-100, bf16 or f32) into the
- * bf16 layout rlx_gqa_project_append streams: N = (H + 2*KVH)*D output
- * features (q heads, then k heads, then v heads); element (n, k) at
- * ((n/16 * d_model/32 + k/32) * 16 + n%16) * 32 + k%32 of out (N * d_model
- * bf16).  Runs on the null stream.  No reference counterpart: a one-time
+ * bf16 layout rlx_gqa_project_append streams: N = (H + 2*KVH)*W output
+ * features (q heads, then k heads, then v heads, W each: W = D when H*D and
+ * KVH*D are multiples of 16, else D rounded up to 16 with zero weights past
+ * D); element (n, k) at
+ * ((n/16 * K/32 + k/32) * 16 + n%16) * 32 + k%32 of out (N * K bf16, K =
+ * d_model rounded up to 32 with zero rows; the projection then copies x rows
+ * of a d_model that is not a multiple of 32 to that width through the
+ * handle's adapter buffer).  Runs on the null stream.  No reference counterpart: a one-time
  * weight preparation. */
 int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t w_dtype,
                      int32_t d_model, int32_t num_heads, int32_t kv_heads, int32_t head_dim,
@@ -194,8 +198,9 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
  * round-to-nearest-even); q_out [sum n][num_heads][head_dim] receives the
  * rotated queries for rlx_gqa_attend.  head_dim is the cache's (its pages
  * may store it padded: the padding of the new rows is written with zeros);
- * num_heads x head_dim and kv_heads x head_dim must be multiples of 16
- * (RLX_ERR_UNSUPPORTED otherwise).  Replaces mha.go:250-289
+ * any even head_dim (RoPE rotates pairs; an odd one fails with
+ * RLX_ERR_UNSUPPORTED), with weights packed by rlx_pack_qkv for the same
+ * heads.  Replaces mha.go:250-289
  * (matmulBatched3D x3, rearrange, RotaryEmbedding.Apply, KVCache.Append).
  * Projections run on MFMA (bf16 operands, f32 sums): results match the
  * reference's f32 loops within tolerance, not bit for bit.  A position at
@@ -236,8 +241,11 @@ int32_t rlx_mla_project_append(void *cache, int32_t layer, int32_t n_seqs, const
  * output [rows][H*D]; mla.go:384-389) and the transformer block's residual
  * add (transformer_block.go:119-142), which the reference runs on the host.
  * W [k_in][n_out] (the reference's in-row/out-col layout, bf16 or f32) is
- * packed once by rlx_pack_out into k_in*n_out bf16; k_in % 32 == 0,
- * n_out % 16 == 0.  x: device [rows][k_in] (RLX_F32 / RLX_BF16; f32 rows are
+ * packed once by rlx_pack_out into n_out' * k_in' bf16 (n_out' = n_out
+ * rounded up to 16, k_in' = k_in rounded up to 32, zero weights in the
+ * padding; x rows of a k_in that is not a multiple of 32 are copied to the
+ * padded width through the handle's adapter buffer).  x: device
+ * [rows][k_in] (RLX_F32 / RLX_BF16; f32 rows are
  * used at f32 precision); residual: NULL or device [rows][n_out] in
  * out_dtype; out: device [rows][n_out].  Runs on cache's stream. */
 int32_t rlx_pack_out(const void *w, int32_t w_dtype, int32_t k_in, int32_t n_out, void *out);

@@ -9,13 +9,14 @@ reference's Go cache types (internal/transformer/kvcache.go, mla_cache.go).
 """
 from ._lib import ReluxError, ReluxPanic, load  # noqa: F401
 
-__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "pack_mla_proj", "pack_out", "rope_tables",
+__all__ = ["KVCache", "MLACache", "ReluxError", "ReluxPanic", "load", "pack_qkv", "gqa_pack_width", "pack_mla_proj", "pack_out", "rope_tables",
            "Sampler", "SpeculativeDecoder", "Draws", "spec_accept", "spec_accept_async"]
 
 
 def __getattr__(name):
     # Lazy: importing the package must not touch the GPU or require torch.
-    if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "pack_mla_proj", "pack_out", "rope_tables"):
+    if name in ("KVCache", "MLACache", "default_scale", "pack_qkv", "gqa_pack_width", "pack_mla_proj", "pack_out",
+                "rope_tables"):
         from . import kvcache
         return getattr(kvcache, name)
     if name in ("Sampler", "SpeculativeDecoder", "Draws", "spec_accept", "spec_accept_async"):

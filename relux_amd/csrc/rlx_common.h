@@ -593,16 +593,23 @@ struct PackSrc {
 };
 hipError_t launch_pack_proj(hipStream_t s, const PackSrc &src, int w_bf16, int K, uint16_t *out);
 // Shapes of a projection: GQA (H, KVH, D = the caller's head dim, DS = the
-// pool's); MLA (H, D = q_c dims per head, DR / DC = d_r / d_c and DRP / DCP =
-// the same rounded up to 16, the packed widths of the rope heads and of the
-// latent); kProjOut (D = output features).
+// pool's, DW = the packed features per head); MLA (H, D = q_c dims per head,
+// DR / DC = d_r / d_c and DRP / DCP = the same rounded up to 16, the packed
+// widths of the rope heads and of the latent); kProjOut (D = output
+// features, DW = the same rounded up to 16, the packed ones).
 struct ProjDims {
-    int H, KVH, D, DS, DR, DRP, DC, DCP;
+    int H, KVH, D, DS, DR, DRP, DC, DCP, DW;
 };
+// Packed features per GQA head: the head dim when the q and k parts are
+// whole 16-feature tiles (H D and KVH D multiples of 16), else the head dim
+// rounded up to 16 (zero weights past it).
+__host__ __device__ inline int gqa_pack_width(int H, int KVH, int D) {
+    return ((H * D) % 16 == 0 && (KVH * D) % 16 == 0) ? D : (D + 15) / 16 * 16;
+}
 __host__ __device__ inline int proj_features(int model, const ProjDims &pd) {
-    return model == kProjModelGQA ? (pd.H + 2 * pd.KVH) * pd.D
+    return model == kProjModelGQA ? (pd.H + 2 * pd.KVH) * pd.DW
          : model == kProjModelMLA ? pd.H * (pd.D + pd.DRP) + pd.DCP + pd.DRP
-                                  : pd.D;
+                                  : pd.DW;
 }
 hipError_t launch_proj_pad_zero(hipStream_t s, int model, const PlanArg *plan, const AppendTok *toks,
                                 int tok_off, int rows, const ProjDims &pd, uint16_t *kpool,

@@ -41,7 +41,7 @@ constexpr int kProjMaxRows = 64;
 // columns, in MFMA-fragment blocks: element (n, k) at ((n/16 * K/32 + k/32)
 // * 16 + n%16) * 32 + k%32, so the B fragment of one (16-feature, 32-k) step
 // is 1 KB of contiguous memory.
-__global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int N, uint16_t *__restrict__ out) {
+__global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int KP, int N, uint16_t *__restrict__ out) {
     __shared__ uint16_t tile[32][33];
     const int n0 = blockIdx.x * 32, k0 = blockIdx.y * 32;
     const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
@@ -60,10 +60,10 @@ __global__ void pack_proj_kernel(PackSrc src, int w_bf16, int K, int N, uint16_t
         tile[r][tx] = v;
     }
     __syncthreads();
-    const int KS = K / 32;
+    const int KS = KP / 32;  // (rows K .. KP - 1: zero weights)
     for (int r = ty; r < 32; r += 8) {
         const int n = n0 + r, k = k0 + tx;
-        if (n < N && k < K)
+        if (n < N && k < KP)
             out[(((int64_t)(n >> 4) * KS + (k >> 5)) * 16 + (n & 15)) * 32 + (k & 31)] = tile[tx][r];
     }
 }
@@ -109,10 +109,11 @@ __device__ __forceinline__ void proj_part(const ProjDims &pd, int n, int &part, 
     nn = n;
     hw = tw = 0;
     if constexpr (MODEL == kProjGQA) {
-        const int NQ = pd.H * pd.D, NK = pd.KVH * pd.D;
+        const int NQ = pd.H * pd.DW, NK = pd.KVH * pd.DW;
         part = n < NQ ? 0 : (n < NQ + NK ? 1 : 2);
         nn = n - (part == 0 ? 0 : (part == 1 ? NQ : NQ + NK));
-        hw = tw = part < 2 ? pd.D : 0;
+        hw = part < 2 ? pd.DW : 0;  // (features past D: zero weights, no rotation)
+        tw = part < 2 ? pd.D : 0;
     } else if constexpr (MODEL == kProjMLA) {
         const int NQC = pd.H * pd.D, NQR = pd.H * pd.DRP;
         part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + pd.DCP ? 2 : 3));
@@ -251,7 +252,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = m * 16 + grp * 4 + i;
-            if (r >= rows) continue;
+            if (r >= rows || n >= pd.D) continue;  // (features past D: packed padding)
             const int64_t off = (int64_t)r * pd.D + n;
             float v = y[i];
             if (q_out2)
@@ -265,7 +266,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
     } else {
         const int part = o.part, nn = o.nn, hw = o.hw;
         const int H = pd.H, KVH = pd.KVH;
-        const int hdim = (MODEL == kProjGQA) ? pd.D : (part == 1 ? pd.DRP : pd.D);
+        const int hdim = (MODEL == kProjGQA) ? pd.DW : (part == 1 ? pd.DRP : pd.D);
         const int head = nn / hdim, d = nn - head * hdim;
         const int dr = hw ? nn % hw : 0;
 #pragma unroll
@@ -285,7 +286,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
             if (to_q) {
                 // (q_r heads are DRP features wide, of which DR are stored)
                 void *dst = (MODEL == kProjMLA && part == 1) ? q_out2 : q_out;
-                const int qw = (MODEL == kProjMLA && part == 1) ? pd.DR : hdim;
+                const int qw = (MODEL == kProjMLA && part == 1) ? pd.DR : pd.D;
                 if (d >= qw) continue;
                 const int64_t off = ((int64_t)r * H + head) * qw + d;
                 if (q_bf16)
@@ -295,6 +296,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
                 continue;
             }
             if constexpr (MODEL == kProjGQA) {
+                if (d >= pd.D) continue;  // (packed padding features)
                 const int DS = pd.DS;  // the pool's dims per head (DS - D padding dims: zeroed apart)
                 if (part == 1)
                     kpool[((int64_t)o.page[i] * KVH + head) * P * DS + k_page_off(o.slot[i], d, DS)] = bf16_rne(v);
@@ -641,7 +643,8 @@ hipError_t launch_proj_pad_zero(hipStream_t s, int model, const PlanArg *plan, c
 hipError_t launch_pack_proj(hipStream_t s, const PackSrc &src, int w_bf16, int K, uint16_t *out) {
     int N = 0;
     for (int i = 0; i < 4; i++) N += src.nh[i] * src.pw[i];
-    pack_proj_kernel<<<dim3((N + 31) / 32, (K + 31) / 32), 256, 0, s>>>(src, w_bf16, K, N, out);
+    const int KP = (K + 31) / 32 * 32;
+    pack_proj_kernel<<<dim3((N + 31) / 32, KP / 32), 256, 0, s>>>(src, w_bf16, K, KP, N, out);
     return hipGetLastError();
 }
 

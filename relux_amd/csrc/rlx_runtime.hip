@@ -1077,10 +1077,11 @@ int32_t rlx_pack_qkv(const void *w_q, const void *w_k, const void *w_v, int32_t 
     if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
     if (d_model <= 0 || num_heads <= 0 || kv_heads <= 0 || head_dim <= 0)
         return fail(RLX_ERR_INVALID, "d_model, heads and head_dim must be > 0");
+    const int pw = gqa_pack_width(num_heads, kv_heads, head_dim);
     const PackSrc src{{w_q, w_k, w_v, w_q},
                       {num_heads, kv_heads, kv_heads, 0},
                       {head_dim, head_dim, head_dim, 0},
-                      {head_dim, head_dim, head_dim, 0}};
+                      {pw, pw, pw, 0}};
     HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
     return RLX_OK;
 }
@@ -1089,10 +1090,8 @@ int32_t rlx_pack_out(const void *w, int32_t w_dtype, int32_t k_in, int32_t n_out
     if (!w || !out) return fail(RLX_ERR_INVALID, "null weight pointer");
     if (w_dtype != RLX_F32 && w_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "w_dtype");
     if (k_in <= 0 || n_out <= 0) return fail(RLX_ERR_INVALID, "k_in and n_out must be > 0");
-    if (k_in % 32 != 0 || n_out % 16 != 0)
-        return fail(RLX_ERR_UNSUPPORTED, "rlx_pack_out: k_in %% 32 and n_out %% 16 must be 0 (k_in=%d n_out=%d)",
-                    k_in, n_out);
-    const PackSrc src{{w, w, w, w}, {1, 0, 0, 0}, {n_out, 0, 0, 0}, {n_out, 0, 0, 0}};
+    // (n_out packed as a multiple of 16 features, k_in as one of 32 rows: zeros)
+    const PackSrc src{{w, w, w, w}, {1, 0, 0, 0}, {n_out, 0, 0, 0}, {(n_out + 15) / 16 * 16, 0, 0, 0}};
     HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, k_in, (uint16_t *)out));
     return RLX_OK;
 }
@@ -1107,16 +1106,26 @@ int32_t rlx_out_project(void *h, int32_t rows, const void *x, int32_t x_dtype, i
     if (!x || !w_packed || !out) return fail(RLX_ERR_INVALID, "rlx_out_project: null pointer");
     if ((x_dtype != RLX_F32 && x_dtype != RLX_BF16) || (out_dtype != RLX_F32 && out_dtype != RLX_BF16))
         return fail(RLX_ERR_INVALID, "rlx_out_project: dtype");
-    if (k_in % 32 != 0 || n_out % 16 != 0)
-        return fail(RLX_ERR_UNSUPPORTED, "rlx_out_project: k_in %% 32 and n_out %% 16 must be 0");
     const size_t xb = x_dtype == RLX_BF16 ? 2 : 4, ob = out_dtype == RLX_BF16 ? 2 : 4;
     int32_t rc;
+    // x rows of a width that is not a multiple of 32: copied to rows of the
+    // next multiple with zeros (the packed weights hold zero rows there).
+    const int kp = (k_in + 31) / 32 * 32;
+    if (kp != k_in) {
+        const size_t sz[1] = {(size_t)rows * kp * xb};
+        char *pad[1];
+        if ((rc = adapter_regions(c, sz, 1, pad))) return rc;
+        HIP_TRY(launch_repack_rows(c->stream, x, k_in, pad[0], kp, rows, (int)xb));
+        x = pad[0];
+        k_in = kp;
+    }
     for (int r0 = 0; r0 < rows; r0 += kProjRows) {
         const int n = std::min(kProjRows, rows - r0);
         hipEvent_t e0, e1;
         if ((rc = timing_events(c, &e0, &e1, RLX_TIME_PROJECT))) return rc;
         ProjDims pd{};
         pd.D = n_out;
+        pd.DW = (n_out + 15) / 16 * 16;
         HIP_TRY(launch_proj(c->stream, kProjModelOut, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, n,
                             (const char *)x + (size_t)r0 * k_in * xb, x_dtype == RLX_BF16, k_in,
                             (const uint16_t *)w_packed, pd, nullptr, nullptr,
@@ -1159,8 +1168,7 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
     if (x_dtype != RLX_F32 && x_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "x_dtype");
     if (q_dtype != RLX_F32 && q_dtype != RLX_BF16) return fail(RLX_ERR_INVALID, "q_dtype");
     if (rope_mode < RLX_ROPE_OFFSET || rope_mode > RLX_ROPE_NONE) return fail(RLX_ERR_INVALID, "rope_mode");
-    if (d_model <= 0 || d_model % 32 != 0)
-        return fail(RLX_ERR_UNSUPPORTED, "d_model=%d must be a positive multiple of 32", d_model);
+    if (d_model <= 0) return fail(RLX_ERR_INVALID, "d_model=%d must be positive", d_model);
     if (rope_mode != RLX_ROPE_NONE && (!rope_cos || !rope_sin || rope_rows <= 0))
         return fail(RLX_ERR_INVALID, "RoPE tables required");
     LayerState &ls = c->L[layer];
@@ -1183,6 +1191,19 @@ int32_t project_append(Cache *c, int model, int32_t layer, int32_t n_seqs, const
     if (total == 0) return RLX_OK;
     if (!x || !w_packed || !q_out || (model == kProjModelMLA && !q_out2))
         return fail(RLX_ERR_INVALID, "null x / weights / q_out");
+    // x rows of a width that is not a multiple of 32: copied to rows of the
+    // next multiple with zeros (the packed weights hold zero rows there),
+    // before anything is appended.
+    const int kp = (d_model + 31) / 32 * 32;
+    if (kp != d_model) {
+        const int xe = x_dtype == RLX_BF16 ? 2 : 4;
+        const size_t sz[1] = {(size_t)total * kp * xe};
+        char *pad[1];
+        if ((rc = adapter_regions(c, sz, 1, pad))) return rc;
+        HIP_TRY(launch_repack_rows(c->stream, x, d_model, pad[0], kp, total, xe));
+        x = pad[0];
+        d_model = kp;
+    }
     std::vector<AppendTok> toks;
     if ((rc = plan_append(c, layer, n_seqs, seq_ids, n_tok, toks))) return rc;
     std::vector<Patch> patches = take_pending(c);
@@ -1239,22 +1260,18 @@ int32_t rlx_gqa_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kGQA) return fail(RLX_ERR_INVALID, "rlx_gqa_project_append on an MLA cache");
-    if (c->hdu != c->hdi)
-        return fail(RLX_ERR_UNSUPPORTED,
-                    "rlx_gqa_project_append: head_dim %d is not a multiple of 8", c->hdu);
+    if (c->hdu % 2 != 0)
+        return fail(RLX_ERR_UNSUPPORTED, "rlx_gqa_project_append: RoPE needs an even head_dim (%d)", c->hdu);
     if (num_heads <= 0 || num_heads % c->kvh != 0)
         return fail(RLX_ERR_INVALID, "numHeads=%d not divisible by numKVHeads=%d", num_heads, c->kvh);
     // The packed features come in 16-feature tiles, each within one of the
-    // q / k / v parts.
-    if ((num_heads * c->hdi) % 16 != 0 || (c->kvh * c->hdi) % 16 != 0)
-        return fail(RLX_ERR_UNSUPPORTED,
-                    "rlx_gqa_project_append: heads x head_dim must be multiples of 16 (%d x %d, %d x %d)",
-                    num_heads, c->hdi, c->kvh, c->hdi);
+    // q / k / v parts: heads are packed DW features wide (rlx_pack_qkv).
     ProjDims pd{};
     pd.H = num_heads;
     pd.KVH = c->kvh;
-    pd.D = c->hdi;
+    pd.D = c->hdu;
     pd.DS = c->hd;
+    pd.DW = gqa_pack_width(num_heads, c->kvh, c->hdu);
     return project_append(c, kProjModelGQA, layer, n_seqs, seq_ids, n_tok, x, x_dtype, d_model,
                           w_packed, pd, rope_cos, rope_sin, rope_rows, rope_mode, q_out, nullptr,
                           q_dtype);

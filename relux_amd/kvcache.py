@@ -404,12 +404,22 @@ class KVCache(_PagedCache):
         return q
 
 
+def gqa_pack_width(num_heads, kv_heads, head_dim):
+    """Packed features per head of pack_qkv: head_dim when H*D and KVH*D are
+    multiples of 16, else head_dim rounded up to 16 (zero weights past it)."""
+    if (num_heads * head_dim) % 16 == 0 and (kv_heads * head_dim) % 16 == 0:
+        return head_dim
+    return -(-head_dim // 16) * 16
+
+
 def pack_qkv(w_q, w_k, w_v, num_heads, kv_heads, head_dim):
     """W_q [d_model][H*D], W_k/W_v [d_model][KVH*D] (bf16 or f32, device) ->
-    packed bf16 weights for KVCache.ProjectAppend: N = (H + 2 KVH) * D
-    features in 16-feature x 32-k fragments (rlx_pack_qkv)."""
+    packed bf16 weights for KVCache.ProjectAppend: N = (H + 2 KVH) * W
+    features (W = gqa_pack_width) in 16-feature x 32-k fragments
+    (rlx_pack_qkv)."""
     d_model = w_q.shape[0]
-    out = torch.empty(((num_heads + 2 * kv_heads) * head_dim, d_model), dtype=torch.bfloat16,
+    W = gqa_pack_width(num_heads, kv_heads, head_dim)
+    out = torch.empty(((num_heads + 2 * kv_heads) * W, -(-d_model // 32) * 32), dtype=torch.bfloat16,
                       device=w_q.device)
     check(_lib.load().rlx_pack_qkv(_dev(w_q, "w_q"), _dev(w_k, "w_k"), _dev(w_v, "w_v"),
                                    _dtype_code(w_q), d_model, num_heads, kv_heads, head_dim,
@@ -422,7 +432,7 @@ def pack_out(w, k_in=None, n_out=None):
     packed bf16 weights for OutProject (rlx_pack_out)."""
     k_in = k_in or w.shape[0]
     n_out = n_out or w.shape[1]
-    out = torch.empty((n_out, k_in), dtype=torch.bfloat16, device=w.device)
+    out = torch.empty((-(-n_out // 16) * 16, -(-k_in // 32) * 32), dtype=torch.bfloat16, device=w.device)
     check(_lib.load().rlx_pack_out(_dev(w, "w"), _dtype_code(w), k_in, n_out, _dev(out, "out")))
     return out
 
@@ -597,7 +607,7 @@ def pack_mla_proj(w_q, w_qr, w_dkv, w_kr, num_heads, head_dim):
     d_c, d_r = w_dkv.shape[1], w_kr.shape[1]
     drp, dcp = -(-d_r // 16) * 16, -(-d_c // 16) * 16
     n = num_heads * (head_dim + drp) + dcp + drp
-    out = torch.empty((n, d_model), dtype=torch.bfloat16, device=w_q.device)
+    out = torch.empty((n, -(-d_model // 32) * 32), dtype=torch.bfloat16, device=w_q.device)
     check(_lib.load().rlx_pack_mla_proj(_dev(w_q, "w_q"), _dev(w_qr, "w_qr"), _dev(w_dkv, "w_dkv"),
                                         _dev(w_kr, "w_kr"), _dtype_code(w_q), d_model, num_heads,
                                         head_dim, d_c, d_r, _dev(out, "out")))

@@ -58,6 +58,13 @@ def _oracle_qkv(x, wq, wk, wv, H, KVH, D, tables, max_seq, positions):
     # decode-size and chunked kernels
     (512, 8, 2, 80, [7, 30], [1, 1], torch.bfloat16, "offset"),
     (256, 4, 2, 80, [0, 12], [40, 30], torch.float32, "offset"),
+    # the reference tests' tiny layers (heads packed 16 features wide, x
+    # rows padded to 32): mha_test.go:86 (dModel 4, 2 heads over 1 kv head)
+    # and NewMHA(8, 4, 2), then H x head_dim 36 and d_model 40
+    (4, 2, 1, 2, [0, 3], [4, 2], torch.float32, "offset"),
+    (8, 4, 2, 2, [5], [3], torch.float32, "ref"),
+    (96, 3, 1, 12, [0, 20], [5, 1], torch.bfloat16, "offset"),
+    (40, 2, 2, 20, [7, 0], [1, 33], torch.float32, "offset"),
 ])
 def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dtype, mode):
     from relux_amd import KVCache, pack_qkv, rope_tables
@@ -70,11 +77,16 @@ def test_project_append_matches_oracle(gpu, d_model, H, KVH, D, lens, ntok, x_dt
     wk = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
     wv = oracle.bf16_from_f32(rng.normal(0, 0.02, (d_model, KVH * D)).astype(np.float32))
     wp = pack_qkv(_bf16_tensor(wq, gpu), _bf16_tensor(wk, gpu), _bf16_tensor(wv, gpu), H, KVH, D)
-    # packed layout: (16-feature x 32-k) fragments of W^T, fragment-major
-    wt = np.concatenate([wq, wk, wv], axis=1).T  # [N][d_model]
+    # packed layout: (16-feature x 32-k) fragments of W^T, fragment-major;
+    # heads W features wide and k rows padded to 32, zeros in the padding
+    from relux_amd import gqa_pack_width
+    W, Kp = gqa_pack_width(H, KVH, D), -(-d_model // 32) * 32
+    heads = lambda w, nh: np.pad(w.reshape(d_model, nh, D), ((0, 0), (0, 0), (0, W - D))).reshape(d_model, nh * W)
+    wt = np.pad(np.concatenate([heads(wq, H), heads(wk, KVH), heads(wv, KVH)], axis=1),
+                ((0, Kp - d_model), (0, 0))).T  # [N][Kp]
     N = wt.shape[0]
-    blk = wt.reshape(N // 16, 16, d_model // 32, 32).transpose(0, 2, 1, 3).reshape(N, d_model)
-    np.testing.assert_array_equal(wp.view(torch.int16).cpu().numpy().view(np.uint16).reshape(N, d_model), blk)
+    blk = wt.reshape(N // 16, 16, Kp // 32, 32).transpose(0, 2, 1, 3).reshape(N, Kp)
+    np.testing.assert_array_equal(wp.view(torch.int16).cpu().numpy().view(np.uint16).reshape(N, Kp), blk)
     rope = rope_tables(D, 10000.0, max_seq, gpu)
     tables = oracle.rope_tables(D, 10000.0, max_seq)
     # existing context through the plain append
@@ -168,6 +180,10 @@ def test_rope_position_overflow_panics(gpu):
     (40, 1024, 512, torch.bfloat16, torch.bfloat16, False),  # 3 row tiles
     (20, 2048, 512, torch.bfloat16, torch.float32, True),    # decode-size kernel, two row tiles
     (8, 512, 4608, torch.bfloat16, torch.bfloat16, True),    # 288 tiles: two per work-group
+    # the reference tests' tiny layers: W_O of dModel 4 (k_in 4, n_out 4), and
+    # k_in / n_out that are not multiples of 32 / 16 (zero-padded packing)
+    (5, 4, 4, torch.float32, torch.float32, True),
+    (33, 40, 24, torch.bfloat16, torch.float32, True),
 ])
 def test_out_project_matches_oracle(gpu, rows, k_in, n_out, x_dtype, out_dtype, resid):
     """out = x . W_O (+ residual): mha.go:356-360 matmulBatched3D (bf16
