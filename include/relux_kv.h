@@ -152,15 +152,19 @@ int32_t rlx_cache_set_stream(void *cache, void *stream);
  * plans do not fit the kernel arguments stage them through 8 upload slots
  * (pinned host + device); a call that needs more than either holds grows it
  * on the spot (stream sync, hipFree, hipMalloc inside that call).  This
- * grows the workspace to at least workspace_bytes and every staging slot
- * to at least staging_bytes now, so that a serving loop pays for it once at
- * set-up; a size the current capacity covers leaves it unchanged.  No
- * reference counterpart: the reference's scratch is Go heap memory. */
-int32_t rlx_cache_reserve(void *cache, uint64_t workspace_bytes, uint64_t staging_bytes);
+ * grows the workspace to at least workspace_bytes, every staging slot to
+ * at least staging_bytes and the adapter buffer (rows of a head_dim, d_model
+ * or k_in that the kernels take padded) to at least adapter_bytes now, so
+ * that a serving loop pays for it once at set-up; a size the current
+ * capacity covers leaves it unchanged.  No reference counterpart: the
+ * reference's scratch is Go heap memory. */
+int32_t rlx_cache_reserve(void *cache, uint64_t workspace_bytes, uint64_t staging_bytes,
+                          uint64_t adapter_bytes);
 /* out[0] workspace capacity, out[1] the largest workspace any call on the
  * handle has asked for, out[2] the smallest staging slot's capacity, out[3]
- * the largest plan any call has staged (bytes).  A trial run of the largest
- * calls followed by rlx_cache_reserve(out[1], out[3]) on a fresh handle
+ * the largest plan any call has staged, out[4] adapter capacity, out[5] the
+ * largest adapter request (bytes).  A trial run of the largest calls
+ * followed by rlx_cache_reserve(out[1], out[3], out[5]) on a fresh handle
  * keeps every later call of those sizes from allocating. */
 int32_t rlx_cache_memory(void *cache, uint64_t *out);
 

@@ -75,7 +75,7 @@ SIGNATURES = {
     "rlx_cache_reset": [_vp],
     "rlx_cache_sync": [_vp],
     "rlx_cache_set_stream": [_vp, _vp],
-    "rlx_cache_reserve": [_vp, ctypes.c_uint64, ctypes.c_uint64],
+    "rlx_cache_reserve": [_vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64],
     "rlx_cache_memory": [_vp, ctypes.POINTER(ctypes.c_uint64)],
     "rlx_kv_append": [_vp, _i32, _i32, _pi32, _pi32, _vp, _vp, _i32, _i32],
     "rlx_pack_qkv": [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp],

@@ -132,6 +132,7 @@ struct Cache {
     size_t ws_peak = 0;     // largest workspace a call asked for
     void *ad = nullptr;     // adapter rows of head dims that are not multiples of 8
     size_t ad_cap = 0;
+    size_t ad_peak = 0;     // largest adapter request
     size_t stage_peak = 0;  // largest plan a call staged
     SpillTier spill;
     // Attention-kernel timing: event pairs, reused across reports.
@@ -297,6 +298,7 @@ int32_t adapter_regions(Cache *c, const size_t *bytes, int n, char **out) {
         off[i] = total;
         total += (bytes[i] + 255) & ~(size_t)255;
     }
+    c->ad_peak = std::max(c->ad_peak, total);
     if (total > c->ad_cap) {
         const size_t cap = (std::max(total, c->ad_cap * 2) + 65535) & ~(size_t)65535;
         HIP_TRY(hipStreamSynchronize(c->stream));
@@ -932,7 +934,7 @@ int32_t rlx_cache_set_stream(void *h, void *stream) {
     return RLX_OK;
 }
 
-int32_t rlx_cache_reserve(void *h, uint64_t ws_bytes, uint64_t stage_bytes) {
+int32_t rlx_cache_reserve(void *h, uint64_t ws_bytes, uint64_t stage_bytes, uint64_t ad_bytes) {
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (ws_bytes > c->ws_cap) {
@@ -943,6 +945,15 @@ int32_t rlx_cache_reserve(void *h, uint64_t ws_bytes, uint64_t stage_bytes) {
         c->ws_cap = 0;
         HIP_TRY(hipMalloc(&c->ws, cap));
         c->ws_cap = cap;
+    }
+    if (ad_bytes > c->ad_cap) {
+        const size_t cap = ((size_t)ad_bytes + 65535) & ~(size_t)65535;
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        if (c->ad) HIP_TRY(hipFree(c->ad));
+        c->ad = nullptr;
+        c->ad_cap = 0;
+        HIP_TRY(hipMalloc(&c->ad, cap));
+        c->ad_cap = cap;
     }
     for (Slot &s : c->slots) {
         if (stage_bytes <= s.cap) continue;
@@ -971,6 +982,8 @@ int32_t rlx_cache_memory(void *h, uint64_t *out) {
     out[1] = c->ws_peak;
     out[2] = smin;
     out[3] = c->stage_peak;
+    out[4] = c->ad_cap;
+    out[5] = c->ad_peak;
     return RLX_OK;
 }
 

@@ -76,17 +76,21 @@ class _PagedCache:
     def Sync(self):
         check(self._lib.rlx_cache_sync(self._h))
 
-    def Reserve(self, workspace_bytes=0, staging_bytes=0):
-        """Grow the device workspace and the plan staging slots now, so that
-        later calls up to these sizes allocate nothing (rlx_cache_reserve)."""
-        check(self._lib.rlx_cache_reserve(self._h, int(workspace_bytes), int(staging_bytes)))
+    def Reserve(self, workspace_bytes=0, staging_bytes=0, adapter_bytes=0):
+        """Grow the device workspace, the plan staging slots and the adapter
+        buffer now, so that later calls up to these sizes allocate nothing
+        (rlx_cache_reserve)."""
+        check(self._lib.rlx_cache_reserve(self._h, int(workspace_bytes), int(staging_bytes),
+                                          int(adapter_bytes)))
 
     def MemoryStats(self):
-        """Workspace and staging capacities and the largest requests so far:
-        dict(workspace, workspace_peak, staging, staging_peak) in bytes."""
-        out = (ctypes.c_uint64 * 4)()
+        """Workspace, staging and adapter capacities and the largest requests
+        so far: dict(workspace, workspace_peak, staging, staging_peak,
+        adapter, adapter_peak) in bytes."""
+        out = (ctypes.c_uint64 * 6)()
         check(self._lib.rlx_cache_memory(self._h, out))
-        return dict(workspace=out[0], workspace_peak=out[1], staging=out[2], staging_peak=out[3])
+        return dict(workspace=out[0], workspace_peak=out[1], staging=out[2], staging_peak=out[3],
+                    adapter=out[4], adapter_peak=out[5])
 
     def Timing(self, enable=True, kernels="attend"):
         """Bracket every later attention kernel ("attend"), projection

@@ -463,11 +463,12 @@ def test_mla_spill_restore_roundtrip(gpu, tmp_path):
 
 def test_reserve_keeps_calls_from_allocating(gpu):
     """rlx_cache_reserve / rlx_cache_memory: a trial handle runs an MLA
-    prefill (expanded latents in the workspace) and an 80-sequence GQA
-    decode (its plan staged, past what the kernel arguments hold); a second
-    handle reserves the peaks the first reported, and the same calls then
-    grow neither its workspace nor its staging slots, with outputs
-    bit-identical to the trial handle's."""
+    prefill (expanded latents in the workspace), an 80-sequence GQA decode
+    (its plan staged, past what the kernel arguments hold) and a head_dim-12
+    decode (rows padded through the adapter buffer); a second handle
+    reserves the peaks the first reported, and the same calls then grow
+    neither its workspace, its staging slots nor its adapter buffer, with
+    outputs bit-identical to the trial handle's."""
     rng = np.random.default_rng(404)
     H, D, lens = 16, 128, [700, 300]
     cc = rng.standard_normal((sum(lens), 512), dtype=np.float32)
@@ -482,33 +483,44 @@ def test_reserve_keeps_calls_from_allocating(gpu):
     gk = t(rng.standard_normal((sum(glens), KVH, D), dtype=np.float32))
     gv = t(rng.standard_normal((sum(glens), KVH, D), dtype=np.float32))
     gq = t(rng.standard_normal((B, 32, D), dtype=np.float32))
+    D12, B12 = 12, 40
+    olens = rng.integers(5, 60, B12).tolist()
+    ok = t(rng.standard_normal((sum(olens), 2, D12), dtype=np.float32))
+    oq = t(rng.standard_normal((B12, 4, D12), dtype=np.float32))
 
     def run(reserve=None):
         m = _mla(gpu, num_layers=1, max_len=1024, page_tokens=64, max_seqs=2)
         g = _kv(gpu, num_layers=1, max_len=256, num_kv_heads=KVH, head_dim=D, page_tokens=16,
                 max_seqs=B)
+        o = _kv(gpu, num_layers=1, max_len=64, num_kv_heads=2, head_dim=D12, max_seqs=B12)
+        hs = (m, g, o)
         if reserve:
-            m.Reserve(*reserve[0])
-            g.Reserve(*reserve[1])
-        before = (m.MemoryStats(), g.MemoryStats())
+            for h, r in zip(hs, reserve):
+                h.Reserve(*r)
+        before = [h.MemoryStats() for h in hs]
         m.Append(0, t(cc), t(kr), seq_ids=[0, 1], n_tok=lens)
         mo = m.Attend(0, qn, qr, w_uk, w_uv, H, D, seq_ids=[0, 1], n_q=lens)
         g.Append(0, gk, gv, seq_ids=list(range(B)), n_tok=glens, layout="SHD")
         go = g.Attend(0, gq, 32, seq_ids=list(range(B)))
-        after = (m.MemoryStats(), g.MemoryStats())
-        out = (mo.cpu(), go.cpu())
-        m.close()
-        g.close()
+        o.Append(0, ok, ok, seq_ids=list(range(B12)), n_tok=olens, layout="SHD")
+        oo = o.Attend(0, oq, 4, seq_ids=list(range(B12)))
+        after = [h.MemoryStats() for h in hs]
+        out = (mo.cpu(), go.cpu(), oo.cpu())
+        for h in hs:
+            h.close()
         return before, after, out
 
-    _, (ms, gs), ref = run()
+    _, stats, ref = run()
+    ms, gs, os_ = stats
     assert ms["workspace_peak"] > 0 and gs["workspace_peak"] > 0 and gs["staging_peak"] > 0
+    assert os_["adapter_peak"] > 0 and ms["adapter_peak"] == 0 and gs["adapter_peak"] == 0
     assert ms["workspace"] >= ms["workspace_peak"]  # (staging: slots unused so far stay empty)
-    want = ((ms["workspace_peak"], ms["staging_peak"]), (gs["workspace_peak"], gs["staging_peak"]))
+    want = [(x["workspace_peak"], x["staging_peak"], x["adapter_peak"]) for x in stats]
     before, after, got = run(want)
-    for b, a, (wsb, stb) in zip(before, after, want):
-        assert b["workspace"] >= wsb and b["staging"] >= stb
-        assert a["workspace"] == b["workspace"] and a["staging"] == b["staging"], (b, a)
+    for b, a, (wsb, stb, adb) in zip(before, after, want):
+        assert b["workspace"] >= wsb and b["staging"] >= stb and b["adapter"] >= adb
+        for k in ("workspace", "staging", "adapter"):
+            assert a[k] == b[k], (k, b, a)
     for x, y in zip(got, ref):
         assert torch.equal(x, y)
 
