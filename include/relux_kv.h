@@ -220,7 +220,9 @@ int32_t rlx_gqa_project_append(void *cache, int32_t layer, int32_t n_seqs, const
  * out (N = H*(D + d_r') + d_c' + d_r' features, d_r' and d_c' = d_r and
  * d_c rounded up to 16 with zero columns, the same fragment layout as
  * rlx_pack_qkv) for rlx_mla_project_append on a cache of these d_c / d_r.
- * head_dim must be a multiple of 16.  Null stream.  No reference
+ * q_c heads are packed head_dim features wide, or rounded up to 16 (zero
+ * columns) when H*head_dim is not a multiple of 16; d_model padded as for
+ * rlx_pack_qkv.  Null stream.  No reference
  * counterpart: a one-time weight preparation. */
 int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, const void *w_kr,
                           int32_t w_dtype, int32_t d_model, int32_t num_heads, int32_t head_dim,

@@ -594,6 +594,7 @@ struct PackSrc {
 hipError_t launch_pack_proj(hipStream_t s, const PackSrc &src, int w_bf16, int K, uint16_t *out);
 // Shapes of a projection: GQA (H, KVH, D = the caller's head dim, DS = the
 // pool's, DW = the packed features per head); MLA (H, D = q_c dims per head,
+// DW = packed q_c features per head,
 // DR / DC = d_r / d_c and DRP / DCP = the same rounded up to 16, the packed
 // widths of the rope heads and of the latent); kProjOut (D = output
 // features, DW = the same rounded up to 16, the packed ones).
@@ -606,9 +607,14 @@ struct ProjDims {
 __host__ __device__ inline int gqa_pack_width(int H, int KVH, int D) {
     return ((H * D) % 16 == 0 && (KVH * D) % 16 == 0) ? D : (D + 15) / 16 * 16;
 }
+// Packed q_c features per MLA head: the head dim when the q_c part is whole
+// 16-feature tiles (H D a multiple of 16), else rounded up to 16.
+__host__ __device__ inline int mla_pack_width(int H, int D) {
+    return (H * D) % 16 == 0 ? D : (D + 15) / 16 * 16;
+}
 __host__ __device__ inline int proj_features(int model, const ProjDims &pd) {
     return model == kProjModelGQA ? (pd.H + 2 * pd.KVH) * pd.DW
-         : model == kProjModelMLA ? pd.H * (pd.D + pd.DRP) + pd.DCP + pd.DRP
+         : model == kProjModelMLA ? pd.H * (pd.DW + pd.DRP) + pd.DCP + pd.DRP
                                   : pd.DW;
 }
 hipError_t launch_proj_pad_zero(hipStream_t s, int model, const PlanArg *plan, const AppendTok *toks,

@@ -115,7 +115,7 @@ __device__ __forceinline__ void proj_part(const ProjDims &pd, int n, int &part, 
         hw = part < 2 ? pd.DW : 0;  // (features past D: zero weights, no rotation)
         tw = part < 2 ? pd.D : 0;
     } else if constexpr (MODEL == kProjMLA) {
-        const int NQC = pd.H * pd.D, NQR = pd.H * pd.DRP;
+        const int NQC = pd.H * pd.DW, NQR = pd.H * pd.DRP;
         part = n < NQC ? 0 : (n < NQC + NQR ? 1 : (n < NQC + NQR + pd.DCP ? 2 : 3));
         nn = n - (part == 0 ? 0 : (part == 1 ? NQC : (part == 2 ? NQC + NQR : NQC + NQR + pd.DCP)));
         hw = (part == 1 || part == 3) ? pd.DRP : 0;
@@ -266,7 +266,7 @@ __device__ __forceinline__ void proj_store(const ProjPlace &o, fl4 y, int m, int
     } else {
         const int part = o.part, nn = o.nn, hw = o.hw;
         const int H = pd.H, KVH = pd.KVH;
-        const int hdim = (MODEL == kProjGQA) ? pd.DW : (part == 1 ? pd.DRP : pd.D);
+        const int hdim = (MODEL == kProjGQA) ? pd.DW : (part == 1 ? pd.DRP : pd.DW);
         const int head = nn / hdim, d = nn - head * hdim;
         const int dr = hw ? nn % hw : 0;
 #pragma unroll

@@ -1160,7 +1160,7 @@ int32_t rlx_pack_mla_proj(const void *w_q, const void *w_qr, const void *w_dkv, 
     const PackSrc src{{w_q, w_qr, w_dkv, w_kr},
                       {num_heads, num_heads, 1, 1},
                       {head_dim, d_r, d_c, d_r},
-                      {head_dim, drp, dcp, drp}};
+                      {mla_pack_width(num_heads, head_dim), drp, dcp, drp}};
     HIP_TRY(launch_pack_proj(nullptr, src, w_dtype == RLX_BF16, d_model, (uint16_t *)out));
     return RLX_OK;
 }
@@ -1299,12 +1299,12 @@ int32_t rlx_mla_project_append(void *h, int32_t layer, int32_t n_seqs, const int
     if (!h) return fail(RLX_ERR_INVALID, "null cache");
     Cache *c = as_cache(h);
     if (c->kind != kMLA) return fail(RLX_ERR_INVALID, "rlx_mla_project_append on a GQA cache");
-    if (num_heads <= 0 || head_dim <= 0 || head_dim % 16 != 0)
-        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim a multiple of 16)",
-                    num_heads, head_dim);
+    if (num_heads <= 0 || head_dim <= 0 || head_dim > 256)
+        return fail(RLX_ERR_UNSUPPORTED, "num_heads=%d head_dim=%d (head_dim 1 to 256)", num_heads, head_dim);
     ProjDims pd{};
     pd.H = num_heads;
     pd.D = head_dim;
+    pd.DW = mla_pack_width(num_heads, head_dim);
     pd.DR = c->dr;
     pd.DRP = (c->dr + 15) & ~15;
     pd.DC = c->dc;

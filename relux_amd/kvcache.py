@@ -606,11 +606,13 @@ def pack_mla_proj(w_q, w_qr, w_dkv, w_kr, num_heads, head_dim):
     """W_Q [d_model][H*D], W_QR [d_model][H*d_r], W_DKV [d_model][d_c], W_KR
     [d_model][d_r] (bf16 or f32, device) -> packed bf16 weights for
     MLACache.ProjectAppend (rlx_pack_mla_proj); d_r and d_c features are
-    padded to multiples of 16 with zero columns."""
+    padded to multiples of 16 with zero columns, and the q_c heads too when
+    H*D is not one."""
     d_model = w_q.shape[0]
     d_c, d_r = w_dkv.shape[1], w_kr.shape[1]
     drp, dcp = -(-d_r // 16) * 16, -(-d_c // 16) * 16
-    n = num_heads * (head_dim + drp) + dcp + drp
+    qw = head_dim if (num_heads * head_dim) % 16 == 0 else -(-head_dim // 16) * 16
+    n = num_heads * (qw + drp) + dcp + drp
     out = torch.empty((n, -(-d_model // 32) * 32), dtype=torch.bfloat16, device=w_q.device)
     check(_lib.load().rlx_pack_mla_proj(_dev(w_q, "w_q"), _dev(w_qr, "w_qr"), _dev(w_dkv, "w_dkv"),
                                         _dev(w_kr, "w_kr"), _dtype_code(w_q), d_model, num_heads,

@@ -267,6 +267,10 @@ def test_cfg1_generate_with_fused_step(gpu):
     (512, 8, 32, [5, 40], [1, 1], "offset", torch.bfloat16, 128, 16),
     (256, 4, 64, [0, 20], [9, 3], "offset", torch.float32, 256, 32),
     (256, 4, 16, [3, 0], [2, 5], "ref", torch.float32, 64, 8),      # config-1-sized MLA layer
+    # mla_test.go's layer (dModel 8, 2 heads, headDim 4, dC 16, dHR 2: q_c
+    # heads packed 16 wide, x rows padded to 32) and H x head_dim 60 at d_model 40
+    (8, 2, 4, [0, 5], [3, 2], "offset", torch.float32, 16, 2),
+    (40, 3, 20, [4, 0], [1, 6], "ref", torch.bfloat16, 80, 10),
 ])
 def test_mla_project_append_matches_oracle(gpu, d_model, H, D, lens, ntok, mode, x_dtype, dC, dR):
     """mla.go:279-314: q_c = x.W_Q, q_r = RoPE(x.W_QR), c = x.W_DKV,
