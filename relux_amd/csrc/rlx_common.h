@@ -526,6 +526,17 @@ __device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff, uint
         : "v"(voff), "s"(sbase), "s"(lds_base)
         : "memory", "m0");
 }
+// The same without the non-temporal hint: the lines stay in L2 for other
+// work-groups that read them soon after (the MLA decode's head groups).
+__device__ __forceinline__ void lds_dma16_keep(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(sbase), "s"(lds_base)
+        : "memory", "m0");
+}
 
 // Work-group barrier for the ring: this wave's LDS accesses complete, then
 // s_barrier.  Unlike __syncthreads() it does not wait for outstanding

@@ -195,7 +195,11 @@ template <int NQT> struct MlaShape {
     static constexpr int CH = kMlaDc / NW;            // latent channels per wave
 };
 
-template <int NQT, bool ARG>
+// KEEP: ring loads without the non-temporal hint, for calls whose head
+// groups re-read the same latent rows (they then meet them in L2: 128 heads
+// at 8k, 66.4 -> 61.3 us); single-group calls keep the hint (config 3:
+// 53.0 against 58.0 us without it).
+template <int NQT, bool ARG, bool KEEP>
 __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void mla_decode_kernel(
     typename PlanSel<ARG>::T plan, const uint16_t *__restrict__ pool,
     const int32_t *__restrict__ table, const AttRow *__restrict__ rows,
@@ -219,7 +223,10 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
     const int grp = lane >> 4;
     const int2 wk = plan_work<ARG>(work, n_rows, blockIdx.x);
     const AttRow R = plan_row<ARG>(rows, wk.x);
-    const int QR = H * R.nq;
+    // This work item's query rows: rows [q0, q0 + qn) of the sequence's
+    // H x nq (query-major: row qi H + h), one head group of a call with more
+    // rows than a work-group holds.
+    const int QR = R.qn;
     const int t_begin = mla_split_bound(R.len, R.nsplit, wk.y);
     const int t_end = mla_split_bound(R.len, R.nsplit, wk.y + 1);
     const int ntiles = (t_end - t_begin + 15) / 16;
@@ -274,14 +281,20 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
 #pragma unroll
             for (int k = 0; k < LB; k++) {
                 if (k == LS && wave >= SH::LOADS % NW) break;
-                lds_dma16(src, loff[k], __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+                if constexpr (KEEP)
+                    lds_dma16_keep(src, loff[k], __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+                else
+                    lds_dma16(src, loff[k], __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
             }
         } else {
 #pragma unroll
             for (int k = 0; k < LB; k++) {
                 if (k == LS && wave >= SH::LOADS % NW) break;
                 const uint32_t off = (uint32_t)(min(lrow[k], lim) * kMlaRow + lcol[k]) * 2;
-                lds_dma16(src, off, __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+                if constexpr (KEEP)
+                    lds_dma16_keep(src, off, __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
+                else
+                    lds_dma16(src, off, __builtin_amdgcn_readfirstlane(dst + (uint32_t)(64 * (NW * k + wave)) * 16));
             }
         }
     };
@@ -321,8 +334,9 @@ __global__ __launch_bounds__(64 * MlaShape<NQT>::NW, MlaShape<NQT>::WGS) void ml
 #pragma unroll
         for (int kk = 0; kk < KB; kk++) qb[nt][kk] = u32x4{0, 0, 0, 0};
         if (qr < QR) {
-            const int qi = qr / H;
-            const int h = qr - qi * H;
+            const int qg = R.q0 + qr;
+            const int qi = qg / H;
+            const int h = qg - qi * H;
             klim[nt] = mla_key_limit(mask_mode, R.len, R.nq, qi);
             const uint16_t *qp = qlat + ((int64_t)(R.qrow + qi) * H + h) * kMlaRow + grp * 8;
 #pragma unroll
@@ -528,6 +542,21 @@ __device__ __forceinline__ int plan_qrow_row(const AttRow *rows, int n_rows, int
     return lo;
 }
 
+// Plan row holding head h of global query row q: the sequence's row (found
+// by its first query row), or -- when the sequence's H x nq query rows were
+// cut into head groups of QRP rows, consecutive plan rows of one sequence --
+// the group that holds row (q - qrow) H + h.
+template <bool ARG>
+__device__ __forceinline__ AttRow mla_group_row(const AttRow *rows, int n_rows, int one_q, int q, int h,
+                                               int H, int QRP) {
+    const int ri = one_q ? q : plan_qrow_row<ARG>(rows, n_rows, q);  // the sequence's last plan row
+    const AttRow R = plan_row<ARG>(rows, ri);
+    const int all = H * R.nq;
+    if (R.qn >= all) return R;
+    const int groups = (all + QRP - 1) / QRP;
+    return plan_row<ARG>(rows, ri - (groups - 1) + ((q - R.qrow) * H + h) / QRP);
+}
+
 // The step after the split loop, for head h and RPB consecutive query rows
 // of the call: merge each query row's split partials into the normalised
 // latent output
@@ -585,9 +614,8 @@ __global__ __launch_bounds__(256) void mla_out_kernel(
         const int q = min(q0 + j, total_q - 1);
         live[j] = q0 + j < total_q;
         // one query per row (decode): query row q is row q
-        const AttRow R = plan_row<ARG>(rows, one_q ? q : plan_qrow_row<ARG>(rows, n_rows, q));
-        const int qi = q - R.qrow;
-        b0[j] = (int64_t)R.part * QRP + qi * H + h;
+        const AttRow R = mla_group_row<ARG>(rows, n_rows, one_q, q, h, H, QRP);
+        b0[j] = (int64_t)R.part * QRP + (q - R.qrow) * H + h - R.q0;
         ns[j] = R.nsplit;
         ob[j] = ((int64_t)q * H + h) * D;
     }
@@ -768,9 +796,8 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
     for (int j = 0; j < RPB; j++) {
         const int q = min(q0 + j, total_q - 1);
         live[j] = q0 + j < total_q;
-        const AttRow R = plan_row<ARG>(rows, one_q ? q : plan_qrow_row<ARG>(rows, n_rows, q));
-        const int qi = q - R.qrow;
-        b0[j] = (int64_t)R.part * QRP + qi * H + h;
+        const AttRow R = mla_group_row<ARG>(rows, n_rows, one_q, q, h, H, QRP);
+        b0[j] = (int64_t)R.part * QRP + (q - R.qrow) * H + h - R.q0;
         ns[j] = R.nsplit;
         ob[j] = ((int64_t)q * H + h) * D;
     }
@@ -926,54 +953,55 @@ __global__ __launch_bounds__(256) void mla_out_mfma_kernel(
 }
 
 template <int NQT, bool ARG>
-static void launch_mla_t(hipStream_t s, typename PlanSel<ARG>::T plan, const uint16_t *pool,
+static void launch_mla_t(hipStream_t s, bool keep, typename PlanSel<ARG>::T plan, const uint16_t *pool,
                          const int32_t *table, const AttRow *rows, int n_rows, const int2 *work,
                          int n_work, const uint16_t *qlat, int H, int P, int mask_mode,
                          uint16_t *part_o, float *part_ml, hipEvent_t ev0, hipEvent_t ev1) {
-    (void)launch_timed(mla_decode_kernel<NQT, ARG>, dim3(n_work), dim3(64 * MlaShape<NQT>::NW), s,
+    (void)launch_timed(keep ? mla_decode_kernel<NQT, ARG, true> : mla_decode_kernel<NQT, ARG, false>,
+                       dim3(n_work), dim3(64 * MlaShape<NQT>::NW), s,
                        ev0, ev1, plan, pool, table, rows, work, n_rows, qlat, H, P, mask_mode,
                        part_o, part_ml);
 }
 
 template <int DMAX, bool ARG>
 static void launch_mla_out_d(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
-                             int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
+                             int n_rows, int total_q, int one_q, const uint16_t *part_o, const float *part_ml,
                              const uint16_t *w_uv, int H, int D, int dc, int QRP, void *out,
                              int out_bf16, int cus) {
     // Two query rows per block share the W_UV read when that still leaves a
     // block per CU.
     if ((int64_t)H * ((total_q + 1) / 2) >= cus)
         mla_out_kernel<DMAX, 2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
-            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, D, dc, QRP, out,
+            plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, D, dc, QRP, out,
             out_bf16);
     else
         mla_out_kernel<DMAX, 1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
-            plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, D, dc, QRP, out,
+            plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, D, dc, QRP, out,
             out_bf16);
 }
 
 template <bool ARG>
 static void launch_mla_out(hipStream_t s, typename PlanSel<ARG>::T plan, const AttRow *rows,
-                           int n_rows, int total_q, const uint16_t *part_o, const float *part_ml,
+                           int n_rows, int total_q, int one_q, const uint16_t *part_o, const float *part_ml,
                            const uint16_t *w_uv, int H, int hd, int dc, int QRP, void *out,
                            int out_bf16, int cus) {
     if (hd == 128) {
         if ((int64_t)H * ((total_q + 1) / 2) >= cus)
             mla_out_mfma_kernel<2, ARG><<<dim3(H, (total_q + 1) / 2), 256, 0, s>>>(
-                plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, dc, QRP,
+                plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, dc, QRP,
                 out, out_bf16);
         else
             mla_out_mfma_kernel<1, ARG><<<dim3(H, total_q), 256, 0, s>>>(
-                plan, rows, n_rows, total_q, total_q == n_rows, part_o, part_ml, w_uv, H, dc, QRP,
+                plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, dc, QRP,
                 out, out_bf16);
     } else if (hd <= 32)
-        launch_mla_out_d<32, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+        launch_mla_out_d<32, ARG>(s, plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
     else if (hd <= 64)
-        launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+        launch_mla_out_d<64, ARG>(s, plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
     else if (hd <= 128)
-        launch_mla_out_d<128, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+        launch_mla_out_d<128, ARG>(s, plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
     else
-        launch_mla_out_d<256, ARG>(s, plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
+        launch_mla_out_d<256, ARG>(s, plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc, QRP, out, out_bf16, cus);
 }
 
 hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t *pool,
@@ -1025,25 +1053,31 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (nqt != 1 && nqt != 2) return hipErrorInvalidValue;
+    // head groups (some sequence's H x nq rows past one work-group's) re-read
+    // latent rows: keep them in L2
+    const bool keep = H * max_nq > 16 * nqt;
     if (plan && nqt == 1)
-        launch_mla_t<1, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+        launch_mla_t<1, true>(s, keep, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                               mask_mode, part_o, part_ml, ev0, ev1);
     else if (plan)
-        launch_mla_t<2, true>(s, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+        launch_mla_t<2, true>(s, keep, *plan, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                               mask_mode, part_o, part_ml, ev0, ev1);
     else if (nqt == 1)
-        launch_mla_t<1, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+        launch_mla_t<1, false>(s, keep, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                                mask_mode, part_o, part_ml, ev0, ev1);
     else
-        launch_mla_t<2, false>(s, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
+        launch_mla_t<2, false>(s, keep, NoPlan{0}, pool, table, rows, n_rows, work, n_work, qlat, H, P,
                                mask_mode, part_o, part_ml, ev0, ev1);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    // Query row q is plan row q only when every sequence has one query and
+    // one plan row (no head groups).
+    const int one_q = total_q == n_rows && max_nq == 1;
     if (plan)
-        launch_mla_out<true>(s, *plan, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc,
+        launch_mla_out<true>(s, *plan, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc,
                              16 * nqt, out, out_bf16, cus);
     else
-        launch_mla_out<false>(s, NoPlan{0}, rows, n_rows, total_q, part_o, part_ml, w_uv, H, hd, dc,
+        launch_mla_out<false>(s, NoPlan{0}, rows, n_rows, total_q, one_q, part_o, part_ml, w_uv, H, hd, dc,
                               16 * nqt, out, out_bf16, cus);
     return hipGetLastError();
 }
@@ -1051,8 +1085,8 @@ hipError_t launch_mla_decode(hipStream_t s, const PlanArg *plan, const uint16_t 
 int mla_decode_wgs_per_cu(int nqt) {
     int n = 0;
     hipError_t e = hipErrorInvalidValue;
-    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1, true>, 64 * MlaShape<1>::NW, 0);
-    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2, true>, 64 * MlaShape<2>::NW, 0);
+    if (nqt == 1) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<1, true, false>, 64 * MlaShape<1>::NW, 0);
+    if (nqt == 2) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, mla_decode_kernel<2, true, false>, 64 * MlaShape<2>::NW, 0);
     return (e == hipSuccess && n > 0) ? n : 1;
 }
 

@@ -1878,12 +1878,20 @@ int32_t rlx_gqa_attend_noalloc(void *h, int32_t layer, int32_t n_seqs, const int
     return RLX_OK;
 }
 
-// Whether an MLA call of max_qr query rows per sequence (heads x queries)
-// runs as chunked prefill (expansion + FA2) rather than through the decode
-// kernel.
+// Whether an MLA call runs as FA2 chunked prefill (latents expanded per
+// call) rather than the absorbed decode kernel: past kMlaGroupRowsMax query
+// rows (heads x queries) per sequence.  Up to that the absorbed kernel runs
+// head groups of 32 rows, each re-reading the sequence's latent rows (1152 B
+// per token and group) -- far less than an expansion writes and reads back
+// (4 bytes x 128 dims x heads per token) at decode and verify sizes.
+// RLX_MLA_FA2_ROWS overrides the bound (tests run both paths on one shape;
+// read per call).
+constexpr int kMlaGroupRowsMax = 1024;
 static bool mla_use_fa2(const Cache *c, int max_qr, int head_dim) {
     (void)c;
-    return max_qr > 32 && head_dim <= 256;
+    const char *e = getenv("RLX_MLA_FA2_ROWS");
+    const int lim = (e && atoi(e) > 0) ? atoi(e) : kMlaGroupRowsMax;
+    return max_qr > lim && head_dim <= 256;
 }
 
 // Padded head dim of the expanded K_c / V^T rows of an MLA prefill.
@@ -2067,13 +2075,11 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         }
         return RLX_OK;
     }
-    // Decode / verify -- and chunked prefill for the shapes the FA2 path
-    // does not take: one work-group covers every head of a row's split, at
-    // most 32 query rows (heads x queries) per row.  A call with more query
-    // rows is cut into rows of at most 32 / H queries: the causal chunk
-    // [q0, q0 + qn) of n_q queries on a sequence of len tokens is the row
-    // (len - n_q + q0 + qn tokens, qn queries), which has the same key
-    // limits; an unmasked query is a row of its own (len tokens, 1 query).
+    // Decode / verify: one work-group covers at most 32 query rows (heads x
+    // queries, query-major: row qi H + h) of a split of a sequence's context.
+    // A sequence with more rows is cut into head groups of QRP rows, each a
+    // plan row of its own (q0 = its first row, qn = its rows) that re-reads
+    // the sequence's latent rows; the merge finds a row's group by index.
     // The host state of app's tokens is committed already: a failure before
     // the launch that carries them still writes them (and their table
     // patches) to the device, so host and device tables stay in agreement.
@@ -2084,8 +2090,8 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
                                     app->kr_src, app->src_bf16, app->dc, app->dr, app->P);
         return r;
     };
-    const bool chunked = max_qr > 32;
-    const int qc = chunked ? 32 / num_heads : 0;
+    const int nqt = max_qr > 16 ? 2 : 1;
+    const int QRP = 16 * nqt;
     std::vector<AttRow> rows;
     std::vector<int> rlen;
     int total_q = 0, row_nq = 0;
@@ -2096,43 +2102,55 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
         if (nq < 1 || nq > st.len)
             return bail(fail(RLX_ERR_INVALID, "n_q=%d must be in [1, len=%d]", nq, st.len));
         const int32_t tab = (int32_t)(c->row_base(layer, seq_ids[i]) + st.first);
-        auto add = [&](int len, int n, int qrow) {
+        const int all = num_heads * nq;
+        for (int q0 = 0; q0 < all; q0 += QRP) {
             AttRow r{};
             r.tab = tab;
-            r.len = len;
-            r.nq = n;
-            r.qrow = qrow;
-            r.q0 = 0;
-            r.qn = n;
+            r.len = st.len;
+            r.nq = nq;
+            r.qrow = total_q;
+            r.q0 = q0;
+            r.qn = std::min(QRP, all - q0);
             rows.push_back(r);
-            rlen.push_back(len);
-            row_nq = std::max(row_nq, n);
-        };
-        if (!chunked) {
-            add(st.len, nq, total_q);
-        } else if (mask_mode == RLX_MASK_CAUSAL || (mask_mode == RLX_MASK_REF && nq == st.len)) {
-            for (int q0 = 0; q0 < nq; q0 += qc) {
-                const int qn = std::min(qc, nq - q0);
-                add(st.len - nq + q0 + qn, qn, total_q + q0);
-            }
-        } else {
-            for (int q = 0; q < nq; q++) add(st.len, 1, total_q + q);
+            rlen.push_back(st.len);
         }
+        row_nq = std::max(row_nq, nq);
         total_q += nq;
     }
-    const int kmask = chunked ? RLX_MASK_CAUSAL : mask_mode;
-    const int nqt = num_heads * row_nq > 16 ? 2 : 1;
+    const int kmask = mask_mode;
     const std::vector<int> nsplit = mla_splits(rlen, (int64_t)c->cus * mla_decode_wgs_per_cu(nqt));
     std::vector<int2> work;
     int parts = 0;
     for (size_t r = 0; r < rows.size(); r++) {
         rows[r].nsplit = nsplit[r];
         rows[r].part = parts;
-        for (int sp = 0; sp < nsplit[r]; sp++) work.push_back(int2{(int)r, sp});
         parts += nsplit[r];
     }
+    // The head groups of a sequence read the same latent rows (equal lengths,
+    // equal splits).  Work-group b runs on XCD b mod 8, so split s of every
+    // group is placed at the same position mod 8 of consecutive runs of 8
+    // work-groups: the groups of a split run on one XCD at about the same
+    // time and all but the first find its tiles in that XCD's L2.  (The
+    // plan then travels staged: the kernel-argument form derives the work
+    // list in row order.)
+    const bool grouped = rows.size() > (size_t)n_seqs;
+    if (!grouped) {
+        for (size_t r = 0; r < rows.size(); r++)
+            for (int sp = 0; sp < nsplit[r]; sp++) work.push_back(int2{(int)r, sp});
+    } else {
+        for (size_t r0 = 0; r0 < rows.size();) {
+            size_t r1 = r0;
+            while (r1 < rows.size() && rows[r1].qrow == rows[r0].qrow) r1++;  // one sequence's groups
+            const int ns = rows[r0].nsplit;
+            for (int s0 = 0; s0 < ns; s0 += 8) {
+                const int m = std::min(8, ns - s0);
+                for (size_t r = r0; r < r1; r++)
+                    for (int j = 0; j < m; j++) work.push_back(int2{(int)r, s0 + j});
+            }
+            r0 = r1;
+        }
+    }
     if ((rc = flush_patches(c))) return bail(rc);
-    const int QRP = 16 * nqt;
     const size_t ql_bytes = ((size_t)total_q * num_heads * kMlaRow * 2 + 255) & ~(size_t)255;
     const size_t po_bytes = ((size_t)parts * QRP * kMlaDc * sizeof(uint16_t) + 255) & ~(size_t)255;
     const size_t pm_bytes = ((size_t)parts * QRP * 2 * sizeof(float) + 255) & ~(size_t)255;
@@ -2141,7 +2159,7 @@ static int32_t mla_attend_impl(Cache *c, int32_t layer, int32_t n_seqs, const in
     const PlanArg *plan = nullptr;
     const AttRow *d_rows = nullptr;
     const int2 *d_work = nullptr;
-    if (rows.size() * sizeof(AttRow) <= sizeof(PlanArg)) {
+    if (!grouped && rows.size() * sizeof(AttRow) <= sizeof(PlanArg)) {
         memcpy(plan_arg.b, rows.data(), rows.size() * sizeof(AttRow));
         plan = &plan_arg;
     } else {

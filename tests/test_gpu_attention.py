@@ -414,8 +414,8 @@ def test_mla_decode_many_splits(gpu):
     (4, 8, 32, 4, [8, 23, 300], 1, "causal"),      # TestTransformer_MLA's dims (transformer_test.go:1012-1027)
     (4, 16, 64, 8, [9, 100, 260], 4, "causal"),    # config-1-sized layer, 4-query verify
     (8, 64, 256, 32, [300, 17], 2, "causal"),
-    (4, 32, 128, 16, [290, 64], 40, "causal"),     # 160 query rows: causal chunks of 8 queries
-    (4, 16, 64, 8, [70, 40], 40, "none"),          # unmasked: a row per query
+    (4, 32, 128, 16, [290, 64], 40, "causal"),     # 160 query rows: 5 head groups
+    (4, 16, 64, 8, [70, 40], 40, "none"),          # unmasked, 160 rows
     (2, 8, 32, 4, [50], 50, "ref"),                # reference rule with n_q == len: causal
     (16, 128, 512, 64, [300, 65], 1, "causal"),    # default DeepSeek dims, generic absorb / out
     (8, 128, 256, 32, [2100, 70], 1, "causal"),    # head_dim 128 with d_c < 512: latent channels past d_c
@@ -426,23 +426,32 @@ def test_mla_decode_many_splits(gpu):
     (2, 4, 16, 2, [9, 70], 1, "causal"),
     (2, 4, 16, 2, [60, 30], 40, "causal"),
     (3, 20, 80, 10, [300, 20], 2, "causal"),
-    (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128 prefill through FA2 (240 rows)
-    # FA2 at the reference's default dims (K_c / V^T expanded with zero rows
-    # to a 128-dim pitch, W_UK / W_UV columns past d_c zero): 64 heads at
+    (8, 128, 512, 64, [280, 40], 30, "causal"),    # head_dim 128, 240 rows (8 head groups / FA2)
+    # the reference's default dims (FA2: K_c / V^T expanded with zero rows to
+    # a 128-dim pitch, W_UK / W_UV columns past d_c zero): 64 heads at
     # headDim 32 (dC 128, dR 16), and 40 heads decoding one query each
     (64, 32, 128, 16, [300, 90], 3, "causal"),
     (40, 64, 256, 32, [280, 50], 1, "causal"),
-    # head_dim 160: 256-dim pitch, two FA2 launches of 128 value dims
+    # head_dim 160 (FA2: 256-dim pitch, two launches of 128 value dims)
     (48, 160, 512, 64, [270], 2, "causal"),
+    # DeepSeek-V3 decode and verify shapes: 128 heads (4 head groups), and
+    # 4-query verify at 64 heads (8 groups)
+    (128, 128, 512, 64, [700, 33, 260], 1, "causal"),
+    (64, 128, 512, 64, [500, 90], 4, "causal"),
 ])
-def test_mla_other_dims_match_oracle(gpu, H, D, dC, dR, lens, nq, mask):
+@pytest.mark.parametrize("path", ["default", "fa2"])
+def test_mla_other_dims_match_oracle(gpu, monkeypatch, path, H, D, dC, dR, lens, nq, mask):
     """MLA at the reference's default dims (dC = 4 headDim, dHR = headDim/2,
     transformer.go:223-233) and others: latent rows stored zero padded,
     absorb and W_UV projection at head_dims that are multiples of 8 (other
-    widths padded to one at the C boundary), and calls with
-    more than 32 query rows cut into causal query chunks (or single-query
-    rows when unmasked) through the decode kernel."""
+    widths padded to one at the C boundary), and calls of more than 32
+    query rows per sequence.  Each case runs on the
+    default path (up to 1024 query rows per sequence: the absorbed decode
+    kernel in head groups of 32 rows) and with the FA2 expansion forced past
+    32 rows (RLX_MLA_FA2_ROWS)."""
     from relux_amd import MLACache
+    if path == "fa2":
+        monkeypatch.setenv("RLX_MLA_FA2_ROWS", "32")
     rng = np.random.default_rng(61 + H + D + nq)
     P = 64 if D >= 64 else 16
     c = MLACache(num_layers=1, max_len=max(lens) + P, d_c=dC, d_r=dR, page_tokens=P,
@@ -783,7 +792,7 @@ def test_gqa_append_attend_equals_append_then_attend(gpu, case):
         c.close()
 
 
-@pytest.mark.parametrize("case", ["decode_f32", "chunked_bf16", "fa2_bf16", "staged_plans"])
+@pytest.mark.parametrize("case", ["decode_f32", "chunked_bf16", "fa2_bf16", "staged_plans", "groups_h128"])
 def test_mla_append_attend_equals_append_then_attend(gpu, case):
     """rlx_mla_append_attend (the append inside the absorb launch on the
     decode path; before the FA2 kernels on the prefill path) against
@@ -793,14 +802,17 @@ def test_mla_append_attend_equals_append_then_attend(gpu, case):
     fused call also carries pending page-table writes.  A call with a bad
     argument appends nothing."""
     from relux_amd import MLACache
-    rng = np.random.default_rng({"decode_f32": 1, "chunked_bf16": 2, "fa2_bf16": 3, "staged_plans": 4}[case])
+    rng = np.random.default_rng({"decode_f32": 1, "chunked_bf16": 2, "fa2_bf16": 3, "staged_plans": 4,
+                                 "groups_h128": 5}[case])
     P = 64
     # chunked_bf16: 48 query rows per sequence at head_dim 64 take the
-    # decode kernels in causal chunks; fa2_bf16: 80 rows at head_dim 128 take
-    # the expansion + FA2 path; staged_plans: 140 sequences, so the append
-    # and the row plans no longer fit the kernel arguments.
+    # decode kernels in two head groups; fa2_bf16: 1120 rows at head_dim 128
+    # take the expansion + FA2 path; staged_plans: 140 sequences, so the
+    # append and the row plans no longer fit the kernel arguments;
+    # groups_h128: a 128-head decode step, 4 head groups per sequence.
     H, D, ntok, B = {"decode_f32": (16, 128, 1, 6), "chunked_bf16": (4, 64, 12, 3),
-                     "fa2_bf16": (16, 128, 5, 2), "staged_plans": (8, 128, 1, 140)}[case]
+                     "fa2_bf16": (16, 128, 70, 2), "staged_plans": (8, 128, 1, 140),
+                     "groups_h128": (128, 128, 1, 5)}[case]
     dt = torch.float32 if case == "decode_f32" else torch.bfloat16
     lens = [int(x) for x in rng.integers(100, 700, size=B)]
     seqs = list(range(B))
@@ -887,8 +899,10 @@ def test_mla_append_attend_failures_keep_host_and_device_in_step(gpu, monkeypatc
     want = a.Attend(0, qn, qr, w[0], w[1], H, D, seq_ids=seqs).cpu()
     got = f.Attend(0, qn, qr, w[0], w[1], H, D, seq_ids=seqs).cpu()
     assert torch.equal(got, want)
-    # prefill (80 query rows per sequence: expansion + FA2) whose single
-    # head would expand past a 1 MB budget: refused before the append
+    # prefill (80 query rows per sequence, the expansion + FA2 path forced
+    # past 32 rows) whose single head would expand past a 1 MB budget:
+    # refused before the append
+    monkeypatch.setenv("RLX_MLA_FA2_ROWS", "32")
     monkeypatch.setenv("RLX_MLA_EXPAND_MB", "1")
     n5 = [5] * B
     c5 = t(rng.standard_normal((5 * B, 512), dtype=np.float32))
