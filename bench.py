@@ -37,6 +37,9 @@ WORKLOADS = {
     # the top of the target's 8k-32k context range, same shapes at 32k
     "gqa32k": dict(kind="gqa", B=16, H=32, KVH=8, D=128, P=16, T=32768, layers=1),
     "mla32k": dict(kind="mla", B=32, H=16, D=128, P=64, T=32768, layers=1),
+    # DeepSeek-V3's head count (128) in decode at 8k: more query rows per
+    # sequence than a decode work-group holds, so the kernel runs 4 head groups
+    "mla8k_h128": dict(kind="mla", B=8, H=128, D=128, P=64, T=8192, layers=4),
     # MLA chunked prefill, 2048 new tokens on 6144 cached
     "mla_prefill": dict(kind="mla_prefill", B=4, H=128, D=128, P=64, T=6144, n_new=2048, layers=1),
     # speculative verify stress, 4 drafts, rollback U{0..4},
@@ -463,7 +466,7 @@ def run_workload(name, steps, warmup, torch, dev):
     rng = np.random.default_rng({"gqa8k": 2, "gqa_cfg2": 2, "mla8k": 3, "mla_prefill": 4,
                                  "spec_stress": 5, "fused8k": 2, "mla_fused8k": 3,
                                  "spec_accept": 6, "sample": 7, "block8k": 2, "spill8k": 2,
-                                 "gqa32k": 2, "mla32k": 3}[name])
+                                 "gqa32k": 2, "mla32k": 3, "mla8k_h128": 3}[name])
     setup = {"gqa": setup_gqa, "mla": setup_mla, "mla_prefill": setup_mla_prefill,
              "spec": setup_spec, "gqa_fused": setup_gqa_fused,
              "mla_fused": setup_mla_fused, "accept": setup_accept, "sample": setup_sample,
@@ -643,7 +646,7 @@ def main():
           f"{r['kernel_rate']:.0f} {r['rate_unit']}", file=sys.stderr, flush=True)
     secondary = []
     if not args.no_secondary:
-        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "gqa32k", "mla32k", "mla_prefill",
+        for name in [w for w in ("mla8k", "gqa_cfg2", "gqa8k", "gqa32k", "mla32k", "mla8k_h128", "mla_prefill",
                                  "spec_stress",
                                  "fused8k", "mla_fused8k", "block8k", "spec_accept", "sample",
                                  "spill8k")
