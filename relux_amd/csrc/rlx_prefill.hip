@@ -5,7 +5,8 @@
 // Work item = (sequence, head group, query tile).  A head group is one kv
 // head with its G = H/KVH query heads (GQA) or one head (MLA, decompressed).
 // A tile holds 256 query rows, query-major: row r = (token r / G, head r % G),
-// so the G heads that share a kv head share every K/V byte the tile loads.
+// so the G heads that share a kv head share every K/V byte the tile loads
+// (floor(256 / G) tokens; rows past them do nothing).
 // 8 waves of 32 rows each.
 //
 // Keys stream in 64-key blocks through a multi-stage LDS ring filled
@@ -272,7 +273,9 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
     const int qrow_t = wave * 32 + l32;
     const int qj = wk.z * toks + qrow_t / G;
     const int qh = hg * G + qrow_t % G;
-    const bool rvalid = qj < R.nq;
+    // (rows past toks x G -- a group size that does not divide 256 -- belong
+    // to no token of this tile: zero queries, every key masked, no store)
+    const bool rvalid = qj < R.nq && qrow_t < toks * G;
     const int klim = rvalid ? pf_limit(a.mask_mode, R.len, R.nq, qj) : -1;
     bf16x8 qb[KS];
     {

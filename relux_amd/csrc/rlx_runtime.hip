@@ -1449,10 +1449,11 @@ int32_t check_gqa_attend(Cache *c, int32_t layer, int32_t n_seqs, const int32_t 
 }
 // Whether GQA calls with more query rows per kv head than the decode kernel
 // holds run as FA2 chunked prefill: stored head dims 64, 128 and 256 (any
-// caller head_dim they hold) with G = heads per kv head dividing 256; other
-// shapes tile their queries through the decode kernel.
+// caller head_dim they hold), any G = heads per kv head up to 256 (a tile
+// holds floor(256 / G) tokens); other shapes tile their queries through
+// the decode kernel.
 bool gqa_use_fa2(const Cache *c, int G) {
-    return (c->hd == 64 || c->hd == 128 || c->hd == 256) && kPrefillRows % G == 0;
+    return (c->hd == 64 || c->hd == 128 || c->hd == 256) && G <= kPrefillRows;
 }
 
 // Query / output rows of a GQA call: sum of n_q (1 per sequence if null)

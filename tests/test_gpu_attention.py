@@ -501,11 +501,13 @@ def test_mla_other_dims_match_oracle(gpu, monkeypatch, path, H, D, dC, dR, lens,
     (32, 4, 64, [257, 129], [200, 129], "causal"),          # G = 8, D = 64
     (8, 8, 128, [90, 70], [90, 30], "ref"),                 # reference mask rule both ways
     (16, 16, 128, [150], [150], "none"),
+    # group sizes that do not divide 256: FA2 tiles of floor(256 / G) tokens
+    (12, 4, 64, [290, 50], [60, 50], "causal"),            # G = 3: 85 tokens, 255 rows
+    (6, 2, 128, [260], [260], "none"),
+    (20, 4, 128, [300, 70], [120, 70], "causal"),          # G = 5: 51 tokens
     # shapes the FA2 kernel does not take: query tiles through the decode kernel
     (4, 2, 16, [300, 40], [70, 40], "causal"),             # head_dim 16
     (8, 2, 32, [280, 100], [120, 100], "ref"),             # head_dim 32
-    (12, 4, 64, [290, 50], [60, 50], "causal"),            # G = 3 does not divide 128
-    (6, 2, 128, [260], [260], "none"),
     (16, 4, 80, [300, 40], [70, 40], "causal"),            # padded head_dim: query tiles
     (8, 8, 96, [270], [40], "ref"),
     # FA2 at head_dim 256: two launches of 128 value dims each
