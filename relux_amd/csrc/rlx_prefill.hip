@@ -197,9 +197,12 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
 #pragma unroll
                 for (int q = 0; q < NKR; q++) lds_dma16(b, ko[q], kdst + q * 8192);
             } else {
+                // Dense K_c / V^T rows are re-read by every query tile of
+                // the head (on one XCD, at consecutive positions): these
+                // loads leave the lines in L2 (no non-temporal hint).
 #pragma unroll
-                for (int q = 0; q < NKR - 1; q++) lds_dma16(kc_blk, ko[q], kdst + q * 8192);
-                lds_dma16(kr_blk, ko[NKR - 1], kdst + (NKR - 1) * 8192);
+                for (int q = 0; q < NKR - 1; q++) lds_dma16_keep(kc_blk, ko[q], kdst + q * 8192);
+                lds_dma16_keep(kr_blk, ko[NKR - 1], kdst + (NKR - 1) * 8192);
             }
             if (SRC == kSrcPaged) {
                 int pg[4];
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(64 * kWaves) void prefill_kernel(const PrefillArgs 
             } else {
 #pragma unroll
                 for (int i = 0; i < LV; i++)
-                    lds_dma16(vt_blk, ov[i], stage + (uint32_t)(NKR * 512 + (8 * i + wave) * 64) * 16);
+                    lds_dma16_keep(vt_blk, ov[i], stage + (uint32_t)(NKR * 512 + (8 * i + wave) * 64) * 16);
             }
             return;
         }
