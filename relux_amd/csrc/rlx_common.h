@@ -528,6 +528,15 @@ __device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff, uint
 }
 // The same without the non-temporal hint: the lines stay in L2 for other
 // work-groups that read them soon after (the MLA decode's head groups).
+__device__ __forceinline__ void lds_dma16_keep(const void *gptr, uint32_t lds_base) {
+    asm volatile(
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %0, off"
+        :
+        : "v"(gptr), "s"(lds_base)
+        : "memory", "m0");
+}
 __device__ __forceinline__ void lds_dma16_keep(const void *sbase, uint32_t voff, uint32_t lds_base) {
     asm volatile(
         "s_mov_b32 m0, %2\n\t"

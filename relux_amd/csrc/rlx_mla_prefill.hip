@@ -66,6 +66,12 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
     const uint16_t *__restrict__ pool, const int32_t *__restrict__ table,
     const AttRow *__restrict__ rows, const int2 *__restrict__ work, int n_work,
     const uint16_t *__restrict__ wt, int N, int H, int P, int dps, uint16_t *__restrict__ dst) {
+    // Ring loads left in L2 (no non-temporal hint): the latent rows (B),
+    // which every feature tile reads, in both kernels; the W^T tile (A),
+    // which the work-group re-reads for each token tile, for K_c only.
+    // Measured (config 4, rocprof, K_c / V^T µs): hinted 767 / 849; A kept
+    // 743 / 889; B kept 765 / 789; both kept 728 / 822.
+    constexpr bool keep_a = OUT_V == 0, keep_b = true;
     __shared__ __attribute__((aligned(16))) uint16_t ring[kXS * kXStage];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (uniform: scalar registers)
@@ -131,7 +137,11 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
         const int c0 = (g % kXSteps) * kXK;
         const uint32_t st = ring0 + (uint32_t)((g % kXS) * kXStage * 2);
         const uint16_t *ab = a_base + c0;
-        if (a_lim == kXM - 1) {
+        if (a_lim == kXM - 1 && keep_a) {
+#pragma unroll
+            for (int i = 0; i < kXLoadsA; i++)
+                lds_dma16_keep(ab, a_off[i], st + (uint32_t)((wave * kXLoadsA + i) * 64 * 16));
+        } else if (a_lim == kXM - 1) {
 #pragma unroll
             for (int i = 0; i < kXLoadsA; i++)
                 lds_dma16(ab, a_off[i], st + (uint32_t)((wave * kXLoadsA + i) * 64 * 16));
@@ -142,9 +152,15 @@ __global__ __launch_bounds__(512, 1) void mla_expand_kernel(
                 lds_dma16(ab, off, st + (uint32_t)((wave * kXLoadsA + i) * 64 * 16));
             }
         }
+        if (keep_b) {
 #pragma unroll
-        for (int i = 0; i < kXLoadsB; i++)
-            lds_dma16(b_ptr[i] + c0, st + (uint32_t)(kXM * kXK * 2 + (wave * kXLoadsB + i) * 64 * 16));
+            for (int i = 0; i < kXLoadsB; i++)
+                lds_dma16_keep(b_ptr[i] + c0, st + (uint32_t)(kXM * kXK * 2 + (wave * kXLoadsB + i) * 64 * 16));
+        } else {
+#pragma unroll
+            for (int i = 0; i < kXLoadsB; i++)
+                lds_dma16(b_ptr[i] + c0, st + (uint32_t)(kXM * kXK * 2 + (wave * kXLoadsB + i) * 64 * 16));
+        }
     };
     static_assert(kXS == 3, "the stage wait covers one stage ahead");
 
