@@ -527,7 +527,8 @@ __device__ __forceinline__ void lds_dma16(const void *sbase, uint32_t voff, uint
         : "memory", "m0");
 }
 // The same without the non-temporal hint: the lines stay in L2 for other
-// work-groups that read them soon after (the MLA decode's head groups).
+// work-groups that read them soon after (the MLA decode's head groups, the
+// query tiles of a dense prefill head, the feature tiles of the expansion).
 __device__ __forceinline__ void lds_dma16_keep(const void *gptr, uint32_t lds_base) {
     asm volatile(
         "s_mov_b32 m0, %1\n\t"
